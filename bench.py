@@ -1,0 +1,266 @@
+"""Benchmark the TurboQuant hot path on one MI355X ("cfg3").
+
+Workload: Llama-3-8B-shaped single-layer decode attention over a 3-bit
+compressed KV cache -- B=32, 32 query heads over 8 kv heads (GQA 4:1),
+head_dim 128, context 8192; keys 3-bit IP (2-bit MSE + 1-bit QJL), values
+3-bit MSE; bf16 queries; keys N(0,1) with 4 outlier channels x10.  The packed
+cache is prebuilt by the HIP compress kernel, then decode steps are timed.
+A step = one decode-attention call over the whole cache (prepare + split-K
+partial + combine).  Several distinct caches are rotated between steps so the
+256 MB MALL cannot serve a repeat.  Compress (bf16 K and V -> packed cache) is
+timed separately and reported in Gvec/s.
+
+Prints one JSON line.  `value` is packed-byte throughput of the decode step
+(GB/s, inputs resident in HBM); `roofline` covers the dominant kernel (the
+split-K partial), timed with HIP events on the launch stream; `cpu_baseline`
+is the CPU oracle on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "decode attn over 3-bit KV: µs/step, HBM GB/s % of peak; compress Gvec/s"
+
+B, HQ, HKV, D, T = 32, 32, 8, 128, 8192
+KEY_BITS, VAL_BITS = 3, 3
+OUTLIERS = (11, 47, 83, 119)
+
+
+def kv_bytes_per_token_head(d: int) -> int:
+    # packed K: 2-bit MSE (d/4) + 1-bit QJL (d/8) + fp32 norm; V: 3-bit (3 ceil(d/8)) + norm
+    return (2 * d) // 8 + d // 8 + 4 + 3 * ((d + 7) // 8) + 4
+
+
+def make_inputs(seed: int, dev, gen_dtype):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(seed)
+    k = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=torch.float32)
+    k[..., list(OUTLIERS)] *= 10.0
+    v = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=torch.float32)
+    return k.to(gen_dtype), v.to(gen_dtype)
+
+
+def cpu_baseline(eng, q, n_batch: int, reps: int):
+    """Oracle online-softmax decode on the first n_batch sequences of the cache."""
+    import torch
+    from oracle import ref_math as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    st = eng._store
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    sl = slice(0, n_batch)
+    kc = torch.from_numpy(R.unpack_bits(st.kcodes[sl, :, :T].cpu().numpy(), 2, D))
+    kb = torch.from_numpy(R.unpack_bits(st.kqjl[sl, :, :T].cpu().numpy(), 1, D))
+    vc = torch.from_numpy(R.unpack_bits(st.vcodes[sl, :, :T].cpu().numpy(), 3, D))
+    blk = dict(kcodes=kc, kbits=kb, knorm=st.knorm[sl, :, :T].cpu(), vcodes=vc,
+               vnorm=st.vnorm[sl, :, :T].cpu())
+    qs = q[sl].float().cpu().reshape(n_batch, HKV, HQ // HKV, D)
+    args = (kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
+            vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+    R.attention_online(qs, [blk], *args)  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        R.attention_online(qs, [blk], *args)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    nbytes = n_batch * HKV * T * kv_bytes_per_token_head(D)
+    return nbytes / med / 1e9, med, torch.get_num_threads()
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--copies", type=int, default=3, help="distinct caches rotated per step")
+    ap.add_argument("--compress-reps", type=int, default=5)
+    ap.add_argument("--cpu-batch", type=int, default=4, help="sequences in the CPU sample")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
+                                   "(multi-GPU sharding is design-only, see DESIGN.md)"}))
+        sys.exit(2)
+
+    import torch
+    import quashkv_amd as Q
+    from quashkv_amd import _native as N
+    from quashkv_amd.quantizer import compress_into
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = N.lib()
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+
+    # ---------------------------------------------------------- build caches
+    engines = []
+    compress_ms = []
+    for c in range(args.copies):
+        k, v = make_inputs(2 + 1000 * c, dev, torch.bfloat16)
+        eng = Q.QuashKVEngine(head_dim=D, key_bits=KEY_BITS, value_bits=VAL_BITS, seed=42,
+                              device=dev, pack_storage=True, capacity=T)
+        eng.append(k, v)
+        engines.append(eng)
+        if c == 0:
+            # time compress of K (IP) + V (MSE) straight into the store
+            st = eng._store
+            kq, vq = eng.key_quantizer, eng.value_quantizer
+            mq = kq.mse_quantizer
+            kr, vr = k.reshape(-1, D), v.reshape(-1, D)
+
+            def do_compress():
+                compress_into(N.QKV_MODE_IP, kr, mq.Pi, mq.codebook.boundaries,
+                              mq.codebook.centroids, 2, kq.S, st.kcodes, st.kqjl, st.knorm,
+                              packed=True, out_seq=T, out_group_stride=st.capacity)
+                compress_into(N.QKV_MODE_MSE, vr, vq.Pi, vq.codebook.boundaries,
+                              vq.codebook.centroids, 3, None, st.vcodes, None, st.vnorm,
+                              packed=True, out_seq=T, out_group_stride=st.capacity)
+
+            do_compress()
+            torch.cuda.synchronize()
+            for _ in range(args.compress_reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                do_compress()
+                e1.record()
+                torch.cuda.synchronize()
+                compress_ms.append(e0.elapsed_time(e1))
+        del k, v
+    torch.cuda.synchronize()
+
+    gq = torch.Generator(device=dev).manual_seed(7)
+    queries = [torch.randn(B, HQ, 1, D, device=dev, generator=gq).to(torch.bfloat16)
+               for _ in range(args.copies)]
+    st0 = engines[0]._store
+    splits = lib.qkv_attention_splits(B, HQ, HKV, 1, D, T)
+    ws_bytes = lib.qkv_attention_workspace_bytes(B, HQ, HKV, 1, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(B, HQ, 1, D, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i, ev=None):
+        eng = engines[i % args.copies]
+        q = queries[i % args.copies]
+        st = eng._store
+        kq, vq = eng.key_quantizer, eng.value_quantizer
+        mq = kq.mse_quantizer
+        N.check(lib.qkv_attention_prepare(q.data_ptr(), N.QKV_BF16, B, HQ, HKV, 1, D,
+                                          mq.Pi.data_ptr(), kq.S.data_ptr(), kq.qjl_scale,
+                                          ws.data_ptr(), ws_bytes, splits, sptr))
+        if ev is not None:
+            ev[0].record(stream)
+        N.check(lib.qkv_attention_partial(st.kcodes.data_ptr(), st.kqjl.data_ptr(),
+                                          st.knorm.data_ptr(), st.vcodes.data_ptr(),
+                                          st.vnorm.data_ptr(), st.capacity, T, B, HQ, HKV, 1, D,
+                                          2, 3, 1, mq.codebook.centroids.data_ptr(),
+                                          vq.codebook.centroids.data_ptr(), scale, 0,
+                                          ws.data_ptr(), ws_bytes, splits, sptr))
+        if ev is not None:
+            ev[1].record(stream)
+        N.check(lib.qkv_attention_combine(B, HQ, HKV, 1, D, mq.Pi.data_ptr(), out.data_ptr(),
+                                          N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    step_ms = t_start.elapsed_time(t_end) / args.steps
+    partial_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
+
+    kv_bytes = B * HKV * T * kv_bytes_per_token_head(D)
+    io_bytes = B * HQ * D * (2 + 4)  # bf16 q in, fp32 out
+    step_gbs = (kv_bytes + io_bytes) / (step_ms * 1e-3) / 1e9
+    partial_gbs = kv_bytes / (partial_ms * 1e-3) / 1e9
+    n_vec = 2 * B * HKV * T
+    comp_ms = statistics.median(compress_ms)
+    comp_gvec = n_vec / (comp_ms * 1e-3) / 1e9
+    comp_bytes = n_vec * (D * 2) + B * HKV * T * kv_bytes_per_token_head(D)
+
+    cpu = None
+    if not args.no_cpu:
+        gbs, med, threads = cpu_baseline(engines[0], queries[0], args.cpu_batch, args.cpu_reps)
+        cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": (f"oracle online-softmax decode (oracle/ref_math.attention_online, "
+                          f"fp32 torch CPU) on {args.cpu_batch} of {B} sequences, all 8 kv "
+                          f"heads, T={T}; median of {args.cpu_reps} reps = {med:.3f} s; "
+                          f"host {cpu_model()}")}
+
+    line = {
+        "metric": METRIC,
+        "value": round(step_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1) K/V/q; keys with 4 outlier channels x10)",
+        "config": {
+            "workload": "cfg3 Llama-3-8B-shaped decode attention over packed 3-bit KV",
+            "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T,
+            "key_bits": KEY_BITS, "value_bits": VAL_BITS, "query_dtype": "bf16",
+            "cache_copies_rotated": args.copies, "n_splits": splits,
+        },
+        "decode_us_per_step": round(step_ms * 1e3, 2),
+        "decode_pct_of_hbm_peak": round(100 * step_gbs / PEAK_HBM_GBS, 2),
+        "compress_gvec_s": round(comp_gvec, 4),
+        "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
+                                              / PEAK_HBM_GBS, 2),
+        "roofline": {
+            "kernel": "split_kernel (qkv_attention_partial)",
+            "bound": "hbm",
+            "achieved": round(partial_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(partial_gbs / PEAK_HBM_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": kv_bytes,
+            "avg_kernel_us": round(partial_ms * 1e3, 2),
+        },
+        "cpu_baseline": cpu,
+        "wall_s_timed": round(wall, 3),
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

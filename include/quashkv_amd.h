@@ -1,0 +1,194 @@
+/*
+ * quashkv_amd -- C ABI of the MI355X (gfx950) TurboQuant hot path.
+ *
+ * Every entry point:
+ *   - takes plain device pointers, sizes and a hipStream_t passed as void*;
+ *   - validates its arguments on the host BEFORE any launch;
+ *   - launches asynchronously on `stream` and never synchronises;
+ *   - never allocates or frees device memory (callers pass outputs and the
+ *     attention workspace, sized by qkv_attention_workspace_bytes);
+ *   - returns QKV_OK (0) or a QKV_E_* status; qkv_last_error() then holds a
+ *     thread-local message.
+ *
+ * Layout conventions (shared with the reference's PyTorch tensors):
+ *   - Pi is the d x d rotation, row-major fp32; y = u Pi^T rotates, x = y Pi
+ *     un-rotates (quashkv/quantizer.py:105-111).
+ *   - Code rows use the reference's pack_bits layout (quashkv/packing.py:8-14):
+ *     LSB-first, 1/2/4-bit groups per byte, 3-bit groups of 8 codes in a
+ *     little-endian 24-bit word; bits = 8 means one uint8 per code (unpacked).
+ *   - "Grouped rows": vector r of a call lives at row
+ *       (r / seq) * group_stride + (r % seq)
+ *     of the code/norm buffers, so a (B, H, S, d) input can be written into,
+ *     or read from, a (B, H, T_capacity, row_bytes) cache at any offset.
+ *
+ * The reference interface each function replaces is cited as path:line
+ * relative to the reference package root.
+ */
+#ifndef QUASHKV_AMD_H
+#define QUASHKV_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QKV_ABI_VERSION 1
+
+/* status codes */
+#define QKV_OK 0
+#define QKV_E_INVALID 1     /* bad argument (maps to ValueError) */
+#define QKV_E_UNSUPPORTED 2 /* valid but unsupported shape/bits (maps to ValueError) */
+#define QKV_E_HIP 3         /* HIP runtime error (maps to RuntimeError) */
+
+/* element types */
+#define QKV_F32 0
+#define QKV_F16 1
+#define QKV_BF16 2
+
+/* compress / decompress modes */
+#define QKV_MODE_MSE 0 /* MSEQuantizer */
+#define QKV_MODE_IP 1  /* InnerProductQuantizer: (b-1)-bit MSE + 1-bit QJL */
+
+/* compress flags */
+#define QKV_FLAG_PACKED 1      /* write packed rows (else one uint8 per code) */
+#define QKV_FLAG_PRE_ROTATED 2 /* x is already y = u Pi^T: skip norm + rotation
+                                  (parity entry: codes from identical y) */
+
+int qkv_abi_version(void);
+const char* qkv_last_error(void);
+
+/* Bytes per packed row as pack_bits lays it out: 3*ceil(d/8) for 3-bit,
+ * ceil(d*bits/8) otherwise, d for bits = 8 (quashkv/packing.py:43-89).
+ * Returns -1 for unsupported bits. */
+int64_t qkv_packed_row_bytes(int32_t d, int32_t bits);
+
+/* pack_bits(indices, bits) -- quashkv/packing.py:22-94.
+ * codes: rows x d uint8, packed: rows x qkv_packed_row_bytes(d, bits). */
+int qkv_pack_bits(const uint8_t* codes, uint8_t* packed, int64_t rows,
+                  int32_t d, int32_t bits, void* stream);
+
+/* unpack_bits(packed, bits, d) -- quashkv/packing.py:97-159.
+ * packed rows are packed_row_bytes apart; codes: rows x d uint8. */
+int qkv_unpack_bits(const uint8_t* packed, int64_t packed_row_bytes,
+                    uint8_t* codes, int64_t rows, int32_t d, int32_t bits,
+                    void* stream);
+
+/* LloydMaxCodebook.quantize_boundary (mode 0; quashkv/codebook.py:239-259,
+ * == torch.bucketize, quashkv/triton_kernels/compress.py:57) and
+ * LloydMaxCodebook.quantize (mode 1, first nearest centroid;
+ * quashkv/codebook.py:209-224) on n contiguous fp32 values.
+ * table: boundaries (mode 0) or centroids (mode 1), count <= 16 entries. */
+int qkv_quantize(const float* y, int64_t n, const float* table, int32_t count,
+                 int32_t mode, uint8_t* out, void* stream);
+
+/* LloydMaxCodebook.dequantize -- quashkv/codebook.py:226-237: out = c[code];
+ * codes >= count give NaN (the reference raises an index error). */
+int qkv_dequantize(const uint8_t* codes, int64_t n, const float* cents,
+                   int32_t count, float* out, void* stream);
+
+/* InnerProductQuantizer.decompress_for_dot -- quashkv/quantizer.py:244-279:
+ * out[r] = n_r (<q_rot_r, c[code_r]> + alpha sum_j |q_rot_rj| (2b_rj-1) S_j)
+ * over unpacked uint8 codes/bits, n rows of d. */
+int qkv_ip_dot(const uint8_t* codes, const uint8_t* qjl, const float* norms,
+               const float* q_rot, int64_t n, int32_t d, const float* cents,
+               int32_t count, const float* signs, float alpha, float* out,
+               void* stream);
+
+/* Fused compress: normalise -> rotate -> boundary search [-> QJL sign] -> store.
+ * Replaces fused_compress_mse / fused_compress_ip
+ * (quashkv/triton_kernels/compress.py:210-303) and MSEQuantizer.compress /
+ * InnerProductQuantizer.compress (quashkv/quantizer.py:113-131, 211-242).
+ *   mode       QKV_MODE_MSE or QKV_MODE_IP
+ *   x          n x d, in_dtype (F32/F16/BF16), contiguous
+ *   pi         d x d fp32 rotation
+ *   boundaries 2^bits - 1 fp32, ascending; centroids 2^bits fp32
+ *   bits       MSE code bits (1..4); for IP this is total_bits - 1
+ *   signs      d fp32 (+-1), IP only (may be NULL for MSE)
+ *   codes      grouped rows of qkv_packed_row_bytes(d, bits) (or d if unpacked)
+ *   qjl        grouped rows of the 1-bit QJL signs (IP only)
+ *   norms      grouped fp32 norms max(||x||, 1e-8) (ignored if PRE_ROTATED)
+ *   out_seq, out_group_stride  grouped-row addressing of codes/qjl/norms */
+int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
+                 const void* x, int64_t n, int32_t d,
+                 const float* pi, const float* boundaries,
+                 const float* centroids, int32_t bits, const float* signs,
+                 uint8_t* codes, uint8_t* qjl, float* norms,
+                 int64_t out_seq, int64_t out_group_stride, void* stream);
+
+/* Fused decompress: unpack -> centroid gather [+ alpha S (2b-1)] -> Pi -> *norm.
+ * Replaces fused_decompress_mse / fused_decompress_ip
+ * (quashkv/triton_kernels/decompress.py:194-285), MSEQuantizer.decompress
+ * (quashkv/quantizer.py:133-147) and QuashKVCache's key/value reconstruction
+ * (quashkv/integrations/hf_cache.py:96-121, mode MSE with the key codebook).
+ *   packed     1: code rows are packed with `bits` (qjl with 1 bit); 0: uint8
+ *   out        n x d, out_dtype, contiguous */
+int qkv_decompress(int32_t mode, int32_t packed,
+                   const uint8_t* codes, const uint8_t* qjl, const float* norms,
+                   int64_t n, int32_t d, int32_t bits,
+                   const float* pi, const float* centroids, const float* signs,
+                   float qjl_scale, int64_t in_seq, int64_t in_group_stride,
+                   void* out, int32_t out_dtype, void* stream);
+
+/* Split-K count the library would use for a decode-attention call. */
+int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                             int32_t d, int64_t T);
+
+/* Workspace bytes qkv_decode_attention needs for `n_splits` splits. */
+int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv,
+                                      int32_t Q, int32_t d, int32_t n_splits);
+
+/* Attention over the compressed cache, scored in the rotated domain.
+ * Replaces QuashKVEngine.attention (quashkv/engine.py:204-299) and
+ * fused_quantized_attention (quashkv/triton_kernels/attention.py:307-394),
+ * with GQA: query head h reads KV head h / (Hq / Hkv).
+ *   q        B x Hq x Q x d, q_dtype, contiguous
+ *   kcodes   B x Hkv x t_stride rows of the key MSE codes (kbits)
+ *   kqjl     same rows of the 1-bit QJL signs
+ *   knorm    B x Hkv x t_stride fp32; vcodes/vnorm likewise for values (vbits)
+ *   packed   1: code rows packed; 0: one uint8 per code
+ *   T        valid tokens (<= t_stride); causal masks kv_pos > T - Q + i
+ *   out      B x Hq x Q x d, out_dtype
+ *   workspace/ws_bytes  >= qkv_attention_workspace_bytes(..., n_splits) */
+int qkv_decode_attention(const void* q, int32_t q_dtype,
+                         const uint8_t* kcodes, const uint8_t* kqjl,
+                         const float* knorm, const uint8_t* vcodes,
+                         const float* vnorm, int64_t t_stride, int64_t T,
+                         int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                         int32_t d, int32_t kbits, int32_t vbits,
+                         int32_t packed, const float* pi, const float* kcent,
+                         const float* vcent, const float* signs,
+                         float qjl_scale, float scale, int32_t causal,
+                         void* out, int32_t out_dtype, void* workspace,
+                         int64_t ws_bytes, int32_t n_splits, void* stream);
+
+/* The three phases qkv_decode_attention runs, exposed so a caller can overlap
+ * or time them separately (same arguments and workspace):
+ *   prepare  q~ = q Pi^T and w = alpha |q~| S into the workspace
+ *            (quashkv/engine.py:237-238, quashkv/triton_kernels/attention.py:94,111)
+ *   partial  split-K online softmax over the cache (quashkv/engine.py:245-289,
+ *            quashkv/triton_kernels/attention.py:97-145)
+ *   combine  log-sum-exp merge of the splits, / max(l, 1e-8), x Pi once, store
+ *            (quashkv/engine.py:292-297, quashkv/triton_kernels/attention.py:147-149) */
+int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
+                          int32_t Hkv, int32_t Q, int32_t d, const float* pi,
+                          const float* signs, float qjl_scale, void* workspace,
+                          int64_t ws_bytes, int32_t n_splits, void* stream);
+int qkv_attention_partial(const uint8_t* kcodes, const uint8_t* kqjl,
+                          const float* knorm, const uint8_t* vcodes,
+                          const float* vnorm, int64_t t_stride, int64_t T,
+                          int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+                          int32_t kbits, int32_t vbits, int32_t packed,
+                          const float* kcent, const float* vcent, float scale,
+                          int32_t causal, void* workspace, int64_t ws_bytes,
+                          int32_t n_splits, void* stream);
+int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+                          const float* pi, void* out, int32_t out_dtype,
+                          void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QUASHKV_AMD_H */

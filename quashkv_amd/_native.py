@@ -1,0 +1,134 @@
+"""ctypes boundary to libquashkv_hip.so (the C ABI in include/quashkv_amd.h).
+
+The Python layer owns every allocation (outputs and workspaces are torch
+tensors on the GPU) and passes raw device pointers plus the current HIP
+stream.  There is exactly one execution path: the HIP kernels.  If the
+library is missing, or a tensor is not on the GPU, the call raises -- the
+package has no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+import torch  # loads torch's HIP runtime first; the library binds to the same one
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libquashkv_hip.so")
+_lib: Optional[ctypes.CDLL] = None
+
+QKV_OK, QKV_E_INVALID, QKV_E_UNSUPPORTED, QKV_E_HIP = 0, 1, 2, 3
+QKV_F32, QKV_F16, QKV_BF16 = 0, 1, 2
+QKV_MODE_MSE, QKV_MODE_IP = 0, 1
+QKV_FLAG_PACKED, QKV_FLAG_PRE_ROTATED = 1, 2
+
+_DTYPE = {torch.float32: QKV_F32, torch.float16: QKV_F16, torch.bfloat16: QKV_BF16}
+
+_i32, _i64, _f32, _p = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/quashkv_amd.h
+_SIGS = {
+    "qkv_abi_version": (_i32, []),
+    "qkv_last_error": (ctypes.c_char_p, []),
+    "qkv_packed_row_bytes": (_i64, [_i32, _i32]),
+    "qkv_pack_bits": (_i32, [_p, _p, _i64, _i32, _i32, _p]),
+    "qkv_unpack_bits": (_i32, [_p, _i64, _p, _i64, _i32, _i32, _p]),
+    "qkv_quantize": (_i32, [_p, _i64, _p, _i32, _i32, _p, _p]),
+    "qkv_dequantize": (_i32, [_p, _i64, _p, _i32, _p, _p]),
+    "qkv_ip_dot": (_i32, [_p, _p, _p, _p, _i64, _i32, _p, _i32, _p, _f32, _p, _p]),
+    "qkv_compress": (_i32, [_i32, _i32, _i32, _p, _i64, _i32, _p, _p, _p, _i32, _p,
+                            _p, _p, _p, _i64, _i64, _p]),
+    "qkv_decompress": (_i32, [_i32, _i32, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _f32,
+                              _i64, _i64, _p, _i32, _p]),
+    "qkv_attention_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64]),
+    "qkv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "qkv_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
+                                    _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
+                                    _f32, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
+    "qkv_attention_prepare": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _f32, _p,
+                                     _i64, _i32, _p]),
+    "qkv_attention_partial": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32,
+                                     _i32, _i32, _i32, _i32, _p, _p, _f32, _i32, _p, _i64, _i32,
+                                     _p]),
+    "qkv_attention_combine": (_i32, [_i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _i64, _i32,
+                                     _p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+class NativeLibraryMissing(ImportError):
+    pass
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise NativeLibraryMissing(
+                f"quashkv_amd: {_LIB_PATH} is not built; run `python -m quashkv_amd.build` "
+                "(or __graft_entry__.build()).  There is no CPU fallback.")
+        handle = ctypes.CDLL(_LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(status: int) -> None:
+    if status == QKV_OK:
+        return
+    msg = lib().qkv_last_error().decode(errors="replace")
+    if status in (QKV_E_INVALID, QKV_E_UNSUPPORTED):
+        raise ValueError(msg)
+    raise RuntimeError(f"quashkv_amd HIP failure: {msg}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE[dt]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16")
+
+
+def require_gpu(*tensors: torch.Tensor, what: str = "quashkv_amd") -> torch.device:
+    """All tensors must live on the same HIP device.  No CPU fallback exists."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise RuntimeError(
+                f"{what} runs on the GPU (HIP); got a tensor on {t.device}. "
+                "Move inputs to the GPU (e.g. .to('cuda')); there is no CPU path.")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"{what}: tensors on different devices ({dev} vs {t.device})")
+    return dev
+
+
+def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def packed_row_bytes(d: int, bits: int) -> int:
+    if bits == 8:
+        return d
+    if bits == 3:
+        return 3 * ((d + 7) // 8)
+    if bits in (1, 2, 4):
+        return (d * bits + 7) // 8
+    raise ValueError(f"Unsupported bits: {bits}")

@@ -1,0 +1,171 @@
+"""Fused operator API (same names and arguments as quashkv/triton_kernels/*).
+
+The reference dispatches ``HAS_TRITON and x.is_cuda`` to Triton and falls
+back to PyTorch otherwise (quashkv/triton_kernels/compress.py:230,275;
+decompress.py:213,260; attention.py:344).  Here there is one path: the HIP
+kernels of libquashkv_hip.so, on GPU tensors.  CPU tensors raise.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _native as N
+from .quantizer import compress_into, decompress_from
+
+HAS_HIP = True
+
+
+def _lead(x: torch.Tensor):
+    lead = x.shape[:-1]
+    return lead, int(torch.Size(lead).numel())
+
+
+def fused_compress_mse(x: torch.Tensor, Pi: torch.Tensor,
+                       boundaries: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """normalise -> rotate -> boundary quantise; (codes uint8 (..., d), norms (...)).
+    Replaces quashkv/triton_kernels/compress.py:210-249."""
+    dev = N.require_gpu(x, Pi, boundaries, what="fused_compress_mse")
+    d = x.shape[-1]
+    lead, n = _lead(x)
+    bits = int(round(math.log2(boundaries.numel() + 1)))
+    if (1 << bits) - 1 != boundaries.numel():
+        raise ValueError("boundaries must have 2**bits - 1 entries")
+    codes = torch.empty(n, d, dtype=torch.uint8, device=dev)
+    norms = torch.empty(n, dtype=torch.float32, device=dev)
+    # centroids are not needed by the MSE stage; pass the boundaries as a
+    # placeholder table of the right device
+    cents = torch.zeros(1 << bits, dtype=torch.float32, device=dev)
+    compress_into(N.QKV_MODE_MSE, x, Pi.float().contiguous(), boundaries.float().contiguous(),
+                  cents, bits, None, codes, None, norms, packed=False)
+    return codes.reshape(*lead, d), norms.reshape(lead)
+
+
+def fused_compress_ip(x: torch.Tensor, Pi: torch.Tensor, boundaries: torch.Tensor,
+                      S: torch.Tensor, centroids: torch.Tensor):
+    """normalise -> rotate -> MSE quantise -> QJL sign of the residual.
+    Replaces quashkv/triton_kernels/compress.py:252-303."""
+    dev = N.require_gpu(x, Pi, boundaries, S, centroids, what="fused_compress_ip")
+    d = x.shape[-1]
+    lead, n = _lead(x)
+    bits = int(round(math.log2(centroids.numel())))
+    if (1 << bits) != centroids.numel() or boundaries.numel() != centroids.numel() - 1:
+        raise ValueError("need 2**b centroids and 2**b - 1 boundaries")
+    codes = torch.empty(n, d, dtype=torch.uint8, device=dev)
+    qjl = torch.empty(n, d, dtype=torch.uint8, device=dev)
+    norms = torch.empty(n, dtype=torch.float32, device=dev)
+    compress_into(N.QKV_MODE_IP, x, Pi.float().contiguous(), boundaries.float().contiguous(),
+                  centroids.float().contiguous(), bits, S.float().contiguous(), codes, qjl, norms,
+                  packed=False)
+    return codes.reshape(*lead, d), qjl.reshape(*lead, d), norms.reshape(lead)
+
+
+def fused_decompress_mse(indices: torch.Tensor, norms: torch.Tensor, Pi: torch.Tensor,
+                         centroids: torch.Tensor) -> torch.Tensor:
+    """(c[code] Pi) * norm, fp32.  Replaces quashkv/triton_kernels/decompress.py:194-232."""
+    N.require_gpu(indices, norms, Pi, centroids, what="fused_decompress_mse")
+    d = indices.shape[-1]
+    lead, n = _lead(indices)
+    bits = max(1, int(math.ceil(math.log2(max(centroids.numel(), 2)))))
+    out = decompress_from(N.QKV_MODE_MSE, indices.reshape(n, d).to(torch.uint8).contiguous(), None,
+                          norms.reshape(n).float().contiguous(), n, Pi.float().contiguous(),
+                          centroids.float().contiguous(), bits, None, 0.0, packed=False)
+    return out.reshape(*lead, d)
+
+
+def fused_decompress_ip(mse_indices: torch.Tensor, qjl_signs: torch.Tensor, norms: torch.Tensor,
+                        Pi: torch.Tensor, centroids: torch.Tensor, S: torch.Tensor,
+                        qjl_scale: float) -> torch.Tensor:
+    """((c[code] + alpha S (2b-1)) Pi) * norm, fp32.
+    Replaces quashkv/triton_kernels/decompress.py:235-285."""
+    N.require_gpu(mse_indices, qjl_signs, norms, Pi, centroids, S, what="fused_decompress_ip")
+    d = mse_indices.shape[-1]
+    lead, n = _lead(mse_indices)
+    bits = max(1, int(math.ceil(math.log2(max(centroids.numel(), 2)))))
+    out = decompress_from(N.QKV_MODE_IP, mse_indices.reshape(n, d).to(torch.uint8).contiguous(),
+                          qjl_signs.reshape(n, d).to(torch.uint8).contiguous(),
+                          norms.reshape(n).float().contiguous(), n, Pi.float().contiguous(),
+                          centroids.float().contiguous(), bits, S.float().contiguous(),
+                          qjl_scale, packed=False)
+    return out.reshape(*lead, d)
+
+
+@dataclass
+class CompressedBlock:
+    """View of one compressed KV block (quashkv/triton_kernels/attention.py:40-48)."""
+    mse_indices: torch.Tensor   # (B, H, S, D) uint8
+    qjl_signs: torch.Tensor     # (B, H, S, D) uint8
+    key_norms: torch.Tensor     # (B, H, S) float32
+    val_indices: torch.Tensor   # (B, H, S, D) uint8
+    val_norms: torch.Tensor     # (B, H, S) float32
+    seq_len: int
+
+
+def attention_call(queries: torch.Tensor, kcodes: torch.Tensor, kqjl: torch.Tensor,
+                   knorm: torch.Tensor, vcodes: torch.Tensor, vnorm: torch.Tensor, T: int,
+                   Pi: torch.Tensor, key_centroids: torch.Tensor, val_centroids: torch.Tensor,
+                   S: torch.Tensor, qjl_scale: float, kbits: int, vbits: int, packed: bool,
+                   scale: Optional[float] = None, causal: bool = False,
+                   out_dtype: torch.dtype = torch.float32,
+                   workspace: Optional[torch.Tensor] = None,
+                   n_splits: Optional[int] = None) -> torch.Tensor:
+    """Launch the decode-attention kernels over a (B, Hkv, t_stride, row) cache.
+
+    Returns (B, Hq, Q, d).  ``workspace`` (uint8, on the device) is grown and
+    reused when given as a one-element list holder; a fresh one is allocated
+    otherwise."""
+    dev = N.require_gpu(queries, kcodes, kqjl, knorm, vcodes, vnorm, Pi, what="attention")
+    B, Hq, Q, d = queries.shape
+    Hkv, t_stride = kcodes.shape[1], kcodes.shape[2]
+    if Hq % Hkv != 0:
+        raise ValueError(f"query heads ({Hq}) must be a multiple of kv heads ({Hkv})")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    L = N.lib()
+    if n_splits is None:
+        n_splits = L.qkv_attention_splits(B, Hq, Hkv, Q, d, T)
+    need = L.qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+    q = queries.contiguous()
+    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        q = q.float()
+    out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
+    N.check(L.qkv_decode_attention(
+        q.data_ptr(), N.dtype_code(q.dtype), kcodes.data_ptr(), kqjl.data_ptr(), knorm.data_ptr(),
+        vcodes.data_ptr(), vnorm.data_ptr(), t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits,
+        1 if packed else 0, Pi.data_ptr(), key_centroids.data_ptr(), val_centroids.data_ptr(),
+        S.data_ptr(), float(qjl_scale), float(scale), 1 if causal else 0, out.data_ptr(),
+        N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
+        N.stream(dev)))
+    return out
+
+
+def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[CompressedBlock],
+                              Pi: torch.Tensor, key_centroids: torch.Tensor,
+                              val_centroids: torch.Tensor, S: torch.Tensor, qjl_scale: float,
+                              scale: Optional[float] = None, causal: bool = False,
+                              total_kv_tokens: int = 0) -> torch.Tensor:
+    """Attention over unpacked compressed blocks (quashkv/triton_kernels/attention.py:307-394).
+
+    Blocks hold one uint8 per code, as in the reference.  Query heads may be a
+    multiple of the blocks' kv heads (GQA)."""
+    if not blocks:
+        raise ValueError("No compressed KV blocks in cache. Call append() first.")
+    N.require_gpu(queries, Pi, what="fused_quantized_attention")
+    kc = torch.cat([b.mse_indices for b in blocks], dim=2).contiguous()
+    kq = torch.cat([b.qjl_signs for b in blocks], dim=2).contiguous()
+    kn = torch.cat([b.key_norms for b in blocks], dim=2).float().contiguous()
+    vc = torch.cat([b.val_indices for b in blocks], dim=2).contiguous()
+    vn = torch.cat([b.val_norms for b in blocks], dim=2).float().contiguous()
+    T = kc.shape[2]
+    kbits = max(1, int(math.ceil(math.log2(max(key_centroids.numel(), 2)))))
+    vbits = max(1, int(math.ceil(math.log2(max(val_centroids.numel(), 2)))))
+    return attention_call(queries, kc, kq, kn, vc, vn, T, Pi.float().contiguous(),
+                          key_centroids.float().contiguous(), val_centroids.float().contiguous(),
+                          S.float().contiguous(), qjl_scale, kbits, vbits, packed=False,
+                          scale=scale, causal=causal)

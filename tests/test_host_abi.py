@@ -1,0 +1,163 @@
+"""CPU tests: the C ABI library loads and exports every declared symbol, host
+validation rejects bad arguments before any launch, and the product's host-side
+parameters (codebooks, Pi, S) equal the reference's golden values bit-for-bit."""
+
+import math
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+import quashkv_amd as Q
+from quashkv_amd import _native as N
+from quashkv_amd.codebook import LloydMaxCodebook, compute_mse_cost, solve_lloyd_max
+from quashkv_amd.quantizer import _random_orthogonal, _random_signs
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "quashkv_amd.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qkv_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = N.lib()
+    names = header_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(N.EXPORTED)
+    assert lib.qkv_abi_version() == 1
+
+
+@pytest.mark.parametrize("d,bits,expect", [(128, 1, 16), (128, 2, 32), (128, 3, 48), (128, 4, 64),
+                                           (65, 3, 27), (63, 2, 16), (100, 4, 50), (8, 8, 8)])
+def test_packed_row_bytes(d, bits, expect):
+    assert N.lib().qkv_packed_row_bytes(d, bits) == expect
+    assert N.packed_row_bytes(d, bits) == expect
+
+
+def test_abi_rejects_before_launch():
+    lib = N.lib()
+    assert lib.qkv_pack_bits(None, None, 4, 128, 5, None) == N.QKV_E_INVALID
+    assert "Unsupported bits" in lib.qkv_last_error().decode()
+    assert lib.qkv_unpack_bits(None, 10, None, 1, 128, 3, None) == N.QKV_E_INVALID
+    assert "cannot hold" in lib.qkv_last_error().decode()
+    # bad head dim -> unsupported
+    st = lib.qkv_compress(0, 0, 0, None, 4, 80, None, None, None, 3, None, None, None, None, 4, 4, None)
+    assert st == N.QKV_E_UNSUPPORTED
+    st = lib.qkv_compress(0, 0, 0, None, 4, 128, None, None, None, 7, None, None, None, None, 4, 4, None)
+    assert st == N.QKV_E_INVALID and "bits must be in" in lib.qkv_last_error().decode()
+    # empty cache
+    st = lib.qkv_decode_attention(None, 0, None, None, None, None, None, 0, 0, 1, 8, 8, 1, 128, 2, 3,
+                                  1, None, None, None, None, 0.1, 0.1, 0, None, 0, None, 0, 1, None)
+    assert st == N.QKV_E_INVALID and "No compressed KV blocks" in lib.qkv_last_error().decode()
+    # workspace too small
+    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 1, 64, 64, 1, 8, 8, 1, 128, 2, 3, 1, 1, 1, 1, 1,
+                                  0.1, 0.1, 0, 1, 0, 16, 8, 1, None)
+    assert st == N.QKV_E_INVALID and "workspace too small" in lib.qkv_last_error().decode()
+    # GQA divisibility
+    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 1, 64, 64, 1, 6, 4, 1, 128, 2, 3, 1, 1, 1, 1, 1,
+                                  0.1, 0.1, 0, 1, 0, 16, 1 << 30, 1, None)
+    assert st == N.QKV_E_INVALID and "multiple of kv heads" in lib.qkv_last_error().decode()
+
+
+def test_check_maps_status_to_exceptions():
+    N.lib().qkv_pack_bits(None, None, 4, 128, 9, None)
+    with pytest.raises(ValueError, match="Unsupported bits"):
+        N.check(N.QKV_E_INVALID)
+
+
+def test_workspace_and_split_policy_are_consistent():
+    lib = N.lib()
+    for (B, Hq, Hkv, Q_, d) in [(32, 32, 8, 1, 128), (1, 32, 8, 1, 128), (16, 14, 2, 1, 64)]:
+        ws = lib.qkv_attention_workspace_bytes(B, Hq, Hkv, Q_, d, 4)
+        R = (Hq // Hkv) * Q_
+        assert ws == 4 * (B * Hkv * R * 2 * d + 4 * B * Hkv * R * d + 4 * B * Hkv * R * 2)
+
+
+# -------------------------------------------------- product host parameters
+
+@pytest.mark.parametrize("d", [64, 96, 128])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_codebook_solver_bit_exact(golden, d, bits):
+    cb = golden("codebooks")
+    c = LloydMaxCodebook(d, bits)
+    assert torch.equal(c.centroids, torch.from_numpy(cb[f"c_d{d}_b{bits}"]))
+    assert torch.equal(c.boundaries, torch.from_numpy(cb[f"t_d{d}_b{bits}"]))
+    c64, t64 = solve_lloyd_max(d, bits)
+    assert np.allclose(c64, cb[f"c64_d{d}_b{bits}"], rtol=0, atol=1e-14)
+
+
+@pytest.mark.parametrize("d,bits", [(64, 2), (64, 3), (128, 2)])
+def test_codebook_exact_pdf_bit_exact(golden, d, bits):
+    cb = golden("codebooks")
+    c = LloydMaxCodebook(d, bits, use_exact_pdf=True)
+    assert torch.equal(c.centroids, torch.from_numpy(cb[f"ce_d{d}_b{bits}"]))
+    assert torch.equal(c.boundaries, torch.from_numpy(cb[f"te_d{d}_b{bits}"]))
+
+
+def test_codebook_closed_forms():
+    # 1-bit Gaussian Lloyd-Max: +-sigma sqrt(2/pi); distortions (Max 1960)
+    for d in (64, 128):
+        c, _ = solve_lloyd_max(d, 1)
+        assert abs(c[1] - math.sqrt(2 / math.pi) / math.sqrt(d)) < 1e-12
+    assert abs(compute_mse_cost(128, 1) - (1 - 2 / math.pi)) < 1e-9
+    assert abs(compute_mse_cost(128, 2) - 0.11748) < 1e-4
+    assert abs(compute_mse_cost(128, 3) - 0.03455) < 1e-4
+    for bits in (1, 2, 3):
+        m = compute_mse_cost(128, bits)
+        assert 0.9 * 4 ** -bits < m < 2.8 * 4 ** -bits
+    with pytest.raises(ValueError, match="bits must be in"):
+        solve_lloyd_max(128, 5)
+
+
+@pytest.mark.parametrize("d,seed", [(64, 42), (64, 65), (96, 42), (128, 42), (128, 7)])
+def test_rotation_and_signs_bit_exact(golden, d, seed):
+    g = golden("rotations")
+    assert torch.equal(_random_orthogonal(d, seed, "cpu"), torch.from_numpy(g[f"Pi_d{d}_s{seed}"]))
+    assert torch.equal(_random_signs(d, seed, "cpu"), torch.from_numpy(g[f"S_d{d}_s{seed}"]))
+
+
+# ---------------------------------------------------------------- host API
+
+def test_engine_host_logic_and_errors():
+    e = Q.QuashKVEngine(head_dim=64, device="cpu")
+    assert e.total_tokens == 0 and e.num_blocks == 0
+    assert e.compression_ratio() == 1.0
+    assert "head_dim=64" in repr(e) and "key_bits=3" in repr(e)
+    with pytest.raises(ValueError, match="No compressed KV blocks"):
+        e.attention(torch.zeros(1, 2, 1, 64))
+    with pytest.raises(RuntimeError, match="runs on the GPU"):
+        e.append(torch.zeros(1, 2, 4, 64), torch.zeros(1, 2, 4, 64))
+    with pytest.raises(ValueError, match="at least 2"):
+        Q.InnerProductQuantizer(d=128, total_bits=1, device="cpu")
+
+
+def test_cpu_tensors_raise_no_fallback():
+    q = Q.MSEQuantizer(64, device="cpu")
+    with pytest.raises(RuntimeError, match="runs on the GPU"):
+        q.compress(torch.randn(2, 64))
+    with pytest.raises(RuntimeError, match="runs on the GPU"):
+        Q.pack_bits(torch.zeros(2, 64, dtype=torch.uint8), 3)
+    assert Q.pack_bits(torch.zeros(2, 8, dtype=torch.uint8), 8).shape == (2, 8)  # passthrough
+    with pytest.raises(ValueError, match="Unsupported bits"):
+        Q.pack_bits(torch.zeros(2, 8, dtype=torch.uint8), 5)
+
+
+def test_hf_cache_host_logic():
+    from quashkv_amd.integrations.hf_cache import QuashKVCache, QuashKVCacheConfig
+    c = QuashKVCache(num_layers=4, head_dim=64, device="cpu")
+    assert [e.seed for e in c.engines] == [42, 43, 44, 45]
+    assert len(c) == 4 and c.get_max_cache_length() is None
+    k, v = c[0]
+    assert k.numel() == 0 and v.numel() == 0
+    st = c.compression_stats()
+    assert st["overall_compression_ratio"] == 0 and st["tokens_per_layer"] == [0] * 4
+    cfg = QuashKVCacheConfig(key_bits=4, value_bits=4, seed=7)
+    c2 = QuashKVCache(num_layers=2, head_dim=128, config=cfg, device="cpu")
+    assert c2.engines[0].key_bits == 4 and c2.engines[1].seed == 8
