@@ -139,7 +139,7 @@ __global__ __launch_bounds__(kTile) void split_kernel(
 #pragma unroll
       for (int i = 0; i < kRowBlk; ++i) s[i] = 0.f;
       for (int j = 0; j < D; ++j) {
-        const float c = kc[qkv_get_code(krow, j, kb)];
+        const float c = kc[qkv_get_code(krow, j, kb) & 15u];
         const float z = qkv_get_code(qrow, j, qb) ? 1.f : -1.f;
 #pragma unroll
         for (int i = 0; i < kRowBlk; ++i) {
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kTile) void split_kernel(
       for (int tt = tt0; tt < tt0 + kTile / 2; ++tt) {
         const int64_t tk = t0 + tt;
         if (tk >= t_end) break;
-        const float v = vc[qkv_get_code(vbase + tk * pv, pj, vb)] * vn[tt];
+        const float v = vc[qkv_get_code(vbase + tk * pv, pj, vb) & 15u] * vn[tt];
 #pragma unroll
         for (int r = 0; r < kMaxRows; ++r)
           if (r < nr) acc[r] = fmaf(ps[r][tt], v, acc[r]);

@@ -134,8 +134,10 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
   __shared__ float pis[D * D];      // Pi row-major
   __shared__ float cs[D * kRows];   // cs[k * kRows + r] = rotated-domain value
   __shared__ float ns[kRows];
+  __shared__ float cl[16];          // centroid table (codes are masked to 4 bits)
   const int tid = threadIdx.x;
   for (int i = tid; i < D * D; i += kThreads) pis[i] = pi[i];
+  if (tid < 16) cl[tid] = tid < (1 << bits) ? cents[tid] : 0.f;
   const int cb = packed ? bits : 8;
   const int qb = packed ? 1 : 8;
   const int64_t pb = packed ? qkv_row_bytes(D, bits) : D;
@@ -151,7 +153,7 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
         float v = 0.f;
         if (r < nr) {
           const int64_t row = qkv_grouped_row(r0 + r, in_seq, in_gstride);
-          v = cents[qkv_get_code(codes + row * pb, tid, cb)];
+          v = cl[qkv_get_code(codes + row * pb, tid, cb) & 15u];
           if (mode == QKV_MODE_IP) {
             const float sv = qkv_get_code(qjl + row * pq, tid, qb) ? 1.f : -1.f;
             v += qs * sv;
