@@ -120,6 +120,20 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def dense(*tensors: Optional[torch.Tensor]):
+    """Row-major fp32 copies (when needed) of parameter tensors whose raw
+    pointers the kernels read as dense arrays (Pi, S, codebook tables).
+    torch.linalg.qr hands back a column-major Q, so a strided Pi is common."""
+    out = []
+    for t in tensors:
+        if t is not None:
+            if t.dtype != torch.float32:
+                t = t.float()
+            t = t.contiguous()
+        out.append(t)
+    return out
+
+
 def stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 

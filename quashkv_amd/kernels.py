@@ -134,6 +134,11 @@ def attention_call(queries: torch.Tensor, kcodes: torch.Tensor, kqjl: torch.Tens
     q = queries.contiguous()
     if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         q = q.float()
+    Pi, key_centroids, val_centroids, S = N.dense(Pi, key_centroids, val_centroids, S)
+    for name, t in (("kcodes", kcodes), ("kqjl", kqjl), ("knorm", knorm), ("vcodes", vcodes),
+                    ("vnorm", vnorm)):
+        if not t.is_contiguous():
+            raise ValueError(f"attention: {name} must be a contiguous (B, H, T, ...) buffer")
     out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
     N.check(L.qkv_decode_attention(
         q.data_ptr(), N.dtype_code(q.dtype), kcodes.data_ptr(), kqjl.data_ptr(), knorm.data_ptr(),

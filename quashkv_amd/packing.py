@@ -37,9 +37,10 @@ def pack_bits(indices: torch.Tensor, bits: int) -> torch.Tensor:
     *lead, d = indices.shape
     rows = int(torch.Size(lead).numel())
     src = indices.reshape(rows, d).to(torch.uint8).contiguous()
-    out = torch.empty(rows, N.packed_row_bytes(d, bits), dtype=torch.uint8, device=dev)
+    pb = N.packed_row_bytes(d, bits)
+    out = torch.empty(rows, pb, dtype=torch.uint8, device=dev)
     N.check(N.lib().qkv_pack_bits(src.data_ptr(), out.data_ptr(), rows, d, bits, N.stream(dev)))
-    return out.reshape(*lead, -1)
+    return out.reshape(*lead, pb)
 
 
 def unpack_bits(packed: torch.Tensor, bits: int, d: int) -> torch.Tensor:

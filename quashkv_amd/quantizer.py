@@ -30,7 +30,8 @@ def _random_orthogonal(d: int, seed: int, device) -> torch.Tensor:
     gen = torch.Generator(device="cpu").manual_seed(seed)
     a = torch.randn(d, d, generator=gen, dtype=torch.float32)
     q, r = torch.linalg.qr(a)
-    return (q * torch.sign(torch.diag(r)).unsqueeze(0)).to(device)
+    # LAPACK returns Q column-major; the kernels read Pi row-major
+    return (q * torch.sign(torch.diag(r)).unsqueeze(0)).contiguous().to(device)
 
 
 def _random_signs(d: int, seed: int, device) -> torch.Tensor:
@@ -63,6 +64,7 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
     seq = out_seq if out_seq is not None else max(n, 1)
     gst = out_group_stride if out_group_stride is not None else seq
     flags = (N.QKV_FLAG_PACKED if packed else 0) | (N.QKV_FLAG_PRE_ROTATED if pre_rotated else 0)
+    pi, boundaries, centroids, signs = N.dense(pi, boundaries, centroids, signs)
     N.check(N.lib().qkv_compress(
         mode, N.dtype_code(xf.dtype), flags, xf.data_ptr(), n, d, N.ptr(pi),
         boundaries.data_ptr(), centroids.data_ptr(), bits, N.ptr(signs), codes.data_ptr(),
@@ -78,6 +80,7 @@ def decompress_from(mode: int, codes: torch.Tensor, qjl: Optional[torch.Tensor],
     d = pi.shape[0]
     dev = N.require_gpu(codes, norms, pi, what="decompress")
     out = torch.empty(n, d, dtype=out_dtype, device=dev)
+    pi, centroids, signs = N.dense(pi, centroids, signs)
     seq = in_seq if in_seq is not None else max(n, 1)
     gst = in_group_stride if in_group_stride is not None else seq
     N.check(N.lib().qkv_decompress(
@@ -199,9 +202,10 @@ class InnerProductQuantizer:
         nr = norms.expand(lead).reshape(n).float().contiguous()
         out = torch.empty(n, dtype=torch.float32, device=dev)
         cb = self.mse_quantizer.codebook
+        S, cents = N.dense(self.S, cb.centroids)
         N.check(N.lib().qkv_ip_dot(codes.data_ptr(), bits.data_ptr(), nr.data_ptr(), qr.data_ptr(),
-                                   n, self.d, cb.centroids.data_ptr(), cb.n_levels,
-                                   self.S.data_ptr(), float(self.qjl_scale), out.data_ptr(),
+                                   n, self.d, cents.data_ptr(), cb.n_levels,
+                                   S.data_ptr(), float(self.qjl_scale), out.data_ptr(),
                                    N.stream(dev)))
         return out.reshape(lead)
 
