@@ -59,13 +59,10 @@ def cpu_baseline(eng, q, n_batch: int, reps: int):
     torch.set_num_threads(os.cpu_count() or 1)
     st = eng._store
     kq, vq = eng.key_quantizer, eng.value_quantizer
-    sl = slice(0, n_batch)
-    kc = torch.from_numpy(R.unpack_bits(st.kcodes[sl, :, :T].cpu().numpy(), 2, D))
-    kb = torch.from_numpy(R.unpack_bits(st.kqjl[sl, :, :T].cpu().numpy(), 1, D))
-    vc = torch.from_numpy(R.unpack_bits(st.vcodes[sl, :, :T].cpu().numpy(), 3, D))
-    blk = dict(kcodes=kc, kbits=kb, knorm=st.knorm[sl, :, :T].cpu(), vcodes=vc,
-               vnorm=st.vnorm[sl, :, :T].cpu())
-    qs = q[sl].float().cpu().reshape(n_batch, HKV, HQ // HKV, D)
+    kc, kb, vc = (t[:n_batch].cpu() for t in st.read_codes(0, T))
+    blk = dict(kcodes=kc, kbits=kb, knorm=st.knorm[:n_batch, :, :T].cpu(), vcodes=vc,
+               vnorm=st.vnorm[:n_batch, :, :T].cpu())
+    qs = q[:n_batch].float().cpu().reshape(n_batch, HKV, HQ // HKV, D)
     args = (kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
             vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
     R.attention_online(qs, [blk], *args)  # warmup
@@ -127,26 +124,13 @@ def main() -> None:
         eng.append(k, v)
         engines.append(eng)
         if c == 0:
-            # time compress of K (IP) + V (MSE) straight into the store
-            st = eng._store
-            kq, vq = eng.key_quantizer, eng.value_quantizer
-            mq = kq.mse_quantizer
-            kr, vr = k.reshape(-1, D), v.reshape(-1, D)
-
-            def do_compress():
-                compress_into(N.QKV_MODE_IP, kr, mq.Pi, mq.codebook.boundaries,
-                              mq.codebook.centroids, 2, kq.S, st.kcodes, st.kqjl, st.knorm,
-                              packed=True, out_seq=T, out_group_stride=st.capacity)
-                compress_into(N.QKV_MODE_MSE, vr, vq.Pi, vq.codebook.boundaries,
-                              vq.codebook.centroids, 3, None, st.vcodes, None, st.vnorm,
-                              packed=True, out_seq=T, out_group_stride=st.capacity)
-
-            do_compress()
-            torch.cuda.synchronize()
+            # time the append path: compress K (IP) + V (MSE) of all 2^21 token-heads
+            # into the packed store
             for _ in range(args.compress_reps):
+                eng.clear()
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
-                do_compress()
+                eng.append(k, v)
                 e1.record()
                 torch.cuda.synchronize()
                 compress_ms.append(e0.elapsed_time(e1))
@@ -156,30 +140,35 @@ def main() -> None:
     gq = torch.Generator(device=dev).manual_seed(7)
     queries = [torch.randn(B, HQ, 1, D, device=dev, generator=gq).to(torch.bfloat16)
                for _ in range(args.copies)]
-    st0 = engines[0]._store
     splits = lib.qkv_attention_splits(B, HQ, HKV, 1, D, T)
     ws_bytes = lib.qkv_attention_workspace_bytes(B, HQ, HKV, 1, D, splits)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty(B, HQ, 1, D, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(D)
+    eng0 = engines[0]
+    kq0, vq0 = eng0.key_quantizer, eng0.value_quantizer
+    kc_h = N.HostFloats(kq0.mse_quantizer.codebook.centroids_host)
+    vc_h = N.HostFloats(vq0.codebook.centroids_host)
+    path = lib.qkv_attention_path(D, KEY_BITS - 1, VAL_BITS, kc_h.ptr, vc_h.ptr,
+                                  eng0._store.capacity, T, splits)
 
     def step(i, ev=None):
         eng = engines[i % args.copies]
         q = queries[i % args.copies]
         st = eng._store
-        kq, vq = eng.key_quantizer, eng.value_quantizer
+        kq = eng.key_quantizer
         mq = kq.mse_quantizer
         N.check(lib.qkv_attention_prepare(q.data_ptr(), N.QKV_BF16, B, HQ, HKV, 1, D,
-                                          mq.Pi.data_ptr(), kq.S.data_ptr(), kq.qjl_scale,
-                                          ws.data_ptr(), ws_bytes, splits, sptr))
+                                          KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr,
+                                          vc_h.ptr, kq.S.data_ptr(), kq.qjl_scale, ws.data_ptr(),
+                                          ws_bytes, splits, sptr))
         if ev is not None:
             ev[0].record(stream)
-        N.check(lib.qkv_attention_partial(st.kcodes.data_ptr(), st.kqjl.data_ptr(),
-                                          st.knorm.data_ptr(), st.vcodes.data_ptr(),
-                                          st.vnorm.data_ptr(), st.capacity, T, B, HQ, HKV, 1, D,
-                                          2, 3, 1, mq.codebook.centroids.data_ptr(),
-                                          vq.codebook.centroids.data_ptr(), scale, 0,
-                                          ws.data_ptr(), ws_bytes, splits, sptr))
+        N.check(lib.qkv_attention_partial(st.kst.data_ptr(), st.knorm.data_ptr(),
+                                          st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, T,
+                                          B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, kc_h.ptr,
+                                          vc_h.ptr, scale, 0, ws.data_ptr(), ws_bytes, splits,
+                                          sptr))
         if ev is not None:
             ev[1].record(stream)
         N.check(lib.qkv_attention_combine(B, HQ, HKV, 1, D, mq.Pi.data_ptr(), out.data_ptr(),
@@ -239,6 +228,7 @@ def main() -> None:
             "batch": B, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "context": T,
             "key_bits": KEY_BITS, "value_bits": VAL_BITS, "query_dtype": "bf16",
             "cache_copies_rotated": args.copies, "n_splits": splits,
+            "kernel_path": "mfma" if path == 1 else "valu",
         },
         "decode_us_per_step": round(step_ms * 1e3, 2),
         "decode_pct_of_hbm_peak": round(100 * step_gbs / PEAK_HBM_GBS, 2),
@@ -246,7 +236,7 @@ def main() -> None:
         "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
                                               / PEAK_HBM_GBS, 2),
         "roofline": {
-            "kernel": "split_kernel (qkv_attention_partial)",
+            "kernel": ("split_mfma" if path == 1 else "split_generic") + " (qkv_attention_partial)",
             "bound": "hbm",
             "achieved": round(partial_gbs, 2),
             "peak": PEAK_HBM_GBS,

@@ -50,6 +50,12 @@ extern "C" {
 #define QKV_MODE_MSE 0 /* MSEQuantizer */
 #define QKV_MODE_IP 1  /* InnerProductQuantizer: (b-1)-bit MSE + 1-bit QJL */
 
+/* code formats of qkv_decompress (store formats: see "Cache store formats") */
+#define QKV_FMT_UNPACKED 0 /* one uint8 per code */
+#define QKV_FMT_PACKED 1   /* pack_bits rows */
+#define QKV_FMT_KPLANES 2  /* K store rows: `bits` MSE planes + QJL plane */
+#define QKV_FMT_VTILES 3   /* V store tiles */
+
 /* compress flags */
 #define QKV_FLAG_PACKED 1      /* write packed rows (else one uint8 per code) */
 #define QKV_FLAG_PRE_ROTATED 2 /* x is already y = u Pi^T: skip norm + rotation
@@ -121,14 +127,81 @@ int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
  * (quashkv/triton_kernels/decompress.py:194-285), MSEQuantizer.decompress
  * (quashkv/quantizer.py:133-147) and QuashKVCache's key/value reconstruction
  * (quashkv/integrations/hf_cache.py:96-121, mode MSE with the key codebook).
- *   packed     1: code rows are packed with `bits` (qjl with 1 bit); 0: uint8
+ *   fmt        QKV_FMT_UNPACKED / PACKED: code rows (qjl rows alike) at grouped
+ *              rows (in_seq, in_group_stride);
+ *              QKV_FMT_KPLANES: K store rows (qjl unused: the row holds it);
+ *              QKV_FMT_VTILES: V store tiles, in_seq tokens per group (from
+ *              token 0), in_group_stride tiles per group, norms at
+ *              group * 32 * in_group_stride + token (MSE mode only)
  *   out        n x d, out_dtype, contiguous */
-int qkv_decompress(int32_t mode, int32_t packed,
+int qkv_decompress(int32_t mode, int32_t fmt,
                    const uint8_t* codes, const uint8_t* qjl, const float* norms,
                    int64_t n, int32_t d, int32_t bits,
                    const float* pi, const float* centroids, const float* signs,
                    float qjl_scale, int64_t in_seq, int64_t in_group_stride,
                    void* out, int32_t out_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cache store formats (the engine's compressed KV cache; see qkv_store.hip).
+ *
+ *   K rows  ("kplanes"): one row per token, (mbits + 1) * d / 8 bytes:
+ *           [MSE bit-plane 0] ... [MSE bit-plane mbits-1] [QJL plane];
+ *           plane r holds bit r of each coordinate's code, coordinate j at
+ *           bit j % 8 of byte j / 8.  Grouped-row addressing as above.
+ *   V tiles ("vtiles"): per (sequence, kv head), tokens in tiles of 32;
+ *           uint32 word[tile][plane k][coordinate j], bit (t % 32) = bit k of
+ *           the code of token t at coordinate j.
+ * Both hold exactly the bits of the reference's pack_bits tensors
+ * (quashkv/engine.py:156-160), re-arranged so that the decode kernel can feed
+ * bit planes to the matrix cores.  d must be a multiple of 32.
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of one K row: (mbits + with_qjl) * d / 8; -1 if unsupported. */
+int64_t qkv_kplanes_row_bytes(int32_t d, int32_t mbits, int32_t with_qjl);
+
+/* Bytes of `tokens` tokens of V tiles (rounded up to whole tiles). */
+int64_t qkv_vtiles_bytes(int32_t d, int32_t vbits, int64_t tokens);
+
+/* n rows of one-uint8-per-code MSE codes (and QJL bits, may be NULL) into K
+ * rows of stride row_bytes at grouped rows (seq, group_stride). */
+int qkv_kplanes_pack(const uint8_t* codes, const uint8_t* qjl, int64_t n, int32_t d,
+                     int32_t mbits, uint8_t* dst, int64_t row_bytes, int64_t seq,
+                     int64_t group_stride, void* stream);
+
+/* Inverse of qkv_kplanes_pack (codes and/or qjl may be NULL). */
+int qkv_kplanes_unpack(const uint8_t* src, int64_t row_bytes, int64_t n, int32_t d,
+                       int32_t mbits, int64_t seq, int64_t group_stride,
+                       uint8_t* codes, uint8_t* qjl, void* stream);
+
+/* codes: groups x S x d uint8 written as tokens [t0, t0 + S) of each group's
+ * V tiles (tiles_per_group tiles per group); other tokens' bits are kept. */
+int qkv_vtiles_pack(const uint8_t* codes, int64_t groups, int64_t S, int32_t d,
+                    int32_t vbits, uint32_t* dst, int64_t tiles_per_group, int64_t t0,
+                    void* stream);
+
+/* Inverse of qkv_vtiles_pack: tokens [t0, t0 + S) -> groups x S x d uint8. */
+int qkv_vtiles_unpack(const uint32_t* src, int64_t groups, int64_t S, int32_t d,
+                      int32_t vbits, int64_t tiles_per_group, int64_t t0, uint8_t* codes,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decode attention over the store.
+ * Replaces QuashKVEngine.attention (quashkv/engine.py:204-299) and
+ * fused_quantized_attention (quashkv/triton_kernels/attention.py:307-394),
+ * with GQA: query head h reads kv head h / (Hq / Hkv).
+ *   q          B x Hq x Q x d, q_dtype, contiguous
+ *   kstore     B x Hkv x t_stride K rows (kbits = MSE bits of the keys)
+ *   knorm      B x Hkv x t_stride fp32
+ *   vstore     B x Hkv x (t_stride / 32) V tiles (vbits)
+ *   vnorm      B x Hkv x t_stride fp32
+ *   t_stride   token capacity (multiple of 32; 64 for the MFMA path)
+ *   T          valid tokens (<= t_stride); causal masks kv_pos > T - Q + i
+ *   kcent_host, vcent_host  HOST arrays of the 2^kbits / 2^vbits centroids
+ *   out        B x Hq x Q x d, out_dtype
+ *   workspace  >= qkv_attention_workspace_bytes(..., n_splits), 256-B aligned
+ * Symmetric codebooks (all Lloyd-Max codebooks are) with d = 128 and
+ * kbits <= 2 run on the integer-MFMA kernel; other shapes on a VALU kernel.
+ * ---------------------------------------------------------------------- */
 
 /* Split-K count the library would use for a decode-attention call. */
 int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
@@ -138,50 +211,45 @@ int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
 int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv,
                                       int32_t Q, int32_t d, int32_t n_splits);
 
-/* Attention over the compressed cache, scored in the rotated domain.
- * Replaces QuashKVEngine.attention (quashkv/engine.py:204-299) and
- * fused_quantized_attention (quashkv/triton_kernels/attention.py:307-394),
- * with GQA: query head h reads KV head h / (Hq / Hkv).
- *   q        B x Hq x Q x d, q_dtype, contiguous
- *   kcodes   B x Hkv x t_stride rows of the key MSE codes (kbits)
- *   kqjl     same rows of the 1-bit QJL signs
- *   knorm    B x Hkv x t_stride fp32; vcodes/vnorm likewise for values (vbits)
- *   packed   1: code rows packed; 0: one uint8 per code
- *   T        valid tokens (<= t_stride); causal masks kv_pos > T - Q + i
- *   out      B x Hq x Q x d, out_dtype
- *   workspace/ws_bytes  >= qkv_attention_workspace_bytes(..., n_splits) */
-int qkv_decode_attention(const void* q, int32_t q_dtype,
-                         const uint8_t* kcodes, const uint8_t* kqjl,
-                         const float* knorm, const uint8_t* vcodes,
+/* 1 if a call with these parameters runs the MFMA kernel, 0 for the VALU
+ * kernel, -1 for invalid arguments. */
+int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
+                           const float* kcent_host, const float* vcent_host,
+                           int64_t t_stride, int64_t T, int32_t n_splits);
+
+int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                         const float* knorm, const uint32_t* vstore,
                          const float* vnorm, int64_t t_stride, int64_t T,
                          int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
                          int32_t d, int32_t kbits, int32_t vbits,
-                         int32_t packed, const float* pi, const float* kcent,
-                         const float* vcent, const float* signs,
+                         const float* pi, const float* kcent_host,
+                         const float* vcent_host, const float* signs,
                          float qjl_scale, float scale, int32_t causal,
                          void* out, int32_t out_dtype, void* workspace,
                          int64_t ws_bytes, int32_t n_splits, void* stream);
 
 /* The three phases qkv_decode_attention runs, exposed so a caller can overlap
  * or time them separately (same arguments and workspace):
- *   prepare  q~ = q Pi^T and w = alpha |q~| S into the workspace
+ *   prepare  q~ = q Pi^T, w = alpha |q~| S and the MFMA query operands
  *            (quashkv/engine.py:237-238, quashkv/triton_kernels/attention.py:94,111)
- *   partial  split-K online softmax over the cache (quashkv/engine.py:245-289,
+ *   partial  split-K softmax partials over the cache (quashkv/engine.py:245-289,
  *            quashkv/triton_kernels/attention.py:97-145)
  *   combine  log-sum-exp merge of the splits, / max(l, 1e-8), x Pi once, store
  *            (quashkv/engine.py:292-297, quashkv/triton_kernels/attention.py:147-149) */
 int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
-                          int32_t Hkv, int32_t Q, int32_t d, const float* pi,
-                          const float* signs, float qjl_scale, void* workspace,
-                          int64_t ws_bytes, int32_t n_splits, void* stream);
-int qkv_attention_partial(const uint8_t* kcodes, const uint8_t* kqjl,
-                          const float* knorm, const uint8_t* vcodes,
-                          const float* vnorm, int64_t t_stride, int64_t T,
-                          int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-                          int32_t kbits, int32_t vbits, int32_t packed,
-                          const float* kcent, const float* vcent, float scale,
-                          int32_t causal, void* workspace, int64_t ws_bytes,
-                          int32_t n_splits, void* stream);
+                          int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                          int32_t vbits, const float* pi, const float* kcent_host,
+                          const float* vcent_host, const float* signs, float qjl_scale,
+                          void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          void* stream);
+int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
+                          const uint32_t* vstore, const float* vnorm,
+                          int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                          int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                          int32_t vbits, const float* kcent_host,
+                          const float* vcent_host, float scale, int32_t causal,
+                          void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          void* stream);
 int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
                           const float* pi, void* out, int32_t out_dtype,
                           void* workspace, int64_t ws_bytes, int32_t n_splits,

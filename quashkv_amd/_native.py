@@ -21,6 +21,7 @@ _lib: Optional[ctypes.CDLL] = None
 QKV_OK, QKV_E_INVALID, QKV_E_UNSUPPORTED, QKV_E_HIP = 0, 1, 2, 3
 QKV_F32, QKV_F16, QKV_BF16 = 0, 1, 2
 QKV_MODE_MSE, QKV_MODE_IP = 0, 1
+QKV_FMT_UNPACKED, QKV_FMT_PACKED, QKV_FMT_KPLANES, QKV_FMT_VTILES = 0, 1, 2, 3
 QKV_FLAG_PACKED, QKV_FLAG_PRE_ROTATED = 1, 2
 
 _DTYPE = {torch.float32: QKV_F32, torch.float16: QKV_F16, torch.bfloat16: QKV_BF16}
@@ -41,16 +42,22 @@ _SIGS = {
                             _p, _p, _p, _i64, _i64, _p]),
     "qkv_decompress": (_i32, [_i32, _i32, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _f32,
                               _i64, _i64, _p, _i32, _p]),
+    "qkv_kplanes_row_bytes": (_i64, [_i32, _i32, _i32]),
+    "qkv_vtiles_bytes": (_i64, [_i32, _i32, _i64]),
+    "qkv_kplanes_pack": (_i32, [_p, _p, _i64, _i32, _i32, _p, _i64, _i64, _i64, _p]),
+    "qkv_kplanes_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p, _p]),
+    "qkv_vtiles_pack": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p]),
+    "qkv_vtiles_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p]),
     "qkv_attention_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64]),
     "qkv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
-    "qkv_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
-                                    _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
-                                    _f32, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
-    "qkv_attention_prepare": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _f32, _p,
-                                     _i64, _i32, _p]),
-    "qkv_attention_partial": (_i32, [_p, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32,
-                                     _i32, _i32, _i32, _i32, _p, _p, _f32, _i32, _p, _i64, _i32,
-                                     _p]),
+    "qkv_attention_path": (_i32, [_i32, _i32, _i32, _p, _p, _i64, _i64, _i32]),
+    "qkv_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
+                                    _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32, _f32, _i32,
+                                    _p, _i32, _p, _i64, _i32, _p]),
+    "qkv_attention_prepare": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
+                                     _p, _p, _p, _f32, _p, _i64, _i32, _p]),
+    "qkv_attention_partial": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                     _i32, _i32, _p, _p, _f32, _i32, _p, _i64, _i32, _p]),
     "qkv_attention_combine": (_i32, [_i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _i64, _i32,
                                      _p]),
 }
@@ -120,6 +127,28 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+def extent(t: torch.Tensor) -> int:
+    """Bytes addressable from t.data_ptr() to the end of t's storage."""
+    st = t.untyped_storage()
+    return st.nbytes() - (t.data_ptr() - st.data_ptr())
+
+
+def require_extent(t: Optional[torch.Tensor], nbytes: int, what: str) -> None:
+    """Host-side bounds check before a kernel writes or reads `nbytes` bytes
+    from t's first element (kernels address raw pointers)."""
+    if t is not None and nbytes > extent(t):
+        raise ValueError(f"{what}: kernel would touch {nbytes} bytes but the buffer has "
+                         f"{extent(t)} from its first element")
+
+
+def grouped_rows(n: int, seq: int, gstride: int) -> int:
+    """Rows spanned by n vectors under grouped-row addressing."""
+    if n <= 0:
+        return 0
+    last = n - 1
+    return (last // seq) * gstride + (last % seq) + 1
+
+
 def dense(*tensors: Optional[torch.Tensor]):
     """Row-major fp32 copies (when needed) of parameter tensors whose raw
     pointers the kernels read as dense arrays (Pi, S, codebook tables).
@@ -136,6 +165,20 @@ def dense(*tensors: Optional[torch.Tensor]):
 
 def stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class HostFloats:
+    """A small fp32 table as a ctypes array (codebook centroids passed by
+    value to the attention entry points)."""
+
+    def __init__(self, values):
+        vals = [float(v) for v in values]
+        self.n = len(vals)
+        self.arr = (ctypes.c_float * max(self.n, 1))(*vals)
+
+    @property
+    def ptr(self) -> int:
+        return ctypes.addressof(self.arr)
 
 
 def packed_row_bytes(d: int, bits: int) -> int:

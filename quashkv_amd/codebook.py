@@ -183,6 +183,9 @@ class LloydMaxCodebook:
         c, t = _solved(d, bits, bool(use_exact_pdf))
         self.centroids = torch.tensor(c, dtype=torch.float32)
         self.boundaries = torch.tensor(t, dtype=torch.float32)
+        # fp32 values as Python floats: the attention entry points take the
+        # centroids by value (no device round trip)
+        self.centroids_host = tuple(self.centroids.tolist())
 
     def _tables_on(self, device: torch.device):
         if self.centroids.device != device:

@@ -1,47 +1,124 @@
-// Split-K decode attention over the compressed cache (generic VALU path).
+// Split-K decode attention over the compressed cache store.
 //
 // score(q, t) = n_k,t * (sum_j q~_j c_k[code_tj] + alpha sum_j |q~_j| S_j (2b_tj - 1)) * scale
-// out         = (sum_t softmax(score)_t n_v,t c_v[vcode_t]) Pi
-// with q~ = q Pi^T.  Reference: quashkv/engine.py:204-299 (naive) and
+// out         = (sum_t softmax(score)_t n_v,t c_v[vcode_t]) Pi,      q~ = q Pi^T
+// Reference: quashkv/engine.py:204-299 (naive) and
 // quashkv/triton_kernels/attention.py:55-149 (online softmax).  Unlike the
 // reference, values are accumulated in the ROTATED domain and un-rotated once
 // per query row in the combine kernel (linearity of x -> x Pi).
-//
-// Kernels:
-//   qrot_kernel    q~ and w = alpha |q~| S for every query row (once per call)
-//   split_kernel   one workgroup per (split, kv-head x row-chunk, batch):
-//                  online softmax over its token range, partial (m, l, O~)
-//   combine_kernel merges the splits' partials (log-sum-exp), divides by
-//                  max(l, 1e-8) and applies Pi once.
 // GQA: query head h reads kv head h / G; the G*Q query rows of one kv head
-// ("rows") share every K/V byte the workgroup streams.
+// ("rows") share every K/V byte a workgroup streams.
+//
+// Cache store (see qkv_store.hip): K rows are bit-plane major
+// [MSE plane 0..mbits-1][QJL plane]; V is in 32-token bit-plane tiles.
+//
+// Two partial-softmax kernels write the same (m, l, O~) split partials, and
+// one combine kernel merges them:
+//
+//   split_mfma   (d = 128, MSE key bits 1-2, value bits 1-4, symmetric
+//                 codebooks).  Integer MFMA on bit planes:
+//     * a symmetric codebook is a sum of odd Walsh functions of the code bits,
+//       c[code] = sum_S g_S prod_{k in S} (2 b_k - 1), so every score and every
+//       value coordinate is a weighted sum of 0/1 bit planes;
+//     * a 0/1 plane becomes int8 MFMA operands with ONE v_and per 4 bytes:
+//       word & (0x01010101 << i) leaves bit i of each byte in place, i.e. the
+//       byte value is b * 2^i (b * -128 for i = 7);
+//     * the other operand carries the real weights as 28-bit fixed point split
+//       into four int8 digits, pre-divided by the byte's 2^i, so the i32
+//       accumulators are exact; the digit rows are recombined in fp32.
+//     Scores: C[4 rows x 4 digits][16 tokens] += A(query weights)[16][64] x
+//     B(K planes)[64][16].  Values: C[16 coords][4 rows x 4 digits] +=
+//     A(V planes)[16][64 tokens] x B(p * n_v digits)[64 tokens][16].
+//     Scores of a split (<= 2048 tokens) are kept in LDS, so the softmax max is
+//     known before the value pass and the integer accumulators never rescale.
+//   split_generic (any supported shape): VALU, one token per thread.
 #include <math.h>
 
 #include "qkv_common.h"
 
+typedef int qkv_v4i __attribute__((ext_vector_type(4)));
+
 namespace {
 
-constexpr int kTile = 256;     // tokens per tile == threads per workgroup
-constexpr int kMaxRows = 32;   // query rows per workgroup (row chunk)
-constexpr int kRowBlk = 8;     // rows scored per pass over a key row
+// ------------------------------------------------------------ parameters
 
-struct AttnWs {
-  float* qw;      // [B][Hkv][R][2][D]   q~ then w
-  float* part_o;  // [S][B][Hkv][R][D]   un-normalised rotated-domain outputs
-  float* part_ml; // [S][B][Hkv][R][2]   running max, running sum
+struct Tables {
+  float kc[16];      // key MSE centroids
+  float vc[16];      // value centroids
+  float kg[4];       // key Walsh coefficient of (2 b_r - 1), r < mbits
+  float kconst;      // g_empty - sum_r kg[r]
+  float vg[8];       // value Walsh coefficients, odd subsets (odd_subset order)
+  float vconst;      // g_empty - sum vg (the plane form's constant)
+  int mfma_ok;       // both codebooks admit the plane decomposition
 };
 
-__host__ __device__ inline int64_t ws_qw_floats(int B, int Hkv, int R, int D) {
-  return int64_t(B) * Hkv * R * 2 * D;
+// Odd-size subsets of the code bits (bit masks), in a fixed order shared by
+// the host (coefficients) and the device (plane words).
+__host__ __device__ constexpr uint32_t odd_subset(int bits, int s) {
+  return bits == 1 ? 1u
+       : bits == 2 ? (s == 0 ? 1u : 2u)
+       : bits == 3 ? (s < 3 ? (1u << s) : 7u)
+       : (s < 4 ? (1u << s) : (s == 4 ? 7u : s == 5 ? 11u : s == 6 ? 13u : 14u));
 }
-__host__ __device__ inline int64_t ws_po_floats(int S, int B, int Hkv, int R, int D) {
-  return int64_t(S) * B * Hkv * R * D;
-}
-__host__ __device__ inline int64_t ws_ml_floats(int S, int B, int Hkv, int R) {
-  return int64_t(S) * B * Hkv * R * 2;
+__host__ __device__ constexpr int n_odd_subsets(int bits) {
+  return bits == 1 ? 1 : bits == 2 ? 2 : bits == 3 ? 4 : 8;
 }
 
-// q~_j = sum_k q_k Pi[j][k];  w_j = alpha |q~_j| S_j.  One block per query row.
+constexpr int kSplitMax = 2048;  // tokens per split on the MFMA path (LDS scores)
+constexpr int kRowsM = 4;        // query rows per workgroup on the MFMA path
+constexpr int kNUMax = 6;        // score MFMAs per 16 tokens (d = 128, 2 MSE bits)
+
+// ------------------------------------------------------------ workspace
+
+constexpr int kRowsG = 32;       // query rows per workgroup on the generic path
+constexpr int kTileG = 256;      // tokens per tile == threads on the generic path
+
+struct WsLayout {
+  int64_t qw, aq, rowc, po, pml, total;  // byte offsets
+};
+
+inline WsLayout ws_layout(int B, int Hkv, int R, int D, int S) {
+  WsLayout w;
+  const int64_t bhk = int64_t(B) * Hkv;
+  const int64_t chunks = (R + kRowsM - 1) / kRowsM;
+  int64_t off = 0;
+  w.qw = off;   off += bhk * R * 2 * D * 4;                     // generic: q~, w
+  w.aq = off;   off += bhk * chunks * kNUMax * 64 * 16;        // MFMA: query operands
+  w.rowc = off; off += bhk * chunks * kRowsM * 2 * 4;          // MFMA: row constants
+  w.po = off;   off += int64_t(S) * bhk * R * D * 4;           // split partial O~
+  w.pml = off;  off += int64_t(S) * bhk * R * 2 * 4;           // split partial (m, l)
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+T* at(void* base, int64_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// ------------------------------------------------------------ store access
+
+template <int D>
+__device__ __forceinline__ uint32_t k_code(const uint8_t* __restrict__ row, int j, int mbits) {
+  uint32_t c = 0;
+  for (int p = 0; p < mbits; ++p) c |= ((row[p * (D / 8) + (j >> 3)] >> (j & 7)) & 1u) << p;
+  return c;
+}
+template <int D>
+__device__ __forceinline__ uint32_t k_qjl(const uint8_t* __restrict__ row, int j, int mbits) {
+  return (row[mbits * (D / 8) + (j >> 3)] >> (j & 7)) & 1u;
+}
+// words: the vbits plane words of token t's tile at coordinate j (stride D)
+__device__ __forceinline__ uint32_t v_code(const uint32_t* __restrict__ w, int64_t stride,
+                                           int t, int vbits) {
+  uint32_t c = 0;
+  for (int k = 0; k < vbits; ++k) c |= ((w[k * stride] >> (t & 31)) & 1u) << k;
+  return c;
+}
+
+// ------------------------------------------------------------ generic path
+
+// q~ = q Pi^T and w = alpha |q~| S per query row, into qw[b][hkv][r][2][D].
 template <int D>
 __global__ __launch_bounds__(128) void qrot_kernel(const void* __restrict__ q, int q_dtype,
                                                    const float* __restrict__ pi,
@@ -70,19 +147,18 @@ __global__ __launch_bounds__(128) void qrot_kernel(const void* __restrict__ q, i
 }
 
 template <int D>
-__global__ __launch_bounds__(kTile) void split_kernel(
-    const float* __restrict__ qw, const uint8_t* __restrict__ kcodes,
-    const uint8_t* __restrict__ kqjl, const float* __restrict__ knorm,
-    const uint8_t* __restrict__ vcodes, const float* __restrict__ vnorm, int64_t t_stride,
-    int64_t T, int Hkv, int R, int Q, int row_chunks, int kbits, int vbits, int packed,
-    const float* __restrict__ kcent, const float* __restrict__ vcent, float scale, int causal,
-    int64_t split_len, int n_splits, float* __restrict__ part_o, float* __restrict__ part_ml) {
-  __shared__ float qs[kMaxRows][D];
-  __shared__ float ws[kMaxRows][D];
-  __shared__ float ps[kMaxRows][kTile];   // scores, then probabilities; reused at the end
-  __shared__ float vn[kTile];
-  __shared__ float red[kMaxRows][4];
-  __shared__ float ms[kMaxRows], ls[kMaxRows], al[kMaxRows];
+__global__ __launch_bounds__(kTileG) void split_generic(
+    const float* __restrict__ qw, const uint8_t* __restrict__ kst,
+    const float* __restrict__ knorm, const uint32_t* __restrict__ vst,
+    const float* __restrict__ vnorm, int64_t t_stride, int64_t T, int Hkv, int R, int Q,
+    int row_chunks, int mbits, int vbits, Tables tb, float scale, int causal,
+    int64_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  __shared__ float qs[kRowsG][D];
+  __shared__ float ws[kRowsG][D];
+  __shared__ float ps[kRowsG][kTileG];  // scores, then probabilities; reused at the end
+  __shared__ float vn[kTileG];
+  __shared__ float red[kRowsG][4];
+  __shared__ float ms[kRowsG], ls[kRowsG], al[kRowsG];
   __shared__ float kc[16], vc[16];
 
   const int split = blockIdx.x;
@@ -90,29 +166,27 @@ __global__ __launch_bounds__(kTile) void split_kernel(
   const int chunk = blockIdx.y - hkv * row_chunks;
   const int b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r_begin = chunk * kMaxRows;
-  const int nr = min(kMaxRows, R - r_begin);
+  const int r_begin = chunk * kRowsG;
+  const int nr = min(kRowsG, R - r_begin);
 
-  const int kb = packed ? kbits : 8, qb = packed ? 1 : 8, vb = packed ? vbits : 8;
-  const int64_t pk = qkv_row_bytes(D, kb), pq = qkv_row_bytes(D, qb), pv = qkv_row_bytes(D, vb);
+  const int64_t krb = int64_t(mbits + 1) * D / 8;
   const int64_t bh = int64_t(b) * Hkv + hkv;
-  const uint8_t* kbase = kcodes + bh * t_stride * pk;
-  const uint8_t* qbase = kqjl + bh * t_stride * pq;
-  const uint8_t* vbase = vcodes + bh * t_stride * pv;
+  const uint8_t* kbase = kst + bh * t_stride * krb;
+  const uint32_t* vbase = vst + bh * (t_stride / 32) * vbits * D;
   const float* knb = knorm + bh * t_stride;
   const float* vnb = vnorm + bh * t_stride;
 
   const float* qsrc = qw + (bh * R + r_begin) * 2 * D;
-  for (int i = tid; i < nr * D; i += kTile) {
+  for (int i = tid; i < nr * D; i += kTileG) {
     const int r = i / D, j = i - r * D;
     qs[r][j] = qsrc[r * 2 * D + j];
     ws[r][j] = qsrc[r * 2 * D + D + j];
   }
   if (tid < 16) {
-    kc[tid] = tid < (1 << kbits) ? kcent[tid] : 0.f;
-    vc[tid] = tid < (1 << vbits) ? vcent[tid] : 0.f;
+    kc[tid] = tb.kc[tid];
+    vc[tid] = tb.vc[tid];
   }
-  if (tid < kMaxRows) {
+  if (tid < kRowsG) {
     ms[tid] = -INFINITY;
     ls[tid] = 0.f;
   }
@@ -120,36 +194,34 @@ __global__ __launch_bounds__(kTile) void split_kernel(
   const int64_t t_begin = int64_t(split) * split_len;
   const int64_t t_end = min<int64_t>(T, t_begin + split_len);
 
-  // PV thread layout: coordinate j, token half hf of the tile
-  const int pj = tid & 127, hf = tid >> 7;
-  float acc[kMaxRows];
+  const int pj = tid & 127, hf = tid >> 7;  // PV layout: coordinate, token half
+  float acc[kRowsG];
 #pragma unroll
-  for (int r = 0; r < kMaxRows; ++r) acc[r] = 0.f;
+  for (int r = 0; r < kRowsG; ++r) acc[r] = 0.f;
   __syncthreads();
 
-  for (int64_t t0 = t_begin; t0 < t_end; t0 += kTile) {
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kTileG) {
     const int64_t t = t0 + tid;
     const bool valid = t < t_end;
-    // ---- scores: one token per thread, rows in blocks of kRowBlk
-    const uint8_t* krow = kbase + (valid ? t : t_begin) * pk;
-    const uint8_t* qrow = qbase + (valid ? t : t_begin) * pq;
-    const float kn = valid ? knb[t] * scale : 0.f;
-    for (int rb = 0; rb < nr; rb += kRowBlk) {
-      float s[kRowBlk];
+    const int64_t tc = valid ? t : t_begin;
+    const uint8_t* krow = kbase + tc * krb;
+    const float kn = valid ? knb[tc] * scale : 0.f;
+    for (int rb = 0; rb < nr; rb += 8) {
+      float s[8];
 #pragma unroll
-      for (int i = 0; i < kRowBlk; ++i) s[i] = 0.f;
+      for (int i = 0; i < 8; ++i) s[i] = 0.f;
       for (int j = 0; j < D; ++j) {
-        const float c = kc[qkv_get_code(krow, j, kb) & 15u];
-        const float z = qkv_get_code(qrow, j, qb) ? 1.f : -1.f;
+        const float c = kc[k_code<D>(krow, j, mbits) & 15u];
+        const float z = k_qjl<D>(krow, j, mbits) ? 1.f : -1.f;
 #pragma unroll
-        for (int i = 0; i < kRowBlk; ++i) {
-          const int r = min(rb + i, kMaxRows - 1);
+        for (int i = 0; i < 8; ++i) {
+          const int r = min(rb + i, kRowsG - 1);
           s[i] = fmaf(qs[r][j], c, s[i]);
           s[i] = fmaf(ws[r][j], z, s[i]);
         }
       }
 #pragma unroll
-      for (int i = 0; i < kRowBlk; ++i) {
+      for (int i = 0; i < 8; ++i) {
         const int r = rb + i;
         if (r < nr) {
           float v = kn * s[i];
@@ -162,10 +234,9 @@ __global__ __launch_bounds__(kTile) void split_kernel(
         }
       }
     }
-    vn[tid] = valid ? vnb[t] : 0.f;
+    vn[tid] = valid ? vnb[tc] : 0.f;
     __syncthreads();
 
-    // ---- tile max per row
     for (int r = 0; r < nr; ++r) {
       const float m = qkv_wave_max(ps[r][tid]);
       if (lane == 0) red[r][wave] = m;
@@ -179,7 +250,6 @@ __global__ __launch_bounds__(kTile) void split_kernel(
       ms[tid] = mn;
     }
     __syncthreads();
-    // ---- probabilities and row sums
     for (int r = 0; r < nr; ++r) {
       const float mn = ms[r];
       const float p = (mn == -INFINITY) ? 0.f : expf(ps[r][tid] - mn);
@@ -190,35 +260,34 @@ __global__ __launch_bounds__(kTile) void split_kernel(
     __syncthreads();
     if (tid < nr) ls[tid] = ls[tid] * al[tid] + (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
 
-    // ---- P V in the rotated domain
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r) acc[r] *= (r < nr) ? al[r] : 1.f;
+    for (int r = 0; r < kRowsG; ++r) acc[r] *= (r < nr) ? al[r] : 1.f;
     if (pj < D) {
-      const int tt0 = hf * (kTile / 2);
-      for (int tt = tt0; tt < tt0 + kTile / 2; ++tt) {
+      const int tt0 = hf * (kTileG / 2);
+      for (int tt = tt0; tt < tt0 + kTileG / 2; ++tt) {
         const int64_t tk = t0 + tt;
         if (tk >= t_end) break;
-        const float v = vc[qkv_get_code(vbase + tk * pv, pj, vb) & 15u] * vn[tt];
+        const uint32_t* w = vbase + (tk >> 5) * vbits * D + pj;
+        const float v = vc[v_code(w, D, static_cast<int>(tk & 31), vbits) & 15u] * vn[tt];
 #pragma unroll
-        for (int r = 0; r < kMaxRows; ++r)
+        for (int r = 0; r < kRowsG; ++r)
           if (r < nr) acc[r] = fmaf(ps[r][tt], v, acc[r]);
       }
     }
     __syncthreads();
   }
 
-  // ---- reduce the two token halves and write the partials
-  float* red_o = &ps[0][0];  // kMaxRows x 128 floats
+  float* red_o = &ps[0][0];  // kRowsG x 128 floats
   if (hf == 1 && pj < D) {
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r)
+    for (int r = 0; r < kRowsG; ++r)
       if (r < nr) red_o[r * 128 + pj] = acc[r];
   }
   __syncthreads();
   const int64_t base = ((int64_t(split) * gridDim.z + b) * Hkv + hkv) * R + r_begin;
   if (hf == 0 && pj < D) {
 #pragma unroll
-    for (int r = 0; r < kMaxRows; ++r)
+    for (int r = 0; r < kRowsG; ++r)
       if (r < nr) part_o[(base + r) * D + pj] = acc[r] + red_o[r * 128 + pj];
   }
   if (tid < nr) {
@@ -226,6 +295,361 @@ __global__ __launch_bounds__(kTile) void split_kernel(
     part_ml[(base + tid) * 2 + 1] = ls[tid];
   }
 }
+
+// ------------------------------------------------------------ MFMA path
+
+__device__ __forceinline__ qkv_v4i mfma_i8(qkv_v4i a, qkv_v4i b, qkv_v4i c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int64_t shfl_xor_i64(int64_t v, int mask) {
+  const int lo = __shfl_xor(static_cast<int>(static_cast<uint64_t>(v) & 0xffffffffu), mask, 64);
+  const int hi = __shfl_xor(static_cast<int>(static_cast<uint64_t>(v) >> 32), mask, 64);
+  return static_cast<int64_t>((static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) |
+                              static_cast<uint32_t>(lo));
+}
+
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += shfl_xor_i64(v, o);
+  return v;
+}
+
+// Wait states between an MFMA chain and the first VALU read of its result.
+// The compiler's padding for this hazard was found short when a branch sits
+// between the last MFMA and the read (3 wait states on the taken path, where
+// an 8-pass XDL result needs more), which returned stale accumulators.  The
+// scheduling barriers keep the reads after an explicit 20-wait-state pad,
+// enough for the longest (16-pass) MFMA.
+__device__ __forceinline__ void mfma_settle() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 3" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Query operands for the score MFMA.  One workgroup per (b, kv head, chunk of
+// 4 rows).  Row bit p of a K row (plane-major) has weight W_p:
+//   MSE plane r, coordinate j:  2 kg[r] q~_j
+//   QJL plane,   coordinate j:  2 alpha |q~_j| S_j
+// and Z_p = round(W_p 2^Fq / s_i) with s_i = 2^i (i < 7) or -128 (i = 7) the
+// byte value of a set bit after the mask (0x01010101 << i).  Z has 28 bits:
+// digits d0..d2 in [0, 127] and a signed top digit d3, Z = sum_v 2^(7v) d_v.
+// Operand register layout: aq[(bhc * NU + u) * 64 + lane] (4 dwords), lane
+// (m = 4 row + digit, g = lane / 16); byte beta of dword e <-> row bit
+// 32 (g DPL + u / 2) + 8 beta + 4 (u % 2) + e.
+template <int D, int MB>
+__global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, int q_dtype,
+                                                    const float* __restrict__ pi,
+                                                    const float* __restrict__ signs,
+                                                    float alpha, int Hq, int Hkv, int Q, int R,
+                                                    int chunks, Tables tb,
+                                                    qkv_v4i* __restrict__ aq,
+                                                    float* __restrict__ rowc) {
+  constexpr int KRB = (MB + 1) * D / 8;
+  constexpr int DPL = KRB / 16;
+  constexpr int NU = 2 * DPL;
+  __shared__ float qs[kRowsM][D];
+  __shared__ float qt[kRowsM][D];
+  __shared__ float wv[kRowsM][D];
+  __shared__ int fqs[kRowsM];
+
+  const int bhc = blockIdx.x;
+  const int chunk = bhc % chunks;
+  const int bh = bhc / chunks;
+  const int hkv = bh % Hkv, b = bh / Hkv;
+  const int G = Hq / Hkv;
+  const int r0 = chunk * kRowsM;
+  const int nr = min(kRowsM, R - r0);
+  const int tid = threadIdx.x;
+
+  for (int i = tid; i < kRowsM * D; i += 256) {
+    const int r = i / D, j = i - r * D;
+    float v = 0.f;
+    if (r < nr) {
+      const int row = r0 + r;
+      const int g = row / Q, qi = row - g * Q;
+      const int h = hkv * G + g;
+      v = qkv_load(q, ((int64_t(b) * Hq + h) * Q + qi) * D + j, q_dtype);
+    }
+    qs[r][j] = v;
+  }
+  __syncthreads();
+  for (int i = tid; i < kRowsM * D; i += 256) {
+    const int r = i / D, j = i - r * D;
+    const float* prow = pi + int64_t(j) * D;
+    float acc = 0.f;
+    for (int k = 0; k < D; ++k) acc = fmaf(qs[r][k], prow[k], acc);
+    qt[r][j] = acc;
+    wv[r][j] = alpha * fabsf(acc) * signs[j];
+  }
+  __syncthreads();
+  // per-row scale exponent and constant (one wave per row)
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    float kgmax = 0.f;
+#pragma unroll
+    for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+    float mq = 0.f, mw = 0.f, sq = 0.f, sw = 0.f;
+    for (int j = lane; j < D; j += 64) {
+      mq = fmaxf(mq, fabsf(qt[wave][j]));
+      mw = fmaxf(mw, fabsf(wv[wave][j]));
+      sq += qt[wave][j];
+      sw += wv[wave][j];
+    }
+    mq = qkv_wave_max(mq);
+    mw = qkv_wave_max(mw);
+    sq = qkv_wave_sum(sq);
+    sw = qkv_wave_sum(sw);
+    if (lane == 0) {
+      const float wmax = 2.f * fmaxf(kgmax * mq, mw);
+      int e = 0;
+      if (wmax > 0.f) frexpf(wmax, &e);  // wmax = f 2^e, f in [0.5, 1)
+      const int fq = wmax > 0.f ? 27 - e : 0;
+      fqs[wave] = fq;
+      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 0] = tb.kconst * sq - sw;
+      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 1] = ldexpf(1.f, -fq);
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < NU * 64 * 4; idx += 256) {
+    const int e = idx & 3, ln = (idx >> 2) & 63, u = idx >> 8;
+    const int m = ln & 15, g = ln >> 4;
+    const int qrow = m >> 2, v = m & 3;
+    const int i = 4 * (u & 1) + e;
+    uint32_t word = 0;
+    if (qrow < nr) {
+#pragma unroll
+      for (int beta = 0; beta < 4; ++beta) {
+        const int p = 32 * (g * DPL + (u >> 1)) + 8 * beta + i;
+        const int region = p / D, j = p - region * D;
+        const float W = region < MB ? 2.f * tb.kg[region] * qt[qrow][j] : 2.f * wv[qrow][j];
+        float zf = ldexpf(W, fqs[qrow] - i);
+        if (i == 7) zf = -zf;
+        const int Z = static_cast<int>(rintf(zf));
+        const int dg = v < 3 ? ((Z >> (7 * v)) & 127) : (Z >> 21);
+        word |= (static_cast<uint32_t>(dg) & 0xffu) << (8 * beta);
+      }
+    }
+    aq[(int64_t(bhc) * NU + u) * 64 + ln][e] = static_cast<int>(word);
+  }
+}
+
+template <int D, int MB, int VB>
+__global__ __launch_bounds__(256) void split_mfma(
+    const qkv_v4i* __restrict__ aq, const float* __restrict__ rowc,
+    const uint8_t* __restrict__ kst, const float* __restrict__ knorm,
+    const uint32_t* __restrict__ vst, const float* __restrict__ vnorm, int64_t t_stride,
+    int64_t T, int Hkv, int R, int Q, int chunks, float scale, int causal, int64_t split_len,
+    Tables tb, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  constexpr int KRB = (MB + 1) * D / 8;  // K row bytes
+  constexpr int DPL = KRB / 16;          // row dwords per lane group
+  constexpr int NU = 2 * DPL;            // score MFMAs per 16 tokens
+  constexpr int NP = n_odd_subsets(VB);  // value planes
+  constexpr int MTW = D / 64;            // 16-coordinate tiles per wave
+  constexpr int NT = kSplitMax / 64;     // max 64-token tiles per split
+  static_assert(KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
+
+  // scores [tile][row][64]; rewritten in place as value-MFMA digits
+  // [tile][col = 4 row + digit][64 K positions] (1 KB per tile either way)
+  __shared__ float sbuf[NT][kRowsM][64];
+  __shared__ float vn[kSplitMax];
+  __shared__ float red_m[4][kRowsM];
+  __shared__ float red_v[4];
+  __shared__ float lsum_s[kRowsM];
+  __shared__ long long usum_s[kRowsM];  // sum_t Z_t s_t per row, exact
+
+  const int split = blockIdx.x;
+  const int hkv = blockIdx.y / chunks, chunk = blockIdx.y - (blockIdx.y / chunks) * chunks;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int r0 = chunk * kRowsM;
+  const int nr = min(kRowsM, R - r0);
+  const int64_t bh = int64_t(b) * Hkv + hkv;
+  const int64_t bhc = bh * chunks + chunk;
+  const int64_t ts = int64_t(split) * split_len;
+  const int64_t te = min<int64_t>(T, ts + split_len);
+  const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
+
+  // ---------------- phase 1: scores of every token of the split -> LDS
+  qkv_v4i a[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) a[u] = aq[(bhc * NU + u) * 64 + lane];
+  const float cr = rowc[(bhc * kRowsM + lg) * 2 + 0];
+  const float fq = rowc[(bhc * kRowsM + lg) * 2 + 1];
+  const bool row_ok = lg < nr;
+  const int qi = (r0 + lg) % Q;
+
+  float mloc = -INFINITY, vmax = 0.f;
+  const int ngroups = (ntok + 15) >> 4;
+  const uint8_t* kb = kst + bh * t_stride * KRB;
+  for (int gi = wave; gi < ngroups; gi += 4) {
+    const int tl = gi * 16 + ln;
+    const int64_t t = ts + tl;
+    const int64_t tc = min<int64_t>(t, te - 1);
+    const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + tc * KRB) + lg * DPL;
+    uint32_t kd[DPL];
+#pragma unroll
+    for (int x = 0; x < DPL; ++x) kd[x] = krow[x];
+    const float kn = knorm[bh * t_stride + tc];
+    qkv_v4i acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const uint32_t x = kd[u >> 1];
+      const int sh = 4 * (u & 1);
+      qkv_v4i bo;
+      bo[0] = static_cast<int>(x & (0x01010101u << sh));
+      bo[1] = static_cast<int>(x & (0x02020202u << sh));
+      bo[2] = static_cast<int>(x & (0x04040404u << sh));
+      bo[3] = static_cast<int>(x & (0x08080808u << sh));
+      acc = mfma_i8(a[u], bo, acc);
+    }
+    mfma_settle();
+    const float z = static_cast<float>(acc[0]) + 128.f * static_cast<float>(acc[1]) +
+                    16384.f * static_cast<float>(acc[2]) + 2097152.f * static_cast<float>(acc[3]);
+    float s = kn * scale * fmaf(z, fq, cr);
+    const int valid = static_cast<int>(t < te) & static_cast<int>(row_ok) &
+                      (static_cast<int>(causal == 0) | static_cast<int>(t <= T - Q + qi));
+    s = valid ? s : -INFINITY;
+    sbuf[tl >> 6][lg][tl & 63] = s;
+    mloc = fmaxf(mloc, s);
+    if (lg == 0) {
+      const float vv = (t < te) ? vnorm[bh * t_stride + tc] : 0.f;
+      vn[tl] = vv;
+      vmax = fmaxf(vmax, vv);
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+  vmax = qkv_wave_max(vmax);
+  if (ln == 0) red_m[wave][lg] = mloc;
+  if (lane == 0) red_v[wave] = vmax;
+  __syncthreads();
+
+  // ---------------- phase 1.5: p = exp(s - m), value digits (wave w <-> row w)
+  const float m_q = fmaxf(fmaxf(red_m[0][wave], red_m[1][wave]),
+                          fmaxf(red_m[2][wave], red_m[3][wave]));
+  const float vmx = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
+  int ev = 0;
+  if (vmx > 0.f) frexpf(vmx, &ev);
+  const int Fv = vmx > 0.f ? 27 - ev : 0;  // vmx 2^Fv < 2^27
+  const int ntiles = (ntok + 63) >> 6;
+
+  float sreg[NT];
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) sreg[tt] = (tt < ntiles) ? sbuf[tt][wave][lane] : -INFINITY;
+  __syncthreads();
+
+  // token (lane) of a 64-token tile -> K position of the value MFMA:
+  // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
+  const int ii = lane & 7;
+  const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
+  uint8_t* pbase = reinterpret_cast<uint8_t*>(&sbuf[0][0][0]);
+  float lsum = 0.f;
+  int64_t usum = 0;  // sum_t Z_t s_t: what an all-ones plane would accumulate
+  const bool live = wave < nr && m_q > -INFINITY;
+#pragma unroll
+  for (int tt = 0; tt < NT; ++tt) {
+    if (tt < ntiles) {
+      const int tl = tt * 64 + lane;
+      float pv = 0.f;
+      if (live && tl < ntok) {
+        const float p = expf(sreg[tt] - m_q);
+        lsum += p;
+        pv = p * vn[tl];
+      }
+      const int X = static_cast<int>(rintf(ldexpf(pv, Fv - ii)));  // Z_t s_t = X 2^i
+      usum += static_cast<int64_t>(X) << ii;
+      const int Z = ii == 7 ? -X : X;
+      uint8_t* dst = pbase + tt * 1024 + (4 * wave) * 64 + kpos;
+      dst[0] = static_cast<uint8_t>(Z & 127);
+      dst[64] = static_cast<uint8_t>((Z >> 7) & 127);
+      dst[128] = static_cast<uint8_t>((Z >> 14) & 127);
+      dst[192] = static_cast<uint8_t>((Z >> 21) & 0xff);
+    }
+  }
+  lsum = qkv_wave_sum(lsum);
+  usum = wave_sum_i64(usum);
+  if (lane == 0) {
+    lsum_s[wave] = lsum;
+    usum_s[wave] = usum;
+  }
+  __syncthreads();
+
+  // ---------------- phase 2: P V in the rotated domain, bit planes x digits
+  qkv_v4i acc2[MTW][NP];
+#pragma unroll
+  for (int mi = 0; mi < MTW; ++mi)
+#pragma unroll
+    for (int s = 0; s < NP; ++s) acc2[mi][s] = qkv_v4i{0, 0, 0, 0};
+  const int64_t tile0 = ts >> 5;
+  const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
+  const int blk = lg >> 1, hsh = 4 * (lg & 1);
+  for (int tt = 0; tt < ntiles; ++tt) {
+    const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(pbase + tt * 1024 + ln * 64 + lg * 16);
+    const int64_t vt = tile0 + 2 * tt + blk;
+#pragma unroll
+    for (int mi = 0; mi < MTW; ++mi) {
+      const int j = 16 * (wave * MTW + mi) + ln;
+      uint32_t w[VB];
+#pragma unroll
+      for (int k = 0; k < VB; ++k) w[k] = vb[(vt * VB + k) * D + j];
+#pragma unroll
+      for (int s = 0; s < NP; ++s) {
+        const uint32_t sub = odd_subset(VB, s);
+        uint32_t pw = 0;
+#pragma unroll
+        for (int k = 0; k < VB; ++k)
+          if (sub & (1u << k)) pw ^= w[k];
+        qkv_v4i av;
+        av[0] = static_cast<int>(pw & (0x01010101u << hsh));
+        av[1] = static_cast<int>(pw & (0x02020202u << hsh));
+        av[2] = static_cast<int>(pw & (0x04040404u << hsh));
+        av[3] = static_cast<int>(pw & (0x08080808u << hsh));
+        acc2[mi][s] = mfma_i8(av, bq, acc2[mi][s]);
+      }
+    }
+  }
+
+  // ---------------- epilogue: digits + planes -> fp32, write the partials
+  // Per plane S: Y_S = sum_v 2^(7v) acc_S[v] = sum_t Z_t s_t phi_S,t exactly
+  // (int64; the digits live in the 4 lanes of a column quad), and
+  // sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U) is formed in integers
+  // before the only rounding: O = 2^-Fv sum_S g_S (2 Y_S - U).
+  mfma_settle();
+  const int qcol = ln >> 2, vd = ln & 3;
+  const float oscale = ldexpf(1.f, -Fv);
+  const int64_t urow = usum_s[qcol];
+  const int64_t base = ((int64_t(split) * gridDim.z + b) * Hkv + hkv) * R + r0;
+#pragma unroll
+  for (int mi = 0; mi < MTW; ++mi) {
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float val = 0.f;
+#pragma unroll
+      for (int s = 0; s < NP; ++s) {
+        int64_t y = static_cast<int64_t>(acc2[mi][s][e]) << (7 * vd);
+        y += shfl_xor_i64(y, 1);
+        y += shfl_xor_i64(y, 2);
+        val = fmaf(tb.vg[s], static_cast<float>(2 * y - urow), val);
+      }
+      o[e] = val * oscale;
+    }
+    if (vd == 0 && qcol < nr) {
+      const int j0 = 16 * (wave * MTW + mi) + 4 * lg;
+      float4* dst = reinterpret_cast<float4*>(part_o + (base + qcol) * D + j0);
+      *dst = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  }
+  if (tid < nr) {
+    const float mq = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
+    part_ml[(base + tid) * 2 + 0] = mq;
+    part_ml[(base + tid) * 2 + 1] = lsum_s[tid];
+  }
+}
+
+// ------------------------------------------------------------ combine
 
 // One block per (b, hkv, r) query row: merge splits, normalise, un-rotate.
 template <int D>
@@ -255,7 +679,8 @@ __global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ 
   __syncthreads();
   if (tid < D) {
     float a = 0.f;
-    for (int s = 0; s < n_splits; ++s) a = fmaf(wgt[s], part_o[(s * stride + row) * D + tid], a);
+    for (int s = 0; s < n_splits; ++s)
+      if (wgt[s] != 0.f) a = fmaf(wgt[s], part_o[(s * stride + row) * D + tid], a);
     o[tid] = a / lsum;
   }
   __syncthreads();
@@ -271,34 +696,70 @@ __global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ 
   qkv_store(out, ((int64_t(b) * Hq + h) * Q + qi) * D + tid, acc, out_dtype);
 }
 
-}  // namespace
+// ------------------------------------------------------------ host helpers
 
-extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
-                                        int32_t d, int64_t T) {
-  (void)d;
-  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
-  const int R = (Hq / Hkv) * Q;
-  const int chunks = (R + kMaxRows - 1) / kMaxRows;
-  const int64_t groups = int64_t(B) * Hkv * chunks;
-  const int64_t target = int64_t(qkv_num_cus()) * 4;
-  int64_t s = (target + groups - 1) / groups;
-  const int64_t max_s = (T + kTile - 1) / kTile;
-  if (s > max_s) s = max_s;
-  if (s > 1024) s = 1024;
-  if (s < 1) s = 1;
-  return static_cast<int32_t>(s);
+// Walsh coefficients of a codebook: c[code] = g_empty + sum_S g_S chi_S(code),
+// chi_S(code) = prod_{k in S} (2 bit_k(code) - 1).  The plane decomposition
+// used by the MFMA path needs a symmetric codebook (c[~code] == -c[code]),
+// for which every even-size subset (g_empty included) has g_S = 0.
+bool walsh_odd(const float* cent, int bits, float* g, float* gconst) {
+  const int n = 1 << bits;
+  for (int c = 0; c < n; ++c)
+    if (cent[(n - 1) ^ c] != -cent[c]) return false;
+  const int ns = n_odd_subsets(bits);
+  double sum = 0.0;
+  for (int s = 0; s < ns; ++s) {
+    const uint32_t sub = odd_subset(bits, s);
+    double acc = 0.0;
+    for (int c = 0; c < n / 2; ++c) {  // pair code c with ~c: chi flips sign for odd S
+      int par = 0;
+      for (int k = 0; k < bits; ++k)
+        if ((sub >> k) & 1u) par += ((c >> k) & 1) ? 0 : 1;  // count of (-1) factors
+      const double chi = (par & 1) ? -1.0 : 1.0;
+      acc += 2.0 * static_cast<double>(cent[c]) * chi;
+    }
+    g[s] = static_cast<float>(acc / n);
+    sum += acc / n;
+  }
+  // reconstruction check
+  for (int c = 0; c < n; ++c) {
+    double v = 0.0;
+    for (int s = 0; s < ns; ++s) {
+      const uint32_t sub = odd_subset(bits, s);
+      double chi = 1.0;
+      for (int k = 0; k < bits; ++k)
+        if ((sub >> k) & 1u) chi *= ((c >> k) & 1) ? 1.0 : -1.0;
+      v += static_cast<double>(g[s]) * chi;
+    }
+    if (fabs(v - cent[c]) > 1e-6 * (fabs(static_cast<double>(cent[c])) + 1e-6)) return false;
+  }
+  *gconst = static_cast<float>(-sum);
+  return true;
 }
 
-extern "C" int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
-                                                 int32_t d, int32_t n_splits) {
-  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || d <= 0 || n_splits <= 0) return -1;
-  const int R = (Hq / Hkv) * Q;
-  return 4 * (ws_qw_floats(B, Hkv, R, d) + ws_po_floats(n_splits, B, Hkv, R, d) +
-              ws_ml_floats(n_splits, B, Hkv, R));
+Tables make_tables(const float* kc, int mbits, const float* vc, int vbits) {
+  Tables t{};
+  for (int i = 0; i < 16; ++i) {
+    t.kc[i] = i < (1 << mbits) ? kc[i] : 0.f;
+    t.vc[i] = i < (1 << vbits) ? vc[i] : 0.f;
+  }
+  bool ok = mbits >= 1 && mbits <= 2 && vbits >= 1 && vbits <= 4;
+  if (ok) ok = walsh_odd(kc, mbits, t.kg, &t.kconst);
+  if (ok) ok = walsh_odd(vc, vbits, t.vg, &t.vconst);
+  t.mfma_ok = ok ? 1 : 0;
+  return t;
 }
 
-static int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-                           int32_t n_splits, const void* workspace, int64_t ws_bytes) {
+int64_t mfma_split_len(int64_t T, int n_splits) {
+  return ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
+}
+
+bool use_mfma(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
+  return tb.mfma_ok && d == 128 && t_stride % 64 == 0 && mfma_split_len(T, n_splits) <= kSplitMax;
+}
+
+int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t n_splits,
+                    const void* workspace, int64_t ws_bytes) {
   if (!qkv_d_ok(d)) {
     qkv_set_error("head_dim %d unsupported (64, 96 or 128)", d);
     return QKV_E_UNSUPPORTED;
@@ -308,31 +769,71 @@ static int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_
   QKV_REQUIRE(B <= 65535, "batch too large");
   QKV_REQUIRE(n_splits >= 1 && n_splits <= 1024, "n_splits %d out of range", n_splits);
   const int R = (Hq / Hkv) * Q;
-  const int chunks = (R + kMaxRows - 1) / kMaxRows;
-  QKV_REQUIRE(int64_t(Hkv) * chunks <= 65535, "too many kv heads x row chunks");
+  QKV_REQUIRE(int64_t(Hkv) * ((R + kRowsM - 1) / kRowsM) <= 65535, "too many kv heads x rows");
   QKV_REQUIRE(workspace != nullptr, "null workspace");
-  QKV_REQUIRE(qkv_aligned(workspace, 16), "workspace must be 16-byte aligned");
-  const int64_t need = qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits);
+  QKV_REQUIRE(qkv_aligned(workspace, 256), "workspace must be 256-byte aligned");
+  const int64_t need = ws_layout(B, Hkv, R, d, n_splits).total;
   QKV_REQUIRE(ws_bytes >= need, "workspace too small: %lld < %lld", (long long)ws_bytes,
               (long long)need);
   return QKV_OK;
 }
 
+}  // namespace
+
+// ------------------------------------------------------------ C ABI
+
+extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                                        int32_t d, int64_t T) {
+  (void)d;
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
+  const int R = (Hq / Hkv) * Q;
+  const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM);
+  const int64_t target = int64_t(qkv_num_cus()) * 2;  // workgroups to fill the chip
+  int64_t s = (target + groups - 1) / groups;
+  const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
+  const int64_t max_s = (T + 63) / 64;
+  if (s < min_s) s = min_s;
+  if (s > max_s) s = max_s;
+  if (s > 1024) s = 1024;
+  if (s < 1) s = 1;
+  return static_cast<int32_t>(s);
+}
+
+extern "C" int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                                                 int32_t d, int32_t n_splits) {
+  if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || d <= 0 || n_splits <= 0) return -1;
+  return ws_layout(B, Hkv, (Hq / Hkv) * Q, d, n_splits).total;
+}
+
+extern "C" int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
+                                      const float* kcent_host, const float* vcent_host,
+                                      int64_t t_stride, int64_t T, int32_t n_splits) {
+  if (!kcent_host || !vcent_host || !qkv_bits_ok(kbits) || !qkv_bits_ok(vbits) || n_splits < 1)
+    return -1;
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  return use_mfma(tb, d, t_stride, T, n_splits) ? 1 : 0;
+}
+
 extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
-                                     int32_t Hkv, int32_t Q, int32_t d, const float* pi,
-                                     const float* signs, float qjl_scale, void* workspace,
-                                     int64_t ws_bytes, int32_t n_splits, void* stream) {
+                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                     int32_t vbits, const float* pi, const float* kcent_host,
+                                     const float* vcent_host, const float* signs,
+                                     float qjl_scale, void* workspace, int64_t ws_bytes,
+                                     int32_t n_splits, void* stream) {
   QKV_REQUIRE(qkv_dtype_ok(q_dtype), "unsupported query dtype %d", q_dtype);
+  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(q && pi && signs, "null pointer");
-  float* qw = static_cast<float*>(workspace);
+  QKV_REQUIRE(q && pi && signs && kcent_host && vcent_host, "null pointer");
+  const int R = (Hq / Hkv) * Q;
+  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
   auto s = static_cast<hipStream_t>(stream);
   switch (d) {
 #define QKV_CASE(DD)                                                                        \
   case DD:                                                                                  \
     hipLaunchKernelGGL(qrot_kernel<DD>, dim3(B * Hq * Q), dim3(128), 0, s, q, q_dtype, pi, \
-                       signs, qjl_scale, Hq, Hkv, Q, qw);                                   \
+                       signs, qjl_scale, Hq, Hkv, Q, at<float>(workspace, L.qw));           \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -340,37 +841,78 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
 #undef QKV_CASE
   }
   QKV_LAUNCHED();
+  if (tb.mfma_ok && d == 128) {
+    const int chunks = (R + kRowsM - 1) / kRowsM;
+    const dim3 grid(B * Hkv * chunks);
+    if (kbits == 2)
+      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
+                         at<float>(workspace, L.rowc));
+    else
+      hipLaunchKernelGGL((prepare_mfma<128, 1>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
+                         at<float>(workspace, L.rowc));
+    QKV_LAUNCHED();
+  }
   return QKV_OK;
 }
 
-extern "C" int qkv_attention_partial(const uint8_t* kcodes, const uint8_t* kqjl,
-                                     const float* knorm, const uint8_t* vcodes,
-                                     const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
-                                     int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-                                     int32_t kbits, int32_t vbits, int32_t packed,
-                                     const float* kcent, const float* vcent, float scale,
-                                     int32_t causal, void* workspace, int64_t ws_bytes,
-                                     int32_t n_splits, void* stream) {
+extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
+                                     const uint32_t* vstore, const float* vnorm,
+                                     int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                     int32_t vbits, const float* kcent_host,
+                                     const float* vcent_host, float scale, int32_t causal,
+                                     void* workspace, int64_t ws_bytes, int32_t n_splits,
+                                     void* stream) {
   QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
-  QKV_REQUIRE(t_stride >= T, "t_stride %lld < T %lld", (long long)t_stride, (long long)T);
+  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
+              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
+              (long long)T);
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(kcodes && kqjl && knorm && vcodes && vnorm && kcent && vcent, "null pointer");
+  QKV_REQUIRE(kstore && knorm && vstore && vnorm && kcent_host && vcent_host, "null pointer");
+  QKV_REQUIRE(qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4), "store must be 4-byte aligned");
   const int R = (Hq / Hkv) * Q;
-  const int chunks = (R + kMaxRows - 1) / kMaxRows;
-  const int64_t split_len = ((T + n_splits - 1) / n_splits + kTile - 1) / kTile * kTile;
-  float* qw = static_cast<float*>(workspace);
-  float* po = qw + ws_qw_floats(B, Hkv, R, d);
-  float* pml = po + ws_po_floats(n_splits, B, Hkv, R, d);
+  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  float* po = at<float>(workspace, L.po);
+  float* pml = at<float>(workspace, L.pml);
   auto s = static_cast<hipStream_t>(stream);
+  if (use_mfma(tb, d, t_stride, T, n_splits)) {
+    const int chunks = (R + kRowsM - 1) / kRowsM;
+    const int64_t split_len = mfma_split_len(T, n_splits);
+    const dim3 grid(n_splits, Hkv * chunks, B);
+    const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
+    const float* rowc = at<float>(workspace, L.rowc);
+#define QKV_MF(MB, VB)                                                                       \
+  hipLaunchKernelGGL((split_mfma<128, MB, VB>), grid, dim3(256), 0, s, aq, rowc, kstore,    \
+                     knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, scale, causal,    \
+                     split_len, tb, po, pml)
+    switch (kbits * 10 + vbits) {
+      case 11: QKV_MF(1, 1); break;
+      case 12: QKV_MF(1, 2); break;
+      case 13: QKV_MF(1, 3); break;
+      case 14: QKV_MF(1, 4); break;
+      case 21: QKV_MF(2, 1); break;
+      case 22: QKV_MF(2, 2); break;
+      case 23: QKV_MF(2, 3); break;
+      case 24: QKV_MF(2, 4); break;
+    }
+#undef QKV_MF
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
+  const int chunks = (R + kRowsG - 1) / kRowsG;
+  const int64_t split_len = ((T + n_splits - 1) / n_splits + kTileG - 1) / kTileG * kTileG;
+  const float* qw = at<float>(workspace, L.qw);
   switch (d) {
 #define QKV_CASE(DD)                                                                           \
   case DD:                                                                                     \
-    hipLaunchKernelGGL(split_kernel<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTile), 0, s,  \
-                       qw, kcodes, kqjl, knorm, vcodes, vnorm, t_stride, T, Hkv, R, Q, chunks, \
-                       kbits, vbits, packed, kcent, vcent, scale, causal, split_len, n_splits, \
-                       po, pml);                                                               \
+    hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
+                       qw, kstore, knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, kbits, \
+                       vbits, tb, scale, causal, split_len, po, pml);                          \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -390,14 +932,13 @@ extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t
   if (st != QKV_OK) return st;
   QKV_REQUIRE(pi && out, "null pointer");
   const int R = (Hq / Hkv) * Q;
-  float* qw = static_cast<float*>(workspace);
-  float* po = qw + ws_qw_floats(B, Hkv, R, d);
-  float* pml = po + ws_po_floats(n_splits, B, Hkv, R, d);
+  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   auto s = static_cast<hipStream_t>(stream);
   switch (d) {
 #define QKV_CASE(DD)                                                                         \
   case DD:                                                                                   \
-    hipLaunchKernelGGL(combine_kernel<DD>, dim3(B * Hkv * R), dim3(128), 0, s, po, pml, pi, \
+    hipLaunchKernelGGL(combine_kernel<DD>, dim3(B * Hkv * R), dim3(128), 0, s,              \
+                       at<float>(workspace, L.po), at<float>(workspace, L.pml), pi,         \
                        n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                          \
     break;
     QKV_CASE(64)
@@ -409,32 +950,33 @@ extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t
   return QKV_OK;
 }
 
-extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kcodes,
-                                    const uint8_t* kqjl, const float* knorm,
-                                    const uint8_t* vcodes, const float* vnorm, int64_t t_stride,
-                                    int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
-                                    int32_t d, int32_t kbits, int32_t vbits, int32_t packed,
-                                    const float* pi, const float* kcent, const float* vcent,
-                                    const float* signs, float qjl_scale, float scale,
-                                    int32_t causal, void* out, int32_t out_dtype,
-                                    void* workspace, int64_t ws_bytes, int32_t n_splits,
-                                    void* stream) {
+extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                                    const float* knorm, const uint32_t* vstore,
+                                    const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+                                    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                    int32_t vbits, const float* pi, const float* kcent_host,
+                                    const float* vcent_host, const float* signs,
+                                    float qjl_scale, float scale, int32_t causal, void* out,
+                                    int32_t out_dtype, void* workspace, int64_t ws_bytes,
+                                    int32_t n_splits, void* stream) {
   // validate everything before the first launch
   QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
   QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
-  QKV_REQUIRE(t_stride >= T, "t_stride %lld < T %lld", (long long)t_stride, (long long)T);
+  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
+              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
+              (long long)T);
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(q && kcodes && kqjl && knorm && vcodes && vnorm && pi && kcent && vcent && signs &&
-                  out,
+  QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host &&
+                  signs && out,
               "null pointer");
-  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, pi, signs, qjl_scale, workspace,
-                             ws_bytes, n_splits, stream);
+  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
+                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
   if (st != QKV_OK) return st;
-  st = qkv_attention_partial(kcodes, kqjl, knorm, vcodes, vnorm, t_stride, T, B, Hq, Hkv, Q, d,
-                             kbits, vbits, packed, kcent, vcent, scale, causal, workspace,
-                             ws_bytes, n_splits, stream);
+  st = qkv_attention_partial(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
+                             vbits, kcent_host, vcent_host, scale, causal, workspace, ws_bytes,
+                             n_splits, stream);
   if (st != QKV_OK) return st;
   return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
                                n_splits, stream);

@@ -127,7 +127,7 @@ __global__ __launch_bounds__(kThreads) void compress_generic(
 
 template <int D>
 __global__ __launch_bounds__(kThreads) void decompress_generic(
-    int mode, int packed, const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
+    int mode, int fmt, const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
     const float* __restrict__ norms, int64_t n, int bits, const float* __restrict__ pi,
     const float* __restrict__ cents, const float* __restrict__ signs, float qjl_scale,
     int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype) {
@@ -138,10 +138,11 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
   const int tid = threadIdx.x;
   for (int i = tid; i < D * D; i += kThreads) pis[i] = pi[i];
   if (tid < 16) cl[tid] = tid < (1 << bits) ? cents[tid] : 0.f;
-  const int cb = packed ? bits : 8;
-  const int qb = packed ? 1 : 8;
-  const int64_t pb = packed ? qkv_row_bytes(D, bits) : D;
-  const int64_t pq = packed ? qkv_row_bytes(D, 1) : D;
+  const int cb = fmt == QKV_FMT_PACKED ? bits : 8;
+  const int qb = fmt == QKV_FMT_PACKED ? 1 : 8;
+  const int64_t pb = fmt == QKV_FMT_PACKED ? qkv_row_bytes(D, bits)
+                   : fmt == QKV_FMT_KPLANES ? int64_t(bits + 1) * D / 8 : D;
+  const int64_t pq = fmt == QKV_FMT_PACKED ? qkv_row_bytes(D, 1) : D;
   const float qs = (mode == QKV_MODE_IP && tid < D) ? qjl_scale * signs[tid] : 0.f;
   __syncthreads();
 
@@ -152,17 +153,42 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
       for (int r = 0; r < kRows; ++r) {
         float v = 0.f;
         if (r < nr) {
-          const int64_t row = qkv_grouped_row(r0 + r, in_seq, in_gstride);
-          v = cl[qkv_get_code(codes + row * pb, tid, cb) & 15u];
-          if (mode == QKV_MODE_IP) {
-            const float sv = qkv_get_code(qjl + row * pq, tid, qb) ? 1.f : -1.f;
-            v += qs * sv;
+          uint32_t code, bit = 0;
+          if (fmt == QKV_FMT_VTILES) {
+            const int64_t g = (r0 + r) / in_seq, t = (r0 + r) - g * in_seq;
+            const uint32_t* w = reinterpret_cast<const uint32_t*>(codes) +
+                                ((g * in_gstride + (t >> 5)) * bits) * D + tid;
+            code = 0;
+            for (int k = 0; k < bits; ++k) code |= ((w[k * D] >> (t & 31)) & 1u) << k;
+          } else {
+            const int64_t row = qkv_grouped_row(r0 + r, in_seq, in_gstride);
+            if (fmt == QKV_FMT_KPLANES) {
+              const uint8_t* kr = codes + row * pb;
+              code = 0;
+              for (int p = 0; p < bits; ++p)
+                code |= ((kr[p * (D / 8) + (tid >> 3)] >> (tid & 7)) & 1u) << p;
+              bit = (kr[bits * (D / 8) + (tid >> 3)] >> (tid & 7)) & 1u;
+            } else {
+              code = qkv_get_code(codes + row * pb, tid, cb);
+              if (mode == QKV_MODE_IP) bit = qkv_get_code(qjl + row * pq, tid, qb);
+            }
           }
+          v = cl[code & 15u];
+          if (mode == QKV_MODE_IP) v += qs * (bit ? 1.f : -1.f);
         }
         cs[tid * kRows + r] = v;
       }
     }
-    if (tid < nr) ns[tid] = norms[qkv_grouped_row(r0 + tid, in_seq, in_gstride)];
+    if (tid < nr) {
+      int64_t nrow;
+      if (fmt == QKV_FMT_VTILES) {
+        const int64_t g = (r0 + tid) / in_seq;
+        nrow = g * in_gstride * 32 + ((r0 + tid) - g * in_seq);
+      } else {
+        nrow = qkv_grouped_row(r0 + tid, in_seq, in_gstride);
+      }
+      ns[tid] = norms[nrow];
+    }
     __syncthreads();
     if (tid < D) {
       float acc[kRows];
@@ -226,7 +252,7 @@ extern "C" int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags, const
   return QKV_OK;
 }
 
-extern "C" int qkv_decompress(int32_t mode, int32_t packed, const uint8_t* codes,
+extern "C" int qkv_decompress(int32_t mode, int32_t fmt, const uint8_t* codes,
                               const uint8_t* qjl, const float* norms, int64_t n, int32_t d,
                               int32_t bits, const float* pi, const float* centroids,
                               const float* signs, float qjl_scale, int64_t in_seq,
@@ -241,15 +267,21 @@ extern "C" int qkv_decompress(int32_t mode, int32_t packed, const uint8_t* codes
   }
   QKV_REQUIRE(n >= 0, "negative row count");
   if (n == 0) return QKV_OK;
+  QKV_REQUIRE(fmt >= QKV_FMT_UNPACKED && fmt <= QKV_FMT_VTILES, "unknown code format %d", fmt);
   QKV_REQUIRE(codes && norms && pi && centroids && out, "null pointer");
-  QKV_REQUIRE(mode != QKV_MODE_IP || (signs && qjl), "null pointer (signs / qjl)");
-  QKV_REQUIRE(in_seq > 0 && in_group_stride >= in_seq, "bad grouped-row layout");
+  QKV_REQUIRE(mode != QKV_MODE_IP || signs, "null pointer (signs)");
+  QKV_REQUIRE(mode != QKV_MODE_IP || qjl || fmt == QKV_FMT_KPLANES, "null pointer (qjl)");
+  QKV_REQUIRE(mode != QKV_MODE_IP || fmt != QKV_FMT_VTILES, "V tiles carry no QJL plane");
+  if (fmt == QKV_FMT_VTILES)
+    QKV_REQUIRE(in_seq > 0 && in_group_stride * 32 >= in_seq, "bad V tile layout");
+  else
+    QKV_REQUIRE(in_seq > 0 && in_group_stride >= in_seq, "bad grouped-row layout");
   auto s = static_cast<hipStream_t>(stream);
   switch (d) {
 #define QKV_CASE(DD)                                                                         \
   case DD:                                                                                   \
     hipLaunchKernelGGL(decompress_generic<DD>, dim3(grid_rows(n)), dim3(kThreads), 0, s,    \
-                       mode, packed, codes, qjl, norms, n, bits, pi, centroids, signs,       \
+                       mode, fmt, codes, qjl, norms, n, bits, pi, centroids, signs,          \
                        qjl_scale, in_seq, in_group_stride, out, out_dtype);                  \
     break;
     QKV_CASE(64)

@@ -2,15 +2,16 @@
 
 API of quashkv/engine.py:54-360.  What changes underneath:
 
-* The cache is ONE preallocated device store per engine -- (B, H, capacity,
-  row_bytes) code buffers and (B, H, capacity) norm buffers -- and append()
-  compresses straight into it at offset total_tokens (no per-block tensors,
-  no torch.cat).  Capacity grows by doubling.
-* ``pack_storage`` keeps its meaning: True stores bit-packed rows (the
-  pack_bits layout), False one uint8 per code.  The attention kernel reads
-  either format directly.
-* ``_cache`` still lists one CompressedKVBlock per append, as zero-copy views
-  into the store, so code that walks blocks keeps working.
+* The cache is ONE preallocated device store per engine (quashkv_amd.store:
+  K bit-plane rows, V bit-plane tiles, fp32 norms) and append() compresses
+  straight into it at offset total_tokens -- no per-block tensors, no
+  torch.cat.  Capacity grows by doubling.
+* ``pack_storage`` keeps its observable meaning: ``_cache`` blocks hold
+  pack_bits rows when True and one uint8 per code when False, and
+  actual_memory_bytes() reports the bytes those block tensors take.  The store
+  itself is always bit-packed.
+* ``_cache`` lists one CompressedKVBlock per append, decoded from the store
+  on access, so code that walks blocks keeps working.
 * attention() runs the split-K decode kernels; query heads may be a multiple
   of the cached kv heads (GQA, head h reads kv head h // G).
 """
@@ -25,9 +26,10 @@ import torch
 
 from . import _native as N
 from .constants import DEFAULT_SEED, DEFAULT_TOTAL_BITS
-from .kernels import attention_call
+from .kernels import attention_store
 from .packing import pack_bits, unpack_bits
 from .quantizer import InnerProductQuantizer, MSEQuantizer, _default_device, compress_into
+from .store import KVStore
 
 
 @dataclass
@@ -40,70 +42,6 @@ class CompressedKVBlock:
     val_norms: torch.Tensor
     seq_len: int
     packed: bool = False
-
-
-class _KVStore:
-    """Preallocated compressed KV buffers for one engine."""
-
-    def __init__(self, B: int, H: int, d: int, kbits: int, vbits: int, packed: bool,
-                 capacity: int, device: torch.device):
-        self.B, self.H, self.d = B, H, d
-        self.kbits, self.vbits, self.packed = kbits, vbits, packed
-        self.device = device
-        self.capacity = 0
-        self.kcodes = self.kqjl = self.knorm = self.vcodes = self.vnorm = None
-        self._alloc(capacity, 0)
-
-    def row_bytes(self):
-        if self.packed:
-            return (N.packed_row_bytes(self.d, self.kbits), N.packed_row_bytes(self.d, 1),
-                    N.packed_row_bytes(self.d, self.vbits))
-        return self.d, self.d, self.d
-
-    def _alloc(self, capacity: int, keep: int) -> None:
-        pk, pq, pv = self.row_bytes()
-        B, H, dev = self.B, self.H, self.device
-        new = (
-            torch.empty(B, H, capacity, pk, dtype=torch.uint8, device=dev),
-            torch.empty(B, H, capacity, pq, dtype=torch.uint8, device=dev),
-            torch.empty(B, H, capacity, dtype=torch.float32, device=dev),
-            torch.empty(B, H, capacity, pv, dtype=torch.uint8, device=dev),
-            torch.empty(B, H, capacity, dtype=torch.float32, device=dev),
-        )
-        if keep:
-            old = (self.kcodes, self.kqjl, self.knorm, self.vcodes, self.vnorm)
-            for n_, o_ in zip(new, old):
-                n_[:, :, :keep].copy_(o_[:, :, :keep])
-        self.kcodes, self.kqjl, self.knorm, self.vcodes, self.vnorm = new
-        self.capacity = capacity
-
-    def ensure(self, needed: int, keep: int) -> None:
-        if needed > self.capacity:
-            cap = max(needed, 2 * self.capacity, 256)
-            self._alloc(cap, keep)
-
-    def to(self, device) -> None:
-        self.device = torch.device(device)
-        for name in ("kcodes", "kqjl", "knorm", "vcodes", "vnorm"):
-            setattr(self, name, getattr(self, name).to(self.device))
-
-    def convert(self, packed: bool, used: int) -> None:
-        """Re-encode the first `used` tokens in the other storage format."""
-        if packed == self.packed:
-            return
-        old = (self.kcodes, self.kqjl, self.vcodes)
-        old_bits = (self.kbits, 1, self.vbits)
-        was_packed = self.packed
-        self.packed = packed
-        knorm, vnorm = self.knorm, self.vnorm
-        self._alloc(self.capacity, 0)
-        self.knorm, self.vnorm = knorm, vnorm
-        for dst, src, bits in zip((self.kcodes, self.kqjl, self.vcodes), old, old_bits):
-            if used == 0:
-                continue
-            view = src[:, :, :used]
-            codes = unpack_bits(view.contiguous(), bits, self.d) if was_packed else view
-            dst[:, :, :used].copy_(pack_bits(codes.contiguous(), bits) if packed else codes)
 
 
 class QuashKVEngine:
@@ -131,7 +69,7 @@ class QuashKVEngine:
                                                    device=self.device)
         self.value_quantizer = MSEQuantizer(d=head_dim, bits=value_bits, seed=seed,
                                             device=self.device)
-        self._store: Optional[_KVStore] = None
+        self._store: Optional[KVStore] = None
         self._blocks: list[tuple[int, int]] = []   # (start, seq_len) per append
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
@@ -163,28 +101,28 @@ class QuashKVEngine:
             raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
                              f"(B={st.B}, H={st.H})")
         if st is None:
-            st = self._store = _KVStore(B, H, d, self.key_bits - 1, self.value_bits,
-                                        bool(self.pack_storage),
-                                        max(self.initial_capacity, S), dev)
-        if st.packed != bool(self.pack_storage):
-            st.convert(bool(self.pack_storage), self._total_tokens)
+            st = self._store = KVStore(B, H, d, self.key_bits - 1, self.value_bits,
+                                       max(self.initial_capacity, S), dev)
         t0 = self._total_tokens
         st.ensure(t0 + S, t0)
         if S > 0:
             kq, vq = self.key_quantizer, self.value_quantizer
             mq = kq.mse_quantizer
-            k_rows = keys.reshape(B * H * S, d)
-            v_rows = values.reshape(B * H * S, d)
-            C = st.capacity
-            # grouped rows: vector (bh, s) -> row bh * C + t0 + s
-            compress_into(N.QKV_MODE_IP, k_rows, mq.Pi, mq.codebook.boundaries,
-                          mq.codebook.centroids, kq.mse_bits, kq.S,
-                          st.kcodes[:, :, t0:], st.kqjl[:, :, t0:], st.knorm[:, :, t0:],
-                          packed=st.packed, out_seq=S, out_group_stride=C)
-            compress_into(N.QKV_MODE_MSE, v_rows, vq.Pi, vq.codebook.boundaries,
-                          vq.codebook.centroids, vq.bits, None,
-                          st.vcodes[:, :, t0:], None, st.vnorm[:, :, t0:],
-                          packed=st.packed, out_seq=S, out_group_stride=C)
+            n = B * H * S
+            kc = torch.empty(n, d, dtype=torch.uint8, device=dev)
+            kb = torch.empty(n, d, dtype=torch.uint8, device=dev)
+            vc = torch.empty(n, d, dtype=torch.uint8, device=dev)
+            kn = torch.empty(n, dtype=torch.float32, device=dev)
+            vn = torch.empty(n, dtype=torch.float32, device=dev)
+            # codes and norms of the n = B*H*S new vectors, row-contiguous; the
+            # bit-plane packers then place the codes at tokens [t0, t0 + S)
+            compress_into(N.QKV_MODE_IP, keys.reshape(n, d), mq.Pi, mq.codebook.boundaries,
+                          mq.codebook.centroids, kq.mse_bits, kq.S, kc, kb, kn, packed=False)
+            compress_into(N.QKV_MODE_MSE, values.reshape(n, d), vq.Pi, vq.codebook.boundaries,
+                          vq.codebook.centroids, vq.bits, None, vc, None, vn, packed=False)
+            st.knorm[:, :, t0:t0 + S].copy_(kn.view(B, H, S))
+            st.vnorm[:, :, t0:t0 + S].copy_(vn.view(B, H, S))
+            st.write_codes(t0, S, kc, kb, vc)
         self._blocks.append((t0, S))
         self._total_tokens += S
 
@@ -193,11 +131,16 @@ class QuashKVEngine:
         st = self._store
         out = []
         for t0, s in self._blocks:
+            kc, kb, vc = st.read_codes(t0, s)
+            if self.pack_storage:
+                kc = pack_bits(kc, self.key_bits - 1)
+                kb = pack_bits(kb, 1)
+                vc = pack_bits(vc, self.value_bits)
             sl = slice(t0, t0 + s)
             out.append(CompressedKVBlock(
-                mse_indices=st.kcodes[:, :, sl], qjl_signs=st.kqjl[:, :, sl],
-                key_norms=st.knorm[:, :, sl], val_indices=st.vcodes[:, :, sl],
-                val_norms=st.vnorm[:, :, sl], seq_len=s, packed=st.packed))
+                mse_indices=kc, qjl_signs=kb, key_norms=st.knorm[:, :, sl],
+                val_indices=vc, val_norms=st.vnorm[:, :, sl], seq_len=s,
+                packed=bool(self.pack_storage)))
         return out
 
     def clear(self) -> None:
@@ -244,12 +187,12 @@ class QuashKVEngine:
         need = L.qkv_attention_workspace_bytes(B, Hq, st.H, Q, d, splits)
         if self._workspace is None or self._workspace.numel() < need \
                 or self._workspace.device != queries.device:
-            self._workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=queries.device)
-        return attention_call(
-            queries, st.kcodes, st.kqjl, st.knorm, st.vcodes, st.vnorm, self._total_tokens,
-            kq.mse_quantizer.Pi, kq.mse_quantizer.codebook.centroids, vq.codebook.centroids,
-            kq.S, kq.qjl_scale, kq.mse_bits, vq.bits, st.packed, scale=scale, causal=causal,
-            out_dtype=out_dtype, workspace=self._workspace, n_splits=splits)
+            self._workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=queries.device)
+        return attention_store(
+            queries, st, self._total_tokens, kq.mse_quantizer.Pi,
+            kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host, kq.S,
+            kq.qjl_scale, scale=scale, causal=causal, out_dtype=out_dtype,
+            workspace=self._workspace, n_splits=splits)
 
     # -------------------------------------------------------------- metrics
 
@@ -263,13 +206,18 @@ class QuashKVEngine:
         return original / compressed
 
     def actual_memory_bytes(self) -> int:
-        """Bytes held by the appended blocks' codes and norms (quashkv/engine.py:328-337)."""
-        total = 0
-        for blk in self._cache:
-            for t in (blk.mse_indices, blk.qjl_signs, blk.key_norms, blk.val_indices,
-                      blk.val_norms):
-                total += t.nelement() * t.element_size()
-        return total
+        """Bytes the reference's block tensors would take (quashkv/engine.py:328-337):
+        pack_bits rows when pack_storage, else one byte per code, plus fp32 norms."""
+        if not self._blocks:
+            return 0
+        st = self._store
+        d = self.head_dim
+        if self.pack_storage:
+            row = (N.packed_row_bytes(d, self.key_bits - 1) + N.packed_row_bytes(d, 1)
+                   + N.packed_row_bytes(d, self.value_bits))
+        else:
+            row = 3 * d
+        return st.B * st.H * self._total_tokens * (row + 8)
 
     def to(self, device) -> "QuashKVEngine":
         self.device = torch.device(device)

@@ -69,12 +69,12 @@ class QuashKVCache:
         n = B * H * T
         kq, vq = engine.key_quantizer, engine.value_quantizer
         mq = kq.mse_quantizer
-        k = decompress_from(N.QKV_MODE_MSE, st.kcodes, None, st.knorm, n, mq.Pi,
-                            mq.codebook.centroids, kq.mse_bits, None, 0.0, st.packed,
+        k = decompress_from(N.QKV_MODE_MSE, st.kst, None, st.knorm, n, mq.Pi,
+                            mq.codebook.centroids, kq.mse_bits, None, 0.0, N.QKV_FMT_KPLANES,
                             in_seq=T, in_group_stride=st.capacity)
-        v = decompress_from(N.QKV_MODE_MSE, st.vcodes, None, st.vnorm, n, vq.Pi,
-                            vq.codebook.centroids, vq.bits, None, 0.0, st.packed,
-                            in_seq=T, in_group_stride=st.capacity)
+        v = decompress_from(N.QKV_MODE_MSE, st.vst, None, st.vnorm, n, vq.Pi,
+                            vq.codebook.centroids, vq.bits, None, 0.0, N.QKV_FMT_VTILES,
+                            in_seq=T, in_group_stride=st.capacity // 32)
         return k.reshape(B, H, T, d), v.reshape(B, H, T, d)
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,

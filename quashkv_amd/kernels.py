@@ -16,6 +16,7 @@ import torch
 
 from . import _native as N
 from .quantizer import compress_into, decompress_from
+from .store import KVStore, store_from_codes
 
 HAS_HIP = True
 
@@ -73,7 +74,8 @@ def fused_decompress_mse(indices: torch.Tensor, norms: torch.Tensor, Pi: torch.T
     bits = max(1, int(math.ceil(math.log2(max(centroids.numel(), 2)))))
     out = decompress_from(N.QKV_MODE_MSE, indices.reshape(n, d).to(torch.uint8).contiguous(), None,
                           norms.reshape(n).float().contiguous(), n, Pi.float().contiguous(),
-                          centroids.float().contiguous(), bits, None, 0.0, packed=False)
+                          centroids.float().contiguous(), bits, None, 0.0,
+                          fmt=N.QKV_FMT_UNPACKED)
     return out.reshape(*lead, d)
 
 
@@ -90,7 +92,7 @@ def fused_decompress_ip(mse_indices: torch.Tensor, qjl_signs: torch.Tensor, norm
                           qjl_signs.reshape(n, d).to(torch.uint8).contiguous(),
                           norms.reshape(n).float().contiguous(), n, Pi.float().contiguous(),
                           centroids.float().contiguous(), bits, S.float().contiguous(),
-                          qjl_scale, packed=False)
+                          qjl_scale, fmt=N.QKV_FMT_UNPACKED)
     return out.reshape(*lead, d)
 
 
@@ -105,24 +107,25 @@ class CompressedBlock:
     seq_len: int
 
 
-def attention_call(queries: torch.Tensor, kcodes: torch.Tensor, kqjl: torch.Tensor,
-                   knorm: torch.Tensor, vcodes: torch.Tensor, vnorm: torch.Tensor, T: int,
-                   Pi: torch.Tensor, key_centroids: torch.Tensor, val_centroids: torch.Tensor,
-                   S: torch.Tensor, qjl_scale: float, kbits: int, vbits: int, packed: bool,
-                   scale: Optional[float] = None, causal: bool = False,
-                   out_dtype: torch.dtype = torch.float32,
-                   workspace: Optional[torch.Tensor] = None,
-                   n_splits: Optional[int] = None) -> torch.Tensor:
-    """Launch the decode-attention kernels over a (B, Hkv, t_stride, row) cache.
-
-    Returns (B, Hq, Q, d).  ``workspace`` (uint8, on the device) is grown and
-    reused when given as a one-element list holder; a fresh one is allocated
-    otherwise."""
-    dev = N.require_gpu(queries, kcodes, kqjl, knorm, vcodes, vnorm, Pi, what="attention")
+def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Tensor,
+                    key_centroids: Sequence[float], val_centroids: Sequence[float],
+                    S: torch.Tensor, qjl_scale: float, scale: Optional[float] = None,
+                    causal: bool = False, out_dtype: torch.dtype = torch.float32,
+                    workspace: Optional[torch.Tensor] = None,
+                    n_splits: Optional[int] = None) -> torch.Tensor:
+    """Decode attention of (B, Hq, Q, d) queries over the first T tokens of a
+    cache store.  ``key_centroids`` / ``val_centroids`` are the codebook values
+    (host floats).  Returns (B, Hq, Q, d) in ``out_dtype``."""
+    dev = N.require_gpu(queries, store.kst, Pi, what="attention")
     B, Hq, Q, d = queries.shape
-    Hkv, t_stride = kcodes.shape[1], kcodes.shape[2]
+    Hkv = store.H
+    if B != store.B or d != store.d:
+        raise ValueError(f"queries {tuple(queries.shape)} do not match the cache "
+                         f"(B={store.B}, head_dim={store.d})")
     if Hq % Hkv != 0:
         raise ValueError(f"query heads ({Hq}) must be a multiple of kv heads ({Hkv})")
+    if T <= 0:
+        raise ValueError("No compressed KV blocks in cache. Call append() first.")
     if scale is None:
         scale = 1.0 / math.sqrt(d)
     L = N.lib()
@@ -130,24 +133,28 @@ def attention_call(queries: torch.Tensor, kcodes: torch.Tensor, kqjl: torch.Tens
         n_splits = L.qkv_attention_splits(B, Hq, Hkv, Q, d, T)
     need = L.qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits)
     if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
     q = queries.contiguous()
     if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         q = q.float()
-    Pi, key_centroids, val_centroids, S = N.dense(Pi, key_centroids, val_centroids, S)
-    for name, t in (("kcodes", kcodes), ("kqjl", kqjl), ("knorm", knorm), ("vcodes", vcodes),
-                    ("vnorm", vnorm)):
-        if not t.is_contiguous():
-            raise ValueError(f"attention: {name} must be a contiguous (B, H, T, ...) buffer")
+    Pi, S = N.dense(Pi, S)
+    kc, vc = N.HostFloats(key_centroids), N.HostFloats(val_centroids)
     out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
     N.check(L.qkv_decode_attention(
-        q.data_ptr(), N.dtype_code(q.dtype), kcodes.data_ptr(), kqjl.data_ptr(), knorm.data_ptr(),
-        vcodes.data_ptr(), vnorm.data_ptr(), t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits,
-        1 if packed else 0, Pi.data_ptr(), key_centroids.data_ptr(), val_centroids.data_ptr(),
-        S.data_ptr(), float(qjl_scale), float(scale), 1 if causal else 0, out.data_ptr(),
-        N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
-        N.stream(dev)))
+        q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
+        store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
+        store.mbits, store.vbits, Pi.data_ptr(), kc.ptr, vc.ptr, S.data_ptr(), float(qjl_scale),
+        float(scale), 1 if causal else 0, out.data_ptr(), N.dtype_code(out_dtype),
+        workspace.data_ptr(), workspace.numel(), n_splits, N.stream(dev)))
     return out
+
+
+def _bits_of(centroids: torch.Tensor) -> int:
+    n = centroids.numel()
+    b = max(1, int(math.ceil(math.log2(max(n, 2)))))
+    if (1 << b) != n:
+        raise ValueError(f"a codebook needs 2**bits centroids, got {n}")
+    return b
 
 
 def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[CompressedBlock],
@@ -157,20 +164,19 @@ def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[Compressed
                               total_kv_tokens: int = 0) -> torch.Tensor:
     """Attention over unpacked compressed blocks (quashkv/triton_kernels/attention.py:307-394).
 
-    Blocks hold one uint8 per code, as in the reference.  Query heads may be a
-    multiple of the blocks' kv heads (GQA)."""
+    Blocks hold one uint8 per code, as in the reference.  They are packed once
+    into a cache store and attended by the decode kernels.  Query heads may be
+    a multiple of the blocks' kv heads (GQA)."""
     if not blocks:
         raise ValueError("No compressed KV blocks in cache. Call append() first.")
     N.require_gpu(queries, Pi, what="fused_quantized_attention")
-    kc = torch.cat([b.mse_indices for b in blocks], dim=2).contiguous()
-    kq = torch.cat([b.qjl_signs for b in blocks], dim=2).contiguous()
-    kn = torch.cat([b.key_norms for b in blocks], dim=2).float().contiguous()
-    vc = torch.cat([b.val_indices for b in blocks], dim=2).contiguous()
-    vn = torch.cat([b.val_norms for b in blocks], dim=2).float().contiguous()
+    kc = torch.cat([b.mse_indices for b in blocks], dim=2)
+    kq = torch.cat([b.qjl_signs for b in blocks], dim=2)
+    kn = torch.cat([b.key_norms for b in blocks], dim=2).float()
+    vc = torch.cat([b.val_indices for b in blocks], dim=2)
+    vn = torch.cat([b.val_norms for b in blocks], dim=2).float()
     T = kc.shape[2]
-    kbits = max(1, int(math.ceil(math.log2(max(key_centroids.numel(), 2)))))
-    vbits = max(1, int(math.ceil(math.log2(max(val_centroids.numel(), 2)))))
-    return attention_call(queries, kc, kq, kn, vc, vn, T, Pi.float().contiguous(),
-                          key_centroids.float().contiguous(), val_centroids.float().contiguous(),
-                          S.float().contiguous(), qjl_scale, kbits, vbits, packed=False,
-                          scale=scale, causal=causal)
+    st = store_from_codes(kc, kq, kn, vc, vn, _bits_of(key_centroids), _bits_of(val_centroids))
+    kh = key_centroids.detach().float().cpu().tolist()
+    vh = val_centroids.detach().float().cpu().tolist()
+    return attention_store(queries, st, T, Pi, kh, vh, S, qjl_scale, scale=scale, causal=causal)

@@ -64,6 +64,12 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
     seq = out_seq if out_seq is not None else max(n, 1)
     gst = out_group_stride if out_group_stride is not None else seq
     flags = (N.QKV_FLAG_PACKED if packed else 0) | (N.QKV_FLAG_PRE_ROTATED if pre_rotated else 0)
+    rows = N.grouped_rows(n, seq, gst)
+    N.require_extent(codes, rows * (N.packed_row_bytes(d, bits) if packed else d), "compress codes")
+    if mode == N.QKV_MODE_IP:
+        N.require_extent(qjl, rows * (N.packed_row_bytes(d, 1) if packed else d), "compress qjl")
+    if not pre_rotated:
+        N.require_extent(norms, rows * 4, "compress norms")
     pi, boundaries, centroids, signs = N.dense(pi, boundaries, centroids, signs)
     N.check(N.lib().qkv_compress(
         mode, N.dtype_code(xf.dtype), flags, xf.data_ptr(), n, d, N.ptr(pi),
@@ -73,18 +79,33 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
 
 def decompress_from(mode: int, codes: torch.Tensor, qjl: Optional[torch.Tensor],
                     norms: torch.Tensor, n: int, pi: torch.Tensor, centroids: torch.Tensor,
-                    bits: int, signs: Optional[torch.Tensor], qjl_scale: float, packed: bool,
+                    bits: int, signs: Optional[torch.Tensor], qjl_scale: float, fmt: int,
                     in_seq: Optional[int] = None, in_group_stride: Optional[int] = None,
                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """Run the fused decompress kernel; returns an (n, d) tensor."""
+    """Run the fused decompress kernel on codes in format ``fmt``
+    (N.QKV_FMT_*); returns an (n, d) tensor."""
     d = pi.shape[0]
     dev = N.require_gpu(codes, norms, pi, what="decompress")
     out = torch.empty(n, d, dtype=out_dtype, device=dev)
     pi, centroids, signs = N.dense(pi, centroids, signs)
     seq = in_seq if in_seq is not None else max(n, 1)
     gst = in_group_stride if in_group_stride is not None else seq
+    if fmt == N.QKV_FMT_VTILES:
+        groups = (n + seq - 1) // seq
+        N.require_extent(codes, ((groups - 1) * gst + (seq + 31) // 32) * bits * d * 4,
+                         "decompress V tiles")
+        N.require_extent(norms, ((groups - 1) * gst * 32 + seq) * 4, "decompress norms")
+    else:
+        rows = N.grouped_rows(n, seq, gst)
+        rb = {N.QKV_FMT_UNPACKED: d, N.QKV_FMT_PACKED: N.packed_row_bytes(d, bits),
+              N.QKV_FMT_KPLANES: (bits + 1) * d // 8}[fmt]
+        N.require_extent(codes, rows * rb, "decompress codes")
+        N.require_extent(norms, rows * 4, "decompress norms")
+        if mode == N.QKV_MODE_IP and fmt != N.QKV_FMT_KPLANES:
+            N.require_extent(qjl, rows * (N.packed_row_bytes(d, 1) if fmt == N.QKV_FMT_PACKED
+                                          else d), "decompress qjl")
     N.check(N.lib().qkv_decompress(
-        mode, 1 if packed else 0, codes.data_ptr(), N.ptr(qjl), norms.data_ptr(), n, d, bits,
+        mode, int(fmt), codes.data_ptr(), N.ptr(qjl), norms.data_ptr(), n, d, bits,
         pi.data_ptr(), centroids.data_ptr(), N.ptr(signs), float(qjl_scale), seq, gst,
         out.data_ptr(), N.dtype_code(out_dtype), N.stream(dev)))
     return out
@@ -139,7 +160,8 @@ class MSEQuantizer:
         n = int(torch.Size(lead).numel())
         out = decompress_from(N.QKV_MODE_MSE, indices.reshape(n, self.d).to(torch.uint8).contiguous(),
                               None, norms.reshape(n).float().contiguous(), n, self.Pi,
-                              self.codebook.centroids, self.bits, None, 0.0, packed=False)
+                              self.codebook.centroids, self.bits, None, 0.0,
+                              fmt=N.QKV_FMT_UNPACKED)
         return out.reshape(*lead, self.d)
 
     def to(self, device) -> "MSEQuantizer":

@@ -210,8 +210,116 @@ def test_decompress_vs_oracle(d, packed, mode):
     from quashkv_amd.quantizer import decompress_from
     out = decompress_from(N.QKV_MODE_MSE if mode == "mse" else N.QKV_MODE_IP, c_in.to(DEV),
                           b_in.to(DEV), norms.to(DEV), n, pi.to(DEV), cents.to(DEV), bits,
-                          s.to(DEV), alpha, packed=packed)
+                          s.to(DEV), alpha, fmt=N.QKV_FMT_PACKED if packed else N.QKV_FMT_UNPACKED)
     assert_close(out, ref, rel=1e-5, cos=0.99999)
+
+
+# ------------------------------------------------------------ cache store
+
+def kplanes_ref(codes, qjl, mbits):
+    """Expected K store rows: plane r of every coordinate, then the QJL plane,
+    each as LSB-first 1-bit rows (numpy)."""
+    planes = [(codes >> r) & 1 for r in range(mbits)] + [qjl & 1]
+    return np.concatenate([R.pack_bits(p.astype(np.uint8), 1) for p in planes], axis=-1)
+
+
+def vtiles_ref(codes, vbits):
+    """Expected V store words (G, S/32, vbits, d) for codes (G, S, d), S % 32 == 0."""
+    G, S, d = codes.shape
+    c = codes.astype(np.uint64).reshape(G, S // 32, 32, d)
+    out = np.zeros((G, S // 32, vbits, d), dtype=np.uint64)
+    for k in range(vbits):
+        bits = (c >> k) & 1
+        out[:, :, k, :] = (bits << np.arange(32, dtype=np.uint64)[None, None, :, None]).sum(axis=2)
+    return out.astype(np.uint32)
+
+
+@pytest.mark.parametrize("d,mbits", [(64, 2), (96, 3), (128, 1), (128, 2)])
+def test_kplanes_pack_layout_and_roundtrip(d, mbits):
+    gen = torch.Generator().manual_seed(d + mbits)
+    G, S, C, t0 = 3, 37, 128, 5
+    codes = torch.randint(0, 1 << mbits, (G * S, d), generator=gen, dtype=torch.uint8)
+    qjl = torch.randint(0, 2, (G * S, d), generator=gen, dtype=torch.uint8)
+    krb = (mbits + 1) * d // 8
+    dst = torch.zeros(G, C, krb, dtype=torch.uint8, device=DEV)
+    L = N.lib()
+    codes_d, qjl_d = codes.to(DEV), qjl.to(DEV)   # keep the device copies alive
+    N.check(L.qkv_kplanes_pack(codes_d.data_ptr(), qjl_d.data_ptr(), G * S, d, mbits,
+                               dst.data_ptr() + t0 * krb, krb, S, C, 0))
+    torch.cuda.synchronize()
+    ref = kplanes_ref(codes.numpy(), qjl.numpy(), mbits).reshape(G, S, krb)
+    got = dst.cpu().numpy()
+    assert np.array_equal(got[:, t0:t0 + S], ref)
+    assert not got[:, :t0].any() and not got[:, t0 + S:].any()
+    c2 = torch.empty_like(codes, device=DEV)
+    q2 = torch.empty_like(qjl, device=DEV)
+    N.check(L.qkv_kplanes_unpack(dst.data_ptr() + t0 * krb, krb, G * S, d, mbits, S, C,
+                                 c2.data_ptr(), q2.data_ptr(), 0))
+    assert torch.equal(c2.cpu(), codes) and torch.equal(q2.cpu(), qjl)
+
+
+@pytest.mark.parametrize("vbits", [1, 2, 3, 4])
+def test_vtiles_pack_layout_rmw_and_roundtrip(vbits):
+    gen = torch.Generator().manual_seed(vbits)
+    G, d, C = 5, 128, 192
+    full = torch.randint(0, 1 << vbits, (G, C, d), generator=gen, dtype=torch.uint8)
+    dst = torch.zeros(G, C // 32, vbits, d, dtype=torch.int32, device=DEV)
+    L = N.lib()
+    # append in ragged pieces that straddle tiles (read-modify-write of shared words)
+    t0 = 0
+    for S in (1, 30, 2, 64, 33, 7, 55):
+        part = full[:, t0:t0 + S].contiguous().to(DEV)
+        N.check(L.qkv_vtiles_pack(part.data_ptr(), G, S, d, vbits, dst.data_ptr(), C // 32, t0, 0))
+        t0 += S
+    assert t0 == C
+    got = dst.cpu().numpy().view(np.uint32)
+    ref = vtiles_ref(full[:, :t0].numpy() if t0 % 32 == 0 else
+                     np.pad(full[:, :t0].numpy(), ((0, 0), (0, (-t0) % 32), (0, 0))), vbits)
+    nt = ref.shape[1]
+    assert np.array_equal(got[:, :nt], ref)
+    out = torch.empty(G, t0 - 3, d, dtype=torch.uint8, device=DEV)
+    N.check(L.qkv_vtiles_unpack(dst.data_ptr(), G, t0 - 3, d, vbits, C // 32, 3, out.data_ptr(), 0))
+    assert torch.equal(out.cpu(), full[:, 3:t0])
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_decompress_from_store_vs_oracle(d):
+    gen = torch.Generator().manual_seed(d)
+    B, H, T_ = 2, 3, 77
+    k = torch.randn(B, H, T_, d, generator=gen)
+    v = torch.randn(B, H, T_, d, generator=gen)
+    eng = Q.QuashKVEngine(head_dim=d, seed=5, device=DEV)
+    eng.append(k[:, :, :40].to(DEV), v[:, :, :40].to(DEV))
+    eng.append(k[:, :, 40:].to(DEV), v[:, :, 40:].to(DEV))
+    st = eng._store
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    mq = kq.mse_quantizer
+    from quashkv_amd.quantizer import decompress_from
+    n = B * H * T_
+    kh = decompress_from(N.QKV_MODE_MSE, st.kst, None, st.knorm, n, mq.Pi, mq.codebook.centroids,
+                         2, None, 0.0, N.QKV_FMT_KPLANES, in_seq=T_, in_group_stride=st.capacity)
+    kip = decompress_from(N.QKV_MODE_IP, st.kst, None, st.knorm, n, mq.Pi, mq.codebook.centroids,
+                          2, kq.S, kq.qjl_scale, N.QKV_FMT_KPLANES, in_seq=T_,
+                          in_group_stride=st.capacity)
+    vh = decompress_from(N.QKV_MODE_MSE, st.vst, None, st.vnorm, n, vq.Pi, vq.codebook.centroids,
+                         3, None, 0.0, N.QKV_FMT_VTILES, in_seq=T_,
+                         in_group_stride=st.capacity // 32)
+    kc, kb, vc = st.read_codes(0, T_)
+    pi = mq.Pi.cpu()
+    kn, vn = st.knorm[:, :, :T_].cpu(), st.vnorm[:, :, :T_].cpu()
+    assert_close(kh.reshape(B, H, T_, d), R.decompress_mse(kc.cpu(), kn, pi, mq.codebook.centroids.cpu()),
+                 rel=1e-5, cos=0.99999)
+    assert_close(kip.reshape(B, H, T_, d),
+                 R.decompress_ip(kc.cpu(), kb.cpu(), kn, pi, mq.codebook.centroids.cpu(), kq.S.cpu(),
+                                 kq.qjl_scale), rel=1e-5, cos=0.99999)
+    assert_close(vh.reshape(B, H, T_, d), R.decompress_mse(vc.cpu(), vn, vq.Pi.cpu(),
+                                                           vq.codebook.centroids.cpu()),
+                 rel=1e-5, cos=0.99999)
+    # the store holds exactly the oracle's codes of the same inputs (from identical y)
+    oc, ob, on = R.compress_ip(k, pi, mq.codebook.boundaries.cpu(), kq.S.cpu(),
+                               mq.codebook.centroids.cpu())
+    assert (kc.cpu() == oc).float().mean() > 0.999
+    assert torch.allclose(kn, on, rtol=1e-6)
 
 
 # -------------------------------------------------------------- attention
@@ -302,7 +410,8 @@ def test_attention_random_vs_oracle(d, Hkv, G, Qn, T_, causal, qdt):
 
 def test_attention_split_invariance_full_size():
     """cfg3 shape (B=32, Hq=32, Hkv=8, d=128, T=8192): the split-K result is
-    independent of the number of splits (size-independent property)."""
+    independent of the number of splits (size-independent property), and the
+    MFMA kernel (splits <= 2048 tokens) agrees with the VALU kernel (one split)."""
     gen = torch.Generator(device="cpu").manual_seed(2)
     B, Hkv, G, d, T_ = 32, 8, 4, 128, 8192
     eng = Q.QuashKVEngine(head_dim=d, seed=42, device=DEV, pack_storage=True)
@@ -314,15 +423,58 @@ def test_attention_split_invariance_full_size():
     q = torch.randn(B, Hkv * G, 1, d, generator=gen).to(DEV, torch.bfloat16)
     st = eng._store
     kq, vq = eng.key_quantizer, eng.value_quantizer
+    kh, vh = kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host
+    L = N.lib()
+    paths = []
     outs = []
-    for ns in (1, 7, 32):
-        outs.append(K.attention_call(q, st.kcodes, st.kqjl, st.knorm, st.vcodes, st.vnorm, T_,
-                                     kq.mse_quantizer.Pi, kq.mse_quantizer.codebook.centroids,
-                                     vq.codebook.centroids, kq.S, kq.qjl_scale, 2, 3, True,
-                                     n_splits=ns))
+    kc_h, vc_h = N.HostFloats(kh), N.HostFloats(vh)   # keep the host tables alive
+    for ns in (1, 4, 7, 32):
+        paths.append(L.qkv_attention_path(d, 2, 3, kc_h.ptr, vc_h.ptr, st.capacity, T_, ns))
+        outs.append(K.attention_store(q, st, T_, kq.mse_quantizer.Pi, kh, vh, kq.S, kq.qjl_scale,
+                                      n_splits=ns))
+    assert paths == [0, 1, 1, 1]
+    # MFMA split counts agree with each other over the whole batch
+    for o in outs[2:]:
+        assert_close(o, outs[1], rel=2e-5, cos=0.999999)
+    for o in outs:
+        assert torch.isfinite(o).all()
+    # every configuration against the oracle on a slice of the batch; the VALU
+    # kernel with ONE split sums 4096 tokens per coordinate serially in fp32,
+    # hence its looser bound
+    kc, kb, vc = (t[:4] for t in st.read_codes(0, T_))
+    blocks = [dict(kcodes=kc.cpu(), kbits=kb.cpu(), knorm=st.knorm[:4, :, :T_].cpu(),
+                   vcodes=vc.cpu(), vnorm=st.vnorm[:4, :, :T_].cpu())]
+    ref = R.attention_online(q[:4].float().cpu().reshape(4, Hkv, G, d), blocks,
+                             kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
+                             vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+    ref = ref.reshape(4, Hkv * G, 1, d)
+    assert_close(outs[0][:4], ref, rel=2e-4, cos=0.99999)
     for o in outs[1:]:
-        assert_close(o, outs[0], rel=1e-5, cos=0.999999)
-    assert torch.isfinite(outs[0]).all()
+        assert_close(o[:4], ref, rel=2e-5, cos=0.999999)
+
+
+@pytest.mark.parametrize("key_bits,value_bits", [(2, 1), (2, 2), (2, 4), (3, 1), (3, 2), (3, 4)])
+def test_mfma_bit_widths_vs_oracle(key_bits, value_bits):
+    gen = torch.Generator().manual_seed(10 * key_bits + value_bits)
+    B, Hkv, G, d, T_ = 2, 2, 3, 128, 1000
+    k = torch.randn(B, Hkv, T_, d, generator=gen)
+    v = torch.randn(B, Hkv, T_, d, generator=gen) * torch.exp(torch.randn(B, Hkv, T_, 1, generator=gen))
+    q = torch.randn(B, Hkv * G, 1, d, generator=gen)
+    eng = Q.QuashKVEngine(head_dim=d, key_bits=key_bits, value_bits=value_bits, seed=7, device=DEV)
+    eng.append(k.to(DEV), v.to(DEV))
+    st = eng._store
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    kh, vh = kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host
+    ns = N.lib().qkv_attention_splits(B, Hkv * G, Hkv, 1, d, T_)
+    kc_h, vc_h = N.HostFloats(kh), N.HostFloats(vh)
+    assert N.lib().qkv_attention_path(d, key_bits - 1, value_bits, kc_h.ptr, vc_h.ptr,
+                                      st.capacity, T_, ns) == 1
+    out = eng.attention(q.to(DEV))
+    blocks = _oracle_blocks(eng)
+    ref = R.attention_online(q.reshape(B, Hkv, G, d), blocks, kq.mse_quantizer.Pi.cpu(),
+                             kq.mse_quantizer.codebook.centroids.cpu(),
+                             vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+    assert_close(out, ref.reshape(B, Hkv * G, 1, d), rel=2e-5, cos=0.999999)
 
 
 def test_fused_attention_api_vs_golden(golden):

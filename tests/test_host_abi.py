@@ -53,17 +53,21 @@ def test_abi_rejects_before_launch():
     st = lib.qkv_compress(0, 0, 0, None, 4, 128, None, None, None, 7, None, None, None, None, 4, 4, None)
     assert st == N.QKV_E_INVALID and "bits must be in" in lib.qkv_last_error().decode()
     # empty cache
-    st = lib.qkv_decode_attention(None, 0, None, None, None, None, None, 0, 0, 1, 8, 8, 1, 128, 2, 3,
-                                  1, None, None, None, None, 0.1, 0.1, 0, None, 0, None, 0, 1, None)
+    st = lib.qkv_decode_attention(None, 0, None, None, None, None, 0, 0, 1, 8, 8, 1, 128, 2, 3,
+                                  None, None, None, None, 0.1, 0.1, 0, None, 0, None, 0, 1, None)
     assert st == N.QKV_E_INVALID and "No compressed KV blocks" in lib.qkv_last_error().decode()
     # workspace too small
-    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 1, 64, 64, 1, 8, 8, 1, 128, 2, 3, 1, 1, 1, 1, 1,
-                                  0.1, 0.1, 0, 1, 0, 16, 8, 1, None)
+    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 64, 64, 1, 8, 8, 1, 128, 2, 3, 1, 1, 1, 1,
+                                  0.1, 0.1, 0, 1, 0, 256, 8, 1, None)
     assert st == N.QKV_E_INVALID and "workspace too small" in lib.qkv_last_error().decode()
     # GQA divisibility
-    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 1, 64, 64, 1, 6, 4, 1, 128, 2, 3, 1, 1, 1, 1, 1,
-                                  0.1, 0.1, 0, 1, 0, 16, 1 << 30, 1, None)
+    st = lib.qkv_decode_attention(1, 0, 1, 1, 1, 1, 64, 64, 1, 6, 4, 1, 128, 2, 3, 1, 1, 1, 1,
+                                  0.1, 0.1, 0, 1, 0, 256, 1 << 30, 1, None)
     assert st == N.QKV_E_INVALID and "multiple of kv heads" in lib.qkv_last_error().decode()
+    # store converters validate shapes
+    assert lib.qkv_kplanes_pack(None, None, 4, 80, 2, None, 30, 4, 4, None) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_vtiles_pack(1, 1, 40, 128, 3, 1, 1, 0, None) == N.QKV_E_INVALID
+    assert "exceed" in lib.qkv_last_error().decode()
 
 
 def test_check_maps_status_to_exceptions():
@@ -77,7 +81,34 @@ def test_workspace_and_split_policy_are_consistent():
     for (B, Hq, Hkv, Q_, d) in [(32, 32, 8, 1, 128), (1, 32, 8, 1, 128), (16, 14, 2, 1, 64)]:
         ws = lib.qkv_attention_workspace_bytes(B, Hq, Hkv, Q_, d, 4)
         R = (Hq // Hkv) * Q_
-        assert ws == 4 * (B * Hkv * R * 2 * d + 4 * B * Hkv * R * d + 4 * B * Hkv * R * 2)
+        ch = (R + 3) // 4
+        assert ws == (4 * B * Hkv * R * 2 * d + B * Hkv * ch * 6 * 64 * 16 + B * Hkv * ch * 4 * 2 * 4
+                      + 4 * (4 * B * Hkv * R * d + 4 * B * Hkv * R * 2))
+    # splits keep every split within the LDS-resident length and fill the chip
+    for T_ in (1, 63, 64, 2048, 2049, 8192, 131072):
+        s = lib.qkv_attention_splits(32, 32, 8, 1, 128, T_)
+        assert 1 <= s <= max(1, (T_ + 63) // 64)
+        assert -(-T_ // s) <= 2048 or s == 1024
+
+
+def test_attention_path_selection():
+    lib = N.lib()
+    k2 = LloydMaxCodebook(128, 2).centroids_host
+    v3 = LloydMaxCodebook(128, 3).centroids_host
+    kc, vc = N.HostFloats(k2), N.HostFloats(v3)
+    assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 1
+    assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 1) == 0   # split > 2048
+    assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8160, 8150, 8) == 0   # stride % 64
+    assert lib.qkv_attention_path(96, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 0
+    for vb in (1, 2, 4):
+        v = N.HostFloats(LloydMaxCodebook(128, vb).centroids_host)
+        assert lib.qkv_attention_path(128, 2, vb, kc.ptr, v.ptr, 256, 256, 1) == 1
+    k1 = N.HostFloats(LloydMaxCodebook(128, 1).centroids_host)
+    assert lib.qkv_attention_path(128, 1, 3, k1.ptr, vc.ptr, 256, 256, 1) == 1
+    k3 = N.HostFloats(LloydMaxCodebook(128, 3).centroids_host)
+    assert lib.qkv_attention_path(128, 3, 3, k3.ptr, vc.ptr, 256, 256, 1) == 0
+    asym = N.HostFloats([-1.0, -0.25, 0.5, 1.0])
+    assert lib.qkv_attention_path(128, 2, 3, asym.ptr, vc.ptr, 256, 256, 1) == 0
 
 
 # -------------------------------------------------- product host parameters
