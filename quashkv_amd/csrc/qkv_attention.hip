@@ -34,6 +34,8 @@
 //   split_generic (any supported shape): VALU, one token per thread.
 #include <math.h>
 
+#include <algorithm>
+
 #include "qkv_common.h"
 
 typedef int qkv_v4i __attribute__((ext_vector_type(4)));
@@ -344,57 +346,96 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
                                                     float alpha, int Hq, int Hkv, int Q, int R,
                                                     int chunks, Tables tb,
                                                     qkv_v4i* __restrict__ aq,
-                                                    float* __restrict__ rowc) {
+                                                    float* __restrict__ rowc,
+                                                    float* __restrict__ qw) {
   constexpr int KRB = (MB + 1) * D / 8;
   constexpr int DPL = KRB / 16;
   constexpr int NU = 2 * DPL;
+  static_assert(D == 128, "one thread pair per output coordinate");
   __shared__ float qs[kRowsM][D];
+  __shared__ float part[2][kRowsM][D];
   __shared__ float qt[kRowsM][D];
   __shared__ float wv[kRowsM][D];
   __shared__ int fqs[kRowsM];
 
+  const int tid = threadIdx.x;
+  const int G = Hq / Hkv;
   const int bhc = blockIdx.x;
   const int chunk = bhc % chunks;
   const int bh = bhc / chunks;
   const int hkv = bh % Hkv, b = bh / Hkv;
-  const int G = Hq / Hkv;
   const int r0 = chunk * kRowsM;
   const int nr = min(kRowsM, R - r0);
-  const int tid = threadIdx.x;
-
-  for (int i = tid; i < kRowsM * D; i += 256) {
-    const int r = i / D, j = i - r * D;
+  // this thread's half row of Pi: all 16 float4 loads issued before use
+  const int j = tid % D, half = tid / D;
+  float4 prow[D / 8];
+  {
+    const float4* src = reinterpret_cast<const float4*>(pi + int64_t(j) * D + half * (D / 2));
+#pragma unroll
+    for (int k4 = 0; k4 < D / 8; ++k4) prow[k4] = src[k4];
+  }
+  float qv[kRowsM * D / 256];
+#pragma unroll
+  for (int x = 0; x < kRowsM * D / 256; ++x) {
+    const int i = tid + 256 * x;
+    const int r = i / D, jj = i - r * D;
     float v = 0.f;
     if (r < nr) {
       const int row = r0 + r;
       const int g = row / Q, qi = row - g * Q;
       const int h = hkv * G + g;
-      v = qkv_load(q, ((int64_t(b) * Hq + h) * Q + qi) * D + j, q_dtype);
+      v = qkv_load(q, ((int64_t(b) * Hq + h) * Q + qi) * D + jj, q_dtype);
     }
-    qs[r][j] = v;
+    qv[x] = v;
+  }
+  const float sgn = signs[j];
+#pragma unroll
+  for (int x = 0; x < kRowsM * D / 256; ++x) {
+    const int i = tid + 256 * x;
+    qs[i / D][i % D] = qv[x];
+  }
+  __syncthreads();
+  {  // q~_j = sum_k q_k Pi[j][k], this thread's half of k for all rows
+    float acc[kRowsM] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k4 = 0; k4 < D / 8; ++k4) {
+      const int k = half * (D / 2) + 4 * k4;
+#pragma unroll
+      for (int r = 0; r < kRowsM; ++r) {
+        acc[r] = fmaf(qs[r][k], prow[k4].x, acc[r]);
+        acc[r] = fmaf(qs[r][k + 1], prow[k4].y, acc[r]);
+        acc[r] = fmaf(qs[r][k + 2], prow[k4].z, acc[r]);
+        acc[r] = fmaf(qs[r][k + 3], prow[k4].w, acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kRowsM; ++r) part[half][r][j] = acc[r];
   }
   __syncthreads();
   for (int i = tid; i < kRowsM * D; i += 256) {
-    const int r = i / D, j = i - r * D;
-    const float* prow = pi + int64_t(j) * D;
-    float acc = 0.f;
-    for (int k = 0; k < D; ++k) acc = fmaf(qs[r][k], prow[k], acc);
-    qt[r][j] = acc;
-    wv[r][j] = alpha * fabsf(acc) * signs[j];
+    const int r = i / D, jj = i - r * D;  // jj == j: 256 threads, D = 128
+    const float v = part[0][r][jj] + part[1][r][jj];
+    const float w = alpha * fabsf(v) * sgn;
+    qt[r][jj] = v;
+    wv[r][jj] = w;
+    if (r < nr) {  // q~ and w for the VALU kernel, qw[b][hkv][row][2][D]
+      float* dst = qw + (int64_t(bh) * R + r0 + r) * 2 * D;
+      dst[jj] = v;
+      dst[D + jj] = w;
+    }
   }
   __syncthreads();
-  // per-row scale exponent and constant (one wave per row)
-  {
+  {  // per-row scale exponent and constant (one wave per row)
     const int wave = tid >> 6, lane = tid & 63;
     float kgmax = 0.f;
 #pragma unroll
     for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
     float mq = 0.f, mw = 0.f, sq = 0.f, sw = 0.f;
-    for (int j = lane; j < D; j += 64) {
-      mq = fmaxf(mq, fabsf(qt[wave][j]));
-      mw = fmaxf(mw, fabsf(wv[wave][j]));
-      sq += qt[wave][j];
-      sw += wv[wave][j];
+    for (int jj = lane; jj < D; jj += 64) {
+      mq = fmaxf(mq, fabsf(qt[wave][jj]));
+      mw = fmaxf(mw, fabsf(wv[wave][jj]));
+      sq += qt[wave][jj];
+      sw += wv[wave][jj];
     }
     mq = qkv_wave_max(mq);
     mw = qkv_wave_max(mw);
@@ -421,8 +462,8 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
 #pragma unroll
       for (int beta = 0; beta < 4; ++beta) {
         const int p = 32 * (g * DPL + (u >> 1)) + 8 * beta + i;
-        const int region = p / D, j = p - region * D;
-        const float W = region < MB ? 2.f * tb.kg[region] * qt[qrow][j] : 2.f * wv[qrow][j];
+        const int region = p / D, jj = p - region * D;
+        const float W = region < MB ? 2.f * tb.kg[region] * qt[qrow][jj] : 2.f * wv[qrow][jj];
         float zf = ldexpf(W, fqs[qrow] - i);
         if (i == 7) zf = -zf;
         const int Z = static_cast<int>(rintf(zf));
@@ -448,6 +489,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   constexpr int MTW = D / 64;            // 16-coordinate tiles per wave
   constexpr int NT = kSplitMax / 64;     // max 64-token tiles per split
   static_assert(KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
+  static_assert(D % 64 == 0, "value tiles split over 4 waves");
 
   // scores [tile][row][64]; rewritten in place as value-MFMA digits
   // [tile][col = 4 row + digit][64 K positions] (1 KB per tile either way)
@@ -479,44 +521,73 @@ __global__ __launch_bounds__(256) void split_mfma(
   const float fq = rowc[(bhc * kRowsM + lg) * 2 + 1];
   const bool row_ok = lg < nr;
   const int qi = (r0 + lg) % Q;
+  const float scale2 = scale * 1.4426950408889634f;  // scores in log2 units on this path
 
+  // Each wave scores 64-token tiles w, w + 4, ... as four 16-token MFMA
+  // groups.  K rows, key norms and value norms of the next PD1 tiles are in
+  // flight in a register ring while the current tile is scored.
   float mloc = -INFINITY, vmax = 0.f;
-  const int ngroups = (ntok + 15) >> 4;
+  const int ntile1 = (ntok + 63) >> 6;
   const uint8_t* kb = kst + bh * t_stride * KRB;
-  for (int gi = wave; gi < ngroups; gi += 4) {
-    const int tl = gi * 16 + ln;
-    const int64_t t = ts + tl;
-    const int64_t tc = min<int64_t>(t, te - 1);
-    const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + tc * KRB) + lg * DPL;
-    uint32_t kd[DPL];
+  const float* knb = knorm + bh * t_stride;
+  const float* vnb = vnorm + bh * t_stride;
+  constexpr int PD1 = 2;
+  uint32_t kd[PD1][4][DPL];
+  float kn[PD1][4], vv[PD1][4];
+  auto load1 = [&](int slot, int tile) {
 #pragma unroll
-    for (int x = 0; x < DPL; ++x) kd[x] = krow[x];
-    const float kn = knorm[bh * t_stride + tc];
-    qkv_v4i acc = {0, 0, 0, 0};
+    for (int sub = 0; sub < 4; ++sub) {
+      const int64_t tc = min<int64_t>(ts + tile * 64 + sub * 16 + ln, te - 1);
+      const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + tc * KRB) + lg * DPL;
 #pragma unroll
-    for (int u = 0; u < NU; ++u) {
-      const uint32_t x = kd[u >> 1];
-      const int sh = 4 * (u & 1);
-      qkv_v4i bo;
-      bo[0] = static_cast<int>(x & (0x01010101u << sh));
-      bo[1] = static_cast<int>(x & (0x02020202u << sh));
-      bo[2] = static_cast<int>(x & (0x04040404u << sh));
-      bo[3] = static_cast<int>(x & (0x08080808u << sh));
-      acc = mfma_i8(a[u], bo, acc);
+      for (int x = 0; x < DPL; ++x) kd[slot][sub][x] = krow[x];
+      kn[slot][sub] = knb[tc];
+      vv[slot][sub] = vnb[tc];
     }
-    mfma_settle();
-    const float z = static_cast<float>(acc[0]) + 128.f * static_cast<float>(acc[1]) +
-                    16384.f * static_cast<float>(acc[2]) + 2097152.f * static_cast<float>(acc[3]);
-    float s = kn * scale * fmaf(z, fq, cr);
-    const int valid = static_cast<int>(t < te) & static_cast<int>(row_ok) &
-                      (static_cast<int>(causal == 0) | static_cast<int>(t <= T - Q + qi));
-    s = valid ? s : -INFINITY;
-    sbuf[tl >> 6][lg][tl & 63] = s;
-    mloc = fmaxf(mloc, s);
-    if (lg == 0) {
-      const float vv = (t < te) ? vnorm[bh * t_stride + tc] : 0.f;
-      vn[tl] = vv;
-      vmax = fmaxf(vmax, vv);
+  };
+  auto score1 = [&](int slot, int tile) {
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      qkv_v4i acc = {0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const uint32_t x = kd[slot][sub][u >> 1];
+        const int sh = 4 * (u & 1);
+        qkv_v4i bo;
+        bo[0] = static_cast<int>(x & (0x01010101u << sh));
+        bo[1] = static_cast<int>(x & (0x02020202u << sh));
+        bo[2] = static_cast<int>(x & (0x04040404u << sh));
+        bo[3] = static_cast<int>(x & (0x08080808u << sh));
+        acc = mfma_i8(a[u], bo, acc);
+      }
+      mfma_settle();
+      const int tl = tile * 64 + sub * 16 + ln;
+      const int64_t t = ts + tl;
+      const float z = static_cast<float>(acc[0]) + 128.f * static_cast<float>(acc[1]) +
+                      16384.f * static_cast<float>(acc[2]) +
+                      2097152.f * static_cast<float>(acc[3]);
+      float sc = kn[slot][sub] * scale2 * fmaf(z, fq, cr);
+      const int valid = static_cast<int>(t < te) & static_cast<int>(row_ok) &
+                        (static_cast<int>(causal == 0) | static_cast<int>(t <= T - Q + qi));
+      sc = valid ? sc : -INFINITY;
+      sbuf[tile][lg][sub * 16 + ln] = sc;
+      mloc = fmaxf(mloc, sc);
+      const float vz = (t < te) ? vv[slot][sub] : 0.f;
+      if (lg == 0) vn[tl] = vz;
+      vmax = fmaxf(vmax, vz);
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < PD1; ++d)
+    if (wave + 4 * d < ntile1) load1(d, wave + 4 * d);
+  for (int tile0 = wave; tile0 < ntile1; tile0 += 4 * PD1) {
+#pragma unroll
+    for (int d = 0; d < PD1; ++d) {
+      const int tile = tile0 + 4 * d;
+      if (tile < ntile1) {
+        score1(d, tile);
+        if (tile + 4 * PD1 < ntile1) load1(d, tile + 4 * PD1);
+      }
     }
   }
 #pragma unroll
@@ -526,7 +597,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   if (lane == 0) red_v[wave] = vmax;
   __syncthreads();
 
-  // ---------------- phase 1.5: p = exp(s - m), value digits (wave w <-> row w)
+  // ---------------- phase 1.5: p = 2^(s - m), value digits (wave w <-> row w)
   const float m_q = fmaxf(fmaxf(red_m[0][wave], red_m[1][wave]),
                           fmaxf(red_m[2][wave], red_m[3][wave]));
   const float vmx = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
@@ -534,79 +605,99 @@ __global__ __launch_bounds__(256) void split_mfma(
   if (vmx > 0.f) frexpf(vmx, &ev);
   const int Fv = vmx > 0.f ? 27 - ev : 0;  // vmx 2^Fv < 2^27
   const int ntiles = (ntok + 63) >> 6;
-
-  float sreg[NT];
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) sreg[tt] = (tt < ntiles) ? sbuf[tt][wave][lane] : -INFINITY;
-  __syncthreads();
-
-  // token (lane) of a 64-token tile -> K position of the value MFMA:
-  // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
-  const int ii = lane & 7;
-  const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
   uint8_t* pbase = reinterpret_cast<uint8_t*>(&sbuf[0][0][0]);
-  float lsum = 0.f;
-  int64_t usum = 0;  // sum_t Z_t s_t: what an all-ones plane would accumulate
-  const bool live = wave < nr && m_q > -INFINITY;
-#pragma unroll
-  for (int tt = 0; tt < NT; ++tt) {
-    if (tt < ntiles) {
-      const int tl = tt * 64 + lane;
-      float pv = 0.f;
-      if (live && tl < ntok) {
-        const float p = expf(sreg[tt] - m_q);
-        lsum += p;
-        pv = p * vn[tl];
-      }
-      const int X = static_cast<int>(rintf(ldexpf(pv, Fv - ii)));  // Z_t s_t = X 2^i
-      usum += static_cast<int64_t>(X) << ii;
-      const int Z = ii == 7 ? -X : X;
-      uint8_t* dst = pbase + tt * 1024 + (4 * wave) * 64 + kpos;
-      dst[0] = static_cast<uint8_t>(Z & 127);
-      dst[64] = static_cast<uint8_t>((Z >> 7) & 127);
-      dst[128] = static_cast<uint8_t>((Z >> 14) & 127);
-      dst[192] = static_cast<uint8_t>((Z >> 21) & 0xff);
-    }
-  }
-  lsum = qkv_wave_sum(lsum);
-  usum = wave_sum_i64(usum);
-  if (lane == 0) {
-    lsum_s[wave] = lsum;
-    usum_s[wave] = usum;
-  }
-  __syncthreads();
 
-  // ---------------- phase 2: P V in the rotated domain, bit planes x digits
   qkv_v4i acc2[MTW][NP];
 #pragma unroll
   for (int mi = 0; mi < MTW; ++mi)
 #pragma unroll
     for (int s = 0; s < NP; ++s) acc2[mi][s] = qkv_v4i{0, 0, 0, 0};
-  const int64_t tile0 = ts >> 5;
+  // V plane words of the next PD2 tiles are in flight in a register ring.
+  const int64_t vtile0 = ts >> 5;
   const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
-  for (int tt = 0; tt < ntiles; ++tt) {
-    const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(pbase + tt * 1024 + ln * 64 + lg * 16);
-    const int64_t vt = tile0 + 2 * tt + blk;
+  constexpr int PD2 = 4;
+  uint32_t vw[PD2][MTW][VB];
+  auto load2 = [&](int slot, int tt) {
+    const int64_t vt = vtile0 + 2 * tt + blk;
 #pragma unroll
     for (int mi = 0; mi < MTW; ++mi) {
       const int j = 16 * (wave * MTW + mi) + ln;
-      uint32_t w[VB];
 #pragma unroll
-      for (int k = 0; k < VB; ++k) w[k] = vb[(vt * VB + k) * D + j];
+      for (int k = 0; k < VB; ++k) vw[slot][mi][k] = vb[(vt * VB + k) * D + j];
+    }
+  };
+  auto pv2 = [&](int slot, int tt) {
+    const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(pbase + tt * 1024 + ln * 64 + lg * 16);
+#pragma unroll
+    for (int mi = 0; mi < MTW; ++mi) {
 #pragma unroll
       for (int s = 0; s < NP; ++s) {
         const uint32_t sub = odd_subset(VB, s);
         uint32_t pw = 0;
 #pragma unroll
         for (int k = 0; k < VB; ++k)
-          if (sub & (1u << k)) pw ^= w[k];
+          if (sub & (1u << k)) pw ^= vw[slot][mi][k];
         qkv_v4i av;
         av[0] = static_cast<int>(pw & (0x01010101u << hsh));
         av[1] = static_cast<int>(pw & (0x02020202u << hsh));
         av[2] = static_cast<int>(pw & (0x04040404u << hsh));
         av[3] = static_cast<int>(pw & (0x08080808u << hsh));
         acc2[mi][s] = mfma_i8(av, bq, acc2[mi][s]);
+      }
+    }
+  };
+  // the first value tiles are in flight during phase 1.5
+#pragma unroll
+  for (int d = 0; d < PD2; ++d)
+    if (d < ntiles) load2(d, d);
+
+  // Row w's digits of tile tt occupy exactly the 256 bytes that held row w's
+  // scores of that tile, and one wave's LDS operations execute in order, so
+  // each wave converts its row in place without a barrier.
+  // token (lane) of a 64-token tile -> K position of the value MFMA:
+  // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
+  const int ii = lane & 7;
+  const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
+  const float zscale = ldexpf(1.f, Fv - ii);  // Z_t s_t = X 2^i, X = round(p' 2^(Fv - i))
+  float lsum = 0.f;
+  int64_t xsum = 0;
+  const bool live = wave < nr && m_q > -INFINITY;
+  for (int tt = 0; tt < ntiles; ++tt) {
+    const int tl = tt * 64 + lane;
+    const float sv = sbuf[tt][wave][lane];
+    float pv = 0.f;
+    if (live && tl < ntok) {
+      const float p = __builtin_amdgcn_exp2f(sv - m_q);
+      lsum += p;
+      pv = p * vn[tl];
+    }
+    const int X = static_cast<int>(fmaf(pv, zscale, 0.5f));
+    xsum += X;
+    const int Z = ii == 7 ? -X : X;
+    uint8_t* dst = pbase + tt * 1024 + (4 * wave) * 64 + kpos;
+    dst[0] = static_cast<uint8_t>(Z & 127);
+    dst[64] = static_cast<uint8_t>((Z >> 7) & 127);
+    dst[128] = static_cast<uint8_t>((Z >> 14) & 127);
+    dst[192] = static_cast<uint8_t>((Z >> 21) & 0xff);
+  }
+  lsum = qkv_wave_sum(lsum);
+  // sum_t Z_t s_t: what an all-ones plane would accumulate (this lane's tokens
+  // all share i = lane % 8)
+  const int64_t usum = wave_sum_i64(xsum << ii);
+  if (lane == 0) {
+    lsum_s[wave] = lsum;
+    usum_s[wave] = usum;
+  }
+  __syncthreads();
+
+  for (int tt0 = 0; tt0 < ntiles; tt0 += PD2) {
+#pragma unroll
+    for (int d = 0; d < PD2; ++d) {
+      const int tt = tt0 + d;
+      if (tt < ntiles) {
+        pv2(d, tt);
+        if (tt + PD2 < ntiles) load2(d, tt + PD2);
       }
     }
   }
@@ -644,56 +735,102 @@ __global__ __launch_bounds__(256) void split_mfma(
   }
   if (tid < nr) {
     const float mq = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
-    part_ml[(base + tid) * 2 + 0] = mq;
+    part_ml[(base + tid) * 2 + 0] = mq * 0.6931471805599453f;  // log2 -> natural units
     part_ml[(base + tid) * 2 + 1] = lsum_s[tid];
   }
 }
 
 // ------------------------------------------------------------ combine
 
-// One block per (b, hkv, r) query row: merge splits, normalise, un-rotate.
+constexpr int kRowsC = 4;    // query rows per combine block
+constexpr int kSplitBatch = 8;  // split partials loaded per batch (one latency)
+
+// One block per 4 consecutive query rows (b, kv head, row) of the B*Hkv*R
+// rows: merge the splits of every row (log-sum-exp), normalise by
+// max(l, 1e-8), un-rotate with Pi, store.  Every thread issues its loads in
+// batches (its 64 Pi[k][j], then 8 splits' partials at a time) so that the
+// kernel waits on few memory round trips; thread (j, half) covers half of k
+// and the two halves meet in LDS.
 template <int D>
-__global__ __launch_bounds__(128) void combine_kernel(const float* __restrict__ part_o,
-                                                      const float* __restrict__ part_ml,
-                                                      const float* __restrict__ pi, int n_splits,
-                                                      int B, int Hkv, int R, int Q, int Hq,
-                                                      void* __restrict__ out, int out_dtype) {
-  __shared__ float o[D];
-  __shared__ float wgt[1024];
-  __shared__ float lsum;
-  const int row = blockIdx.x;  // ((b * Hkv) + hkv) * R + r
+__global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict__ part_o,
+                                                        const float* __restrict__ part_ml,
+                                                        const float* __restrict__ pi,
+                                                        int n_splits, int B, int Hkv, int R,
+                                                        int Q, int Hq, void* __restrict__ out,
+                                                        int out_dtype) {
+  __shared__ float o[kRowsC][D];
+  __shared__ float red[2][kRowsC][D];
   const int tid = threadIdx.x;
-  const int64_t stride = int64_t(B) * Hkv * R;
-  if (tid == 0) {
-    float M = -INFINITY;
-    for (int s = 0; s < n_splits; ++s) M = fmaxf(M, part_ml[(s * stride + row) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < n_splits; ++s) {
-      const float m = part_ml[(s * stride + row) * 2];
-      const float w = (m == -INFINITY) ? 0.f : expf(m - M);
-      wgt[s] = w;
-      L = fmaf(w, part_ml[(s * stride + row) * 2 + 1], L);
+  const int j = tid % D, half = tid / D;
+  const int64_t nrows = int64_t(B) * Hkv * R;
+  const int64_t row0 = int64_t(blockIdx.x) * kRowsC;
+  const int nr = static_cast<int>(min<int64_t>(kRowsC, nrows - row0));
+  float pcol[D / 2];
+#pragma unroll
+  for (int k = 0; k < D / 2; ++k) pcol[k] = pi[(half * (D / 2) + k) * D + j];
+  // rows half, half + 2 of this block for coordinate j
+#pragma unroll
+  for (int rr = 0; rr < kRowsC / 2; ++rr) {
+    const int r = half + 2 * rr;
+    if (r >= nr) continue;
+    const int64_t row = row0 + r;
+    float M = -INFINITY, L = 0.f, a = 0.f;  // running log-sum-exp merge
+    for (int s0 = 0; s0 < n_splits; s0 += kSplitBatch) {
+      float mb[kSplitBatch], lb[kSplitBatch], ob[kSplitBatch];
+#pragma unroll
+      for (int x = 0; x < kSplitBatch; ++x) {
+        const int sidx = s0 + x;
+        const bool ok = sidx < n_splits;
+        const int64_t base = (ok ? sidx : 0) * nrows + row;
+        mb[x] = ok ? part_ml[base * 2] : -INFINITY;
+        lb[x] = ok ? part_ml[base * 2 + 1] : 0.f;
+        ob[x] = ok ? part_o[base * D + j] : 0.f;
+      }
+      float bm = M;
+#pragma unroll
+      for (int x = 0; x < kSplitBatch; ++x) bm = fmaxf(bm, mb[x]);
+      if (bm != -INFINITY) {
+        const float c = (M == -INFINITY) ? 0.f : expf(M - bm);
+        L *= c;
+        a *= c;
+#pragma unroll
+        for (int x = 0; x < kSplitBatch; ++x) {
+          if (mb[x] != -INFINITY) {
+            const float w = expf(mb[x] - bm);
+            L = fmaf(w, lb[x], L);
+            a = fmaf(w, ob[x], a);
+          }
+        }
+        M = bm;
+      }
     }
-    lsum = fmaxf(L, 1e-8f);
+    o[r][j] = a / fmaxf(L, 1e-8f);
   }
   __syncthreads();
-  if (tid < D) {
-    float a = 0.f;
-    for (int s = 0; s < n_splits; ++s)
-      if (wgt[s] != 0.f) a = fmaf(wgt[s], part_o[(s * stride + row) * D + tid], a);
-    o[tid] = a / lsum;
-  }
+  float acc[kRowsC];
+#pragma unroll
+  for (int r = 0; r < kRowsC; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int k = 0; k < D / 2; ++k)
+#pragma unroll
+    for (int r = 0; r < kRowsC; ++r) acc[r] = fmaf(o[r][half * (D / 2) + k], pcol[k], acc[r]);
+#pragma unroll
+  for (int r = 0; r < kRowsC; ++r) red[half][r][j] = acc[r];
   __syncthreads();
-  if (tid >= D) return;
-  float acc = 0.f;
-  for (int k = 0; k < D; ++k) acc = fmaf(o[k], pi[k * D + tid], acc);
-  const int r = row % R;
-  const int hkv = (row / R) % Hkv;
-  const int b = row / (R * Hkv);
+  if (half != 0) return;
   const int G = Hq / Hkv;
-  const int g = r / Q, qi = r - (r / Q) * Q;
-  const int h = hkv * G + g;
-  qkv_store(out, ((int64_t(b) * Hq + h) * Q + qi) * D + tid, acc, out_dtype);
+#pragma unroll
+  for (int r = 0; r < kRowsC; ++r) {
+    if (r < nr) {
+      const int64_t row = row0 + r;  // ((b * Hkv) + hkv) * R + r
+      const int rq = static_cast<int>(row % R);
+      const int hkv = static_cast<int>((row / R) % Hkv);
+      const int b = static_cast<int>(row / (int64_t(R) * Hkv));
+      const int g = rq / Q, qi = rq - g * Q;
+      qkv_store(out, ((int64_t(b) * Hq + hkv * G + g) * Q + qi) * D + j,
+                red[0][r][j] + red[1][r][j], out_dtype);
+    }
+  }
 }
 
 // ------------------------------------------------------------ host helpers
@@ -778,6 +915,21 @@ int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, in
   return QKV_OK;
 }
 
+// Resident split_mfma workgroups per CU (queried once; the kernel's LDS and
+// register use set it).
+int mfma_blocks_per_cu() {
+  static int n = 0;
+  if (n == 0) {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<128, 2, 3>, 256, 0) !=
+            hipSuccess ||
+        v <= 0)
+      v = 2;
+    n = v;
+  }
+  return n;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------ C ABI
@@ -788,15 +940,27 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
   const int R = (Hq / Hkv) * Q;
   const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM);
-  const int64_t target = int64_t(qkv_num_cus()) * 2;  // workgroups to fill the chip
-  int64_t s = (target + groups - 1) / groups;
+  const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu();
   const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
-  const int64_t max_s = (T + 63) / 64;
-  if (s < min_s) s = min_s;
+  const int64_t max_s = std::min<int64_t>((T + 63) / 64, 1024);
+  int64_t s = std::max<int64_t>(min_s, (slots + groups - 1) / groups);
   if (s > max_s) s = max_s;
-  if (s > 1024) s = 1024;
-  if (s < 1) s = 1;
-  return static_cast<int32_t>(s);
+  // prefer a count that fills whole rounds of resident workgroups (no short
+  // last round), searching a little above the minimum
+  int64_t best = s;
+  double best_eff = 0.0;
+  for (int64_t c = s; c <= std::min<int64_t>(max_s, 4 * s); ++c) {
+    const int64_t wg = groups * c;
+    const int64_t rounds = (wg + slots - 1) / slots;
+    const double eff = static_cast<double>(wg) / static_cast<double>(rounds * slots);
+    if (eff > best_eff + 1e-9) {
+      best_eff = eff;
+      best = c;
+    }
+    if (eff > 0.999) break;
+  }
+  if (best < 1) best = 1;
+  return static_cast<int32_t>(best);
 }
 
 extern "C" int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
@@ -829,6 +993,21 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
   auto s = static_cast<hipStream_t>(stream);
+  if (tb.mfma_ok && d == 128) {
+    // MFMA query operands; the same kernel writes q~ and w for the VALU kernel
+    const int chunks = (R + kRowsM - 1) / kRowsM;
+    const dim3 grid(B * Hkv * chunks);
+    if (kbits == 2)
+      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
+                         at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
+    else
+      hipLaunchKernelGGL((prepare_mfma<128, 1>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
+                         at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
   switch (d) {
 #define QKV_CASE(DD)                                                                        \
   case DD:                                                                                  \
@@ -841,19 +1020,6 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
 #undef QKV_CASE
   }
   QKV_LAUNCHED();
-  if (tb.mfma_ok && d == 128) {
-    const int chunks = (R + kRowsM - 1) / kRowsM;
-    const dim3 grid(B * Hkv * chunks);
-    if (kbits == 2)
-      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
-                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
-                         at<float>(workspace, L.rowc));
-    else
-      hipLaunchKernelGGL((prepare_mfma<128, 1>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
-                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
-                         at<float>(workspace, L.rowc));
-    QKV_LAUNCHED();
-  }
   return QKV_OK;
 }
 
@@ -937,9 +1103,11 @@ extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t
   switch (d) {
 #define QKV_CASE(DD)                                                                         \
   case DD:                                                                                   \
-    hipLaunchKernelGGL(combine_kernel<DD>, dim3(B * Hkv * R), dim3(128), 0, s,              \
-                       at<float>(workspace, L.po), at<float>(workspace, L.pml), pi,         \
-                       n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                          \
+    hipLaunchKernelGGL(combine_kernel<DD>,                                                   \
+                       dim3(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC)), \
+                       dim3(2 * DD), 0, s, at<float>(workspace, L.po),                       \
+                       at<float>(workspace, L.pml), pi, n_splits, B, Hkv, R, Q, Hq, out,     \
+                       out_dtype);                                                           \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
