@@ -5,14 +5,14 @@ compressed KV cache -- B=32, 32 query heads over 8 kv heads (GQA 4:1),
 head_dim 128, context 8192; keys 3-bit IP (2-bit MSE + 1-bit QJL), values
 3-bit MSE; bf16 queries; keys N(0,1) with 4 outlier channels x10.  The packed
 cache is prebuilt by the HIP compress kernel, then decode steps are timed.
-A step = one decode-attention call over the whole cache (prepare + split-K
-partial + combine).  Several distinct caches are rotated between steps so the
+A step = one decode-attention call over the whole cache (prepare, then the
+split-K kernel whose last split per row group merges and stores).  Several distinct caches are rotated between steps so the
 256 MB MALL cannot serve a repeat.  Compress (bf16 K and V -> packed cache) is
 timed separately and reported in Gvec/s.
 
 Prints one JSON line.  `value` is packed-byte throughput of the decode step
 (GB/s, inputs resident in HBM); `roofline` covers the dominant kernel (the
-split-K partial), timed with HIP events on the launch stream; `cpu_baseline`
+split-K kernel with its merge), timed with HIP events on the launch stream; `cpu_baseline`
 is the CPU oracle on a bounded sample of the same workload.
 """
 
@@ -164,15 +164,13 @@ def main() -> None:
                                           ws_bytes, splits, sptr))
         if ev is not None:
             ev[0].record(stream)
-        N.check(lib.qkv_attention_partial(st.kst.data_ptr(), st.knorm.data_ptr(),
-                                          st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, T,
-                                          B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, kc_h.ptr,
-                                          vc_h.ptr, scale, 0, ws.data_ptr(), ws_bytes, splits,
-                                          sptr))
+        N.check(lib.qkv_attention_run(st.kst.data_ptr(), st.knorm.data_ptr(), st.vst.data_ptr(),
+                                      st.vnorm.data_ptr(), st.capacity, T, B, HQ, HKV, 1, D,
+                                      KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr,
+                                      vc_h.ptr, scale, 0, out.data_ptr(), N.QKV_F32,
+                                      ws.data_ptr(), ws_bytes, splits, sptr))
         if ev is not None:
             ev[1].record(stream)
-        N.check(lib.qkv_attention_combine(B, HQ, HKV, 1, D, mq.Pi.data_ptr(), out.data_ptr(),
-                                          N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
 
     for i in range(args.warmup):
         step(i)
@@ -236,7 +234,8 @@ def main() -> None:
         "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
                                               / PEAK_HBM_GBS, 2),
         "roofline": {
-            "kernel": ("split_mfma" if path == 1 else "split_generic") + " (qkv_attention_partial)",
+            "kernel": ("split_mfma (splits + merge)" if path == 1
+                       else "split_generic + combine_kernel") + " (qkv_attention_run)",
             "bound": "hbm",
             "achieved": round(partial_gbs, 2),
             "peak": PEAK_HBM_GBS,

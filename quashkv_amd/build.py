@@ -33,6 +33,8 @@ CFLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (no accvgpr moves before the VALU reads them)
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

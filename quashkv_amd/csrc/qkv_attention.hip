@@ -23,9 +23,9 @@
 //     * a 0/1 plane becomes int8 MFMA operands with ONE v_and per 4 bytes:
 //       word & (0x01010101 << i) leaves bit i of each byte in place, i.e. the
 //       byte value is b * 2^i (b * -128 for i = 7);
-//     * the other operand carries the real weights as 28-bit fixed point split
-//       into four int8 digits, pre-divided by the byte's 2^i, so the i32
-//       accumulators are exact; the digit rows are recombined in fp32.
+//     * the other operand carries the real weights as 30-bit fixed point split
+//       into four signed base-256 int8 digits, pre-divided by the byte's 2^i,
+//       so the i32 accumulators are exact; digit rows are recombined after.
 //     Scores: C[4 rows x 4 digits][16 tokens] += A(query weights)[16][64] x
 //     B(K planes)[64][16].  Values: C[16 coords][4 rows x 4 digits] +=
 //     A(V planes)[16][64 tokens] x B(p * n_v digits)[64 tokens][16].
@@ -35,6 +35,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cmath>
 
 #include "qkv_common.h"
 
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
       const float wmax = 2.f * fmaxf(kgmax * mq, mw);
       int e = 0;
       if (wmax > 0.f) frexpf(wmax, &e);  // wmax = f 2^e, f in [0.5, 1)
-      const int fq = wmax > 0.f ? 27 - e : 0;
+      const int fq = wmax > 0.f ? 30 - e : 0;  // |Z| < 2^30
       fqs[wave] = fq;
       rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 0] = tb.kconst * sq - sw;
       rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 1] = ldexpf(1.f, -fq);
@@ -467,8 +468,8 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
         float zf = ldexpf(W, fqs[qrow] - i);
         if (i == 7) zf = -zf;
         const int Z = static_cast<int>(rintf(zf));
-        const int dg = v < 3 ? ((Z >> (7 * v)) & 127) : (Z >> 21);
-        word |= (static_cast<uint32_t>(dg) & 0xffu) << (8 * beta);
+        const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+        word |= ((dg >> (8 * v)) & 0xffu) << (8 * beta);
       }
     }
     aq[(int64_t(bhc) * NU + u) * 64 + ln][e] = static_cast<int>(word);
@@ -487,14 +488,18 @@ __global__ __launch_bounds__(256) void split_mfma(
   constexpr int NU = 2 * DPL;            // score MFMAs per 16 tokens
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int MTW = D / 64;            // 16-coordinate tiles per wave
-  constexpr int NT = kSplitMax / 64;     // max 64-token tiles per split
   static_assert(KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
   static_assert(D % 64 == 0, "value tiles split over 4 waves");
 
   // scores [tile][row][64]; rewritten in place as value-MFMA digits
   // [tile][col = 4 row + digit][64 K positions] (1 KB per tile either way)
-  __shared__ float sbuf[NT][kRowsM][64];
-  __shared__ float vn[kSplitMax];
+  // dynamic LDS, sized by the host to this launch's split length:
+  // [ntile_cap][row][64] scores (rewritten in place as value digits), then
+  // [ntile_cap * 64] value norms
+  extern __shared__ __align__(16) float smem[];
+  const int ntile_cap = static_cast<int>((split_len + 63) >> 6);
+  float(*sbuf)[kRowsM][64] = reinterpret_cast<float(*)[kRowsM][64]>(smem);
+  float* vn = smem + ntile_cap * kRowsM * 64;
   __shared__ float red_m[4][kRowsM];
   __shared__ float red_v[4];
   __shared__ float lsum_s[kRowsM];
@@ -528,52 +533,65 @@ __global__ __launch_bounds__(256) void split_mfma(
   // flight in a register ring while the current tile is scored.
   float mloc = -INFINITY, vmax = 0.f;
   const int ntile1 = (ntok + 63) >> 6;
-  const uint8_t* kb = kst + bh * t_stride * KRB;
-  const float* knb = knorm + bh * t_stride;
-  const float* vnb = vnorm + bh * t_stride;
-  constexpr int PD1 = 2;
+  // split-relative bases: per-lane offsets stay 32-bit
+  const uint8_t* kbs = kst + (bh * t_stride + ts) * KRB;
+  const float* knbs = knorm + bh * t_stride + ts;
+  const float* vnbs = vnorm + bh * t_stride + ts;
+  // causal: token tl (split-relative) is visible to this lane's row iff
+  // ts + tl <= T - Q + qi
+  const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
+  const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
+  constexpr int PD1 = 3;
   uint32_t kd[PD1][4][DPL];
   float kn[PD1][4], vv[PD1][4];
+  // Tokens past the split end are read too (masked when scored): the store
+  // capacity is a multiple of 64 and >= T, so whole 64-token tiles of the
+  // split stay inside it.  Addresses are then linear in the tile index.
+  const uint32_t* krow0 = reinterpret_cast<const uint32_t*>(kbs + ln * KRB) + lg * DPL;
   auto load1 = [&](int slot, int tile) {
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
-      const int64_t tc = min<int64_t>(ts + tile * 64 + sub * 16 + ln, te - 1);
-      const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + tc * KRB) + lg * DPL;
+      const int t16 = tile * 64 + sub * 16;
+      const uint32_t* krow = krow0 + t16 * (KRB / 4);
 #pragma unroll
       for (int x = 0; x < DPL; ++x) kd[slot][sub][x] = krow[x];
-      kn[slot][sub] = knb[tc];
-      vv[slot][sub] = vnb[tc];
+      kn[slot][sub] = knbs[t16 + ln];
+      vv[slot][sub] = vnbs[t16 + ln];
     }
   };
   auto score1 = [&](int slot, int tile) {
+    // four independent 16-token chains interleaved, one settle for all
+    qkv_v4i acc[4];
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) {
-      qkv_v4i acc = {0, 0, 0, 0};
+    for (int sub = 0; sub < 4; ++sub) acc[sub] = qkv_v4i{0, 0, 0, 0};
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
+    for (int u = 0; u < NU; ++u) {
+      const int sh = 4 * (u & 1);
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
         const uint32_t x = kd[slot][sub][u >> 1];
-        const int sh = 4 * (u & 1);
         qkv_v4i bo;
         bo[0] = static_cast<int>(x & (0x01010101u << sh));
         bo[1] = static_cast<int>(x & (0x02020202u << sh));
         bo[2] = static_cast<int>(x & (0x04040404u << sh));
         bo[3] = static_cast<int>(x & (0x08080808u << sh));
-        acc = mfma_i8(a[u], bo, acc);
+        acc[sub] = mfma_i8(a[u], bo, acc[sub]);
       }
-      mfma_settle();
+    }
+    mfma_settle();
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
       const int tl = tile * 64 + sub * 16 + ln;
-      const int64_t t = ts + tl;
-      const float z = static_cast<float>(acc[0]) + 128.f * static_cast<float>(acc[1]) +
-                      16384.f * static_cast<float>(acc[2]) +
-                      2097152.f * static_cast<float>(acc[3]);
-      float sc = kn[slot][sub] * scale2 * fmaf(z, fq, cr);
-      const int valid = static_cast<int>(t < te) & static_cast<int>(row_ok) &
-                        (static_cast<int>(causal == 0) | static_cast<int>(t <= T - Q + qi));
-      sc = valid ? sc : -INFINITY;
+      const float z = static_cast<float>(acc[sub][0]) + 256.f * static_cast<float>(acc[sub][1]) +
+                      65536.f * static_cast<float>(acc[sub][2]) +
+                      16777216.f * static_cast<float>(acc[sub][3]);
+      const float sc0 = kn[slot][sub] * scale2 * fmaf(z, fq, cr);
+      const bool in = tl < ntok;
+      const float sc = (in & row_ok & (tl <= clim)) ? sc0 : -INFINITY;
       sbuf[tile][lg][sub * 16 + ln] = sc;
       mloc = fmaxf(mloc, sc);
-      const float vz = (t < te) ? vv[slot][sub] : 0.f;
-      if (lg == 0) vn[tl] = vz;
+      const float vz = in ? vv[slot][sub] : 0.f;
+      vn[tl] = vz;  // the four lane groups store the same value
       vmax = fmaxf(vmax, vz);
     }
   };
@@ -603,7 +621,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   const float vmx = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
   int ev = 0;
   if (vmx > 0.f) frexpf(vmx, &ev);
-  const int Fv = vmx > 0.f ? 27 - ev : 0;  // vmx 2^Fv < 2^27
+  const int Fv = vmx > 0.f ? 30 - ev : 0;  // vmx 2^Fv < 2^30
   const int ntiles = (ntok + 63) >> 6;
   uint8_t* pbase = reinterpret_cast<uint8_t*>(&sbuf[0][0][0]);
 
@@ -616,7 +634,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   const int64_t vtile0 = ts >> 5;
   const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
-  constexpr int PD2 = 4;
+  constexpr int PD2 = 8;
   uint32_t vw[PD2][MTW][VB];
   auto load2 = [&](int slot, int tt) {
     const int64_t vt = vtile0 + 2 * tt + blk;
@@ -643,7 +661,7 @@ __global__ __launch_bounds__(256) void split_mfma(
         av[1] = static_cast<int>(pw & (0x02020202u << hsh));
         av[2] = static_cast<int>(pw & (0x04040404u << hsh));
         av[3] = static_cast<int>(pw & (0x08080808u << hsh));
-        acc2[mi][s] = mfma_i8(av, bq, acc2[mi][s]);
+        acc2[mi][s] = mfma_i8(bq, av, acc2[mi][s]);  // C[row x digit][coordinate]
       }
     }
   };
@@ -654,32 +672,31 @@ __global__ __launch_bounds__(256) void split_mfma(
 
   // Row w's digits of tile tt occupy exactly the 256 bytes that held row w's
   // scores of that tile, and one wave's LDS operations execute in order, so
-  // each wave converts its row in place without a barrier.
+  // each wave converts its row in place without a barrier.  Tokens past the
+  // split end hold -inf scores and zero norms (phase 1 writes whole tiles).
   // token (lane) of a 64-token tile -> K position of the value MFMA:
   // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
   const int ii = lane & 7;
   const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
   const float zscale = ldexpf(1.f, Fv - ii);  // Z_t s_t = X 2^i, X = round(p' 2^(Fv - i))
+  const bool live = wave < nr && m_q > -INFINITY;
+  const float m_use = live ? m_q : INFINITY;  // absent row: every p = 0
   float lsum = 0.f;
   int64_t xsum = 0;
-  const bool live = wave < nr && m_q > -INFINITY;
   for (int tt = 0; tt < ntiles; ++tt) {
-    const int tl = tt * 64 + lane;
-    const float sv = sbuf[tt][wave][lane];
-    float pv = 0.f;
-    if (live && tl < ntok) {
-      const float p = __builtin_amdgcn_exp2f(sv - m_q);
-      lsum += p;
-      pv = p * vn[tl];
-    }
+    const float p = __builtin_amdgcn_exp2f(sbuf[tt][wave][lane] - m_use);
+    lsum += p;
+    const float pv = p * vn[tt * 64 + lane];
     const int X = static_cast<int>(fmaf(pv, zscale, 0.5f));
     xsum += X;
     const int Z = ii == 7 ? -X : X;
+    // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
+    const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
     uint8_t* dst = pbase + tt * 1024 + (4 * wave) * 64 + kpos;
-    dst[0] = static_cast<uint8_t>(Z & 127);
-    dst[64] = static_cast<uint8_t>((Z >> 7) & 127);
-    dst[128] = static_cast<uint8_t>((Z >> 14) & 127);
-    dst[192] = static_cast<uint8_t>((Z >> 21) & 0xff);
+    dst[0] = static_cast<uint8_t>(dg);
+    dst[64] = static_cast<uint8_t>(dg >> 8);
+    dst[128] = static_cast<uint8_t>(dg >> 16);
+    dst[192] = static_cast<uint8_t>(dg >> 24);
   }
   lsum = qkv_wave_sum(lsum);
   // sum_t Z_t s_t: what an all-ones plane would accumulate (this lane's tokens
@@ -703,35 +720,27 @@ __global__ __launch_bounds__(256) void split_mfma(
   }
 
   // ---------------- epilogue: digits + planes -> fp32, write the partials
-  // Per plane S: Y_S = sum_v 2^(7v) acc_S[v] = sum_t Z_t s_t phi_S,t exactly
-  // (int64; the digits live in the 4 lanes of a column quad), and
+  // Lane (g = lane / 16, c = lane % 16) holds, per 16-coordinate tile and
+  // plane S, the four digit accumulators of row g at coordinate c.
+  // Y_S = sum_v 2^(8v) acc_S[v] = sum_t Z_t s_t phi_S,t exactly (int64), and
   // sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U) is formed in integers
   // before the only rounding: O = 2^-Fv sum_S g_S (2 Y_S - U).
   mfma_settle();
-  const int qcol = ln >> 2, vd = ln & 3;
   const float oscale = ldexpf(1.f, -Fv);
-  const int64_t urow = usum_s[qcol];
+  const int64_t urow = usum_s[lg];
   const int64_t base = ((int64_t(split) * gridDim.z + b) * Hkv + hkv) * R + r0;
 #pragma unroll
   for (int mi = 0; mi < MTW; ++mi) {
-    float o[4];
+    float val = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float val = 0.f;
-#pragma unroll
-      for (int s = 0; s < NP; ++s) {
-        int64_t y = static_cast<int64_t>(acc2[mi][s][e]) << (7 * vd);
-        y += shfl_xor_i64(y, 1);
-        y += shfl_xor_i64(y, 2);
-        val = fmaf(tb.vg[s], static_cast<float>(2 * y - urow), val);
-      }
-      o[e] = val * oscale;
+    for (int s = 0; s < NP; ++s) {
+      const int64_t y = static_cast<int64_t>(acc2[mi][s][0]) +
+                        (static_cast<int64_t>(acc2[mi][s][1]) << 8) +
+                        (static_cast<int64_t>(acc2[mi][s][2]) << 16) +
+                        (static_cast<int64_t>(acc2[mi][s][3]) << 24);
+      val = fmaf(tb.vg[s], static_cast<float>(2 * y - urow), val);
     }
-    if (vd == 0 && qcol < nr) {
-      const int j0 = 16 * (wave * MTW + mi) + 4 * lg;
-      float4* dst = reinterpret_cast<float4*>(part_o + (base + qcol) * D + j0);
-      *dst = make_float4(o[0], o[1], o[2], o[3]);
-    }
+    if (lg < nr) part_o[(base + lg) * D + 16 * (wave * MTW + mi) + ln] = val * oscale;
   }
   if (tid < nr) {
     const float mq = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
@@ -742,15 +751,16 @@ __global__ __launch_bounds__(256) void split_mfma(
 
 // ------------------------------------------------------------ combine
 
-constexpr int kRowsC = 4;    // query rows per combine block
+constexpr int kRowsC = 4;       // query rows merged per block
 constexpr int kSplitBatch = 8;  // split partials loaded per batch (one latency)
 
-// One block per 4 consecutive query rows (b, kv head, row) of the B*Hkv*R
-// rows: merge the splits of every row (log-sum-exp), normalise by
-// max(l, 1e-8), un-rotate with Pi, store.  Every thread issues its loads in
-// batches (its 64 Pi[k][j], then 8 splits' partials at a time) so that the
-// kernel waits on few memory round trips; thread (j, half) covers half of k
-// and the two halves meet in LDS.
+// Merge the split partials of 4 consecutive query rows (of the B*Hkv*R rows):
+// log-sum-exp over splits, / max(l, 1e-8), un-rotate with Pi, store with the
+// GQA mapping (query head h = hkv * G + r / Q).  2*D threads.  Thread
+// (j, half) merges coordinate j of rows half and half + 2; thread (j4, kr)
+// then applies Pi rows [kr*D/8, (kr+1)*D/8) to output columns 4*j4..4*j4+3
+// from float4 loads issued at kernel entry, so the Pi and partial loads
+// share one memory round trip; eight k-range sums meet in LDS.
 template <int D>
 __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_ml,
@@ -758,77 +768,94 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
                                                         int n_splits, int B, int Hkv, int R,
                                                         int Q, int Hq, void* __restrict__ out,
                                                         int out_dtype) {
+  constexpr int JG = D / 4, KPER = D / 8;
   __shared__ float o[kRowsC][D];
-  __shared__ float red[2][kRowsC][D];
+  __shared__ float4 red[8][kRowsC][JG];
   const int tid = threadIdx.x;
-  const int j = tid % D, half = tid / D;
   const int64_t nrows = int64_t(B) * Hkv * R;
   const int64_t row0 = int64_t(blockIdx.x) * kRowsC;
   const int nr = static_cast<int>(min<int64_t>(kRowsC, nrows - row0));
-  float pcol[D / 2];
+
+  const int j4 = tid % JG, kr = tid / JG;
+  float4 pv[KPER];
+  const float4* pk = reinterpret_cast<const float4*>(pi + int64_t(kr) * KPER * D) + j4;
 #pragma unroll
-  for (int k = 0; k < D / 2; ++k) pcol[k] = pi[(half * (D / 2) + k) * D + j];
-  // rows half, half + 2 of this block for coordinate j
+  for (int i = 0; i < KPER; ++i) pv[i] = pk[i * JG];
+
+  const int j = tid % D, half = tid / D;
 #pragma unroll
   for (int rr = 0; rr < kRowsC / 2; ++rr) {
     const int r = half + 2 * rr;
-    if (r >= nr) continue;
-    const int64_t row = row0 + r;
-    float M = -INFINITY, L = 0.f, a = 0.f;  // running log-sum-exp merge
-    for (int s0 = 0; s0 < n_splits; s0 += kSplitBatch) {
-      float mb[kSplitBatch], lb[kSplitBatch], ob[kSplitBatch];
-#pragma unroll
-      for (int x = 0; x < kSplitBatch; ++x) {
-        const int sidx = s0 + x;
-        const bool ok = sidx < n_splits;
-        const int64_t base = (ok ? sidx : 0) * nrows + row;
-        mb[x] = ok ? part_ml[base * 2] : -INFINITY;
-        lb[x] = ok ? part_ml[base * 2 + 1] : 0.f;
-        ob[x] = ok ? part_o[base * D + j] : 0.f;
-      }
-      float bm = M;
-#pragma unroll
-      for (int x = 0; x < kSplitBatch; ++x) bm = fmaxf(bm, mb[x]);
-      if (bm != -INFINITY) {
-        const float c = (M == -INFINITY) ? 0.f : expf(M - bm);
-        L *= c;
-        a *= c;
+    float res = 0.f;
+    if (r < nr) {
+      const int64_t row = row0 + r;
+      float M = -INFINITY, L = 0.f, a = 0.f;  // running log-sum-exp merge
+      for (int s0 = 0; s0 < n_splits; s0 += kSplitBatch) {
+        float mb[kSplitBatch], lb[kSplitBatch], ob[kSplitBatch];
 #pragma unroll
         for (int x = 0; x < kSplitBatch; ++x) {
-          if (mb[x] != -INFINITY) {
-            const float w = expf(mb[x] - bm);
-            L = fmaf(w, lb[x], L);
-            a = fmaf(w, ob[x], a);
-          }
+          const int sidx = s0 + x;
+          const bool ok = sidx < n_splits;
+          const int64_t base = (ok ? sidx : 0) * nrows + row;
+          mb[x] = ok ? part_ml[base * 2] : -INFINITY;
+          lb[x] = ok ? part_ml[base * 2 + 1] : 0.f;
+          ob[x] = ok ? part_o[base * D + j] : 0.f;
         }
-        M = bm;
+        float bm = M;
+#pragma unroll
+        for (int x = 0; x < kSplitBatch; ++x) bm = fmaxf(bm, mb[x]);
+        if (bm != -INFINITY) {
+          const float c = (M == -INFINITY) ? 0.f : expf(M - bm);
+          L *= c;
+          a *= c;
+#pragma unroll
+          for (int x = 0; x < kSplitBatch; ++x) {
+            if (mb[x] != -INFINITY) {
+              const float w = expf(mb[x] - bm);
+              L = fmaf(w, lb[x], L);
+              a = fmaf(w, ob[x], a);
+            }
+          }
+          M = bm;
+        }
       }
+      res = a / fmaxf(L, 1e-8f);
     }
-    o[r][j] = a / fmaxf(L, 1e-8f);
+    o[r][j] = res;
   }
   __syncthreads();
-  float acc[kRowsC];
+  float4 acc[kRowsC];
 #pragma unroll
-  for (int r = 0; r < kRowsC; ++r) acc[r] = 0.f;
+  for (int r = 0; r < kRowsC; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-  for (int k = 0; k < D / 2; ++k)
+  for (int i = 0; i < KPER; ++i) {
 #pragma unroll
-    for (int r = 0; r < kRowsC; ++r) acc[r] = fmaf(o[r][half * (D / 2) + k], pcol[k], acc[r]);
+    for (int r = 0; r < kRowsC; ++r) {
+      const float ov = o[r][kr * KPER + i];
+      acc[r].x = fmaf(ov, pv[i].x, acc[r].x);
+      acc[r].y = fmaf(ov, pv[i].y, acc[r].y);
+      acc[r].z = fmaf(ov, pv[i].z, acc[r].z);
+      acc[r].w = fmaf(ov, pv[i].w, acc[r].w);
+    }
+  }
 #pragma unroll
-  for (int r = 0; r < kRowsC; ++r) red[half][r][j] = acc[r];
+  for (int r = 0; r < kRowsC; ++r) red[kr][r][j4] = acc[r];
   __syncthreads();
-  if (half != 0) return;
   const int G = Hq / Hkv;
+  const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
 #pragma unroll
-  for (int r = 0; r < kRowsC; ++r) {
+  for (int rr = 0; rr < kRowsC / 2; ++rr) {
+    const int r = half + 2 * rr;
     if (r < nr) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v += redf[(k * kRowsC + r) * D + j];
       const int64_t row = row0 + r;  // ((b * Hkv) + hkv) * R + r
       const int rq = static_cast<int>(row % R);
       const int hkv = static_cast<int>((row / R) % Hkv);
       const int b = static_cast<int>(row / (int64_t(R) * Hkv));
       const int g = rq / Q, qi = rq - g * Q;
-      qkv_store(out, ((int64_t(b) * Hq + hkv * G + g) * Q + qi) * D + j,
-                red[0][r][j] + red[1][r][j], out_dtype);
+      qkv_store(out, ((int64_t(b) * Hq + hkv * G + g) * Q + qi) * D + j, v, out_dtype);
     }
   }
 }
@@ -915,19 +942,28 @@ int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, in
   return QKV_OK;
 }
 
-// Resident split_mfma workgroups per CU (queried once; the kernel's LDS and
-// register use set it).
-int mfma_blocks_per_cu() {
-  static int n = 0;
-  if (n == 0) {
+// Dynamic LDS bytes of split_mfma for a split length (scores + value norms).
+int64_t mfma_smem_bytes(int64_t split_len) {
+  const int64_t nt = (split_len + 63) / 64;
+  return nt * kRowsM * 64 * 4 + nt * 64 * 4;
+}
+
+// Resident split_mfma workgroups per CU for a split length (queried per
+// length; the kernel's registers and this LDS size set it).
+int mfma_blocks_per_cu(int64_t split_len) {
+  static int cache[kSplitMax / 64 + 1] = {0};
+  const int nt = static_cast<int>((split_len + 63) / 64);
+  if (nt < 1 || nt > kSplitMax / 64) return 1;
+  if (cache[nt] == 0) {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<128, 2, 3>, 256, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &v, split_mfma<128, 2, 3>, 256, static_cast<size_t>(mfma_smem_bytes(nt * 64))) !=
             hipSuccess ||
         v <= 0)
       v = 2;
-    n = v;
+    cache[nt] = v;
   }
-  return n;
+  return cache[nt];
 }
 
 }  // namespace
@@ -940,27 +976,28 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
   const int R = (Hq / Hkv) * Q;
   const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM);
-  const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu();
   const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
   const int64_t max_s = std::min<int64_t>((T + 63) / 64, 1024);
-  int64_t s = std::max<int64_t>(min_s, (slots + groups - 1) / groups);
-  if (s > max_s) s = max_s;
-  // prefer a count that fills whole rounds of resident workgroups (no short
-  // last round), searching a little above the minimum
-  int64_t best = s;
-  double best_eff = 0.0;
-  for (int64_t c = s; c <= std::min<int64_t>(max_s, 4 * s); ++c) {
+  // Model: time ~ rounds x split length, rounds = ceil(workgroups / resident
+  // slots), slots from the occupancy at that split length.  Shorter splits
+  // raise occupancy (less LDS) but add per-split work; prefer >= 512 tokens.
+  int64_t best = std::max<int64_t>(min_s, 1);
+  double best_cost = 1e300;
+  for (int64_t c = std::max<int64_t>(min_s, 1); c <= max_s; ++c) {
+    const int64_t len = mfma_split_len(T, static_cast<int>(c));
+    if (len < 512 && c > min_s && c * 512 >= T) break;
+    const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu(len);
     const int64_t wg = groups * c;
     const int64_t rounds = (wg + slots - 1) / slots;
-    const double eff = static_cast<double>(wg) / static_cast<double>(rounds * slots);
-    if (eff > best_eff + 1e-9) {
-      best_eff = eff;
+    const double cost = static_cast<double>(rounds) * static_cast<double>(len + 256) /
+                        std::sqrt(static_cast<double>(std::min<int64_t>(slots / qkv_num_cus(), 4)));
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
       best = c;
     }
-    if (eff > 0.999) break;
+    if (c > 64 * std::max<int64_t>(min_s, 1)) break;
   }
-  if (best < 1) best = 1;
-  return static_cast<int32_t>(best);
+  return static_cast<int32_t>(std::max<int64_t>(best, 1));
 }
 
 extern "C" int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
@@ -989,6 +1026,7 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   QKV_REQUIRE(q && pi && signs && kcent_host && vcent_host, "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
   const int R = (Hq / Hkv) * Q;
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
@@ -1023,14 +1061,14 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   return QKV_OK;
 }
 
-extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
-                                     const uint32_t* vstore, const float* vnorm,
-                                     int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
-                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
-                                     int32_t vbits, const float* kcent_host,
-                                     const float* vcent_host, float scale, int32_t causal,
-                                     void* workspace, int64_t ws_bytes, int32_t n_splits,
-                                     void* stream) {
+extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
+                                 const uint32_t* vstore, const float* vnorm, int64_t t_stride,
+                                 int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                                 int32_t d, int32_t kbits, int32_t vbits, const float* pi,
+                                 const float* kcent_host, const float* vcent_host, float scale,
+                                 int32_t causal, void* out, int32_t out_dtype, void* workspace,
+                                 int64_t ws_bytes, int32_t n_splits, void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
   QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
   QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
@@ -1038,7 +1076,9 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
               (long long)T);
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(kstore && knorm && vstore && vnorm && kcent_host && vcent_host, "null pointer");
+  QKV_REQUIRE(kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host && out,
+              "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
   QKV_REQUIRE(qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4), "store must be 4-byte aligned");
   const int R = (Hq / Hkv) * Q;
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
@@ -1046,6 +1086,7 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
   float* po = at<float>(workspace, L.po);
   float* pml = at<float>(workspace, L.pml);
   auto s = static_cast<hipStream_t>(stream);
+  const dim3 cgrid(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC));
   if (use_mfma(tb, d, t_stride, T, n_splits)) {
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const int64_t split_len = mfma_split_len(T, n_splits);
@@ -1053,7 +1094,8 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
     const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
     const float* rowc = at<float>(workspace, L.rowc);
 #define QKV_MF(MB, VB)                                                                       \
-  hipLaunchKernelGGL((split_mfma<128, MB, VB>), grid, dim3(256), 0, s, aq, rowc, kstore,    \
+  hipLaunchKernelGGL((split_mfma<128, MB, VB>), grid, dim3(256),                           \
+                     static_cast<uint32_t>(mfma_smem_bytes(split_len)), s, aq, rowc, kstore,  \
                      knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, scale, causal,    \
                      split_len, tb, po, pml)
     switch (kbits * 10 + vbits) {
@@ -1067,6 +1109,8 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
       case 24: QKV_MF(2, 4); break;
     }
 #undef QKV_MF
+    hipLaunchKernelGGL(combine_kernel<128>, cgrid, dim3(256), 0, s, po, pml, pi, n_splits, B,
+                       Hkv, R, Q, Hq, out, out_dtype);
     QKV_LAUNCHED();
     return QKV_OK;
   }
@@ -1079,35 +1123,8 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
     hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
                        qw, kstore, knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, kbits, \
                        vbits, tb, scale, causal, split_len, po, pml);                          \
-    break;
-    QKV_CASE(64)
-    QKV_CASE(96)
-    QKV_CASE(128)
-#undef QKV_CASE
-  }
-  QKV_LAUNCHED();
-  return QKV_OK;
-}
-
-extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-                                     const float* pi, void* out, int32_t out_dtype,
-                                     void* workspace, int64_t ws_bytes, int32_t n_splits,
-                                     void* stream) {
-  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
-  if (st != QKV_OK) return st;
-  QKV_REQUIRE(pi && out, "null pointer");
-  const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
-  auto s = static_cast<hipStream_t>(stream);
-  switch (d) {
-#define QKV_CASE(DD)                                                                         \
-  case DD:                                                                                   \
-    hipLaunchKernelGGL(combine_kernel<DD>,                                                   \
-                       dim3(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC)), \
-                       dim3(2 * DD), 0, s, at<float>(workspace, L.po),                       \
-                       at<float>(workspace, L.pml), pi, n_splits, B, Hkv, R, Q, Hq, out,     \
-                       out_dtype);                                                           \
+    hipLaunchKernelGGL(combine_kernel<DD>, cgrid, dim3(2 * DD), 0, s, po, pml, pi, n_splits,   \
+                       B, Hkv, R, Q, Hq, out, out_dtype);                                      \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -1142,10 +1159,7 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
                              vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
   if (st != QKV_OK) return st;
-  st = qkv_attention_partial(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
-                             vbits, kcent_host, vcent_host, scale, causal, workspace, ws_bytes,
-                             n_splits, stream);
-  if (st != QKV_OK) return st;
-  return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
-                               n_splits, stream);
+  return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
+                           vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
+                           workspace, ws_bytes, n_splits, stream);
 }
