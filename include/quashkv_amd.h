@@ -179,6 +179,32 @@ int qkv_vtiles_pack(const uint8_t* codes, int64_t groups, int64_t S, int32_t d,
                     int32_t vbits, uint32_t* dst, int64_t tiles_per_group, int64_t t0,
                     void* stream);
 
+/* Fused compress of new K and V rows straight into the store: normalise ->
+ * rotate (MFMA, Pi split into two 16-bit parts) -> Lloyd-Max boundary search
+ * -> QJL sign -> K-row / V-tile bit planes and norms.
+ * Replaces the compress half of QuashKVEngine.append (quashkv/engine.py:
+ * 145-172: InnerProductQuantizer.compress for keys, quashkv/quantizer.py:
+ * 211-242, MSEQuantizer.compress for values, quashkv/quantizer.py:113-131).
+ *   in_dtype   QKV_BF16 or QKV_F16 (others: QKV_E_UNSUPPORTED)
+ *   keys, values  groups x S x 128 rows, 16-byte aligned; either may be NULL
+ *              to append only the other
+ *   mbits      key MSE bits (1..3; key total bits - 1), vbits value bits (1..4)
+ *   kcent_host, kbound_host  HOST arrays of the key MSE codebook (2^mbits
+ *              centroids, 2^mbits - 1 boundaries; must be symmetric);
+ *   vbound_host  HOST array of the 2^vbits - 1 value boundaries
+ *   kstore/knorm/vstore/vnorm  the store of groups x t_stride tokens; tokens
+ *              [t0, t0 + S) of every group are written, all others kept
+ * Codes equal the reference's except where the rotated value lies within
+ * ~1e-5 relative of a boundary (the rotation carries ~16 significant bits of
+ * Pi for bf16 inputs, ~22 for fp16). */
+int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
+                     int64_t groups, int64_t S, int32_t d, int32_t mbits,
+                     int32_t vbits, const float* pi, const float* signs,
+                     const float* kcent_host, const float* kbound_host,
+                     const float* vbound_host, uint8_t* kstore, float* knorm,
+                     uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
+                     void* stream);
+
 /* Inverse of qkv_vtiles_pack: tokens [t0, t0 + S) -> groups x S x d uint8. */
 int qkv_vtiles_unpack(const uint32_t* src, int64_t groups, int64_t S, int32_t d,
                       int32_t vbits, int64_t tiles_per_group, int64_t t0, uint8_t* codes,

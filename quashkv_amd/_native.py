@@ -48,6 +48,8 @@ _SIGS = {
     "qkv_kplanes_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p, _p]),
     "qkv_vtiles_pack": (_i32, [_p, _i64, _i64, _i32, _i32, _p, _i64, _i64, _p]),
     "qkv_vtiles_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p]),
+    "qkv_store_append": (_i32, [_i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p,
+                                _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_attention_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64]),
     "qkv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "qkv_attention_path": (_i32, [_i32, _i32, _i32, _p, _p, _i64, _i64, _i32]),

@@ -186,6 +186,7 @@ class LloydMaxCodebook:
         # fp32 values as Python floats: the attention entry points take the
         # centroids by value (no device round trip)
         self.centroids_host = tuple(self.centroids.tolist())
+        self.boundaries_host = tuple(self.boundaries.tolist())
 
     def _tables_on(self, device: torch.device):
         if self.centroids.device != device:

@@ -73,6 +73,7 @@ class QuashKVEngine:
         self._blocks: list[tuple[int, int]] = []   # (start, seq_len) per append
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
+        self._host_tables = None   # codebook tables passed by value to qkv_store_append
 
     # ---------------------------------------------------------- compression
 
@@ -105,7 +106,7 @@ class QuashKVEngine:
                                        max(self.initial_capacity, S), dev)
         t0 = self._total_tokens
         st.ensure(t0 + S, t0)
-        if S > 0:
+        if S > 0 and not self._append_fused(keys, values, t0):
             kq, vq = self.key_quantizer, self.value_quantizer
             mq = kq.mse_quantizer
             n = B * H * S
@@ -125,6 +126,38 @@ class QuashKVEngine:
             st.write_codes(t0, S, kc, kb, vc)
         self._blocks.append((t0, S))
         self._total_tokens += S
+
+    def _append_fused(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
+        """bf16 / fp16 rows at head_dim 128: compress straight into the store
+        (qkv_store_append).  False when that kernel does not cover the call."""
+        if (keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype
+                or self.head_dim != 128 or not 2 <= self.key_bits <= 4):
+            return False
+        B, H, S, d = keys.shape
+        kq, vq = self.key_quantizer, self.value_quantizer
+        mq = kq.mse_quantizer
+        if self._host_tables is None:
+            self._host_tables = (N.HostFloats(mq.codebook.centroids_host),
+                                 N.HostFloats(mq.codebook.boundaries_host),
+                                 N.HostFloats(vq.codebook.boundaries_host))
+        kc, kb, vb = self._host_tables
+        st = self._store
+        k, v = keys.contiguous(), values.contiguous()
+        dt = N.dtype_code(k.dtype)
+        stream = N.stream(k.device)
+        L = N.lib()
+        status = L.qkv_store_append(dt, k.data_ptr(), None, B * H, S, d, kq.mse_bits, vq.bits,
+                                    mq.Pi.data_ptr(), kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr,
+                                    st.kst.data_ptr(), st.knorm.data_ptr(), st.vst.data_ptr(),
+                                    st.vnorm.data_ptr(), st.capacity, t0, stream)
+        if status == N.QKV_E_UNSUPPORTED:
+            return False
+        N.check(status)
+        N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, d, kq.mse_bits, vq.bits,
+                                   vq.Pi.data_ptr(), None, None, None, vb.ptr,
+                                   None, None, st.vst.data_ptr(), st.vnorm.data_ptr(),
+                                   st.capacity, t0, stream))
+        return True
 
     @property
     def _cache(self) -> list[CompressedKVBlock]:

@@ -70,6 +70,25 @@ def test_abi_rejects_before_launch():
     assert "exceed" in lib.qkv_last_error().decode()
 
 
+def test_store_append_validation():
+    lib = N.lib()
+    # fp32 rows and head_dim != 128 are not covered by the fused kernel
+    assert lib.qkv_store_append(N.QKV_F32, 16, None, 1, 1, 128, 2, 3, 16, 16, 16, 16, 16, 16,
+                                16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 64, 2, 3, 16, 16, 16, 16, 16, 16,
+                                16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
+    # capacity must hold the appended tokens
+    st = lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 10, 128, 2, 3, 16, 16, 16, 16, 16, 16,
+                              16, 16, 16, 64, 60, None)
+    assert st == N.QKV_E_INVALID and "capacity" in lib.qkv_last_error().decode()
+    # an asymmetric key codebook is refused (the sign folding needs symmetry)
+    kc = N.HostFloats([-1.0, -0.4, 0.5, 1.0])
+    kb = N.HostFloats([-0.7, 0.05, 0.75])
+    st = lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 128, 2, 3, 16, 16, kc.ptr, kb.ptr,
+                              16, 16, 16, 16, 16, 64, 0, None)
+    assert st == N.QKV_E_UNSUPPORTED and "symmetric" in lib.qkv_last_error().decode()
+
+
 def test_check_maps_status_to_exceptions():
     N.lib().qkv_pack_bits(None, None, 4, 128, 9, None)
     with pytest.raises(ValueError, match="Unsupported bits"):
