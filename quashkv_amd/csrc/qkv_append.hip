@@ -18,28 +18,31 @@
 // boundary (about 1e-6 of the coordinates); codes from an identical y go
 // through qkv_compress(QKV_FLAG_PRE_ROTATED), which is exact.
 //
-// Boundary search without per-element codes.  For the value y of one
-// coordinate, code = #{i : t_i < y} (torch.bucketize, right=False).  Bit k of
-// that count is the XOR of the comparisons [y > t_i] over i = 2^k - 1,
-// 2^k - 1 + 2^k, ..., so a wave compares its 64 values with every boundary
-// (one v_cmp each, giving a 64-bit lane mask) and forms the bit planes with
-// scalar XORs of the masks.  Keys interleave centroids and boundaries,
-// c_0 < t_0 < c_1 < ... < c_{2^m-1}: the QJL bit [(y - c[code]) S_j >= 0] is
-// the parity of #{f : f < y S_j} over that fine list (y S_j lies in
-// (c_code', t_code'] exactly when the count is odd), using the codebook's
-// symmetry (c_i = -c_{2^m-1-i}, t_i = -t_{2^m-2-i}) to fold the sign S_j into
-// y: with y' = y S_j, code(y) = code'(y') for S_j = +1 and its complement for
-// S_j = -1.  Pi is staged with its rows scaled by S, so the MFMA yields y S
-// directly.  Exact ties (y equal to a boundary or centroid) are a measure-zero
-// event on this path and resolve as [y' > f].
+// Boundary search as lane masks.  For the value y of one coordinate,
+// code = #{i : t_i < y} (torch.bucketize, right=False).  A binary search over
+// the sorted thresholds decides one code bit per level with one compare,
+// [y > threshold], whose 64-lane result mask is directly that bit plane for
+// the wave's 64 values; the next level's threshold is picked per lane with
+// v_cndmask on the masks already found (levels of 1, 2, 4, ... candidates).
+// Keys search the fine list c_0 < t_0 < c_1 < ... < c_{2^m-1} (centroids and
+// boundaries interleaved): its count f gives code = f >> 1 and the QJL bit
+// [(y - c[code]) S_j >= 0] = f & 1 (y lies in (c_code, t_code] exactly when f
+// is odd).  The sign S_j is folded in through the codebook's symmetry
+// (c_i = -c_{2^m-1-i}, t_i = -t_{2^m-2-i}): with y' = y S_j the search runs on
+// y', the QJL bit is unchanged and the code is complemented where S_j = -1.
+// Pi is staged with its rows scaled by S, so the MFMA yields y S directly.
+// Exact ties (y equal to a boundary or centroid) are a measure-zero event on
+// this path and resolve as [y' > f].
 //
-// Orientation.  Keys: C = tokens x coordinates, so a mask's 16-lane groups are
-// 16 coordinates of one token -- two bytes of one K-row plane.  Values:
-// C = coordinates x tokens, so a mask's 16-lane groups are 16 tokens of one
-// coordinate -- half a V-tile word.  The MFMA operand layouts of the 16x16x32
-// instructions are symmetric, so the same x and Pi register fragments serve
-// both orders.  Plane words are assembled in SGPRs and placed into staging
-// VGPRs with v_writelane, then stored with coalesced vector stores.
+// Orientation.  32x32x16 MFMAs: a result VGPR holds one C row per 32-lane
+// half, 32 consecutive columns, so each half of a compare mask is one whole
+// 32-bit store word.  Keys: C = tokens x coordinates, a mask half is the
+// plane word of 32 coordinates of one token (one dword of a K row).  Values:
+// C = coordinates x tokens, a mask half is the plane word of one coordinate
+// over 32 tokens (one V-tile word).  The A and B operand layouts are
+// symmetric, so the same x and Pi register fragments serve both orders.
+// Mask words are placed into staging VGPRs with v_writelane and stored with
+// coalesced vector stores.
 
 #include <cmath>
 #include <type_traits>
@@ -51,52 +54,51 @@ namespace {
 
 typedef __bf16 qkv_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 qkv_f16x8 __attribute__((ext_vector_type(8)));
-typedef float qkv_f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;                 // head dim of this path
 constexpr int kTok = 64;                // tokens per wave tile
 constexpr int kWaves = 4;               // waves per workgroup
-constexpr int kFragN = 8 * 4 * 2 * 64;  // Pi fragments [block][k-step][split][lane] (64 KiB)
+constexpr int kFragN = 4 * 8 * 2 * 64;  // Pi fragments [block][k-step][split][lane] (64 KiB)
 constexpr float kPScaleF16 = 256.f;     // keeps the fp16 low part of Pi out of subnormals
 
 struct Thresh {
   float v[15];  // ascending comparison list
 };
 
+typedef float qkv_f32x16 __attribute__((ext_vector_type(16)));
+
 template <bool F16>
-__device__ __forceinline__ qkv_f32x4 mma(uint4 a, uint4 b, qkv_f32x4 c) {
+__device__ __forceinline__ qkv_f32x16 mma(uint4 a, uint4 b, qkv_f32x16 c) {
   if constexpr (F16)
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(qkv_f16x8, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qkv_f16x8, a),
                                                   __builtin_bit_cast(qkv_f16x8, b), c, 0, 0, 0);
   else
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(qkv_bf16x8, a),
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(qkv_bf16x8, a),
                                                    __builtin_bit_cast(qkv_bf16x8, b), c, 0, 0, 0);
 }
+
+// v_writelane through the LLVM intrinsic (no clang builtin spells it), so the
+// compiler sees the SGPR read and pads the VALU-writes-SGPR hazard before it.
+extern "C" __device__ int qkv_llvm_writelane(int val, int lane, int old) __asm(
+    "llvm.amdgcn.writelane.i32");
 
 // Value `val` (wave-uniform) into lane L of `old`.
 template <int L>
 __device__ __forceinline__ uint32_t put_lane(uint32_t old, uint32_t val) {
   static_assert(L >= 0 && L < 64, "lane");
-  uint32_t r;
-  asm("v_writelane_b32 %0, %1, %2" : "=v"(r) : "s"(val), "i"(L), "0"(old));
+  return static_cast<uint32_t>(
+      qkv_llvm_writelane(static_cast<int>(val), L, static_cast<int>(old)));
+}
+
+// A wave-uniform value held in a VGPR (a v_cndmask may then take two of them
+// with its mask without exceeding the one-scalar-operand limit).
+__device__ __forceinline__ float in_vgpr(float x) {
+  float r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
   return r;
 }
 
 __device__ __forceinline__ uint64_t lanes_where(bool p) { return __builtin_amdgcn_ballot_w64(p); }
-
-// 16-bit chunk G (lanes 16 G .. 16 G + 15) of mask a, with that of mask b in
-// the high half: one scalar pack (s_pack_{ll,hh}_b32_b16) on wave-uniform masks.
-template <int G>
-__device__ __forceinline__ uint32_t chunk_pair(uint64_t a, uint64_t b) {
-  const uint32_t x = static_cast<uint32_t>(a >> (32 * (G >> 1)));
-  const uint32_t y = static_cast<uint32_t>(b >> (32 * (G >> 1)));
-  uint32_t r;
-  if constexpr ((G & 1) == 0)
-    asm("s_pack_ll_b32_b16 %0, %1, %2" : "=s"(r) : "s"(x), "s"(y));
-  else
-    asm("s_pack_hh_b32_b16 %0, %1, %2" : "=s"(r) : "s"(x), "s"(y));
-  return r;
-}
 
 // f(std::integral_constant<int, 0>), ..., f(<N - 1>): compile-time unrolled
 // loops whose index feeds template arguments (v_writelane lane numbers).
@@ -107,6 +109,28 @@ __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int
 template <int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Binary search of y in the ascending list t[0 .. 2^L - 2]: bit i of
+// #{j : t[j] < y} as the lane mask m[i].
+template <int L>
+__device__ __forceinline__ void search(float y, const float* t, uint64_t (&m)[L]) {
+  bool c[L];
+  static_for<L>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;  // level k decides bit L - 1 - k
+    float cand[1 << k];
+#pragma unroll
+    for (int p = 0; p < (1 << k); ++p) cand[p] = t[(2 * p + 1) * (1 << (L - 1 - k)) - 1];
+    // prefix bit j (LSB first) is c[L - k + j]
+#pragma unroll
+    for (int j = 0; j < k; ++j)
+#pragma unroll
+      for (int q = 0; q < (1 << (k - 1 - j)); ++q)
+        cand[q] = c[L - k + j] ? cand[2 * q + 1] : cand[2 * q];
+    c[L - 1 - k] = y > cand[0];
+  });
+#pragma unroll
+  for (int i = 0; i < L; ++i) m[i] = lanes_where(c[i]);
 }
 
 template <bool F16>
@@ -153,16 +177,16 @@ __device__ __forceinline__ float from16(uint16_t h) {
     return qkv_bf16_to_f32(h);
 }
 
-// Stage the rotation operand in LDS.  Entry ((b * 4 + s) * 2 + split) * 64 + l
-// holds, for lane l, Pi'[16 b + (l & 15)][32 s + 8 (l >> 4) + e], e = 0..7, as
+// Stage the rotation operand in LDS.  Entry ((b * 8 + s) * 2 + split) * 64 + l
+// holds, for lane l, Pi'[32 b + (l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
 // eight 16-bit values: the high part (split 0) or the low part (split 1) of
 // Pi' = diag(rowsign) Pi * pscale (rowsign = S for keys, none for values).
 template <bool F16>
 __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
                          const float* __restrict__ rowsign, float pscale) {
   for (int e = threadIdx.x; e < kFragN; e += blockDim.x) {
-    const int ln = e & 63, split = (e >> 6) & 1, s = (e >> 7) & 3, b = e >> 9;
-    const int j = 16 * b + (ln & 15), k0 = 32 * s + 8 * (ln >> 4);
+    const int ln = e & 63, split = (e >> 6) & 1, s = (e >> 7) & 7, b = e >> 10;
+    const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
     const float4 p0 = *reinterpret_cast<const float4*>(pi + j * kD + k0);
     const float4 p1 = *reinterpret_cast<const float4*>(pi + j * kD + k0 + 4);
     const float sc = (rowsign ? rowsign[j] : 1.f) * pscale;  // +-2^k: exact
@@ -179,13 +203,17 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
   }
 }
 
-// Bit k of the thermometer count of masks m[0..n): XOR of m[i], i = 2^k - 1 (step 2^k).
-template <int K, int N>
-__device__ __forceinline__ uint64_t count_bit(const uint64_t* m) {
-  uint64_t a = 0;
+// x fragments of 64 tokens: xf[tt][s], lane l = (row l & 31, half l >> 5) holds
+// x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt] (this
+// lane's token row of tile half tt; callers point lanes without a token at a
+// valid row, whose results are never stored).
+__device__ __forceinline__ void load_x(uint4 (&xf)[2][8], const uint16_t* const (&row)[2],
+                                       int lane) {
 #pragma unroll
-  for (int i = (1 << K) - 1; i < N; i += (1 << K)) a ^= m[i];
-  return a;
+  for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      xf[tt][s] = *reinterpret_cast<const uint4*>(row[tt] + 16 * s + 8 * (lane >> 5));
 }
 
 // ------------------------------------------------------------------ keys
@@ -198,109 +226,91 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, const float* __restrict__ signs, Thresh fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
-  constexpr int NF = (2 << MB) - 1;  // c_0, t_0, c_1, ..., c_{2^MB - 1}
-  constexpr int NT = (1 << MB) - 1;  // boundaries
-  constexpr int NP = MB + 1;         // planes per row
-  constexpr int RD = 4 * NP;         // dwords per row = staging dwords per lane
+  constexpr int L = MB + 1;           // search levels over the fine list
+  constexpr int NF = (1 << L) - 1;    // c_0, t_0, c_1, ..., c_{2^MB - 1}
+  constexpr int RD = 4 * L;           // dwords per row = staging dwords per lane
   __shared__ uint4 frag[kFragN];
+  __shared__ float4 inv_s[kWaves][kTok / 4];  // 1 / norm of the wave's 64 tokens
   stage_pi<F16>(frag, pi, signs, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
-  uint32_t sneg = 0;  // bit b: S < 0 at this lane's coordinate of block b
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  float fv[NF];
 #pragma unroll
-  for (int b = 0; b < 8; ++b) sneg |= (signs[16 * b + li] < 0.f ? 1u : 0u) << b;
+  for (int i = 0; i < NF; ++i) fv[i] = in_vgpr(fine.v[i]);
+  uint64_t sneg[4];  // lanes whose coordinate 32 n + (l & 31) has S < 0
+#pragma unroll
+  for (int n = 0; n < 4; ++n) sneg[n] = lanes_where(signs[32 * n + li] < 0.f);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
-  for (int64_t tile = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6); tile < ntiles;
-       tile += int64_t(gridDim.x) * kWaves) {
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
-    const uint16_t* xt = x + (grp * S + s0) * kD;
+    uint4 xf[2][8];  // tokens past S read the last row; their results are not stored
+    {
+      const uint16_t* const row[2] = {x + (grp * S + s0 + min(li, nv - 1)) * kD,
+                                      x + (grp * S + s0 + min(32 + li, nv - 1)) * kD};
+      load_x(xf, row, lane);
+    }
 
-    // A operand: lane (li, g) holds x[16 mt + li][32 s + 8 g .. + 7]
-    uint4 xf[4][4];
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        xf[mt][s] = (16 * mt + li < nv)
-                        ? *reinterpret_cast<const uint4*>(xt + (16 * mt + li) * kD + 32 * s + 8 * g)
-                        : make_uint4(0u, 0u, 0u, 0u);
-
-    // norms; inv[mt][v] = 1 / n of token 16 mt + 4 g + v (the C-row of VGPR v)
-    float inv[4][4];
+    // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
+    // 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four consecutive tokens)
     float* nrow = knorm + grp * t_stride + t0 + s0;
+    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+    for (int tt = 0; tt < 2; ++tt) {
       float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ss = sumsq<F16>(xf[mt][s], ss);
-      ss += __shfl_xor(ss, 16, 64);
+      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (g == 0 && 16 * mt + li < nv) nrow[16 * mt + li] = nrm;
-      const float iv = iscale / nrm;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) inv[mt][v] = __shfl(iv, 4 * g + v, 64);
+      if (lane < 32) {
+        if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
+        invw[32 * tt + li] = iscale / nrm;
+      }
     }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
 
     uint32_t stg[RD];
 #pragma unroll
     for (int i = 0; i < RD; ++i) stg[i] = 0u;
 
-    static_for<4>([&](auto wc) {  // coordinates 32 w .. 32 w + 31 (blocks 2w, 2w+1)
-      constexpr int w = decltype(wc)::value;
-      qkv_f32x4 acc[2][4];
+    static_for<4>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
+      constexpr int n = decltype(nc)::value;
+      // one coordinate block at a time: keeps the scheduler from overlapping
+      // blocks (and their accumulators and fragments) beyond the register file
+      __builtin_amdgcn_sched_barrier(0);
+      qkv_f32x16 acc[2] = {};
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int s = 0; s < 8; ++s)
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) acc[h][mt] = qkv_f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < 2; ++sp) {
+          const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+          for (int tt = 0; tt < 2; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+        }
+      static_for<2>([&](auto tc) {
+        constexpr int tt = decltype(tc)::value;
+        float4 iv4[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-#pragma unroll
-          for (int sp = 0; sp < 2; ++sp) {
-            const uint4 bf = frag[(((2 * w + h) * 4 + s) * 2 + sp) * 64 + lane];
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt) acc[h][mt] = mma<F16>(xf[mt][s], bf, acc[h][mt]);
-          }
-      const uint64_t sn[2] = {lanes_where((sneg >> (2 * w)) & 1u),
-                              lanes_where((sneg >> (2 * w + 1)) & 1u)};
-      static_for<4>([&](auto mtc) {
-        constexpr int mt = decltype(mtc)::value;
-        static_for<4>([&](auto vc) {
+        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+        static_for<16>([&](auto vc) {
           constexpr int v = decltype(vc)::value;
-          uint64_t pl[2][NP];
-#pragma unroll
-          for (int h = 0; h < 2; ++h) {
-            const float ys = acc[h][mt][v] * inv[mt][v];  // y_j S_j
-            uint64_t f[NF];
-#pragma unroll
-            for (int i = 0; i < NF; ++i) f[i] = lanes_where(ys > fine.v[i]);
-            uint64_t m[NT];
-#pragma unroll
-            for (int i = 0; i < NT; ++i) m[i] = f[2 * i + 1];
-            uint64_t q = 0;
-#pragma unroll
-            for (int i = 0; i < NF; ++i) q ^= f[i];
-            static_for<MB>([&](auto kc) {
-              pl[h][decltype(kc)::value] = count_bit<decltype(kc)::value, NT>(m) ^ sn[h];
-            });
-            pl[h][MB] = q;
-          }
-          // token 16 mt + 4 g2 + v: bits [16 g2, 16 g2 + 16) of each mask; the
-          // two 16-coordinate blocks of the pair fill one dword of plane r
-          static_for<4>([&](auto g2c) {
-            constexpr int g2 = decltype(g2c)::value;
-            static_for<NP>([&](auto rc) {
-              constexpr int r = decltype(rc)::value;
-              constexpr int D = (16 * mt + 4 * g2 + v) * RD + 4 * r + w;
-              const uint32_t dw = chunk_pair<g2>(pl[0][r], pl[1][r]);
-              stg[D >> 6] = put_lane<(D & 63)>(stg[D >> 6], dw);
-            });
+          const float4 q4 = iv4[v >> 2];
+          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+          uint64_t f[L];
+          search<L>(acc[tt][v] * iv, fv, f);  // on y_j S_j
+          // token ta (lanes 0..31) and ta + 4 (lanes 32..63)
+          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);
+          static_for<L>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;  // plane r: MSE bit r, r = MB: QJL
+            const uint64_t w = r < MB ? (f[r + 1 < L ? r + 1 : 0] ^ sneg[n]) : f[0];
+            constexpr int D0 = ta * RD + 4 * r + n, D1 = (ta + 4) * RD + 4 * r + n;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w >> 32));
           });
         });
       });
@@ -331,85 +341,73 @@ __global__ __launch_bounds__(256, 2) void append_v_mfma(
   stage_pi<F16>(frag, pi, nullptr, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
-  const int lane = threadIdx.x & 63, g = lane >> 4, li = lane & 15;
+  const int lane = threadIdx.x & 63, li = lane & 31;
+  float bv[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) bv[i] = in_vgpr(bnd.v[i]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t a_base = t0 & ~int64_t(31);
   const int64_t tiles_per_group = t_stride / 32;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
   for (int64_t tile = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6); tile < ntiles;
-       tile += int64_t(gridDim.x) * kWaves) {
+       tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
-    const uint16_t* xg = x + grp * S * kD;
-
-    // B operand: lane (li, g) holds x[token 16 n + li][32 s + 8 g .. + 7]
-    uint4 xf[4][4];
-    bool ok[4];
+    bool ok[2];
+    uint4 xf[2][8];  // tokens outside [t0, t0 + S) read a valid row; their bits are not stored
+    {
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const int64_t si = d0 + 16 * n + li;
-      ok[n] = si >= 0 && si < S;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        xf[n][s] = ok[n] ? *reinterpret_cast<const uint4*>(xg + si * kD + 32 * s + 8 * g)
-                         : make_uint4(0u, 0u, 0u, 0u);
+      for (int tt = 0; tt < 2; ++tt) ok[tt] = d0 + 32 * tt + li >= 0 && d0 + 32 * tt + li < S;
+      const uint16_t* const row[2] = {
+          x + (grp * S + min<int64_t>(max<int64_t>(d0 + li, 0), S - 1)) * kD,
+          x + (grp * S + min<int64_t>(max<int64_t>(d0 + 32 + li, 0), S - 1)) * kD};
+      load_x(xf, row, lane);
     }
-    float inv[4];  // token 16 n + li: the C-column of this lane
+
+    float inv[2];  // token 32 tt + (l & 31): the C-column of this lane
     float* nrow = vnorm + grp * t_stride + A0;
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
+    for (int tt = 0; tt < 2; ++tt) {
       float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ss = sumsq<F16>(xf[n][s], ss);
-      ss += __shfl_xor(ss, 16, 64);
+      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (g == 0 && ok[n]) nrow[16 * n + li] = nrm;
-      inv[n] = iscale / nrm;
+      if (lane < 32 && ok[tt]) nrow[32 * tt + li] = nrm;
+      inv[tt] = iscale / nrm;
     }
 
     uint32_t stg[NS];
 #pragma unroll
     for (int i = 0; i < NS; ++i) stg[i] = 0u;
 
-    static_for<8>([&](auto mbc) {  // coordinates 16 mb .. 16 mb + 15
-      constexpr int mb = decltype(mbc)::value;
-      qkv_f32x4 acc[4];
+    static_for<4>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
+      constexpr int mb = decltype(mc)::value;
+      __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
+      qkv_f32x16 acc[2] = {};
 #pragma unroll
-      for (int n = 0; n < 4; ++n) acc[n] = qkv_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < 8; ++s)
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
-          const uint4 af = frag[((mb * 4 + s) * 2 + sp) * 64 + lane];
+          const uint4 af = frag[((mb * 8 + s) * 2 + sp) * 64 + lane];
 #pragma unroll
-          for (int n = 0; n < 4; ++n) acc[n] = mma<F16>(af, xf[n][s], acc[n]);
+          for (int tt = 0; tt < 2; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
         }
-      static_for<4>([&](auto vc) {
-        constexpr int v = decltype(vc)::value;
-        uint64_t pl[4][VB];
-#pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const float ys = acc[n][v] * inv[n];
-          uint64_t m[NB];
-#pragma unroll
-          for (int i = 0; i < NB; ++i) m[i] = lanes_where(ys > bnd.v[i]);
+      static_for<2>([&](auto tc) {  // V tile tt of the wave tile
+        constexpr int tt = decltype(tc)::value;
+        static_for<16>([&](auto vc) {
+          constexpr int v = decltype(vc)::value;
+          uint64_t m[VB];
+          search<VB>(acc[tt][v] * inv[tt], bv, m);
+          // coordinate ca (lanes 0..31) and ca + 4 (lanes 32..63), tokens 32 tt + 0..31
+          constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
           static_for<VB>([&](auto kc) {
-            pl[n][decltype(kc)::value] = count_bit<decltype(kc)::value, NB>(m);
-          });
-        }
-        // coordinate 16 mb + 4 g2 + v of tile tau: tokens 32 tau + 0..15 | 16..31
-        static_for<2>([&](auto tc) {
-          constexpr int tau = decltype(tc)::value;
-          static_for<4>([&](auto g2c) {
-            constexpr int g2 = decltype(g2c)::value;
-            static_for<VB>([&](auto kc) {
-              constexpr int k = decltype(kc)::value;
-              constexpr int D = (tau * VB + k) * 128 + 16 * mb + 4 * g2 + v;
-              const uint32_t dw = chunk_pair<g2>(pl[2 * tau][k], pl[2 * tau + 1][k]);
-              stg[D >> 6] = put_lane<(D & 63)>(stg[D >> 6], dw);
-            });
+            constexpr int k = decltype(kc)::value;
+            constexpr int D0 = (tt * VB + k) * kD + ca, D1 = D0 + 4;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(m[k]));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(m[k] >> 32));
           });
         });
       });
