@@ -24,6 +24,9 @@
 // [y > threshold], whose 64-lane result mask is directly that bit plane for
 // the wave's 64 values; the next level's threshold is picked per lane with
 // v_cndmask on the masks already found (levels of 1, 2, 4, ... candidates).
+// Lloyd-Max lists are symmetric about 0, so the top bit is [y > 0] and the
+// rest is a search of |y| in the positive half (the compare's abs modifier),
+// complemented for y <= 0: 4 VALU operations per 64 values for 3-bit codes.
 // Keys search the fine list c_0 < t_0 < c_1 < ... < c_{2^m-1} (centroids and
 // boundaries interleaved): its count f gives code = f >> 1 and the QJL bit
 // [(y - c[code]) S_j >= 0] = f & 1 (y lies in (c_code, t_code] exactly when f
@@ -56,8 +59,10 @@ typedef __bf16 qkv_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 qkv_f16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kD = 128;                 // head dim of this path
-constexpr int kTok = 64;                // tokens per wave tile
-constexpr int kWaves = 4;               // waves per workgroup
+constexpr int kHalves = 1;              // 32-token MFMA column blocks per wave tile
+constexpr int kTok = 32 * kHalves;      // tokens per wave tile
+constexpr int kWaves = 8;               // waves per workgroup (two workgroups per CU)
+constexpr int kThreads = 64 * kWaves;
 constexpr int kFragN = 4 * 8 * 2 * 64;  // Pi fragments [block][k-step][split][lane] (64 KiB)
 constexpr float kPScaleF16 = 256.f;     // keeps the fp16 low part of Pi out of subnormals
 
@@ -133,32 +138,41 @@ __device__ __forceinline__ void search(float y, const float* t, uint64_t (&m)[L]
   for (int i = 0; i < L; ++i) m[i] = lanes_where(c[i]);
 }
 
-template <bool F16>
-__device__ __forceinline__ float half_lo(uint32_t w) {
-  if constexpr (F16)
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
-  else
-    return __uint_as_float(w << 16);
-}
+typedef __bf16 qkv_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 qkv_f16x2 __attribute__((ext_vector_type(2)));
 
-template <bool F16>
-__device__ __forceinline__ float half_hi(uint32_t w) {
-  if constexpr (F16)
-    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
-  else
-    return __uint_as_float(w & 0xffff0000u);
-}
-
+// s + sum of squares of the eight 16-bit values in q (v_dot2: exact products,
+// fp32 accumulation)
 template <bool F16>
 __device__ __forceinline__ float sumsq(uint4 q, float s) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float a = half_lo<F16>(w[i]), b = half_hi<F16>(w[i]);
-    s = fmaf(a, a, s);
-    s = fmaf(b, b, s);
+    if constexpr (F16)
+      s = __builtin_amdgcn_fdot2(__builtin_bit_cast(qkv_f16x2, w[i]),
+                                 __builtin_bit_cast(qkv_f16x2, w[i]), s, false);
+    else
+      s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(qkv_bf16x2, w[i]),
+                                          __builtin_bit_cast(qkv_bf16x2, w[i]), s, false);
   }
   return s;
+}
+
+// Search of y in a list symmetric about 0 (t[i] = -t[2^L - 2 - i], t[2^(L-1) - 1]
+// = 0), given its positive half p[0 .. 2^(L-1) - 2]: bit i of #{j : t[j] < y}
+// as m[i].  The top bit is [y > 0]; the others search |y| in the positive
+// half and are complemented for y <= 0 (the count mirrors; exact ties with a
+// threshold on the negative side land one code lower than a strict count).
+template <int L>
+__device__ __forceinline__ void search_sym(float y, const float* p, uint64_t (&m)[L]) {
+  const uint64_t pos = lanes_where(y > 0.f);
+  m[L - 1] = pos;
+  if constexpr (L > 1) {
+    uint64_t g[L - 1];
+    search<L - 1>(fabsf(y), p, g);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
+  }
 }
 
 template <bool F16>
@@ -203,14 +217,14 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
   }
 }
 
-// x fragments of 64 tokens: xf[tt][s], lane l = (row l & 31, half l >> 5) holds
-// x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt] (this
-// lane's token row of tile half tt; callers point lanes without a token at a
+// x fragments of a wave tile: xf[tt][s], lane l = (row l & 31, half l >> 5)
+// holds x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt]
+// (this lane's token row of block tt; callers point lanes without a token at a
 // valid row, whose results are never stored).
-__device__ __forceinline__ void load_x(uint4 (&xf)[2][8], const uint16_t* const (&row)[2],
-                                       int lane) {
+__device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][8],
+                                       const uint16_t* const (&row)[kHalves], int lane) {
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt)
+  for (int tt = 0; tt < kHalves; ++tt)
 #pragma unroll
     for (int s = 0; s < 8; ++s)
       xf[tt][s] = *reinterpret_cast<const uint4*>(row[tt] + 16 * s + 8 * (lane >> 5));
@@ -218,26 +232,27 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[2][8], const uint16_t* const 
 
 // ------------------------------------------------------------------ keys
 
-// One wave per tile of 64 consecutive tokens of one (b, h) group.  Input rows
+// One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
 // grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
 // MB MSE planes, then the QJL plane).
 template <int MB, bool F16>
-__global__ __launch_bounds__(256, 2) void append_k_mfma(
+__global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, const float* __restrict__ signs, Thresh fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NF = (1 << L) - 1;    // c_0, t_0, c_1, ..., c_{2^MB - 1}
-  constexpr int RD = 4 * L;           // dwords per row = staging dwords per lane
+  constexpr int RD = 4 * L;           // dwords per row
+  constexpr int NSK = RD * kTok / 64; // staging dwords per lane
   __shared__ uint4 frag[kFragN];
-  __shared__ float4 inv_s[kWaves][kTok / 4];  // 1 / norm of the wave's 64 tokens
+  __shared__ float4 inv_s[kWaves][kTok / 4];  // 1 / norm of the wave's tokens
   stage_pi<F16>(frag, pi, signs, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
-  float fv[NF];
+  float fv[NF / 2];  // positive half of the fine list
 #pragma unroll
-  for (int i = 0; i < NF; ++i) fv[i] = in_vgpr(fine.v[i]);
+  for (int i = 0; i < NF / 2; ++i) fv[i] = in_vgpr(fine.v[NF / 2 + 1 + i]);
   uint64_t sneg[4];  // lanes whose coordinate 32 n + (l & 31) has S < 0
 #pragma unroll
   for (int n = 0; n < 4; ++n) sneg[n] = lanes_where(signs[32 * n + li] < 0.f);
@@ -248,10 +263,11 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
-    uint4 xf[2][8];  // tokens past S read the last row; their results are not stored
+    uint4 xf[kHalves][8];  // tokens past S read the last row; their results are not stored
     {
-      const uint16_t* const row[2] = {x + (grp * S + s0 + min(li, nv - 1)) * kD,
-                                      x + (grp * S + s0 + min(32 + li, nv - 1)) * kD};
+      const uint16_t* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
       load_x(xf, row, lane);
     }
 
@@ -260,7 +276,7 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
     float* nrow = knorm + grp * t_stride + t0 + s0;
     float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < kHalves; ++tt) {
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
@@ -274,25 +290,25 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
     __builtin_amdgcn_wave_barrier();
 
-    uint32_t stg[RD];
+    uint32_t stg[NSK];
 #pragma unroll
-    for (int i = 0; i < RD; ++i) stg[i] = 0u;
+    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
 
     static_for<4>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
       constexpr int n = decltype(nc)::value;
       // one coordinate block at a time: keeps the scheduler from overlapping
       // blocks (and their accumulators and fragments) beyond the register file
       __builtin_amdgcn_sched_barrier(0);
-      qkv_f32x16 acc[2] = {};
+      qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
           const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
         }
-      static_for<2>([&](auto tc) {
+      static_for<kHalves>([&](auto tc) {
         constexpr int tt = decltype(tc)::value;
         float4 iv4[4];
 #pragma unroll
@@ -302,7 +318,7 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
           const float4 q4 = iv4[v >> 2];
           const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
           uint64_t f[L];
-          search<L>(acc[tt][v] * iv, fv, f);  // on y_j S_j
+          search_sym<L>(acc[tt][v] * iv, fv, f);  // on y_j S_j
           // token ta (lanes 0..31) and ta + 4 (lanes 32..63)
           constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);
           static_for<L>([&](auto rc) {
@@ -318,7 +334,7 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
 
     uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
 #pragma unroll
-    for (int i = 0; i < RD; ++i) {
+    for (int i = 0; i < NSK; ++i) {
       const int D = i * 64 + lane;
       if (D < nv * RD) dst[D] = stg[i];
     }
@@ -327,24 +343,24 @@ __global__ __launch_bounds__(256, 2) void append_k_mfma(
 
 // ---------------------------------------------------------------- values
 
-// One wave per 64 store tokens [A0, A0 + 64) of one group, A0 = 32-aligned, so
-// the wave owns two whole V tiles; tokens outside [t0, t0 + S) keep the bits
+// One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
+// so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
 // already in the store.
 template <int VB, bool F16>
-__global__ __launch_bounds__(256, 2) void append_v_mfma(
+__global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, Thresh bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0) {
   constexpr int NB = (1 << VB) - 1;  // boundaries
-  constexpr int NS = 4 * VB;         // staging dwords per lane: 2 tiles x VB planes x 128 / 64
+  constexpr int NS = 2 * VB * kHalves;  // staging dwords per lane: tiles x VB planes x 128 / 64
   __shared__ uint4 frag[kFragN];
   stage_pi<F16>(frag, pi, nullptr, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, li = lane & 31;
-  float bv[NB];
+  float bv[NB / 2 > 0 ? NB / 2 : 1];  // positive half of the boundaries
 #pragma unroll
-  for (int i = 0; i < NB; ++i) bv[i] = in_vgpr(bnd.v[i]);
+  for (int i = 0; i < NB / 2; ++i) bv[i] = in_vgpr(bnd.v[NB / 2 + 1 + i]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t a_base = t0 & ~int64_t(31);
   const int64_t tiles_per_group = t_stride / 32;
@@ -355,21 +371,23 @@ __global__ __launch_bounds__(256, 2) void append_v_mfma(
     const int64_t grp = tile / tpg;
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
-    bool ok[2];
-    uint4 xf[2][8];  // tokens outside [t0, t0 + S) read a valid row; their bits are not stored
+    bool ok[kHalves];
+    uint4 xf[kHalves][8];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
     {
+      const uint16_t* row[kHalves];
 #pragma unroll
-      for (int tt = 0; tt < 2; ++tt) ok[tt] = d0 + 32 * tt + li >= 0 && d0 + 32 * tt + li < S;
-      const uint16_t* const row[2] = {
-          x + (grp * S + min<int64_t>(max<int64_t>(d0 + li, 0), S - 1)) * kD,
-          x + (grp * S + min<int64_t>(max<int64_t>(d0 + 32 + li, 0), S - 1)) * kD};
+      for (int tt = 0; tt < kHalves; ++tt) {
+        const int64_t si = d0 + 32 * tt + li;
+        ok[tt] = si >= 0 && si < S;
+        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1)) * kD;
+      }
       load_x(xf, row, lane);
     }
 
-    float inv[2];  // token 32 tt + (l & 31): the C-column of this lane
+    float inv[kHalves];  // token 32 tt + (l & 31): the C-column of this lane
     float* nrow = vnorm + grp * t_stride + A0;
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < kHalves; ++tt) {
       float ss = 0.f;
 #pragma unroll
       for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
@@ -386,21 +404,21 @@ __global__ __launch_bounds__(256, 2) void append_v_mfma(
     static_for<4>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
       constexpr int mb = decltype(mc)::value;
       __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
-      qkv_f32x16 acc[2] = {};
+      qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
       for (int s = 0; s < 8; ++s)
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
           const uint4 af = frag[((mb * 8 + s) * 2 + sp) * 64 + lane];
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
+          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
         }
-      static_for<2>([&](auto tc) {  // V tile tt of the wave tile
+      static_for<kHalves>([&](auto tc) {  // V tile tt of the wave tile
         constexpr int tt = decltype(tc)::value;
         static_for<16>([&](auto vc) {
           constexpr int v = decltype(vc)::value;
           uint64_t m[VB];
-          search<VB>(acc[tt][v] * inv[tt], bv, m);
+          search_sym<VB>(acc[tt][v] * inv[tt], bv, m);
           // coordinate ca (lanes 0..31) and ca + 4 (lanes 32..63), tokens 32 tt + 0..31
           constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
           static_for<VB>([&](auto kc) {
@@ -494,8 +512,16 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
       return QKV_E_UNSUPPORTED;
     }
   }
-  if (values)
-    for (int i = 0; i < (1 << vbits) - 1; ++i) bnd.v[i] = vbound_host[i];
+  if (values) {
+    const int nb = (1 << vbits) - 1;
+    for (int i = 0; i < nb; ++i) bnd.v[i] = vbound_host[i];
+    bool asc = true;
+    for (int i = 0; i + 1 < nb; ++i) asc = asc && bnd.v[i] < bnd.v[i + 1];
+    if (!asc || !symmetric(bnd.v, nb)) {
+      qkv_set_error("store append needs ascending value boundaries symmetric about 0");
+      return QKV_E_UNSUPPORTED;
+    }
+  }
   if (groups == 0 || S == 0) return QKV_OK;
   auto s = static_cast<hipStream_t>(stream);
   const bool f16 = in_dtype == QKV_F16;
@@ -504,7 +530,7 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const dim3 grid(append_blocks(ntiles));
     const auto* xk = static_cast<const uint16_t*>(keys);
 #define QKV_K(MB, F)                                                                        \
-  hipLaunchKernelGGL((append_k_mfma<MB, F>), grid, dim3(256), 0, s, xk, S, tpg, ntiles, pi, \
+  hipLaunchKernelGGL((append_k_mfma<MB, F>), grid, dim3(kThreads), 0, s, xk, S, tpg, ntiles, pi, \
                      signs, fine, kstore, knorm, t_stride, t0)
     switch (mbits * 2 + (f16 ? 1 : 0)) {
       case 2: QKV_K(1, false); break;
@@ -523,7 +549,7 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const dim3 grid(append_blocks(ntiles));
     const auto* xv = static_cast<const uint16_t*>(values);
 #define QKV_V(VB, F)                                                                        \
-  hipLaunchKernelGGL((append_v_mfma<VB, F>), grid, dim3(256), 0, s, xv, S, tpg, ntiles, pi, \
+  hipLaunchKernelGGL((append_v_mfma<VB, F>), grid, dim3(kThreads), 0, s, xv, S, tpg, ntiles, pi, \
                      bnd, vstore, vnorm, t_stride, t0)
     switch (vbits * 2 + (f16 ? 1 : 0)) {
       case 2: QKV_V(1, false); break;
