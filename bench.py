@@ -5,14 +5,14 @@ compressed KV cache -- B=32, 32 query heads over 8 kv heads (GQA 4:1),
 head_dim 128, context 8192; keys 3-bit IP (2-bit MSE + 1-bit QJL), values
 3-bit MSE; bf16 queries; keys N(0,1) with 4 outlier channels x10.  The packed
 cache is prebuilt by the HIP compress kernel, then decode steps are timed.
-A step = one decode-attention call over the whole cache (prepare, then the
-split-K kernel whose last split per row group merges and stores).  Several distinct caches are rotated between steps so the
+A step = one decode-attention call over the whole cache (prepare + split-K
+partial + combine).  Several distinct caches are rotated between steps so the
 256 MB MALL cannot serve a repeat.  Compress (bf16 K and V -> packed cache) is
 timed separately and reported in Gvec/s.
 
 Prints one JSON line.  `value` is packed-byte throughput of the decode step
 (GB/s, inputs resident in HBM); `roofline` covers the dominant kernel (the
-split-K kernel with its merge), timed with HIP events on the launch stream; `cpu_baseline`
+split-K partial), timed with HIP events on the launch stream; `cpu_baseline`
 is the CPU oracle on a bounded sample of the same workload.
 """
 
@@ -35,6 +35,12 @@ METRIC = "decode attn over 3-bit KV: µs/step, HBM GB/s % of peak; compress Gvec
 B, HQ, HKV, D, T = 32, 32, 8, 128, 8192
 KEY_BITS, VAL_BITS = 3, 3
 OUTLIERS = (11, 47, 83, 119)
+
+# HBM bytes per split_mfma launch at this workload, from the two rocprofv3 --pmc
+# passes summarised in profiles/split_mfma_cfg3_decode.md: FETCH_SIZE x 2.0 +
+# WRITE_SIZE x 1.0 (KiB per dispatch; the factors are what the counters read
+# for a 256 MiB device copy, `bench.py --copy-calibration`).
+SPLIT_MFMA_TRAFFIC_BYTES = (111262 * 2 + 3120) * 1024
 
 
 def kv_bytes_per_token_head(d: int) -> int:
@@ -86,6 +92,21 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def copy_calibration() -> None:
+    """A plain device copy of known size: what rocprofv3's FETCH_SIZE / WRITE_SIZE
+    read for it scales the counters of the kernels measured against it."""
+    import torch
+    n = 256 * 1024 * 1024 // 4
+    a = torch.empty(n, device="cuda").uniform_()
+    b = torch.empty_like(a)
+    flush = torch.empty(512 * 1024 * 1024 // 4, device="cuda")  # evicts the MALL between copies
+    for i in range(3):
+        flush.fill_(float(i))
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_per_copy": n * 4, "copies": 3}))
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -96,7 +117,13 @@ def main() -> None:
     ap.add_argument("--cpu-batch", type=int, default=4, help="sequences in the CPU sample")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB three times (calibrates FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
@@ -126,7 +153,11 @@ def main() -> None:
         if c == 0:
             # time the append path: compress K (IP) + V (MSE) of all 2^21 token-heads
             # into the packed store; appends are queued back to back so host-side
-            # launch work overlaps the device
+            # launch work overlaps the device; untimed appends first bring the
+            # clocks up
+            for _ in range(10):
+                eng.clear()
+                eng.append(k, v)
             for _ in range(3):
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
@@ -166,13 +197,15 @@ def main() -> None:
                                           ws_bytes, splits, sptr))
         if ev is not None:
             ev[0].record(stream)
-        N.check(lib.qkv_attention_run(st.kst.data_ptr(), st.knorm.data_ptr(), st.vst.data_ptr(),
-                                      st.vnorm.data_ptr(), st.capacity, T, B, HQ, HKV, 1, D,
-                                      KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr,
-                                      vc_h.ptr, scale, 0, out.data_ptr(), N.QKV_F32,
-                                      ws.data_ptr(), ws_bytes, splits, sptr))
+        N.check(lib.qkv_attention_partial(st.kst.data_ptr(), st.knorm.data_ptr(),
+                                          st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, T,
+                                          B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, kc_h.ptr,
+                                          vc_h.ptr, scale, 0, ws.data_ptr(), ws_bytes, splits,
+                                          sptr))
         if ev is not None:
             ev[1].record(stream)
+        N.check(lib.qkv_attention_combine(B, HQ, HKV, 1, D, mq.Pi.data_ptr(), out.data_ptr(),
+                                          N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
 
     for i in range(args.warmup):
         step(i)
@@ -236,14 +269,13 @@ def main() -> None:
         "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
                                               / PEAK_HBM_GBS, 2),
         "roofline": {
-            "kernel": ("split_mfma (splits + merge)" if path == 1
-                       else "split_generic + combine_kernel") + " (qkv_attention_run)",
+            "kernel": ("split_mfma" if path == 1 else "split_generic") + " (qkv_attention_partial)",
             "bound": "hbm",
             "achieved": round(partial_gbs, 2),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(partial_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": SPLIT_MFMA_TRAFFIC_BYTES if path == 1 else None,
             "algorithmic_bytes_per_launch": kv_bytes,
             "avg_kernel_us": round(partial_ms * 1e3, 2),
         },

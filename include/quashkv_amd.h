@@ -254,21 +254,32 @@ int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
                          void* out, int32_t out_dtype, void* workspace,
                          int64_t ws_bytes, int32_t n_splits, void* stream);
 
-/* The two launches qkv_decode_attention makes, exposed so a caller can
- * overlap or time them separately (same arguments and workspace):
+/* The phases qkv_decode_attention runs, exposed so a caller can overlap or
+ * time them separately (same arguments and workspace, one stream):
  *   prepare  q~ = q Pi^T, w = alpha |q~| S and the MFMA query operands
  *            (quashkv/engine.py:237-238, quashkv/triton_kernels/attention.py:94,111)
- *   run      split-K online-softmax partials over the cache (quashkv/engine.py:
- *            245-289, quashkv/triton_kernels/attention.py:97-145), then the
- *            log-sum-exp merge of the splits, / max(l, 1e-8), x Pi once and
- *            the store (quashkv/engine.py:292-297,
- *            quashkv/triton_kernels/attention.py:147-149): two launches.
- * pi (d x d fp32, row-major) must be 16-byte aligned.
- * Calls that share one workspace must be ordered (one stream). */
+ *   partial  split-K online-softmax partials (m, l, O~) over the cache
+ *            (quashkv/engine.py:245-289, quashkv/triton_kernels/attention.py:97-145)
+ *   combine  log-sum-exp merge of the splits, / max(l, 1e-8), x Pi once, store
+ *            (quashkv/engine.py:292-297, quashkv/triton_kernels/attention.py:147-149)
+ *   run      partial + combine
+ * pi (d x d fp32, row-major) must be 16-byte aligned. */
 int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
                           int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
                           int32_t vbits, const float* pi, const float* kcent_host,
                           const float* vcent_host, const float* signs, float qjl_scale,
+                          void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          void* stream);
+int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
+                          const uint32_t* vstore, const float* vnorm,
+                          int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                          int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                          int32_t vbits, const float* kcent_host,
+                          const float* vcent_host, float scale, int32_t causal,
+                          void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          void* stream);
+int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+                          const float* pi, void* out, int32_t out_dtype,
                           void* workspace, int64_t ws_bytes, int32_t n_splits,
                           void* stream);
 int qkv_attention_run(const uint8_t* kstore, const float* knorm,

@@ -58,6 +58,10 @@ _SIGS = {
                                     _p, _i32, _p, _i64, _i32, _p]),
     "qkv_attention_prepare": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
                                      _p, _p, _p, _f32, _p, _i64, _i32, _p]),
+    "qkv_attention_partial": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
+                                     _i32, _i32, _p, _p, _f32, _i32, _p, _i64, _i32, _p]),
+    "qkv_attention_combine": (_i32, [_i32, _i32, _i32, _i32, _i32, _p, _p, _i32, _p, _i64, _i32,
+                                     _p]),
     "qkv_attention_run": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
                                  _i32, _i32, _p, _p, _p, _f32, _i32, _p, _i32, _p, _i64, _i32,
                                  _p]),

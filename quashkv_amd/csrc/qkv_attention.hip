@@ -1061,14 +1061,14 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   return QKV_OK;
 }
 
-extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
-                                 const uint32_t* vstore, const float* vnorm, int64_t t_stride,
-                                 int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
-                                 int32_t d, int32_t kbits, int32_t vbits, const float* pi,
-                                 const float* kcent_host, const float* vcent_host, float scale,
-                                 int32_t causal, void* out, int32_t out_dtype, void* workspace,
-                                 int64_t ws_bytes, int32_t n_splits, void* stream) {
-  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
+extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
+                                     const uint32_t* vstore, const float* vnorm,
+                                     int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                     int32_t vbits, const float* kcent_host,
+                                     const float* vcent_host, float scale, int32_t causal,
+                                     void* workspace, int64_t ws_bytes, int32_t n_splits,
+                                     void* stream) {
   QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
   QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
@@ -1076,9 +1076,7 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
               (long long)T);
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host && out,
-              "null pointer");
-  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  QKV_REQUIRE(kstore && knorm && vstore && vnorm && kcent_host && vcent_host, "null pointer");
   QKV_REQUIRE(qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4), "store must be 4-byte aligned");
   const int R = (Hq / Hkv) * Q;
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
@@ -1086,7 +1084,6 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
   float* po = at<float>(workspace, L.po);
   float* pml = at<float>(workspace, L.pml);
   auto s = static_cast<hipStream_t>(stream);
-  const dim3 cgrid(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC));
   if (use_mfma(tb, d, t_stride, T, n_splits)) {
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const int64_t split_len = mfma_split_len(T, n_splits);
@@ -1109,8 +1106,6 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
       case 24: QKV_MF(2, 4); break;
     }
 #undef QKV_MF
-    hipLaunchKernelGGL(combine_kernel<128>, cgrid, dim3(256), 0, s, po, pml, pi, n_splits, B,
-                       Hkv, R, Q, Hq, out, out_dtype);
     QKV_LAUNCHED();
     return QKV_OK;
   }
@@ -1123,8 +1118,6 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
     hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
                        qw, kstore, knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, kbits, \
                        vbits, tb, scale, causal, split_len, po, pml);                          \
-    hipLaunchKernelGGL(combine_kernel<DD>, cgrid, dim3(2 * DD), 0, s, po, pml, pi, n_splits,   \
-                       B, Hkv, R, Q, Hq, out, out_dtype);                                      \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -1133,6 +1126,55 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
   }
   QKV_LAUNCHED();
   return QKV_OK;
+}
+
+extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+                                     const float* pi, void* out, int32_t out_dtype,
+                                     void* workspace, int64_t ws_bytes, int32_t n_splits,
+                                     void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
+  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  QKV_REQUIRE(pi && out, "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  const int R = (Hq / Hkv) * Q;
+  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
+  auto s = static_cast<hipStream_t>(stream);
+  const dim3 cgrid(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC));
+  const float* po = at<float>(workspace, L.po);
+  const float* pml = at<float>(workspace, L.pml);
+  switch (d) {
+#define QKV_CASE(DD)                                                                          \
+  case DD:                                                                                    \
+    hipLaunchKernelGGL(combine_kernel<DD>, cgrid, dim3(2 * DD), 0, s, po, pml, pi, n_splits,  \
+                       B, Hkv, R, Q, Hq, out, out_dtype);                                     \
+    break;
+    QKV_CASE(64)
+    QKV_CASE(96)
+    QKV_CASE(128)
+#undef QKV_CASE
+  }
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
+                                 const uint32_t* vstore, const float* vnorm, int64_t t_stride,
+                                 int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                                 int32_t d, int32_t kbits, int32_t vbits, const float* pi,
+                                 const float* kcent_host, const float* vcent_host, float scale,
+                                 int32_t causal, void* out, int32_t out_dtype, void* workspace,
+                                 int64_t ws_bytes, int32_t n_splits, void* stream) {
+  // validate both halves before the first launch
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
+  QKV_REQUIRE(pi && out, "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  int st = qkv_attention_partial(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d,
+                                 kbits, vbits, kcent_host, vcent_host, scale, causal, workspace,
+                                 ws_bytes, n_splits, stream);
+  if (st != QKV_OK) return st;
+  return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
+                               n_splits, stream);
 }
 
 extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
