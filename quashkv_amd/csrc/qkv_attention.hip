@@ -476,8 +476,10 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   }
 }
 
+// Four waves per SIMD (at most 128 VGPRs): with 4 workgroups per CU the split
+// count fills the chip in whole rounds and hides the K/V load latency.
 template <int D, int MB, int VB>
-__global__ __launch_bounds__(256) void split_mfma(
+__global__ __launch_bounds__(256, 4) void split_mfma(
     const qkv_v4i* __restrict__ aq, const float* __restrict__ rowc,
     const uint8_t* __restrict__ kst, const float* __restrict__ knorm,
     const uint32_t* __restrict__ vst, const float* __restrict__ vnorm, int64_t t_stride,
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   // ts + tl <= T - Q + qi
   const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
   const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
-  constexpr int PD1 = 3;
+  constexpr int PD1 = 2;
   uint32_t kd[PD1][4][DPL];
   float kn[PD1][4], vv[PD1][4];
   // Tokens past the split end are read too (masked when scored): the store
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(256) void split_mfma(
   const int64_t vtile0 = ts >> 5;
   const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
-  constexpr int PD2 = 8;
+  constexpr int PD2 = 6;
   uint32_t vw[PD2][MTW][VB];
   auto load2 = [&](int slot, int tt) {
     const int64_t vt = vtile0 + 2 * tt + blk;
