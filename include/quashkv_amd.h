@@ -290,6 +290,31 @@ int qkv_attention_run(const uint8_t* kstore, const float* knorm,
                       int32_t causal, void* out, int32_t out_dtype, void* workspace,
                       int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Maximum inner-product search over K rows (the index form of the key store).
+ * Replaces QuashIndex.search (quashkv/nn_search/index.py:121-163): for M
+ * queries against N database rows,
+ *   score = n_x (<q Pi^T, c[code]> + qjl_scale sum_j |q~_j| S_j (2 b_j - 1))
+ * (no 1/sqrt(d)), then the k largest per query, descending; equal scores
+ * list the lower index first.  The (M, N) score matrix is never formed.
+ *   queries    M x d, q_dtype
+ *   d          64, 96 or 128; mbits key MSE bits 1..3 (index bits - 1)
+ *   kcent_host HOST array of the 2^mbits MSE centroids (symmetric)
+ *   kstore     N K rows of (mbits + 1) * d / 8 bytes (qkv_kplanes_pack layout)
+ *   norms      N fp32
+ *   k          <= 256 after clamping to N
+ *   out_scores M x k fp32, out_indices M x k int64
+ *   workspace  >= qkv_mips_workspace_bytes(M, d, mbits, k, N), 256-B aligned
+ * ---------------------------------------------------------------------- */
+int64_t qkv_mips_workspace_bytes(int32_t M, int32_t d, int32_t mbits, int32_t k,
+                                 int64_t N);
+int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, int32_t d,
+                    int32_t mbits, const float* pi, const float* signs,
+                    const float* kcent_host, float qjl_scale, const uint8_t* kstore,
+                    const float* norms, int64_t N, int32_t k, float* out_scores,
+                    int64_t* out_indices, void* workspace, int64_t ws_bytes,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

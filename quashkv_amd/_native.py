@@ -50,6 +50,9 @@ _SIGS = {
     "qkv_vtiles_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p]),
     "qkv_store_append": (_i32, [_i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                 _p, _p, _p, _p, _i64, _i64, _p]),
+    "qkv_mips_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i64]),
+    "qkv_mips_search": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _f32, _p, _p, _i64, _i32,
+                               _p, _p, _p, _i64, _p]),
     "qkv_attention_splits": (_i32, [_i32, _i32, _i32, _i32, _i32, _i64]),
     "qkv_attention_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "qkv_attention_path": (_i32, [_i32, _i32, _i32, _p, _p, _i64, _i64, _i32]),

@@ -35,6 +35,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 
 #include "qkv_common.h"
@@ -340,7 +341,11 @@ __device__ __forceinline__ void mfma_settle() {
 // Operand register layout: aq[(bhc * NU + u) * 64 + lane] (4 dwords), lane
 // (m = 4 row + digit, g = lane / 16); byte beta of dword e <-> row bit
 // 32 (g DPL + u / 2) + 8 beta + 4 (u % 2) + e.
-template <int D, int MB>
+// NPL planes per row: NPL - 1 MSE planes (odd bit subsets s, weight
+// 2 kg[s] q~_j), then the QJL plane.  The decode rows have NPL = mbits + 1
+// (mbits <= 2: the subsets are the single bits); the search index also uses
+// NPL = 5 for 3-bit MSE codes (three bits and their parity).
+template <int D, int NPL>
 __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, int q_dtype,
                                                     const float* __restrict__ pi,
                                                     const float* __restrict__ signs,
@@ -349,7 +354,8 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
                                                     qkv_v4i* __restrict__ aq,
                                                     float* __restrict__ rowc,
                                                     float* __restrict__ qw) {
-  constexpr int KRB = (MB + 1) * D / 8;
+  constexpr int MB = NPL - 1;  // weighted MSE planes
+  constexpr int KRB = NPL * D / 8;
   constexpr int DPL = KRB / 16;
   constexpr int NU = 2 * DPL;
   static_assert(D == 128, "one thread pair per output coordinate");
@@ -419,7 +425,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
     const float w = alpha * fabsf(v) * sgn;
     qt[r][jj] = v;
     wv[r][jj] = w;
-    if (r < nr) {  // q~ and w for the VALU kernel, qw[b][hkv][row][2][D]
+    if (qw != nullptr && r < nr) {  // q~ and w for the VALU kernel, qw[b][hkv][row][2][D]
       float* dst = qw + (int64_t(bh) * R + r0 + r) * 2 * D;
       dst[jj] = v;
       dst[D + jj] = w;
@@ -862,6 +868,241 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
   }
 }
 
+// ------------------------------------------------------------ MIPS search
+
+// QuashIndex.search (quashkv/nn_search/index.py:121-163): for each query q and
+// database vector x (K row + norm), score = n_x (<q~, c[code]> + alpha
+// sum_j |q~_j| S_j (2 b_j - 1)), no 1/sqrt(d); then the k largest scores per
+// query (descending; equal scores: lower index first).
+//
+// The scores are the decode kernel's integer MFMA dot products (same query
+// operands from prepare_mfma), with the database row bits as the B operand.
+// A workgroup (4 waves) takes 16 QC queries (QC chunks of 4 per wave) and a
+// range of vectors; the 64 rows of each step are staged once in LDS and every
+// wave expands them against its own query operands, held in registers.  Each
+// wave keeps a sorted top-k list per query in LDS; a score enters only if it
+// beats the list's k-th (a ballot finds the rare candidates).  Lists go to the
+// workspace per (query, vector split) and mips_merge picks the final k.
+constexpr int kMipsStep = 64;  // vectors staged per workgroup step
+constexpr int kMipsKMax = 256;
+
+template <int MB, int PDW>
+struct MipsCfg {
+  static constexpr int NS = n_odd_subsets(MB);  // MSE planes of the virtual row
+  static constexpr int NPL = NS + 1;            // + QJL plane
+  static constexpr int RAWD = (MB + 1) * PDW;   // stored row dwords (PDW = d / 32)
+  static constexpr int DPL = NPL;               // virtual dwords per lane group
+  static constexpr int NU = 2 * DPL;            // MFMAs per 16 vectors and chunk
+  static constexpr int QC = MB <= 2 ? 4 : 2;    // query chunks (of 4) per wave
+};
+
+// Rows of d < 128 (PDW = d / 32 dwords per plane) run as 128-wide rows whose
+// missing plane words are zero, against queries padded with zeros.
+template <int MB, int PDW>
+__global__ __launch_bounds__(256) void mips_scan(const qkv_v4i* __restrict__ aq,
+                                                 const float* __restrict__ rowc, int M,
+                                                 const uint8_t* __restrict__ kst,
+                                                 const float* __restrict__ norms, int64_t N,
+                                                 int64_t vlen, int k, float* __restrict__ cand_s,
+                                                 int* __restrict__ cand_i) {
+  using C = MipsCfg<MB, PDW>;
+  constexpr int NU = C::NU, QC = C::QC, RAWD = C::RAWD;
+  constexpr int QW = 4 * QC;  // queries per wave
+  extern __shared__ __align__(16) float smem_ms[];
+  uint32_t* rows = reinterpret_cast<uint32_t*>(smem_ms);           // [64][RAWD]
+  float* nrm_s = smem_ms + kMipsStep * RAWD;                        // [64]
+  float* ls = nrm_s + kMipsStep;                                    // [4][QW][k] scores
+  int* li = reinterpret_cast<int*>(ls + 4 * QW * k);                // [4][QW][k] indices
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int nchunks = (M + 3) / 4;
+  const int chunk0 = (blockIdx.y * 4 + wave) * QC;  // first chunk of this wave
+  const int64_t v0 = int64_t(blockIdx.x) * vlen;
+  const int64_t v1 = min<int64_t>(N, v0 + vlen);
+
+  qkv_v4i a[QC][NU];
+  float fq[QC], cr[QC], theta[QC];
+#pragma unroll
+  for (int c = 0; c < QC; ++c) {
+    const int ch = min(chunk0 + c, nchunks - 1);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) a[c][u] = aq[(int64_t(ch) * NU + u) * 64 + lane];
+    cr[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 0];
+    fq[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 1];
+    theta[c] = -INFINITY;
+  }
+  float* wls = ls + wave * QW * k;
+  int* wli = li + wave * QW * k;
+  for (int i = lane; i < QW * k; i += 64) {
+    wls[i] = -INFINITY;
+    wli[i] = -1;
+  }
+
+  for (int64_t s0 = v0; s0 < v1; s0 += kMipsStep) {
+    __syncthreads();  // the previous step's rows are consumed
+    for (int i = tid; i < kMipsStep * RAWD; i += 256) {
+      const int64_t v = s0 + i / RAWD;
+      rows[i] = v < v1 ? reinterpret_cast<const uint32_t*>(kst)[v * RAWD + i % RAWD] : 0u;
+    }
+    if (tid < kMipsStep) nrm_s[tid] = s0 + tid < v1 ? norms[s0 + tid] : 0.f;
+    __syncthreads();
+#pragma unroll 1
+    for (int g = 0; g < kMipsStep / 16; ++g) {
+      const int vl = g * 16 + ln;
+      // virtual row dwords lg*DPL .. : plane p < NS is the parity of the code
+      // bits in odd subset p, plane NS the QJL plane
+      uint32_t vd[C::DPL];
+#pragma unroll
+      for (int x = 0; x < C::DPL; ++x) {
+        const int vv = lg * C::DPL + x, pv = vv >> 2, w = vv & 3;
+        uint32_t val = 0;
+        if (w < PDW) {
+          if (pv < C::NS) {
+            const uint32_t sub = odd_subset(MB, pv < C::NS ? pv : 0);
+#pragma unroll
+            for (int r = 0; r < MB; ++r)
+              if ((sub >> r) & 1u) val ^= rows[vl * RAWD + PDW * r + w];
+          } else {
+            val = rows[vl * RAWD + PDW * MB + w];
+          }
+        }
+        vd[x] = val;
+      }
+      qkv_v4i bo[NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const uint32_t x = vd[u >> 1];
+        const int sh = 4 * (u & 1);
+        bo[u][0] = static_cast<int>(x & (0x01010101u << sh));
+        bo[u][1] = static_cast<int>(x & (0x02020202u << sh));
+        bo[u][2] = static_cast<int>(x & (0x04040404u << sh));
+        bo[u][3] = static_cast<int>(x & (0x08080808u << sh));
+      }
+      const float nv = nrm_s[vl];
+      const int64_t vidx = s0 + vl;
+      const bool valid = vidx < v1;
+      float sc[QC];
+      {
+        qkv_v4i acc[QC];
+#pragma unroll
+        for (int c = 0; c < QC; ++c) acc[c] = qkv_v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < NU; ++u)
+#pragma unroll
+          for (int c = 0; c < QC; ++c) acc[c] = mfma_i8(a[c][u], bo[u], acc[c]);
+        mfma_settle();
+#pragma unroll
+        for (int c = 0; c < QC; ++c) {
+          const float z = static_cast<float>(acc[c][0]) + 256.f * static_cast<float>(acc[c][1]) +
+                          65536.f * static_cast<float>(acc[c][2]) +
+                          16777216.f * static_cast<float>(acc[c][3]);
+          sc[c] = nv * fmaf(z, fq[c], cr[c]);
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < QC; ++c) {
+        const bool qok = (chunk0 + c) * 4 + lg < M;
+        uint64_t cand = __builtin_amdgcn_ballot_w64(valid && qok && sc[c] > theta[c]);
+        while (cand) {  // rare: insert in ascending lane (= index) order
+          const int L = __builtin_ctzll(cand);
+          cand &= cand - 1;
+          const float s_new = __shfl(sc[c], L, 64);
+          const int q = c * 4 + (L >> 4);  // wave-local query
+          float* qs = wls + q * k;
+          int* qi = wli + q * k;
+          if (s_new > qs[k - 1]) {
+            // position = number of entries >= s_new (they hold lower indices)
+            int ge = 0;
+            for (int j = lane; j < k; j += 64) ge += qs[j] >= s_new ? 1 : 0;
+            ge = qkv_wave_sum(ge);
+            // shift [ge, k-1) up by one, then write
+            float sv[kMipsKMax / 64];
+            int iv[kMipsKMax / 64];
+#pragma unroll
+            for (int t = 0; t < kMipsKMax / 64; ++t) {
+              const int j = lane + 64 * t;
+              sv[t] = (j > ge && j < k) ? qs[j - 1] : 0.f;
+              iv[t] = (j > ge && j < k) ? qi[j - 1] : 0;
+            }
+#pragma unroll
+            for (int t = 0; t < kMipsKMax / 64; ++t) {
+              const int j = lane + 64 * t;
+              if (j > ge && j < k) {
+                qs[j] = sv[t];
+                qi[j] = iv[t];
+              }
+            }
+            if (lane == 0) {
+              qs[ge] = s_new;
+              qi[ge] = static_cast<int>(s0 + g * 16 + (L & 15));
+            }
+            const float th = qs[k - 1];
+            if (lg == (L >> 4)) theta[c] = th;
+          }
+        }
+      }
+    }
+  }
+  // this wave's lists -> candidates [query][vsplit][k]
+  for (int q = 0; q < QW; ++q) {
+    const int qg = (chunk0 + q / 4) * 4 + (q % 4);
+    if (qg >= M) break;
+    const int64_t base = (int64_t(qg) * gridDim.x + blockIdx.x) * k;
+    for (int j = lane; j < k; j += 64) {
+      cand_s[base + j] = wls[q * k + j];
+      cand_i[base + j] = wli[q * k + j];
+    }
+  }
+}
+
+// Final top-k per query over its (vector split) candidate lists: k rounds of a
+// wave-wide arg-max (score descending, index ascending).
+__global__ __launch_bounds__(64) void mips_merge(const float* __restrict__ cand_s,
+                                                 const int* __restrict__ cand_i, int nsplit,
+                                                 int k, float* __restrict__ out_s,
+                                                 int64_t* __restrict__ out_i) {
+  extern __shared__ __align__(16) float smem_mm[];
+  const int q = blockIdx.x, lane = threadIdx.x;
+  const int n = nsplit * k;
+  float* cs = smem_mm;
+  int* ci = reinterpret_cast<int*>(smem_mm + n);
+  for (int i = lane; i < n; i += 64) {
+    cs[i] = cand_s[int64_t(q) * n + i];
+    ci[i] = cand_i[int64_t(q) * n + i];
+  }
+  __syncthreads();
+  for (int r = 0; r < k; ++r) {
+    float bs = -INFINITY;
+    int bi = INT_MAX, bp = -1;
+    for (int i = lane; i < n; i += 64) {
+      const float s = cs[i];
+      const int id = ci[i];
+      if (id >= 0 && (s > bs || (s == bs && id < bi))) {
+        bs = s;
+        bi = id;
+        bp = i;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float os = __shfl_xor(bs, o, 64);
+      const int oi = __shfl_xor(bi, o, 64), op = __shfl_xor(bp, o, 64);
+      if (op >= 0 && (bp < 0 || os > bs || (os == bs && oi < bi))) {
+        bs = os;
+        bi = oi;
+        bp = op;
+      }
+    }
+    if (lane == 0) {
+      out_s[int64_t(q) * k + r] = bs;
+      out_i[int64_t(q) * k + r] = bi;
+      if (bp >= 0) ci[bp] = -1;
+    }
+    __syncthreads();
+  }
+}
+
 // ------------------------------------------------------------ host helpers
 
 // Walsh coefficients of a codebook: c[code] = g_empty + sum_S g_S chi_S(code),
@@ -1038,11 +1279,11 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const dim3 grid(B * Hkv * chunks);
     if (kbits == 2)
-      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+      hipLaunchKernelGGL((prepare_mfma<128, 3>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
                          qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
                          at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
     else
-      hipLaunchKernelGGL((prepare_mfma<128, 1>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
+      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
                          qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
                          at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
     QKV_LAUNCHED();
@@ -1206,4 +1447,179 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
                            vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
                            workspace, ws_bytes, n_splits, stream);
+}
+
+// ------------------------------------------------------------ MIPS search (ABI)
+
+// Queries (fp32), Pi and S of a d < 128 index zero-padded to 128.
+__global__ __launch_bounds__(256) void mips_pad(const void* __restrict__ q, int q_dtype, int M,
+                                                int d, const float* __restrict__ pi,
+                                                const float* __restrict__ signs,
+                                                float* __restrict__ qp, float* __restrict__ pip,
+                                                float* __restrict__ sp) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t nq = int64_t(M) * 128;
+  if (i < nq) {
+    const int64_t m = i / 128;
+    const int j = static_cast<int>(i - m * 128);
+    qp[i] = j < d ? qkv_load(q, m * d + j, q_dtype) : 0.f;
+  } else if (i < nq + 128 * 128) {
+    const int64_t e = i - nq;
+    const int r = static_cast<int>(e / 128), c = static_cast<int>(e % 128);
+    pip[e] = (r < d && c < d) ? pi[r * d + c] : 0.f;
+  } else if (i < nq + 128 * 128 + 128) {
+    const int j = static_cast<int>(i - nq - 128 * 128);
+    sp[j] = j < d ? signs[j] : 0.f;
+  }
+}
+
+namespace {
+
+struct MipsLayout {
+  int64_t aq, rowc, cs, ci, pad, total;
+};
+
+int mips_splits(int32_t M, int64_t N, int mbits) {
+  const int qc = mbits <= 2 ? 4 : 2;
+  const int64_t qtiles = (M + 16 * qc - 1) / (16 * qc);
+  const int64_t want = (4 * int64_t(qkv_num_cus()) + qtiles - 1) / qtiles;
+  const int64_t maxs = std::max<int64_t>(1, (N + 4 * kMipsStep - 1) / (4 * kMipsStep));
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, maxs, 256})));
+}
+
+MipsLayout mips_layout(int32_t M, int d, int mbits, int k, int nsplit) {
+  const int ns = n_odd_subsets(mbits);
+  const int64_t nu = 2 * (ns + 1);
+  const int64_t chunks = (M + kRowsM - 1) / kRowsM;
+  MipsLayout w{};
+  int64_t off = 0;
+  auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+  w.aq = off;   off += up(chunks * nu * 64 * 16);
+  w.rowc = off; off += up(chunks * kRowsM * 2 * 4);
+  w.cs = off;   off += up(int64_t(M) * nsplit * k * 4);
+  w.ci = off;   off += up(int64_t(M) * nsplit * k * 4);
+  w.pad = off;  // d < 128: padded queries, Pi and S (fp32)
+  if (d < 128) off += up((int64_t(M) * 128 + 128 * 128 + 128) * 4);
+  w.total = off;
+  return w;
+}
+
+int64_t mips_scan_smem(int d, int mbits, int k) {
+  const int rawd = (mbits + 1) * (d / 32), qw = 4 * (mbits <= 2 ? 4 : 2);
+  return int64_t(kMipsStep) * rawd * 4 + kMipsStep * 4 + int64_t(4) * qw * k * 8;
+}
+
+}  // namespace
+
+extern "C" int64_t qkv_mips_workspace_bytes(int32_t M, int32_t d, int32_t mbits, int32_t k,
+                                            int64_t N) {
+  if (M <= 0 || !qkv_d_ok(d) || mbits < 1 || mbits > 3 || k <= 0 || N <= 0) return -1;
+  const int kk = static_cast<int>(std::min<int64_t>(k, N));
+  return mips_layout(M, d, mbits, kk, mips_splits(M, N, mbits)).total;
+}
+
+extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, int32_t d,
+                               int32_t mbits, const float* pi, const float* signs,
+                               const float* kcent_host, float qjl_scale, const uint8_t* kstore,
+                               const float* norms, int64_t N, int32_t k, float* out_scores,
+                               int64_t* out_indices, void* workspace, int64_t ws_bytes,
+                               void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype), "unsupported query dtype %d", q_dtype);
+  QKV_REQUIRE(N > 0, "Index is empty. Call add() first.");
+  QKV_REQUIRE(N < (int64_t(1) << 31), "index holds at most 2^31 - 1 vectors");
+  QKV_REQUIRE(M > 0 && k > 0, "invalid shape");
+  if (!qkv_d_ok(d) || mbits < 1 || mbits > 3) {
+    qkv_set_error("search runs on dim 64, 96 or 128 with 2..4-bit codes (got dim %d, %d MSE "
+                  "bits)", d, mbits);
+    return QKV_E_UNSUPPORTED;
+  }
+  k = static_cast<int32_t>(std::min<int64_t>(k, N));
+  if (k > kMipsKMax) {
+    qkv_set_error("search returns at most %d neighbours per query (asked %d)", kMipsKMax, k);
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(queries && pi && signs && kcent_host && kstore && norms && out_scores &&
+                  out_indices && workspace,
+              "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(workspace, 256),
+              "pi 16-B, store 4-B and workspace 256-B aligned");
+  Tables tb{};
+  for (int i = 0; i < (1 << mbits); ++i) tb.kc[i] = kcent_host[i];
+  if (!walsh_odd(kcent_host, mbits, tb.kg, &tb.kconst)) {
+    qkv_set_error("search needs a symmetric key codebook");
+    return QKV_E_UNSUPPORTED;
+  }
+  tb.mfma_ok = 1;
+  const int nsplit = mips_splits(M, N, mbits);
+  const MipsLayout L = mips_layout(M, d, mbits, k, nsplit);
+  QKV_REQUIRE(ws_bytes >= L.total, "workspace too small: %lld < %lld", (long long)ws_bytes,
+              (long long)L.total);
+  auto s = static_cast<hipStream_t>(stream);
+  const int chunks = (M + kRowsM - 1) / kRowsM;
+  qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
+  float* rowc = at<float>(workspace, L.rowc);
+  float* cs = at<float>(workspace, L.cs);
+  int* ci = at<int>(workspace, L.ci);
+  const void* qsrc = queries;
+  int qdt = q_dtype;
+  const float* pisrc = pi;
+  const float* ssrc = signs;
+  if (d < 128) {
+    float* qp = at<float>(workspace, L.pad);
+    float* pip = qp + int64_t(M) * 128;
+    float* sp = pip + 128 * 128;
+    const int64_t n = int64_t(M) * 128 + 128 * 128 + 128;
+    hipLaunchKernelGGL(mips_pad, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                       queries, q_dtype, M, d, pi, signs, qp, pip, sp);
+    QKV_LAUNCHED();
+    qsrc = qp;
+    qdt = QKV_F32;
+    pisrc = pip;
+    ssrc = sp;
+  }
+  // query operands: the decode prepare kernel with one "kv head" of M rows
+#define QKV_PREP(NPLV)                                                                           \
+  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256), 0, s, qsrc, qdt, pisrc, \
+                     ssrc, qjl_scale, M, 1, 1, M, chunks, tb, aq, rowc, nullptr)
+  if (mbits == 1) QKV_PREP(2);
+  else if (mbits == 2) QKV_PREP(3);
+  else QKV_PREP(5);
+#undef QKV_PREP
+  QKV_LAUNCHED();
+  const int qc = mbits <= 2 ? 4 : 2;
+  const int64_t vlen = ((N + nsplit - 1) / nsplit + kMipsStep - 1) / kMipsStep * kMipsStep;
+  const dim3 grid(nsplit, (chunks + 4 * qc - 1) / (4 * qc));
+  const int64_t smem = mips_scan_smem(d, mbits, k);
+#define QKV_SCAN(MBV, PDWV)                                                                       \
+  do {                                                                                            \
+    if (smem > 65536)                                                                             \
+      QKV_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mips_scan<MBV, PDWV>),          \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,                     \
+                                  static_cast<int>(smem)));                                       \
+    hipLaunchKernelGGL((mips_scan<MBV, PDWV>), grid, dim3(256), static_cast<uint32_t>(smem), s,  \
+                       aq, rowc, M, kstore, norms, N, vlen, k, cs, ci);                           \
+  } while (0)
+  switch (mbits * 10 + d / 32) {
+    case 12: QKV_SCAN(1, 2); break;
+    case 13: QKV_SCAN(1, 3); break;
+    case 14: QKV_SCAN(1, 4); break;
+    case 22: QKV_SCAN(2, 2); break;
+    case 23: QKV_SCAN(2, 3); break;
+    case 24: QKV_SCAN(2, 4); break;
+    case 32: QKV_SCAN(3, 2); break;
+    case 33: QKV_SCAN(3, 3); break;
+    case 34: QKV_SCAN(3, 4); break;
+  }
+#undef QKV_SCAN
+  QKV_LAUNCHED();
+  const int64_t msmem = int64_t(nsplit) * k * 8;
+  if (msmem > 65536)
+    QKV_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&mips_merge),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                static_cast<int>(std::min<int64_t>(msmem, 160 * 1024))));
+  QKV_REQUIRE(msmem <= 160 * 1024, "too many candidates per query");
+  hipLaunchKernelGGL(mips_merge, dim3(M), dim3(64), static_cast<uint32_t>(msmem), s, cs, ci,
+                     nsplit, k, out_scores, out_indices);
+  QKV_LAUNCHED();
+  return QKV_OK;
 }

@@ -89,6 +89,22 @@ def test_store_append_validation():
     assert st == N.QKV_E_UNSUPPORTED and "symmetric" in lib.qkv_last_error().decode()
 
 
+def test_mips_host_validation():
+    lib = N.lib()
+    assert lib.qkv_mips_workspace_bytes(10, 80, 2, 10, 100) == -1      # dim
+    assert lib.qkv_mips_workspace_bytes(10, 128, 4, 10, 100) == -1     # 5-bit codes
+    assert lib.qkv_mips_workspace_bytes(10, 128, 2, 10, 100) > 0
+    st = lib.qkv_mips_search(16, 0, 4, 128, 2, 16, 16, 16, 0.1, 16, 16, 0, 10, 16, 16, 256,
+                             1 << 20, None)
+    assert st == N.QKV_E_INVALID and "Index is empty" in lib.qkv_last_error().decode()
+    from quashkv_amd.nn_search import QuashIndex
+    idx = QuashIndex(dim=64, bits=3, device="cpu")
+    with pytest.raises(ValueError, match="Expected"):
+        idx.add(torch.randn(5, 32))
+    with pytest.raises(ValueError, match="Index is empty"):
+        idx.search(torch.randn(2, 64))
+
+
 def test_check_maps_status_to_exceptions():
     N.lib().qkv_pack_bits(None, None, 4, 128, 9, None)
     with pytest.raises(ValueError, match="Unsupported bits"):
