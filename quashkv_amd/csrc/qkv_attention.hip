@@ -886,6 +886,16 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
 constexpr int kMipsStep = 64;  // vectors staged per workgroup step
 constexpr int kMipsKMax = 256;
 
+// Order-preserving float <-> uint32 map, for a device-wide running maximum
+// (atomicMax on the image) of each query's k-th best score.
+__device__ __forceinline__ uint32_t fkey(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b ^ 0x80000000u);
+}
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
+
 template <int MB, int PDW>
 struct MipsCfg {
   static constexpr int NS = n_odd_subsets(MB);  // MSE planes of the virtual row
@@ -899,159 +909,221 @@ struct MipsCfg {
 // Rows of d < 128 (PDW = d / 32 dwords per plane) run as 128-wide rows whose
 // missing plane words are zero, against queries padded with zeros.
 template <int MB, int PDW>
-__global__ __launch_bounds__(256) void mips_scan(const qkv_v4i* __restrict__ aq,
+__global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ aq,
                                                  const float* __restrict__ rowc, int M,
                                                  const uint8_t* __restrict__ kst,
                                                  const float* __restrict__ norms, int64_t N,
-                                                 int64_t vlen, int k, float* __restrict__ cand_s,
-                                                 int* __restrict__ cand_i) {
+                                                 int nvc, int64_t vlen, int64_t n_items, int k,
+                                                 float* __restrict__ cand_s,
+                                                 int* __restrict__ cand_i,
+                                                 uint32_t* __restrict__ gth) {
   using C = MipsCfg<MB, PDW>;
   constexpr int NU = C::NU, QC = C::QC, RAWD = C::RAWD;
-  constexpr int QW = 4 * QC;  // queries per wave
+  constexpr int QW = 4 * QC;                      // queries per wave
+  constexpr int SD = kMipsStep * RAWD;            // row dwords per step
+  constexpr int LPT = (SD + 255) / 256;           // row dwords each thread stages
   extern __shared__ __align__(16) float smem_ms[];
-  uint32_t* rows = reinterpret_cast<uint32_t*>(smem_ms);           // [64][RAWD]
-  float* nrm_s = smem_ms + kMipsStep * RAWD;                        // [64]
-  float* ls = nrm_s + kMipsStep;                                    // [4][QW][k] scores
+  uint32_t* rows = reinterpret_cast<uint32_t*>(smem_ms);           // [2][64][RAWD]
+  float* nrm_s = smem_ms + 2 * kMipsStep * RAWD;                    // [2][64]
+  float* ls = nrm_s + 2 * kMipsStep;                                // [4][QW][k] scores
   int* li = reinterpret_cast<int*>(ls + 4 * QW * k);                // [4][QW][k] indices
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   const int nchunks = (M + 3) / 4;
-  const int chunk0 = (blockIdx.y * 4 + wave) * QC;  // first chunk of this wave
-  const int64_t v0 = int64_t(blockIdx.x) * vlen;
-  const int64_t v1 = min<int64_t>(N, v0 + vlen);
-
-  qkv_v4i a[QC][NU];
-  float fq[QC], cr[QC], theta[QC];
-#pragma unroll
-  for (int c = 0; c < QC; ++c) {
-    const int ch = min(chunk0 + c, nchunks - 1);
-#pragma unroll
-    for (int u = 0; u < NU; ++u) a[c][u] = aq[(int64_t(ch) * NU + u) * 64 + lane];
-    cr[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 0];
-    fq[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 1];
-    theta[c] = -INFINITY;
-  }
   float* wls = ls + wave * QW * k;
   int* wli = li + wave * QW * k;
-  for (int i = lane; i < QW * k; i += 64) {
-    wls[i] = -INFINITY;
-    wli[i] = -1;
+  const uint32_t* kw = reinterpret_cast<const uint32_t*>(kst);
+  // this lane's virtual row dwords lg*DPL + x: up to three stored dwords
+  // (offsets within a row) XORed, a zero mask where the plane word is absent
+  // (d < 128) -- precomputed so the row loop has no divergent branches
+  constexpr int NT = MB >= 3 ? 3 : 1;
+  int voff[C::DPL][NT];
+  uint32_t vmask[C::DPL][NT];
+#pragma unroll
+  for (int x = 0; x < C::DPL; ++x) {
+    const int vv = lg * C::DPL + x, pv = vv >> 2, w = vv & 3;
+    int t = 0;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      voff[x][j] = 0;
+      vmask[x][j] = 0u;
+    }
+    if (w < PDW) {
+      if (pv < C::NS) {
+        const uint32_t sub = odd_subset(MB, pv);
+        for (int r = 0; r < MB; ++r)
+          if (((sub >> r) & 1u) && t < NT) {
+            voff[x][t] = PDW * r + w;
+            vmask[x][t] = 0xffffffffu;
+            ++t;
+          }
+      } else {
+        voff[x][0] = PDW * MB + w;
+        vmask[x][0] = 0xffffffffu;
+      }
+    }
   }
 
-  for (int64_t s0 = v0; s0 < v1; s0 += kMipsStep) {
-    __syncthreads();  // the previous step's rows are consumed
-    for (int i = tid; i < kMipsStep * RAWD; i += 256) {
-      const int64_t v = s0 + i / RAWD;
-      rows[i] = v < v1 ? reinterpret_cast<const uint32_t*>(kst)[v * RAWD + i % RAWD] : 0u;
+  // items (query tile, vector chunk), vector-chunk major, so that a query's
+  // later chunks start from the k-th best score its earlier chunks published
+  // (gth); a workgroup takes items blockIdx.x, blockIdx.x + gridDim.x, ...
+  const int qtiles = static_cast<int>(n_items / nvc);
+  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int vc = static_cast<int>(item / qtiles), qt = static_cast<int>(item % qtiles);
+    const int chunk0 = (qt * 4 + wave) * QC;  // first query chunk of this wave
+    const int64_t v0 = int64_t(vc) * vlen;
+    const int64_t v1 = min<int64_t>(N, v0 + vlen);
+
+    qkv_v4i a[QC][NU];
+    // theta: this chunk list's k-th score (a candidate must beat it);
+    // tg: the query's device-wide bound (a candidate must reach it)
+    float fq[QC], cr[QC], theta[QC], tg[QC];
+#pragma unroll
+    for (int c = 0; c < QC; ++c) {
+      const int ch = min(chunk0 + c, nchunks - 1);
+#pragma unroll
+      for (int u = 0; u < NU; ++u) a[c][u] = aq[(int64_t(ch) * NU + u) * 64 + lane];
+      cr[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 0];
+      fq[c] = rowc[(int64_t(ch) * kRowsM + lg) * 2 + 1];
+      theta[c] = -INFINITY;
+      const int qg = (chunk0 + c) * 4 + lg;
+      tg[c] = qg < M ? fkey_inv(__hip_atomic_load(&gth[qg], __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT))
+                     : INFINITY;
     }
-    if (tid < kMipsStep) nrm_s[tid] = s0 + tid < v1 ? norms[s0 + tid] : 0.f;
+    for (int i = lane; i < QW * k; i += 64) {
+      wls[i] = -INFINITY;
+      wli[i] = -1;
+    }
+
+    // rows of step s0 staged through registers: loaded one step ahead
+    uint32_t pre[LPT];
+    float pn = 0.f;
+    auto fetch = [&](int64_t s0) {
+#pragma unroll
+      for (int x = 0; x < LPT; ++x) {
+        const int i = tid + 256 * x;
+        const int64_t v = s0 + i / RAWD;
+        pre[x] = (i < SD && v < v1) ? kw[v * RAWD + i % RAWD] : 0u;
+      }
+      if (tid < kMipsStep) pn = s0 + tid < v1 ? norms[s0 + tid] : 0.f;
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+      for (int x = 0; x < LPT; ++x)
+        if (tid + 256 * x < SD) rows[buf * SD + tid + 256 * x] = pre[x];
+      if (tid < kMipsStep) nrm_s[buf * kMipsStep + tid] = pn;
+    };
+    __syncthreads();  // the previous item's buffers are consumed
+    fetch(v0);
+    stash(0);
     __syncthreads();
+    int buf = 0;
+    for (int64_t s0 = v0; s0 < v1; s0 += kMipsStep) {
+      const bool more = s0 + kMipsStep < v1;
+      if (more) fetch(s0 + kMipsStep);  // in flight during this step
+      const uint32_t* rb = rows + buf * kMipsStep * RAWD;
+      const float* nb = nrm_s + buf * kMipsStep;
 #pragma unroll 1
-    for (int g = 0; g < kMipsStep / 16; ++g) {
-      const int vl = g * 16 + ln;
-      // virtual row dwords lg*DPL .. : plane p < NS is the parity of the code
-      // bits in odd subset p, plane NS the QJL plane
-      uint32_t vd[C::DPL];
+      for (int g = 0; g < kMipsStep / 16; ++g) {
+        const int vl = g * 16 + ln;
+        // virtual row dwords lg*DPL .. : plane p < NS is the parity of the
+        // code bits in odd subset p, plane NS the QJL plane
+        uint32_t vd[C::DPL];
+        const uint32_t* rv = rb + vl * RAWD;
 #pragma unroll
-      for (int x = 0; x < C::DPL; ++x) {
-        const int vv = lg * C::DPL + x, pv = vv >> 2, w = vv & 3;
-        uint32_t val = 0;
-        if (w < PDW) {
-          if (pv < C::NS) {
-            const uint32_t sub = odd_subset(MB, pv < C::NS ? pv : 0);
+        for (int x = 0; x < C::DPL; ++x) {
+          uint32_t val = rv[voff[x][0]] & vmask[x][0];
 #pragma unroll
-            for (int r = 0; r < MB; ++r)
-              if ((sub >> r) & 1u) val ^= rows[vl * RAWD + PDW * r + w];
-          } else {
-            val = rows[vl * RAWD + PDW * MB + w];
+          for (int j = 1; j < NT; ++j) val ^= rv[voff[x][j]] & vmask[x][j];
+          vd[x] = val;
+        }
+        qkv_v4i bo[NU];
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          const uint32_t x = vd[u >> 1];
+          const int sh = 4 * (u & 1);
+          bo[u][0] = static_cast<int>(x & (0x01010101u << sh));
+          bo[u][1] = static_cast<int>(x & (0x02020202u << sh));
+          bo[u][2] = static_cast<int>(x & (0x04040404u << sh));
+          bo[u][3] = static_cast<int>(x & (0x08080808u << sh));
+        }
+        const float nv = nb[vl];
+        const bool valid = s0 + vl < v1;
+        float sc[QC];
+        {
+          qkv_v4i acc[QC];
+#pragma unroll
+          for (int c = 0; c < QC; ++c) acc[c] = qkv_v4i{0, 0, 0, 0};
+#pragma unroll
+          for (int u = 0; u < NU; ++u)
+#pragma unroll
+            for (int c = 0; c < QC; ++c) acc[c] = mfma_i8(a[c][u], bo[u], acc[c]);
+          mfma_settle();
+#pragma unroll
+          for (int c = 0; c < QC; ++c) {
+            const float z = static_cast<float>(acc[c][0]) +
+                            256.f * static_cast<float>(acc[c][1]) +
+                            65536.f * static_cast<float>(acc[c][2]) +
+                            16777216.f * static_cast<float>(acc[c][3]);
+            sc[c] = nv * fmaf(z, fq[c], cr[c]);
           }
         }
-        vd[x] = val;
-      }
-      qkv_v4i bo[NU];
-#pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const uint32_t x = vd[u >> 1];
-        const int sh = 4 * (u & 1);
-        bo[u][0] = static_cast<int>(x & (0x01010101u << sh));
-        bo[u][1] = static_cast<int>(x & (0x02020202u << sh));
-        bo[u][2] = static_cast<int>(x & (0x04040404u << sh));
-        bo[u][3] = static_cast<int>(x & (0x08080808u << sh));
-      }
-      const float nv = nrm_s[vl];
-      const int64_t vidx = s0 + vl;
-      const bool valid = vidx < v1;
-      float sc[QC];
-      {
-        qkv_v4i acc[QC];
-#pragma unroll
-        for (int c = 0; c < QC; ++c) acc[c] = qkv_v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int u = 0; u < NU; ++u)
-#pragma unroll
-          for (int c = 0; c < QC; ++c) acc[c] = mfma_i8(a[c][u], bo[u], acc[c]);
-        mfma_settle();
 #pragma unroll
         for (int c = 0; c < QC; ++c) {
-          const float z = static_cast<float>(acc[c][0]) + 256.f * static_cast<float>(acc[c][1]) +
-                          65536.f * static_cast<float>(acc[c][2]) +
-                          16777216.f * static_cast<float>(acc[c][3]);
-          sc[c] = nv * fmaf(z, fq[c], cr[c]);
-        }
-      }
-#pragma unroll
-      for (int c = 0; c < QC; ++c) {
-        const bool qok = (chunk0 + c) * 4 + lg < M;
-        uint64_t cand = __builtin_amdgcn_ballot_w64(valid && qok && sc[c] > theta[c]);
-        while (cand) {  // rare: insert in ascending lane (= index) order
-          const int L = __builtin_ctzll(cand);
-          cand &= cand - 1;
-          const float s_new = __shfl(sc[c], L, 64);
-          const int q = c * 4 + (L >> 4);  // wave-local query
-          float* qs = wls + q * k;
-          int* qi = wli + q * k;
-          if (s_new > qs[k - 1]) {
-            // position = number of entries >= s_new (they hold lower indices)
-            int ge = 0;
-            for (int j = lane; j < k; j += 64) ge += qs[j] >= s_new ? 1 : 0;
-            ge = qkv_wave_sum(ge);
-            // shift [ge, k-1) up by one, then write
-            float sv[kMipsKMax / 64];
-            int iv[kMipsKMax / 64];
-#pragma unroll
-            for (int t = 0; t < kMipsKMax / 64; ++t) {
-              const int j = lane + 64 * t;
-              sv[t] = (j > ge && j < k) ? qs[j - 1] : 0.f;
-              iv[t] = (j > ge && j < k) ? qi[j - 1] : 0;
-            }
-#pragma unroll
-            for (int t = 0; t < kMipsKMax / 64; ++t) {
-              const int j = lane + 64 * t;
-              if (j > ge && j < k) {
-                qs[j] = sv[t];
-                qi[j] = iv[t];
+          uint64_t cand =
+              __builtin_amdgcn_ballot_w64(valid && sc[c] > theta[c] && sc[c] >= tg[c]);
+          while (cand) {  // rare: insert in ascending lane (= index) order
+            const int L = __builtin_ctzll(cand);
+            cand &= cand - 1;
+            const float s_new = __shfl(sc[c], L, 64);
+            const int q = c * 4 + (L >> 4);  // wave-local query
+            float* qs = wls + q * k;
+            int* qi = wli + q * k;
+            if (s_new > qs[k - 1]) {
+              // position = number of entries >= s_new (they hold lower indices)
+              int ge = 0;
+              for (int j = lane; j < k; j += 64) ge += qs[j] >= s_new ? 1 : 0;
+              ge = qkv_wave_sum(ge);
+              // shift [ge, k - 1) up by one, 64-entry blocks from the top down
+              // (a block reads its entries before the block below is written)
+              for (int t = (k - 1) >> 6; t >= 0; --t) {
+                const int j = lane + 64 * t;
+                const bool mv = j > ge && j < k;
+                const float sv = mv ? qs[j - 1] : 0.f;
+                const int iv = mv ? qi[j - 1] : 0;
+                if (mv) {
+                  qs[j] = sv;
+                  qi[j] = iv;
+                }
               }
+              if (lane == 0) {
+                qs[ge] = s_new;
+                qi[ge] = static_cast<int>(s0 + g * 16 + (L & 15));
+              }
+              const float th = qs[k - 1];
+              if (lg == (L >> 4)) theta[c] = th;
             }
-            if (lane == 0) {
-              qs[ge] = s_new;
-              qi[ge] = static_cast<int>(s0 + g * 16 + (L & 15));
-            }
-            const float th = qs[k - 1];
-            if (lg == (L >> 4)) theta[c] = th;
           }
         }
       }
+      if (more) stash(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
     }
-  }
-  // this wave's lists -> candidates [query][vsplit][k]
-  for (int q = 0; q < QW; ++q) {
-    const int qg = (chunk0 + q / 4) * 4 + (q % 4);
-    if (qg >= M) break;
-    const int64_t base = (int64_t(qg) * gridDim.x + blockIdx.x) * k;
-    for (int j = lane; j < k; j += 64) {
-      cand_s[base + j] = wls[q * k + j];
-      cand_i[base + j] = wli[q * k + j];
+    // this wave's lists -> candidates [query][vector chunk][k]; a full list's
+    // k-th score raises the query's device-wide bound
+    for (int q = 0; q < QW; ++q) {
+      const int qg = (chunk0 + q / 4) * 4 + (q % 4);
+      if (qg >= M) break;
+      const int64_t base = (int64_t(qg) * nvc + vc) * k;
+      for (int j = lane; j < k; j += 64) {
+        cand_s[base + j] = wls[q * k + j];
+        cand_i[base + j] = wli[q * k + j];
+      }
+      if (lane == 0 && wli[q * k + k - 1] >= 0)
+        atomicMax(&gth[qg], fkey(wls[q * k + k - 1]));
     }
   }
 }
@@ -1451,6 +1523,12 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
 
 // ------------------------------------------------------------ MIPS search (ABI)
 
+// Device-wide per-query bounds start at -inf.
+__global__ __launch_bounds__(256) void mips_init(uint32_t* __restrict__ gth, int M) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < M) gth[i] = 0x007fffffu;  // fkey(-inf)
+}
+
 // Queries (fp32), Pi and S of a d < 128 index zero-padded to 128.
 __global__ __launch_bounds__(256) void mips_pad(const void* __restrict__ q, int q_dtype, int M,
                                                 int d, const float* __restrict__ pi,
@@ -1476,14 +1554,16 @@ __global__ __launch_bounds__(256) void mips_pad(const void* __restrict__ q, int 
 namespace {
 
 struct MipsLayout {
-  int64_t aq, rowc, cs, ci, pad, total;
+  int64_t aq, rowc, cs, ci, gth, pad, total;
 };
 
+// Vector chunks per query tile: enough (query tile, chunk) items for several
+// per workgroup slot, chunks of at least 16 steps, at most 256 chunks.
 int mips_splits(int32_t M, int64_t N, int mbits) {
   const int qc = mbits <= 2 ? 4 : 2;
   const int64_t qtiles = (M + 16 * qc - 1) / (16 * qc);
-  const int64_t want = (4 * int64_t(qkv_num_cus()) + qtiles - 1) / qtiles;
-  const int64_t maxs = std::max<int64_t>(1, (N + 4 * kMipsStep - 1) / (4 * kMipsStep));
+  const int64_t want = (24 * int64_t(qkv_num_cus()) + qtiles - 1) / qtiles;
+  const int64_t maxs = std::max<int64_t>(1, (N + 16 * kMipsStep - 1) / (16 * kMipsStep));
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, maxs, 256})));
 }
 
@@ -1498,6 +1578,7 @@ MipsLayout mips_layout(int32_t M, int d, int mbits, int k, int nsplit) {
   w.rowc = off; off += up(chunks * kRowsM * 2 * 4);
   w.cs = off;   off += up(int64_t(M) * nsplit * k * 4);
   w.ci = off;   off += up(int64_t(M) * nsplit * k * 4);
+  w.gth = off;  off += up(int64_t(M) * 4);
   w.pad = off;  // d < 128: padded queries, Pi and S (fp32)
   if (d < 128) off += up((int64_t(M) * 128 + 128 * 128 + 128) * 4);
   w.total = off;
@@ -1506,7 +1587,7 @@ MipsLayout mips_layout(int32_t M, int d, int mbits, int k, int nsplit) {
 
 int64_t mips_scan_smem(int d, int mbits, int k) {
   const int rawd = (mbits + 1) * (d / 32), qw = 4 * (mbits <= 2 ? 4 : 2);
-  return int64_t(kMipsStep) * rawd * 4 + kMipsStep * 4 + int64_t(4) * qw * k * 8;
+  return 2 * (int64_t(kMipsStep) * rawd * 4 + kMipsStep * 4) + int64_t(4) * qw * k * 8;
 }
 
 }  // namespace
@@ -1560,6 +1641,8 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
   float* rowc = at<float>(workspace, L.rowc);
   float* cs = at<float>(workspace, L.cs);
   int* ci = at<int>(workspace, L.ci);
+  uint32_t* gth = at<uint32_t>(workspace, L.gth);
+  hipLaunchKernelGGL(mips_init, dim3((M + 255) / 256), dim3(256), 0, s, gth, M);
   const void* qsrc = queries;
   int qdt = q_dtype;
   const float* pisrc = pi;
@@ -1588,8 +1671,25 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
   QKV_LAUNCHED();
   const int qc = mbits <= 2 ? 4 : 2;
   const int64_t vlen = ((N + nsplit - 1) / nsplit + kMipsStep - 1) / kMipsStep * kMipsStep;
-  const dim3 grid(nsplit, (chunks + 4 * qc - 1) / (4 * qc));
+  const int64_t qtiles = (chunks + 4 * qc - 1) / (4 * qc);
+  const int64_t n_items = qtiles * nsplit;
   const int64_t smem = mips_scan_smem(d, mbits, k);
+  int per_cu = 0;
+  switch (mbits * 10 + d / 32) {
+#define QKV_OCC(MBV, PDWV, CASEV)                                                         \
+  case CASEV:                                                                             \
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, mips_scan<MBV, PDWV>, 256,  \
+                                                     static_cast<size_t>(smem)) != hipSuccess) \
+      per_cu = 0;                                                                         \
+    break;
+    QKV_OCC(1, 2, 12) QKV_OCC(1, 3, 13) QKV_OCC(1, 4, 14)
+    QKV_OCC(2, 2, 22) QKV_OCC(2, 3, 23) QKV_OCC(2, 4, 24)
+    QKV_OCC(3, 2, 32) QKV_OCC(3, 3, 33) QKV_OCC(3, 4, 34)
+#undef QKV_OCC
+  }
+  per_cu = std::max(per_cu, 1);
+  const dim3 grid(static_cast<unsigned>(
+      std::min<int64_t>(n_items, int64_t(per_cu) * qkv_num_cus())));
 #define QKV_SCAN(MBV, PDWV)                                                                       \
   do {                                                                                            \
     if (smem > 65536)                                                                             \
@@ -1597,7 +1697,7 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
                                   hipFuncAttributeMaxDynamicSharedMemorySize,                     \
                                   static_cast<int>(smem)));                                       \
     hipLaunchKernelGGL((mips_scan<MBV, PDWV>), grid, dim3(256), static_cast<uint32_t>(smem), s,  \
-                       aq, rowc, M, kstore, norms, N, vlen, k, cs, ci);                           \
+                       aq, rowc, M, kstore, norms, N, nsplit, vlen, n_items, k, cs, ci, gth);     \
   } while (0)
   switch (mbits * 10 + d / 32) {
     case 12: QKV_SCAN(1, 2); break;
