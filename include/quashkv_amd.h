@@ -141,6 +141,28 @@ int qkv_decompress(int32_t mode, int32_t fmt,
                    float qjl_scale, int64_t in_seq, int64_t in_group_stride,
                    void* out, int32_t out_dtype, void* stream);
 
+/* Mixed precision (quashkv/mixed_precision.py:25-322): qkv_compress /
+ * qkv_decompress with a per-coordinate choice of codebook.  Coordinate j uses
+ * the outlier codebook where outlier_mask[j] != 0 (d bytes), else the regular
+ * one.  Replaces MixedPrecisionMSEQuantizer.compress/decompress (:132-187;
+ * mode MSE) and MixedPrecisionIPQuantizer.compress (:271-322; mode IP: the
+ * QJL residual uses each coordinate's own codebook).  Codes are one uint8 per
+ * coordinate (the reference stores them unpacked); grouped-row addressing as
+ * above. */
+int qkv_compress_mixed(int32_t mode, int32_t in_dtype, int32_t flags, const void* x,
+                       int64_t n, int32_t d, const float* pi, const uint8_t* outlier_mask,
+                       const float* out_bounds, const float* out_cents, int32_t out_bits,
+                       const float* reg_bounds, const float* reg_cents, int32_t reg_bits,
+                       const float* signs, uint8_t* codes, uint8_t* qjl, float* norms,
+                       int64_t out_seq, int64_t out_group_stride, void* stream);
+int qkv_decompress_mixed(int32_t mode, const uint8_t* codes, const uint8_t* qjl,
+                         const float* norms, int64_t n, int32_t d,
+                         const uint8_t* outlier_mask, const float* out_cents,
+                         int32_t out_bits, const float* reg_cents, int32_t reg_bits,
+                         const float* pi, const float* signs, float qjl_scale,
+                         int64_t in_seq, int64_t in_group_stride, void* out,
+                         int32_t out_dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Cache store formats (the engine's compressed KV cache; see qkv_store.hip).
  *

@@ -50,6 +50,10 @@ _SIGS = {
     "qkv_vtiles_unpack": (_i32, [_p, _i64, _i64, _i32, _i32, _i64, _i64, _p, _p]),
     "qkv_store_append": (_i32, [_i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _p, _p,
                                 _p, _p, _p, _p, _i64, _i64, _p]),
+    "qkv_compress_mixed": (_i32, [_i32, _i32, _i32, _p, _i64, _i32, _p, _p, _p, _p, _i32, _p, _p,
+                                  _i32, _p, _p, _p, _p, _i64, _i64, _p]),
+    "qkv_decompress_mixed": (_i32, [_i32, _p, _p, _p, _i64, _i32, _p, _p, _i32, _p, _i32, _p, _p,
+                                    _f32, _i64, _i64, _p, _i32, _p]),
     "qkv_mips_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i64]),
     "qkv_mips_search": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _f32, _p, _p, _i64, _i32,
                                _p, _p, _p, _i64, _p]),

@@ -24,7 +24,8 @@ __global__ __launch_bounds__(kThreads) void compress_generic(
     const float* __restrict__ pi, const float* __restrict__ bounds,
     const float* __restrict__ cents, int bits, const float* __restrict__ signs,
     uint8_t* __restrict__ codes, uint8_t* __restrict__ qjl, float* __restrict__ norms,
-    int64_t out_seq, int64_t out_gstride) {
+    int64_t out_seq, int64_t out_gstride, const uint8_t* __restrict__ sel,
+    const float* __restrict__ alt_bounds, const float* __restrict__ alt_cents, int alt_bits) {
   __shared__ float piT[D * D];          // piT[k * D + j] = Pi[j][k]
   __shared__ float us[D * kRows];       // us[k * kRows + r] = u_r[k]
   __shared__ uint8_t cs[kRows * D];     // codes of the tile
@@ -36,7 +37,11 @@ __global__ __launch_bounds__(kThreads) void compress_generic(
   const int lane = tid & 63, wave = tid >> 6;
   const bool pre_rot = (flags & QKV_FLAG_PRE_ROTATED) != 0;
   const bool packed = (flags & QKV_FLAG_PACKED) != 0;
-  const int nb = (1 << bits) - 1;
+  // mixed precision: coordinates with sel[j] != 0 use the alternate codebook
+  const bool alt = sel != nullptr && tid < D && sel[tid] != 0;
+  const int nb = (1 << (alt ? alt_bits : bits)) - 1;
+  const float* tb = alt ? alt_bounds : bounds;
+  const float* cb = alt ? alt_cents : cents;
 
   if (!pre_rot) {
     for (int i = tid; i < D * D; i += kThreads) {
@@ -46,9 +51,9 @@ __global__ __launch_bounds__(kThreads) void compress_generic(
   }
   float t[15], c[16];
 #pragma unroll
-  for (int i = 0; i < 15; ++i) t[i] = i < nb ? bounds[i] : 0.f;
+  for (int i = 0; i < 15; ++i) t[i] = i < nb ? tb[i] : 0.f;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) c[i] = i <= nb ? cents[i] : 0.f;
+  for (int i = 0; i < 16; ++i) c[i] = i <= nb ? cb[i] : 0.f;
   const float sj = (mode == QKV_MODE_IP && tid < D) ? signs[tid] : 1.f;
   const int64_t pb = packed ? qkv_row_bytes(D, bits) : D;
   const int64_t pq = packed ? qkv_row_bytes(D, 1) : D;
@@ -130,14 +135,18 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
     int mode, int fmt, const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
     const float* __restrict__ norms, int64_t n, int bits, const float* __restrict__ pi,
     const float* __restrict__ cents, const float* __restrict__ signs, float qjl_scale,
-    int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype) {
+    int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype,
+    const uint8_t* __restrict__ sel, const float* __restrict__ alt_cents, int alt_bits) {
   __shared__ float pis[D * D];      // Pi row-major
   __shared__ float cs[D * kRows];   // cs[k * kRows + r] = rotated-domain value
   __shared__ float ns[kRows];
-  __shared__ float cl[16];          // centroid table (codes are masked to 4 bits)
+  __shared__ float cl[2][16];       // centroid tables (codes are masked to 4 bits)
   const int tid = threadIdx.x;
   for (int i = tid; i < D * D; i += kThreads) pis[i] = pi[i];
-  if (tid < 16) cl[tid] = tid < (1 << bits) ? cents[tid] : 0.f;
+  if (tid < 16) cl[0][tid] = tid < (1 << bits) ? cents[tid] : 0.f;
+  if (tid < 16 && sel) cl[1][tid] = tid < (1 << alt_bits) ? alt_cents[tid] : 0.f;
+  // mixed precision: coordinates with sel[j] != 0 use the alternate codebook
+  const int tsel = (sel != nullptr && tid < D && sel[tid] != 0) ? 1 : 0;
   const int cb = fmt == QKV_FMT_PACKED ? bits : 8;
   const int qb = fmt == QKV_FMT_PACKED ? 1 : 8;
   const int64_t pb = fmt == QKV_FMT_PACKED ? qkv_row_bytes(D, bits)
@@ -173,7 +182,7 @@ __global__ __launch_bounds__(kThreads) void decompress_generic(
               if (mode == QKV_MODE_IP) bit = qkv_get_code(qjl + row * pq, tid, qb);
             }
           }
-          v = cl[code & 15u];
+          v = cl[tsel][code & 15u];
           if (mode == QKV_MODE_IP) v += qs * (bit ? 1.f : -1.f);
         }
         cs[tid * kRows + r] = v;
@@ -216,11 +225,12 @@ int grid_rows(int64_t n) {
 
 }  // namespace
 
-extern "C" int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags, const void* x,
-                            int64_t n, int32_t d, const float* pi, const float* boundaries,
-                            const float* centroids, int32_t bits, const float* signs,
-                            uint8_t* codes, uint8_t* qjl, float* norms, int64_t out_seq,
-                            int64_t out_group_stride, void* stream) {
+static int compress_impl(int32_t mode, int32_t in_dtype, int32_t flags, const void* x,
+                         int64_t n, int32_t d, const float* pi, const float* boundaries,
+                         const float* centroids, int32_t bits, const float* signs,
+                         uint8_t* codes, uint8_t* qjl, float* norms, int64_t out_seq,
+                         int64_t out_group_stride, const uint8_t* sel, const float* alt_bounds,
+                         const float* alt_cents, int32_t alt_bits, void* stream) {
   QKV_REQUIRE(mode == QKV_MODE_MSE || mode == QKV_MODE_IP, "unknown mode %d", mode);
   QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
   QKV_REQUIRE(qkv_bits_ok(bits), "bits must be in {1, 2, 3, 4}, got %d", bits);
@@ -241,7 +251,8 @@ extern "C" int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags, const
   case DD:                                                                                    \
     hipLaunchKernelGGL(compress_generic<DD>, dim3(grid_rows(n)), dim3(kThreads), 0, s, mode, \
                        in_dtype, flags, x, n, pi, boundaries, centroids, bits, signs, codes,  \
-                       qjl, norms, out_seq, out_group_stride);                                \
+                       qjl, norms, out_seq, out_group_stride, sel, alt_bounds, alt_cents,     \
+                       alt_bits);                                                             \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -252,12 +263,13 @@ extern "C" int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags, const
   return QKV_OK;
 }
 
-extern "C" int qkv_decompress(int32_t mode, int32_t fmt, const uint8_t* codes,
-                              const uint8_t* qjl, const float* norms, int64_t n, int32_t d,
-                              int32_t bits, const float* pi, const float* centroids,
-                              const float* signs, float qjl_scale, int64_t in_seq,
-                              int64_t in_group_stride, void* out, int32_t out_dtype,
-                              void* stream) {
+static int decompress_impl(int32_t mode, int32_t fmt, const uint8_t* codes,
+                           const uint8_t* qjl, const float* norms, int64_t n, int32_t d,
+                           int32_t bits, const float* pi, const float* centroids,
+                           const float* signs, float qjl_scale, int64_t in_seq,
+                           int64_t in_group_stride, void* out, int32_t out_dtype,
+                           const uint8_t* sel, const float* alt_cents, int32_t alt_bits,
+                           void* stream) {
   QKV_REQUIRE(mode == QKV_MODE_MSE || mode == QKV_MODE_IP, "unknown mode %d", mode);
   QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
   QKV_REQUIRE(qkv_bits_ok(bits), "bits must be in {1, 2, 3, 4}, got %d", bits);
@@ -282,7 +294,8 @@ extern "C" int qkv_decompress(int32_t mode, int32_t fmt, const uint8_t* codes,
   case DD:                                                                                   \
     hipLaunchKernelGGL(decompress_generic<DD>, dim3(grid_rows(n)), dim3(kThreads), 0, s,    \
                        mode, fmt, codes, qjl, norms, n, bits, pi, centroids, signs,          \
-                       qjl_scale, in_seq, in_group_stride, out, out_dtype);                  \
+                       qjl_scale, in_seq, in_group_stride, out, out_dtype, sel, alt_cents,   \
+                       alt_bits);                                                            \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -291,4 +304,55 @@ extern "C" int qkv_decompress(int32_t mode, int32_t fmt, const uint8_t* codes,
   }
   QKV_LAUNCHED();
   return QKV_OK;
+}
+
+extern "C" int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags, const void* x,
+                            int64_t n, int32_t d, const float* pi, const float* boundaries,
+                            const float* centroids, int32_t bits, const float* signs,
+                            uint8_t* codes, uint8_t* qjl, float* norms, int64_t out_seq,
+                            int64_t out_group_stride, void* stream) {
+  return compress_impl(mode, in_dtype, flags, x, n, d, pi, boundaries, centroids, bits, signs,
+                       codes, qjl, norms, out_seq, out_group_stride, nullptr, nullptr, nullptr,
+                       0, stream);
+}
+
+extern "C" int qkv_decompress(int32_t mode, int32_t fmt, const uint8_t* codes,
+                              const uint8_t* qjl, const float* norms, int64_t n, int32_t d,
+                              int32_t bits, const float* pi, const float* centroids,
+                              const float* signs, float qjl_scale, int64_t in_seq,
+                              int64_t in_group_stride, void* out, int32_t out_dtype,
+                              void* stream) {
+  return decompress_impl(mode, fmt, codes, qjl, norms, n, d, bits, pi, centroids, signs,
+                         qjl_scale, in_seq, in_group_stride, out, out_dtype, nullptr, nullptr,
+                         0, stream);
+}
+
+extern "C" int qkv_compress_mixed(int32_t mode, int32_t in_dtype, int32_t flags, const void* x,
+                                  int64_t n, int32_t d, const float* pi,
+                                  const uint8_t* outlier_mask, const float* out_bounds,
+                                  const float* out_cents, int32_t out_bits,
+                                  const float* reg_bounds, const float* reg_cents,
+                                  int32_t reg_bits, const float* signs, uint8_t* codes,
+                                  uint8_t* qjl, float* norms, int64_t out_seq,
+                                  int64_t out_group_stride, void* stream) {
+  QKV_REQUIRE((flags & QKV_FLAG_PACKED) == 0, "mixed-precision codes are stored unpacked");
+  QKV_REQUIRE(outlier_mask && out_bounds && out_cents, "null pointer (outlier tables)");
+  QKV_REQUIRE(qkv_bits_ok(out_bits), "outlier bits must be in {1, 2, 3, 4}, got %d", out_bits);
+  return compress_impl(mode, in_dtype, flags, x, n, d, pi, reg_bounds, reg_cents, reg_bits,
+                       signs, codes, qjl, norms, out_seq, out_group_stride, outlier_mask,
+                       out_bounds, out_cents, out_bits, stream);
+}
+
+extern "C" int qkv_decompress_mixed(int32_t mode, const uint8_t* codes, const uint8_t* qjl,
+                                    const float* norms, int64_t n, int32_t d,
+                                    const uint8_t* outlier_mask, const float* out_cents,
+                                    int32_t out_bits, const float* reg_cents, int32_t reg_bits,
+                                    const float* pi, const float* signs, float qjl_scale,
+                                    int64_t in_seq, int64_t in_group_stride, void* out,
+                                    int32_t out_dtype, void* stream) {
+  QKV_REQUIRE(outlier_mask && out_cents, "null pointer (outlier tables)");
+  QKV_REQUIRE(qkv_bits_ok(out_bits), "outlier bits must be in {1, 2, 3, 4}, got %d", out_bits);
+  return decompress_impl(mode, QKV_FMT_UNPACKED, codes, qjl, norms, n, d, reg_bits, pi,
+                         reg_cents, signs, qjl_scale, in_seq, in_group_stride, out, out_dtype,
+                         outlier_mask, out_cents, out_bits, stream);
 }
