@@ -181,6 +181,153 @@ def bench_mips(args) -> None:
     print(json.dumps(line))
 
 
+def bench_cfg4(args) -> None:
+    """BASELINE configs[3] (cfg4): long-context mixed precision.  B=1, 32 query
+    heads over 8 kv heads, d=128; 131072 tokens appended in 64 chunks of 2048;
+    K MixedPrecisionMSEQuantizer(128, 3, 2, 32) calibrated on 65536 keys whose
+    32 channels 0, 4, ..., 124 have sigma 8 (the rest 1); V 4-bit MSE; bf16
+    K, V and query.  Times the 64 chunked appends and one decode query (the
+    MALL is flushed before every timed decode).  Prints one JSON line."""
+    import torch
+    import quashkv_amd as Q
+    from quashkv_amd import _native as N
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    lib = N.lib()
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+    B4, HQ4, HKV4, TT, CH = 1, 32, 8, 131072, 2048
+    out_ch = list(range(0, 128, 4))
+    g = torch.Generator(device=dev).manual_seed(3)
+    cal = torch.randn(65536, D, device=dev, generator=g)
+    cal[:, out_ch] *= 8.0
+    kq = Q.MixedPrecisionMSEQuantizer(D, outlier_bits=3, regular_bits=2, n_outliers=32,
+                                      seed=42, device=dev)
+    kq.calibrate(cal)
+    k = torch.randn(B4, HKV4, TT, D, device=dev, generator=g)
+    k[..., out_ch] *= 8.0
+    k = k.to(torch.bfloat16)
+    v = torch.randn(B4, HKV4, TT, D, device=dev, generator=g).to(torch.bfloat16)
+    q = torch.randn(B4, HQ4, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    eng = Q.QuashKVEngine(head_dim=D, value_bits=4, seed=42, device=dev, key_quantizer=kq,
+                          capacity=TT)
+    chunks = [(k[:, :, a:a + CH].contiguous(), v[:, :, a:a + CH].contiguous())
+              for a in range(0, TT, CH)]
+
+    def append_all():
+        eng.clear()
+        for kc, vc in chunks:
+            eng.append(kc, vc)
+
+    for _ in range(2):
+        append_all()
+    torch.cuda.synchronize()
+    app_ms = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        append_all()
+        e1.record()
+        torch.cuda.synchronize()
+        app_ms.append(e0.elapsed_time(e1))
+    append_ms = statistics.median(app_ms)
+
+    st = eng._store
+    _, pi_perm, n_out, (oc_h, rc_h, _, _, _) = eng._kmix_setup()
+    vq = eng.value_quantizer
+    vc_h = N.HostFloats(vq.codebook.centroids_host)
+    splits = lib.qkv_attention_splits(B4, HQ4, HKV4, 1, D, TT)
+    ws_bytes = lib.qkv_attention_workspace_bytes(B4, HQ4, HKV4, 1, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(B4, HQ4, 1, D, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    flush = torch.empty(512 * 1024 * 1024 // 4, device=dev)
+
+    def decode(ev):
+        ev[0].record(stream)
+        N.check(lib.qkv_attention_prepare_kmixed(q.data_ptr(), N.QKV_BF16, B4, HQ4, HKV4, 1, D,
+                                                 pi_perm.data_ptr(), n_out, oc_h.ptr, rc_h.ptr,
+                                                 ws.data_ptr(), ws_bytes, splits, sptr))
+        ev[1].record(stream)
+        N.check(lib.qkv_attention_partial(st.kst.data_ptr(), st.knorm.data_ptr(),
+                                          st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity,
+                                          TT, B4, HQ4, HKV4, 1, D, 2, 4, rc_h.ptr, vc_h.ptr, scale,
+                                          0, ws.data_ptr(), ws_bytes, splits, sptr))
+        ev[2].record(stream)
+        N.check(lib.qkv_attention_combine(B4, HQ4, HKV4, 1, D, vq.Pi.data_ptr(), out.data_ptr(),
+                                          N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
+        ev[3].record(stream)
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)]
+           for _ in range(args.warmup + args.steps)]
+    for i in range(args.warmup + args.steps):
+        flush.fill_(float(i))
+        decode(evs[i])
+    torch.cuda.synchronize()
+    timed = evs[args.warmup:]
+    dec_ms = statistics.median(e[0].elapsed_time(e[3]) for e in timed)
+    prep_ms = statistics.median(e[0].elapsed_time(e[1]) for e in timed)
+    part_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in timed)
+    comb_ms = statistics.median(e[2].elapsed_time(e[3]) for e in timed)
+    ref = eng.attention(q)
+    torch.cuda.synchronize()
+    same = bool(torch.equal(ref, out))
+
+    n_th = B4 * HKV4 * TT
+    alg_bytes = n_th * (36 + 4 + 64 + 4)       # 2.25-bit K packed tight + 4-bit V + norms
+    read_bytes = n_th * (48 + 4 + 64 + 4)      # what the kmixed rows actually hold
+    part_gbs = alg_bytes / (part_ms * 1e-3) / 1e9
+    line = {
+        "metric": "cfg4 mixed-precision decode: µs per query over 131072 tokens; append Gvec/s",
+        "value": round(dec_ms * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dec_ms, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8 (MFMA) / f32",
+        "data": "synthetic (seeded N(0,1); raw key channels 0,4,..,124 x8)",
+        "config": {"workload": "cfg4 long-context mixed precision", "batch": B4,
+                   "q_heads": HQ4, "kv_heads": HKV4, "head_dim": D, "context": TT,
+                   "chunk": CH, "key": "MixedPrecisionMSE 3/2 bits, 32 outliers",
+                   "value_bits": 4, "n_splits": splits},
+        "decode_us": round(dec_ms * 1e3, 2),
+        "decode_prepare_us": round(prep_ms * 1e3, 2),
+        "decode_partial_us": round(part_ms * 1e3, 2),
+        "decode_combine_us": round(comb_ms * 1e3, 2),
+        "decode_engine_output_identical": same,
+        "append_ms_total": round(append_ms, 3),
+        "append_gvec_s": round(2 * n_th / (append_ms * 1e-3) / 1e9, 4),
+        "roofline": {"kernel": "split_mfma (qkv_attention_partial)", "bound": "hbm",
+                     "achieved": round(part_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(part_gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg_bytes,
+                     "store_bytes_per_launch": read_bytes,
+                     "avg_kernel_us": round(part_ms * 1e3, 2)},
+    }
+    if not args.no_cpu:
+        from oracle import ref_math as R
+        torch.set_num_threads(os.cpu_count() or 1)
+        kc, _, vc = st.read_codes(0, TT)
+        cargs = (kc.cpu(), st.knorm[:, :, :TT].cpu(), vc.cpu(), st.vnorm[:, :, :TT].cpu(),
+                 kq.Pi.cpu(), kq._outlier_indices.cpu(), kq.outlier_codebook.centroids.cpu(),
+                 kq.regular_codebook.centroids.cpu(), vq.Pi.cpu(), vq.codebook.centroids.cpu())
+        qs = q.float().cpu()
+        ro = R.attention_mixed_keys(qs, *cargs)   # warmup
+        reps = []
+        for _ in range(max(args.cpu_reps, 1)):
+            t0 = time.perf_counter()
+            ro = R.attention_mixed_keys(qs, *cargs)
+            reps.append(time.perf_counter() - t0)
+        cpu_s = statistics.median(reps)
+        got = out.cpu().double()
+        line["oracle_rel_err"] = float((got - ro.double()).norm() / ro.double().norm())
+        line["cpu_baseline"] = {"value": round(cpu_s * 1e6, 1), "unit": "us",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"oracle attention_mixed_keys (fp32 torch CPU) over the "
+                                          f"whole cache, median of {len(reps)} reps"}
+    print(json.dumps(line), flush=True)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,8 +340,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB three times (calibrates FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg5"), default="cfg3",
-                    help="cfg3: the headline decode/compress line; cfg5: the MIPS index")
+    ap.add_argument("--workload", choices=("cfg3", "cfg4", "cfg5"), default="cfg3",
+                    help="cfg3: the headline decode/compress line; cfg4: mixed-precision "
+                         "long context; cfg5: the MIPS index")
     args = ap.parse_args()
 
     if args.copy_calibration:
@@ -202,6 +350,9 @@ def main() -> None:
         return
     if args.workload == "cfg5":
         bench_mips(args)
+        return
+    if args.workload == "cfg4":
+        bench_cfg4(args)
         return
 
     if args.gpus != 1:

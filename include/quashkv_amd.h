@@ -313,6 +313,65 @@ int qkv_attention_run(const uint8_t* kstore, const float* knorm,
                       int64_t ws_bytes, int32_t n_splits, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Mixed-precision keys in the store (MixedPrecisionMSEQuantizer with 3-bit
+ * outlier and 2-bit regular channels, quashkv/mixed_precision.py:25-197).
+ * The reference has no packed format or attention for these keys; it keeps
+ * one uint8 per code (:132-158) and reconstructs keys with decompress
+ * (:160-187).  Here keys live in "kmixed" rows of 48 bytes (d = 128) over
+ * coordinates permuted outliers first -- slot j holds rotated channel
+ * perm[j] -- as [plane b0][plane b1][plane 2], where plane 2 holds b2 of the
+ * n_out outlier slots at bits 0.. and their parity b0^b1^b2 at bits 64..
+ *   perm_host  HOST int32[128], a permutation with the n_out outlier
+ *              channels (ascending) first, then the regular ones (ascending)
+ *   pi_perm    device d x d fp32: row j = Pi row perm[j]
+ *   n_out      32 or 64 (else QKV_E_UNSUPPORTED)
+ * ---------------------------------------------------------------------- */
+
+/* One-uint8-per-code mixed codes (n x 128, channel order) into kmixed rows at
+ * grouped rows (seq, group_stride), and back. */
+int qkv_kmixed_pack(const uint8_t* codes, int64_t n, const int32_t* perm_host,
+                    int32_t n_out, uint8_t* dst, int64_t seq, int64_t group_stride,
+                    void* stream);
+int qkv_kmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
+                      int32_t n_out, int64_t seq, int64_t group_stride, uint8_t* codes,
+                      void* stream);
+
+/* Fused compress of bf16 / fp16 keys (groups x S x 128) straight into
+ * kmixed rows and norms at tokens [t0, t0 + S) of each group: the key half of
+ * qkv_store_append with MixedPrecisionMSEQuantizer.compress
+ * (quashkv/mixed_precision.py:132-158) in place of InnerProductQuantizer.
+ * out_bound_host (7) / reg_bound_host (3): HOST boundaries of the 3-bit and
+ * 2-bit codebooks (symmetric). */
+int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups, int64_t S,
+                            int32_t d, const float* pi_perm, int32_t n_out,
+                            const float* out_bound_host, const float* reg_bound_host,
+                            uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
+                            void* stream);
+
+/* Decode attention over kmixed K rows and V tiles: scores
+ * n_k <q Pi^T, c_channel[code]> (the reference's decompress-then-attend,
+ * quashkv/mixed_precision.py:160-187 with quashkv/engine.py:245-297), values
+ * un-rotated by pi_v.  out_cent_host (8) / reg_cent_host (4): HOST centroids.
+ * The prepare phase alone (query operands into the workspace) is exposed for
+ * timing; qkv_attention_run with kbits = 2 and kcent_host = reg_cent_host
+ * completes it. */
+int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
+                                 int32_t Hkv, int32_t Q, int32_t d, const float* pi_perm,
+                                 int32_t n_out, const float* out_cent_host,
+                                 const float* reg_cent_host, void* workspace,
+                                 int64_t ws_bytes, int32_t n_splits, void* stream);
+int qkv_decode_attention_kmixed(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                                const float* knorm, const uint32_t* vstore,
+                                const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+                                int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits,
+                                const float* pi_perm, int32_t n_out,
+                                const float* out_cent_host, const float* reg_cent_host,
+                                const float* pi_v, const float* vcent_host, float scale,
+                                int32_t causal, void* out, int32_t out_dtype,
+                                void* workspace, int64_t ws_bytes, int32_t n_splits,
+                                void* stream);
+
+/* ------------------------------------------------------------------------
  * Maximum inner-product search over K rows (the index form of the key store).
  * Replaces QuashIndex.search (quashkv/nn_search/index.py:121-163): for M
  * queries against N database rows,

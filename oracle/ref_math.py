@@ -384,6 +384,26 @@ def mixed_decompress(codes, norms, pi, outlier_idx, c_out, c_reg):
     return (xr @ pi) * norms.unsqueeze(-1)
 
 
+def attention_mixed_keys(q, kcodes, knorm, vcodes, vnorm, pi_k, outlier_idx, c_out, c_reg,
+                         pi_v, vcent, scale: Optional[float] = None) -> torch.Tensor:
+    """Decode attention over mixed-precision keys, decompress-then-attend:
+    K^ = mixed_decompress (mixed_precision.py:160-187), V^ = c_v[code] Pi_v n
+    (quantizer.py:133-152), softmax(q K^T scale) V^ (engine.py:245-297 with
+    K^ in place of the IP key estimate).  q (B, Hq, Q, d) with Hq a multiple of
+    the cache's heads (head h reads kv head h // G); codes (B, H, T, d)."""
+    q = q.float()
+    B, Hq, Q, d = q.shape
+    H = kcodes.shape[1]
+    G = Hq // H
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    k = mixed_decompress(kcodes, knorm, pi_k, outlier_idx, c_out, c_reg)   # (B, H, T, d)
+    v = (vcent[vcodes.long()] @ pi_v) * vnorm.unsqueeze(-1)
+    qg = q.reshape(B, H, G * Q, d)
+    w = torch.softmax((qg @ k.transpose(-1, -2)) * scale, dim=-1)
+    return (w @ v).reshape(B, Hq, Q, d)
+
+
 # ---------------------------------------------------------------------------
 # MIPS index search (quashkv/nn_search/index.py:121-163)
 # ---------------------------------------------------------------------------

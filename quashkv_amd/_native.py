@@ -54,6 +54,15 @@ _SIGS = {
                                   _i32, _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_decompress_mixed": (_i32, [_i32, _p, _p, _p, _i64, _i32, _p, _p, _i32, _p, _i32, _p, _p,
                                     _f32, _i64, _i64, _p, _i32, _p]),
+    "qkv_kmixed_pack": (_i32, [_p, _i64, _p, _i32, _p, _i64, _i64, _p]),
+    "qkv_kmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p]),
+    "qkv_store_append_kmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p, _p,
+                                       _i64, _i64, _p]),
+    "qkv_attention_prepare_kmixed": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32,
+                                            _p, _p, _p, _i64, _i32, _p]),
+    "qkv_decode_attention_kmixed": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
+                                           _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _p,
+                                           _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
     "qkv_mips_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32, _i64]),
     "qkv_mips_search": (_i32, [_p, _i32, _i32, _i32, _i32, _p, _p, _p, _f32, _p, _p, _i64, _i32,
                                _p, _p, _p, _i64, _p]),
@@ -187,6 +196,19 @@ class HostFloats:
         vals = [float(v) for v in values]
         self.n = len(vals)
         self.arr = (ctypes.c_float * max(self.n, 1))(*vals)
+
+    @property
+    def ptr(self) -> int:
+        return ctypes.addressof(self.arr)
+
+
+class HostInts:
+    """A small int32 table as a ctypes array (passed by value, like HostFloats)."""
+
+    def __init__(self, values):
+        vals = [int(v) for v in values]
+        self.n = len(vals)
+        self.arr = (ctypes.c_int32 * max(self.n, 1))(*vals)
 
     @property
     def ptr(self) -> int:

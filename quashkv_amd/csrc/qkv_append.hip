@@ -341,6 +341,128 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
   }
 }
 
+// ------------------------------------------------- mixed-precision keys
+
+// MixedPrecisionMSEQuantizer keys (quashkv/mixed_precision.py:132-158) with
+// 3-bit outlier and 2-bit regular channels, into 48-byte rows over permuted
+// coordinates (outliers first; the caller passes Pi with its rows permuted):
+// plane b0 and plane b1 of every coordinate, then a third plane holding b2 of
+// the NO outlier coordinates at bits 0.. and their parity b0^b1^b2 at bits
+// 64..  The outlier coordinates fill whole 32-coordinate blocks (NO = 32 or
+// 64), so each block's codebook is fixed at compile time.
+template <int NO, bool F16>
+__global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
+    const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
+    const float* __restrict__ pi_perm, Thresh po, Thresh pr, uint8_t* __restrict__ kst,
+    float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
+  constexpr int RD = 12;              // dwords per row
+  constexpr int NSK = RD * kTok / 64; // staging dwords per lane
+  constexpr int NOB = NO / 32;        // outlier blocks
+  __shared__ uint4 frag[kFragN];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  stage_pi<F16>(frag, pi_perm, nullptr, F16 ? kPScaleF16 : 1.f);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  float pov[3], prv[1];  // positive halves: outlier (3-bit) and regular (2-bit) boundaries
+#pragma unroll
+  for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.v[i]);
+  prv[0] = in_vgpr(pr.v[0]);
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
+
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
+    const int64_t grp = tile / tpg;
+    const int64_t s0 = (tile - grp * tpg) * kTok;
+    const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    uint4 xf[kHalves][8];
+    {
+      const uint16_t* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+      load_x(xf, row, lane);
+    }
+    float* nrow = knorm + grp * t_stride + t0 + s0;
+    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+#pragma unroll
+    for (int tt = 0; tt < kHalves; ++tt) {
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+      ss += __shfl_xor(ss, 32, 64);
+      const float nrm = fmaxf(sqrtf(ss), 1e-8f);
+      if (lane < 32) {
+        if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
+        invw[32 * tt + li] = iscale / nrm;
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+
+    uint32_t stg[NSK];
+#pragma unroll
+    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
+
+    static_for<4>([&](auto nc) {  // coordinate block n
+      constexpr int n = decltype(nc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp) {
+          const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+        }
+      static_for<kHalves>([&](auto tc) {
+        constexpr int tt = decltype(tc)::value;
+        float4 iv4[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+        static_for<16>([&](auto vc) {
+          constexpr int v = decltype(vc)::value;
+          const float4 q4 = iv4[v >> 2];
+          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+          const float y = acc[tt][v] * iv;
+          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);  // token of lanes 0..31
+          uint64_t w[4];  // plane words: b0, b1 (+ outliers: b2, parity)
+          if constexpr (n < NOB) {
+            uint64_t m[3];
+            search_sym<3>(y, pov, m);
+            w[0] = m[0];
+            w[1] = m[1];
+            w[2] = m[2];
+            w[3] = m[0] ^ m[1] ^ m[2];
+          } else {
+            uint64_t m[2];
+            search_sym<2>(y, prv, m);
+            w[0] = m[0];
+            w[1] = m[1];
+            w[2] = w[3] = 0;
+          }
+          static_for<(n < NOB ? 4 : 2)>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            // row dword: planes b0, b1 at word n; b2 / parity in the third plane
+            constexpr int dw = r < 2 ? 4 * r + n : 8 + n + (r == 3 ? 2 : 0);
+            constexpr int D0 = ta * RD + dw, D1 = (ta + 4) * RD + dw;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w[r]));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w[r] >> 32));
+          });
+        });
+      });
+    });
+
+    uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+#pragma unroll
+    for (int i = 0; i < NSK; ++i) {
+      const int D = i * 64 + lane;
+      if (D < nv * RD) dst[D] = stg[i];
+    }
+  }
+}
+
 // ---------------------------------------------------------------- values
 
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
@@ -564,5 +686,52 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
 #undef QKV_V
     QKV_LAUNCHED();
   }
+  return QKV_OK;
+}
+
+extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups,
+                                       int64_t S, int32_t d, const float* pi_perm,
+                                       int32_t n_out, const float* out_bound_host,
+                                       const float* reg_bound_host, uint8_t* kstore,
+                                       float* knorm, int64_t t_stride, int64_t t0,
+                                       void* stream) {
+  QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
+              (long long)t_stride, (long long)t0, (long long)(t0 + S));
+  if (in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
+    qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
+    return QKV_E_UNSUPPORTED;
+  }
+  if (d != kD || (n_out != 32 && n_out != 64)) {
+    qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(keys && pi_perm && out_bound_host && reg_bound_host && kstore && knorm,
+              "null pointer");
+  QKV_REQUIRE(qkv_aligned(keys, 16) && qkv_aligned(kstore, 4) && qkv_aligned(pi_perm, 16),
+              "keys / pi 16-B and store 4-B aligned");
+  Thresh po{}, pr{};
+  if (!symmetric(out_bound_host, 7) || !symmetric(reg_bound_host, 3)) {
+    qkv_set_error("mixed-precision keys need boundaries symmetric about 0");
+    return QKV_E_UNSUPPORTED;
+  }
+  for (int i = 0; i < 3; ++i) po.v[i] = out_bound_host[4 + i];
+  pr.v[0] = reg_bound_host[2];
+  if (groups == 0 || S == 0) return QKV_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
+  const dim3 grid(append_blocks(ntiles));
+  const auto* xk = static_cast<const uint16_t*>(keys);
+  const bool f16 = in_dtype == QKV_F16;
+#define QKV_KM(NOV, F)                                                                         \
+  hipLaunchKernelGGL((append_kmix_mfma<NOV, F>), grid, dim3(kThreads), 0, s, xk, S, tpg,     \
+                     ntiles, pi_perm, po, pr, kstore, knorm, t_stride, t0)
+  if (n_out == 32) {
+    if (f16) QKV_KM(32, true); else QKV_KM(32, false);
+  } else {
+    if (f16) QKV_KM(64, true); else QKV_KM(64, false);
+  }
+#undef QKV_KM
+  QKV_LAUNCHED();
   return QKV_OK;
 }

@@ -54,6 +54,14 @@ struct Tables {
   float vg[8];       // value Walsh coefficients, odd subsets (odd_subset order)
   float vconst;      // g_empty - sum vg (the plane form's constant)
   int mfma_ok;       // both codebooks admit the plane decomposition
+  // mixed-precision MSE keys (no QJL): rows hold planes b0, b1 of every
+  // coordinate, then b2 of the n_out first (outlier, 3-bit) coordinates at
+  // bits 0.. and their parity b0^b1^b2 at bits 64.. of the third plane
+  int kmix;
+  int n_out;
+  float kgo[4];      // outlier Walsh coefficients: b0, b1, b2, b0b1b2
+  float kgr[2];      // regular (2-bit) Walsh coefficients: b0, b1
+  float kco, kcr;    // -(sum of the coefficients) per kind
 };
 
 // Odd-size subsets of the code bits (bit masks), in a fixed order shared by
@@ -435,13 +443,19 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   {  // per-row scale exponent and constant (one wave per row)
     const int wave = tid >> 6, lane = tid & 63;
     float kgmax = 0.f;
+    if (tb.kmix) {
 #pragma unroll
-    for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+      for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
+      kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
+    } else {
+#pragma unroll
+      for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+    }
     float mq = 0.f, mw = 0.f, sq = 0.f, sw = 0.f;
     for (int jj = lane; jj < D; jj += 64) {
       mq = fmaxf(mq, fabsf(qt[wave][jj]));
       mw = fmaxf(mw, fabsf(wv[wave][jj]));
-      sq += qt[wave][jj];
+      sq += tb.kmix ? (jj < tb.n_out ? tb.kco : tb.kcr) * qt[wave][jj] : qt[wave][jj];
       sw += wv[wave][jj];
     }
     mq = qkv_wave_max(mq);
@@ -454,7 +468,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
       if (wmax > 0.f) frexpf(wmax, &e);  // wmax = f 2^e, f in [0.5, 1)
       const int fq = wmax > 0.f ? 30 - e : 0;  // |Z| < 2^30
       fqs[wave] = fq;
-      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 0] = tb.kconst * sq - sw;
+      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
       rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 1] = ldexpf(1.f, -fq);
     }
   }
@@ -470,7 +484,17 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
       for (int beta = 0; beta < 4; ++beta) {
         const int p = 32 * (g * DPL + (u >> 1)) + 8 * beta + i;
         const int region = p / D, jj = p - region * D;
-        const float W = region < MB ? 2.f * tb.kg[region] * qt[qrow][jj] : 2.f * wv[qrow][jj];
+        float W;
+        if (tb.kmix) {
+          if (region < 2) {
+            W = 2.f * (jj < tb.n_out ? tb.kgo[region] : tb.kgr[region]) * qt[qrow][jj];
+          } else {
+            const int c = jj & 63;  // b2 (bits 0..63) or parity (bits 64..127) of c
+            W = c < tb.n_out ? 2.f * tb.kgo[jj < 64 ? 2 : 3] * qt[qrow][c] : 0.f;
+          }
+        } else {
+          W = region < MB ? 2.f * tb.kg[region] * qt[qrow][jj] : 2.f * wv[qrow][jj];
+        }
         float zf = ldexpf(W, fqs[qrow] - i);
         if (i == 7) zf = -zf;
         const int Z = static_cast<int>(rintf(zf));
@@ -1376,6 +1400,47 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   return QKV_OK;
 }
 
+extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int32_t B,
+                                            int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+                                            const float* pi_perm, int32_t n_out,
+                                            const float* out_cent_host,
+                                            const float* reg_cent_host, void* workspace,
+                                            int64_t ws_bytes, int32_t n_splits, void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype), "unsupported query dtype %d", q_dtype);
+  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  if (d != 128 || (n_out != 32 && n_out != 64)) {
+    qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(q && pi_perm && out_cent_host && reg_cent_host, "null pointer");
+  QKV_REQUIRE(qkv_aligned(pi_perm, 16), "pi must be 16-byte aligned");
+  Tables tb{};
+  float kc_tmp[4];
+  float kconst_o = 0.f, kconst_r = 0.f;
+  if (!walsh_odd(out_cent_host, 3, tb.kgo, &kconst_o) ||
+      !walsh_odd(reg_cent_host, 2, kc_tmp, &kconst_r)) {
+    qkv_set_error("mixed-precision keys need symmetric codebooks");
+    return QKV_E_UNSUPPORTED;
+  }
+  tb.kgr[0] = kc_tmp[0];
+  tb.kgr[1] = kc_tmp[1];
+  tb.kco = kconst_o;
+  tb.kcr = kconst_r;
+  tb.kmix = 1;
+  tb.n_out = n_out;
+  tb.mfma_ok = 1;
+  const int R = (Hq / Hkv) * Q;
+  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
+  const int chunks = (R + kRowsM - 1) / kRowsM;
+  auto s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256), 0, s, q, q_dtype,
+                     pi_perm, pi_perm, 0.f, Hq, Hkv, Q, R, chunks, tb,
+                     at<qkv_v4i>(workspace, L.aq), at<float>(workspace, L.rowc), nullptr);
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
 extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
                                      const uint32_t* vstore, const float* vnorm,
                                      int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
@@ -1518,6 +1583,39 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   if (st != QKV_OK) return st;
   return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
                            vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
+                           workspace, ws_bytes, n_splits, stream);
+}
+
+// Decode attention over mixed-precision K rows (3-bit outlier / 2-bit regular
+// MSE keys, no QJL) and b-bit MSE V tiles.  Only the MFMA path reads this row
+// format, so the store and split shape must admit it.
+extern "C" int qkv_decode_attention_kmixed(
+    const void* q, int32_t q_dtype, const uint8_t* kstore, const float* knorm,
+    const uint32_t* vstore, const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits, const float* pi_perm,
+    int32_t n_out, const float* out_cent_host, const float* reg_cent_host, const float* pi_v,
+    const float* vcent_host, float scale, int32_t causal, void* out, int32_t out_dtype,
+    void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
+  QKV_REQUIRE(qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
+  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
+  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi_perm && out_cent_host &&
+                  reg_cent_host && pi_v && vcent_host && out,
+              "null pointer");
+  const Tables tb = make_tables(reg_cent_host, 2, vcent_host, vbits);
+  if (!use_mfma(tb, d, t_stride, T, n_splits)) {
+    qkv_set_error("mixed-precision keys need head_dim 128, a store capacity that is a "
+                  "multiple of 64, symmetric codebooks and splits of at most %d tokens",
+                  kSplitMax);
+    return QKV_E_UNSUPPORTED;
+  }
+  st = qkv_attention_prepare_kmixed(q, q_dtype, B, Hq, Hkv, Q, d, pi_perm, n_out, out_cent_host,
+                                    reg_cent_host, workspace, ws_bytes, n_splits, stream);
+  if (st != QKV_OK) return st;
+  return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, 2, vbits,
+                           pi_v, reg_cent_host, vcent_host, scale, causal, out, out_dtype,
                            workspace, ws_bytes, n_splits, stream);
 }
 

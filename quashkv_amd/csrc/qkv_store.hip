@@ -16,6 +16,13 @@
 //       the code of token t at coordinate j.
 //     vbits * d * 4 bytes per 32 tokens == the pack_bits size.
 //
+//   Mixed K rows ("kmixed", d = 128): 48 bytes per token over coordinates
+//   permuted outliers first (slot j holds rotated channel perm[j]):
+//       [plane b0 (16 B)][plane b1 (16 B)][plane 2 (16 B)]
+//     plane 2 holds b2 of slots 0 .. n_out-1 at bits 0.., and their parity
+//     b0^b1^b2 at bits 64..; outlier slots carry 3-bit codes, the others
+//     2-bit ones.
+//
 // Converters to and from one-uint8-per-code tensors serve the reference's
 // block views (CompressedKVBlock, quashkv/engine.py:30-51) and the tests.
 #include "qkv_common.h"
@@ -131,6 +138,67 @@ int check_d(int d) {
   return QKV_OK;
 }
 
+
+struct Perm128 {
+  uint8_t p[128];  // slot -> channel
+};
+
+// one thread per (row, row dword)
+__global__ void kmixed_pack_kernel(const uint8_t* __restrict__ codes, int64_t n, Perm128 perm,
+                                   int n_out, uint8_t* __restrict__ dst, int64_t seq,
+                                   int64_t gstride) {
+  const int64_t total = n * 12;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i / 12;
+    const int w = static_cast<int>(i - r * 12);
+    const uint8_t* c = codes + r * 128;
+    uint32_t word = 0;
+    for (int b = 0; b < 32; ++b) {
+      uint32_t bit;
+      if (w < 8) {  // planes b0, b1
+        bit = (uint32_t(c[perm.p[32 * (w & 3) + b]]) >> (w >> 2)) & 1u;
+      } else {
+        const int j = 32 * (w & 1) + b;  // outlier slot
+        if (j >= n_out) break;
+        const uint32_t code = c[perm.p[j]];
+        bit = w < 10 ? (code >> 2) & 1u : (code ^ (code >> 1) ^ (code >> 2)) & 1u;
+      }
+      word |= bit << b;
+    }
+    const int64_t row = qkv_grouped_row(r, seq, gstride);
+    reinterpret_cast<uint32_t*>(dst + row * 48)[w] = word;
+  }
+}
+
+// one thread per (row, slot)
+__global__ void kmixed_unpack_kernel(const uint8_t* __restrict__ src, int64_t n, Perm128 perm,
+                                     int n_out, int64_t seq, int64_t gstride,
+                                     uint8_t* __restrict__ codes) {
+  const int64_t total = n * 128;
+  for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t r = i >> 7;
+    const int j = static_cast<int>(i & 127);
+    const uint8_t* row = src + qkv_grouped_row(r, seq, gstride) * 48;
+    uint32_t code = (row[j >> 3] >> (j & 7)) & 1u;
+    code |= ((row[16 + (j >> 3)] >> (j & 7)) & 1u) << 1;
+    if (j < n_out) code |= ((row[32 + (j >> 3)] >> (j & 7)) & 1u) << 2;
+    codes[r * 128 + perm.p[j]] = static_cast<uint8_t>(code);
+  }
+}
+
+bool make_perm(const int32_t* perm_host, int n_out, Perm128* out) {
+  if (n_out != 32 && n_out != 64) return false;
+  bool seen[128] = {};
+  for (int j = 0; j < 128; ++j) {
+    const int32_t c = perm_host[j];
+    if (c < 0 || c >= 128 || seen[c]) return false;
+    seen[c] = true;
+    out->p[j] = static_cast<uint8_t>(c);
+  }
+  return true;
+}
 }  // namespace
 
 extern "C" int64_t qkv_kplanes_row_bytes(int32_t d, int32_t mbits, int32_t with_qjl) {
@@ -217,6 +285,44 @@ extern "C" int qkv_vtiles_unpack(const uint32_t* src, int64_t groups, int64_t S,
   hipLaunchKernelGGL(vtiles_unpack_kernel, dim3(grid_for(groups * S * d)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), src, groups, S, d, vbits,
                      tiles_per_group, t0, codes);
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+
+extern "C" int qkv_kmixed_pack(const uint8_t* codes, int64_t n, const int32_t* perm_host,
+                               int32_t n_out, uint8_t* dst, int64_t seq, int64_t group_stride,
+                               void* stream) {
+  QKV_REQUIRE(n >= 0, "negative row count");
+  QKV_REQUIRE(perm_host, "null pointer");
+  Perm128 perm;
+  QKV_REQUIRE(make_perm(perm_host, n_out, &perm),
+              "perm must be a permutation of 0..127 and n_out 32 or 64");
+  if (n == 0) return QKV_OK;
+  QKV_REQUIRE(codes && dst, "null pointer");
+  QKV_REQUIRE(qkv_aligned(dst, 4), "K rows must be 4-byte aligned");
+  QKV_REQUIRE(seq > 0 && group_stride >= seq, "bad grouped-row layout");
+  hipLaunchKernelGGL(kmixed_pack_kernel, dim3(grid_for(n * 12)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), codes, n, perm, n_out, dst, seq,
+                     group_stride);
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+extern "C" int qkv_kmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
+                                 int32_t n_out, int64_t seq, int64_t group_stride,
+                                 uint8_t* codes, void* stream) {
+  QKV_REQUIRE(n >= 0, "negative row count");
+  QKV_REQUIRE(perm_host, "null pointer");
+  Perm128 perm;
+  QKV_REQUIRE(make_perm(perm_host, n_out, &perm),
+              "perm must be a permutation of 0..127 and n_out 32 or 64");
+  if (n == 0) return QKV_OK;
+  QKV_REQUIRE(src && codes, "null pointer");
+  QKV_REQUIRE(seq > 0 && group_stride >= seq, "bad grouped-row layout");
+  hipLaunchKernelGGL(kmixed_unpack_kernel, dim3(grid_for(n * 128)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, n, perm, n_out, seq, group_stride,
+                     codes);
   QKV_LAUNCHED();
   return QKV_OK;
 }

@@ -14,6 +14,12 @@ API of quashkv/engine.py:54-360.  What changes underneath:
   on access, so code that walks blocks keeps working.
 * attention() runs the split-K decode kernels; query heads may be a multiple
   of the cached kv heads (GQA, head h reads kv head h // G).
+* ``key_quantizer=MixedPrecisionMSEQuantizer(128, 3, 2, 32 or 64)`` (an
+  extension: the reference engine takes IP keys only) keeps 2.5 / 3-bit
+  mixed-precision MSE keys in the store's "kmixed" rows; attention scores
+  them as the reference's decompress-then-attend would
+  (quashkv/mixed_precision.py:160-187).  The outlier channels are fixed at the
+  first append.
 """
 
 from __future__ import annotations
@@ -26,7 +32,8 @@ import torch
 
 from . import _native as N
 from .constants import DEFAULT_SEED, DEFAULT_TOTAL_BITS
-from .kernels import attention_store
+from .kernels import attention_store, attention_store_kmixed
+from .mixed_precision import MixedPrecisionMSEQuantizer
 from .packing import pack_bits, unpack_bits
 from .quantizer import InnerProductQuantizer, MSEQuantizer, _default_device, compress_into
 from .store import KVStore
@@ -56,6 +63,7 @@ class QuashKVEngine:
         device=None,
         pack_storage: bool = False,
         capacity: int = 0,
+        key_quantizer: Optional[MixedPrecisionMSEQuantizer] = None,
     ):
         self.head_dim = head_dim
         self.key_bits = key_bits
@@ -65,8 +73,20 @@ class QuashKVEngine:
         self.pack_storage = pack_storage
         self.initial_capacity = capacity
 
-        self.key_quantizer = InnerProductQuantizer(d=head_dim, total_bits=key_bits, seed=seed,
-                                                   device=self.device)
+        self._kmix = key_quantizer is not None
+        if self._kmix:
+            kq = key_quantizer
+            if not isinstance(kq, MixedPrecisionMSEQuantizer):
+                raise ValueError("key_quantizer must be a MixedPrecisionMSEQuantizer")
+            if (kq.d != head_dim or head_dim != 128 or kq.outlier_bits != 3
+                    or kq.regular_bits != 2 or kq.n_outliers not in (32, 64)):
+                raise ValueError("mixed-precision keys run on head_dim 128 with 3-bit outlier "
+                                 "and 2-bit regular channels, 32 or 64 outliers")
+            self.key_quantizer = kq.to(self.device)
+            self.key_bits = kq.effective_bits
+        else:
+            self.key_quantizer = InnerProductQuantizer(d=head_dim, total_bits=key_bits,
+                                                       seed=seed, device=self.device)
         self.value_quantizer = MSEQuantizer(d=head_dim, bits=value_bits, seed=seed,
                                             device=self.device)
         self._store: Optional[KVStore] = None
@@ -74,6 +94,7 @@ class QuashKVEngine:
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
         self._host_tables = None   # codebook tables passed by value to qkv_store_append
+        self._kmix_tables = None   # (perm, pi_perm, n_out, host tables) of mixed keys
 
     # ---------------------------------------------------------- compression
 
@@ -94,7 +115,7 @@ class QuashKVEngine:
             raise ValueError(
                 f"Expected keys and values of shape (batch, n_heads, seq_len, {self.head_dim}); "
                 f"got {tuple(keys.shape)} and {tuple(values.shape)}")
-        if self.key_quantizer.S.device != dev:
+        if self.value_quantizer.Pi.device != dev:
             self.to(dev)
         B, H, S, d = keys.shape
         st = self._store
@@ -102,11 +123,18 @@ class QuashKVEngine:
             raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
                              f"(B={st.B}, H={st.H})")
         if st is None:
-            st = self._store = KVStore(B, H, d, self.key_bits - 1, self.value_bits,
-                                       max(self.initial_capacity, S), dev)
+            kmix = None
+            if self._kmix:
+                perm, _, n_out, _ = self._kmix_setup()
+                kmix = (perm, n_out)
+            st = self._store = KVStore(B, H, d, 2 if self._kmix else self.key_bits - 1,
+                                       self.value_bits, max(self.initial_capacity, S), dev,
+                                       kmix=kmix)
         t0 = self._total_tokens
         st.ensure(t0 + S, t0)
-        if S > 0 and not self._append_fused(keys, values, t0):
+        if S > 0 and self._kmix:
+            self._append_kmix(keys, values, t0)
+        elif S > 0 and not self._append_fused(keys, values, t0):
             kq, vq = self.key_quantizer, self.value_quantizer
             mq = kq.mse_quantizer
             n = B * H * S
@@ -159,15 +187,73 @@ class QuashKVEngine:
                                    st.capacity, t0, stream))
         return True
 
+    def _kmix_setup(self):
+        """Slot order (outlier channels ascending, then the rest), Pi with its
+        rows in that order, n_out and the host codebook tables; fixed at the
+        first append."""
+        if self._kmix_tables is None:
+            kq = self.key_quantizer
+            if not kq.calibrated:
+                raise ValueError("mixed-precision keys need calibrate() or "
+                                 "set_outlier_channels() before the first append")
+            mask = kq._outlier_mask.cpu()
+            out = [j for j in range(self.head_dim) if bool(mask[j])]
+            reg = [j for j in range(self.head_dim) if not bool(mask[j])]
+            perm = out + reg
+            pi_perm = kq.Pi[torch.tensor(perm, device=kq.Pi.device)].contiguous()
+            oc, rc = kq.outlier_codebook, kq.regular_codebook
+            host = (N.HostFloats(oc.centroids_host), N.HostFloats(rc.centroids_host),
+                    N.HostFloats(oc.boundaries_host), N.HostFloats(rc.boundaries_host),
+                    N.HostFloats(self.value_quantizer.codebook.boundaries_host))
+            self._kmix_tables = (perm, pi_perm, len(out), host)
+        return self._kmix_tables
+
+    def _append_kmix(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
+        """Mixed-precision keys: bf16 / fp16 rows straight into kmixed rows
+        (qkv_store_append_kmixed); other dtypes through qkv_compress_mixed and
+        the kmixed packer.  Values as in the IP-key engine."""
+        B, H, S, d = keys.shape
+        st = self._store
+        kq, vq = self.key_quantizer, self.value_quantizer
+        perm, pi_perm, n_out, (_, _, ob, rb, vb) = self._kmix_setup()
+        if pi_perm.device != keys.device:
+            pi_perm = pi_perm.to(keys.device)
+            self._kmix_tables = (perm, pi_perm, n_out, self._kmix_tables[3])
+        L = N.lib()
+        stream = N.stream(keys.device)
+        n = B * H * S
+        fused = keys.dtype in (torch.bfloat16, torch.float16) and values.dtype == keys.dtype
+        if fused:
+            k, v = keys.contiguous(), values.contiguous()
+            dt = N.dtype_code(k.dtype)
+            N.check(L.qkv_store_append_kmixed(dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(),
+                                              n_out, ob.ptr, rb.ptr, st.kst.data_ptr(),
+                                              st.knorm.data_ptr(), st.capacity, t0, stream))
+            N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, d, 2, vq.bits,
+                                       vq.Pi.data_ptr(), None, None, None, vb.ptr, None, None,
+                                       st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, t0,
+                                       stream))
+            return
+        kc, _, kn = kq._compress_into(N.QKV_MODE_MSE, keys.reshape(n, d), None)
+        vc = torch.empty(n, d, dtype=torch.uint8, device=keys.device)
+        vn = torch.empty(n, dtype=torch.float32, device=keys.device)
+        compress_into(N.QKV_MODE_MSE, values.reshape(n, d), vq.Pi, vq.codebook.boundaries,
+                      vq.codebook.centroids, vq.bits, None, vc, None, vn, packed=False)
+        st.knorm[:, :, t0:t0 + S].copy_(kn.view(B, H, S))
+        st.vnorm[:, :, t0:t0 + S].copy_(vn.view(B, H, S))
+        st.write_codes(t0, S, kc, None, vc)
+
     @property
     def _cache(self) -> list[CompressedKVBlock]:
         st = self._store
         out = []
         for t0, s in self._blocks:
             kc, kb, vc = st.read_codes(t0, s)
-            if self.pack_storage:
+            if self.pack_storage and not self._kmix:
                 kc = pack_bits(kc, self.key_bits - 1)
                 kb = pack_bits(kb, 1)
+                vc = pack_bits(vc, self.value_bits)
+            elif self.pack_storage:
                 vc = pack_bits(vc, self.value_bits)
             sl = slice(t0, t0 + s)
             out.append(CompressedKVBlock(
@@ -193,6 +279,9 @@ class QuashKVEngine:
         if not block.packed:
             return block.mse_indices, block.qjl_signs, block.val_indices
         d = self.head_dim
+        if self._kmix:
+            return (block.mse_indices, None,
+                    unpack_bits(block.val_indices.contiguous(), self.value_bits, d))
         return (unpack_bits(block.mse_indices.contiguous(), self.key_bits - 1, d),
                 unpack_bits(block.qjl_signs.contiguous(), 1, d),
                 unpack_bits(block.val_indices.contiguous(), self.value_bits, d))
@@ -221,6 +310,12 @@ class QuashKVEngine:
         if self._workspace is None or self._workspace.numel() < need \
                 or self._workspace.device != queries.device:
             self._workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=queries.device)
+        if self._kmix:
+            _, pi_perm, n_out, (oc, rc, _, _, _) = self._kmix_setup()
+            return attention_store_kmixed(
+                queries, st, self._total_tokens, pi_perm, n_out, oc, rc, vq.Pi,
+                vq.codebook.centroids_host, scale=scale, causal=causal, out_dtype=out_dtype,
+                workspace=self._workspace, n_splits=splits)
         return attention_store(
             queries, st, self._total_tokens, kq.mse_quantizer.Pi,
             kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host, kq.S,
@@ -235,6 +330,7 @@ class QuashKVEngine:
             return 1.0
         orig_bits = torch.finfo(original_dtype).bits
         original = 2 * self.head_dim * orig_bits
+        # key_bits is the effective (average) width with mixed-precision keys
         compressed = (self.key_bits * self.head_dim + 32 + self.value_bits * self.head_dim + 32)
         return original / compressed
 
@@ -245,6 +341,9 @@ class QuashKVEngine:
             return 0
         st = self._store
         d = self.head_dim
+        if self._kmix:   # one uint8 per key code (as MixedPrecisionMSEQuantizer keeps them)
+            row = d + (N.packed_row_bytes(d, self.value_bits) if self.pack_storage else d)
+            return st.B * st.H * self._total_tokens * (row + 8)
         if self.pack_storage:
             row = (N.packed_row_bytes(d, self.key_bits - 1) + N.packed_row_bytes(d, 1)
                    + N.packed_row_bytes(d, self.value_bits))
@@ -258,6 +357,9 @@ class QuashKVEngine:
         self.value_quantizer.to(device)
         if self._store is not None:
             self._store.to(device)
+        if self._kmix_tables is not None:
+            perm, pi_perm, n_out, host = self._kmix_tables
+            self._kmix_tables = (perm, pi_perm.to(self.device), n_out, host)
         self._workspace = None
         return self
 

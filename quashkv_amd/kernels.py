@@ -149,6 +149,50 @@ def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Ten
     return out
 
 
+def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
+                           pi_perm: torch.Tensor, n_out: int, out_centroids: "N.HostFloats",
+                           reg_centroids: "N.HostFloats", Pi_v: torch.Tensor,
+                           val_centroids: Sequence[float], scale: Optional[float] = None,
+                           causal: bool = False, out_dtype: torch.dtype = torch.float32,
+                           workspace: Optional[torch.Tensor] = None,
+                           n_splits: Optional[int] = None) -> torch.Tensor:
+    """Decode attention over a store with mixed-precision ("kmixed") K rows:
+    scores n_k <q Pi^T, c_channel[code]> in the slot order of ``pi_perm``
+    (Pi's rows permuted outliers first), values un-rotated by ``Pi_v``."""
+    dev = N.require_gpu(queries, store.kst, pi_perm, Pi_v, what="attention")
+    B, Hq, Q, d = queries.shape
+    Hkv = store.H
+    if B != store.B or d != store.d:
+        raise ValueError(f"queries {tuple(queries.shape)} do not match the cache "
+                         f"(B={store.B}, head_dim={store.d})")
+    if Hq % Hkv != 0:
+        raise ValueError(f"query heads ({Hq}) must be a multiple of kv heads ({Hkv})")
+    if T <= 0:
+        raise ValueError("No compressed KV blocks in cache. Call append() first.")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    L = N.lib()
+    if n_splits is None:
+        n_splits = L.qkv_attention_splits(B, Hq, Hkv, Q, d, T)
+    need = L.qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    q = queries.contiguous()
+    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        q = q.float()
+    pi_perm, Pi_v = N.dense(pi_perm, Pi_v)
+    vc = N.HostFloats(val_centroids)
+    out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
+    N.check(L.qkv_decode_attention_kmixed(
+        q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
+        store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
+        store.vbits, pi_perm.data_ptr(), int(n_out), out_centroids.ptr, reg_centroids.ptr,
+        Pi_v.data_ptr(), vc.ptr, float(scale), 1 if causal else 0, out.data_ptr(),
+        N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
+        N.stream(dev)))
+    return out
+
+
 def _bits_of(centroids: torch.Tensor) -> int:
     n = centroids.numel()
     b = max(1, int(math.ceil(math.log2(max(n, 2)))))

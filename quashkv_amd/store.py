@@ -12,6 +12,11 @@ stream (C ABI "Cache store formats"):
 * ``vst``   (B, H, C / 32, vbits, d) int32 -- V bit-plane tiles of 32 tokens;
 * ``vnorm`` (B, H, C) fp32.
 
+With mixed-precision keys (``kmix = (perm, n_out)``) ``kst`` holds 48-byte
+"kmixed" rows instead: planes b0 and b1 of every coordinate, then b2 and the
+parity b0^b1^b2 of the n_out outlier coordinates, over coordinates permuted
+outliers first (slot j = rotated channel perm[j]).
+
 The capacity C is a multiple of 64 and doubles when an append needs room.
 Writes and reads go through the store converters of libquashkv_hip.so.
 """
@@ -33,11 +38,18 @@ def round_capacity(n: int) -> int:
 
 class KVStore:
     def __init__(self, B: int, H: int, d: int, mbits: int, vbits: int, capacity: int,
-                 device: torch.device):
+                 device: torch.device, kmix: Optional[tuple] = None):
         if d % 32 != 0:
             raise ValueError(f"head_dim {d} must be a multiple of 32 for the cache store")
         self.B, self.H, self.d = B, H, d
         self.mbits, self.vbits = mbits, vbits
+        self.kmix = None
+        if kmix is not None:
+            perm, n_out = kmix
+            if d != 128 or n_out not in (32, 64):
+                raise ValueError("mixed-precision keys need head_dim 128 and 32 or 64 outliers")
+            self.kmix = (N.HostInts(perm), int(n_out))
+            mbits = self.mbits = 2   # rows of three 16-byte planes
         self.krb = (mbits + 1) * d // 8
         self.device = torch.device(device)
         self.capacity = 0
@@ -78,29 +90,41 @@ class KVStore:
     def k_row_ptr(self, t0: int) -> int:
         return self.kst.data_ptr() + t0 * self.krb
 
-    def write_codes(self, t0: int, S: int, kcodes: torch.Tensor, kqjl: torch.Tensor,
+    def write_codes(self, t0: int, S: int, kcodes: torch.Tensor, kqjl: Optional[torch.Tensor],
                     vcodes: torch.Tensor) -> None:
-        """Unpacked uint8 codes (B*H*S, d) of tokens [t0, t0 + S) into the store."""
+        """Unpacked uint8 codes (B*H*S, d) of tokens [t0, t0 + S) into the store
+        (``kqjl`` None with mixed-precision keys)."""
         L = N.lib()
         n = self.B * self.H * S
         stream = N.stream(self.device)
-        N.check(L.qkv_kplanes_pack(kcodes.data_ptr(), kqjl.data_ptr(), n, self.d, self.mbits,
-                                   self.k_row_ptr(t0), self.krb, S, self.capacity, stream))
+        if self.kmix is not None:
+            perm, n_out = self.kmix
+            N.check(L.qkv_kmixed_pack(kcodes.data_ptr(), n, perm.ptr, n_out, self.k_row_ptr(t0),
+                                      S, self.capacity, stream))
+        else:
+            N.check(L.qkv_kplanes_pack(kcodes.data_ptr(), kqjl.data_ptr(), n, self.d, self.mbits,
+                                       self.k_row_ptr(t0), self.krb, S, self.capacity, stream))
         N.check(L.qkv_vtiles_pack(vcodes.data_ptr(), self.B * self.H, S, self.d, self.vbits,
                                   self.vst.data_ptr(), self.capacity // 32, t0, stream))
 
     def read_codes(self, t0: int, S: int):
-        """(kcodes, kqjl, vcodes) of tokens [t0, t0 + S) as (B, H, S, d) uint8."""
+        """(kcodes, kqjl, vcodes) of tokens [t0, t0 + S) as (B, H, S, d) uint8
+        (kqjl None with mixed-precision keys)."""
         L = N.lib()
         B, H, d = self.B, self.H, self.d
         kc = torch.empty(B, H, S, d, dtype=torch.uint8, device=self.device)
-        kq = torch.empty_like(kc)
+        kq = torch.empty_like(kc) if self.kmix is None else None
         vc = torch.empty_like(kc)
         if S == 0:
             return kc, kq, vc
         stream = N.stream(self.device)
-        N.check(L.qkv_kplanes_unpack(self.k_row_ptr(t0), self.krb, B * H * S, d, self.mbits, S,
-                                     self.capacity, kc.data_ptr(), kq.data_ptr(), stream))
+        if self.kmix is not None:
+            perm, n_out = self.kmix
+            N.check(L.qkv_kmixed_unpack(self.k_row_ptr(t0), B * H * S, perm.ptr, n_out, S,
+                                        self.capacity, kc.data_ptr(), stream))
+        else:
+            N.check(L.qkv_kplanes_unpack(self.k_row_ptr(t0), self.krb, B * H * S, d, self.mbits,
+                                         S, self.capacity, kc.data_ptr(), kq.data_ptr(), stream))
         N.check(L.qkv_vtiles_unpack(self.vst.data_ptr(), B * H, S, d, self.vbits,
                                     self.capacity // 32, t0, vc.data_ptr(), stream))
         return kc, kq, vc

@@ -1,0 +1,202 @@
+"""GPU parity of mixed-precision keys in the engine's store: kmixed rows
+(qkv_kmixed_pack / _unpack), the fused bf16 / fp16 key append
+(qkv_store_append_kmixed) and decode attention over them
+(qkv_decode_attention_kmixed), against the CPU oracle's mixed_compress and
+decompress-then-attend attention.
+
+Bars: the row format bit-exact (round trip and an independent bit model);
+fused codes as in the IP-key append (mismatch rate <= 1e-4, one code step);
+attention from the store's own codes within 1e-3 relative (fp32 queries),
+end to end from bf16 inputs within 1e-2 with cosine >= 0.9999."""
+
+import numpy as np
+import pytest
+import torch
+
+import quashkv_amd as Q
+from quashkv_amd import _native as N
+from oracle import ref_math as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+    N.lib()
+
+
+def _outliers(n_out, seed=1):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randperm(128, generator=g)[:n_out].sort().values
+
+
+def _engine(n_out, vbits=4, seed=42, out_idx=None, capacity=0):
+    kq = Q.MixedPrecisionMSEQuantizer(128, outlier_bits=3, regular_bits=2, n_outliers=n_out,
+                                      seed=seed, device=DEV)
+    kq.set_outlier_channels((out_idx if out_idx is not None else _outliers(n_out)).to(DEV))
+    return Q.QuashKVEngine(head_dim=128, value_bits=vbits, seed=seed, device=DEV,
+                           key_quantizer=kq, capacity=capacity)
+
+
+def _mismatch(a, b):
+    a, b = a.cpu().to(torch.int16), b.cpu().to(torch.int16)
+    diff = (a - b).abs()
+    return float((diff != 0).double().mean()), int(diff.max()) if diff.numel() else 0
+
+
+def _perm(out_idx):
+    o = [int(i) for i in out_idx]
+    return o + [j for j in range(128) if j not in set(o)]
+
+
+@pytest.mark.parametrize("n_out", [32, 64])
+def test_kmixed_rows_round_trip_and_bit_model(n_out):
+    gen = torch.Generator().manual_seed(n_out)
+    out_idx = _outliers(n_out, seed=n_out)
+    n, seq, gstride = 70, 35, 64          # 2 groups of 35 rows in a 64-row stride
+    codes = torch.randint(0, 4, (n, 128), generator=gen, dtype=torch.uint8)
+    codes[:, out_idx] = torch.randint(0, 8, (n, n_out), generator=gen, dtype=torch.uint8)
+    perm = _perm(out_idx)
+    ph = N.HostInts(perm)
+    L = N.lib()
+    dst = torch.zeros(2 * gstride, 48, dtype=torch.uint8, device=DEV)
+    N.check(L.qkv_kmixed_pack(codes.to(DEV).data_ptr(), n, ph.ptr, n_out, dst.data_ptr(), seq,
+                              gstride, N.stream(dst.device)))
+    back = torch.empty(n, 128, dtype=torch.uint8, device=DEV)
+    N.check(L.qkv_kmixed_unpack(dst.data_ptr(), n, ph.ptr, n_out, seq, gstride,
+                                back.data_ptr(), N.stream(dst.device)))
+    assert torch.equal(back.cpu(), codes)
+    # independent model of the row: bit (slot % 8) of byte slot / 8 per plane
+    rows = dst.cpu().numpy()
+    c = codes.numpy()[:, perm].astype(np.uint32)
+    for r in range(n):
+        row = rows[(r // seq) * gstride + r % seq]
+        bits = np.unpackbits(row, bitorder="little")
+        assert np.array_equal(bits[0:128], c[r] & 1)
+        assert np.array_equal(bits[128:256], (c[r] >> 1) & 1)
+        p2 = np.zeros(128, np.uint32)
+        p2[:n_out] = (c[r, :n_out] >> 2) & 1
+        p2[64:64 + n_out] = (c[r, :n_out] ^ (c[r, :n_out] >> 1) ^ (c[r, :n_out] >> 2)) & 1
+        assert np.array_equal(bits[256:384], p2)
+    # rows outside the groups' first 35 stay zero
+    assert not dst.cpu()[seq:gstride].any() and not dst.cpu()[gstride + seq:].any()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("n_out", [32, 64])
+def test_kmixed_append_vs_oracle(dtype, n_out):
+    """Codes and norms in the store against the oracle's mixed_compress
+    (quashkv/mixed_precision.py:132-158) on the same (upcast) keys; ragged
+    appends with unaligned starts."""
+    gen = torch.Generator().manual_seed(7 + n_out)
+    B, H = 2, 3
+    eng = _engine(n_out)
+    kq = eng.key_quantizer
+    out_idx = kq._outlier_indices.cpu()
+    pi = kq.Pi.cpu()
+    ks, vs, total = [], [], 0
+    for S in (150, 37, 1, 64, 0, 95):
+        y = torch.randn(B, H, S, 128, generator=gen)
+        y[..., out_idx] *= 8.0
+        k = (y @ pi).to(dtype)                     # rotated outliers -> key space
+        v = torch.randn(B, H, S, 128, generator=gen).to(dtype)
+        eng.append(k.to(DEV), v.to(DEV))
+        ks.append(k)
+        vs.append(v)
+        total += S
+    k, v = torch.cat(ks, dim=2), torch.cat(vs, dim=2)
+    st = eng._store
+    kc, kb, vc = st.read_codes(0, total)
+    assert kb is None
+    kc, vc = kc.cpu(), vc.cpu()
+    oc, on = R.mixed_compress(k.float().reshape(-1, 128), pi, out_idx,
+                              kq.outlier_codebook.boundaries.cpu(),
+                              kq.regular_codebook.boundaries.cpu())
+    vq = eng.value_quantizer
+    ovc, ovn = R.compress_mse(v.float().reshape(-1, 128), vq.Pi.cpu(),
+                              vq.codebook.boundaries.cpu())
+    for got, ref in ((kc, oc), (vc, ovc)):
+        rate, step = _mismatch(got.reshape(-1, 128), ref.reshape(-1, 128))
+        assert rate <= 1e-4 and step <= 1, (rate, step)
+    for got, ref in ((st.knorm[:, :, :total], on), (st.vnorm[:, :, :total], ovn)):
+        got, ref = got.cpu().double().reshape(-1), ref.double().reshape(-1)
+        assert float(((got - ref).abs() / ref).max()) <= 2e-6
+    # outlier codes reach the top of 8 levels, regular ones stay within 4
+    assert int(kc[..., out_idx].max()) == 7
+    mask = torch.ones(128, dtype=torch.bool)
+    mask[out_idx] = False
+    assert int(kc[..., mask].max()) <= 3
+
+
+@pytest.mark.parametrize("n_out,G,Q_", [(32, 4, 1), (64, 4, 1), (32, 1, 2)])
+def test_kmixed_attention_from_store_codes(n_out, G, Q_):
+    """Attention kernel alone: the oracle's decompress-then-attend on the
+    codes and norms read back from the store, fp32 queries, rel-err <= 1e-3."""
+    gen = torch.Generator().manual_seed(3 * n_out + G)
+    B, Hkv, S = 2, 2, 777
+    eng = _engine(n_out)
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    out_idx = kq._outlier_indices.cpu()
+    y = torch.randn(B, Hkv, S, 128, generator=gen)
+    y[..., out_idx] *= 8.0
+    k = (y @ kq.Pi.cpu()).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, 128, generator=gen).to(torch.bfloat16)
+    eng.append(k[:, :, :500].to(DEV), v[:, :, :500].to(DEV))
+    eng.append(k[:, :, 500:].to(DEV), v[:, :, 500:].to(DEV))
+    q = torch.randn(B, Hkv * G, Q_, 128, generator=gen)
+    out = eng.attention(q.to(DEV)).cpu().double()
+    st = eng._store
+    kc, _, vc = st.read_codes(0, S)
+    ref = R.attention_mixed_keys(q, kc.cpu(), st.knorm[:, :, :S].cpu(), vc.cpu(),
+                                 st.vnorm[:, :, :S].cpu(), kq.Pi.cpu(), out_idx,
+                                 kq.outlier_codebook.centroids.cpu(),
+                                 kq.regular_codebook.centroids.cpu(), vq.Pi.cpu(),
+                                 vq.codebook.centroids.cpu()).double()
+    err = float((out - ref).norm() / ref.norm())
+    assert err <= 1e-3, err
+
+
+def test_kmixed_engine_attention_end_to_end():
+    """bf16 keys, values and query through the fused append and the decode
+    kernel, against the oracle on its own codes of the same inputs."""
+    gen = torch.Generator().manual_seed(5)
+    B, Hkv, G, S = 1, 4, 4, 1500
+    eng = _engine(32)
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    out_idx = kq._outlier_indices.cpu()
+    y = torch.randn(B, Hkv, S, 128, generator=gen)
+    y[..., out_idx] *= 8.0
+    k = (y @ kq.Pi.cpu()).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(B, Hkv * G, 1, 128, generator=gen).to(torch.bfloat16)
+    for a in range(0, S, 512):
+        eng.append(k[:, :, a:a + 512].to(DEV), v[:, :, a:a + 512].to(DEV))
+    out = eng.attention(q.to(DEV)).cpu().double()
+    kc, kn = R.mixed_compress(k.float(), kq.Pi.cpu(), out_idx,
+                              kq.outlier_codebook.boundaries.cpu(),
+                              kq.regular_codebook.boundaries.cpu())
+    vc, vn = R.compress_mse(v.float(), vq.Pi.cpu(), vq.codebook.boundaries.cpu())
+    ref = R.attention_mixed_keys(q.float(), kc, kn, vc, vn, kq.Pi.cpu(), out_idx,
+                                 kq.outlier_codebook.centroids.cpu(),
+                                 kq.regular_codebook.centroids.cpu(), vq.Pi.cpu(),
+                                 vq.codebook.centroids.cpu()).double()
+    err = float((out - ref).norm() / ref.norm())
+    cos = float((out.flatten() @ ref.flatten()) / (out.norm() * ref.norm()))
+    assert err <= 1e-2 and cos >= 0.9999, (err, cos)
+    assert eng.key_bits == 2.25 and eng.total_tokens == S
+
+
+def test_kmixed_engine_errors():
+    kq = Q.MixedPrecisionMSEQuantizer(128, outlier_bits=3, regular_bits=2, n_outliers=32,
+                                      device=DEV)
+    eng = Q.QuashKVEngine(head_dim=128, value_bits=4, device=DEV, key_quantizer=kq)
+    x = torch.randn(1, 1, 8, 128, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="calibrate"):
+        eng.append(x, x)
+    with pytest.raises(ValueError, match="32 or 64 outliers"):
+        Q.QuashKVEngine(head_dim=128, device=DEV, key_quantizer=Q.MixedPrecisionMSEQuantizer(
+            128, outlier_bits=3, regular_bits=2, n_outliers=16, device=DEV))

@@ -89,6 +89,32 @@ def test_store_append_validation():
     assert st == N.QKV_E_UNSUPPORTED and "symmetric" in lib.qkv_last_error().decode()
 
 
+def test_kmixed_host_validation():
+    lib = N.lib()
+    perm = N.HostInts(list(range(128)))
+    bad = N.HostInts([0] * 128)
+    assert lib.qkv_kmixed_pack(16, 4, bad.ptr, 32, 16, 4, 4, None) == N.QKV_E_INVALID
+    assert "permutation" in lib.qkv_last_error().decode()
+    assert lib.qkv_kmixed_pack(16, 4, perm.ptr, 48, 16, 4, 4, None) == N.QKV_E_INVALID
+    assert lib.qkv_kmixed_unpack(16, 4, perm.ptr, 32, 4, 2, 16, None) == N.QKV_E_INVALID
+    # fp32 keys and other outlier counts are not covered by the fused append
+    ob, rb = N.HostFloats([-3, -2, -1, 0, 1, 2, 3]), N.HostFloats([-1, 0, 1])
+    assert lib.qkv_store_append_kmixed(N.QKV_F32, 16, 1, 1, 128, 16, 32, ob.ptr, rb.ptr, 16, 16,
+                                       64, 0, None) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append_kmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 16, ob.ptr, rb.ptr, 16,
+                                       16, 64, 0, None) == N.QKV_E_UNSUPPORTED
+    asym = N.HostFloats([-3, -2, -1, 0.1, 1, 2, 3])
+    assert lib.qkv_store_append_kmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 32, asym.ptr, rb.ptr, 16,
+                                       16, 64, 0, None) == N.QKV_E_UNSUPPORTED
+    # attention: only the MFMA path reads kmixed rows (capacity a multiple of 64)
+    oc = N.HostFloats([-4, -3, -2, -1, 1, 2, 3, 4])
+    rc, vc = N.HostFloats([-2, -1, 1, 2]), N.HostFloats([-2, -1, 1, 2])
+    st = lib.qkv_decode_attention_kmixed(256, 0, 256, 256, 256, 256, 96, 90, 1, 8, 8, 1, 128, 2,
+                                         256, 32, oc.ptr, rc.ptr, 256, vc.ptr, 0.1, 0, 256, 0,
+                                         256, 1 << 30, 1, None)
+    assert st == N.QKV_E_UNSUPPORTED and "multiple of 64" in lib.qkv_last_error().decode()
+
+
 def test_mips_host_validation():
     lib = N.lib()
     assert lib.qkv_mips_workspace_bytes(10, 80, 2, 10, 100) == -1      # dim

@@ -260,6 +260,35 @@ def test_mixed_golden(golden):
     assert torch.allclose(xh2, T(g["xhat2"]), rtol=1e-5, atol=1e-6)
 
 
+def test_attention_mixed_keys_pinned(golden):
+    """attention_mixed_keys (decompress-then-attend) against a scalar fp64 loop
+    of softmax(q k / sqrt(d)) v over keys from the golden-pinned
+    mixed_decompress, with GQA head h -> kv head h // G."""
+    cb = golden("codebooks")
+    g = torch.Generator().manual_seed(4)
+    B, H, G, Tn, d = 1, 2, 3, 9, 128
+    pi_k, pi_v = R.random_orthogonal(d, 42), R.random_orthogonal(d, 7)
+    out_idx = torch.arange(0, 128, 4)
+    kc = torch.randint(0, 4, (B, H, Tn, d), generator=g, dtype=torch.uint8)
+    kc[..., out_idx] = torch.randint(0, 8, (B, H, Tn, 32), generator=g, dtype=torch.uint8)
+    vc = torch.randint(0, 16, (B, H, Tn, d), generator=g, dtype=torch.uint8)
+    kn = torch.rand(B, H, Tn, generator=g) + 0.5
+    vn = torch.rand(B, H, Tn, generator=g) + 0.5
+    q = torch.randn(B, H * G, 1, d, generator=g)
+    c_out, c_reg, c_v = T(cb["c_d128_b3"]), T(cb["c_d128_b2"]), T(cb["c_d128_b4"])
+    got = R.attention_mixed_keys(q, kc, kn, vc, vn, pi_k, out_idx, c_out, c_reg, pi_v, c_v)
+    k = R.mixed_decompress(kc, kn, pi_k, out_idx, c_out, c_reg).double()
+    v = ((c_v[vc.long()] @ pi_v) * vn.unsqueeze(-1)).double()
+    ref = torch.zeros(B, H * G, 1, d, dtype=torch.float64)
+    for h in range(H * G):
+        kv = h // G
+        s = [float(q[0, h, 0].double() @ k[0, kv, t]) / math.sqrt(d) for t in range(Tn)]
+        m = max(s)
+        p = [math.exp(x - m) for x in s]
+        ref[0, h, 0] = sum(p[t] * v[0, kv, t] for t in range(Tn)) / sum(p)
+    assert torch.allclose(got.double(), ref, rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("d,bits", [(64, 3), (128, 3), (128, 4)])
 def test_index_golden(golden, d, bits):
     g, cb = golden("index"), golden("codebooks")
