@@ -198,22 +198,40 @@ __device__ __forceinline__ float from16(uint16_t h) {
 template <bool F16>
 __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
                          const float* __restrict__ rowsign, float pscale) {
-  for (int e = threadIdx.x; e < kFragN; e += blockDim.x) {
-    const int ln = e & 63, split = (e >> 6) & 1, s = (e >> 7) & 7, b = e >> 10;
+  // kThreads threads (every launch uses that block size); each takes NPT
+  // (block, k-step, lane) slots and writes both splits of each, with all of
+  // its Pi loads in flight before the first conversion
+  constexpr int NPT = kFragN / 2 / kThreads;
+  float4 p[NPT][2];
+  float sc[NPT];
+#pragma unroll
+  for (int x = 0; x < NPT; ++x) {
+    const int u = threadIdx.x + kThreads * x;
+    const int ln = u & 63, s = (u >> 6) & 7, b = u >> 9;
     const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
-    const float4 p0 = *reinterpret_cast<const float4*>(pi + j * kD + k0);
-    const float4 p1 = *reinterpret_cast<const float4*>(pi + j * kD + k0 + 4);
-    const float sc = (rowsign ? rowsign[j] : 1.f) * pscale;  // +-2^k: exact
-    const float p[8] = {p0.x * sc, p0.y * sc, p0.z * sc, p0.w * sc,
-                        p1.x * sc, p1.y * sc, p1.z * sc, p1.w * sc};
-    uint32_t h[8];
+    p[x][0] = *reinterpret_cast<const float4*>(pi + j * kD + k0);
+    p[x][1] = *reinterpret_cast<const float4*>(pi + j * kD + k0 + 4);
+    sc[x] = (rowsign ? rowsign[j] : 1.f) * pscale;  // +-2^k: exact
+  }
+#pragma unroll
+  for (int x = 0; x < NPT; ++x) {
+    const int u = threadIdx.x + kThreads * x;
+    const int ln = u & 63, s = (u >> 6) & 7, b = u >> 9;
+    const float v[8] = {p[x][0].x * sc[x], p[x][0].y * sc[x], p[x][0].z * sc[x],
+                        p[x][0].w * sc[x], p[x][1].x * sc[x], p[x][1].y * sc[x],
+                        p[x][1].z * sc[x], p[x][1].w * sc[x]};
+    uint32_t hi[8], lo[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint16_t hi = to16<F16>(p[i]);
-      h[i] = split == 0 ? hi : to16<F16>(p[i] - from16<F16>(hi));
+      const uint16_t h = to16<F16>(v[i]);
+      hi[i] = h;
+      lo[i] = to16<F16>(v[i] - from16<F16>(h));
     }
-    frag[e] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                         h[6] | (h[7] << 16));
+    const int e = ((b * 8 + s) * 2) * 64 + ln;
+    frag[e] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                         hi[6] | (hi[7] << 16));
+    frag[e + 64] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                              lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
   }
 }
 

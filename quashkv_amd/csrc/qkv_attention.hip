@@ -783,105 +783,155 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 
 // ------------------------------------------------------------ combine
 
-constexpr int kRowsC = 4;       // query rows merged per block
-constexpr int kSplitBatch = 8;  // split partials loaded per batch (one latency)
+constexpr int kRowsC = 4;       // query rows merged per block (many rows)
 
-// Merge the split partials of 4 consecutive query rows (of the B*Hkv*R rows):
-// log-sum-exp over splits, / max(l, 1e-8), un-rotate with Pi, store with the
-// GQA mapping (query head h = hkv * G + r / Q).  2*D threads.  Thread
-// (j, half) merges coordinate j of rows half and half + 2; thread (j4, kr)
-// then applies Pi rows [kr*D/8, (kr+1)*D/8) to output columns 4*j4..4*j4+3
-// from float4 loads issued at kernel entry, so the Pi and partial loads
-// share one memory round trip; eight k-range sums meet in LDS.
-template <int D>
+// Merge the split partials of RPB consecutive query rows (of the B*Hkv*R
+// rows): log-sum-exp over splits, / max(l, 1e-8), un-rotate with Pi, store
+// with the GQA mapping (query head h = hkv * G + r / Q).  2*D threads as
+// (j4, sp): coordinates 4 j4 .. 4 j4 + 3 and split lane sp of 8.
+//   1. lane sp merges splits sp, sp + 8, ... of every row (float4 partial
+//      loads, BATCH splits per row in flight);
+//   2. the 8 lane results meet in LDS: thread (j, half) finishes coordinate j
+//      of rows half, half + 2, ...;
+//   3. thread (j4, kr) applies Pi rows [kr D/8, (kr+1) D/8) to output columns
+//      4 j4 .. 4 j4 + 3 from float4 loads issued at kernel entry; the eight
+//      k-range sums meet in LDS.
+// RPB = 4 shares each Pi load among 4 rows; RPB = 1 spreads few rows with
+// many splits over more workgroups.
+template <int D, int RPB>
 __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_ml,
                                                         const float* __restrict__ pi,
                                                         int n_splits, int B, int Hkv, int R,
                                                         int Q, int Hq, void* __restrict__ out,
                                                         int out_dtype) {
-  constexpr int JG = D / 4, KPER = D / 8;
-  __shared__ float o[kRowsC][D];
-  __shared__ float4 red[8][kRowsC][JG];
+  constexpr int JG = D / 4, KPER = D / 8, NSP = 8;
+  constexpr int BATCH = RPB == 1 ? 8 : 2;  // splits per row per load round
+  __shared__ float o[RPB][D];
+  __shared__ float4 red[NSP][RPB][JG];
+  __shared__ float2 mls[NSP][RPB];
   const int tid = threadIdx.x;
   const int64_t nrows = int64_t(B) * Hkv * R;
-  const int64_t row0 = int64_t(blockIdx.x) * kRowsC;
-  const int nr = static_cast<int>(min<int64_t>(kRowsC, nrows - row0));
+  const int64_t row0 = int64_t(blockIdx.x) * RPB;
+  const int nr = static_cast<int>(min<int64_t>(RPB, nrows - row0));
 
-  const int j4 = tid % JG, kr = tid / JG;
+  const int j4 = tid % JG, kr = tid / JG;  // kr doubles as the split lane
   float4 pv[KPER];
   const float4* pk = reinterpret_cast<const float4*>(pi + int64_t(kr) * KPER * D) + j4;
 #pragma unroll
   for (int i = 0; i < KPER; ++i) pv[i] = pk[i * JG];
 
-  const int j = tid % D, half = tid / D;
+  {  // 1. per-lane merge
+    float M[RPB], L[RPB];
+    float4 a[RPB];
 #pragma unroll
-  for (int rr = 0; rr < kRowsC / 2; ++rr) {
-    const int r = half + 2 * rr;
-    float res = 0.f;
-    if (r < nr) {
-      const int64_t row = row0 + r;
-      float M = -INFINITY, L = 0.f, a = 0.f;  // running log-sum-exp merge
-      for (int s0 = 0; s0 < n_splits; s0 += kSplitBatch) {
-        float mb[kSplitBatch], lb[kSplitBatch], ob[kSplitBatch];
+    for (int r = 0; r < RPB; ++r) {
+      M[r] = -INFINITY;
+      L[r] = 0.f;
+      a[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float2* ml2 = reinterpret_cast<const float2*>(part_ml);
+    const float4* o4 = reinterpret_cast<const float4*>(part_o);
+    for (int s0 = kr; s0 < n_splits; s0 += NSP * BATCH) {
+      float2 mlb[BATCH][RPB];
+      float4 ob[BATCH][RPB];
 #pragma unroll
-        for (int x = 0; x < kSplitBatch; ++x) {
-          const int sidx = s0 + x;
-          const bool ok = sidx < n_splits;
-          const int64_t base = (ok ? sidx : 0) * nrows + row;
-          mb[x] = ok ? part_ml[base * 2] : -INFINITY;
-          lb[x] = ok ? part_ml[base * 2 + 1] : 0.f;
-          ob[x] = ok ? part_o[base * D + j] : 0.f;
-        }
-        float bm = M;
+      for (int x = 0; x < BATCH; ++x) {
+        const int sidx = s0 + NSP * x;
 #pragma unroll
-        for (int x = 0; x < kSplitBatch; ++x) bm = fmaxf(bm, mb[x]);
-        if (bm != -INFINITY) {
-          const float c = (M == -INFINITY) ? 0.f : expf(M - bm);
-          L *= c;
-          a *= c;
-#pragma unroll
-          for (int x = 0; x < kSplitBatch; ++x) {
-            if (mb[x] != -INFINITY) {
-              const float w = expf(mb[x] - bm);
-              L = fmaf(w, lb[x], L);
-              a = fmaf(w, ob[x], a);
-            }
-          }
-          M = bm;
+        for (int r = 0; r < RPB; ++r) {
+          const bool ok = sidx < n_splits && r < nr;
+          const int64_t base = int64_t(ok ? sidx : 0) * nrows + (ok ? row0 + r : 0);
+          mlb[x][r] = ok ? ml2[base] : make_float2(-INFINITY, 0.f);
+          ob[x][r] = ok ? o4[base * JG + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
       }
-      res = a / fmaxf(L, 1e-8f);
+#pragma unroll
+      for (int r = 0; r < RPB; ++r) {
+        float bm = M[r];
+#pragma unroll
+        for (int x = 0; x < BATCH; ++x) bm = fmaxf(bm, mlb[x][r].x);
+        if (bm != -INFINITY) {
+          const float c = (M[r] == -INFINITY) ? 0.f : expf(M[r] - bm);
+          L[r] *= c;
+          a[r].x *= c;
+          a[r].y *= c;
+          a[r].z *= c;
+          a[r].w *= c;
+#pragma unroll
+          for (int x = 0; x < BATCH; ++x) {
+            if (mlb[x][r].x != -INFINITY) {
+              const float w = expf(mlb[x][r].x - bm);
+              L[r] = fmaf(w, mlb[x][r].y, L[r]);
+              a[r].x = fmaf(w, ob[x][r].x, a[r].x);
+              a[r].y = fmaf(w, ob[x][r].y, a[r].y);
+              a[r].z = fmaf(w, ob[x][r].z, a[r].z);
+              a[r].w = fmaf(w, ob[x][r].w, a[r].w);
+            }
+          }
+          M[r] = bm;
+        }
+      }
     }
-    o[r][j] = res;
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) {
+      red[kr][r][j4] = a[r];
+      if (j4 == 0) mls[kr][r] = make_float2(M[r], L[r]);
+    }
   }
   __syncthreads();
-  float4 acc[kRowsC];
+  const int j = tid % D, half = tid / D;
+  {  // 2. merge the lanes
 #pragma unroll
-  for (int r = 0; r < kRowsC; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int rr = 0; rr < (RPB + 1) / 2; ++rr) {
+      const int r = half + 2 * rr;
+      if (r < RPB) {
+        float mx = -INFINITY;
 #pragma unroll
-  for (int i = 0; i < KPER; ++i) {
+        for (int k = 0; k < NSP; ++k) mx = fmaxf(mx, mls[k][r].x);
+        float L = 0.f, a = 0.f;
+        if (mx != -INFINITY) {
+          const float* redf = reinterpret_cast<const float*>(&red[0][r][0]);
 #pragma unroll
-    for (int r = 0; r < kRowsC; ++r) {
-      const float ov = o[r][kr * KPER + i];
-      acc[r].x = fmaf(ov, pv[i].x, acc[r].x);
-      acc[r].y = fmaf(ov, pv[i].y, acc[r].y);
-      acc[r].z = fmaf(ov, pv[i].z, acc[r].z);
-      acc[r].w = fmaf(ov, pv[i].w, acc[r].w);
+          for (int k = 0; k < NSP; ++k) {
+            const float w = mls[k][r].x == -INFINITY ? 0.f : expf(mls[k][r].x - mx);
+            L = fmaf(w, mls[k][r].y, L);
+            a = fmaf(w, redf[k * RPB * D + j], a);
+          }
+        }
+        o[r][j] = r < nr ? a / fmaxf(L, 1e-8f) : 0.f;
+      }
     }
   }
+  __syncthreads();
+  {  // 3. un-rotate
+    float4 acc[RPB];
 #pragma unroll
-  for (int r = 0; r < kRowsC; ++r) red[kr][r][j4] = acc[r];
+    for (int r = 0; r < RPB; ++r) acc[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < KPER; ++i) {
+#pragma unroll
+      for (int r = 0; r < RPB; ++r) {
+        const float ov = o[r][kr * KPER + i];
+        acc[r].x = fmaf(ov, pv[i].x, acc[r].x);
+        acc[r].y = fmaf(ov, pv[i].y, acc[r].y);
+        acc[r].z = fmaf(ov, pv[i].z, acc[r].z);
+        acc[r].w = fmaf(ov, pv[i].w, acc[r].w);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPB; ++r) red[kr][r][j4] = acc[r];
+  }
   __syncthreads();
   const int G = Hq / Hkv;
   const float* redf = reinterpret_cast<const float*>(&red[0][0][0]);
 #pragma unroll
-  for (int rr = 0; rr < kRowsC / 2; ++rr) {
+  for (int rr = 0; rr < (RPB + 1) / 2; ++rr) {
     const int r = half + 2 * rr;
     if (r < nr) {
       float v = 0.f;
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v += redf[(k * kRowsC + r) * D + j];
+      for (int k = 0; k < NSP; ++k) v += redf[(k * RPB + r) * D + j];
       const int64_t row = row0 + r;  // ((b * Hkv) + hkv) * R + r
       const int rq = static_cast<int>(row % R);
       const int hkv = static_cast<int>((row / R) % Hkv);
@@ -1520,14 +1570,22 @@ extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t
   const int R = (Hq / Hkv) * Q;
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   auto s = static_cast<hipStream_t>(stream);
-  const dim3 cgrid(static_cast<int>((int64_t(B) * Hkv * R + kRowsC - 1) / kRowsC));
+  const int64_t nrows = int64_t(B) * Hkv * R;
+  // few rows: one per workgroup (more workgroups over the splits); many rows:
+  // four per workgroup (each Pi load serves four)
+  const bool wide = nrows < int64_t(kRowsC) * qkv_num_cus();
+  const dim3 cgrid(static_cast<int>(wide ? nrows : (nrows + kRowsC - 1) / kRowsC));
   const float* po = at<float>(workspace, L.po);
   const float* pml = at<float>(workspace, L.pml);
   switch (d) {
 #define QKV_CASE(DD)                                                                          \
   case DD:                                                                                    \
-    hipLaunchKernelGGL(combine_kernel<DD>, cgrid, dim3(2 * DD), 0, s, po, pml, pi, n_splits,  \
-                       B, Hkv, R, Q, Hq, out, out_dtype);                                     \
+    if (wide)                                                                                 \
+      hipLaunchKernelGGL((combine_kernel<DD, 1>), cgrid, dim3(2 * DD), 0, s, po, pml, pi,     \
+                         n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                         \
+    else                                                                                      \
+      hipLaunchKernelGGL((combine_kernel<DD, kRowsC>), cgrid, dim3(2 * DD), 0, s, po, pml,    \
+                         pi, n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                     \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
