@@ -340,12 +340,15 @@ __device__ __forceinline__ void mfma_settle() {
 }
 
 // Query operands for the score MFMA.  One workgroup per (b, kv head, chunk of
-// 4 rows).  Row bit p of a K row (plane-major) has weight W_p:
+// 4 rows).  Row bit p of a K row (plane-major, D bits per plane) has weight W_p:
 //   MSE plane r, coordinate j:  2 kg[r] q~_j
 //   QJL plane,   coordinate j:  2 alpha |q~_j| S_j
-// and Z_p = round(W_p 2^Fq / s_i) with s_i = 2^i (i < 7) or -128 (i = 7) the
-// byte value of a set bit after the mask (0x01010101 << i).  Z has 28 bits:
-// digits d0..d2 in [0, 127] and a signed top digit d3, Z = sum_v 2^(7v) d_v.
+// (mixed-precision rows: per-slot coefficients, see Tables).  The operand
+// holds Z_p = round(W_p 2^Fq / 2^i), negated for i = 7 (a set bit masks to
+// the byte value -128), where i = p % 8 is the bit's place in its byte, as
+// signed base-256 digits; |Z| < 2^30.  Fq comes from the bound
+// max |W| <= 2 max(kg, alpha) ||q|| (Pi is orthogonal), so no reduction over
+// the rotated row stands between the rotation and the digits.
 // Operand register layout: aq[(bhc * NU + u) * 64 + lane] (4 dwords), lane
 // (m = 4 row + digit, g = lane / 16); byte beta of dword e <-> row bit
 // 32 (g DPL + u / 2) + 8 beta + 4 (u % 2) + e.
@@ -353,6 +356,9 @@ __device__ __forceinline__ void mfma_settle() {
 // 2 kg[s] q~_j), then the QJL plane.  The decode rows have NPL = mbits + 1
 // (mbits <= 2: the subsets are the single bits); the search index also uses
 // NPL = 5 for 3-bit MSE codes (three bits and their parity).
+// Thread (j, half) rotates coordinate j of all rows over half of k, then
+// turns coordinate j of rows half and half + 2 into digit bytes, scattered
+// into an LDS image of the operands that is copied out whole.
 template <int D, int NPL>
 __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, int q_dtype,
                                                     const float* __restrict__ pi,
@@ -366,12 +372,14 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   constexpr int KRB = NPL * D / 8;
   constexpr int DPL = KRB / 16;
   constexpr int NU = 2 * DPL;
+  constexpr int NW = NU * 64 * 4;  // operand dwords per chunk
   static_assert(D == 128, "one thread pair per output coordinate");
+  static_assert(kRowsM == 4, "two rows per thread");
   __shared__ float qs[kRowsM][D];
   __shared__ float part[2][kRowsM][D];
-  __shared__ float qt[kRowsM][D];
-  __shared__ float wv[kRowsM][D];
-  __shared__ int fqs[kRowsM];
+  __shared__ float nqs[kRowsM];
+  __shared__ uint32_t stage[NW];
+  __shared__ float red[4][2][2];  // [wave][row of the wave's half][sq, sw]
 
   const int tid = threadIdx.x;
   const int G = Hq / Hkv;
@@ -410,6 +418,12 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
     qs[i / D][i % D] = qv[x];
   }
   __syncthreads();
+  {  // ||q_r||^2: wave w sums row w
+    const int wave = tid >> 6, lane = tid & 63;
+    const float a = qs[wave][2 * lane], c = qs[wave][2 * lane + 1];
+    const float ss = qkv_wave_sum(fmaf(a, a, c * c));
+    if (lane == 0) nqs[wave] = ss;
+  }
   {  // q~_j = sum_k q_k Pi[j][k], this thread's half of k for all rows
     float acc[kRowsM] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -426,83 +440,88 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
 #pragma unroll
     for (int r = 0; r < kRowsM; ++r) part[half][r][j] = acc[r];
   }
+  float kgmax = alpha;
+  if (tb.kmix) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
+    kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
+  } else {
+#pragma unroll
+    for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+  }
   __syncthreads();
-  for (int i = tid; i < kRowsM * D; i += 256) {
-    const int r = i / D, jj = i - r * D;  // jj == j: 256 threads, D = 128
-    const float v = part[0][r][jj] + part[1][r][jj];
+
+  uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
+  // digit bytes of weight W at row bit p of row r
+  auto put = [&](int p, float W, int fq, int r) {
+    const int i = p & 7;
+    int Z = static_cast<int>(rintf(ldexpf(W, fq - i)));
+    if (i == 7) Z = -Z;
+    const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+    const int w32 = p >> 5, g = w32 / DPL;
+    const int u = 2 * (w32 - g * DPL) + (i >> 2), e = i & 3, beta = (p >> 3) & 3;
+    const int base = ((u * 64 + 16 * g + 4 * r) * 4 + e) * 4 + beta;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) sb[base + 16 * v] = static_cast<uint8_t>(dg >> (8 * v));
+  };
+  float csq[2], csw[2];
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = half + 2 * rr;
+    const float v = part[0][r][j] + part[1][r][j];
     const float w = alpha * fabsf(v) * sgn;
-    qt[r][jj] = v;
-    wv[r][jj] = w;
     if (qw != nullptr && r < nr) {  // q~ and w for the VALU kernel, qw[b][hkv][row][2][D]
       float* dst = qw + (int64_t(bh) * R + r0 + r) * 2 * D;
-      dst[jj] = v;
-      dst[D + jj] = w;
+      dst[j] = v;
+      dst[D + j] = w;
     }
-  }
-  __syncthreads();
-  {  // per-row scale exponent and constant (one wave per row)
-    const int wave = tid >> 6, lane = tid & 63;
-    float kgmax = 0.f;
+    const float wmax = 2.f * kgmax * sqrtf(nqs[r]);
+    int ex = 0;
+    if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
+    const int fq = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
     if (tb.kmix) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
-      kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
+      const bool outl = j < tb.n_out;
+      csq[rr] = (outl ? tb.kco : tb.kcr) * v;
+      put(j, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v, fq, r);
+      put(D + j, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v, fq, r);
+      if (j < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers only
+        put(2 * D + j, outl ? 2.f * tb.kgo[2] * v : 0.f, fq, r);
+        put(2 * D + 64 + j, outl ? 2.f * tb.kgo[3] * v : 0.f, fq, r);
+      }
     } else {
+      csq[rr] = v;
 #pragma unroll
-      for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+      for (int pl = 0; pl < MB; ++pl) put(pl * D + j, 2.f * tb.kg[pl] * v, fq, r);
+      put(MB * D + j, 2.f * w, fq, r);
     }
-    float mq = 0.f, mw = 0.f, sq = 0.f, sw = 0.f;
-    for (int jj = lane; jj < D; jj += 64) {
-      mq = fmaxf(mq, fabsf(qt[wave][jj]));
-      mw = fmaxf(mw, fabsf(wv[wave][jj]));
-      sq += tb.kmix ? (jj < tb.n_out ? tb.kco : tb.kcr) * qt[wave][jj] : qt[wave][jj];
-      sw += wv[wave][jj];
-    }
-    mq = qkv_wave_max(mq);
-    mw = qkv_wave_max(mw);
-    sq = qkv_wave_sum(sq);
-    sw = qkv_wave_sum(sw);
-    if (lane == 0) {
-      const float wmax = 2.f * fmaxf(kgmax * mq, mw);
-      int e = 0;
-      if (wmax > 0.f) frexpf(wmax, &e);  // wmax = f 2^e, f in [0.5, 1)
-      const int fq = wmax > 0.f ? 30 - e : 0;  // |Z| < 2^30
-      fqs[wave] = fq;
-      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
-      rowc[(int64_t(bhc) * kRowsM + wave) * 2 + 1] = ldexpf(1.f, -fq);
-    }
+    csw[rr] = w;
   }
-  __syncthreads();
-  for (int idx = tid; idx < NU * 64 * 4; idx += 256) {
-    const int e = idx & 3, ln = (idx >> 2) & 63, u = idx >> 8;
-    const int m = ln & 15, g = ln >> 4;
-    const int qrow = m >> 2, v = m & 3;
-    const int i = 4 * (u & 1) + e;
-    uint32_t word = 0;
-    if (qrow < nr) {
+  {  // row constants: sums over j (a wave holds 64 j of one half)
+    const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-      for (int beta = 0; beta < 4; ++beta) {
-        const int p = 32 * (g * DPL + (u >> 1)) + 8 * beta + i;
-        const int region = p / D, jj = p - region * D;
-        float W;
-        if (tb.kmix) {
-          if (region < 2) {
-            W = 2.f * (jj < tb.n_out ? tb.kgo[region] : tb.kgr[region]) * qt[qrow][jj];
-          } else {
-            const int c = jj & 63;  // b2 (bits 0..63) or parity (bits 64..127) of c
-            W = c < tb.n_out ? 2.f * tb.kgo[jj < 64 ? 2 : 3] * qt[qrow][c] : 0.f;
-          }
-        } else {
-          W = region < MB ? 2.f * tb.kg[region] * qt[qrow][jj] : 2.f * wv[qrow][jj];
-        }
-        float zf = ldexpf(W, fqs[qrow] - i);
-        if (i == 7) zf = -zf;
-        const int Z = static_cast<int>(rintf(zf));
-        const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
-        word |= ((dg >> (8 * v)) & 0xffu) << (8 * beta);
+    for (int rr = 0; rr < 2; ++rr) {
+      const float a = qkv_wave_sum(csq[rr]);
+      const float c = qkv_wave_sum(csw[rr]);
+      if (lane == 0) {
+        red[wave][rr][0] = a;
+        red[wave][rr][1] = c;
       }
     }
-    aq[(int64_t(bhc) * NU + u) * 64 + ln][e] = static_cast<int>(word);
+  }
+  __syncthreads();
+  uint32_t* aqw = reinterpret_cast<uint32_t*>(aq) + int64_t(bhc) * NW;
+#pragma unroll
+  for (int x = 0; x < NW / 256; ++x) aqw[tid + 256 * x] = stage[tid + 256 * x];
+  if (tid < kRowsM) {  // row r = tid: half r % 2 (waves 2h, 2h + 1), slot r / 2
+    const int r = tid, h = r & 1, rr = r >> 1;
+    const float sq = red[2 * h][rr][0] + red[2 * h + 1][rr][0];
+    const float sw = red[2 * h][rr][1] + red[2 * h + 1][rr][1];
+    const float wmax = 2.f * kgmax * sqrtf(nqs[r]);
+    int ex = 0;
+    if (wmax > 0.f) frexpf(wmax, &ex);
+    const int fq = wmax > 0.f ? 30 - ex : 0;
+    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
+    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 1] = ldexpf(1.f, -fq);
   }
 }
 
