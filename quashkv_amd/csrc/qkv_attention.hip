@@ -351,14 +351,17 @@ __device__ __forceinline__ void mfma_settle() {
 // the rotated row stands between the rotation and the digits.
 // Operand register layout: aq[(bhc * NU + u) * 64 + lane] (4 dwords), lane
 // (m = 4 row + digit, g = lane / 16); byte beta of dword e <-> row bit
-// 32 (g DPL + u / 2) + 8 beta + 4 (u % 2) + e.
+//   D = 128:  32 (g DPL + u / 2) + 8 beta + 4 (u % 2) + e   (NU = 2 DPL)
+//   D = 64:   32 (2 u + g / 2) + 8 beta + 4 (g % 2) + e      (NU = NPL)
+// i.e. the score kernel's lane group g reads row dwords g DPL .. (D = 128) or
+// 2 u + g / 2 (D = 64) and masks nibble half u % 2 (D = 128) or g % 2.
 // NPL planes per row: NPL - 1 MSE planes (odd bit subsets s, weight
 // 2 kg[s] q~_j), then the QJL plane.  The decode rows have NPL = mbits + 1
 // (mbits <= 2: the subsets are the single bits); the search index also uses
 // NPL = 5 for 3-bit MSE codes (three bits and their parity).
-// Thread (j, half) rotates coordinate j of all rows over half of k, then
-// turns coordinate j of rows half and half + 2 into digit bytes, scattered
-// into an LDS image of the operands that is copied out whole.
+// Thread (j, part) rotates coordinate j of all rows over one of 256 / D parts
+// of k, then turns coordinate j of rows part, part + 256 / D, ... into digit
+// bytes, scattered into an LDS image of the operands that is copied out whole.
 template <int D, int NPL>
 __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, int q_dtype,
                                                     const float* __restrict__ pi,
@@ -371,15 +374,20 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   constexpr int MB = NPL - 1;  // weighted MSE planes
   constexpr int KRB = NPL * D / 8;
   constexpr int DPL = KRB / 16;
-  constexpr int NU = 2 * DPL;
-  constexpr int NW = NU * 64 * 4;  // operand dwords per chunk
-  static_assert(D == 128, "one thread pair per output coordinate");
-  static_assert(kRowsM == 4, "two rows per thread");
+  constexpr int NU = KRB / 8;        // score MFMAs per 16 tokens
+  constexpr int NW = NU * 64 * 4;    // operand dwords per chunk
+  constexpr int NPART = 256 / D;     // threads per coordinate
+  constexpr int KP = D / NPART;      // k per thread in the rotation
+  constexpr int RPT = kRowsM / NPART;  // rows per thread in the digit phase
+  constexpr int WPP = D / 64;        // waves per part
+  static_assert(D == 128 || D == 64, "64- or 128-dim rows");
+  static_assert(D == 64 || KRB % 16 == 0, "128-dim rows split into 4 lane groups");
+  static_assert(kRowsM == 4, "rows per chunk");
   __shared__ float qs[kRowsM][D];
-  __shared__ float part[2][kRowsM][D];
+  __shared__ float part[NPART][kRowsM][D];
   __shared__ float nqs[kRowsM];
   __shared__ uint32_t stage[NW];
-  __shared__ float red[4][2][2];  // [wave][row of the wave's half][sq, sw]
+  __shared__ float red[4][RPT][2];  // [wave][row slot][sq, sw]
 
   const int tid = threadIdx.x;
   const int G = Hq / Hkv;
@@ -389,13 +397,13 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   const int hkv = bh % Hkv, b = bh / Hkv;
   const int r0 = chunk * kRowsM;
   const int nr = min(kRowsM, R - r0);
-  // this thread's half row of Pi: all 16 float4 loads issued before use
+  // this thread's part of a Pi row: all float4 loads issued before use
   const int j = tid % D, half = tid / D;
-  float4 prow[D / 8];
+  float4 prow[KP / 4];
   {
-    const float4* src = reinterpret_cast<const float4*>(pi + int64_t(j) * D + half * (D / 2));
+    const float4* src = reinterpret_cast<const float4*>(pi + int64_t(j) * D + half * KP);
 #pragma unroll
-    for (int k4 = 0; k4 < D / 8; ++k4) prow[k4] = src[k4];
+    for (int k4 = 0; k4 < KP / 4; ++k4) prow[k4] = src[k4];
   }
   float qv[kRowsM * D / 256];
 #pragma unroll
@@ -420,15 +428,20 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   __syncthreads();
   {  // ||q_r||^2: wave w sums row w
     const int wave = tid >> 6, lane = tid & 63;
-    const float a = qs[wave][2 * lane], c = qs[wave][2 * lane + 1];
-    const float ss = qkv_wave_sum(fmaf(a, a, c * c));
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < D / 64; ++c) {
+      const float a = qs[wave][lane + 64 * c];
+      ss = fmaf(a, a, ss);
+    }
+    ss = qkv_wave_sum(ss);
     if (lane == 0) nqs[wave] = ss;
   }
-  {  // q~_j = sum_k q_k Pi[j][k], this thread's half of k for all rows
+  {  // q~_j = sum_k q_k Pi[j][k], this thread's part of k for all rows
     float acc[kRowsM] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k4 = 0; k4 < D / 8; ++k4) {
-      const int k = half * (D / 2) + 4 * k4;
+    for (int k4 = 0; k4 < KP / 4; ++k4) {
+      const int k = half * KP + 4 * k4;
 #pragma unroll
       for (int r = 0; r < kRowsM; ++r) {
         acc[r] = fmaf(qs[r][k], prow[k4].x, acc[r]);
@@ -458,17 +471,26 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
     int Z = static_cast<int>(rintf(ldexpf(W, fq - i)));
     if (i == 7) Z = -Z;
     const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
-    const int w32 = p >> 5, g = w32 / DPL;
-    const int u = 2 * (w32 - g * DPL) + (i >> 2), e = i & 3, beta = (p >> 3) & 3;
+    const int w32 = p >> 5, e = i & 3, beta = (p >> 3) & 3;
+    int g, u;
+    if constexpr (D == 128) {
+      g = w32 / DPL;
+      u = 2 * (w32 - g * DPL) + (i >> 2);
+    } else {
+      g = 2 * (w32 & 1) + (i >> 2);
+      u = w32 >> 1;
+    }
     const int base = ((u * 64 + 16 * g + 4 * r) * 4 + e) * 4 + beta;
 #pragma unroll
     for (int v = 0; v < 4; ++v) sb[base + 16 * v] = static_cast<uint8_t>(dg >> (8 * v));
   };
-  float csq[2], csw[2];
+  float csq[RPT], csw[RPT];
 #pragma unroll
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = half + 2 * rr;
-    const float v = part[0][r][j] + part[1][r][j];
+  for (int rr = 0; rr < RPT; ++rr) {
+    const int r = half + NPART * rr;
+    float v = 0.f;
+#pragma unroll
+    for (int pp = 0; pp < NPART; ++pp) v += part[pp][r][j];
     const float w = alpha * fabsf(v) * sgn;
     if (qw != nullptr && r < nr) {  // q~ and w for the VALU kernel, qw[b][hkv][row][2][D]
       float* dst = qw + (int64_t(bh) * R + r0 + r) * 2 * D;
@@ -479,12 +501,12 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
     int ex = 0;
     if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
     const int fq = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
-    if (tb.kmix) {
+    if (D == 128 && tb.kmix) {
       const bool outl = j < tb.n_out;
       csq[rr] = (outl ? tb.kco : tb.kcr) * v;
       put(j, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v, fq, r);
       put(D + j, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v, fq, r);
-      if (j < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers only
+      if (NPL == 3 && j < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers only
         put(2 * D + j, outl ? 2.f * tb.kgo[2] * v : 0.f, fq, r);
         put(2 * D + 64 + j, outl ? 2.f * tb.kgo[3] * v : 0.f, fq, r);
       }
@@ -496,10 +518,10 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
     }
     csw[rr] = w;
   }
-  {  // row constants: sums over j (a wave holds 64 j of one half)
+  {  // row constants: sums over j (a wave holds 64 j of one part)
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < RPT; ++rr) {
       const float a = qkv_wave_sum(csq[rr]);
       const float c = qkv_wave_sum(csw[rr]);
       if (lane == 0) {
@@ -512,10 +534,14 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
   uint32_t* aqw = reinterpret_cast<uint32_t*>(aq) + int64_t(bhc) * NW;
 #pragma unroll
   for (int x = 0; x < NW / 256; ++x) aqw[tid + 256 * x] = stage[tid + 256 * x];
-  if (tid < kRowsM) {  // row r = tid: half r % 2 (waves 2h, 2h + 1), slot r / 2
-    const int r = tid, h = r & 1, rr = r >> 1;
-    const float sq = red[2 * h][rr][0] + red[2 * h + 1][rr][0];
-    const float sw = red[2 * h][rr][1] + red[2 * h + 1][rr][1];
+  if (tid < kRowsM) {  // row r = tid: part r % NPART (waves WPP h ..), slot r / NPART
+    const int r = tid, h = r % NPART, rr = r / NPART;
+    float sq = 0.f, sw = 0.f;
+#pragma unroll
+    for (int w = 0; w < WPP; ++w) {
+      sq += red[WPP * h + w][rr][0];
+      sw += red[WPP * h + w][rr][1];
+    }
     const float wmax = 2.f * kgmax * sqrtf(nqs[r]);
     int ex = 0;
     if (wmax > 0.f) frexpf(wmax, &ex);
@@ -535,11 +561,15 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     int64_t T, int Hkv, int R, int Q, int chunks, float scale, int causal, int64_t split_len,
     Tables tb, float* __restrict__ part_o, float* __restrict__ part_ml) {
   constexpr int KRB = (MB + 1) * D / 8;  // K row bytes
-  constexpr int DPL = KRB / 16;          // row dwords per lane group
-  constexpr int NU = 2 * DPL;            // score MFMAs per 16 tokens
+  constexpr int DPL = KRB / 16;          // row dwords per lane group (D = 128)
+  constexpr int NU = KRB / 8;            // score MFMAs per 16 tokens
+  // row dwords each lane loads per token: its group's DPL (D = 128), or
+  // dword 2 u + g / 2 for each MFMA u (D = 64; nibble half g % 2)
+  constexpr int NLD = D == 128 ? DPL : NU;
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int MTW = D / 64;            // 16-coordinate tiles per wave
-  static_assert(KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
+  static_assert(D == 128 || D == 64, "64- or 128-dim rows");
+  static_assert(D == 64 || KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
   static_assert(D % 64 == 0, "value tiles split over 4 waves");
 
   // scores [tile][row][64]; rewritten in place as value-MFMA digits
@@ -593,19 +623,21 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
   const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
   constexpr int PD1 = 2;
-  uint32_t kd[PD1][4][DPL];
+  uint32_t kd[PD1][4][NLD];
   float kn[PD1][4], vv[PD1][4];
   // Tokens past the split end are read too (masked when scored): the store
   // capacity is a multiple of 64 and >= T, so whole 64-token tiles of the
   // split stay inside it.  Addresses are then linear in the tile index.
-  const uint32_t* krow0 = reinterpret_cast<const uint32_t*>(kbs + ln * KRB) + lg * DPL;
+  const uint32_t* krow0 =
+      reinterpret_cast<const uint32_t*>(kbs + ln * KRB) + (D == 128 ? lg * DPL : (lg >> 1));
+  const int lsh = 4 * (lg & 1);  // D = 64: this lane group's nibble half
   auto load1 = [&](int slot, int tile) {
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const int t16 = tile * 64 + sub * 16;
       const uint32_t* krow = krow0 + t16 * (KRB / 4);
 #pragma unroll
-      for (int x = 0; x < DPL; ++x) kd[slot][sub][x] = krow[x];
+      for (int x = 0; x < NLD; ++x) kd[slot][sub][x] = krow[D == 128 ? x : 2 * x];
       kn[slot][sub] = knbs[t16 + ln];
       vv[slot][sub] = vnbs[t16 + ln];
     }
@@ -617,10 +649,10 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     for (int sub = 0; sub < 4; ++sub) acc[sub] = qkv_v4i{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
-      const int sh = 4 * (u & 1);
+      const int sh = D == 128 ? 4 * (u & 1) : lsh;
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
-        const uint32_t x = kd[slot][sub][u >> 1];
+        const uint32_t x = kd[slot][sub][D == 128 ? u >> 1 : u];
         qkv_v4i bo;
         bo[0] = static_cast<int>(x & (0x01010101u << sh));
         bo[1] = static_cast<int>(x & (0x02020202u << sh));
@@ -1327,7 +1359,8 @@ int64_t mfma_split_len(int64_t T, int n_splits) {
 }
 
 bool use_mfma(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
-  return tb.mfma_ok && d == 128 && t_stride % 64 == 0 && mfma_split_len(T, n_splits) <= kSplitMax;
+  return tb.mfma_ok && (d == 128 || d == 64) && t_stride % 64 == 0 &&
+         mfma_split_len(T, n_splits) <= kSplitMax;
 }
 
 int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t n_splits,
@@ -1439,18 +1472,20 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
   auto s = static_cast<hipStream_t>(stream);
-  if (tb.mfma_ok && d == 128) {
+  if (tb.mfma_ok && (d == 128 || d == 64)) {
     // MFMA query operands; the same kernel writes q~ and w for the VALU kernel
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const dim3 grid(B * Hkv * chunks);
-    if (kbits == 2)
-      hipLaunchKernelGGL((prepare_mfma<128, 3>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
-                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
-                         at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
-    else
-      hipLaunchKernelGGL((prepare_mfma<128, 2>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,
-                         qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
-                         at<float>(workspace, L.rowc), at<float>(workspace, L.qw));
+#define QKV_PREP(DD, NPLV)                                                                     \
+  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,  \
+                     qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),      \
+                     at<float>(workspace, L.rowc), at<float>(workspace, L.qw))
+    if (d == 128) {
+      if (kbits == 2) QKV_PREP(128, 3); else QKV_PREP(128, 2);
+    } else {
+      if (kbits == 2) QKV_PREP(64, 3); else QKV_PREP(64, 2);
+    }
+#undef QKV_PREP
     QKV_LAUNCHED();
     return QKV_OK;
   }
@@ -1539,21 +1574,28 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
     const dim3 grid(n_splits, Hkv * chunks, B);
     const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
     const float* rowc = at<float>(workspace, L.rowc);
-#define QKV_MF(MB, VB)                                                                       \
-  hipLaunchKernelGGL((split_mfma<128, MB, VB>), grid, dim3(256),                           \
+#define QKV_MF(DD, MB, VB)                                                                   \
+  hipLaunchKernelGGL((split_mfma<DD, MB, VB>), grid, dim3(256),                            \
                      static_cast<uint32_t>(mfma_smem_bytes(split_len)), s, aq, rowc, kstore,  \
                      knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, scale, causal,    \
                      split_len, tb, po, pml)
-    switch (kbits * 10 + vbits) {
-      case 11: QKV_MF(1, 1); break;
-      case 12: QKV_MF(1, 2); break;
-      case 13: QKV_MF(1, 3); break;
-      case 14: QKV_MF(1, 4); break;
-      case 21: QKV_MF(2, 1); break;
-      case 22: QKV_MF(2, 2); break;
-      case 23: QKV_MF(2, 3); break;
-      case 24: QKV_MF(2, 4); break;
+#define QKV_MFD(DD)                           \
+  switch (kbits * 10 + vbits) {               \
+    case 11: QKV_MF(DD, 1, 1); break;         \
+    case 12: QKV_MF(DD, 1, 2); break;         \
+    case 13: QKV_MF(DD, 1, 3); break;         \
+    case 14: QKV_MF(DD, 1, 4); break;         \
+    case 21: QKV_MF(DD, 2, 1); break;         \
+    case 22: QKV_MF(DD, 2, 2); break;         \
+    case 23: QKV_MF(DD, 2, 3); break;         \
+    case 24: QKV_MF(DD, 2, 4); break;         \
+  }
+    if (d == 128) {
+      QKV_MFD(128)
+    } else {
+      QKV_MFD(64)
     }
+#undef QKV_MFD
 #undef QKV_MF
     QKV_LAUNCHED();
     return QKV_OK;

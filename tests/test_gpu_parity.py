@@ -13,6 +13,7 @@ import quashkv_amd as Q
 from quashkv_amd import _native as N
 from quashkv_amd import kernels as K
 from quashkv_amd.quantizer import compress_into
+from quashkv_amd.store import KVStore
 from oracle import ref_math as R
 
 pytestmark = pytest.mark.gpu
@@ -453,10 +454,56 @@ def test_attention_split_invariance_full_size():
         assert_close(o[:4], ref, rel=2e-5, cos=0.999999)
 
 
+def test_attention_d64_cfg2_shape_splits_and_paths():
+    """cfg2 shape (B=16, Hq=14, Hkv=2, d=64, T=2048, fp16 K/V with log-normal
+    token norms): the 64-dim MFMA kernel at several split counts agrees with
+    itself, with the VALU kernel (forced by a 32-multiple capacity), and with
+    the oracle on a slice of the batch."""
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    B, Hkv, G, d, T_ = 16, 2, 7, 64, 2048
+    k = torch.randn(B, Hkv, T_, d, generator=gen) * torch.exp(0.5 * torch.randn(B, Hkv, T_, 1, generator=gen))
+    v = torch.randn(B, Hkv, T_, d, generator=gen) * torch.exp(0.5 * torch.randn(B, Hkv, T_, 1, generator=gen))
+    q = torch.randn(B, Hkv * G, 1, d, generator=gen).to(DEV, torch.float16)
+    eng = Q.QuashKVEngine(head_dim=d, seed=42, device=DEV)
+    eng.append(k.to(DEV, torch.float16), v.to(DEV, torch.float16))
+    st = eng._store
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    kh, vh = kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host
+    kc_h, vc_h = N.HostFloats(kh), N.HostFloats(vh)
+    L = N.lib()
+    outs = []
+    for ns in (1, 2, 5, 16):
+        assert L.qkv_attention_path(d, 2, 3, kc_h.ptr, vc_h.ptr, st.capacity, T_, ns) == 1
+        outs.append(K.attention_store(q, st, T_, kq.mse_quantizer.Pi, kh, vh, kq.S, kq.qjl_scale,
+                                      n_splits=ns))
+    for o in outs[1:]:
+        assert_close(o, outs[0], rel=2e-5, cos=0.999999)
+    # the VALU kernel over a copy of the store whose capacity is not a multiple of 64
+    kc, kb, vc = st.read_codes(0, T_)
+    st2 = KVStore(B, Hkv, d, 2, 3, 64, st.device)
+    st2._alloc(T_ + 32, 0)
+    st2.knorm[:, :, :T_].copy_(st.knorm[:, :, :T_])
+    st2.vnorm[:, :, :T_].copy_(st.vnorm[:, :, :T_])
+    st2.write_codes(0, T_, kc.reshape(-1, d).contiguous(), kb.reshape(-1, d).contiguous(),
+                    vc.reshape(-1, d).contiguous())
+    assert L.qkv_attention_path(d, 2, 3, kc_h.ptr, vc_h.ptr, st2.capacity, T_, 2) == 0
+    valu = K.attention_store(q, st2, T_, kq.mse_quantizer.Pi, kh, vh, kq.S, kq.qjl_scale,
+                             n_splits=2)
+    assert_close(outs[0], valu, rel=2e-5, cos=0.999999)
+    kc, kb, vc = (t[:3] for t in st.read_codes(0, T_))
+    blocks = [dict(kcodes=kc.cpu(), kbits=kb.cpu(), knorm=st.knorm[:3, :, :T_].cpu(),
+                   vcodes=vc.cpu(), vnorm=st.vnorm[:3, :, :T_].cpu())]
+    ref = R.attention_online(q[:3].float().cpu().reshape(3, Hkv, G, d), blocks,
+                             kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
+                             vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+    assert_close(outs[0][:3], ref.reshape(3, Hkv * G, 1, d), rel=2e-5, cos=0.999999)
+
+
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("key_bits,value_bits", [(2, 1), (2, 2), (2, 4), (3, 1), (3, 2), (3, 4)])
-def test_mfma_bit_widths_vs_oracle(key_bits, value_bits):
-    gen = torch.Generator().manual_seed(10 * key_bits + value_bits)
-    B, Hkv, G, d, T_ = 2, 2, 3, 128, 1000
+def test_mfma_bit_widths_vs_oracle(key_bits, value_bits, d):
+    gen = torch.Generator().manual_seed(10 * key_bits + value_bits + d)
+    B, Hkv, G, T_ = 2, 2, 3, 1000
     k = torch.randn(B, Hkv, T_, d, generator=gen)
     v = torch.randn(B, Hkv, T_, d, generator=gen) * torch.exp(torch.randn(B, Hkv, T_, 1, generator=gen))
     q = torch.randn(B, Hkv * G, 1, d, generator=gen)
