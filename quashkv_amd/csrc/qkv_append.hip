@@ -1,5 +1,5 @@
 // Fused compress straight into the cache store, for bf16 / fp16 K and V rows
-// with d = 128: normalise -> rotate (MFMA) -> Lloyd-Max boundary search ->
+// with d = 128 or 64: normalise -> rotate (MFMA) -> Lloyd-Max boundary search ->
 // QJL sign -> bit planes, one pass over the inputs.
 //
 // Reference: QuashKVEngine.append (quashkv/engine.py:145-172) compresses keys
@@ -58,12 +58,15 @@ namespace {
 typedef __bf16 qkv_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 qkv_f16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kD = 128;                 // head dim of this path
+constexpr int kD = 128;                 // head dim of the mixed-key path
 constexpr int kHalves = 1;              // 32-token MFMA column blocks per wave tile
 constexpr int kTok = 32 * kHalves;      // tokens per wave tile
 constexpr int kWaves = 8;               // waves per workgroup (two workgroups per CU)
 constexpr int kThreads = 64 * kWaves;
-constexpr int kFragN = 4 * 8 * 2 * 64;  // Pi fragments [block][k-step][split][lane] (64 KiB)
+// Pi fragments [block of 32 rows][k-step of 16][split][lane]: 64 KiB at d = 128
+template <int D>
+constexpr int frag_n() { return (D / 32) * (D / 16) * 2 * 64; }
+constexpr int kFragN = frag_n<kD>();
 constexpr float kPScaleF16 = 256.f;     // keeps the fp16 low part of Pi out of subnormals
 
 struct Thresh {
@@ -195,28 +198,30 @@ __device__ __forceinline__ float from16(uint16_t h) {
 // holds, for lane l, Pi'[32 b + (l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
 // eight 16-bit values: the high part (split 0) or the low part (split 1) of
 // Pi' = diag(rowsign) Pi * pscale (rowsign = S for keys, none for values).
-template <bool F16>
+template <bool F16, int D = kD>
 __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
                          const float* __restrict__ rowsign, float pscale) {
   // kThreads threads (every launch uses that block size); each takes NPT
   // (block, k-step, lane) slots and writes both splits of each, with all of
   // its Pi loads in flight before the first conversion
-  constexpr int NPT = kFragN / 2 / kThreads;
+  constexpr int NKS = D / 16;  // k-steps
+  constexpr int NPT = frag_n<D>() / 2 / kThreads;
+  static_assert(NPT * 2 * kThreads == frag_n<D>(), "whole slots per thread");
   float4 p[NPT][2];
   float sc[NPT];
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
-    const int ln = u & 63, s = (u >> 6) & 7, b = u >> 9;
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
     const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
-    p[x][0] = *reinterpret_cast<const float4*>(pi + j * kD + k0);
-    p[x][1] = *reinterpret_cast<const float4*>(pi + j * kD + k0 + 4);
+    p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
+    p[x][1] = *reinterpret_cast<const float4*>(pi + j * D + k0 + 4);
     sc[x] = (rowsign ? rowsign[j] : 1.f) * pscale;  // +-2^k: exact
   }
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
-    const int ln = u & 63, s = (u >> 6) & 7, b = u >> 9;
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
     const float v[8] = {p[x][0].x * sc[x], p[x][0].y * sc[x], p[x][0].z * sc[x],
                         p[x][0].w * sc[x], p[x][1].x * sc[x], p[x][1].y * sc[x],
                         p[x][1].z * sc[x], p[x][1].w * sc[x]};
@@ -227,7 +232,7 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
       hi[i] = h;
       lo[i] = to16<F16>(v[i] - from16<F16>(h));
     }
-    const int e = ((b * 8 + s) * 2) * 64 + ln;
+    const int e = ((b * NKS + s) * 2) * 64 + ln;
     frag[e] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
                          hi[6] | (hi[7] << 16));
     frag[e + 64] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
@@ -239,12 +244,13 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
 // holds x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt]
 // (this lane's token row of block tt; callers point lanes without a token at a
 // valid row, whose results are never stored).
-__device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][8],
+template <int NKS>
+__device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
                                        const uint16_t* const (&row)[kHalves], int lane) {
 #pragma unroll
   for (int tt = 0; tt < kHalves; ++tt)
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+    for (int s = 0; s < NKS; ++s)
       xf[tt][s] = *reinterpret_cast<const uint4*>(row[tt] + 16 * s + 8 * (lane >> 5));
 }
 
@@ -253,27 +259,30 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][8],
 // One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
 // grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
 // MB MSE planes, then the QJL plane).
-template <int MB, bool F16>
+template <int MB, bool F16, int D>
 __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, const float* __restrict__ signs, Thresh fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NF = (1 << L) - 1;    // c_0, t_0, c_1, ..., c_{2^MB - 1}
-  constexpr int RD = 4 * L;           // dwords per row
+  constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
+  constexpr int NKS = D / 16;         // k-steps
+  constexpr int RD = NBK * L;         // dwords per row
   constexpr int NSK = RD * kTok / 64; // staging dwords per lane
-  __shared__ uint4 frag[kFragN];
+  static_assert(RD * kTok % 64 == 0, "whole staging dwords");
+  __shared__ uint4 frag[frag_n<D>()];
   __shared__ float4 inv_s[kWaves][kTok / 4];  // 1 / norm of the wave's tokens
-  stage_pi<F16>(frag, pi, signs, F16 ? kPScaleF16 : 1.f);
+  stage_pi<F16, D>(frag, pi, signs, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
   float fv[NF / 2];  // positive half of the fine list
 #pragma unroll
   for (int i = 0; i < NF / 2; ++i) fv[i] = in_vgpr(fine.v[NF / 2 + 1 + i]);
-  uint64_t sneg[4];  // lanes whose coordinate 32 n + (l & 31) has S < 0
+  uint64_t sneg[NBK];  // lanes whose coordinate 32 n + (l & 31) has S < 0
 #pragma unroll
-  for (int n = 0; n < 4; ++n) sneg[n] = lanes_where(signs[32 * n + li] < 0.f);
+  for (int n = 0; n < NBK; ++n) sneg[n] = lanes_where(signs[32 * n + li] < 0.f);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
@@ -281,12 +290,12 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
-    uint4 xf[kHalves][8];  // tokens past S read the last row; their results are not stored
+    uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
     {
       const uint16_t* row[kHalves];
 #pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-      load_x(xf, row, lane);
+      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x<NKS>(xf, row, lane);
     }
 
     // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
@@ -297,7 +306,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     for (int tt = 0; tt < kHalves; ++tt) {
       float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+      for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
       if (lane < 32) {
@@ -312,17 +321,17 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 #pragma unroll
     for (int i = 0; i < NSK; ++i) stg[i] = 0u;
 
-    static_for<4>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
+    static_for<NBK>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
       constexpr int n = decltype(nc)::value;
       // one coordinate block at a time: keeps the scheduler from overlapping
       // blocks (and their accumulators and fragments) beyond the register file
       __builtin_amdgcn_sched_barrier(0);
       qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
+      for (int s = 0; s < NKS; ++s)
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
-          const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
+          const uint4 bf = frag[((n * NKS + s) * 2 + sp) * 64 + lane];
 #pragma unroll
           for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
         }
@@ -342,7 +351,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
           static_for<L>([&](auto rc) {
             constexpr int r = decltype(rc)::value;  // plane r: MSE bit r, r = MB: QJL
             const uint64_t w = r < MB ? (f[r + 1 < L ? r + 1 : 0] ^ sneg[n]) : f[0];
-            constexpr int D0 = ta * RD + 4 * r + n, D1 = (ta + 4) * RD + 4 * r + n;
+            constexpr int D0 = ta * RD + NBK * r + n, D1 = (ta + 4) * RD + NBK * r + n;
             stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w));
             stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w >> 32));
           });
@@ -353,8 +362,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
 #pragma unroll
     for (int i = 0; i < NSK; ++i) {
-      const int D = i * 64 + lane;
-      if (D < nv * RD) dst[D] = stg[i];
+      const int w = i * 64 + lane;
+      if (w < nv * RD) dst[w] = stg[i];
     }
   }
 }
@@ -486,15 +495,18 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
 // so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
 // already in the store.
-template <int VB, bool F16>
+template <int VB, bool F16, int D>
 __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, Thresh bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0) {
   constexpr int NB = (1 << VB) - 1;  // boundaries
-  constexpr int NS = 2 * VB * kHalves;  // staging dwords per lane: tiles x VB planes x 128 / 64
-  __shared__ uint4 frag[kFragN];
-  stage_pi<F16>(frag, pi, nullptr, F16 ? kPScaleF16 : 1.f);
+  constexpr int NBK = D / 32;        // coordinate blocks
+  constexpr int NKS = D / 16;        // k-steps
+  constexpr int NPW = D / 64;        // staging dwords per (tile, plane)
+  constexpr int NS = NPW * VB * kHalves;  // staging dwords per lane: tiles x VB planes x D / 64
+  __shared__ uint4 frag[frag_n<D>()];
+  stage_pi<F16, D>(frag, pi, nullptr, F16 ? kPScaleF16 : 1.f);
   __syncthreads();
 
   const int lane = threadIdx.x & 63, li = lane & 31;
@@ -512,16 +524,16 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
     bool ok[kHalves];
-    uint4 xf[kHalves][8];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
+    uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
     {
       const uint16_t* row[kHalves];
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
         const int64_t si = d0 + 32 * tt + li;
         ok[tt] = si >= 0 && si < S;
-        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1)) * kD;
+        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1)) * D;
       }
-      load_x(xf, row, lane);
+      load_x<NKS>(xf, row, lane);
     }
 
     float inv[kHalves];  // token 32 tt + (l & 31): the C-column of this lane
@@ -530,7 +542,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     for (int tt = 0; tt < kHalves; ++tt) {
       float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+      for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
       if (lane < 32 && ok[tt]) nrow[32 * tt + li] = nrm;
@@ -541,15 +553,15 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
 #pragma unroll
     for (int i = 0; i < NS; ++i) stg[i] = 0u;
 
-    static_for<4>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
+    static_for<NBK>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
       constexpr int mb = decltype(mc)::value;
       __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
       qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
+      for (int s = 0; s < NKS; ++s)
 #pragma unroll
         for (int sp = 0; sp < 2; ++sp) {
-          const uint4 af = frag[((mb * 8 + s) * 2 + sp) * 64 + lane];
+          const uint4 af = frag[((mb * NKS + s) * 2 + sp) * 64 + lane];
 #pragma unroll
           for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
         }
@@ -563,7 +575,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
           constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
           static_for<VB>([&](auto kc) {
             constexpr int k = decltype(kc)::value;
-            constexpr int D0 = (tt * VB + k) * kD + ca, D1 = D0 + 4;
+            constexpr int D0 = (tt * VB + k) * D + ca, D1 = D0 + 4;
             stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(m[k]));
             stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(m[k] >> 32));
           });
@@ -571,17 +583,17 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       });
     });
 
-    // store: staging dword i covers tile i / (2 VB), plane (i / 2) % VB,
-    // coordinates 64 (i % 2) + lane
+    // store: staging dword i covers tile i / (NPW VB), plane (i / NPW) % VB,
+    // coordinates 64 (i % NPW) + lane
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int tau = i / (2 * VB), k = (i / 2) % VB, j = 64 * (i % 2) + lane;
+      const int tau = i / (NPW * VB), k = (i / NPW) % VB, j = 64 * (i % NPW) + lane;
       const int64_t tok0 = A0 + 32 * tau;
       const int64_t lo = max<int64_t>(t0 - tok0, 0), hi = min<int64_t>(t0 + S - tok0, 32);
       if (hi <= lo) continue;
       const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
                                           : (((1u << (hi - lo)) - 1u) << lo);
-      uint32_t* p = vst + ((grp * tiles_per_group + tok0 / 32) * VB + k) * kD + j;
+      uint32_t* p = vst + ((grp * tiles_per_group + tok0 / 32) * VB + k) * D + j;
       uint32_t val = stg[i];
       if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
       *p = val;
@@ -619,8 +631,8 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
     return QKV_E_UNSUPPORTED;
   }
-  if (d != kD) {
-    qkv_set_error("store append runs on head_dim 128 (got %d)", d);
+  if (d != 128 && d != 64) {
+    qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
     return QKV_E_UNSUPPORTED;
   }
   if (keys) {
@@ -669,17 +681,24 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
     const auto* xk = static_cast<const uint16_t*>(keys);
-#define QKV_K(MB, F)                                                                        \
-  hipLaunchKernelGGL((append_k_mfma<MB, F>), grid, dim3(kThreads), 0, s, xk, S, tpg, ntiles, pi, \
-                     signs, fine, kstore, knorm, t_stride, t0)
-    switch (mbits * 2 + (f16 ? 1 : 0)) {
-      case 2: QKV_K(1, false); break;
-      case 3: QKV_K(1, true); break;
-      case 4: QKV_K(2, false); break;
-      case 5: QKV_K(2, true); break;
-      case 6: QKV_K(3, false); break;
-      case 7: QKV_K(3, true); break;
+#define QKV_K(MB, F, DD)                                                                    \
+  hipLaunchKernelGGL((append_k_mfma<MB, F, DD>), grid, dim3(kThreads), 0, s, xk, S, tpg, ntiles, \
+                     pi, signs, fine, kstore, knorm, t_stride, t0)
+#define QKV_KD(DD)                                  \
+  switch (mbits * 2 + (f16 ? 1 : 0)) {              \
+    case 2: QKV_K(1, false, DD); break;             \
+    case 3: QKV_K(1, true, DD); break;              \
+    case 4: QKV_K(2, false, DD); break;             \
+    case 5: QKV_K(2, true, DD); break;              \
+    case 6: QKV_K(3, false, DD); break;             \
+    case 7: QKV_K(3, true, DD); break;              \
+  }
+    if (d == 128) {
+      QKV_KD(128)
+    } else {
+      QKV_KD(64)
     }
+#undef QKV_KD
 #undef QKV_K
     QKV_LAUNCHED();
   }
@@ -688,19 +707,26 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const int64_t tpg = (t0 + S - a_base + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
     const auto* xv = static_cast<const uint16_t*>(values);
-#define QKV_V(VB, F)                                                                        \
-  hipLaunchKernelGGL((append_v_mfma<VB, F>), grid, dim3(kThreads), 0, s, xv, S, tpg, ntiles, pi, \
-                     bnd, vstore, vnorm, t_stride, t0)
-    switch (vbits * 2 + (f16 ? 1 : 0)) {
-      case 2: QKV_V(1, false); break;
-      case 3: QKV_V(1, true); break;
-      case 4: QKV_V(2, false); break;
-      case 5: QKV_V(2, true); break;
-      case 6: QKV_V(3, false); break;
-      case 7: QKV_V(3, true); break;
-      case 8: QKV_V(4, false); break;
-      case 9: QKV_V(4, true); break;
+#define QKV_V(VB, F, DD)                                                                    \
+  hipLaunchKernelGGL((append_v_mfma<VB, F, DD>), grid, dim3(kThreads), 0, s, xv, S, tpg, ntiles, \
+                     pi, bnd, vstore, vnorm, t_stride, t0)
+#define QKV_VD(DD)                                  \
+  switch (vbits * 2 + (f16 ? 1 : 0)) {              \
+    case 2: QKV_V(1, false, DD); break;             \
+    case 3: QKV_V(1, true, DD); break;              \
+    case 4: QKV_V(2, false, DD); break;             \
+    case 5: QKV_V(2, true, DD); break;              \
+    case 6: QKV_V(3, false, DD); break;             \
+    case 7: QKV_V(3, true, DD); break;              \
+    case 8: QKV_V(4, false, DD); break;             \
+    case 9: QKV_V(4, true, DD); break;              \
+  }
+    if (d == 128) {
+      QKV_VD(128)
+    } else {
+      QKV_VD(64)
     }
+#undef QKV_VD
 #undef QKV_V
     QKV_LAUNCHED();
   }

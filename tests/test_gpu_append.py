@@ -1,5 +1,5 @@
 """GPU parity of the fused store append (qkv_store_append: bf16 / fp16 K and V
-rows at head_dim 128 compressed straight into the K-row / V-tile store).
+rows at head_dim 128 or 64 compressed straight into the K-row / V-tile store).
 
 Its rotation carries ~16 (bf16) / ~22 (fp16) significant bits of Pi, so codes
 agree with the fp32 reference except where the rotated value sits within
@@ -30,14 +30,14 @@ def _need_gpu():
 def _rows(gen, shape, dtype, outliers=True):
     x = torch.randn(*shape, generator=gen)
     if outliers:
-        x[..., [11, 47, 83, 119]] *= 10.0
+        x[..., [c for c in (11, 47, 83, 119) if c < shape[-1]]] *= 10.0
     return x.to(dtype)
 
 
-def _engines(key_bits, value_bits, seed=5):
-    fused = Q.QuashKVEngine(head_dim=128, key_bits=key_bits, value_bits=value_bits, seed=seed,
+def _engines(key_bits, value_bits, seed=5, d=128):
+    fused = Q.QuashKVEngine(head_dim=d, key_bits=key_bits, value_bits=value_bits, seed=seed,
                             device=DEV)
-    generic = Q.QuashKVEngine(head_dim=128, key_bits=key_bits, value_bits=value_bits, seed=seed,
+    generic = Q.QuashKVEngine(head_dim=d, key_bits=key_bits, value_bits=value_bits, seed=seed,
                               device=DEV)
     generic._append_fused = lambda *a: False   # the unfused compress + converters path
     return fused, generic
@@ -49,16 +49,17 @@ def _mismatch(a, b):
     return float((diff != 0).double().mean()), int(diff.max()) if diff.numel() else 0
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (2, 1), (4, 4), (3, 2)])
-def test_store_append_matches_unfused_path(dtype, key_bits, value_bits):
-    gen = torch.Generator().manual_seed(key_bits * 10 + value_bits)
+def test_store_append_matches_unfused_path(dtype, key_bits, value_bits, d):
+    gen = torch.Generator().manual_seed(key_bits * 10 + value_bits + d)
     B, H = 2, 3
-    fused, generic = _engines(key_bits, value_bits)
+    fused, generic = _engines(key_bits, value_bits, d=d)
     total = 0
     for S in (150, 37, 1, 64, 0, 95):        # ragged sizes, unaligned starts
-        k = _rows(gen, (B, H, S, 128), dtype)
-        v = _rows(gen, (B, H, S, 128), dtype, outliers=False)
+        k = _rows(gen, (B, H, S, d), dtype)
+        v = _rows(gen, (B, H, S, d), dtype, outliers=False)
         fused.append(k.to(DEV), v.to(DEV))
         generic.append(k.to(DEV), v.to(DEV))
         total += S
@@ -71,27 +72,28 @@ def test_store_append_matches_unfused_path(dtype, key_bits, value_bits):
         assert float(((a - b).abs() / b).max()) <= 2e-6
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_store_append_vs_oracle(dtype):
+def test_store_append_vs_oracle(dtype, d):
     """Codes and norms against the CPU restatement of compress_ip / compress_mse
     (quashkv/quantizer.py:113-131, 211-242) on the same (upcast) inputs."""
     gen = torch.Generator().manual_seed(3)
     B, H, S = 2, 4, 700
-    k = _rows(gen, (B, H, S, 128), dtype)
-    v = _rows(gen, (B, H, S, 128), dtype, outliers=False)
-    eng = Q.QuashKVEngine(head_dim=128, seed=42, device=DEV)
+    k = _rows(gen, (B, H, S, d), dtype)
+    v = _rows(gen, (B, H, S, d), dtype, outliers=False)
+    eng = Q.QuashKVEngine(head_dim=d, seed=42, device=DEV)
     eng.append(k.to(DEV), v.to(DEV))
     st = eng._store
     kc, kb, vc = st.read_codes(0, S)
     kq, vq = eng.key_quantizer, eng.value_quantizer
     mq = kq.mse_quantizer
-    okc, okb, okn = R.compress_ip(k.float().reshape(-1, 128), mq.Pi.cpu(),
+    okc, okb, okn = R.compress_ip(k.float().reshape(-1, d), mq.Pi.cpu(),
                                   mq.codebook.boundaries.cpu(), kq.S.cpu(),
                                   mq.codebook.centroids.cpu())
-    ovc, ovn = R.compress_mse(v.float().reshape(-1, 128), vq.Pi.cpu(),
+    ovc, ovn = R.compress_mse(v.float().reshape(-1, d), vq.Pi.cpu(),
                               vq.codebook.boundaries.cpu())
     for got, ref in ((kc, okc), (kb, okb), (vc, ovc)):
-        rate, step = _mismatch(got.reshape(-1, 128), ref.reshape(-1, 128))
+        rate, step = _mismatch(got.reshape(-1, d), ref.reshape(-1, d))
         assert rate <= 1e-4 and step <= 1, (rate, step)
     for got, ref in ((st.knorm[:, :, :S], okn), (st.vnorm[:, :, :S], ovn)):
         got, ref = got.cpu().double().reshape(-1), ref.double().reshape(-1)

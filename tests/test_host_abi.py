@@ -72,10 +72,10 @@ def test_abi_rejects_before_launch():
 
 def test_store_append_validation():
     lib = N.lib()
-    # fp32 rows and head_dim != 128 are not covered by the fused kernel
+    # fp32 rows and head_dims other than 128 / 64 are not covered by the fused kernel
     assert lib.qkv_store_append(N.QKV_F32, 16, None, 1, 1, 128, 2, 3, 16, 16, 16, 16, 16, 16,
                                 16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
-    assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 64, 2, 3, 16, 16, 16, 16, 16, 16,
+    assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 96, 2, 3, 16, 16, 16, 16, 16, 16,
                                 16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
     # capacity must hold the appended tokens
     st = lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 10, 128, 2, 3, 16, 16, 16, 16, 16, 16,
