@@ -181,6 +181,123 @@ def bench_mips(args) -> None:
     print(json.dumps(line))
 
 
+def bench_cfg2(args) -> None:
+    """BASELINE configs[1] (cfg2): Qwen2.5-0.5B-shaped decode over all 24 layers.
+    Engine seeds 42 + l; B=16, Hq=14, Hkv=2 (GQA 7:1), d=64, context 2048;
+    K 3-bit IP, V 3-bit MSE; per token-head K, V = fp16(z / |z| r) with
+    z ~ N(0, I_64), r ~ LogNormal(0, 0.5); queries fp16 N(0, 1); data seed 1.
+    A step = decode attention of one query per sequence in every layer, as one
+    layer-batched call (qkv_decode_attention_layers); the MALL is flushed
+    before every timed step.  Also timed: the same step as 24 engine calls, and
+    a step with the one-token append per layer.  Prints one JSON line."""
+    import torch
+    import quashkv_amd as Q
+    from quashkv_amd import _native as N
+    from quashkv_amd import kernels as K
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    NL, B2, HQ2, HKV2, D2, T2 = 24, 16, 14, 2, 64, 2048
+    g = torch.Generator(device=dev).manual_seed(1)
+
+    def kv():
+        z = torch.randn(B2, HKV2, T2, D2, device=dev, generator=g)
+        r = torch.exp(0.5 * torch.randn(B2, HKV2, T2, 1, device=dev, generator=g))
+        return (z / z.norm(dim=-1, keepdim=True) * r).half()
+
+    engines = []
+    for l in range(NL):
+        e = Q.QuashKVEngine(head_dim=D2, key_bits=3, value_bits=3, seed=42 + l, device=dev,
+                            capacity=T2 + 64)
+        e.append(kv(), kv())
+        engines.append(e)
+    qs = [torch.randn(B2, HQ2, 1, D2, device=dev, generator=g).half() for _ in range(NL)]
+    torch.cuda.synchronize()
+    lib = N.lib()
+    splits = lib.qkv_attention_splits(B2 * NL, HQ2, HKV2, 1, D2, T2)
+    ws = torch.empty(lib.qkv_attention_workspace_bytes(B2 * NL, HQ2, HKV2, 1, D2, splits),
+                     dtype=torch.uint8, device=dev)
+    flush = torch.empty(512 * 1024 * 1024 // 4, device=dev)
+
+    def timed(fn, reps):
+        ts = []
+        for i in range(reps):
+            flush.fill_(float(i))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1))
+        return ts
+
+    step = lambda: K.attention_layers(engines, qs, workspace=ws, n_splits=splits)
+    timed(step, args.warmup)
+    ms = statistics.median(timed(step, args.steps))
+    outs = step()
+    per_layer = lambda: [e.attention(q) for e, q in zip(engines, qs)]
+    timed(per_layer, 2)
+    ms_pl = statistics.median(timed(per_layer, 5))
+    ref = per_layer()
+    torch.cuda.synchronize()
+    agree = max(float((a - b).norm() / b.norm()) for a, b in zip(outs, ref))
+    k1 = [kv()[:, :, :1].contiguous() for _ in range(2)]
+
+    def with_append():
+        for e in engines:
+            e.append(k1[0], k1[1])
+        return K.attention_layers(engines, qs, workspace=ws, n_splits=splits)
+
+    ms_app = statistics.median(timed(with_append, 5))
+    alg = NL * B2 * HKV2 * T2 * 56
+    line = {
+        "metric": "cfg2 decode step over 24 layers (layer-batched): us per step",
+        "value": round(ms * 1e3, 2), "unit": "us", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8 (MFMA) / f32",
+        "data": "synthetic (seeded; fp16 K/V with log-normal token norms)",
+        "config": {"workload": "cfg2 Qwen2.5-0.5B-shaped decode, 24 layers", "batch": B2,
+                   "q_heads": HQ2, "kv_heads": HKV2, "head_dim": D2, "context": T2,
+                   "layers": NL, "key_bits": 3, "value_bits": 3, "n_splits": splits},
+        "tokens_per_s": round(B2 / (ms * 1e-3), 1),
+        "per_layer_calls_us": round(ms_pl * 1e3, 2),
+        "layer_batched_vs_per_layer_rel_diff": agree,
+        "step_with_one_token_append_us": round(ms_app * 1e3, 2),
+        "roofline": {"kernel": "prepare + split_mfma + combine (one layer-batched call)",
+                     "bound": "hbm", "achieved": round(alg / (ms * 1e-3) / 1e9, 2),
+                     "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(alg / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": alg, "avg_kernel_us": round(ms * 1e3, 2)},
+    }
+    if not args.no_cpu:
+        from oracle import ref_math as R
+        torch.set_num_threads(os.cpu_count() or 1)
+        e = engines[0]
+        st, kq, vq = e._store, e.key_quantizer, e.value_quantizer
+        T = e.total_tokens
+        kc, kb, vc = st.read_codes(0, T)
+        blocks = [dict(kcodes=kc.cpu(), kbits=kb.cpu(), knorm=st.knorm[:, :, :T].cpu(),
+                       vcodes=vc.cpu(), vnorm=st.vnorm[:, :, :T].cpu())]
+        cargs = (kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
+                 vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+        qc = qs[0].float().cpu().reshape(B2, HKV2, HQ2 // HKV2, D2)
+        R.attention_online(qc, blocks, *cargs)
+        reps = []
+        for _ in range(max(args.cpu_reps, 1)):
+            t0 = time.perf_counter()
+            R.attention_online(qc, blocks, *cargs)
+            reps.append(time.perf_counter() - t0)
+        cpu_s = statistics.median(reps)
+        line["cpu_baseline"] = {"value": round(cpu_s * NL * 1e6, 1), "unit": "us",
+                                "cores": torch.get_num_threads(), "kind": "port",
+                                "sample": f"oracle attention_online on layer 0 of {NL} (all 16 "
+                                          f"sequences, {cpu_s:.3f} s, median of {len(reps)}), "
+                                          f"scaled x{NL}"}
+    print(json.dumps(line), flush=True)
+
+
 def bench_cfg4(args) -> None:
     """BASELINE configs[3] (cfg4): long-context mixed precision.  B=1, 32 query
     heads over 8 kv heads, d=128; 131072 tokens appended in 64 chunks of 2048;
@@ -340,9 +457,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB three times (calibrates FETCH_SIZE / WRITE_SIZE)")
-    ap.add_argument("--workload", choices=("cfg3", "cfg4", "cfg5"), default="cfg3",
-                    help="cfg3: the headline decode/compress line; cfg4: mixed-precision "
-                         "long context; cfg5: the MIPS index")
+    ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5"), default="cfg3",
+                    help="cfg3: the headline decode/compress line; cfg2: 24-layer d=64 "
+                         "decode step; cfg4: mixed-precision long context; cfg5: the MIPS index")
     args = ap.parse_args()
 
     if args.copy_calibration:
@@ -353,6 +470,9 @@ def main() -> None:
         return
     if args.workload == "cfg4":
         bench_cfg4(args)
+        return
+    if args.workload == "cfg2":
+        bench_cfg2(args)
         return
 
     if args.gpus != 1:

@@ -312,6 +312,27 @@ int qkv_attention_run(const uint8_t* kstore, const float* knorm,
                       int32_t causal, void* out, int32_t out_dtype, void* workspace,
                       int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* One decode step over n_layers (1..32) layers sharing shapes, bit widths and
+ * codebooks -- a model's layers, each with its own store, Pi, S, query and
+ * output -- in three launches instead of 3 n_layers (quashkv/engine.py:
+ * 204-299 per layer).  q, kstore, knorm, vstore, vnorm, pi, signs and out are
+ * HOST arrays of n_layers device pointers, each as in qkv_decode_attention;
+ * the other arguments are shared.  The workspace and split count are those of
+ * a batch of B * n_layers sequences (qkv_attention_splits /
+ * qkv_attention_workspace_bytes with B * n_layers).  MFMA path only
+ * (QKV_E_UNSUPPORTED otherwise). */
+int qkv_decode_attention_layers(int32_t n_layers, const void* const* q, int32_t q_dtype,
+                                const uint8_t* const* kstore, const float* const* knorm,
+                                const uint32_t* const* vstore, const float* const* vnorm,
+                                int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                                int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                int32_t vbits, const float* const* pi,
+                                const float* kcent_host, const float* vcent_host,
+                                const float* const* signs, float qjl_scale, float scale,
+                                int32_t causal, void* const* out, int32_t out_dtype,
+                                void* workspace, int64_t ws_bytes, int32_t n_splits,
+                                void* stream);
+
 /* ------------------------------------------------------------------------
  * Mixed-precision keys in the store (MixedPrecisionMSEQuantizer with 3-bit
  * outlier and 2-bit regular channels, quashkv/mixed_precision.py:25-197).

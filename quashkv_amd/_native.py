@@ -54,6 +54,9 @@ _SIGS = {
                                   _i32, _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_decompress_mixed": (_i32, [_i32, _p, _p, _p, _i64, _i32, _p, _p, _i32, _p, _i32, _p, _p,
                                     _f32, _i64, _i64, _p, _i32, _p]),
+    "qkv_decode_attention_layers": (_i32, [_i32, _p, _i32, _p, _p, _p, _p, _i64, _i64, _i32,
+                                           _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
+                                           _f32, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
     "qkv_kmixed_pack": (_i32, [_p, _i64, _p, _i32, _p, _i64, _i64, _p]),
     "qkv_kmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p]),
     "qkv_store_append_kmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p, _p,
@@ -213,6 +216,11 @@ class HostInts:
     @property
     def ptr(self) -> int:
         return ctypes.addressof(self.arr)
+
+
+def ptr_array(ptrs) -> "ctypes.Array":
+    """Device pointers (ints) as a host array of void* (per-layer arguments)."""
+    return (ctypes.c_void_p * max(len(ptrs), 1))(*[ctypes.c_void_p(int(x)) for x in ptrs])
 
 
 def packed_row_bytes(d: int, bits: int) -> int:

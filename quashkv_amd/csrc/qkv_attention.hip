@@ -64,6 +64,28 @@ struct Tables {
   float kco, kcr;    // -(sum of the coefficients) per kind
 };
 
+// Per-layer pointers of a layer-batched decode call (one model step over
+// n <= kMaxLayers layers that share shapes and codebooks), passed by value as
+// kernel arguments.  The workspace then holds the layers as one batch of
+// B * n sequences (layer l, sequence b <-> batch index l B + b).  The
+// single-layer entry points use entry 0.
+constexpr int kMaxLayers = 32;
+struct QLayers {  // query, rotation (row-major d x d), QJL signs
+  const void* q[kMaxLayers];
+  const float* pi[kMaxLayers];
+  const float* signs[kMaxLayers];
+};
+struct KVLayers {  // the store
+  const uint8_t* kst[kMaxLayers];
+  const float* knorm[kMaxLayers];
+  const uint32_t* vst[kMaxLayers];
+  const float* vnorm[kMaxLayers];
+};
+struct OutLayers {  // un-rotation and output
+  const float* pi[kMaxLayers];
+  void* out[kMaxLayers];
+};
+
 // Odd-size subsets of the code bits (bit masks), in a fixed order shared by
 // the host (coefficients) and the device (plane words).
 __host__ __device__ constexpr uint32_t odd_subset(int bits, int s) {
@@ -363,9 +385,7 @@ __device__ __forceinline__ void mfma_settle() {
 // of k, then turns coordinate j of rows part, part + 256 / D, ... into digit
 // bytes, scattered into an LDS image of the operands that is copied out whole.
 template <int D, int NPL>
-__global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, int q_dtype,
-                                                    const float* __restrict__ pi,
-                                                    const float* __restrict__ signs,
+__global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dtype,
                                                     float alpha, int Hq, int Hkv, int Q, int R,
                                                     int chunks, Tables tb,
                                                     qkv_v4i* __restrict__ aq,
@@ -391,10 +411,14 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
 
   const int tid = threadIdx.x;
   const int G = Hq / Hkv;
-  const int bhc = blockIdx.x;
+  const int bhc = blockIdx.x;  // over the batch of all layers
   const int chunk = bhc % chunks;
   const int bh = bhc / chunks;
-  const int hkv = bh % Hkv, b = bh / Hkv;
+  const int hkv = bh % Hkv, bz = bh / Hkv;
+  const int layer = bz / Bl, b = bz - layer * Bl;
+  const void* __restrict__ q = ql.q[layer];
+  const float* __restrict__ pi = ql.pi[layer];
+  const float* __restrict__ signs = ql.signs[layer];
   const int r0 = chunk * kRowsM;
   const int nr = min(kRowsM, R - r0);
   // this thread's part of a Pi row: all float4 loads issued before use
@@ -553,13 +577,14 @@ __global__ __launch_bounds__(256) void prepare_mfma(const void* __restrict__ q, 
 
 // Four waves per SIMD (at most 128 VGPRs): with 4 workgroups per CU the split
 // count fills the chip in whole rounds and hides the K/V load latency.
-template <int D, int MB, int VB>
+// RC row chunks (of 4 query rows) per workgroup: with RC = 2 (GQA groups of
+// 5..8 rows at d = 64) each K/V operand expanded from the store feeds two
+// MFMAs, and the split's K/V bytes are read once for 8 rows.
+template <int D, int MB, int VB, int RC>
 __global__ __launch_bounds__(256, 4) void split_mfma(
-    const qkv_v4i* __restrict__ aq, const float* __restrict__ rowc,
-    const uint8_t* __restrict__ kst, const float* __restrict__ knorm,
-    const uint32_t* __restrict__ vst, const float* __restrict__ vnorm, int64_t t_stride,
-    int64_t T, int Hkv, int R, int Q, int chunks, float scale, int causal, int64_t split_len,
-    Tables tb, float* __restrict__ part_o, float* __restrict__ part_ml) {
+    const qkv_v4i* __restrict__ aq, const float* __restrict__ rowc, KVLayers kv, int Bl,
+    int64_t t_stride, int64_t T, int Hkv, int R, int Q, int chunks, float scale, int causal,
+    int64_t split_len, Tables tb, float* __restrict__ part_o, float* __restrict__ part_ml) {
   constexpr int KRB = (MB + 1) * D / 8;  // K row bytes
   constexpr int DPL = KRB / 16;          // row dwords per lane group (D = 128)
   constexpr int NU = KRB / 8;            // score MFMAs per 16 tokens
@@ -568,61 +593,79 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   constexpr int NLD = D == 128 ? DPL : NU;
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int MTW = D / 64;            // 16-coordinate tiles per wave
+  constexpr int RW = kRowsM * RC;        // query rows per workgroup
   static_assert(D == 128 || D == 64, "64- or 128-dim rows");
   static_assert(D == 64 || KRB % 16 == 0, "K rows must split into 4 lane groups of whole dwords");
   static_assert(D % 64 == 0, "value tiles split over 4 waves");
+  static_assert(RC == 1 || RC == 2, "one or two row chunks");
 
-  // scores [tile][row][64]; rewritten in place as value-MFMA digits
-  // [tile][col = 4 row + digit][64 K positions] (1 KB per tile either way)
   // dynamic LDS, sized by the host to this launch's split length:
-  // [ntile_cap][row][64] scores (rewritten in place as value digits), then
-  // [ntile_cap * 64] value norms
+  // [ntile_cap][RW rows][64] scores, rewritten in place as value-MFMA digits
+  // [ntile_cap][RC][col = 4 row + digit][64 K positions] (RC KB per tile
+  // either way), then [ntile_cap * 64] value norms
   extern __shared__ __align__(16) float smem[];
   const int ntile_cap = static_cast<int>((split_len + 63) >> 6);
-  float(*sbuf)[kRowsM][64] = reinterpret_cast<float(*)[kRowsM][64]>(smem);
-  float* vn = smem + ntile_cap * kRowsM * 64;
-  __shared__ float red_m[4][kRowsM];
+  float(*sbuf)[RW][64] = reinterpret_cast<float(*)[RW][64]>(smem);
+  float* vn = smem + ntile_cap * RW * 64;
+  __shared__ float red_m[4][RW];
   __shared__ float red_v[4];
-  __shared__ float lsum_s[kRowsM];
-  __shared__ long long usum_s[kRowsM];  // sum_t Z_t s_t per row, exact
+  __shared__ float lsum_s[RW];
+  __shared__ long long usum_s[RW];  // sum_t Z_t s_t per row, exact
 
   const int split = blockIdx.x;
-  const int hkv = blockIdx.y / chunks, chunk = blockIdx.y - (blockIdx.y / chunks) * chunks;
-  const int b = blockIdx.z;
+  const int cgroups = (chunks + RC - 1) / RC;
+  const int hkv = blockIdx.y / cgroups, cgi = blockIdx.y - hkv * cgroups;
+  const int b = blockIdx.z;  // over the batch of all layers
+  const int layer = b / Bl;
+  const uint8_t* __restrict__ kst = kv.kst[layer];
+  const float* __restrict__ knorm = kv.knorm[layer];
+  const uint32_t* __restrict__ vst = kv.vst[layer];
+  const float* __restrict__ vnorm = kv.vnorm[layer];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  const int r0 = chunk * kRowsM;
-  const int nr = min(kRowsM, R - r0);
-  const int64_t bh = int64_t(b) * Hkv + hkv;
-  const int64_t bhc = bh * chunks + chunk;
+  const int r0 = cgi * RW;
+  const int nr = min(RW, R - r0);  // valid rows of the workgroup
+  const int64_t bh = int64_t(b - layer * Bl) * Hkv + hkv;   // in the layer's store
   const int64_t ts = int64_t(split) * split_len;
   const int64_t te = min<int64_t>(T, ts + split_len);
   const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
 
   // ---------------- phase 1: scores of every token of the split -> LDS
-  qkv_v4i a[NU];
-#pragma unroll
-  for (int u = 0; u < NU; ++u) a[u] = aq[(bhc * NU + u) * 64 + lane];
-  const float cr = rowc[(bhc * kRowsM + lg) * 2 + 0];
-  const float fq = rowc[(bhc * kRowsM + lg) * 2 + 1];
-  const bool row_ok = lg < nr;
-  const int qi = (r0 + lg) % Q;
+  qkv_v4i a[RC][NU];
+  float cr[RC], fq[RC];
+  bool row_ok[RC];
+  int clim[RC];
   const float scale2 = scale * 1.4426950408889634f;  // scores in log2 units on this path
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const int chunk = cgi * RC + c;
+    const bool cv = chunk < chunks;
+    const int64_t bhc = (int64_t(b) * Hkv + hkv) * chunks + (cv ? chunk : 0);  // workspace
+#pragma unroll
+    for (int u = 0; u < NU; ++u)
+      a[c][u] = cv ? aq[(bhc * NU + u) * 64 + lane] : qkv_v4i{0, 0, 0, 0};
+    cr[c] = cv ? rowc[(bhc * kRowsM + lg) * 2 + 0] : 0.f;
+    fq[c] = cv ? rowc[(bhc * kRowsM + lg) * 2 + 1] : 0.f;
+    row_ok[c] = kRowsM * c + lg < nr;
+    // causal: token tl (split-relative) is visible to this lane's row iff
+    // ts + tl <= T - Q + qi
+    const int qi = (r0 + kRowsM * c + lg) % Q;
+    const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
+    clim[c] = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
+  }
 
   // Each wave scores 64-token tiles w, w + 4, ... as four 16-token MFMA
   // groups.  K rows, key norms and value norms of the next PD1 tiles are in
   // flight in a register ring while the current tile is scored.
-  float mloc = -INFINITY, vmax = 0.f;
+  float mloc[RC], vmax = 0.f;
+#pragma unroll
+  for (int c = 0; c < RC; ++c) mloc[c] = -INFINITY;
   const int ntile1 = (ntok + 63) >> 6;
   // split-relative bases: per-lane offsets stay 32-bit
   const uint8_t* kbs = kst + (bh * t_stride + ts) * KRB;
   const float* knbs = knorm + bh * t_stride + ts;
   const float* vnbs = vnorm + bh * t_stride + ts;
-  // causal: token tl (split-relative) is visible to this lane's row iff
-  // ts + tl <= T - Q + qi
-  const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
-  const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
-  constexpr int PD1 = 2;
+  constexpr int PD1 = RC == 2 ? 1 : 2;  // (registers: two chunks' accumulators)
   uint32_t kd[PD1][4][NLD];
   float kn[PD1][4], vv[PD1][4];
   // Tokens past the split end are read too (masked when scored): the store
@@ -643,10 +686,12 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     }
   };
   auto score1 = [&](int slot, int tile) {
-    // four independent 16-token chains interleaved, one settle for all
-    qkv_v4i acc[4];
+    // four independent 16-token chains per chunk interleaved, one settle for all
+    qkv_v4i acc[RC][4];
 #pragma unroll
-    for (int sub = 0; sub < 4; ++sub) acc[sub] = qkv_v4i{0, 0, 0, 0};
+    for (int c = 0; c < RC; ++c)
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) acc[c][sub] = qkv_v4i{0, 0, 0, 0};
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       const int sh = D == 128 ? 4 * (u & 1) : lsh;
@@ -658,21 +703,26 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
         bo[1] = static_cast<int>(x & (0x02020202u << sh));
         bo[2] = static_cast<int>(x & (0x04040404u << sh));
         bo[3] = static_cast<int>(x & (0x08080808u << sh));
-        acc[sub] = mfma_i8(a[u], bo, acc[sub]);
+#pragma unroll
+        for (int c = 0; c < RC; ++c) acc[c][sub] = mfma_i8(a[c][u], bo, acc[c][sub]);
       }
     }
     mfma_settle();
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const int tl = tile * 64 + sub * 16 + ln;
-      const float z = static_cast<float>(acc[sub][0]) + 256.f * static_cast<float>(acc[sub][1]) +
-                      65536.f * static_cast<float>(acc[sub][2]) +
-                      16777216.f * static_cast<float>(acc[sub][3]);
-      const float sc0 = kn[slot][sub] * scale2 * fmaf(z, fq, cr);
       const bool in = tl < ntok;
-      const float sc = (in & row_ok & (tl <= clim)) ? sc0 : -INFINITY;
-      sbuf[tile][lg][sub * 16 + ln] = sc;
-      mloc = fmaxf(mloc, sc);
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        const float z = static_cast<float>(acc[c][sub][0]) +
+                        256.f * static_cast<float>(acc[c][sub][1]) +
+                        65536.f * static_cast<float>(acc[c][sub][2]) +
+                        16777216.f * static_cast<float>(acc[c][sub][3]);
+        const float sc0 = kn[slot][sub] * scale2 * fmaf(z, fq[c], cr[c]);
+        const float sc = (in & row_ok[c] & (tl <= clim[c])) ? sc0 : -INFINITY;
+        sbuf[tile][kRowsM * c + lg][sub * 16 + ln] = sc;
+        mloc[c] = fmaxf(mloc[c], sc);
+      }
       const float vz = in ? vv[slot][sub] : 0.f;
       vn[tl] = vz;  // the four lane groups store the same value
       vmax = fmaxf(vmax, vz);
@@ -692,15 +742,16 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     }
   }
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, o, 64));
+  for (int c = 0; c < RC; ++c) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mloc[c] = fmaxf(mloc[c], __shfl_xor(mloc[c], o, 64));
+    if (ln == 0) red_m[wave][kRowsM * c + lg] = mloc[c];
+  }
   vmax = qkv_wave_max(vmax);
-  if (ln == 0) red_m[wave][lg] = mloc;
   if (lane == 0) red_v[wave] = vmax;
   __syncthreads();
 
-  // ---------------- phase 1.5: p = 2^(s - m), value digits (wave w <-> row w)
-  const float m_q = fmaxf(fmaxf(red_m[0][wave], red_m[1][wave]),
-                          fmaxf(red_m[2][wave], red_m[3][wave]));
+  // ---------------- phase 1.5: p = 2^(s - m), value digits (wave w <-> rows w, w + 4)
   const float vmx = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
   int ev = 0;
   if (vmx > 0.f) frexpf(vmx, &ev);
@@ -708,16 +759,18 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int ntiles = (ntok + 63) >> 6;
   uint8_t* pbase = reinterpret_cast<uint8_t*>(&sbuf[0][0][0]);
 
-  qkv_v4i acc2[MTW][NP];
+  qkv_v4i acc2[RC][MTW][NP];
 #pragma unroll
-  for (int mi = 0; mi < MTW; ++mi)
+  for (int c = 0; c < RC; ++c)
 #pragma unroll
-    for (int s = 0; s < NP; ++s) acc2[mi][s] = qkv_v4i{0, 0, 0, 0};
+    for (int mi = 0; mi < MTW; ++mi)
+#pragma unroll
+      for (int s = 0; s < NP; ++s) acc2[c][mi][s] = qkv_v4i{0, 0, 0, 0};
   // V plane words of the next PD2 tiles are in flight in a register ring.
   const int64_t vtile0 = ts >> 5;
   const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
-  constexpr int PD2 = 6;
+  constexpr int PD2 = MTW * VB * RC > 6 ? 4 : 6;
   uint32_t vw[PD2][MTW][VB];
   auto load2 = [&](int slot, int tt) {
     const int64_t vt = vtile0 + 2 * tt + blk;
@@ -729,7 +782,10 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     }
   };
   auto pv2 = [&](int slot, int tt) {
-    const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(pbase + tt * 1024 + ln * 64 + lg * 16);
+    qkv_v4i bq[RC];
+#pragma unroll
+    for (int c = 0; c < RC; ++c)
+      bq[c] = *reinterpret_cast<const qkv_v4i*>(pbase + (tt * RC + c) * 1024 + ln * 64 + lg * 16);
 #pragma unroll
     for (int mi = 0; mi < MTW; ++mi) {
 #pragma unroll
@@ -744,7 +800,9 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
         av[1] = static_cast<int>(pw & (0x02020202u << hsh));
         av[2] = static_cast<int>(pw & (0x04040404u << hsh));
         av[3] = static_cast<int>(pw & (0x08080808u << hsh));
-        acc2[mi][s] = mfma_i8(bq, av, acc2[mi][s]);  // C[row x digit][coordinate]
+#pragma unroll
+        for (int c = 0; c < RC; ++c)  // C[row x digit][coordinate]
+          acc2[c][mi][s] = mfma_i8(bq[c], av, acc2[c][mi][s]);
       }
     }
   };
@@ -755,39 +813,45 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 
   // Row w's digits of tile tt occupy exactly the 256 bytes that held row w's
   // scores of that tile, and one wave's LDS operations execute in order, so
-  // each wave converts its row in place without a barrier.  Tokens past the
+  // each wave converts its rows in place without a barrier.  Tokens past the
   // split end hold -inf scores and zero norms (phase 1 writes whole tiles).
   // token (lane) of a 64-token tile -> K position of the value MFMA:
   // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
   const int ii = lane & 7;
   const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
   const float zscale = ldexpf(1.f, Fv - ii);  // Z_t s_t = X 2^i, X = round(p' 2^(Fv - i))
-  const bool live = wave < nr && m_q > -INFINITY;
-  const float m_use = live ? m_q : INFINITY;  // absent row: every p = 0
-  float lsum = 0.f;
-  int64_t xsum = 0;
-  for (int tt = 0; tt < ntiles; ++tt) {
-    const float p = __builtin_amdgcn_exp2f(sbuf[tt][wave][lane] - m_use);
-    lsum += p;
-    const float pv = p * vn[tt * 64 + lane];
-    const int X = static_cast<int>(fmaf(pv, zscale, 0.5f));
-    xsum += X;
-    const int Z = ii == 7 ? -X : X;
-    // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
-    const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
-    uint8_t* dst = pbase + tt * 1024 + (4 * wave) * 64 + kpos;
-    dst[0] = static_cast<uint8_t>(dg);
-    dst[64] = static_cast<uint8_t>(dg >> 8);
-    dst[128] = static_cast<uint8_t>(dg >> 16);
-    dst[192] = static_cast<uint8_t>(dg >> 24);
-  }
-  lsum = qkv_wave_sum(lsum);
-  // sum_t Z_t s_t: what an all-ones plane would accumulate (this lane's tokens
-  // all share i = lane % 8)
-  const int64_t usum = wave_sum_i64(xsum << ii);
-  if (lane == 0) {
-    lsum_s[wave] = lsum;
-    usum_s[wave] = usum;
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const int row = kRowsM * c + wave;
+    const float m_q = fmaxf(fmaxf(red_m[0][row], red_m[1][row]),
+                            fmaxf(red_m[2][row], red_m[3][row]));
+    const bool live = row < nr && m_q > -INFINITY;
+    const float m_use = live ? m_q : INFINITY;  // absent row: every p = 0
+    float lsum = 0.f;
+    int64_t xsum = 0;
+    for (int tt = 0; tt < ntiles; ++tt) {
+      const float p = __builtin_amdgcn_exp2f(sbuf[tt][row][lane] - m_use);
+      lsum += p;
+      const float pv = p * vn[tt * 64 + lane];
+      const int X = static_cast<int>(fmaf(pv, zscale, 0.5f));
+      xsum += X;
+      const int Z = ii == 7 ? -X : X;
+      // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
+      const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+      uint8_t* dst = pbase + (tt * RC + c) * 1024 + (4 * wave) * 64 + kpos;
+      dst[0] = static_cast<uint8_t>(dg);
+      dst[64] = static_cast<uint8_t>(dg >> 8);
+      dst[128] = static_cast<uint8_t>(dg >> 16);
+      dst[192] = static_cast<uint8_t>(dg >> 24);
+    }
+    lsum = qkv_wave_sum(lsum);
+    // sum_t Z_t s_t: what an all-ones plane would accumulate (this lane's
+    // tokens all share i = lane % 8)
+    const int64_t usum = wave_sum_i64(xsum << ii);
+    if (lane == 0) {
+      lsum_s[row] = lsum;
+      usum_s[row] = usum;
+    }
   }
   __syncthreads();
 
@@ -803,27 +867,31 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   }
 
   // ---------------- epilogue: digits + planes -> fp32, write the partials
-  // Lane (g = lane / 16, c = lane % 16) holds, per 16-coordinate tile and
-  // plane S, the four digit accumulators of row g at coordinate c.
+  // Lane (g = lane / 16, c = lane % 16) holds, per chunk, 16-coordinate tile
+  // and plane S, the four digit accumulators of row g at coordinate c.
   // Y_S = sum_v 2^(8v) acc_S[v] = sum_t Z_t s_t phi_S,t exactly (int64), and
   // sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U) is formed in integers
   // before the only rounding: O = 2^-Fv sum_S g_S (2 Y_S - U).
   mfma_settle();
   const float oscale = ldexpf(1.f, -Fv);
-  const int64_t urow = usum_s[lg];
   const int64_t base = ((int64_t(split) * gridDim.z + b) * Hkv + hkv) * R + r0;
 #pragma unroll
-  for (int mi = 0; mi < MTW; ++mi) {
-    float val = 0.f;
+  for (int c = 0; c < RC; ++c) {
+    const int row = kRowsM * c + lg;
+    const int64_t urow = usum_s[row];
 #pragma unroll
-    for (int s = 0; s < NP; ++s) {
-      const int64_t y = static_cast<int64_t>(acc2[mi][s][0]) +
-                        (static_cast<int64_t>(acc2[mi][s][1]) << 8) +
-                        (static_cast<int64_t>(acc2[mi][s][2]) << 16) +
-                        (static_cast<int64_t>(acc2[mi][s][3]) << 24);
-      val = fmaf(tb.vg[s], static_cast<float>(2 * y - urow), val);
+    for (int mi = 0; mi < MTW; ++mi) {
+      float val = 0.f;
+#pragma unroll
+      for (int s = 0; s < NP; ++s) {
+        const int64_t y = static_cast<int64_t>(acc2[c][mi][s][0]) +
+                          (static_cast<int64_t>(acc2[c][mi][s][1]) << 8) +
+                          (static_cast<int64_t>(acc2[c][mi][s][2]) << 16) +
+                          (static_cast<int64_t>(acc2[c][mi][s][3]) << 24);
+        val = fmaf(tb.vg[s], static_cast<float>(2 * y - urow), val);
+      }
+      if (row < nr) part_o[(base + row) * D + 16 * (wave * MTW + mi) + ln] = val * oscale;
     }
-    if (lg < nr) part_o[(base + lg) * D + 16 * (wave * MTW + mi) + ln] = val * oscale;
   }
   if (tid < nr) {
     const float mq = fmaxf(fmaxf(red_m[0][tid], red_m[1][tid]), fmaxf(red_m[2][tid], red_m[3][tid]));
@@ -852,9 +920,8 @@ constexpr int kRowsC = 4;       // query rows merged per block (many rows)
 template <int D, int RPB>
 __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict__ part_o,
                                                         const float* __restrict__ part_ml,
-                                                        const float* __restrict__ pi,
-                                                        int n_splits, int B, int Hkv, int R,
-                                                        int Q, int Hq, void* __restrict__ out,
+                                                        OutLayers ol, int n_splits, int Bl,
+                                                        int Hkv, int R, int Q, int Hq,
                                                         int out_dtype) {
   constexpr int JG = D / 4, KPER = D / 8, NSP = 8;
   constexpr int BATCH = RPB == 1 ? 8 : 2;  // splits per row per load round
@@ -862,9 +929,14 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
   __shared__ float4 red[NSP][RPB][JG];
   __shared__ float2 mls[NSP][RPB];
   const int tid = threadIdx.x;
-  const int64_t nrows = int64_t(B) * Hkv * R;
-  const int64_t row0 = int64_t(blockIdx.x) * RPB;
-  const int nr = static_cast<int>(min<int64_t>(RPB, nrows - row0));
+  const int layer = blockIdx.y;
+  const float* __restrict__ pi = ol.pi[layer];
+  void* __restrict__ out = ol.out[layer];
+  const int64_t nrl = int64_t(Bl) * Hkv * R;           // rows of one layer
+  const int64_t nrows = nrl * gridDim.y;               // rows of the partials
+  const int64_t row0 = int64_t(blockIdx.x) * RPB;      // in the layer
+  const int64_t grow0 = int64_t(layer) * nrl + row0;   // in the partials
+  const int nr = static_cast<int>(min<int64_t>(RPB, nrl - row0));
 
   const int j4 = tid % JG, kr = tid / JG;  // kr doubles as the split lane
   float4 pv[KPER];
@@ -892,7 +964,7 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
 #pragma unroll
         for (int r = 0; r < RPB; ++r) {
           const bool ok = sidx < n_splits && r < nr;
-          const int64_t base = int64_t(ok ? sidx : 0) * nrows + (ok ? row0 + r : 0);
+          const int64_t base = int64_t(ok ? sidx : 0) * nrows + (ok ? grow0 + r : 0);
           mlb[x][r] = ok ? ml2[base] : make_float2(-INFINITY, 0.f);
           ob[x][r] = ok ? o4[base * JG + j4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -983,7 +1055,7 @@ __global__ __launch_bounds__(2 * D) void combine_kernel(const float* __restrict_
       float v = 0.f;
 #pragma unroll
       for (int k = 0; k < NSP; ++k) v += redf[(k * RPB + r) * D + j];
-      const int64_t row = row0 + r;  // ((b * Hkv) + hkv) * R + r
+      const int64_t row = row0 + r;  // in the layer: ((b * Hkv) + hkv) * R + r
       const int rq = static_cast<int>(row % R);
       const int hkv = static_cast<int>((row / R) % Hkv);
       const int b = static_cast<int>(row / (int64_t(R) * Hkv));
@@ -1383,28 +1455,35 @@ int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, in
   return QKV_OK;
 }
 
+// Row chunks per split_mfma workgroup: two at d = 64 when the GQA group has
+// more than 4 rows (the K/V operands then serve 8 rows), else one.
+int mfma_rc(int d, int R) { return d == 64 && R > kRowsM ? 2 : 1; }
+
 // Dynamic LDS bytes of split_mfma for a split length (scores + value norms).
-int64_t mfma_smem_bytes(int64_t split_len) {
+int64_t mfma_smem_bytes(int64_t split_len, int rc) {
   const int64_t nt = (split_len + 63) / 64;
-  return nt * kRowsM * 64 * 4 + nt * 64 * 4;
+  return nt * kRowsM * rc * 64 * 4 + nt * 64 * 4;
 }
 
 // Resident split_mfma workgroups per CU for a split length (queried per
 // length; the kernel's registers and this LDS size set it).
-int mfma_blocks_per_cu(int64_t split_len) {
-  static int cache[kSplitMax / 64 + 1] = {0};
+int mfma_blocks_per_cu(int64_t split_len, int rc) {
+  static int cache[2][kSplitMax / 64 + 1] = {};
   const int nt = static_cast<int>((split_len + 63) / 64);
   if (nt < 1 || nt > kSplitMax / 64) return 1;
-  if (cache[nt] == 0) {
+  int& slot = cache[rc == 2][nt];
+  if (slot == 0) {
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &v, split_mfma<128, 2, 3>, 256, static_cast<size_t>(mfma_smem_bytes(nt * 64))) !=
-            hipSuccess ||
-        v <= 0)
-      v = 2;
-    cache[nt] = v;
+    const size_t smem = static_cast<size_t>(mfma_smem_bytes(nt * 64, rc));
+    const hipError_t e =
+        rc == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 2>, 256,
+                                                               smem)
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<128, 2, 3, 1>, 256,
+                                                               smem);
+    if (e != hipSuccess || v <= 0) v = 1;
+    slot = v;
   }
-  return cache[nt];
+  return slot;
 }
 
 }  // namespace
@@ -1413,10 +1492,10 @@ int mfma_blocks_per_cu(int64_t split_len) {
 
 extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
                                         int32_t d, int64_t T) {
-  (void)d;
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
   const int R = (Hq / Hkv) * Q;
-  const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM);
+  const int rc = mfma_rc(d, R);
+  const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM * rc - 1) / (kRowsM * rc));
   const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
   const int64_t max_s = std::min<int64_t>((T + 63) / 64, 1024);
   // Model: time ~ rounds x split length, rounds = ceil(workgroups / resident
@@ -1427,7 +1506,7 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
   for (int64_t c = std::max<int64_t>(min_s, 1); c <= max_s; ++c) {
     const int64_t len = mfma_split_len(T, static_cast<int>(c));
     if (len < 512 && c > min_s && c * 512 >= T) break;
-    const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu(len);
+    const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu(len, rc);
     const int64_t wg = groups * c;
     const int64_t rounds = (wg + slots - 1) / slots;
     const double cost = static_cast<double>(rounds) * static_cast<double>(len + 256) /
@@ -1456,29 +1535,30 @@ extern "C" int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
   return use_mfma(tb, d, t_stride, T, n_splits) ? 1 : 0;
 }
 
-extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
-                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
-                                     int32_t vbits, const float* pi, const float* kcent_host,
-                                     const float* vcent_host, const float* signs,
-                                     float qjl_scale, void* workspace, int64_t ws_bytes,
-                                     int32_t n_splits, void* stream) {
+// prepare for nl layers (B sequences each; the workspace holds B * nl)
+int prepare_layers(const QLayers& ql, int nl, int32_t q_dtype, int32_t B, int32_t Hq,
+                   int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+                   const float* kcent_host, const float* vcent_host, float qjl_scale,
+                   void* workspace, int64_t ws_bytes, int32_t n_splits, hipStream_t s) {
   QKV_REQUIRE(qkv_dtype_ok(q_dtype), "unsupported query dtype %d", q_dtype);
   QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  int st = validate_common(B * nl, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(q && pi && signs && kcent_host && vcent_host, "null pointer");
-  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  QKV_REQUIRE(kcent_host && vcent_host, "null pointer");
+  for (int l = 0; l < nl; ++l) {
+    QKV_REQUIRE(ql.q[l] && ql.pi[l] && ql.signs[l], "null pointer");
+    QKV_REQUIRE(qkv_aligned(ql.pi[l], 16), "pi must be 16-byte aligned");
+  }
   const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
+  const WsLayout L = ws_layout(B * nl, Hkv, R, d, n_splits);
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  auto s = static_cast<hipStream_t>(stream);
   if (tb.mfma_ok && (d == 128 || d == 64)) {
     // MFMA query operands; the same kernel writes q~ and w for the VALU kernel
     const int chunks = (R + kRowsM - 1) / kRowsM;
-    const dim3 grid(B * Hkv * chunks);
-#define QKV_PREP(DD, NPLV)                                                                     \
-  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), 0, s, q, q_dtype, pi, signs,  \
-                     qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),      \
+    const dim3 grid(B * nl * Hkv * chunks);
+#define QKV_PREP(DD, NPLV)                                                                   \
+  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), 0, s, ql, B, q_dtype,       \
+                     qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),    \
                      at<float>(workspace, L.rowc), at<float>(workspace, L.qw))
     if (d == 128) {
       if (kbits == 2) QKV_PREP(128, 3); else QKV_PREP(128, 2);
@@ -1489,11 +1569,17 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
     QKV_LAUNCHED();
     return QKV_OK;
   }
+  if (nl != 1) {
+    qkv_set_error("layer-batched decode runs on the MFMA path (symmetric codebooks, key MSE "
+                  "bits <= 2, head_dim 64 or 128)");
+    return QKV_E_UNSUPPORTED;
+  }
   switch (d) {
-#define QKV_CASE(DD)                                                                        \
-  case DD:                                                                                  \
-    hipLaunchKernelGGL(qrot_kernel<DD>, dim3(B * Hq * Q), dim3(128), 0, s, q, q_dtype, pi, \
-                       signs, qjl_scale, Hq, Hkv, Q, at<float>(workspace, L.qw));           \
+#define QKV_CASE(DD)                                                                          \
+  case DD:                                                                                    \
+    hipLaunchKernelGGL(qrot_kernel<DD>, dim3(B * Hq * Q), dim3(128), 0, s, ql.q[0], q_dtype,  \
+                       ql.pi[0], ql.signs[0], qjl_scale, Hq, Hkv, Q,                          \
+                       at<float>(workspace, L.qw));                                           \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -1502,6 +1588,21 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
   }
   QKV_LAUNCHED();
   return QKV_OK;
+}
+
+extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
+                                     int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                     int32_t vbits, const float* pi, const float* kcent_host,
+                                     const float* vcent_host, const float* signs,
+                                     float qjl_scale, void* workspace, int64_t ws_bytes,
+                                     int32_t n_splits, void* stream) {
+  QLayers ql{};
+  ql.q[0] = q;
+  ql.pi[0] = pi;
+  ql.signs[0] = signs;
+  return prepare_layers(ql, 1, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
+                        qjl_scale, workspace, ws_bytes, n_splits,
+                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int32_t B,
@@ -1538,9 +1639,102 @@ extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int3
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
   const int chunks = (R + kRowsM - 1) / kRowsM;
   auto s = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256), 0, s, q, q_dtype,
-                     pi_perm, pi_perm, 0.f, Hq, Hkv, Q, R, chunks, tb,
-                     at<qkv_v4i>(workspace, L.aq), at<float>(workspace, L.rowc), nullptr);
+  QLayers ql{};
+  ql.q[0] = q;
+  ql.pi[0] = pi_perm;
+  ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
+  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256), 0, s, ql, B,
+                     q_dtype, 0.f, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
+                     at<float>(workspace, L.rowc), nullptr);
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+// partial for nl layers (B sequences each)
+int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int32_t B,
+                   int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+                   const float* kcent_host, const float* vcent_host, float scale,
+                   int32_t causal, void* workspace, int64_t ws_bytes, int32_t n_splits,
+                   hipStream_t s) {
+  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
+  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
+  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
+              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
+              (long long)T);
+  int st = validate_common(B * nl, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  QKV_REQUIRE(kcent_host && vcent_host, "null pointer");
+  for (int l = 0; l < nl; ++l) {
+    QKV_REQUIRE(kv.kst[l] && kv.knorm[l] && kv.vst[l] && kv.vnorm[l], "null pointer");
+    QKV_REQUIRE(qkv_aligned(kv.kst[l], 4) && qkv_aligned(kv.vst[l], 4),
+                "store must be 4-byte aligned");
+  }
+  const int R = (Hq / Hkv) * Q;
+  const WsLayout L = ws_layout(B * nl, Hkv, R, d, n_splits);
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  float* po = at<float>(workspace, L.po);
+  float* pml = at<float>(workspace, L.pml);
+  if (use_mfma(tb, d, t_stride, T, n_splits)) {
+    const int chunks = (R + kRowsM - 1) / kRowsM;
+    const int rc = mfma_rc(d, R);
+    const int64_t split_len = mfma_split_len(T, n_splits);
+    const int64_t smem = mfma_smem_bytes(split_len, rc);
+    const dim3 grid(n_splits, Hkv * ((chunks + rc - 1) / rc), B * nl);
+    const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
+    const float* rowc = at<float>(workspace, L.rowc);
+#define QKV_MF(DD, MB, VB, RCV)                                                                \
+  do {                                                                                         \
+    if (smem > 65536)                                                                          \
+      QKV_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&split_mfma<DD, MB, VB, RCV>), \
+                                  hipFuncAttributeMaxDynamicSharedMemorySize,                  \
+                                  static_cast<int>(smem)));                                    \
+    hipLaunchKernelGGL((split_mfma<DD, MB, VB, RCV>), grid, dim3(256),                         \
+                       static_cast<uint32_t>(smem), s, aq, rowc, kv, B, t_stride, T, Hkv, R,   \
+                       Q, chunks, scale, causal, split_len, tb, po, pml);                      \
+  } while (0)
+#define QKV_MFD(DD, RCV)                           \
+  switch (kbits * 10 + vbits) {                    \
+    case 11: QKV_MF(DD, 1, 1, RCV); break;         \
+    case 12: QKV_MF(DD, 1, 2, RCV); break;         \
+    case 13: QKV_MF(DD, 1, 3, RCV); break;         \
+    case 14: QKV_MF(DD, 1, 4, RCV); break;         \
+    case 21: QKV_MF(DD, 2, 1, RCV); break;         \
+    case 22: QKV_MF(DD, 2, 2, RCV); break;         \
+    case 23: QKV_MF(DD, 2, 3, RCV); break;         \
+    case 24: QKV_MF(DD, 2, 4, RCV); break;         \
+  }
+    if (d == 128) {
+      QKV_MFD(128, 1)
+    } else if (rc == 2) {
+      QKV_MFD(64, 2)
+    } else {
+      QKV_MFD(64, 1)
+    }
+#undef QKV_MFD
+#undef QKV_MF
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
+  if (nl != 1) {
+    qkv_set_error("layer-batched decode runs on the MFMA path (store capacity a multiple of "
+                  "64, splits of at most %d tokens)", kSplitMax);
+    return QKV_E_UNSUPPORTED;
+  }
+  const int chunks = (R + kRowsG - 1) / kRowsG;
+  const int64_t split_len = ((T + n_splits - 1) / n_splits + kTileG - 1) / kTileG * kTileG;
+  const float* qw = at<float>(workspace, L.qw);
+  switch (d) {
+#define QKV_CASE(DD)                                                                           \
+  case DD:                                                                                     \
+    hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
+                       qw, kv.kst[0], kv.knorm[0], kv.vst[0], kv.vnorm[0], t_stride, T, Hkv,   \
+                       R, Q, chunks, kbits, vbits, tb, scale, causal, split_len, po, pml);     \
+    break;
+    QKV_CASE(64)
+    QKV_CASE(96)
+    QKV_CASE(128)
+#undef QKV_CASE
+  }
   QKV_LAUNCHED();
   return QKV_OK;
 }
@@ -1553,62 +1747,45 @@ extern "C" int qkv_attention_partial(const uint8_t* kstore, const float* knorm,
                                      const float* vcent_host, float scale, int32_t causal,
                                      void* workspace, int64_t ws_bytes, int32_t n_splits,
                                      void* stream) {
-  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
-  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
-  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
-              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
-              (long long)T);
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  KVLayers kv{};
+  kv.kst[0] = kstore;
+  kv.knorm[0] = knorm;
+  kv.vst[0] = vstore;
+  kv.vnorm[0] = vnorm;
+  return partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
+                        vcent_host, scale, causal, workspace, ws_bytes, n_splits,
+                        static_cast<hipStream_t>(stream));
+}
+
+// combine for nl layers (B sequences each)
+int combine_layers(const OutLayers& ol, int nl, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                   int32_t d, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+                   int32_t n_splits, hipStream_t s) {
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
+  int st = validate_common(B * nl, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
-  QKV_REQUIRE(kstore && knorm && vstore && vnorm && kcent_host && vcent_host, "null pointer");
-  QKV_REQUIRE(qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4), "store must be 4-byte aligned");
+  for (int l = 0; l < nl; ++l) {
+    QKV_REQUIRE(ol.pi[l] && ol.out[l], "null pointer");
+    QKV_REQUIRE(qkv_aligned(ol.pi[l], 16), "pi must be 16-byte aligned");
+  }
   const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
-  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  float* po = at<float>(workspace, L.po);
-  float* pml = at<float>(workspace, L.pml);
-  auto s = static_cast<hipStream_t>(stream);
-  if (use_mfma(tb, d, t_stride, T, n_splits)) {
-    const int chunks = (R + kRowsM - 1) / kRowsM;
-    const int64_t split_len = mfma_split_len(T, n_splits);
-    const dim3 grid(n_splits, Hkv * chunks, B);
-    const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
-    const float* rowc = at<float>(workspace, L.rowc);
-#define QKV_MF(DD, MB, VB)                                                                   \
-  hipLaunchKernelGGL((split_mfma<DD, MB, VB>), grid, dim3(256),                            \
-                     static_cast<uint32_t>(mfma_smem_bytes(split_len)), s, aq, rowc, kstore,  \
-                     knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, scale, causal,    \
-                     split_len, tb, po, pml)
-#define QKV_MFD(DD)                           \
-  switch (kbits * 10 + vbits) {               \
-    case 11: QKV_MF(DD, 1, 1); break;         \
-    case 12: QKV_MF(DD, 1, 2); break;         \
-    case 13: QKV_MF(DD, 1, 3); break;         \
-    case 14: QKV_MF(DD, 1, 4); break;         \
-    case 21: QKV_MF(DD, 2, 1); break;         \
-    case 22: QKV_MF(DD, 2, 2); break;         \
-    case 23: QKV_MF(DD, 2, 3); break;         \
-    case 24: QKV_MF(DD, 2, 4); break;         \
-  }
-    if (d == 128) {
-      QKV_MFD(128)
-    } else {
-      QKV_MFD(64)
-    }
-#undef QKV_MFD
-#undef QKV_MF
-    QKV_LAUNCHED();
-    return QKV_OK;
-  }
-  const int chunks = (R + kRowsG - 1) / kRowsG;
-  const int64_t split_len = ((T + n_splits - 1) / n_splits + kTileG - 1) / kTileG * kTileG;
-  const float* qw = at<float>(workspace, L.qw);
+  const WsLayout L = ws_layout(B * nl, Hkv, R, d, n_splits);
+  const int64_t nrl = int64_t(B) * Hkv * R;  // rows per layer
+  // few rows: one per workgroup (more workgroups over the splits); many rows:
+  // four per workgroup (each Pi load serves four)
+  const bool wide = nrl * nl < int64_t(kRowsC) * qkv_num_cus();
+  const dim3 cgrid(static_cast<int>(wide ? nrl : (nrl + kRowsC - 1) / kRowsC), nl);
+  const float* po = at<float>(workspace, L.po);
+  const float* pml = at<float>(workspace, L.pml);
   switch (d) {
-#define QKV_CASE(DD)                                                                           \
-  case DD:                                                                                     \
-    hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
-                       qw, kstore, knorm, vstore, vnorm, t_stride, T, Hkv, R, Q, chunks, kbits, \
-                       vbits, tb, scale, causal, split_len, po, pml);                          \
+#define QKV_CASE(DD)                                                                          \
+  case DD:                                                                                    \
+    if (wide)                                                                                 \
+      hipLaunchKernelGGL((combine_kernel<DD, 1>), cgrid, dim3(2 * DD), 0, s, po, pml, ol,     \
+                         n_splits, B, Hkv, R, Q, Hq, out_dtype);                              \
+    else                                                                                      \
+      hipLaunchKernelGGL((combine_kernel<DD, kRowsC>), cgrid, dim3(2 * DD), 0, s, po, pml,    \
+                         ol, n_splits, B, Hkv, R, Q, Hq, out_dtype);                          \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -1623,38 +1800,11 @@ extern "C" int qkv_attention_combine(int32_t B, int32_t Hq, int32_t Hkv, int32_t
                                      const float* pi, void* out, int32_t out_dtype,
                                      void* workspace, int64_t ws_bytes, int32_t n_splits,
                                      void* stream) {
-  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
-  if (st != QKV_OK) return st;
-  QKV_REQUIRE(pi && out, "null pointer");
-  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
-  const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
-  auto s = static_cast<hipStream_t>(stream);
-  const int64_t nrows = int64_t(B) * Hkv * R;
-  // few rows: one per workgroup (more workgroups over the splits); many rows:
-  // four per workgroup (each Pi load serves four)
-  const bool wide = nrows < int64_t(kRowsC) * qkv_num_cus();
-  const dim3 cgrid(static_cast<int>(wide ? nrows : (nrows + kRowsC - 1) / kRowsC));
-  const float* po = at<float>(workspace, L.po);
-  const float* pml = at<float>(workspace, L.pml);
-  switch (d) {
-#define QKV_CASE(DD)                                                                          \
-  case DD:                                                                                    \
-    if (wide)                                                                                 \
-      hipLaunchKernelGGL((combine_kernel<DD, 1>), cgrid, dim3(2 * DD), 0, s, po, pml, pi,     \
-                         n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                         \
-    else                                                                                      \
-      hipLaunchKernelGGL((combine_kernel<DD, kRowsC>), cgrid, dim3(2 * DD), 0, s, po, pml,    \
-                         pi, n_splits, B, Hkv, R, Q, Hq, out, out_dtype);                     \
-    break;
-    QKV_CASE(64)
-    QKV_CASE(96)
-    QKV_CASE(128)
-#undef QKV_CASE
-  }
-  QKV_LAUNCHED();
-  return QKV_OK;
+  OutLayers ol{};
+  ol.pi[0] = pi;
+  ol.out[0] = out;
+  return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits,
+                        static_cast<hipStream_t>(stream));
 }
 
 extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
@@ -1703,6 +1853,65 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
                            vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
                            workspace, ws_bytes, n_splits, stream);
+}
+
+// One decode step over n_layers layers that share shapes, bit widths and
+// codebooks (a model's layers), as three launches instead of 3 n_layers.
+// Per-layer device pointers come in HOST arrays of n_layers entries; the
+// workspace is sized for a batch of B * n_layers sequences.  Only the MFMA
+// path takes layers (symmetric codebooks, key MSE bits <= 2, d = 64 or 128,
+// store capacity a multiple of 64, splits of at most 2048 tokens).
+extern "C" int qkv_decode_attention_layers(
+    int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kstore,
+    const float* const* knorm, const uint32_t* const* vstore, const float* const* vnorm,
+    int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+    int32_t kbits, int32_t vbits, const float* const* pi, const float* kcent_host,
+    const float* vcent_host, const float* const* signs, float qjl_scale, float scale,
+    int32_t causal, void* const* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+    int32_t n_splits, void* stream) {
+  QKV_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, "n_layers %d not in 1..%d", n_layers,
+              kMaxLayers);
+  QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && signs && out && kcent_host &&
+                  vcent_host,
+              "null pointer");
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
+  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
+  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
+  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
+              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
+              (long long)T);
+  int st = validate_common(B * n_layers, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  if (!use_mfma(tb, d, t_stride, T, n_splits)) {
+    qkv_set_error("layer-batched decode runs on the MFMA path (symmetric codebooks, key MSE "
+                  "bits <= 2, head_dim 64 or 128, capacity a multiple of 64, splits of at "
+                  "most %d tokens)", kSplitMax);
+    return QKV_E_UNSUPPORTED;
+  }
+  QLayers ql{};
+  KVLayers kv{};
+  OutLayers ol{};
+  for (int l = 0; l < n_layers; ++l) {
+    ql.q[l] = q[l];
+    ql.pi[l] = pi[l];
+    ql.signs[l] = signs[l];
+    kv.kst[l] = kstore[l];
+    kv.knorm[l] = knorm[l];
+    kv.vst[l] = vstore[l];
+    kv.vnorm[l] = vnorm[l];
+    ol.pi[l] = pi[l];
+    ol.out[l] = out[l];
+  }
+  auto s = static_cast<hipStream_t>(stream);
+  st = prepare_layers(ql, n_layers, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
+                      vcent_host, qjl_scale, workspace, ws_bytes, n_splits, s);
+  if (st != QKV_OK) return st;
+  st = partial_layers(kv, n_layers, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
+                      vcent_host, scale, causal, workspace, ws_bytes, n_splits, s);
+  if (st != QKV_OK) return st;
+  return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
+                        n_splits, s);
 }
 
 // Decode attention over mixed-precision K rows (3-bit outlier / 2-bit regular
@@ -1878,9 +2087,13 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
     ssrc = sp;
   }
   // query operands: the decode prepare kernel with one "kv head" of M rows
-#define QKV_PREP(NPLV)                                                                           \
-  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256), 0, s, qsrc, qdt, pisrc, \
-                     ssrc, qjl_scale, M, 1, 1, M, chunks, tb, aq, rowc, nullptr)
+  QLayers ql{};
+  ql.q[0] = qsrc;
+  ql.pi[0] = pisrc;
+  ql.signs[0] = ssrc;
+#define QKV_PREP(NPLV)                                                                        \
+  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256), 0, s, ql, 1, qdt,    \
+                     qjl_scale, M, 1, 1, M, chunks, tb, aq, rowc, nullptr)
   if (mbits == 1) QKV_PREP(2);
   else if (mbits == 2) QKV_PREP(3);
   else QKV_PREP(5);

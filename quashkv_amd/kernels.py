@@ -193,6 +193,72 @@ def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
     return out
 
 
+def attention_layers(engines: Sequence, queries: Sequence[torch.Tensor],
+                     scale: Optional[float] = None, causal: bool = False,
+                     out_dtype: torch.dtype = torch.float32,
+                     workspace: Optional[torch.Tensor] = None,
+                     n_splits: Optional[int] = None) -> list[torch.Tensor]:
+    """One decode step over several layers' engines at once
+    (qkv_decode_attention_layers): ``queries[l]`` (B, Hq, Q, d) attends the
+    whole cache of ``engines[l]``; every engine must share head_dim, bit
+    widths, batch, kv heads, cached length and store capacity (a model's
+    layers).  Returns one output per layer, as ``engines[l].attention`` would."""
+    n = len(engines)
+    if n == 0 or n != len(queries):
+        raise ValueError("one query per engine, at least one engine")
+    if n > 32:
+        raise ValueError("at most 32 layers per call")
+    e0 = engines[0]
+    st0 = e0._store
+    if st0 is None or e0.total_tokens == 0:
+        raise ValueError("No compressed KV blocks in cache. Call append() first.")
+    T = e0.total_tokens
+    for e in engines:
+        st = e._store
+        if (st is None or e._kmix or e.head_dim != e0.head_dim or e.key_bits != e0.key_bits
+                or e.value_bits != e0.value_bits or e.total_tokens != T
+                or (st.B, st.H, st.capacity) != (st0.B, st0.H, st0.capacity)):
+            raise ValueError("attention_layers needs engines of one shape, bit widths and "
+                             "cached length")
+    q0 = queries[0]
+    dev = N.require_gpu(q0, st0.kst, what="attention_layers")
+    B, Hq, Q, d = q0.shape
+    Hkv = st0.H
+    if B != st0.B or d != e0.head_dim or Hq % Hkv != 0:
+        raise ValueError(f"queries {tuple(q0.shape)} do not match the cache "
+                         f"(B={st0.B}, kv heads={Hkv}, head_dim={e0.head_dim})")
+    dt = q0.dtype if q0.dtype in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
+    if any(q.shape != q0.shape for q in queries):
+        raise ValueError("queries of one shape")
+    qs = [q.to(dt).contiguous() for q in queries]
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    L = N.lib()
+    if n_splits is None:
+        n_splits = L.qkv_attention_splits(B * n, Hq, Hkv, Q, d, T)
+    need = L.qkv_attention_workspace_bytes(B * n, Hq, Hkv, Q, d, n_splits)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+    kq = [e.key_quantizer for e in engines]
+    pis = [N.dense(k.mse_quantizer.Pi)[0] for k in kq]
+    sgs = [N.dense(k.S)[0] for k in kq]
+    outs = [torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev) for _ in range(n)]
+    kc = N.HostFloats(kq[0].mse_quantizer.codebook.centroids_host)
+    vc = N.HostFloats(e0.value_quantizer.codebook.centroids_host)
+    arr = N.ptr_array
+    stores = [e._store for e in engines]
+    N.check(L.qkv_decode_attention_layers(
+        n, arr([q.data_ptr() for q in qs]), N.dtype_code(qs[0].dtype),
+        arr([st.kst.data_ptr() for st in stores]), arr([st.knorm.data_ptr() for st in stores]),
+        arr([st.vst.data_ptr() for st in stores]), arr([st.vnorm.data_ptr() for st in stores]),
+        st0.capacity, T, B, Hq, Hkv, Q, d, st0.mbits, st0.vbits,
+        arr([p.data_ptr() for p in pis]), kc.ptr, vc.ptr, arr([x.data_ptr() for x in sgs]),
+        float(kq[0].qjl_scale), float(scale), 1 if causal else 0,
+        arr([o.data_ptr() for o in outs]), N.dtype_code(out_dtype), workspace.data_ptr(),
+        workspace.numel(), n_splits, N.stream(dev)))
+    return outs
+
+
 def _bits_of(centroids: torch.Tensor) -> int:
     n = centroids.numel()
     b = max(1, int(math.ceil(math.log2(max(n, 2)))))

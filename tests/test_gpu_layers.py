@@ -1,0 +1,85 @@
+"""GPU parity of the layer-batched decode step (qkv_decode_attention_layers):
+several layers' engines (own Pi, S, store, query) attended in three launches
+agree with each layer's own decode call and with the oracle."""
+
+import pytest
+import torch
+
+import quashkv_amd as Q
+from quashkv_amd import _native as N
+from quashkv_amd import kernels as K
+from oracle import ref_math as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+    N.lib()
+
+
+def _close(a, b, rel):
+    a, b = a.detach().cpu().double(), b.detach().cpu().double()
+    err = float((a - b).norm() / b.norm())
+    assert err <= rel, err
+
+
+@pytest.mark.parametrize("d,G,Qn,causal", [(64, 7, 1, False), (128, 4, 1, False),
+                                            (128, 2, 3, True)])
+def test_layers_match_per_layer_and_oracle(d, G, Qn, causal):
+    gen = torch.Generator().manual_seed(d + G)
+    n, B, Hkv, T = 5, 3, 2, 700
+    engines = [Q.QuashKVEngine(head_dim=d, seed=42 + l, device=DEV) for l in range(n)]
+    for e in engines:
+        k = torch.randn(B, Hkv, T, d, generator=gen) * torch.exp(0.5 * torch.randn(B, Hkv, T, 1, generator=gen))
+        v = torch.randn(B, Hkv, T, d, generator=gen)
+        e.append(k[:, :, :300].to(DEV, torch.float16), v[:, :, :300].to(DEV, torch.float16))
+        e.append(k[:, :, 300:].to(DEV, torch.float16), v[:, :, 300:].to(DEV, torch.float16))
+    qs = [torch.randn(B, Hkv * G, Qn, d, generator=gen).to(DEV, torch.float16) for _ in range(n)]
+    L = N.lib()
+    ns = L.qkv_attention_splits(B * n, Hkv * G, Hkv, Qn, d, T)
+    outs = K.attention_layers(engines, qs, causal=causal, n_splits=ns)
+    assert len(outs) == n and outs[0].shape == (B, Hkv * G, Qn, d)
+    for e, q, o in zip(engines, qs, outs):
+        st, kq, vq = e._store, e.key_quantizer, e.value_quantizer
+        ref = K.attention_store(q, st, T, kq.mse_quantizer.Pi, kq.mse_quantizer.codebook.centroids_host,
+                                vq.codebook.centroids_host, kq.S, kq.qjl_scale, causal=causal,
+                                n_splits=ns)
+        _close(o, ref, 1e-6)
+    # one layer against the oracle on its stored codes
+    e, q, o = engines[2], qs[2], outs[2]
+    st, kq, vq = e._store, e.key_quantizer, e.value_quantizer
+    kc, kb, vc = st.read_codes(0, T)
+    blocks = [dict(kcodes=kc.cpu(), kbits=kb.cpu(), knorm=st.knorm[:, :, :T].cpu(),
+                   vcodes=vc.cpu(), vnorm=st.vnorm[:, :, :T].cpu())]
+    args = (kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
+            vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
+    if causal:
+        qg = q.float().cpu().reshape(B, Hkv, G, Qn, d)
+        ref = torch.stack([R.attention_naive(qg[:, :, g], blocks, *args, causal=True)
+                           for g in range(G)], dim=2).reshape(B, Hkv * G, Qn, d)
+    else:
+        ref = R.attention_online(q.float().cpu().reshape(B, Hkv, G * Qn, d), blocks,
+                                 *args).reshape(B, Hkv * G, Qn, d)
+    _close(o, ref, 2e-5)
+
+
+def test_layers_default_splits_and_errors():
+    gen = torch.Generator().manual_seed(1)
+    engines = [Q.QuashKVEngine(head_dim=64, seed=7 + l, device=DEV) for l in range(3)]
+    for e in engines:
+        x = torch.randn(2, 2, 130, 64, generator=gen).to(DEV, torch.float16)
+        e.append(x, x)
+    qs = [torch.randn(2, 14, 1, 64, generator=gen).to(DEV, torch.float16) for _ in range(3)]
+    outs = K.attention_layers(engines, qs)
+    for e, q, o in zip(engines, qs, outs):
+        _close(o, e.attention(q), 2e-5)
+    engines[1].append(x[:, :, :1], x[:, :, :1])     # lengths differ
+    with pytest.raises(ValueError, match="one shape"):
+        K.attention_layers(engines, qs)
+    with pytest.raises(ValueError, match="one query per engine"):
+        K.attention_layers(engines[:2], qs)

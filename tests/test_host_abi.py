@@ -115,6 +115,21 @@ def test_kmixed_host_validation():
     assert st == N.QKV_E_UNSUPPORTED and "multiple of 64" in lib.qkv_last_error().decode()
 
 
+def test_layers_host_validation():
+    lib = N.lib()
+    a = N.ptr_array([256] * 33)
+    kc = N.HostFloats(LloydMaxCodebook(64, 2).centroids_host)
+    vc = N.HostFloats(LloydMaxCodebook(64, 3).centroids_host)
+    args = lambda n, k: (n, a, 0, a, a, a, a, 128, 100, 1, 8, 8, 1, 64, 2, 3, a, k.ptr, vc.ptr,
+                         a, 0.1, 0.1, 0, a, 0, 256, 1 << 30, 1, None)
+    assert lib.qkv_decode_attention_layers(*args(0, kc)) == N.QKV_E_INVALID
+    assert lib.qkv_decode_attention_layers(*args(33, kc)) == N.QKV_E_INVALID
+    assert "n_layers" in lib.qkv_last_error().decode()
+    asym = N.HostFloats([-1.0, -0.25, 0.5, 1.0])
+    assert lib.qkv_decode_attention_layers(*args(2, asym)) == N.QKV_E_UNSUPPORTED
+    assert "MFMA path" in lib.qkv_last_error().decode()
+
+
 def test_mips_host_validation():
     lib = N.lib()
     assert lib.qkv_mips_workspace_bytes(10, 80, 2, 10, 100) == -1      # dim
