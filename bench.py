@@ -217,8 +217,6 @@ def bench_cfg2(args) -> None:
     torch.cuda.synchronize()
     lib = N.lib()
     splits = lib.qkv_attention_splits(B2 * NL, HQ2, HKV2, 1, D2, T2)
-    ws = torch.empty(lib.qkv_attention_workspace_bytes(B2 * NL, HQ2, HKV2, 1, D2, splits),
-                     dtype=torch.uint8, device=dev)
     flush = torch.empty(512 * 1024 * 1024 // 4, device=dev)
 
     def timed(fn, reps):
@@ -233,7 +231,8 @@ def bench_cfg2(args) -> None:
             ts.append(e0.elapsed_time(e1))
         return ts
 
-    step = lambda: K.attention_layers(engines, qs, workspace=ws, n_splits=splits)
+    batch = K.LayerBatch(engines)
+    step = lambda: batch(qs, n_splits=splits)
     timed(step, args.warmup)
     ms = statistics.median(timed(step, args.steps))
     outs = step()
@@ -248,7 +247,7 @@ def bench_cfg2(args) -> None:
     def with_append():
         for e in engines:
             e.append(k1[0], k1[1])
-        return K.attention_layers(engines, qs, workspace=ws, n_splits=splits)
+        return batch(qs, n_splits=splits)
 
     ms_app = statistics.median(timed(with_append, 5))
     alg = NL * B2 * HKV2 * T2 * 56

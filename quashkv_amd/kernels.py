@@ -193,70 +193,111 @@ def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
     return out
 
 
+class LayerBatch:
+    """Layer-batched decode over a fixed list of engines (a model's layers:
+    one head_dim, bit widths, batch and kv heads), through
+    qkv_decode_attention_layers.  Per-layer constants (Pi, S, codebook tables)
+    and the workspace are prepared once; each call reads the current stores,
+    so appends between calls are seen.  ``batch(queries)`` returns one
+    (B, Hq, Q, d) output per layer, as ``engines[l].attention(queries[l])``."""
+
+    def __init__(self, engines: Sequence):
+        n = len(engines)
+        if n == 0 or n > 32:
+            raise ValueError("1 to 32 engines per layer batch")
+        e0 = engines[0]
+        for e in engines:
+            if (e._kmix or e.head_dim != e0.head_dim or e.key_bits != e0.key_bits
+                    or e.value_bits != e0.value_bits):
+                raise ValueError("attention_layers needs engines of one shape, bit widths and "
+                                 "cached length")
+        self.engines = list(engines)
+        kq = [e.key_quantizer for e in engines]
+        self._pi = [N.dense(k.mse_quantizer.Pi)[0] for k in kq]
+        self._s = [N.dense(k.S)[0] for k in kq]
+        self._pi_arr = N.ptr_array([t.data_ptr() for t in self._pi])
+        self._s_arr = N.ptr_array([t.data_ptr() for t in self._s])
+        self._kc = N.HostFloats(kq[0].mse_quantizer.codebook.centroids_host)
+        self._vc = N.HostFloats(e0.value_quantizer.codebook.centroids_host)
+        self._qjl = float(kq[0].qjl_scale)
+        self._ws: Optional[torch.Tensor] = None
+        self._stores = None   # (key, four pointer arrays) of the stores last seen
+
+    def _store_arrays(self):
+        sts = [e._store for e in self.engines]
+        ptrs = tuple(tuple(getattr(st, f).data_ptr() for st in sts)
+                     for f in ("kst", "knorm", "vst", "vnorm"))
+        if self._stores is None or self._stores[0] != ptrs:
+            self._stores = (ptrs, tuple(N.ptr_array(p) for p in ptrs))
+        return self._stores[1]
+
+    def __call__(self, queries: Sequence[torch.Tensor], scale: Optional[float] = None,
+                 causal: bool = False, out_dtype: torch.dtype = torch.float32,
+                 n_splits: Optional[int] = None) -> list[torch.Tensor]:
+        engines = self.engines
+        n = len(engines)
+        if len(queries) != n:
+            raise ValueError("one query per engine, at least one engine")
+        e0 = engines[0]
+        st0 = e0._store
+        T = e0.total_tokens
+        if st0 is None or T == 0:
+            raise ValueError("No compressed KV blocks in cache. Call append() first.")
+        for e in engines:
+            st = e._store
+            if (st is None or e.total_tokens != T
+                    or (st.B, st.H, st.capacity) != (st0.B, st0.H, st0.capacity)):
+                raise ValueError("attention_layers needs engines of one shape, bit widths and "
+                                 "cached length")
+        q0 = queries[0]
+        dev = N.require_gpu(q0, st0.kst, what="attention_layers")
+        B, Hq, Q, d = q0.shape
+        Hkv = st0.H
+        if B != st0.B or d != e0.head_dim or Hq % Hkv != 0:
+            raise ValueError(f"queries {tuple(q0.shape)} do not match the cache "
+                             f"(B={st0.B}, kv heads={Hkv}, head_dim={e0.head_dim})")
+        if any(q.shape != q0.shape for q in queries):
+            raise ValueError("queries of one shape")
+        dt = q0.dtype if q0.dtype in (torch.float32, torch.float16, torch.bfloat16) \
+            else torch.float32
+        qs = [q if (q.dtype == dt and q.is_contiguous()) else q.to(dt).contiguous()
+              for q in queries]
+        if scale is None:
+            scale = 1.0 / math.sqrt(d)
+        L = N.lib()
+        if n_splits is None:
+            n_splits = L.qkv_attention_splits(B * n, Hq, Hkv, Q, d, T)
+        need = L.qkv_attention_workspace_bytes(B * n, Hq, Hkv, Q, d, n_splits)
+        if self._ws is None or self._ws.numel() < need or self._ws.device != dev:
+            self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        out = torch.empty(n, B, Hq, Q, d, dtype=out_dtype, device=dev)
+        step = out[0].numel() * out.element_size()
+        kst, knorm, vst, vnorm = self._store_arrays()
+        N.check(L.qkv_decode_attention_layers(
+            n, N.ptr_array([q.data_ptr() for q in qs]), N.dtype_code(dt), kst, knorm, vst,
+            vnorm, st0.capacity, T, B, Hq, Hkv, Q, d, st0.mbits, st0.vbits, self._pi_arr,
+            self._kc.ptr, self._vc.ptr, self._s_arr, self._qjl, float(scale),
+            1 if causal else 0, N.ptr_array([out.data_ptr() + l * step for l in range(n)]),
+            N.dtype_code(out_dtype), self._ws.data_ptr(), self._ws.numel(), n_splits,
+            N.stream(dev)))
+        return list(out.unbind(0))
+
+
 def attention_layers(engines: Sequence, queries: Sequence[torch.Tensor],
                      scale: Optional[float] = None, causal: bool = False,
                      out_dtype: torch.dtype = torch.float32,
-                     workspace: Optional[torch.Tensor] = None,
                      n_splits: Optional[int] = None) -> list[torch.Tensor]:
     """One decode step over several layers' engines at once
     (qkv_decode_attention_layers): ``queries[l]`` (B, Hq, Q, d) attends the
     whole cache of ``engines[l]``; every engine must share head_dim, bit
     widths, batch, kv heads, cached length and store capacity (a model's
-    layers).  Returns one output per layer, as ``engines[l].attention`` would."""
-    n = len(engines)
-    if n == 0 or n != len(queries):
+    layers).  Returns one output per layer, as ``engines[l].attention`` would.
+    A decode loop keeps a ``LayerBatch`` instead, which prepares the per-layer
+    constants once."""
+    if len(engines) != len(queries):
         raise ValueError("one query per engine, at least one engine")
-    if n > 32:
-        raise ValueError("at most 32 layers per call")
-    e0 = engines[0]
-    st0 = e0._store
-    if st0 is None or e0.total_tokens == 0:
-        raise ValueError("No compressed KV blocks in cache. Call append() first.")
-    T = e0.total_tokens
-    for e in engines:
-        st = e._store
-        if (st is None or e._kmix or e.head_dim != e0.head_dim or e.key_bits != e0.key_bits
-                or e.value_bits != e0.value_bits or e.total_tokens != T
-                or (st.B, st.H, st.capacity) != (st0.B, st0.H, st0.capacity)):
-            raise ValueError("attention_layers needs engines of one shape, bit widths and "
-                             "cached length")
-    q0 = queries[0]
-    dev = N.require_gpu(q0, st0.kst, what="attention_layers")
-    B, Hq, Q, d = q0.shape
-    Hkv = st0.H
-    if B != st0.B or d != e0.head_dim or Hq % Hkv != 0:
-        raise ValueError(f"queries {tuple(q0.shape)} do not match the cache "
-                         f"(B={st0.B}, kv heads={Hkv}, head_dim={e0.head_dim})")
-    dt = q0.dtype if q0.dtype in (torch.float32, torch.float16, torch.bfloat16) else torch.float32
-    if any(q.shape != q0.shape for q in queries):
-        raise ValueError("queries of one shape")
-    qs = [q.to(dt).contiguous() for q in queries]
-    if scale is None:
-        scale = 1.0 / math.sqrt(d)
-    L = N.lib()
-    if n_splits is None:
-        n_splits = L.qkv_attention_splits(B * n, Hq, Hkv, Q, d, T)
-    need = L.qkv_attention_workspace_bytes(B * n, Hq, Hkv, Q, d, n_splits)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
-    kq = [e.key_quantizer for e in engines]
-    pis = [N.dense(k.mse_quantizer.Pi)[0] for k in kq]
-    sgs = [N.dense(k.S)[0] for k in kq]
-    outs = [torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev) for _ in range(n)]
-    kc = N.HostFloats(kq[0].mse_quantizer.codebook.centroids_host)
-    vc = N.HostFloats(e0.value_quantizer.codebook.centroids_host)
-    arr = N.ptr_array
-    stores = [e._store for e in engines]
-    N.check(L.qkv_decode_attention_layers(
-        n, arr([q.data_ptr() for q in qs]), N.dtype_code(qs[0].dtype),
-        arr([st.kst.data_ptr() for st in stores]), arr([st.knorm.data_ptr() for st in stores]),
-        arr([st.vst.data_ptr() for st in stores]), arr([st.vnorm.data_ptr() for st in stores]),
-        st0.capacity, T, B, Hq, Hkv, Q, d, st0.mbits, st0.vbits,
-        arr([p.data_ptr() for p in pis]), kc.ptr, vc.ptr, arr([x.data_ptr() for x in sgs]),
-        float(kq[0].qjl_scale), float(scale), 1 if causal else 0,
-        arr([o.data_ptr() for o in outs]), N.dtype_code(out_dtype), workspace.data_ptr(),
-        workspace.numel(), n_splits, N.stream(dev)))
-    return outs
+    return LayerBatch(engines)(queries, scale=scale, causal=causal, out_dtype=out_dtype,
+                               n_splits=n_splits)
 
 
 def _bits_of(centroids: torch.Tensor) -> int:

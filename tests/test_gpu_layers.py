@@ -83,3 +83,24 @@ def test_layers_default_splits_and_errors():
         K.attention_layers(engines, qs)
     with pytest.raises(ValueError, match="one query per engine"):
         K.attention_layers(engines[:2], qs)
+
+
+def test_layer_batch_follows_appends_and_store_growth():
+    """A LayerBatch kept across decode steps sees each step's appends, also
+    when an append reallocates the stores (capacity doubling)."""
+    gen = torch.Generator().manual_seed(2)
+    engines = [Q.QuashKVEngine(head_dim=64, seed=11 + l, device=DEV) for l in range(4)]
+    for e in engines:
+        x = torch.randn(2, 2, 100, 64, generator=gen).to(DEV, torch.float16)
+        e.append(x, x)
+    batch = K.LayerBatch(engines)
+    caps = [e._store.capacity for e in engines]
+    for step in range(3):
+        qs = [torch.randn(2, 14, 1, 64, generator=gen).to(DEV, torch.float16) for _ in range(4)]
+        outs = batch(qs)
+        for e, q, o in zip(engines, qs, outs):
+            _close(o, e.attention(q), 2e-5)
+        for e in engines:   # 60 more tokens per step: the stores outgrow their capacity
+            x = torch.randn(2, 2, 60, 64, generator=gen).to(DEV, torch.float16)
+            e.append(x, x)
+    assert engines[0]._store.capacity > caps[0]
