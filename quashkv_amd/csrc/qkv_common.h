@@ -150,3 +150,30 @@ __device__ __forceinline__ T qkv_wave_max(T v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+
+// ------------------------------------------------ decompress (shared host side)
+
+// Arguments of one decompress call (validated by the C ABI entry points).
+struct QkvDecompressArgs {
+  int mode, fmt;
+  const uint8_t* codes;
+  const uint8_t* qjl;
+  const float* norms;
+  int64_t n;
+  int d, bits;
+  const float* pi;
+  const float* cents;
+  const float* signs;
+  float qjl_scale;
+  int64_t in_seq, in_gstride;
+  void* out;
+  int out_dtype;
+  const uint8_t* sel;  // mixed precision: per-coordinate codebook selector
+  const float* alt_cents;
+  int alt_bits;
+};
+
+// The MFMA decompress kernels take d = 64 / 128 with aligned operands;
+// qkv_decompress_mfma launches them.
+bool qkv_decompress_mfma_ok(const QkvDecompressArgs& a);
+int qkv_decompress_mfma(const QkvDecompressArgs& a, hipStream_t s);

@@ -289,6 +289,15 @@ static int decompress_impl(int32_t mode, int32_t fmt, const uint8_t* codes,
   else
     QKV_REQUIRE(in_seq > 0 && in_group_stride >= in_seq, "bad grouped-row layout");
   auto s = static_cast<hipStream_t>(stream);
+  const QkvDecompressArgs args{mode,      fmt,     codes,   qjl,       norms,    n,
+                               d,         bits,    pi,      centroids, signs,    qjl_scale,
+                               in_seq,    in_group_stride,  out,       out_dtype, sel,
+                               alt_cents, alt_bits};
+  if (qkv_decompress_mfma_ok(args)) {
+    qkv_decompress_mfma(args, s);
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
   switch (d) {
 #define QKV_CASE(DD)                                                                         \
   case DD:                                                                                   \
