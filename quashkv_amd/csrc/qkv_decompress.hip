@@ -46,6 +46,8 @@ namespace {
 
 typedef _Float16 qkv_f16x8 __attribute__((ext_vector_type(8)));
 typedef float qkv_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t qkv_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t qkv_u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -222,121 +224,161 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
   const float ofac = 1.f / (ps * sv);  // exact: a power of two
   __syncthreads();
 
-  const int64_t groups = (n + in_seq - 1) / in_seq;
-  const int64_t bpg = (in_seq + RB - 1) / RB;
-  const int64_t nblk = groups * bpg;
+  // Blocks of RB vectors, numbered group by group (the host keeps the count
+  // below 2^31); block numbers are wave-uniform, so their arithmetic is scalar.
+  const int bpg = static_cast<int>((in_seq + RB - 1) / RB);
+  const int nblk = static_cast<int>((n + in_seq - 1) / in_seq) * bpg;
   const int64_t pb = FMT == QKV_FMT_PACKED ? qkv_row_bytes(D, BITS)
                    : FMT == QKV_FMT_KPLANES ? int64_t(bits + 1) * (D / 8) : D;
   const int64_t pq = FMT == QKV_FMT_PACKED ? D / 8 : D;
+  const int obytes = out_dtype == QKV_F32 ? 4 : 2;
   uint4* stg = &stage[VT ? wave * D : 0];
 
-  for (int64_t blk = int64_t(blockIdx.x) * kWaves + wave; blk < nblk;
-       blk += int64_t(gridDim.x) * kWaves) {
-    const int64_t grp = blk / bpg;
-    const int64_t t0 = (blk - grp * bpg) * RB;
+  // Software pipeline per wave: fetch block b+1 (loads only), MFMAs and stores
+  // of block b, then expand block b+1's codes.  The loads are issued before
+  // block b's stores, so the wait for them does not wait for those stores
+  // (one in-order counter covers both); rows past a group's end are clamped
+  // loads and range-checked buffer stores, so no branch hides a memory
+  // instruction from that count.
+  constexpr int CWN = FMT == QKV_FMT_KPLANES ? 4 : CodeWords<D, FMT, BITS>::N;
+  constexpr int QWN = IP ? QjlWords<D, FMT>::N : 1;
+  constexpr int TV = VT ? R / 2 : 1, TU = VT ? D / 64 : 1;
+  uint32_t rc[R][CWN];  // code words (K rows: plane words)
+  uint32_t rq[R][QWN];  // QJL words
+  uint4 rt[TV][TU];     // V tiles: this lane's share of each tile's words
+  float rn[R];          // norms
+
+  auto fetch = [&](int blk) {
+    const int gi = blk / bpg;
+    const int64_t grp = gi;
+    const int64_t t0 = int64_t(blk - gi * bpg) * RB;
     const int64_t tend = min(in_seq, n - grp * in_seq);  // valid tokens of the group
-
-    uint4 ah[R][NK], al[R][NK];
-    float nf[R];
-    CodeWords<D, FMT, BITS> cw[R];
-    QjlWords<D, FMT> qw[R];
-
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      // rows past the group's end read its last row; their outputs are dropped
+      const int64_t t = min(t0 + 16 * r + m, tend - 1);
+      const int64_t row = grp * in_gstride + t;
+      rn[r] = norms[VT ? grp * in_gstride * 32 + t : row];
+#pragma unroll
+      for (int i = 0; i < CWN; ++i) rc[r][i] = 0u;
+#pragma unroll
+      for (int i = 0; i < QWN; ++i) rq[r][i] = 0u;
+      if constexpr (FMT == QKV_FMT_UNPACKED) {
+        const uint4* src = reinterpret_cast<const uint4*>(codes + row * D + g * NE);
+#pragma unroll
+        for (int i = 0; i < NE / 16; ++i) {
+          const uint4 v = src[i];
+          rc[r][4 * i] = v.x; rc[r][4 * i + 1] = v.y; rc[r][4 * i + 2] = v.z; rc[r][4 * i + 3] = v.w;
+        }
+        if constexpr (IP) {
+          const uint4* qsrc = reinterpret_cast<const uint4*>(qjl + row * D + g * NE);
+#pragma unroll
+          for (int i = 0; i < NE / 16; ++i) {
+            const uint4 v = qsrc[i];
+            rq[r][4 * i] = v.x; rq[r][4 * i + 1] = v.y; rq[r][4 * i + 2] = v.z; rq[r][4 * i + 3] = v.w;
+          }
+        }
+      } else if constexpr (FMT == QKV_FMT_PACKED) {
+        const uint8_t* rp = codes + row * pb;
+        if constexpr (D == 128) {
+          const uint32_t* src = reinterpret_cast<const uint32_t*>(rp) + BITS * g;
+#pragma unroll
+          for (int i = 0; i < BITS; ++i) rc[r][i] = src[i];
+        } else {
+          const uint16_t* src = reinterpret_cast<const uint16_t*>(rp) + BITS * g;
+#pragma unroll
+          for (int i = 0; i < BITS; ++i) rc[r][i >> 1] |= uint32_t(src[i]) << (16 * (i & 1));
+        }
+        if constexpr (IP) rq[r][0] = lane_bits<D>(qjl + row * pq, g);
+      } else if constexpr (FMT == QKV_FMT_KPLANES) {
+        const uint8_t* rp = codes + row * pb;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)  // planes past `bits` re-read plane 0 (masked at use)
+          rc[r][p] = lane_bits<D>(rp + (p < bits ? p : 0) * (D / 8), g);
+        if constexpr (IP) rq[r][0] = lane_bits<D>(rp + bits * (D / 8), g);
+      }
+    }
     if constexpr (VT) {
-      // tiles of 32 tokens: stage, then gather bit (m + 16 h) of the lane's NE
-      // coordinate words of every plane into nibble codes
       const int nd4 = bits * D / 4;  // uint4 per tile
 #pragma unroll
-      for (int h = 0; h < R / 2; ++h) {
-        const int64_t tt = t0 + 32 * h;
+      for (int h = 0; h < TV; ++h) {
+        const int64_t tt = min(t0 + 32 * h, tend - 1);  // a tile past the end re-reads the last
+        const uint4* src = reinterpret_cast<const uint4*>(codes) +
+                           ((grp * in_gstride + (tt >> 5)) * bits) * (D / 4);
+#pragma unroll
+        for (int u = 0; u < TU; ++u) {
+          const int i = lane + 64 * u;
+          rt[h][u] = src[i < nd4 ? i : nd4 - 1];
+        }
+      }
+    }
+  };
+
+  uint4 ah[R][NK], al[R][NK];
+  float nf[R];
+  // codes of the fetched block -> fp16 (hi, lo) value fragments and scaled norms
+  auto expand = [&]() {
+    CodeWords<D, FMT, BITS> cw[R];
+    QjlWords<D, FMT> qw[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if constexpr (FMT == QKV_FMT_UNPACKED) {
+#pragma unroll
+        for (int i = 0; i < NE / 4; ++i) {
+          cw[r].w[i] = rc[r][i] & 0x0F0F0F0Fu;
+          if constexpr (SEL) cw[r].w[i] |= selw[i];
+        }
+      } else if constexpr (FMT == QKV_FMT_PACKED) {
+#pragma unroll
+        for (int i = 0; i < CodeWords<D, FMT, BITS>::N; ++i) cw[r].w[i] = rc[r][i];
+      } else if constexpr (FMT == QKV_FMT_KPLANES) {
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+          uint32_t v = 0u;
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            if (p < bits) v |= spread8(bfe(rc[r][p], 8 * i, 8)) << p;
+          cw[r].w[i] = v;
+        }
+      }
+      if constexpr (IP) {
+#pragma unroll
+        for (int i = 0; i < QjlWords<D, FMT>::N; ++i) qw[r].w[i] = rq[r][i];
+      }
+    }
+    if constexpr (VT) {
+      // tiles of 32 tokens: stage in LDS, then gather bit (m + 16 h) of the
+      // lane's NE coordinate words of every plane into nibble codes
+#pragma unroll
+      for (int h = 0; h < TV; ++h) {
 #pragma unroll
         for (int r = 2 * h; r < 2 * h + 2; ++r)
 #pragma unroll
           for (int i = 0; i < NW; ++i) cw[r].w[i] = 0u;
-        if (tt < tend) {
-          const uint4* src = reinterpret_cast<const uint4*>(codes) +
-                             ((grp * in_gstride + (tt >> 5)) * bits) * (D / 4);
-          __builtin_amdgcn_wave_barrier();
-          for (int i = lane; i < nd4; i += 64) stg[i] = src[i];
-          __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
-          __builtin_amdgcn_wave_barrier();
-          for (int p = 0; p < bits; ++p) {
-            const uint4* row = stg + p * (D / 4) + g * (NE / 4);
+        __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int c = 0; c < NE / 4; ++c) {
-              const uint4 v = row[c];
-              const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+        for (int u = 0; u < TU; ++u) stg[lane + 64 * u] = rt[h][u];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
+        __builtin_amdgcn_wave_barrier();
+        for (int p = 0; p < bits; ++p) {
+          const uint4* row = stg + p * (D / 4) + g * (NE / 4);
 #pragma unroll
-              for (int u = 0; u < 4; ++u) {
-                const int e = 4 * c + u;
-                const uint32_t sh = 4 * (e & 7) + p;
-                cw[2 * h].w[e >> 3] |= bfe(wv[u], m, 1) << sh;
-                cw[2 * h + 1].w[e >> 3] |= bfe(wv[u], m + 16, 1) << sh;
-              }
+          for (int c = 0; c < NE / 4; ++c) {
+            const uint4 v = row[c];
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int e = 4 * c + u;
+              const uint32_t sh = 4 * (e & 7) + p;
+              cw[2 * h].w[e >> 3] |= bfe(wv[u], m, 1) << sh;
+              cw[2 * h + 1].w[e >> 3] |= bfe(wv[u], m + 16, 1) << sh;
             }
           }
         }
       }
     }
-
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const int64_t t = t0 + 16 * r + m;
-      const bool ok = t < tend;
-      const int64_t row = grp * in_gstride + t;
-      nf[r] = ok ? norms[VT ? grp * in_gstride * 32 + t : row] * ofac : 0.f;
-      if constexpr (!VT) {
-#pragma unroll
-        for (int i = 0; i < CodeWords<D, FMT, BITS>::N; ++i) cw[r].w[i] = 0u;
-#pragma unroll
-        for (int i = 0; i < QjlWords<D, FMT>::N; ++i) qw[r].w[i] = 0u;
-      }
-      if (ok) {
-        if constexpr (FMT == QKV_FMT_UNPACKED) {
-          const uint4* src = reinterpret_cast<const uint4*>(codes + row * D + g * NE);
-#pragma unroll
-          for (int i = 0; i < NE / 16; ++i) {
-            const uint4 v = src[i];
-            cw[r].w[4 * i] = v.x; cw[r].w[4 * i + 1] = v.y;
-            cw[r].w[4 * i + 2] = v.z; cw[r].w[4 * i + 3] = v.w;
-          }
-#pragma unroll
-          for (int i = 0; i < NE / 4; ++i) {
-            cw[r].w[i] &= 0x0F0F0F0Fu;
-            if constexpr (SEL) cw[r].w[i] |= selw[i];
-          }
-          if constexpr (IP) {
-            const uint4* qsrc = reinterpret_cast<const uint4*>(qjl + row * D + g * NE);
-#pragma unroll
-            for (int i = 0; i < NE / 16; ++i) {
-              const uint4 v = qsrc[i];
-              qw[r].w[4 * i] = v.x; qw[r].w[4 * i + 1] = v.y;
-              qw[r].w[4 * i + 2] = v.z; qw[r].w[4 * i + 3] = v.w;
-            }
-          }
-        } else if constexpr (FMT == QKV_FMT_PACKED) {
-          const uint8_t* rp = codes + row * pb;
-          if constexpr (D == 128) {
-            const uint32_t* src = reinterpret_cast<const uint32_t*>(rp) + BITS * g;
-#pragma unroll
-            for (int i = 0; i < BITS; ++i) cw[r].w[i] = src[i];
-          } else {
-            const uint16_t* src = reinterpret_cast<const uint16_t*>(rp) + BITS * g;
-#pragma unroll
-            for (int i = 0; i < BITS; ++i) cw[r].w[i >> 1] |= uint32_t(src[i]) << (16 * (i & 1));
-          }
-          if constexpr (IP) qw[r].w[0] = lane_bits<D>(qjl + row * pq, g);
-        } else if constexpr (FMT == QKV_FMT_KPLANES) {
-          const uint8_t* rp = codes + row * pb;
-          for (int p = 0; p < bits; ++p) {
-            const uint32_t pw = lane_bits<D>(rp + p * (D / 8), g);
-#pragma unroll
-            for (int i = 0; i < NW; ++i) cw[r].w[i] |= spread8(bfe(pw, 8 * i, 8)) << p;
-          }
-          if constexpr (IP) qw[r].w[0] = lane_bits<D>(rp + bits * (D / 8), g);
-        }
-      }
-
-      // values -> fp16 (hi, lo) fragments
 #pragma unroll
       for (int ks = 0; ks < NK; ++ks) {
         uint32_t hv[4], lv[4];
@@ -344,23 +386,45 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
         for (int q = 0; q < 4; ++q) {
           const int e0 = 8 * ks + 2 * q, e1 = e0 + 1;
           const uint32_t i0 = cw[r].code(e0), i1 = cw[r].code(e1);
+          uint32_t a, b;
           if constexpr (IP) {
             const float c0 = __uint_as_float(tab[i0]), c1 = __uint_as_float(tab[i1]);
-            const float v0 = c0 + (qw[r].bit(e0) ? qs[e0] : -qs[e0]);
-            const float v1 = c1 + (qw[r].bit(e1) ? qs[e1] : -qs[e1]);
-            const uint32_t a = split_pair(v0), b = split_pair(v1);
-            hv[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);
-            lv[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+            a = split_pair(c0 + (qw[r].bit(e0) ? qs[e0] : -qs[e0]));
+            b = split_pair(c1 + (qw[r].bit(e1) ? qs[e1] : -qs[e1]));
           } else {
-            const uint32_t a = tab[i0], b = tab[i1];
-            hv[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);
-            lv[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+            a = tab[i0];
+            b = tab[i1];
           }
+          hv[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+          lv[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);
         }
         ah[r][ks] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
         al[r][ks] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
       }
+      nf[r] = rn[r] * ofac;
     }
+  };
+
+  const int stride = static_cast<int>(gridDim.x) * kWaves;
+  int blk = static_cast<int>(blockIdx.x) * kWaves + __builtin_amdgcn_readfirstlane(wave);
+  if (blk >= nblk) return;
+  fetch(blk);
+  expand();
+  for (;;) {
+    const int nb = blk + stride;
+    const bool more = nb < nblk;
+    fetch(more ? nb : blk);  // unconditional: the last round re-reads its own block
+
+    const int gi = blk / bpg;
+    const int64_t grp = gi;
+    const int64_t t0 = int64_t(blk - gi * bpg) * RB;
+    const int64_t tend = min(in_seq, n - grp * in_seq);
+    // this block's outputs: rows t0 .. tend - 1 of the group, as one buffer
+    // whose byte range drops the stores of rows past the end
+    const int64_t nrows = min<int64_t>(RB, tend - t0);
+    const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char*>(out) + (grp * in_seq + t0) * D * obytes, 0,
+        static_cast<int>(nrows * D * obytes), 0x00020000);
 
     // ---- C = Pi^T V^T, two column tiles (32 output coordinates) at a time
 #pragma unroll
@@ -388,51 +452,54 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
           for (int r = 0; r < R; ++r) acc[hh][r] = mma(ph, al[r][ks], acc[hh][r]);
         }
       }
-      // lane (m, g) holds coordinates 32 p + 8 g + 0..7 of vector t0 + 16 r + m
+      // lane (m, g) holds coordinates 32 p + 8 g + 0..7 of row 16 r + m
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const int64_t t = t0 + 16 * r + m;
-        if (t >= tend) continue;
-        const int64_t o = (grp * in_seq + t) * D + 32 * p + 8 * g;
+        const int off = ((16 * r + m) * D + 32 * p + 8 * g) * obytes;
         const float f = nf[r];
-        const float v[8] = {acc[0][r][0] * f, acc[0][r][1] * f, acc[0][r][2] * f,
-                            acc[0][r][3] * f, acc[1][r][0] * f, acc[1][r][1] * f,
-                            acc[1][r][2] * f, acc[1][r][3] * f};
-        if (out_dtype == QKV_F32) {
-          float4* dst = reinterpret_cast<float4*>(static_cast<float*>(out) + o);
-          dst[0] = make_float4(v[0], v[1], v[2], v[3]);
-          dst[1] = make_float4(v[4], v[5], v[6], v[7]);
-        } else {
-          uint32_t h[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            uint32_t a, b;
+        for (int hh = 0; hh < 2; ++hh) {
+          const float v0 = acc[hh][r][0] * f, v1 = acc[hh][r][1] * f;
+          const float v2 = acc[hh][r][2] * f, v3 = acc[hh][r][3] * f;
+          if (out_dtype == QKV_F32) {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                __builtin_bit_cast(qkv_u32x4, make_float4(v0, v1, v2, v3)), ob, off + 16 * hh, 0, 0);
+          } else {
+            uint32_t w0, w1;
             if (out_dtype == QKV_F16) {
-              a = h16(static_cast<_Float16>(v[2 * q]));
-              b = h16(static_cast<_Float16>(v[2 * q + 1]));
+              w0 = h16(static_cast<_Float16>(v0)) | (h16(static_cast<_Float16>(v1)) << 16);
+              w1 = h16(static_cast<_Float16>(v2)) | (h16(static_cast<_Float16>(v3)) << 16);
             } else {
-              a = qkv_f32_to_bf16(v[2 * q]);
-              b = qkv_f32_to_bf16(v[2 * q + 1]);
+              w0 = qkv_f32_to_bf16(v0) | (uint32_t(qkv_f32_to_bf16(v1)) << 16);
+              w1 = qkv_f32_to_bf16(v2) | (uint32_t(qkv_f32_to_bf16(v3)) << 16);
             }
-            h[q] = a | (b << 16);
+            __builtin_amdgcn_raw_buffer_store_b64(qkv_u32x2{w0, w1}, ob, off + 8 * hh, 0, 0);
           }
-          *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + o) =
-              make_uint4(h[0], h[1], h[2], h[3]);
         }
       }
     }
+    if (!more) break;
+    expand();
+    blk = nb;
   }
 }
 
 template <int D, int FMT, int BITS, bool IP, bool SEL, int R>
 int launch(const QkvDecompressArgs& a, hipStream_t s) {
   auto k = decompress_mfma<D, FMT, BITS, IP, SEL, R>;
+  // resident workgroups per CU from the kernel's LDS (160 KiB per gfx950 CU)
+  // and VGPRs (512 per SIMD lane, four SIMDs)
   static int per_cu = 0;
   if (per_cu == 0) {
-    int b = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k, kThreads, 0) != hipSuccess || b < 1)
-      b = 1;
-    per_cu = b;
+    int b = 2;
+    hipFuncAttributes at;
+    if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(k)) == hipSuccess) {
+      const int by_lds = 160 * 1024 / static_cast<int>(at.sharedSizeBytes > 0 ? at.sharedSizeBytes : 1);
+      const int regs = at.numRegs > 0 ? (at.numRegs + 7) / 8 * 8 : 512;
+      const int by_regs = (512 / regs) * 4 / kWaves;
+      b = by_lds < by_regs ? by_lds : by_regs;
+    }
+    per_cu = b < 1 ? 1 : b;
   }
   const int64_t in_seq = a.in_seq;
   const int64_t groups = (a.n + in_seq - 1) / in_seq;
@@ -479,6 +546,9 @@ int dispatch(const QkvDecompressArgs& a, hipStream_t s) {
 
 bool qkv_decompress_mfma_ok(const QkvDecompressArgs& a) {
   if (a.d != 64 && a.d != 128) return false;
+  // block numbers (32 vectors per block, per group) are 32-bit
+  const int64_t groups = (a.n + a.in_seq - 1) / a.in_seq;
+  if (groups * ((a.in_seq + 31) / 32) > int64_t(0x7fffffff) - int64_t(qkv_num_cus()) * 64) return false;
   if (a.sel && a.fmt != QKV_FMT_UNPACKED) return false;
   if (a.fmt == QKV_FMT_PACKED && a.mode == QKV_MODE_IP && a.bits == 4) return false;
   // 16-byte unpacked reads, 4-byte (2-byte at d = 64) packed and plane reads
