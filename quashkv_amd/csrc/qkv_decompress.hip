@@ -76,11 +76,10 @@ __device__ __forceinline__ float pow2_scale(float m) {
   return ldexpf(1.f, 1 - e);
 }
 
-// Output coordinate of C row mm (0..15) in column tile jt: tiles 2p and 2p+1
-// interleave in quads so that lane group g holds coordinates 32 p + 8 g + 0..7.
-__device__ __forceinline__ int out_col(int jt, int mm) {
-  return 32 * (jt >> 1) + 8 * (mm >> 2) + 4 * (jt & 1) + (mm & 3);
-}
+// Output coordinate of C row mm (0..15) in column tile jt: lane group g of a
+// tile holds coordinates 16 jt + 4 g + 0..3, so one store instruction writes
+// 64 contiguous bytes (fp32) of each of its 16 vectors.
+__device__ __forceinline__ int out_col(int jt, int mm) { return 16 * jt + mm; }
 
 __device__ __forceinline__ uint32_t bfe(uint32_t w, uint32_t off, uint32_t width) {
   return __builtin_amdgcn_ubfe(w, off, width);
@@ -145,29 +144,20 @@ __device__ __forceinline__ uint32_t lane_bits(const uint8_t* p, int g) {
   else return reinterpret_cast<const uint16_t*>(p)[g];
 }
 
-template <int D, int FMT, int BITS, bool IP, bool SEL, int R>
-__global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
-    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
-    const float* __restrict__ norms, int64_t n, int bits, const float* __restrict__ pi,
-    const float* __restrict__ cents, const float* __restrict__ signs, float qjl_scale,
-    int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype,
-    const uint8_t* __restrict__ sel, const float* __restrict__ alt_cents, int alt_bits) {
-  using G = Geo<D>;
-  constexpr int NE = G::NE, NK = G::NK, NJ = G::NJ, NW = G::NW;
-  constexpr int RB = 16 * R;  // vectors per wave block
-  constexpr bool VT = FMT == QKV_FMT_VTILES;
-  static_assert(!VT || R % 2 == 0, "V tiles are 32 tokens: R must be even");
-  __shared__ uint4 frag[NJ * NK * 2 * 64];  // [jt][ks][hi, lo][lane]
-  __shared__ uint32_t tab[32];              // [codebook][code]
-  __shared__ float red[kWaves + 1];
-  __shared__ uint4 stage[VT ? kWaves * D : 1];  // one V tile (<= 4 planes) per wave
+// ------------------------------------------------------------------ shared parts
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m = lane & 15, g = lane >> 4;
-
-  // ---- scales: Pi and the values into [1, 2) before the fp16 split
+// Per-workgroup set-up: the power-of-two scales that bring Pi's and the
+// values' largest magnitudes into [1, 2), the value table and Pi's fragments
+// in LDS.  Returns the value scale sv and the exact output factor 1 / (ps sv).
+template <int D, bool IP, bool SEL>
+__device__ void setup(int nthreads, float* red, uint32_t* tab, uint4* frag,
+                      const float* __restrict__ pi, const float* __restrict__ cents, int bits,
+                      const float* __restrict__ alt_cents, int alt_bits, float qjl_scale,
+                      float& sv, float& ofac) {
+  constexpr int NE = Geo<D>::NE, NK = Geo<D>::NK, NJ = Geo<D>::NJ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nw = nthreads / 64;
   float pm = 0.f;
-  for (int i = tid; i < D * D; i += kThreads) pm = fmaxf(pm, fabsf(pi[i]));
+  for (int i = tid; i < D * D; i += nthreads) pm = fmaxf(pm, fabsf(pi[i]));
   pm = qkv_wave_max(pm);
   float tv = 0.f;
   if (tid < 32) {
@@ -177,22 +167,20 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
   }
   const float vm = qkv_wave_max(fabsf(tv));
   if (lane == 0) red[wave] = pm;
-  if (tid == 0) red[kWaves] = vm;
+  if (tid == 0) red[nw] = vm;
   __syncthreads();
   float pmax = red[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) pmax = fmaxf(pmax, red[w]);
+  for (int w = 1; w < nw; ++w) pmax = fmaxf(pmax, red[w]);
   const float ps = pow2_scale(pmax);
-  const float sv = pow2_scale(red[kWaves] + (IP ? fabsf(qjl_scale) : 0.f));
+  sv = pow2_scale(red[nw] + (IP ? fabsf(qjl_scale) : 0.f));
+  ofac = 1.f / (ps * sv);
   if (tid < 32) tab[tid] = IP ? __float_as_uint(tv * sv) : split_pair(tv * sv);
-
-  // ---- Pi fragments: lane l of (jt, ks) holds Pi[k][out_col(jt, l % 16)] for
-  // the 8 coordinates k = (l / 16) NE + 8 ks + 0..7
-  for (int i = tid; i < NJ * NK * 64; i += kThreads) {
+  // lane l of fragment (jt, ks) holds Pi[k][out_col(jt, l % 16)] for the 8
+  // coordinates k = (l / 16) NE + 8 ks + 0..7, fp16 high part then low part
+  for (int i = tid; i < NJ * NK * 64; i += nthreads) {
     const int l = i & 63, blk = i >> 6;
     const int jt = blk / NK, ks = blk - jt * NK;
-    const int col = out_col(jt, l & 15);
-    const float* src = pi + int64_t((l >> 4) * NE + 8 * ks) * D + col;
+    const float* src = pi + int64_t((l >> 4) * NE + 8 * ks) * D + out_col(jt, l & 15);
     uint32_t hi[4], lo[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -204,78 +192,320 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
     frag[(2 * blk) * 64 + l] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
     frag[(2 * blk + 1) * 64 + l] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
   }
+}
 
-  // ---- per-lane constants of its coordinates g NE .. g NE + NE - 1
+// Per-lane constants of the lane's coordinates g NE .. g NE + NE - 1: the
+// mixed-precision selector bits (bit 4 of each code byte) and the scaled
+// QJL terms qjl_scale S_k sv.
+template <int D, bool IP, bool SEL>
+struct LaneConsts {
+  static constexpr int NE = Geo<D>::NE;
   uint32_t selw[SEL ? NE / 4 : 1];
-  if constexpr (SEL) {
+  float qs[IP ? NE : 1];
+  __device__ __forceinline__ void load(int g, const uint8_t* __restrict__ sel,
+                                       const float* __restrict__ signs, float qjl_scale, float sv) {
+    if constexpr (SEL) {
 #pragma unroll
-    for (int c = 0; c < NE / 4; ++c) {
-      uint32_t s = 0;
+      for (int c = 0; c < NE / 4; ++c) {
+        uint32_t s = 0;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) s |= (sel[g * NE + 4 * c + b] != 0 ? 0x10u : 0u) << (8 * b);
-      selw[c] = s;
+        for (int b = 0; b < 4; ++b) s |= (sel[g * NE + 4 * c + b] != 0 ? 0x10u : 0u) << (8 * b);
+        selw[c] = s;
+      }
+    }
+    if constexpr (IP) {
+#pragma unroll
+      for (int e = 0; e < NE; ++e) qs[e] = qjl_scale * signs[g * NE + e] * sv;
     }
   }
-  float qs[IP ? NE : 1];
-  if constexpr (IP) {
+};
+
+// Raw words of one wave block (R row tiles of 16 vectors) as this lane needs
+// them (V tiles are read from a staged tile in LDS instead).
+template <int D, int FMT, int BITS, bool IP, int R>
+struct Raw {
+  static constexpr int CWN = FMT == QKV_FMT_KPLANES ? 4 : CodeWords<D, FMT, BITS>::N;
+  static constexpr int QWN = IP ? QjlWords<D, FMT>::N : 1;
+  uint32_t c[R][CWN];  // code words (K rows: plane words)
+  uint32_t q[R][QWN];  // QJL words
+  float n[R];          // norms
+};
+
+// Codes -> fp16 (hi, lo) value fragments ah / al of the lane's R vectors.
+// `tile`: the block's V tile (32 tokens) staged in LDS, for V tiles.
+template <int D, int FMT, int BITS, bool IP, bool SEL, int R>
+__device__ __forceinline__ void expand(const Raw<D, FMT, BITS, IP, R>& x, const uint4* tile,
+                                       int bits, int lane, const uint32_t* tab,
+                                       const LaneConsts<D, IP, SEL>& lc,
+                                       uint4 (&ah)[R][Geo<D>::NK], uint4 (&al)[R][Geo<D>::NK]) {
+  constexpr int NE = Geo<D>::NE, NK = Geo<D>::NK, NW = Geo<D>::NW;
+  const int m = lane & 15, g = lane >> 4;
+  CodeWords<D, FMT, BITS> cw[R];
+  QjlWords<D, FMT> qw[R];
 #pragma unroll
-    for (int e = 0; e < NE; ++e) qs[e] = qjl_scale * signs[g * NE + e] * sv;
+  for (int r = 0; r < R; ++r) {
+    if constexpr (FMT == QKV_FMT_UNPACKED) {
+#pragma unroll
+      for (int i = 0; i < NE / 4; ++i) {
+        cw[r].w[i] = x.c[r][i] & 0x0F0F0F0Fu;
+        if constexpr (SEL) cw[r].w[i] |= lc.selw[i];
+      }
+    } else if constexpr (FMT == QKV_FMT_PACKED) {
+#pragma unroll
+      for (int i = 0; i < CodeWords<D, FMT, BITS>::N; ++i) cw[r].w[i] = x.c[r][i];
+    } else if constexpr (FMT == QKV_FMT_KPLANES) {
+#pragma unroll
+      for (int i = 0; i < NW; ++i) {
+        uint32_t v = 0u;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          if (p < bits) v |= spread8(bfe(x.c[r][p], 8 * i, 8)) << p;
+        cw[r].w[i] = v;
+      }
+    }
+    if constexpr (IP) {
+#pragma unroll
+      for (int i = 0; i < QjlWords<D, FMT>::N; ++i) qw[r].w[i] = x.q[r][i];
+    }
   }
-  const float ofac = 1.f / (ps * sv);  // exact: a power of two
+  if constexpr (FMT == QKV_FMT_VTILES) {
+    // gather bit m (row tile 0) and m + 16 (row tile 1) of the lane's NE
+    // coordinate words of every plane into nibble codes
+    static_assert(R == 2, "one 32-token V tile per block");
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < NW; ++i) cw[r].w[i] = 0u;
+    for (int p = 0; p < bits; ++p) {
+      const uint4* row = tile + p * (D / 4) + g * (NE / 4);
+#pragma unroll
+      for (int c = 0; c < NE / 4; ++c) {
+        const uint4 v = row[c];
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int e = 4 * c + u;
+          const uint32_t sh = 4 * (e & 7) + p;
+          cw[0].w[e >> 3] |= bfe(wv[u], m, 1) << sh;
+          cw[1].w[e >> 3] |= bfe(wv[u], m + 16, 1) << sh;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int ks = 0; ks < NK; ++ks) {
+      uint32_t hv[4], lv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e0 = 8 * ks + 2 * q, e1 = e0 + 1;
+        const uint32_t i0 = cw[r].code(e0), i1 = cw[r].code(e1);
+        uint32_t a, b;
+        if constexpr (IP) {
+          const float c0 = __uint_as_float(tab[i0]), c1 = __uint_as_float(tab[i1]);
+          a = split_pair(c0 + (qw[r].bit(e0) ? lc.qs[e0] : -lc.qs[e0]));
+          b = split_pair(c1 + (qw[r].bit(e1) ? lc.qs[e1] : -lc.qs[e1]));
+        } else {
+          a = tab[i0];
+          b = tab[i1];
+        }
+        hv[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+        lv[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+      }
+      ah[r][ks] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+      al[r][ks] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+    }
+  }
+}
+
+// Orders this wave's LDS accesses across its lanes (LDS executes a wave's
+// accesses in order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+}
+
+// C = Pi^T V^T for the lane's R vectors and the stores (rows 16 r + m of the
+// buffer `ob`, whose byte range drops rows past the group's end).  Steps
+// (p, ks): column tiles 2p, 2p+1 (32 output coordinates), k-step ks; Pi's
+// fragments of step s+1 are read from LDS while the MFMAs of step s run (two
+// register buffers; the scheduling barriers keep the compiler from sinking
+// the reads to their use).
+template <int D, int R>
+__device__ __forceinline__ void mma_store(const uint4 (&ah)[R][Geo<D>::NK],
+                                          const uint4 (&al)[R][Geo<D>::NK], const float (&nf)[R],
+                                          const uint4* frag, int lane, uint8_t* ost,
+                                          __amdgpu_buffer_rsrc_t ob, int out_dtype) {
+  constexpr int NK = Geo<D>::NK, NJ = Geo<D>::NJ;
+  constexpr int NSTEP = (NJ / 2) * NK;
+  const int m = lane & 15, g = lane >> 4;
+  const int obytes = out_dtype == QKV_F32 ? 4 : 2;
+  uint4 fh[2][2], fl[2][2];  // [buffer][column tile of the pair]
+  auto read_frags = [&](int s, int buf) {
+    const int p = s / NK, ks = s - p * NK;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int f = 2 * ((2 * p + hh) * NK + ks);
+      fh[buf][hh] = frag[f * 64 + lane];
+      fl[buf][hh] = frag[(f + 1) * 64 + lane];
+    }
+  };
+  qkv_f32x4 acc[2][R];
+  read_frags(0, 0);
+#pragma unroll
+  for (int s = 0; s < NSTEP; ++s) {
+    const int p = s / NK, ks = s - p * NK, cur = s & 1;
+    if (s + 1 < NSTEP) read_frags(s + 1, cur ^ 1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (ks == 0) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[hh][r] = qkv_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[hh][r] = mma(fh[cur][hh], ah[r][ks], acc[hh][r]);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[hh][r] = mma(fl[cur][hh], ah[r][ks], acc[hh][r]);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[hh][r] = mma(fh[cur][hh], al[r][ks], acc[hh][r]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (ks != NK - 1) continue;
+    // lane (m, g) holds coordinates 16 (2p + hh) + 4 g + 0..3 of row 16 r + m:
+    // through the wave's LDS staging rows (32 coordinates, 16 bytes of padding)
+    // into stores of whole 128-byte (fp32) / 64-byte (16-bit) row segments
+    const int rsb = 32 * obytes + 16;
+    wave_lds_sync();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float f = nf[r];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const float v0 = acc[hh][r][0] * f, v1 = acc[hh][r][1] * f;
+        const float v2 = acc[hh][r][2] * f, v3 = acc[hh][r][3] * f;
+        uint8_t* dst = ost + (16 * r + m) * rsb + (16 * hh + 4 * g) * obytes;
+        if (out_dtype == QKV_F32) {
+          *reinterpret_cast<float4*>(dst) = make_float4(v0, v1, v2, v3);
+        } else {
+          uint32_t w0, w1;
+          if (out_dtype == QKV_F16) {
+            w0 = h16(static_cast<_Float16>(v0)) | (h16(static_cast<_Float16>(v1)) << 16);
+            w1 = h16(static_cast<_Float16>(v2)) | (h16(static_cast<_Float16>(v3)) << 16);
+          } else {
+            w0 = qkv_f32_to_bf16(v0) | (uint32_t(qkv_f32_to_bf16(v1)) << 16);
+            w1 = qkv_f32_to_bf16(v2) | (uint32_t(qkv_f32_to_bf16(v3)) << 16);
+          }
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w0, w1);
+        }
+      }
+    }
+    wave_lds_sync();
+    // 16-byte chunks: cpr per row segment, 64 / cpr rows per store
+    const int cpr = 2 * obytes, rows = 64 / cpr;
+    const int q = lane % cpr;
+    for (int v = lane / cpr; v < 16 * R; v += rows) {
+      const uint4 w = *reinterpret_cast<const uint4*>(ost + v * rsb + 16 * q);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(qkv_u32x4, w), ob,
+                                             (v * D + 32 * p) * obytes + 16 * q, 0, 0);
+    }
+  }
+}
+
+// A block's place: group, first token, end of the group's valid tokens.
+struct BlockPos {
+  int64_t grp, t0, tend;
+  __device__ __forceinline__ BlockPos(int blk, int bpg, int rb, int64_t n, int64_t in_seq) {
+    const int gi = blk / bpg;
+    grp = gi;
+    t0 = int64_t(blk - gi * bpg) * rb;
+    tend = min(in_seq, n - grp * in_seq);
+  }
+};
+
+// Output buffer of a block: rows t0 .. tend - 1 of the group (range-checked
+// buffer stores drop the rest).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void* out, const BlockPos& b, int rb,
+                                                           int d, int obytes, int64_t in_seq) {
+  const int64_t nrows = min<int64_t>(rb, b.tend - b.t0);
+  return __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<char*>(out) + (b.grp * in_seq + b.t0) * d * obytes, 0,
+      static_cast<int>(nrows * d * obytes), 0x00020000);
+}
+
+// ------------------------------------------------- d = 64: per-wave pipeline
+
+// One wave per block of 32 vectors, each wave fetching its next block (loads
+// only) before the current block's MFMAs and stores, then expanding it.
+// Rows past a group's end are clamped loads and dropped stores, so no branch
+// hides a memory instruction from the compiler's wait counts.
+template <int D, int FMT, int BITS, bool IP, bool SEL>
+__global__ __launch_bounds__(kThreads, 2) void decompress_waves(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
+    const float* __restrict__ norms, int64_t n, int bits, const float* __restrict__ pi,
+    const float* __restrict__ cents, const float* __restrict__ signs, float qjl_scale,
+    int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype,
+    const uint8_t* __restrict__ sel, const float* __restrict__ alt_cents, int alt_bits) {
+  using G = Geo<D>;
+  constexpr int NE = G::NE, NK = G::NK, R = 2, RB = 32;
+  constexpr bool VT = FMT == QKV_FMT_VTILES;
+  __shared__ uint4 frag[G::NJ * NK * 2 * 64];  // [jt][ks][hi, lo][lane]
+  __shared__ uint32_t tab[32];                 // [codebook][code]
+  __shared__ float red[kWaves + 1];
+  // per wave: a V tile (<= 4 planes) while expanding, output rows while storing
+  __shared__ uint4 stage[kWaves * 288];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m = lane & 15, g = lane >> 4;
+  float sv, ofac;
+  setup<D, IP, SEL>(kThreads, red, tab, frag, pi, cents, bits, alt_cents, alt_bits, qjl_scale,
+                    sv, ofac);
+  LaneConsts<D, IP, SEL> lc;
+  lc.load(g, sel, signs, qjl_scale, sv);
   __syncthreads();
 
-  // Blocks of RB vectors, numbered group by group (the host keeps the count
-  // below 2^31); block numbers are wave-uniform, so their arithmetic is scalar.
+  // blocks of 32 vectors numbered group by group (below 2^31: host check)
   const int bpg = static_cast<int>((in_seq + RB - 1) / RB);
   const int nblk = static_cast<int>((n + in_seq - 1) / in_seq) * bpg;
   const int64_t pb = FMT == QKV_FMT_PACKED ? qkv_row_bytes(D, BITS)
                    : FMT == QKV_FMT_KPLANES ? int64_t(bits + 1) * (D / 8) : D;
   const int64_t pq = FMT == QKV_FMT_PACKED ? D / 8 : D;
   const int obytes = out_dtype == QKV_F32 ? 4 : 2;
-  uint4* stg = &stage[VT ? wave * D : 0];
+  uint4* stg = &stage[wave * 288];
 
-  // Software pipeline per wave: fetch block b+1 (loads only), MFMAs and stores
-  // of block b, then expand block b+1's codes.  The loads are issued before
-  // block b's stores, so the wait for them does not wait for those stores
-  // (one in-order counter covers both); rows past a group's end are clamped
-  // loads and range-checked buffer stores, so no branch hides a memory
-  // instruction from that count.
-  constexpr int CWN = FMT == QKV_FMT_KPLANES ? 4 : CodeWords<D, FMT, BITS>::N;
-  constexpr int QWN = IP ? QjlWords<D, FMT>::N : 1;
-  constexpr int TV = VT ? R / 2 : 1, TU = VT ? D / 64 : 1;
-  uint32_t rc[R][CWN];  // code words (K rows: plane words)
-  uint32_t rq[R][QWN];  // QJL words
-  uint4 rt[TV][TU];     // V tiles: this lane's share of each tile's words
-  float rn[R];          // norms
-
+  Raw<D, FMT, BITS, IP, R> x;
+  uint4 rt[VT ? D / 64 : 1];  // V tiles: this lane's share of the tile's words
   auto fetch = [&](int blk) {
-    const int gi = blk / bpg;
-    const int64_t grp = gi;
-    const int64_t t0 = int64_t(blk - gi * bpg) * RB;
-    const int64_t tend = min(in_seq, n - grp * in_seq);  // valid tokens of the group
+    const BlockPos b(blk, bpg, RB, n, in_seq);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      // rows past the group's end read its last row; their outputs are dropped
-      const int64_t t = min(t0 + 16 * r + m, tend - 1);
-      const int64_t row = grp * in_gstride + t;
-      rn[r] = norms[VT ? grp * in_gstride * 32 + t : row];
+      const int64_t t = min(b.t0 + 16 * r + m, b.tend - 1);  // clamped: last valid row
+      const int64_t row = b.grp * in_gstride + t;
+      x.n[r] = norms[VT ? b.grp * in_gstride * 32 + t : row];
 #pragma unroll
-      for (int i = 0; i < CWN; ++i) rc[r][i] = 0u;
+      for (int i = 0; i < Raw<D, FMT, BITS, IP, R>::CWN; ++i) x.c[r][i] = 0u;
 #pragma unroll
-      for (int i = 0; i < QWN; ++i) rq[r][i] = 0u;
+      for (int i = 0; i < Raw<D, FMT, BITS, IP, R>::QWN; ++i) x.q[r][i] = 0u;
       if constexpr (FMT == QKV_FMT_UNPACKED) {
         const uint4* src = reinterpret_cast<const uint4*>(codes + row * D + g * NE);
 #pragma unroll
         for (int i = 0; i < NE / 16; ++i) {
           const uint4 v = src[i];
-          rc[r][4 * i] = v.x; rc[r][4 * i + 1] = v.y; rc[r][4 * i + 2] = v.z; rc[r][4 * i + 3] = v.w;
+          x.c[r][4 * i] = v.x; x.c[r][4 * i + 1] = v.y; x.c[r][4 * i + 2] = v.z; x.c[r][4 * i + 3] = v.w;
         }
         if constexpr (IP) {
           const uint4* qsrc = reinterpret_cast<const uint4*>(qjl + row * D + g * NE);
 #pragma unroll
           for (int i = 0; i < NE / 16; ++i) {
             const uint4 v = qsrc[i];
-            rq[r][4 * i] = v.x; rq[r][4 * i + 1] = v.y; rq[r][4 * i + 2] = v.z; rq[r][4 * i + 3] = v.w;
+            x.q[r][4 * i] = v.x; x.q[r][4 * i + 1] = v.y; x.q[r][4 * i + 2] = v.z; x.q[r][4 * i + 3] = v.w;
           }
         }
       } else if constexpr (FMT == QKV_FMT_PACKED) {
@@ -283,262 +513,326 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_mfma(
         if constexpr (D == 128) {
           const uint32_t* src = reinterpret_cast<const uint32_t*>(rp) + BITS * g;
 #pragma unroll
-          for (int i = 0; i < BITS; ++i) rc[r][i] = src[i];
+          for (int i = 0; i < BITS; ++i) x.c[r][i] = src[i];
         } else {
           const uint16_t* src = reinterpret_cast<const uint16_t*>(rp) + BITS * g;
 #pragma unroll
-          for (int i = 0; i < BITS; ++i) rc[r][i >> 1] |= uint32_t(src[i]) << (16 * (i & 1));
+          for (int i = 0; i < BITS; ++i) x.c[r][i >> 1] |= uint32_t(src[i]) << (16 * (i & 1));
         }
-        if constexpr (IP) rq[r][0] = lane_bits<D>(qjl + row * pq, g);
+        if constexpr (IP) x.q[r][0] = lane_bits<D>(qjl + row * pq, g);
       } else if constexpr (FMT == QKV_FMT_KPLANES) {
         const uint8_t* rp = codes + row * pb;
 #pragma unroll
         for (int p = 0; p < 4; ++p)  // planes past `bits` re-read plane 0 (masked at use)
-          rc[r][p] = lane_bits<D>(rp + (p < bits ? p : 0) * (D / 8), g);
-        if constexpr (IP) rq[r][0] = lane_bits<D>(rp + bits * (D / 8), g);
+          x.c[r][p] = lane_bits<D>(rp + (p < bits ? p : 0) * (D / 8), g);
+        if constexpr (IP) x.q[r][0] = lane_bits<D>(rp + bits * (D / 8), g);
       }
     }
     if constexpr (VT) {
       const int nd4 = bits * D / 4;  // uint4 per tile
+      const uint4* src = reinterpret_cast<const uint4*>(codes) +
+                         ((b.grp * in_gstride + (b.t0 >> 5)) * bits) * (D / 4);
 #pragma unroll
-      for (int h = 0; h < TV; ++h) {
-        const int64_t tt = min(t0 + 32 * h, tend - 1);  // a tile past the end re-reads the last
-        const uint4* src = reinterpret_cast<const uint4*>(codes) +
-                           ((grp * in_gstride + (tt >> 5)) * bits) * (D / 4);
-#pragma unroll
-        for (int u = 0; u < TU; ++u) {
-          const int i = lane + 64 * u;
-          rt[h][u] = src[i < nd4 ? i : nd4 - 1];
-        }
+      for (int u = 0; u < D / 64; ++u) {
+        const int i = lane + 64 * u;
+        rt[u] = src[i < nd4 ? i : nd4 - 1];
       }
     }
   };
 
   uint4 ah[R][NK], al[R][NK];
   float nf[R];
-  // codes of the fetched block -> fp16 (hi, lo) value fragments and scaled norms
-  auto expand = [&]() {
-    CodeWords<D, FMT, BITS> cw[R];
-    QjlWords<D, FMT> qw[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      if constexpr (FMT == QKV_FMT_UNPACKED) {
-#pragma unroll
-        for (int i = 0; i < NE / 4; ++i) {
-          cw[r].w[i] = rc[r][i] & 0x0F0F0F0Fu;
-          if constexpr (SEL) cw[r].w[i] |= selw[i];
-        }
-      } else if constexpr (FMT == QKV_FMT_PACKED) {
-#pragma unroll
-        for (int i = 0; i < CodeWords<D, FMT, BITS>::N; ++i) cw[r].w[i] = rc[r][i];
-      } else if constexpr (FMT == QKV_FMT_KPLANES) {
-#pragma unroll
-        for (int i = 0; i < NW; ++i) {
-          uint32_t v = 0u;
-#pragma unroll
-          for (int p = 0; p < 4; ++p)
-            if (p < bits) v |= spread8(bfe(rc[r][p], 8 * i, 8)) << p;
-          cw[r].w[i] = v;
-        }
-      }
-      if constexpr (IP) {
-#pragma unroll
-        for (int i = 0; i < QjlWords<D, FMT>::N; ++i) qw[r].w[i] = rq[r][i];
-      }
-    }
+  auto expand_fetched = [&]() {
     if constexpr (VT) {
-      // tiles of 32 tokens: stage in LDS, then gather bit (m + 16 h) of the
-      // lane's NE coordinate words of every plane into nibble codes
+      wave_lds_sync();
 #pragma unroll
-      for (int h = 0; h < TV; ++h) {
-#pragma unroll
-        for (int r = 2 * h; r < 2 * h + 2; ++r)
-#pragma unroll
-          for (int i = 0; i < NW; ++i) cw[r].w[i] = 0u;
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int u = 0; u < TU; ++u) stg[lane + 64 * u] = rt[h][u];
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the tile is in LDS
-        __builtin_amdgcn_wave_barrier();
-        for (int p = 0; p < bits; ++p) {
-          const uint4* row = stg + p * (D / 4) + g * (NE / 4);
-#pragma unroll
-          for (int c = 0; c < NE / 4; ++c) {
-            const uint4 v = row[c];
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int e = 4 * c + u;
-              const uint32_t sh = 4 * (e & 7) + p;
-              cw[2 * h].w[e >> 3] |= bfe(wv[u], m, 1) << sh;
-              cw[2 * h + 1].w[e >> 3] |= bfe(wv[u], m + 16, 1) << sh;
-            }
-          }
-        }
-      }
+      for (int u = 0; u < D / 64; ++u) stg[lane + 64 * u] = rt[u];
+      wave_lds_sync();
     }
+    expand<D, FMT, BITS, IP, SEL, R>(x, stg, bits, lane, tab, lc, ah, al);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-#pragma unroll
-      for (int ks = 0; ks < NK; ++ks) {
-        uint32_t hv[4], lv[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int e0 = 8 * ks + 2 * q, e1 = e0 + 1;
-          const uint32_t i0 = cw[r].code(e0), i1 = cw[r].code(e1);
-          uint32_t a, b;
-          if constexpr (IP) {
-            const float c0 = __uint_as_float(tab[i0]), c1 = __uint_as_float(tab[i1]);
-            a = split_pair(c0 + (qw[r].bit(e0) ? qs[e0] : -qs[e0]));
-            b = split_pair(c1 + (qw[r].bit(e1) ? qs[e1] : -qs[e1]));
-          } else {
-            a = tab[i0];
-            b = tab[i1];
-          }
-          hv[q] = __builtin_amdgcn_perm(b, a, 0x05040100u);
-          lv[q] = __builtin_amdgcn_perm(b, a, 0x07060302u);
-        }
-        ah[r][ks] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
-        al[r][ks] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
-      }
-      nf[r] = rn[r] * ofac;
-    }
+    for (int r = 0; r < R; ++r) nf[r] = x.n[r] * ofac;
   };
 
   const int stride = static_cast<int>(gridDim.x) * kWaves;
   int blk = static_cast<int>(blockIdx.x) * kWaves + __builtin_amdgcn_readfirstlane(wave);
   if (blk >= nblk) return;
   fetch(blk);
-  expand();
+  expand_fetched();
   for (;;) {
     const int nb = blk + stride;
     const bool more = nb < nblk;
     fetch(more ? nb : blk);  // unconditional: the last round re-reads its own block
-
-    const int gi = blk / bpg;
-    const int64_t grp = gi;
-    const int64_t t0 = int64_t(blk - gi * bpg) * RB;
-    const int64_t tend = min(in_seq, n - grp * in_seq);
-    // this block's outputs: rows t0 .. tend - 1 of the group, as one buffer
-    // whose byte range drops the stores of rows past the end
-    const int64_t nrows = min<int64_t>(RB, tend - t0);
-    const __amdgpu_buffer_rsrc_t ob = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<char*>(out) + (grp * in_seq + t0) * D * obytes, 0,
-        static_cast<int>(nrows * D * obytes), 0x00020000);
-
-    // ---- C = Pi^T V^T, two column tiles (32 output coordinates) at a time
-#pragma unroll
-    for (int p = 0; p < NJ / 2; ++p) {
-      // one column pair at a time: keeps the scheduler from hoisting every
-      // fragment read of the block ahead of the MFMAs
-      __builtin_amdgcn_sched_barrier(0);
-      qkv_f32x4 acc[2][R];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[hh][r] = qkv_f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < NK; ++ks) {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int blk2 = 2 * ((2 * p + hh) * NK + ks);
-          const uint4 ph = frag[blk2 * 64 + lane];
-          const uint4 pl = frag[(blk2 + 1) * 64 + lane];
-#pragma unroll
-          for (int r = 0; r < R; ++r) acc[hh][r] = mma(ph, ah[r][ks], acc[hh][r]);
-#pragma unroll
-          for (int r = 0; r < R; ++r) acc[hh][r] = mma(pl, ah[r][ks], acc[hh][r]);
-#pragma unroll
-          for (int r = 0; r < R; ++r) acc[hh][r] = mma(ph, al[r][ks], acc[hh][r]);
-        }
-      }
-      // lane (m, g) holds coordinates 32 p + 8 g + 0..7 of row 16 r + m
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int off = ((16 * r + m) * D + 32 * p + 8 * g) * obytes;
-        const float f = nf[r];
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const float v0 = acc[hh][r][0] * f, v1 = acc[hh][r][1] * f;
-          const float v2 = acc[hh][r][2] * f, v3 = acc[hh][r][3] * f;
-          if (out_dtype == QKV_F32) {
-            __builtin_amdgcn_raw_buffer_store_b128(
-                __builtin_bit_cast(qkv_u32x4, make_float4(v0, v1, v2, v3)), ob, off + 16 * hh, 0, 0);
-          } else {
-            uint32_t w0, w1;
-            if (out_dtype == QKV_F16) {
-              w0 = h16(static_cast<_Float16>(v0)) | (h16(static_cast<_Float16>(v1)) << 16);
-              w1 = h16(static_cast<_Float16>(v2)) | (h16(static_cast<_Float16>(v3)) << 16);
-            } else {
-              w0 = qkv_f32_to_bf16(v0) | (uint32_t(qkv_f32_to_bf16(v1)) << 16);
-              w1 = qkv_f32_to_bf16(v2) | (uint32_t(qkv_f32_to_bf16(v3)) << 16);
-            }
-            __builtin_amdgcn_raw_buffer_store_b64(qkv_u32x2{w0, w1}, ob, off + 8 * hh, 0, 0);
-          }
-        }
-      }
-    }
+    const BlockPos b(blk, bpg, RB, n, in_seq);
+    mma_store<D, R>(ah, al, nf, frag, lane, reinterpret_cast<uint8_t*>(stg),
+                    out_rsrc(out, b, RB, D, obytes, in_seq), out_dtype);
     if (!more) break;
-    expand();
+    expand_fetched();
     blk = nb;
   }
 }
 
-template <int D, int FMT, int BITS, bool IP, bool SEL, int R>
-int launch(const QkvDecompressArgs& a, hipStream_t s) {
-  auto k = decompress_mfma<D, FMT, BITS, IP, SEL, R>;
-  // resident workgroups per CU from the kernel's LDS (160 KiB per gfx950 CU)
-  // and VGPRs (512 per SIMD lane, four SIMDs)
-  static int per_cu = 0;
-  if (per_cu == 0) {
-    int b = 2;
-    hipFuncAttributes at;
-    if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(k)) == hipSuccess) {
-      const int by_lds = 160 * 1024 / static_cast<int>(at.sharedSizeBytes > 0 ? at.sharedSizeBytes : 1);
-      const int regs = at.numRegs > 0 ? (at.numRegs + 7) / 8 * 8 : 512;
-      const int by_regs = (512 / regs) * 4 / kWaves;
-      b = by_lds < by_regs ? by_lds : by_regs;
+// ------------------------------------- d = 128: loader wave + compute waves
+
+typedef __attribute__((address_space(3))) void* qkv_lds_ptr;
+typedef __attribute__((address_space(1))) void* qkv_global_ptr;
+
+// size-byte global -> LDS copy per lane (lane i lands at dst + i * max(size, 4))
+template <int SIZE>
+__device__ __forceinline__ void to_lds(const void* src, void* dst) {
+  static_assert(SIZE == 4 || SIZE == 16, "copy size");
+  if constexpr (SIZE == 16)
+    __builtin_amdgcn_global_load_lds((qkv_global_ptr)(src), (qkv_lds_ptr)(dst), 16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds((qkv_global_ptr)(src), (qkv_lds_ptr)(dst), 4, 0, 0);
+}
+
+// All workgroup waves meet; orders LDS accesses only (a global-memory fence
+// would wait for the compute waves' outstanding stores).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Bytes of one compute wave's staging slot (codes, QJL words, norms) at d = 128.
+template <int FMT, int BITS, bool IP>
+struct Slot {
+  static constexpr int CB = FMT == QKV_FMT_UNPACKED ? 4096
+                          : FMT == QKV_FMT_PACKED   ? 2 * BITS * 256
+                          : FMT == QKV_FMT_KPLANES  ? 2 * 5 * 256
+                                                    : 2048;
+  static constexpr int QB = !IP ? 0 : FMT == QKV_FMT_UNPACKED ? 4096 : FMT == QKV_FMT_PACKED ? 512 : 0;
+  // also the output staging rows of the wave's stores: 32 x 144 bytes
+  static constexpr int BYTES = CB + QB + 512 > 4608 ? CB + QB + 512 : 4608;
+};
+
+// The loader wave (the last of the workgroup) copies the codes, QJL words and
+// norms of the NC compute waves' next blocks into LDS with global->LDS loads,
+// laid out in the compute lanes' order; the compute waves read them from LDS
+// and so never wait on global loads, which on this architecture would also
+// wait for their own outstanding output stores (one in-order counter covers
+// both).  Double-buffered slots, one LDS-only barrier per round.
+template <int FMT, int BITS, bool IP, bool SEL, int NC>
+__global__ __launch_bounds__(64 * (NC + 1), 1) void decompress_staged(
+    const uint8_t* __restrict__ codes, const uint8_t* __restrict__ qjl,
+    const float* __restrict__ norms, int64_t n, int bits, const float* __restrict__ pi,
+    const float* __restrict__ cents, const float* __restrict__ signs, float qjl_scale,
+    int64_t in_seq, int64_t in_gstride, void* __restrict__ out, int out_dtype,
+    const uint8_t* __restrict__ sel, const float* __restrict__ alt_cents, int alt_bits) {
+  constexpr int D = 128, NT = 64 * (NC + 1), R = 2, RB = 32;
+  using G = Geo<D>;
+  using S = Slot<FMT, BITS, IP>;
+  constexpr int NK = G::NK;
+  constexpr bool VT = FMT == QKV_FMT_VTILES;
+  __shared__ uint4 frag[G::NJ * NK * 2 * 64];
+  __shared__ uint32_t tab[32];
+  __shared__ float red[NC + 2];
+  __shared__ uint4 slots[2 * NC * S::BYTES / 16];  // [buffer][compute wave]
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int m = lane & 15, g = lane >> 4;
+  float sv, ofac;
+  setup<D, IP, SEL>(NT, red, tab, frag, pi, cents, bits, alt_cents, alt_bits, qjl_scale, sv,
+                    ofac);
+  __syncthreads();
+
+  const int bpg = static_cast<int>((in_seq + RB - 1) / RB);
+  const int nblk = static_cast<int>((n + in_seq - 1) / in_seq) * bpg;
+  const int per_round = static_cast<int>(gridDim.x) * NC;
+  const int rounds = (nblk + per_round - 1) / per_round;
+  const int64_t pb = FMT == QKV_FMT_PACKED ? qkv_row_bytes(D, BITS)
+                   : FMT == QKV_FMT_KPLANES ? int64_t(bits + 1) * (D / 8) : D;
+  const int64_t pq = D / 8;
+  uint8_t* slot0 = reinterpret_cast<uint8_t*>(slots);
+  auto slot = [&](int buf, int c) { return slot0 + (buf * NC + c) * S::BYTES; };
+  auto block_of = [&](int round, int c) { return (round * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x)) * NC + c; };
+
+  if (wave == NC) {
+    // ---- loader
+    auto load_round = [&](int round, int buf) {
+      for (int c = 0; c < NC; ++c) {
+        const int blk = block_of(round, c);
+        if (blk >= nblk) break;
+        const BlockPos b(blk, bpg, RB, n, in_seq);
+        uint8_t* sl = slot(buf, c);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int64_t t = min(b.t0 + 16 * r + m, b.tend - 1);  // clamped: last valid row
+          const int64_t row = b.grp * in_gstride + t;
+          to_lds<4>(norms + (VT ? b.grp * in_gstride * 32 + t : row), sl + S::CB + S::QB + r * 256);
+          if constexpr (FMT == QKV_FMT_UNPACKED) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              to_lds<16>(codes + row * D + 32 * g + 16 * h, sl + (2 * r + h) * 1024);
+              if constexpr (IP) to_lds<16>(qjl + row * D + 32 * g + 16 * h, sl + S::CB + (2 * r + h) * 1024);
+            }
+          } else if constexpr (FMT == QKV_FMT_PACKED) {
+#pragma unroll
+            for (int i = 0; i < BITS; ++i)
+              to_lds<4>(codes + row * pb + 4 * (BITS * g + i), sl + (r * BITS + i) * 256);
+            if constexpr (IP) to_lds<4>(qjl + row * pq + 4 * g, sl + S::CB + r * 256);
+          } else if constexpr (FMT == QKV_FMT_KPLANES) {
+            for (int p = 0; p < bits; ++p)
+              to_lds<4>(codes + row * pb + 16 * p + 4 * g, sl + (r * 5 + p) * 256);
+            if constexpr (IP) to_lds<4>(codes + row * pb + 16 * bits + 4 * g, sl + (r * 5 + 4) * 256);
+          }
+        }
+        if constexpr (VT) {
+          const int nd4 = bits * D / 4;  // uint4 per tile
+          const uint4* src = reinterpret_cast<const uint4*>(codes) +
+                             ((b.grp * in_gstride + (b.t0 >> 5)) * bits) * (D / 4);
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int i = lane + 64 * u;
+            to_lds<16>(src + (i < nd4 ? i : nd4 - 1), sl + u * 1024);
+          }
+        }
+      }
+    };
+    load_round(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): the round's copies landed
+    lds_barrier();
+    for (int round = 0; round < rounds; ++round) {
+      if (round + 1 < rounds) load_round(round + 1, (round + 1) & 1);
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+      lds_barrier();
     }
-    per_cu = b < 1 ? 1 : b;
+  } else {
+    // ---- compute
+    LaneConsts<D, IP, SEL> lc;
+    lc.load(g, sel, signs, qjl_scale, sv);
+    const int obytes = out_dtype == QKV_F32 ? 4 : 2;
+    lds_barrier();
+    for (int round = 0; round < rounds; ++round) {
+      const int blk = block_of(round, wave);
+      if (blk < nblk) {
+        const uint8_t* sl = slot(round & 1, wave);
+        Raw<D, FMT, BITS, IP, R> x;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          x.n[r] = reinterpret_cast<const float*>(sl + S::CB + S::QB + r * 256)[lane];
+#pragma unroll
+          for (int i = 0; i < Raw<D, FMT, BITS, IP, R>::CWN; ++i) x.c[r][i] = 0u;
+#pragma unroll
+          for (int i = 0; i < Raw<D, FMT, BITS, IP, R>::QWN; ++i) x.q[r][i] = 0u;
+          if constexpr (FMT == QKV_FMT_UNPACKED) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const uint4 v = reinterpret_cast<const uint4*>(sl + (2 * r + h) * 1024)[lane];
+              x.c[r][4 * h] = v.x; x.c[r][4 * h + 1] = v.y; x.c[r][4 * h + 2] = v.z; x.c[r][4 * h + 3] = v.w;
+              if constexpr (IP) {
+                const uint4 u = reinterpret_cast<const uint4*>(sl + S::CB + (2 * r + h) * 1024)[lane];
+                x.q[r][4 * h] = u.x; x.q[r][4 * h + 1] = u.y; x.q[r][4 * h + 2] = u.z; x.q[r][4 * h + 3] = u.w;
+              }
+            }
+          } else if constexpr (FMT == QKV_FMT_PACKED) {
+#pragma unroll
+            for (int i = 0; i < BITS; ++i)
+              x.c[r][i] = reinterpret_cast<const uint32_t*>(sl + (r * BITS + i) * 256)[lane];
+            if constexpr (IP) x.q[r][0] = reinterpret_cast<const uint32_t*>(sl + S::CB + r * 256)[lane];
+          } else if constexpr (FMT == QKV_FMT_KPLANES) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+              x.c[r][p] = p < bits ? reinterpret_cast<const uint32_t*>(sl + (r * 5 + p) * 256)[lane] : 0u;
+            if constexpr (IP) x.q[r][0] = reinterpret_cast<const uint32_t*>(sl + (r * 5 + 4) * 256)[lane];
+          }
+        }
+        uint4 ah[R][NK], al[R][NK];
+        expand<D, FMT, BITS, IP, SEL, R>(x, reinterpret_cast<const uint4*>(sl), bits, lane, tab, lc,
+                                         ah, al);
+        float nf[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) nf[r] = x.n[r] * ofac;
+        const BlockPos b(blk, bpg, RB, n, in_seq);
+        mma_store<D, R>(ah, al, nf, frag, lane, const_cast<uint8_t*>(sl),
+                        out_rsrc(out, b, RB, D, obytes, in_seq), out_dtype);
+      }
+      lds_barrier();
+    }
   }
-  const int64_t in_seq = a.in_seq;
-  const int64_t groups = (a.n + in_seq - 1) / in_seq;
-  const int64_t nblk = groups * ((in_seq + 16 * R - 1) / (16 * R));
-  int64_t grid = (nblk + kWaves - 1) / kWaves;
-  const int64_t cap = int64_t(qkv_num_cus()) * per_cu;
+}
+
+// ------------------------------------------------------------------- launch
+
+// resident workgroups per CU from a kernel's LDS (160 KiB per gfx950 CU) and
+// VGPRs (512 per SIMD lane, four SIMDs)
+template <typename K>
+int per_cu(K k, int waves) {
+  int b = 1;
+  hipFuncAttributes at;
+  if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(k)) == hipSuccess) {
+    const int by_lds = 160 * 1024 / static_cast<int>(at.sharedSizeBytes > 0 ? at.sharedSizeBytes : 1);
+    const int regs = at.numRegs > 0 ? (at.numRegs + 7) / 8 * 8 : 512;
+    const int by_regs = (512 / regs) * 4 / waves;
+    b = by_lds < by_regs ? by_lds : by_regs;
+  }
+  return b < 1 ? 1 : b;
+}
+
+int64_t blocks_of(const QkvDecompressArgs& a) {
+  return (a.n + a.in_seq - 1) / a.in_seq * ((a.in_seq + 31) / 32);
+}
+
+template <int D, int FMT, int BITS, bool IP, bool SEL>
+int launch_waves(const QkvDecompressArgs& a, hipStream_t s) {
+  auto k = decompress_waves<D, FMT, BITS, IP, SEL>;
+  static const int pc = per_cu(k, kWaves);
+  int64_t grid = (blocks_of(a) + kWaves - 1) / kWaves;
+  const int64_t cap = int64_t(qkv_num_cus()) * pc;
   if (grid > cap) grid = cap;
-  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, a.codes,
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(kThreads), 0, s, a.codes, a.qjl,
+                     a.norms, a.n, a.bits, a.pi, a.cents, a.signs, a.qjl_scale, a.in_seq,
+                     a.in_gstride, a.out, a.out_dtype, a.sel, a.alt_cents, a.alt_bits);
+  return QKV_OK;
+}
+
+template <int FMT, int BITS, bool IP, bool SEL>
+int launch_staged(const QkvDecompressArgs& a, hipStream_t s) {
+  constexpr int NC = IP ? 4 : 8;  // compute waves (VGPRs / LDS slots)
+  auto k = decompress_staged<FMT, BITS, IP, SEL, NC>;
+  static const int pc = per_cu(k, NC + 1);
+  int64_t grid = (blocks_of(a) + NC - 1) / NC;
+  const int64_t cap = int64_t(qkv_num_cus()) * pc;
+  if (grid > cap) grid = cap;
+  hipLaunchKernelGGL(k, dim3(static_cast<unsigned>(grid)), dim3(64 * (NC + 1)), 0, s, a.codes,
                      a.qjl, a.norms, a.n, a.bits, a.pi, a.cents, a.signs, a.qjl_scale, a.in_seq,
                      a.in_gstride, a.out, a.out_dtype, a.sel, a.alt_cents, a.alt_bits);
   return QKV_OK;
 }
 
+template <int D, int FMT, int BITS, bool IP, bool SEL>
+int launch(const QkvDecompressArgs& a, hipStream_t s) {
+  if constexpr (D == 128) return launch_staged<FMT, BITS, IP, SEL>(a, s);
+  else return launch_waves<D, FMT, BITS, IP, SEL>(a, s);
+}
+
 template <int D>
 int dispatch(const QkvDecompressArgs& a, hipStream_t s) {
-  constexpr int R = 2;
   const bool ip = a.mode == QKV_MODE_IP;
   const bool sel = a.sel != nullptr;
   switch (a.fmt) {
     case QKV_FMT_UNPACKED:
-      if (ip) return sel ? launch<D, QKV_FMT_UNPACKED, 0, true, true, R>(a, s)
-                         : launch<D, QKV_FMT_UNPACKED, 0, true, false, R>(a, s);
-      return sel ? launch<D, QKV_FMT_UNPACKED, 0, false, true, R>(a, s)
-                 : launch<D, QKV_FMT_UNPACKED, 0, false, false, R>(a, s);
+      if (ip) return sel ? launch<D, QKV_FMT_UNPACKED, 0, true, true>(a, s)
+                         : launch<D, QKV_FMT_UNPACKED, 0, true, false>(a, s);
+      return sel ? launch<D, QKV_FMT_UNPACKED, 0, false, true>(a, s)
+                 : launch<D, QKV_FMT_UNPACKED, 0, false, false>(a, s);
     case QKV_FMT_PACKED:
       switch (a.bits) {
-        case 1: return ip ? launch<D, QKV_FMT_PACKED, 1, true, false, R>(a, s)
-                          : launch<D, QKV_FMT_PACKED, 1, false, false, R>(a, s);
-        case 2: return ip ? launch<D, QKV_FMT_PACKED, 2, true, false, R>(a, s)
-                          : launch<D, QKV_FMT_PACKED, 2, false, false, R>(a, s);
-        case 3: return ip ? launch<D, QKV_FMT_PACKED, 3, true, false, R>(a, s)
-                          : launch<D, QKV_FMT_PACKED, 3, false, false, R>(a, s);
-        default: return launch<D, QKV_FMT_PACKED, 4, false, false, R>(a, s);
+        case 1: return ip ? launch<D, QKV_FMT_PACKED, 1, true, false>(a, s)
+                          : launch<D, QKV_FMT_PACKED, 1, false, false>(a, s);
+        case 2: return ip ? launch<D, QKV_FMT_PACKED, 2, true, false>(a, s)
+                          : launch<D, QKV_FMT_PACKED, 2, false, false>(a, s);
+        case 3: return ip ? launch<D, QKV_FMT_PACKED, 3, true, false>(a, s)
+                          : launch<D, QKV_FMT_PACKED, 3, false, false>(a, s);
+        default: return launch<D, QKV_FMT_PACKED, 4, false, false>(a, s);
       }
     case QKV_FMT_KPLANES:
-      return ip ? launch<D, QKV_FMT_KPLANES, 0, true, false, R>(a, s)
-                : launch<D, QKV_FMT_KPLANES, 0, false, false, R>(a, s);
+      return ip ? launch<D, QKV_FMT_KPLANES, 0, true, false>(a, s)
+                : launch<D, QKV_FMT_KPLANES, 0, false, false>(a, s);
     default:
-      return launch<D, QKV_FMT_VTILES, 0, false, false, R>(a, s);
+      return launch<D, QKV_FMT_VTILES, 0, false, false>(a, s);
   }
 }
 
