@@ -456,6 +456,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy 256 MiB three times (calibrates FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--decompress-reps", type=int, default=10,
+                    help="timed full-cache reconstructions (cfg3)")
     ap.add_argument("--workload", choices=("cfg2", "cfg3", "cfg4", "cfg5"), default="cfg3",
                     help="cfg3: the headline decode/compress line; cfg2: 24-layer d=64 "
                          "decode step; cfg4: mixed-precision long context; cfg5: the MIPS index")
@@ -583,6 +585,36 @@ def main() -> None:
     comp_gvec = n_vec / (comp_ms * 1e-3) / 1e9
     comp_bytes = n_vec * (D * 2) + B * HKV * T * kv_bytes_per_token_head(D)
 
+    # full-cache reconstruction (QuashKVCache.update's decompress of every K
+    # and V row, quashkv/integrations/hf_cache.py:96-121) of cache 0 to fp32
+    from quashkv_amd.quantizer import decompress_from
+    st0 = eng0._store
+    n_rows = B * HKV * T
+    mq0 = kq0.mse_quantizer
+
+    def reconstruct():
+        kh = decompress_from(N.QKV_MODE_MSE, st0.kst, None, st0.knorm, n_rows, mq0.Pi,
+                             mq0.codebook.centroids, KEY_BITS - 1, None, 0.0, N.QKV_FMT_KPLANES,
+                             in_seq=T, in_group_stride=st0.capacity)
+        vh = decompress_from(N.QKV_MODE_MSE, st0.vst, None, st0.vnorm, n_rows, vq0.Pi,
+                             vq0.codebook.centroids, VAL_BITS, None, 0.0, N.QKV_FMT_VTILES,
+                             in_seq=T, in_group_stride=st0.capacity // 32)
+        return kh, vh
+
+    for _ in range(3):
+        reconstruct()
+    torch.cuda.synchronize()
+    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    d0.record(stream)
+    for _ in range(args.decompress_reps):
+        reconstruct()
+    d1.record(stream)
+    torch.cuda.synchronize()
+    dec_ms = d0.elapsed_time(d1) / args.decompress_reps
+    # bytes moved per row: the code planes read + fp32 norm + d fp32 outputs
+    dec_bytes = n_rows * ((KEY_BITS - 1) * D // 8 + VAL_BITS * D // 8 + 2 * 4 + 2 * D * 4)
+    dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
+
     cpu = None
     if not args.no_cpu:
         gbs, med, threads = cpu_baseline(engines[0], queries[0], args.cpu_batch, args.cpu_reps)
@@ -617,6 +649,13 @@ def main() -> None:
         "compress_gvec_s": round(comp_gvec, 4),
         "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
                                               / PEAK_HBM_GBS, 2),
+        "decompress": {
+            "what": "full K (2-bit MSE planes) + V (3-bit tiles) reconstruction to fp32, "
+                    f"{n_rows} rows each",
+            "us": round(dec_ms * 1e3, 1), "GB_s": round(dec_gbs, 1),
+            "pct_of_hbm_peak": round(100 * dec_gbs / PEAK_HBM_GBS, 2),
+            "bytes": dec_bytes,
+        },
         "roofline": {
             "kernel": ("split_mfma" if path == 1 else "split_generic") + " (qkv_attention_partial)",
             "bound": "hbm",
