@@ -133,7 +133,12 @@ int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
  *              QKV_FMT_VTILES: V store tiles, in_seq tokens per group (from
  *              token 0), in_group_stride tiles per group, norms at
  *              group * 32 * in_group_stride + token (MSE mode only)
- *   out        n x d, out_dtype, contiguous */
+ *   out        n x d, out_dtype, contiguous
+ * d = 64 / 128 run on the matrix cores (fp16 high/low split of Pi and of the
+ * values, fp32 accumulation: within ~3e-6 relative of an fp32 evaluation);
+ * they need 16-byte aligned out and unpacked code / V-tile pointers (4-byte,
+ * 2-byte at d = 64, for packed rows and K rows).  d = 96 and other pointers
+ * use a VALU kernel with fp32 arithmetic. */
 int qkv_decompress(int32_t mode, int32_t fmt,
                    const uint8_t* codes, const uint8_t* qjl, const float* norms,
                    int64_t n, int32_t d, int32_t bits,
