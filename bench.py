@@ -615,6 +615,25 @@ def main() -> None:
     dec_bytes = n_rows * ((KEY_BITS - 1) * D // 8 + VAL_BITS * D // 8 + 2 * 4 + 2 * D * 4)
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
 
+    # measured HBM ceiling on this device: a 1 GiB device copy (read + write;
+    # each buffer exceeds the 256 MB MALL)
+    big = torch.empty(1 << 28, device=dev).uniform_()
+    dst = torch.empty_like(big)
+
+    def timed_ms(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps
+
+    copy_gbs = 2 * big.numel() * 4 / (timed_ms(lambda: dst.copy_(big)) * 1e-3) / 1e9
+    del big, dst
+
     cpu = None
     if not args.no_cpu:
         gbs, med, threads = cpu_baseline(engines[0], queries[0], args.cpu_batch, args.cpu_reps)
@@ -649,6 +668,19 @@ def main() -> None:
         "compress_gvec_s": round(comp_gvec, 4),
         "compress_pct_of_hbm_roofline": round(100 * comp_bytes / (comp_ms * 1e-3) / 1e9
                                               / PEAK_HBM_GBS, 2),
+        "compress_mfma": {
+            "what": "rotation GEMM of the append (2 d^2 flops per vector; executed as "
+                    "two bf16 passes, Pi split into high and low parts)",
+            "algorithmic_tflops": round(n_vec * 2 * D * D / (comp_ms * 1e-3) / 1e12, 1),
+            "executed_tflops": round(2 * n_vec * 2 * D * D / (comp_ms * 1e-3) / 1e12, 1),
+            "peak_tflops": 2500.0,
+            "executed_frac": round(2 * n_vec * 2 * D * D / (comp_ms * 1e-3) / 2.5e15, 4),
+        },
+        "hbm_ceiling_measured": {
+            "copy_GB_s": round(copy_gbs, 1),
+            "decode_pct_of_copy": round(100 * step_gbs / copy_gbs, 2),
+            "decompress_pct_of_copy": round(100 * dec_gbs / copy_gbs, 2),
+        },
         "decompress": {
             "what": "full K (2-bit MSE planes) + V (3-bit tiles) reconstruction to fp32, "
                     f"{n_rows} rows each",
