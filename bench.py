@@ -82,6 +82,46 @@ def cpu_baseline(eng, q, n_batch: int, reps: int):
     return nbytes / med / 1e9, med, torch.get_num_threads()
 
 
+def cpu_compress_decompress(eng, n_batch: int, reps: int):
+    """Oracle compress (keys IP, values MSE; quashkv/triton_kernels/compress.py:34-97
+    restated) and decompress (decompress.py:32-55 restated: keys MSE-only and
+    values, as QuashKVCache reconstructs) on the host, for n_batch sequences'
+    worth of rows.  Returns (compress Gvec/s, decompress GB/s, rows, threads)."""
+    import torch
+    from oracle import ref_math as R
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    mq = kq.mse_quantizer
+    n = n_batch * HKV * T
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(n, D, generator=g)
+    k[:, list(OUTLIERS)] *= 10.0
+    k = k.to(torch.bfloat16).float()
+    v = torch.randn(n, D, generator=g).to(torch.bfloat16).float()
+    kpi, kb, ks, kc = (mq.Pi.cpu(), mq.codebook.boundaries.cpu(), kq.S.cpu(),
+                       mq.codebook.centroids.cpu())
+    vpi, vb, vc = vq.Pi.cpu(), vq.codebook.boundaries.cpu(), vq.codebook.centroids.cpu()
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    t_c = med(lambda: (R.compress_ip(k, kpi, kb, ks, kc), R.compress_mse(v, vpi, vb)))
+    st = eng._store
+    kcodes, _, vcodes = (t[:n_batch].cpu().reshape(n, D) for t in st.read_codes(0, T))
+    kn = st.knorm[:n_batch, :, :T].cpu().reshape(n)
+    vn = st.vnorm[:n_batch, :, :T].cpu().reshape(n)
+    t_d = med(lambda: (R.decompress_mse(kcodes, kn, kpi, kc), R.decompress_mse(vcodes, vn, vpi, vc)))
+    dec_bytes = n * ((KEY_BITS - 1) * D // 8 + VAL_BITS * D // 8 + 2 * 4 + 2 * D * 4)
+    return 2 * n / t_c / 1e9, dec_bytes / t_d / 1e9, n, torch.get_num_threads(), t_c, t_d
+
+
 def cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -634,8 +674,16 @@ def main() -> None:
     copy_gbs = 2 * big.numel() * 4 / (timed_ms(lambda: dst.copy_(big)) * 1e-3) / 1e9
     del big, dst
 
-    cpu = None
+    cpu = cpu_comp = cpu_dec = None
     if not args.no_cpu:
+        cg, dg, nrow, thr, tc, td = cpu_compress_decompress(engines[0], 4, args.cpu_reps)
+        cpu_comp = {"value": round(cg, 5), "unit": "Gvec/s", "cores": thr, "kind": "port",
+                    "sample": (f"oracle compress_ip (keys) + compress_mse (values), fp32 torch "
+                               f"CPU, {nrow} rows each (4 sequences, 8 kv heads); median of "
+                               f"{args.cpu_reps} = {tc:.3f} s")}
+        cpu_dec = {"value": round(dg, 3), "unit": "GB/s", "cores": thr, "kind": "port",
+                   "sample": (f"oracle decompress_mse of the store's K and V codes to fp32, "
+                              f"{nrow} rows each; median of {args.cpu_reps} = {td:.3f} s")}
         gbs, med, threads = cpu_baseline(engines[0], queries[0], args.cpu_batch, args.cpu_reps)
         cpu = {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
                "sample": (f"oracle online-softmax decode (oracle/ref_math.attention_online, "
@@ -700,6 +748,8 @@ def main() -> None:
             "avg_kernel_us": round(partial_ms * 1e3, 2),
         },
         "cpu_baseline": cpu,
+        "cpu_baseline_compress": cpu_comp,
+        "cpu_baseline_decompress": cpu_dec,
         "wall_s_timed": round(wall, 3),
     }
     print(json.dumps(line), flush=True)
