@@ -259,11 +259,12 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
 // One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
 // grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
 // MB MSE planes, then the QJL plane).
-template <int MB, bool F16, int D>
+template <int MB, bool F16, int D, bool PAGED>
 __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, const float* __restrict__ signs, Thresh fine,
-    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
+    QkvPages pg) {
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NF = (1 << L) - 1;    // c_0, t_0, c_1, ..., c_{2^MB - 1}
   constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
@@ -300,7 +301,6 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 
     // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
     // 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four consecutive tokens)
-    float* nrow = knorm + grp * t_stride + t0 + s0;
     float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
     for (int tt = 0; tt < kHalves; ++tt) {
@@ -310,7 +310,10 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
       if (lane < 32) {
-        if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
+        if (32 * tt + li < nv) {
+          const int64_t t = t0 + s0 + 32 * tt + li;
+          knorm[PAGED ? qkv_store_row(pg, grp, t_stride, t) : grp * t_stride + t] = nrm;
+        }
         invw[32 * tt + li] = iscale / nrm;
       }
     }
@@ -359,11 +362,22 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       });
     });
 
-    uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+    if constexpr (PAGED) {
+      // dword w of the tile: row w / RD (token t0 + s0 + w / RD), dword w % RD
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kst);
 #pragma unroll
-    for (int i = 0; i < NSK; ++i) {
-      const int w = i * 64 + lane;
-      if (w < nv * RD) dst[w] = stg[i];
+      for (int i = 0; i < NSK; ++i) {
+        const int w = i * 64 + lane, r = w / RD;
+        if (w < nv * RD)
+          dst[qkv_store_row(pg, grp, t_stride, t0 + s0 + r) * RD + (w - r * RD)] = stg[i];
+      }
+    } else {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+#pragma unroll
+      for (int i = 0; i < NSK; ++i) {
+        const int w = i * 64 + lane;
+        if (w < nv * RD) dst[w] = stg[i];
+      }
     }
   }
 }
@@ -495,11 +509,11 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
 // so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
 // already in the store.
-template <int VB, bool F16, int D>
+template <int VB, bool F16, int D, bool PAGED>
 __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
     const float* __restrict__ pi, Thresh bnd, uint32_t* __restrict__ vst,
-    float* __restrict__ vnorm, int64_t t_stride, int64_t t0) {
+    float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
   constexpr int NB = (1 << VB) - 1;  // boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
@@ -515,7 +529,6 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
   for (int i = 0; i < NB / 2; ++i) bv[i] = in_vgpr(bnd.v[NB / 2 + 1 + i]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t a_base = t0 & ~int64_t(31);
-  const int64_t tiles_per_group = t_stride / 32;
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
   for (int64_t tile = int64_t(blockIdx.x) * kWaves + (threadIdx.x >> 6); tile < ntiles;
@@ -537,7 +550,6 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     }
 
     float inv[kHalves];  // token 32 tt + (l & 31): the C-column of this lane
-    float* nrow = vnorm + grp * t_stride + A0;
 #pragma unroll
     for (int tt = 0; tt < kHalves; ++tt) {
       float ss = 0.f;
@@ -545,7 +557,10 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
       ss += __shfl_xor(ss, 32, 64);
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (lane < 32 && ok[tt]) nrow[32 * tt + li] = nrm;
+      if (lane < 32 && ok[tt]) {
+        const int64_t t = A0 + 32 * tt + li;
+        vnorm[PAGED ? qkv_store_row(pg, grp, t_stride, t) : grp * t_stride + t] = nrm;
+      }
       inv[tt] = iscale / nrm;
     }
 
@@ -593,7 +608,9 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       if (hi <= lo) continue;
       const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
                                           : (((1u << (hi - lo)) - 1u) << lo);
-      uint32_t* p = vst + ((grp * tiles_per_group + tok0 / 32) * VB + k) * D + j;
+      const int64_t vt = PAGED ? qkv_store_vtile(pg, grp, t_stride, tok0)
+                               : grp * (t_stride >> 5) + (tok0 >> 5);
+      uint32_t* p = vst + (vt * VB + k) * D + j;
       uint32_t val = stg[i];
       if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
       *p = val;
@@ -616,17 +633,24 @@ int append_blocks(int64_t ntiles) {
 
 }  // namespace
 
-extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
-                                int64_t groups, int64_t S, int32_t d, int32_t mbits,
-                                int32_t vbits, const float* pi, const float* signs,
-                                const float* kcent_host, const float* kbound_host,
-                                const float* vbound_host, uint8_t* kstore, float* knorm,
-                                uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
-                                void* stream) {
+static int store_append_impl(int32_t in_dtype, const void* keys, const void* values,
+                             int64_t groups, int64_t S, int32_t d, int32_t mbits,
+                             int32_t vbits, const float* pi, const float* signs,
+                             const float* kcent_host, const float* kbound_host,
+                             const float* vbound_host, uint8_t* kstore, float* knorm,
+                             uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
+                             QkvPages pg, void* stream) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
-  QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
-              "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
-              (long long)t_stride, (long long)t0, (long long)(t0 + S));
+  if (pg.tab == nullptr) {
+    QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
+                "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
+                (long long)t_stride, (long long)t0, (long long)(t0 + S));
+  } else {
+    QKV_REQUIRE(pg.H > 0 && groups % pg.H == 0, "groups must be batch x kv heads");
+    QKV_REQUIRE(t0 + S <= int64_t(pg.pmax) * kPageTokens,
+                "page table of %d pages per sequence must hold tokens [%lld, %lld)", pg.pmax,
+                (long long)t0, (long long)(t0 + S));
+  }
   if (in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
     qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
     return QKV_E_UNSUPPORTED;
@@ -681,9 +705,13 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
     const auto* xk = static_cast<const uint16_t*>(keys);
-#define QKV_K(MB, F, DD)                                                                    \
-  hipLaunchKernelGGL((append_k_mfma<MB, F, DD>), grid, dim3(kThreads), 0, s, xk, S, tpg, ntiles, \
-                     pi, signs, fine, kstore, knorm, t_stride, t0)
+#define QKV_K(MB, F, DD)                                                                   \
+  if (pg.tab)                                                                              \
+    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, true>), grid, dim3(kThreads), 0, s, xk, S,  \
+                       tpg, ntiles, pi, signs, fine, kstore, knorm, t_stride, t0, pg);     \
+  else                                                                                     \
+    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, false>), grid, dim3(kThreads), 0, s, xk, S, \
+                       tpg, ntiles, pi, signs, fine, kstore, knorm, t_stride, t0, pg)
 #define QKV_KD(DD)                                  \
   switch (mbits * 2 + (f16 ? 1 : 0)) {              \
     case 2: QKV_K(1, false, DD); break;             \
@@ -707,9 +735,13 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     const int64_t tpg = (t0 + S - a_base + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
     const auto* xv = static_cast<const uint16_t*>(values);
-#define QKV_V(VB, F, DD)                                                                    \
-  hipLaunchKernelGGL((append_v_mfma<VB, F, DD>), grid, dim3(kThreads), 0, s, xv, S, tpg, ntiles, \
-                     pi, bnd, vstore, vnorm, t_stride, t0)
+#define QKV_V(VB, F, DD)                                                                   \
+  if (pg.tab)                                                                              \
+    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, true>), grid, dim3(kThreads), 0, s, xv, S,  \
+                       tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0, pg);             \
+  else                                                                                     \
+    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, false>), grid, dim3(kThreads), 0, s, xv, S, \
+                       tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0, pg)
 #define QKV_VD(DD)                                  \
   switch (vbits * 2 + (f16 ? 1 : 0)) {              \
     case 2: QKV_V(1, false, DD); break;             \
@@ -731,6 +763,34 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
     QKV_LAUNCHED();
   }
   return QKV_OK;
+}
+
+extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
+                                int64_t groups, int64_t S, int32_t d, int32_t mbits,
+                                int32_t vbits, const float* pi, const float* signs,
+                                const float* kcent_host, const float* kbound_host,
+                                const float* vbound_host, uint8_t* kstore, float* knorm,
+                                uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
+                                void* stream) {
+  return store_append_impl(in_dtype, keys, values, groups, S, d, mbits, vbits, pi, signs,
+                           kcent_host, kbound_host, vbound_host, kstore, knorm, vstore, vnorm,
+                           t_stride, t0, QkvPages{nullptr, 0, 1}, stream);
+}
+
+extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
+                                      int32_t B, int32_t H, int64_t S, int32_t d, int32_t mbits,
+                                      int32_t vbits, const float* pi, const float* signs,
+                                      const float* kcent_host, const float* kbound_host,
+                                      const float* vbound_host, uint8_t* kpool, float* knorm,
+                                      uint32_t* vpool, float* vnorm, const int32_t* page_table,
+                                      int32_t pages_per_seq, int64_t t0, void* stream) {
+  QKV_REQUIRE(B >= 0 && H > 0, "invalid shape");
+  QKV_REQUIRE(page_table && pages_per_seq > 0, "null page table");
+  QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
+  return store_append_impl(in_dtype, keys, values, int64_t(B) * H, S, d, mbits, vbits, pi,
+                           signs, kcent_host, kbound_host, vbound_host, kpool, knorm, vpool,
+                           vnorm, kPageTokens, t0, QkvPages{page_table, pages_per_seq, H},
+                           stream);
 }
 
 extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups,

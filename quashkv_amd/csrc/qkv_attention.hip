@@ -80,6 +80,8 @@ struct KVLayers {  // the store
   const float* knorm[kMaxLayers];
   const uint32_t* vst[kMaxLayers];
   const float* vnorm[kMaxLayers];
+  const int32_t* ptab;  // paged store: page of sequence b's token t at ptab[b * pmax + t / 64]
+  int32_t pmax;         // (nullptr: contiguous streams of t_stride rows)
 };
 struct OutLayers {  // un-rotation and output
   const float* pi[kMaxLayers];
@@ -625,7 +627,8 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int ln = lane & 15, lg = lane >> 4;
   const int r0 = cgi * RW;
   const int nr = min(RW, R - r0);  // valid rows of the workgroup
-  const int64_t bh = int64_t(b - layer * Bl) * Hkv + hkv;   // in the layer's store
+  const int64_t bseq = b - layer * Bl;                       // sequence in the layer
+  const int64_t bh = bseq * Hkv + hkv;                        // in the layer's store
   const int64_t ts = int64_t(split) * split_len;
   const int64_t te = min<int64_t>(T, ts + split_len);
   const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
@@ -661,28 +664,33 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 #pragma unroll
   for (int c = 0; c < RC; ++c) mloc[c] = -INFINITY;
   const int ntile1 = (ntok + 63) >> 6;
-  // split-relative bases: per-lane offsets stay 32-bit
-  const uint8_t* kbs = kst + (bh * t_stride + ts) * KRB;
-  const float* knbs = knorm + bh * t_stride + ts;
-  const float* vnbs = vnorm + bh * t_stride + ts;
+  // First store row of the split's 64-token tile `tile`: linear in the tile
+  // for a contiguous store, the tile's page for a paged one.
+  const int32_t* __restrict__ ptab = kv.ptab;
+  auto tile_row = [&](int tile) -> int64_t {
+    if (ptab) return (int64_t(ptab[bseq * kv.pmax + (ts >> 6) + tile]) * Hkv + hkv) * 64;
+    return bh * t_stride + ts + int64_t(tile) * 64;
+  };
   constexpr int PD1 = RC == 2 ? 1 : 2;  // (registers: two chunks' accumulators)
   uint32_t kd[PD1][4][NLD];
   float kn[PD1][4], vv[PD1][4];
   // Tokens past the split end are read too (masked when scored): the store
-  // capacity is a multiple of 64 and >= T, so whole 64-token tiles of the
-  // split stay inside it.  Addresses are then linear in the tile index.
-  const uint32_t* krow0 =
-      reinterpret_cast<const uint32_t*>(kbs + ln * KRB) + (D == 128 ? lg * DPL : (lg >> 1));
+  // capacity (a contiguous stream's, or a page) is a multiple of 64 and >= T,
+  // so whole 64-token tiles of the split stay inside it.
   const int lsh = 4 * (lg & 1);  // D = 64: this lane group's nibble half
   auto load1 = [&](int slot, int tile) {
+    const int64_t rb = tile_row(tile);
+    const uint32_t* krow0 = reinterpret_cast<const uint32_t*>(kst + (rb + ln) * KRB) +
+                            (D == 128 ? lg * DPL : (lg >> 1));
+    const float* knt = knorm + rb;
+    const float* vnt = vnorm + rb;
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
-      const int t16 = tile * 64 + sub * 16;
-      const uint32_t* krow = krow0 + t16 * (KRB / 4);
+      const uint32_t* krow = krow0 + sub * 16 * (KRB / 4);
 #pragma unroll
       for (int x = 0; x < NLD; ++x) kd[slot][sub][x] = krow[D == 128 ? x : 2 * x];
-      kn[slot][sub] = knbs[t16 + ln];
-      vv[slot][sub] = vnbs[t16 + ln];
+      kn[slot][sub] = knt[sub * 16 + ln];
+      vv[slot][sub] = vnt[sub * 16 + ln];
     }
   };
   auto score1 = [&](int slot, int tile) {
@@ -767,18 +775,16 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 #pragma unroll
       for (int s = 0; s < NP; ++s) acc2[c][mi][s] = qkv_v4i{0, 0, 0, 0};
   // V plane words of the next PD2 tiles are in flight in a register ring.
-  const int64_t vtile0 = ts >> 5;
-  const uint32_t* vb = vst + bh * (t_stride >> 5) * VB * D;
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
   constexpr int PD2 = MTW * VB * RC > 6 ? 4 : 6;
   uint32_t vw[PD2][MTW][VB];
   auto load2 = [&](int slot, int tt) {
-    const int64_t vt = vtile0 + 2 * tt + blk;
+    const int64_t vt = (tile_row(tt) >> 5) + blk;  // 32-token V tile
 #pragma unroll
     for (int mi = 0; mi < MTW; ++mi) {
       const int j = 16 * (wave * MTW + mi) + ln;
 #pragma unroll
-      for (int k = 0; k < VB; ++k) vw[slot][mi][k] = vb[(vt * VB + k) * D + j];
+      for (int k = 0; k < VB; ++k) vw[slot][mi][k] = vst[(vt * VB + k) * D + j];
     }
   };
   auto pv2 = [&](int slot, int tt) {
@@ -1853,6 +1859,53 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
                            vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
                            workspace, ws_bytes, n_splits, stream);
+}
+
+// Decode attention over a paged store (pages of 64 tokens holding all Hkv
+// heads of one sequence; see QkvPages): the MFMA path only.
+extern "C" int qkv_paged_decode_attention(
+    const void* q, int32_t q_dtype, const uint8_t* kpool, const float* knorm,
+    const uint32_t* vpool, const float* vnorm, const int32_t* page_table, int32_t pages_per_seq,
+    int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+    int32_t vbits, const float* pi, const float* kcent_host, const float* vcent_host,
+    const float* signs, float qjl_scale, float scale, int32_t causal, void* out,
+    int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
+  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
+  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
+  QKV_REQUIRE(page_table && pages_per_seq > 0 && qkv_aligned(page_table, 4),
+              "page table missing or not 4-byte aligned");
+  QKV_REQUIRE(T <= int64_t(pages_per_seq) * kPageTokens,
+              "%lld tokens exceed the page table's %d pages of %d", (long long)T, pages_per_seq,
+              kPageTokens);
+  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  QKV_REQUIRE(q && kpool && knorm && vpool && vnorm && pi && kcent_host && vcent_host && signs &&
+                  out,
+              "null pointer");
+  const int64_t t_stride = int64_t(pages_per_seq) * kPageTokens;
+  if (!use_mfma(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride, T, n_splits)) {
+    qkv_set_error("paged stores decode on the MFMA path only (symmetric codebooks, key MSE "
+                  "bits <= 2, d = 64 or 128, splits of at most %d tokens)", kSplitMax);
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype) && qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
+                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
+  if (st != QKV_OK) return st;
+  KVLayers kv{};
+  kv.kst[0] = kpool;
+  kv.knorm[0] = knorm;
+  kv.vst[0] = vpool;
+  kv.vnorm[0] = vnorm;
+  kv.ptab = page_table;
+  kv.pmax = pages_per_seq;
+  st = partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
+                      scale, causal, workspace, ws_bytes, n_splits,
+                      static_cast<hipStream_t>(stream));
+  if (st != QKV_OK) return st;
+  return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
+                               n_splits, stream);
 }
 
 // One decode step over n_layers layers that share shapes, bit widths and

@@ -177,3 +177,36 @@ struct QkvDecompressArgs {
 // qkv_decompress_mfma launches them.
 bool qkv_decompress_mfma_ok(const QkvDecompressArgs& a);
 int qkv_decompress_mfma(const QkvDecompressArgs& a, hipStream_t s);
+
+// ------------------------------------------------------ paged cache stores
+
+// A paged store: pages of 64 tokens, each holding those tokens of all H kv
+// heads of one sequence; tab[b * pmax + t / 64] is the page of sequence b's
+// token t.  tab == nullptr: the contiguous store (stream grp = b * H + h at
+// rows grp * t_stride ..).  Page pg's stream h then occupies the 64 rows
+// (pg * H + h) * 64 .. of the same row / tile arrays.
+struct QkvPages {
+  const int32_t* tab;
+  int32_t pmax;  // pages per sequence in the table
+  int32_t H;     // kv heads
+};
+
+constexpr int kPageTokens = 64;
+
+// Store row (K row, norm) of token p of stream grp.
+__device__ __forceinline__ int64_t qkv_store_row(const QkvPages& pg, int64_t grp,
+                                                 int64_t t_stride, int64_t p) {
+  if (pg.tab == nullptr) return grp * t_stride + p;
+  const int64_t b = grp / pg.H, h = grp - b * pg.H;
+  const int64_t page = pg.tab[b * pg.pmax + (p >> 6)];
+  return (page * pg.H + h) * kPageTokens + (p & 63);
+}
+
+// 32-token V tile holding token p of stream grp.
+__device__ __forceinline__ int64_t qkv_store_vtile(const QkvPages& pg, int64_t grp,
+                                                   int64_t t_stride, int64_t p) {
+  if (pg.tab == nullptr) return grp * (t_stride >> 5) + (p >> 5);
+  const int64_t b = grp / pg.H, h = grp - b * pg.H;
+  const int64_t page = pg.tab[b * pg.pmax + (p >> 6)];
+  return (page * pg.H + h) * (kPageTokens / 32) + ((p >> 5) & 1);
+}

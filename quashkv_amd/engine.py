@@ -339,17 +339,21 @@ class QuashKVEngine:
         pack_bits rows when pack_storage, else one byte per code, plus fp32 norms."""
         if not self._blocks:
             return 0
-        st = self._store
+        B, H = self._heads()
         d = self.head_dim
         if self._kmix:   # one uint8 per key code (as MixedPrecisionMSEQuantizer keeps them)
             row = d + (N.packed_row_bytes(d, self.value_bits) if self.pack_storage else d)
-            return st.B * st.H * self._total_tokens * (row + 8)
+            return B * H * self._total_tokens * (row + 8)
         if self.pack_storage:
             row = (N.packed_row_bytes(d, self.key_bits - 1) + N.packed_row_bytes(d, 1)
                    + N.packed_row_bytes(d, self.value_bits))
         else:
             row = 3 * d
-        return st.B * st.H * self._total_tokens * (row + 8)
+        return B * H * self._total_tokens * (row + 8)
+
+    def _heads(self) -> tuple[int, int]:
+        """(batch, kv heads) of the cache."""
+        return self._store.B, self._store.H
 
     def to(self, device) -> "QuashKVEngine":
         self.device = torch.device(device)

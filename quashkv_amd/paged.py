@@ -1,0 +1,387 @@
+"""Paged compressed KV cache: fixed 64-token pages from a shared pool and a
+page table per sequence, the "preallocated, paged packed-cache format" the
+reference's vLLM page manager leaves open (QuashKVPageManager,
+quashkv/integrations/vllm_backend.py:82-195, whose ``block_size`` is unused:
+it keeps one engine of per-append tensors).
+
+A page holds 64 tokens of all H kv heads of one sequence, in the store
+formats of quashkv_amd.store (C ABI "Paged cache store"):
+
+* ``kpool`` (P, H, 64, (mbits + 1) d / 8) uint8 -- K rows (MSE planes, QJL plane);
+* ``knorm`` / ``vnorm`` (P, H, 64) fp32;
+* ``vpool`` (P, H, 2, vbits, d) int32 -- two 32-token V bit-plane tiles.
+
+``table`` (B, pages_per_seq) int32 on the device maps sequence b's token t to
+page ``table[b, t // 64]``.  The append kernels (qkv_paged_store_append)
+compress bf16 / fp16 K/V straight into the pages; the split-K decode kernel
+(qkv_paged_decode_attention) follows the table per 32-token tile.  Pages come
+from a free list, are cleared when handed out and return to it on clear();
+the pool doubles when the free list runs dry (page ids stay valid).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _native as N
+from .engine import CompressedKVBlock, QuashKVEngine
+from .kernels import CompressedBlock
+from .packing import pack_bits
+from .quantizer import compress_into
+from .store import KVStore
+
+PAGE_TOKENS = 64
+
+
+class PagedKVStore:
+    """Page pool + page table of B sequences with H kv heads each."""
+
+    def __init__(self, B: int, H: int, d: int, mbits: int, vbits: int, num_pages: int,
+                 device: torch.device):
+        if d % 32 != 0:
+            raise ValueError(f"head_dim {d} must be a multiple of 32 for the cache store")
+        self.B, self.H, self.d = B, H, d
+        self.mbits, self.vbits = mbits, vbits
+        self.krb = (mbits + 1) * d // 8
+        self.device = torch.device(device)
+        self.num_pages = 0
+        self.kpool = self.knorm = self.vpool = self.vnorm = None
+        self.free: list[int] = []
+        self.pages: list[list[int]] = [[] for _ in range(B)]   # page ids of each sequence
+        self.table = torch.zeros(B, 1, dtype=torch.int32, device=self.device)
+        self._grow_pool(max(int(num_pages), 1))
+
+    # ------------------------------------------------------------- pool
+
+    def _grow_pool(self, pages: int) -> None:
+        H, d, dev = self.H, self.d, self.device
+        old = self.num_pages
+        kpool = torch.zeros(pages, H, PAGE_TOKENS, self.krb, dtype=torch.uint8, device=dev)
+        knorm = torch.zeros(pages, H, PAGE_TOKENS, dtype=torch.float32, device=dev)
+        vpool = torch.zeros(pages, H, PAGE_TOKENS // 32, self.vbits, d, dtype=torch.int32,
+                            device=dev)
+        vnorm = torch.zeros(pages, H, PAGE_TOKENS, dtype=torch.float32, device=dev)
+        if old:
+            kpool[:old].copy_(self.kpool)
+            knorm[:old].copy_(self.knorm)
+            vpool[:old].copy_(self.vpool)
+            vnorm[:old].copy_(self.vnorm)
+        self.kpool, self.knorm, self.vpool, self.vnorm = kpool, knorm, vpool, vnorm
+        self.free.extend(range(old, pages))
+        self.num_pages = pages
+
+    def _take(self, n: int) -> list[int]:
+        if n > len(self.free):
+            self._grow_pool(max(2 * self.num_pages, self.num_pages + n - len(self.free)))
+        got, self.free = self.free[:n], self.free[n:]
+        return got
+
+    @property
+    def pages_per_seq(self) -> int:
+        return self.table.shape[1]
+
+    def ensure(self, tokens: int) -> None:
+        """Pages for tokens [0, tokens) of every sequence, new pages cleared."""
+        need = -(-tokens // PAGE_TOKENS)
+        have = len(self.pages[0])
+        if need <= have:
+            return
+        new = self._take(self.B * (need - have))
+        idx = torch.tensor(new, dtype=torch.long, device=self.device)
+        for t in (self.kpool, self.knorm, self.vpool, self.vnorm):
+            t.index_fill_(0, idx, 0)
+        for b in range(self.B):
+            self.pages[b].extend(new[b * (need - have):(b + 1) * (need - have)])
+        width = max(need, self.pages_per_seq)
+        if width > self.pages_per_seq:
+            width = max(width, 2 * self.pages_per_seq)
+        tab = torch.zeros(self.B, width, dtype=torch.int32)
+        for b in range(self.B):
+            tab[b, :need] = torch.tensor(self.pages[b], dtype=torch.int32)
+        self.table = tab.to(self.device)
+
+    def release(self) -> None:
+        """Every sequence's pages back to the free list."""
+        for p in self.pages:
+            self.free.extend(p)
+            p.clear()
+
+    def to(self, device) -> None:
+        self.device = torch.device(device)
+        for name in ("kpool", "knorm", "vpool", "vnorm", "table"):
+            setattr(self, name, getattr(self, name).to(self.device))
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size()
+                   for t in (self.kpool, self.knorm, self.vpool, self.vnorm))
+
+    # ------------------------------------------------ token <-> page rows
+
+    def _rows(self, t0: int, S: int) -> torch.Tensor:
+        """(B, H, S) flat row ids (pool row p H 64 + h 64 + slot) of tokens [t0, t0 + S)."""
+        t = torch.arange(t0, t0 + S, device=self.device)
+        page = self.table.long()[:, t // PAGE_TOKENS]                      # (B, S)
+        h = torch.arange(self.H, device=self.device)
+        return (page[:, None, :] * self.H + h[None, :, None]) * PAGE_TOKENS + \
+            (t % PAGE_TOKENS)[None, None, :]
+
+    def _tiles(self, t0: int, S: int) -> tuple[torch.Tensor, int, int]:
+        """Flat V tile ids (B, H, n) of the 32-token tiles covering [t0, t0 + S),
+        with the first tile index j0 = t0 // 32 and n."""
+        j0, j1 = t0 // 32, (t0 + S - 1) // 32 + 1
+        j = torch.arange(j0, j1, device=self.device)
+        page = self.table.long()[:, j // 2]
+        h = torch.arange(self.H, device=self.device)
+        return (page[:, None, :] * self.H + h[None, :, None]) * 2 + (j % 2)[None, None, :], \
+            j0, j1 - j0
+
+    def write_from(self, tmp: KVStore, t0: int, S: int) -> None:
+        """Tokens [t0 % 64, t0 % 64 + S) of a contiguous store into the pages at
+        [t0, t0 + S).  The pages' bits of those tokens are still clear (pages
+        are cleared when handed out and each token is written once)."""
+        o = t0 % PAGE_TOKENS
+        rows = self._rows(t0, S).reshape(-1)
+        self.kpool.view(-1, self.krb)[rows] = tmp.kst[:, :, o:o + S].reshape(-1, self.krb)
+        self.knorm.view(-1)[rows] = tmp.knorm[:, :, o:o + S].reshape(-1)
+        self.vnorm.view(-1)[rows] = tmp.vnorm[:, :, o:o + S].reshape(-1)
+        tiles, j0, n = self._tiles(t0, S)
+        jt = j0 - (t0 - o) // 32                   # tmp tile of global tile j0
+        flat = self.vpool.view(-1, self.vbits, self.d)
+        tiles = tiles.reshape(-1)
+        flat[tiles] = flat[tiles] | tmp.vst[:, :, jt:jt + n].reshape(-1, self.vbits, self.d)
+
+    def gather(self, T: int) -> KVStore:
+        """Tokens [0, T) as a contiguous KVStore (capacity T rounded to 64)."""
+        st = KVStore(self.B, self.H, self.d, self.mbits, self.vbits, max(T, 1), self.device)
+        if T == 0:
+            return st
+        rows = self._rows(0, T).reshape(-1)
+        st.kst[:, :, :T] = self.kpool.view(-1, self.krb)[rows].view(self.B, self.H, T, self.krb)
+        st.knorm[:, :, :T] = self.knorm.view(-1)[rows].view(self.B, self.H, T)
+        st.vnorm[:, :, :T] = self.vnorm.view(-1)[rows].view(self.B, self.H, T)
+        tiles, _, n = self._tiles(0, T)
+        st.vst[:, :, :n] = self.vpool.view(-1, self.vbits, self.d)[tiles.reshape(-1)].view(
+            self.B, self.H, n, self.vbits, self.d)
+        return st
+
+
+class PagedQuashKVEngine(QuashKVEngine):
+    """QuashKVEngine (quashkv/engine.py:54-360) over a paged store.
+
+    Same quantizers, append / attention / clear / metrics semantics; tokens
+    live in 64-token pages of one pool (``num_pages`` to start with).  bf16 /
+    fp16 K/V compress straight into the pages; other dtypes go through the
+    generic compress kernel and are scattered into the pages.  Attention runs
+    the integer-MFMA split-K kernel, which covers head_dim 64 / 128 with keys
+    of 2 or 3 total bits (``covers``)."""
+
+    def __init__(self, head_dim: int = 128, key_bits: int = 3, value_bits: int = 3,
+                 seed: int = 42, device=None, num_pages: int = 0):
+        super().__init__(head_dim=head_dim, key_bits=key_bits, value_bits=value_bits, seed=seed,
+                         device=device)
+        if not self.covers(head_dim, key_bits, value_bits):
+            raise ValueError("the paged cache runs head_dim 64 or 128, key_bits 2 or 3 and "
+                             "value_bits 1..4")
+        self.initial_pages = num_pages
+        self._paged: Optional[PagedKVStore] = None
+
+    @staticmethod
+    def covers(head_dim: int, key_bits: int, value_bits: int) -> bool:
+        return head_dim in (64, 128) and key_bits in (2, 3) and 1 <= value_bits <= 4
+
+    # -------------------------------------------------------------- storage
+
+    def append(self, keys: torch.Tensor, values: torch.Tensor) -> None:
+        """Compress (B, H, S, d) keys/values into the pages (quashkv/engine.py:145-172)."""
+        dev = N.require_gpu(keys, values, what="PagedQuashKVEngine.append")
+        if keys.dim() != 4 or keys.shape != values.shape or keys.shape[-1] != self.head_dim:
+            raise ValueError(
+                f"Expected keys and values of shape (batch, n_heads, seq_len, {self.head_dim}); "
+                f"got {tuple(keys.shape)} and {tuple(values.shape)}")
+        if self.value_quantizer.Pi.device != dev:
+            self.to(dev)
+        B, H, S, d = keys.shape
+        st = self._paged
+        if st is not None and (st.B, st.H) != (B, H):
+            raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
+                             f"(B={st.B}, H={st.H})")
+        if st is None:
+            pages = self.initial_pages or B * max(1, -(-S // PAGE_TOKENS))
+            st = self._paged = PagedKVStore(B, H, d, self.key_bits - 1, self.value_bits, pages,
+                                            dev)
+        t0 = self._total_tokens
+        st.ensure(t0 + S)
+        if S > 0 and not self._append_paged(keys, values, t0):
+            self._append_scatter(keys, values, t0)
+        self._blocks.append((t0, S))
+        self._total_tokens += S
+
+    def _append_paged(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
+        """bf16 / fp16 K/V straight into the pages (qkv_paged_store_append)."""
+        if keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype:
+            return False
+        B, H, S, d = keys.shape
+        kq, vq = self.key_quantizer, self.value_quantizer
+        mq = kq.mse_quantizer
+        if self._host_tables is None:
+            self._host_tables = (N.HostFloats(mq.codebook.centroids_host),
+                                 N.HostFloats(mq.codebook.boundaries_host),
+                                 N.HostFloats(vq.codebook.boundaries_host))
+        kc, kb, vb = self._host_tables
+        st = self._paged
+        k, v = keys.contiguous(), values.contiguous()
+        dt = N.dtype_code(k.dtype)
+        stream = N.stream(k.device)
+        L = N.lib()
+        N.check(L.qkv_paged_store_append(
+            dt, k.data_ptr(), None, B, H, S, d, kq.mse_bits, vq.bits, mq.Pi.data_ptr(),
+            kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(), st.knorm.data_ptr(),
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, t0,
+            stream))
+        N.check(L.qkv_paged_store_append(
+            dt, None, v.data_ptr(), B, H, S, d, kq.mse_bits, vq.bits, vq.Pi.data_ptr(), None,
+            None, None, vb.ptr, None, None, st.vpool.data_ptr(), st.vnorm.data_ptr(),
+            st.table.data_ptr(), st.pages_per_seq, t0, stream))
+        return True
+
+    def _append_scatter(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
+        """Other dtypes: the generic compress kernel into a contiguous store at
+        the pages' token offset, then rows and tiles into the pages."""
+        B, H, S, d = keys.shape
+        kq, vq = self.key_quantizer, self.value_quantizer
+        mq = kq.mse_quantizer
+        dev = keys.device
+        n = B * H * S
+        kc = torch.empty(n, d, dtype=torch.uint8, device=dev)
+        kb = torch.empty(n, d, dtype=torch.uint8, device=dev)
+        vc = torch.empty(n, d, dtype=torch.uint8, device=dev)
+        kn = torch.empty(n, dtype=torch.float32, device=dev)
+        vn = torch.empty(n, dtype=torch.float32, device=dev)
+        compress_into(N.QKV_MODE_IP, keys.reshape(n, d), mq.Pi, mq.codebook.boundaries,
+                      mq.codebook.centroids, kq.mse_bits, kq.S, kc, kb, kn, packed=False)
+        compress_into(N.QKV_MODE_MSE, values.reshape(n, d), vq.Pi, vq.codebook.boundaries,
+                      vq.codebook.centroids, vq.bits, None, vc, None, vn, packed=False)
+        o = t0 % PAGE_TOKENS
+        st = self._paged
+        tmp = KVStore(B, H, d, st.mbits, st.vbits, o + S, dev)
+        tmp.knorm[:, :, o:o + S].copy_(kn.view(B, H, S))
+        tmp.vnorm[:, :, o:o + S].copy_(vn.view(B, H, S))
+        tmp.write_codes(o, S, kc, kb, vc)
+        st.write_from(tmp, t0, S)
+
+    @property
+    def _store(self):
+        """Tokens so far as a contiguous store (gathered from the pages), for
+        code that reads codes back; None before the first append."""
+        if self._paged is None:
+            return None
+        return self._paged.gather(self._total_tokens)
+
+    @_store.setter
+    def _store(self, value) -> None:
+        if value is not None:
+            raise AttributeError("PagedQuashKVEngine keeps its tokens in pages")
+
+    @property
+    def paged_store(self) -> Optional[PagedKVStore]:
+        return self._paged
+
+    @property
+    def _cache(self) -> list:
+        st = self._store
+        out = []
+        for t0, s in self._blocks:
+            kc, kb, vc = st.read_codes(t0, s)
+            sl = slice(t0, t0 + s)
+            if self.pack_storage:
+                kc, kb, vc = pack_bits(kc, self.key_bits - 1), pack_bits(kb, 1), \
+                    pack_bits(vc, self.value_bits)
+            out.append(CompressedKVBlock(
+                mse_indices=kc, qjl_signs=kb, key_norms=st.knorm[:, :, sl],
+                val_indices=vc, val_norms=st.vnorm[:, :, sl], seq_len=s,
+                packed=bool(self.pack_storage)))
+        return out
+
+    def _heads(self) -> tuple[int, int]:
+        return self._paged.B, self._paged.H
+
+    def clear(self) -> None:
+        if self._paged is not None:
+            self._paged.release()
+        super().clear()
+
+    # ------------------------------------------------------------ attention
+
+    def attention(self, queries: torch.Tensor, scale: Optional[float] = None,
+                  causal: bool = False, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+        """Attention of (B, Hq, Q, d) queries over every cached token
+        (quashkv/engine.py:204-299), Hq a multiple of the kv heads."""
+        if not self._blocks or self._total_tokens == 0:
+            raise ValueError("No compressed KV blocks in cache. Call append() first.")
+        st = self._paged
+        dev = N.require_gpu(queries, what="PagedQuashKVEngine.attention")
+        B, Hq, Q, d = queries.shape
+        if B != st.B or d != self.head_dim or Hq % st.H != 0:
+            raise ValueError(f"queries {tuple(queries.shape)} do not match the cache "
+                             f"(B={st.B}, kv heads={st.H}, head_dim={self.head_dim})")
+        if scale is None:
+            scale = 1.0 / math.sqrt(d)
+        T = self._total_tokens
+        kq, vq = self.key_quantizer, self.value_quantizer
+        mq = kq.mse_quantizer
+        L = N.lib()
+        splits = L.qkv_attention_splits(B, Hq, st.H, Q, d, T)
+        need = L.qkv_attention_workspace_bytes(B, Hq, st.H, Q, d, splits)
+        if self._workspace is None or self._workspace.numel() < need \
+                or self._workspace.device != dev:
+            self._workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+        q = queries.contiguous()
+        if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            q = q.float()
+        kc = N.HostFloats(mq.codebook.centroids_host)
+        vc = N.HostFloats(vq.codebook.centroids_host)
+        out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
+        N.check(L.qkv_paged_decode_attention(
+            q.data_ptr(), N.dtype_code(q.dtype), st.kpool.data_ptr(), st.knorm.data_ptr(),
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, T,
+            B, Hq, st.H, Q, d, st.mbits, st.vbits, mq.Pi.data_ptr(), kc.ptr, vc.ptr,
+            kq.S.data_ptr(), float(kq.qjl_scale), float(scale), 1 if causal else 0,
+            out.data_ptr(), N.dtype_code(out_dtype), self._workspace.data_ptr(),
+            self._workspace.numel(), splits, N.stream(dev)))
+        return out
+
+    # -------------------------------------------------------------- metrics
+
+    def pool_bytes(self) -> int:
+        """Device bytes of the page pool."""
+        return 0 if self._paged is None else self._paged.nbytes()
+
+    def to(self, device) -> "PagedQuashKVEngine":
+        self.device = torch.device(device)
+        self.key_quantizer.to(device)
+        self.value_quantizer.to(device)
+        if self._paged is not None:
+            self._paged.to(device)
+        self._workspace = None
+        return self
+
+    def __repr__(self) -> str:
+        pages = 0 if self._paged is None else self._paged.num_pages
+        return (f"PagedQuashKVEngine(head_dim={self.head_dim}, key_bits={self.key_bits}, "
+                f"value_bits={self.value_bits}, cached_tokens={self._total_tokens}, "
+                f"pages={pages}, device={self.device})")
+
+
+def compressed_blocks(engine: QuashKVEngine) -> list[CompressedBlock]:
+    """The engine's blocks as unpacked CompressedBlocks (quashkv/integrations/
+    vllm_backend.py:116-129)."""
+    out = []
+    for blk in engine._cache:
+        mse, qjl, val = engine._unpack_block(blk)
+        out.append(CompressedBlock(mse_indices=mse, qjl_signs=qjl, key_norms=blk.key_norms,
+                                   val_indices=val, val_norms=blk.val_norms,
+                                   seq_len=blk.seq_len))
+    return out
