@@ -484,6 +484,80 @@ def bench_cfg4(args) -> None:
     print(json.dumps(line), flush=True)
 
 
+def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_bytes):
+    """cfg3 over the paged store (quashkv_amd.paged: 64-token pages handed out
+    in shuffled order, a device page table per sequence): the same K/V as the
+    contiguous caches, appended with qkv_paged_store_append and decoded with
+    qkv_paged_decode_attention (prepare + split + combine in one call)."""
+    import random
+    import torch
+    from quashkv_amd import _native as N
+    from quashkv_amd.paged import PagedKVStore, PagedQuashKVEngine
+
+    pengs, app_ms = [], []
+    for c in range(args.copies):
+        k, v = make_inputs(2 + 1000 * c, dev, torch.bfloat16)
+        pe = PagedQuashKVEngine(head_dim=D, key_bits=KEY_BITS, value_bits=VAL_BITS, seed=42,
+                                device=dev)
+        pe._paged = PagedKVStore(B, HKV, D, KEY_BITS - 1, VAL_BITS, B * T // 64, dev)
+        random.Random(c).shuffle(pe._paged.free)
+        pe.append(k, v)
+        if c == 0:
+            # the append kernels into the allocated pages (as the contiguous
+            # measurement re-appends into its allocated store)
+            for _ in range(3):
+                pe._append_paged(k, v, 0)
+            for _ in range(3):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                for _ in range(args.compress_reps):
+                    pe._append_paged(k, v, 0)
+                e1.record(stream)
+                torch.cuda.synchronize()
+                app_ms.append(e0.elapsed_time(e1) / args.compress_reps)
+        pengs.append(pe)
+        del k, v
+    same = all(torch.equal(pe.attention(q), e.attention(q))
+               for pe, e, q in zip(pengs, engines, queries))
+    splits = lib.qkv_attention_splits(B, HQ, HKV, 1, D, T)
+    ws_bytes = lib.qkv_attention_workspace_bytes(B, HQ, HKV, 1, D, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty(B, HQ, 1, D, dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i):
+        pe, q = pengs[i % args.copies], queries[i % args.copies]
+        st, kq = pe.paged_store, pe.key_quantizer
+        mq = kq.mse_quantizer
+        N.check(lib.qkv_paged_decode_attention(
+            q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, T,
+            B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr, vc_h.ptr,
+            kq.S.data_ptr(), kq.qjl_scale, scale, 0, out.data_ptr(), N.QKV_F32, ws.data_ptr(),
+            ws_bytes, splits, sptr))
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(args.steps):
+        step(args.warmup + i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    io_bytes = B * HQ * D * (2 + 4)
+    gbs = (kv_bytes + io_bytes) / (ms * 1e-3) / 1e9
+    n_vec = 2 * B * HKV * T
+    a_ms = statistics.median(app_ms)
+    return {"what": "cfg3 decode + append over 64-token pages (shuffled page order, "
+                    "one page table per sequence)",
+            "decode_us_per_step": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+            "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
+            "append_gvec_s": round(n_vec / (a_ms * 1e-3) / 1e9, 4),
+            "output_identical_to_contiguous": same}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -655,6 +729,8 @@ def main() -> None:
     dec_bytes = n_rows * ((KEY_BITS - 1) * D // 8 + VAL_BITS * D // 8 + 2 * 4 + 2 * D * 4)
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
 
+    paged = paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_bytes)
+
     # measured HBM ceiling on this device: a 1 GiB device copy (read + write;
     # each buffer exceeds the 256 MB MALL)
     big = torch.empty(1 << 28, device=dev).uniform_()
@@ -747,6 +823,7 @@ def main() -> None:
             "algorithmic_bytes_per_launch": kv_bytes,
             "avg_kernel_us": round(partial_ms * 1e3, 2),
         },
+        "paged": paged,
         "cpu_baseline": cpu,
         "cpu_baseline_compress": cpu_comp,
         "cpu_baseline_decompress": cpu_dec,

@@ -291,6 +291,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    QkvSpan sp{};
+    if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, t0 + s0);
     uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
     {
       const uint16_t* row[kHalves];
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       if (lane < 32) {
         if (32 * tt + li < nv) {
           const int64_t t = t0 + s0 + 32 * tt + li;
-          knorm[PAGED ? qkv_store_row(pg, grp, t_stride, t) : grp * t_stride + t] = nrm;
+          knorm[PAGED ? sp.row(t) : grp * t_stride + t] = nrm;
         }
         invw[32 * tt + li] = iscale / nrm;
       }
@@ -369,7 +371,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       for (int i = 0; i < NSK; ++i) {
         const int w = i * 64 + lane, r = w / RD;
         if (w < nv * RD)
-          dst[qkv_store_row(pg, grp, t_stride, t0 + s0 + r) * RD + (w - r * RD)] = stg[i];
+          dst[sp.row(t0 + s0 + r) * RD + (w - r * RD)] = stg[i];
       }
     } else {
       uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
@@ -536,6 +538,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const int64_t grp = tile / tpg;
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
+    QkvSpan sp{};
+    if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, A0);
     bool ok[kHalves];
     uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
     {
@@ -559,7 +563,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
       if (lane < 32 && ok[tt]) {
         const int64_t t = A0 + 32 * tt + li;
-        vnorm[PAGED ? qkv_store_row(pg, grp, t_stride, t) : grp * t_stride + t] = nrm;
+        vnorm[PAGED ? sp.row(t) : grp * t_stride + t] = nrm;
       }
       inv[tt] = iscale / nrm;
     }
@@ -608,7 +612,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       if (hi <= lo) continue;
       const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
                                           : (((1u << (hi - lo)) - 1u) << lo);
-      const int64_t vt = PAGED ? qkv_store_vtile(pg, grp, t_stride, tok0)
+      const int64_t vt = PAGED ? (sp.row(tok0) >> 5)
                                : grp * (t_stride >> 5) + (tok0 >> 5);
       uint32_t* p = vst + (vt * VB + k) * D + j;
       uint32_t val = stg[i];

@@ -101,6 +101,7 @@ __host__ __device__ constexpr int n_odd_subsets(int bits) {
 }
 
 constexpr int kSplitMax = 2048;  // tokens per split on the MFMA path (LDS scores)
+static_assert(kSplitMax / 64 <= 64, "a split's tiles fit one page entry per lane");
 constexpr int kRowsM = 4;        // query rows per workgroup on the MFMA path
 constexpr int kNUMax = 6;        // score MFMAs per 16 tokens (d = 128, 2 MSE bits)
 
@@ -666,9 +667,13 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int ntile1 = (ntok + 63) >> 6;
   // First store row of the split's 64-token tile `tile`: linear in the tile
   // for a contiguous store, the tile's page for a paged one.
+  // (paged: lane l holds the page of the split's tile l, read once; a split
+  // has at most kSplitMax / 64 <= 64 tiles)
   const int32_t* __restrict__ ptab = kv.ptab;
+  int tile_page = 0;
+  if (ptab != nullptr && lane < ntile1) tile_page = ptab[bseq * kv.pmax + (ts >> 6) + lane];
   auto tile_row = [&](int tile) -> int64_t {
-    if (ptab) return (int64_t(ptab[bseq * kv.pmax + (ts >> 6) + tile]) * Hkv + hkv) * 64;
+    if (ptab) return (int64_t(__builtin_amdgcn_readlane(tile_page, tile)) * Hkv + hkv) * 64;
     return bh * t_stride + ts + int64_t(tile) * 64;
   };
   constexpr int PD1 = RC == 2 ? 1 : 2;  // (registers: two chunks' accumulators)

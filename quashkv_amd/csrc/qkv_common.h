@@ -193,20 +193,35 @@ struct QkvPages {
 
 constexpr int kPageTokens = 64;
 
-// Store row (K row, norm) of token p of stream grp.
-__device__ __forceinline__ int64_t qkv_store_row(const QkvPages& pg, int64_t grp,
-                                                 int64_t t_stride, int64_t p) {
-  if (pg.tab == nullptr) return grp * t_stride + p;
-  const int64_t b = grp / pg.H, h = grp - b * pg.H;
-  const int64_t page = pg.tab[b * pg.pmax + (p >> 6)];
-  return (page * pg.H + h) * kPageTokens + (p & 63);
+// Store rows of the 64-token span [t, t + 64) of stream grp.  On a paged
+// store the span meets at most two pages, looked up once; row(t) >> 5 is the
+// token's 32-token V tile (store capacity a multiple of 32).
+struct QkvSpan {
+  int64_t base0, base1;  // store row of token 64 p0 and of token 64 (p0 + 1)
+  int64_t p0;
+  __device__ __forceinline__ int64_t row(int64_t t) const {
+    return ((t >> 6) == p0 ? base0 : base1) + (t & 63);
+  }
+};
+
+// Span rows of stream grp from token t (t and every token the caller asks
+// for lie below the table's pages_per_seq * 64).
+__device__ __forceinline__ QkvSpan qkv_span(const QkvPages& pg, int64_t grp, int64_t t_stride,
+                                            int64_t t) {
+  QkvSpan s;
+  s.p0 = t >> 6;
+  if (pg.tab == nullptr) {
+    s.base0 = grp * t_stride + (s.p0 << 6);
+    s.base1 = s.base0 + 64;
+    return s;
+  }
+  const int g = static_cast<int>(grp), b = g / pg.H, h = g - b * pg.H;
+  const int32_t* tb = pg.tab + int64_t(b) * pg.pmax;
+  const int p = static_cast<int>(s.p0);
+  const int64_t pa = tb[p];
+  const int64_t pb = p + 1 < pg.pmax ? tb[p + 1] : pa;
+  s.base0 = (pa * pg.H + h) * kPageTokens;
+  s.base1 = (pb * pg.H + h) * kPageTokens;
+  return s;
 }
 
-// 32-token V tile holding token p of stream grp.
-__device__ __forceinline__ int64_t qkv_store_vtile(const QkvPages& pg, int64_t grp,
-                                                   int64_t t_stride, int64_t p) {
-  if (pg.tab == nullptr) return grp * (t_stride >> 5) + (p >> 5);
-  const int64_t b = grp / pg.H, h = grp - b * pg.H;
-  const int64_t page = pg.tab[b * pg.pmax + (p >> 6)];
-  return (page * pg.H + h) * (kPageTokens / 32) + ((p >> 5) & 1);
-}

@@ -15,8 +15,10 @@ formats of quashkv_amd.store (C ABI "Paged cache store"):
 page ``table[b, t // 64]``.  The append kernels (qkv_paged_store_append)
 compress bf16 / fp16 K/V straight into the pages; the split-K decode kernel
 (qkv_paged_decode_attention) follows the table per 32-token tile.  Pages come
-from a free list, are cleared when handed out and return to it on clear();
-the pool doubles when the free list runs dry (page ids stay valid).
+from a free list and return to it on clear(); a reused page keeps its old
+bits until tokens overwrite them (appends write whole K rows and merge V
+tile bits under a token mask; decode masks tokens past the cached length).
+The pool doubles when the free list runs dry (page ids stay valid).
 """
 
 from __future__ import annotations
@@ -84,15 +86,12 @@ class PagedKVStore:
         return self.table.shape[1]
 
     def ensure(self, tokens: int) -> None:
-        """Pages for tokens [0, tokens) of every sequence, new pages cleared."""
+        """Pages for tokens [0, tokens) of every sequence."""
         need = -(-tokens // PAGE_TOKENS)
         have = len(self.pages[0])
         if need <= have:
             return
         new = self._take(self.B * (need - have))
-        idx = torch.tensor(new, dtype=torch.long, device=self.device)
-        for t in (self.kpool, self.knorm, self.vpool, self.vnorm):
-            t.index_fill_(0, idx, 0)
         for b in range(self.B):
             self.pages[b].extend(new[b * (need - have):(b + 1) * (need - have)])
         width = max(need, self.pages_per_seq)
@@ -140,8 +139,8 @@ class PagedKVStore:
 
     def write_from(self, tmp: KVStore, t0: int, S: int) -> None:
         """Tokens [t0 % 64, t0 % 64 + S) of a contiguous store into the pages at
-        [t0, t0 + S).  The pages' bits of those tokens are still clear (pages
-        are cleared when handed out and each token is written once)."""
+        [t0, t0 + S): K rows and norms by row, V tile words merged under the
+        mask of those tokens' bits."""
         o = t0 % PAGE_TOKENS
         rows = self._rows(t0, S).reshape(-1)
         self.kpool.view(-1, self.krb)[rows] = tmp.kst[:, :, o:o + S].reshape(-1, self.krb)
@@ -151,7 +150,15 @@ class PagedKVStore:
         jt = j0 - (t0 - o) // 32                   # tmp tile of global tile j0
         flat = self.vpool.view(-1, self.vbits, self.d)
         tiles = tiles.reshape(-1)
-        flat[tiles] = flat[tiles] | tmp.vst[:, :, jt:jt + n].reshape(-1, self.vbits, self.d)
+        j = torch.arange(j0, j0 + n, device=self.device, dtype=torch.int64)
+        lo = (t0 - 32 * j).clamp(0, 32)
+        hi = (t0 + S - 32 * j).clamp(0, 32)
+        m = (torch.ones_like(j) << hi) - (torch.ones_like(j) << lo)       # bits [lo, hi)
+        m = torch.where(m >= 1 << 31, m - (1 << 32), m).to(torch.int32)
+        m = m.view(1, 1, n, 1, 1)
+        src = tmp.vst[:, :, jt:jt + n] & m
+        dst = flat[tiles].view(self.B, self.H, n, self.vbits, self.d)
+        flat[tiles] = ((dst & ~m) | src).reshape(-1, self.vbits, self.d)
 
     def gather(self, T: int) -> KVStore:
         """Tokens [0, T) as a contiguous KVStore (capacity T rounded to 64)."""

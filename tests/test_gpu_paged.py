@@ -106,11 +106,12 @@ def test_paged_matches_contiguous(d, dtype, key_bits, value_bits):
     _close(paged.attention(q, causal=True), _oracle(q, paged, causal=True))
 
 
-def test_paged_clear_reuses_pages():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_paged_clear_reuses_pages(dtype):
     B, H, d = 2, 4, 128
     cont, paged = _pair(d, 3, 3, B, H, seed=9, pool_pages=2)
     gen = torch.Generator(device=DEV).manual_seed(9)
-    kv = lambda S: [torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+    kv = lambda S: [torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=dtype)
                     for _ in range(2)]
     paged.append(*kv(150))
     pages_before = paged.paged_store.num_pages
