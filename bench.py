@@ -558,6 +558,77 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
             "output_identical_to_contiguous": same}
 
 
+def hf_decode_step(args, dev, stream):
+    """One decode step of cfg2's 24 layers (batch 16, 14 query / 2 kv heads,
+    head_dim 64, 2048 cached tokens, fp16 K/V) through the HF integrations:
+    the fused path (quashkv_amd.integrations.hf_attention: append the new
+    token, fused attention over the compressed cache) against the reference's
+    QuashKVCache path (append, reconstruct the whole K^ / V^ of the layer,
+    quashkv/integrations/hf_cache.py:123-152, then softmax attention over them)
+    and against attention over an uncompressed fp32 cache."""
+    import torch
+    import torch.nn.functional as F
+    from quashkv_amd.integrations.hf_attention import QuashKVHFCache
+    from quashkv_amd.integrations.hf_cache import QuashKVCache
+
+    NL, B2, HQ2, HKV2, D2, T2 = 24, 16, 14, 2, 64, 2048
+    steps = max(4, args.steps // 3)
+    cap = T2 + 2 * (args.warmup + steps) + 64
+    g = torch.Generator(device=dev).manual_seed(5)
+    fused = QuashKVHFCache(NL, D2, device=dev)
+    recon = QuashKVCache(NL, D2, device=dev)
+    for l in range(NL):
+        k = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.float16)
+        v = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.float16)
+        for e in (fused.engines[l], recon.engines[l]):
+            e.initial_capacity = cap
+            e.append(k, v)
+    raw = [torch.randn(2, B2, HKV2, cap, D2, generator=g, device=dev) for _ in range(NL)]
+    q = torch.randn(B2, HQ2, 1, D2, generator=g, device=dev).to(torch.float16)
+    kn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.float16)
+    vn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.float16)
+    t_raw = [T2]
+
+    def step_fused():
+        for l in range(NL):
+            e = fused.engines[l]
+            e.append(kn, vn)
+            e.attention(q, out_dtype=torch.float16)
+
+    def step_recon():
+        for l in range(NL):
+            kh, vh = recon.update(kn, vn, l)
+            F.scaled_dot_product_attention(q.float(), kh, vh, enable_gqa=True)
+
+    def step_raw():
+        t = t_raw[0]
+        for l in range(NL):
+            raw[l][0, :, :, t].copy_(kn[:, :, 0])
+            raw[l][1, :, :, t].copy_(vn[:, :, 0])
+            F.scaled_dot_product_attention(q.float(), raw[l][0, :, :, :t + 1],
+                                           raw[l][1, :, :, :t + 1], enable_gqa=True)
+        t_raw[0] = t + 1
+
+    res = {}
+    for name, fn in (("fused", step_fused), ("reconstruct", step_recon), ("fp32_raw", step_raw)):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(steps):
+            fn()
+        b.record(stream)
+        torch.cuda.synchronize()
+        res[name] = a.elapsed_time(b) / steps * 1e3
+    return {"what": "cfg2 decode step, 24 layers (B 16, 14/2 heads, d 64, ~2048 cached tokens): "
+                    "append + attention per layer",
+            "fused_us_per_step": round(res["fused"], 1),
+            "reconstruct_us_per_step": round(res["reconstruct"], 1),
+            "fp32_uncompressed_us_per_step": round(res["fp32_raw"], 1),
+            "fused_speedup_vs_reconstruct": round(res["reconstruct"] / res["fused"], 2)}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -730,6 +801,7 @@ def main() -> None:
     dec_gbs = dec_bytes / (dec_ms * 1e-3) / 1e9
 
     paged = paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_bytes)
+    hf_step = hf_decode_step(args, dev, stream)
 
     # measured HBM ceiling on this device: a 1 GiB device copy (read + write;
     # each buffer exceeds the 256 MB MALL)
@@ -824,6 +896,7 @@ def main() -> None:
             "avg_kernel_us": round(partial_ms * 1e3, 2),
         },
         "paged": paged,
+        "hf_attention_cfg2": hf_step,
         "cpu_baseline": cpu,
         "cpu_baseline_compress": cpu_comp,
         "cpu_baseline_decompress": cpu_dec,
