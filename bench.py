@@ -40,7 +40,7 @@ OUTLIERS = (11, 47, 83, 119)
 # passes summarised in profiles/split_mfma_cfg3_decode.md: FETCH_SIZE x 2.0 +
 # WRITE_SIZE x 1.0 (KiB per dispatch; the factors are what the counters read
 # for a 256 MiB device copy, `bench.py --copy-calibration`).
-SPLIT_MFMA_TRAFFIC_BYTES = (112780 * 2 + 4160) * 1024
+SPLIT_MFMA_TRAFFIC_BYTES = (112796 * 2 + 4160) * 1024
 
 
 def kv_bytes_per_token_head(d: int) -> int:
