@@ -743,22 +743,43 @@ def main() -> None:
         N.check(lib.qkv_attention_combine(B, HQ, HKV, 1, D, mq.Pi.data_ptr(), out.data_ptr(),
                                           N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
 
+    def decode(i):
+        # the whole step as one call of the product entry point
+        eng = engines[i % args.copies]
+        q = queries[i % args.copies]
+        st = eng._store
+        kq = eng.key_quantizer
+        mq = kq.mse_quantizer
+        N.check(lib.qkv_decode_attention(
+            q.data_ptr(), N.QKV_BF16, st.kst.data_ptr(), st.knorm.data_ptr(), st.vst.data_ptr(),
+            st.vnorm.data_ptr(), st.capacity, T, B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS,
+            mq.Pi.data_ptr(), kc_h.ptr, vc_h.ptr, kq.S.data_ptr(), kq.qjl_scale, scale, 0,
+            out.data_ptr(), N.QKV_F32, ws.data_ptr(), ws_bytes, splits, sptr))
+
+    for i in range(args.warmup):
+        decode(i)
+    torch.cuda.synchronize()
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        decode(args.warmup + i)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    step_ms = t_start.elapsed_time(t_end) / args.steps
+    # the split kernel's own average: the same steps as three calls, HIP
+    # events around the partial launch on its stream (a separate loop, so the
+    # event records do not enter the step time above)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_start.record(stream)
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
-    t_end.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    step_ms = t_start.elapsed_time(t_end) / args.steps
     partial_ms = statistics.mean(a.elapsed_time(b) for a, b in evs)
 
     kv_bytes = B * HKV * T * kv_bytes_per_token_head(D)
