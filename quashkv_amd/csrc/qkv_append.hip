@@ -788,7 +788,7 @@ extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const 
                                       const float* vbound_host, uint8_t* kpool, float* knorm,
                                       uint32_t* vpool, float* vnorm, const int32_t* page_table,
                                       int32_t pages_per_seq, int64_t t0, void* stream) {
-  QKV_REQUIRE(B >= 0 && H > 0, "invalid shape");
+  QKV_REQUIRE(B >= 0 && H > 0 && int64_t(B) * H < (int64_t(1) << 31), "invalid shape");
   QKV_REQUIRE(page_table && pages_per_seq > 0, "null page table");
   QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
   return store_append_impl(in_dtype, keys, values, int64_t(B) * H, S, d, mbits, vbits, pi,
