@@ -499,7 +499,8 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
         k, v = make_inputs(2 + 1000 * c, dev, torch.bfloat16)
         pe = PagedQuashKVEngine(head_dim=D, key_bits=KEY_BITS, value_bits=VAL_BITS, seed=42,
                                 device=dev)
-        pe._paged = PagedKVStore(B, HKV, D, KEY_BITS - 1, VAL_BITS, B * T // 64, dev)
+        pe._paged = PagedKVStore(B, HKV, D, KEY_BITS - 1, VAL_BITS, B * T // pe.page_tokens, dev,
+                                 pe.page_tokens)
         random.Random(c).shuffle(pe._paged.free)
         pe.append(k, v)
         if c == 0:
@@ -531,8 +532,8 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
         mq = kq.mse_quantizer
         N.check(lib.qkv_paged_decode_attention(
             q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
-            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, T,
-            B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr, vc_h.ptr,
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq,
+            st.pt, T, B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr, vc_h.ptr,
             kq.S.data_ptr(), kq.qjl_scale, scale, 0, out.data_ptr(), N.QKV_F32, ws.data_ptr(),
             ws_bytes, splits, sptr))
 
@@ -550,8 +551,9 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
     gbs = (kv_bytes + io_bytes) / (ms * 1e-3) / 1e9
     n_vec = 2 * B * HKV * T
     a_ms = statistics.median(app_ms)
-    return {"what": "cfg3 decode + append over 64-token pages (shuffled page order, "
-                    "one page table per sequence)",
+    return {"what": f"cfg3 decode + append over {pengs[0].page_tokens}-token pages "
+                    "(shuffled page order, one page table per sequence)",
+            "page_tokens": pengs[0].page_tokens,
             "decode_us_per_step": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
             "pct_of_hbm_peak": round(100 * gbs / PEAK_HBM_GBS, 2),
             "append_gvec_s": round(n_vec / (a_ms * 1e-3) / 1e9, 4),

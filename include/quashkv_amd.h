@@ -426,12 +426,12 @@ int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, int32_t d,
  * Paged cache store (the "preallocated, paged packed-cache format" the
  * reference's vLLM page manager leaves unimplemented: QuashKVPageManager,
  * quashkv/integrations/vllm_backend.py:82-195, whose block_size is unused).
- * A page holds 64 tokens of all H kv heads of one sequence, in the K-row and
- * V-tile formats above: for page p and head h,
- *   kpool   rows (p H + h) 64 .. + 63, (mbits + 1) d / 8 bytes each
+ * A page holds P = page_tokens tokens (64, 128, ..., 2048) of all H kv heads
+ * of one sequence, in the K-row and V-tile formats above: for page p, head h,
+ *   kpool   rows (p H + h) P .. + P - 1, (mbits + 1) d / 8 bytes each
  *   knorm / vnorm   the same rows, fp32
- *   vpool   32-token tiles (p H + h) 2 and + 1, vbits x d uint32 words each
- * page_table[b * pages_per_seq + t / 64] is the page of sequence b's token t
+ *   vpool   32-token tiles (p H + h) P / 32 .. + P / 32 - 1, vbits x d uint32
+ * page_table[b * pages_per_seq + t / P] is the page of sequence b's token t
  * (int32, device).  Every sequence of a call holds the same token count.
  * ---------------------------------------------------------------------- */
 
@@ -444,15 +444,18 @@ int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* value
                            const float* kcent_host, const float* kbound_host,
                            const float* vbound_host, uint8_t* kpool, float* knorm,
                            uint32_t* vpool, float* vnorm, const int32_t* page_table,
-                           int32_t pages_per_seq, int64_t t0, void* stream);
+                           int32_t pages_per_seq, int32_t page_tokens, int64_t t0,
+                           void* stream);
 
 /* qkv_decode_attention over a paged store of T tokens per sequence (the MFMA
  * path: symmetric codebooks, key MSE bits <= 2, d = 64 or 128; returns
  * QKV_E_UNSUPPORTED otherwise).  Same arguments as qkv_decode_attention with
- * (kpool, knorm, vpool, vnorm, page_table, pages_per_seq) for the store. */
+ * (kpool, knorm, vpool, vnorm, page_table, pages_per_seq, page_tokens) for the
+ * store. */
 int qkv_paged_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kpool,
                                const float* knorm, const uint32_t* vpool, const float* vnorm,
-                               const int32_t* page_table, int32_t pages_per_seq, int64_t T,
+                               const int32_t* page_table, int32_t pages_per_seq,
+                               int32_t page_tokens, int64_t T,
                                int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
                                int32_t kbits, int32_t vbits, const float* pi,
                                const float* kcent_host, const float* vcent_host,

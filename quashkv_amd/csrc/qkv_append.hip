@@ -651,9 +651,9 @@ static int store_append_impl(int32_t in_dtype, const void* keys, const void* val
                 (long long)t_stride, (long long)t0, (long long)(t0 + S));
   } else {
     QKV_REQUIRE(pg.H > 0 && groups % pg.H == 0, "groups must be batch x kv heads");
-    QKV_REQUIRE(t0 + S <= int64_t(pg.pmax) * kPageTokens,
-                "page table of %d pages per sequence must hold tokens [%lld, %lld)", pg.pmax,
-                (long long)t0, (long long)(t0 + S));
+    QKV_REQUIRE(t0 + S <= (int64_t(pg.pmax) << pg.lg),
+                "page table of %d pages of %d tokens per sequence must hold tokens "
+                "[%lld, %lld)", pg.pmax, 1 << pg.lg, (long long)t0, (long long)(t0 + S));
   }
   if (in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
     qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
@@ -778,7 +778,7 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
                                 void* stream) {
   return store_append_impl(in_dtype, keys, values, groups, S, d, mbits, vbits, pi, signs,
                            kcent_host, kbound_host, vbound_host, kstore, knorm, vstore, vnorm,
-                           t_stride, t0, QkvPages{nullptr, 0, 1}, stream);
+                           t_stride, t0, QkvPages{nullptr, 0, 1, 6}, stream);
 }
 
 extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
@@ -787,13 +787,16 @@ extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const 
                                       const float* kcent_host, const float* kbound_host,
                                       const float* vbound_host, uint8_t* kpool, float* knorm,
                                       uint32_t* vpool, float* vnorm, const int32_t* page_table,
-                                      int32_t pages_per_seq, int64_t t0, void* stream) {
+                                      int32_t pages_per_seq, int32_t page_tokens, int64_t t0,
+                                      void* stream) {
   QKV_REQUIRE(B >= 0 && H > 0 && int64_t(B) * H < (int64_t(1) << 31), "invalid shape");
   QKV_REQUIRE(page_table && pages_per_seq > 0, "null page table");
+  const int lg = qkv_page_lg(page_tokens);
+  QKV_REQUIRE(lg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
   QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
   return store_append_impl(in_dtype, keys, values, int64_t(B) * H, S, d, mbits, vbits, pi,
                            signs, kcent_host, kbound_host, vbound_host, kpool, knorm, vpool,
-                           vnorm, kPageTokens, t0, QkvPages{page_table, pages_per_seq, H},
+                           vnorm, page_tokens, t0, QkvPages{page_table, pages_per_seq, H, lg},
                            stream);
 }
 

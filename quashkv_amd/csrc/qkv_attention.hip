@@ -80,8 +80,9 @@ struct KVLayers {  // the store
   const float* knorm[kMaxLayers];
   const uint32_t* vst[kMaxLayers];
   const float* vnorm[kMaxLayers];
-  const int32_t* ptab;  // paged store: page of sequence b's token t at ptab[b * pmax + t / 64]
-  int32_t pmax;         // (nullptr: contiguous streams of t_stride rows)
+  const int32_t* ptab;  // paged store: page of sequence b's token t at
+  int32_t pmax;         // ptab[b * pmax + (t >> plg)] (nullptr: contiguous
+  int32_t plg;          // streams of t_stride rows); pages of 1 << plg tokens
 };
 struct OutLayers {  // un-rotation and output
   const float* pi[kMaxLayers];
@@ -671,9 +672,13 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   // has at most kSplitMax / 64 <= 64 tiles)
   const int32_t* __restrict__ ptab = kv.ptab;
   int tile_page = 0;
-  if (ptab != nullptr && lane < ntile1) tile_page = ptab[bseq * kv.pmax + (ts >> 6) + lane];
+  const int tsh = kv.plg - 6;  // log2 of the 64-token tiles per page
+  if (ptab != nullptr && lane < ntile1)
+    tile_page = ptab[bseq * kv.pmax + ((static_cast<int>(ts >> 6) + lane) >> tsh)];
   auto tile_row = [&](int tile) -> int64_t {
-    if (ptab) return (int64_t(__builtin_amdgcn_readlane(tile_page, tile)) * Hkv + hkv) * 64;
+    if (ptab)
+      return ((int64_t(__builtin_amdgcn_readlane(tile_page, tile)) * Hkv + hkv) << kv.plg) +
+             (((static_cast<int>(ts >> 6) + tile) & ((1 << tsh) - 1)) << 6);
     return bh * t_stride + ts + int64_t(tile) * 64;
   };
   constexpr int PD1 = RC == 2 ? 1 : 2;  // (registers: two chunks' accumulators)
@@ -1871,7 +1876,7 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
 extern "C" int qkv_paged_decode_attention(
     const void* q, int32_t q_dtype, const uint8_t* kpool, const float* knorm,
     const uint32_t* vpool, const float* vnorm, const int32_t* page_table, int32_t pages_per_seq,
-    int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+    int32_t page_tokens, int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
     int32_t vbits, const float* pi, const float* kcent_host, const float* vcent_host,
     const float* signs, float qjl_scale, float scale, int32_t causal, void* out,
     int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
@@ -1880,15 +1885,17 @@ extern "C" int qkv_paged_decode_attention(
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
   QKV_REQUIRE(page_table && pages_per_seq > 0 && qkv_aligned(page_table, 4),
               "page table missing or not 4-byte aligned");
-  QKV_REQUIRE(T <= int64_t(pages_per_seq) * kPageTokens,
+  const int plg = qkv_page_lg(page_tokens);
+  QKV_REQUIRE(plg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
+  QKV_REQUIRE(T <= (int64_t(pages_per_seq) << plg),
               "%lld tokens exceed the page table's %d pages of %d", (long long)T, pages_per_seq,
-              kPageTokens);
+              page_tokens);
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   QKV_REQUIRE(q && kpool && knorm && vpool && vnorm && pi && kcent_host && vcent_host && signs &&
                   out,
               "null pointer");
-  const int64_t t_stride = int64_t(pages_per_seq) * kPageTokens;
+  const int64_t t_stride = int64_t(pages_per_seq) << plg;
   if (!use_mfma(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride, T, n_splits)) {
     qkv_set_error("paged stores decode on the MFMA path only (symmetric codebooks, key MSE "
                   "bits <= 2, d = 64 or 128, splits of at most %d tokens)", kSplitMax);
@@ -1905,6 +1912,7 @@ extern "C" int qkv_paged_decode_attention(
   kv.vnorm[0] = vnorm;
   kv.ptab = page_table;
   kv.pmax = pages_per_seq;
+  kv.plg = plg;
   st = partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
                       scale, causal, workspace, ws_bytes, n_splits,
                       static_cast<hipStream_t>(stream));

@@ -189,39 +189,53 @@ struct QkvPages {
   const int32_t* tab;
   int32_t pmax;  // pages per sequence in the table
   int32_t H;     // kv heads
+  int32_t lg;    // log2 of the tokens per page
 };
 
-constexpr int kPageTokens = 64;
+// Pages hold 64 << k tokens, k = 0 .. 5 (whole 64-token tiles, at most one
+// split's worth).
+constexpr int kPageLgMin = 6, kPageLgMax = 11;
+
+// log2 of a page token count, or -1 when it is not 64 << k, k = 0 .. 5.
+inline int qkv_page_lg(int32_t page_tokens) {
+  for (int lg = kPageLgMin; lg <= kPageLgMax; ++lg)
+    if (page_tokens == (1 << lg)) return lg;
+  return -1;
+}
 
 // Store rows of the 64-token span [t, t + 64) of stream grp.  On a paged
 // store the span meets at most two pages, looked up once; row(t) >> 5 is the
 // token's 32-token V tile (store capacity a multiple of 32).
 struct QkvSpan {
-  int64_t base0, base1;  // store row of token 64 p0 and of token 64 (p0 + 1)
+  int64_t base0, base1;  // store row of the first token of page p0 and of p0 + 1
   int64_t p0;
+  int lg;                // log2 of the page (64-token blocks on a contiguous store)
   __device__ __forceinline__ int64_t row(int64_t t) const {
-    return ((t >> 6) == p0 ? base0 : base1) + (t & 63);
+    return ((t >> lg) == p0 ? base0 : base1) + (t & ((int64_t(1) << lg) - 1));
   }
 };
 
 // Span rows of stream grp from token t (t and every token the caller asks
-// for lie below the table's pages_per_seq * 64).
+// for lie below the table's pages_per_seq pages).
 __device__ __forceinline__ QkvSpan qkv_span(const QkvPages& pg, int64_t grp, int64_t t_stride,
                                             int64_t t) {
   QkvSpan s;
-  s.p0 = t >> 6;
   if (pg.tab == nullptr) {
+    s.lg = 6;
+    s.p0 = t >> 6;
     s.base0 = grp * t_stride + (s.p0 << 6);
     s.base1 = s.base0 + 64;
     return s;
   }
+  s.lg = pg.lg;
+  s.p0 = t >> pg.lg;
   const int g = static_cast<int>(grp), b = g / pg.H, h = g - b * pg.H;
   const int32_t* tb = pg.tab + int64_t(b) * pg.pmax;
   const int p = static_cast<int>(s.p0);
   const int64_t pa = tb[p];
   const int64_t pb = p + 1 < pg.pmax ? tb[p + 1] : pa;
-  s.base0 = (pa * pg.H + h) * kPageTokens;
-  s.base1 = (pb * pg.H + h) * kPageTokens;
+  s.base0 = (pa * pg.H + h) << pg.lg;
+  s.base1 = (pb * pg.H + h) << pg.lg;
   return s;
 }
 

@@ -7,11 +7,11 @@ layers) and register_quashkv_backend (raises ImportError without vLLM).
 
 The reference's page manager wraps an engine of per-append tensors and never
 uses ``block_size``.  Here a layer keeps its tokens in the paged store
-(quashkv_amd.paged: 64-token pages of one pool, a device page table per
-sequence) whenever the paged kernels cover the configuration (head_size 64 or
+(quashkv_amd.paged: pages of PAGE_TOKENS tokens from one pool, a device page
+table per sequence) whenever the paged kernels cover the configuration (head_size 64 or
 128, key_bits 2 or 3), and a contiguous-store QuashKVEngine otherwise; both
-give the same codes and attention.  ``block_size`` must divide the 64-token
-page (vLLM blocks then map onto page slots).
+give the same codes and attention.  ``block_size`` must divide the page
+(vLLM blocks then map onto page slots).
 """
 
 from __future__ import annotations

@@ -1,18 +1,21 @@
-"""Paged compressed KV cache: fixed 64-token pages from a shared pool and a
-page table per sequence, the "preallocated, paged packed-cache format" the
+"""Paged compressed KV cache: fixed-size pages from a shared pool and a page
+table per sequence, the "preallocated, paged packed-cache format" the
 reference's vLLM page manager leaves open (QuashKVPageManager,
 quashkv/integrations/vllm_backend.py:82-195, whose ``block_size`` is unused:
 it keeps one engine of per-append tensors).
 
-A page holds 64 tokens of all H kv heads of one sequence, in the store
-formats of quashkv_amd.store (C ABI "Paged cache store"):
+A page holds ``page_tokens`` = 64 << k tokens (k = 0..5; 256 by default) of
+all H kv heads of one sequence, in the store formats of quashkv_amd.store (C
+ABI "Paged cache store"), with n = page_tokens:
 
-* ``kpool`` (P, H, 64, (mbits + 1) d / 8) uint8 -- K rows (MSE planes, QJL plane);
-* ``knorm`` / ``vnorm`` (P, H, 64) fp32;
-* ``vpool`` (P, H, 2, vbits, d) int32 -- two 32-token V bit-plane tiles.
+* ``kpool`` (P, H, n, (mbits + 1) d / 8) uint8 -- K rows (MSE planes, QJL plane);
+* ``knorm`` / ``vnorm`` (P, H, n) fp32;
+* ``vpool`` (P, H, n / 32, vbits, d) int32 -- 32-token V bit-plane tiles.
 
 ``table`` (B, pages_per_seq) int32 on the device maps sequence b's token t to
-page ``table[b, t // 64]``.  The append kernels (qkv_paged_store_append)
+page ``table[b, t // n]``.  Larger pages keep more of a sequence's K/V
+contiguous in HBM (better DRAM locality when pages are scattered); smaller
+ones waste less of the last page.  The append kernels (qkv_paged_store_append)
 compress bf16 / fp16 K/V straight into the pages; the split-K decode kernel
 (qkv_paged_decode_attention) follows the table per 32-token tile.  Pages come
 from a free list and return to it on clear(); a reused page keeps its old
@@ -35,16 +38,20 @@ from .packing import pack_bits
 from .quantizer import compress_into
 from .store import KVStore
 
-PAGE_TOKENS = 64
+PAGE_TOKENS = 256          # default page size
+PAGE_SIZES = tuple(64 << k for k in range(6))
 
 
 class PagedKVStore:
     """Page pool + page table of B sequences with H kv heads each."""
 
     def __init__(self, B: int, H: int, d: int, mbits: int, vbits: int, num_pages: int,
-                 device: torch.device):
+                 device: torch.device, page_tokens: int = PAGE_TOKENS):
         if d % 32 != 0:
             raise ValueError(f"head_dim {d} must be a multiple of 32 for the cache store")
+        if page_tokens not in PAGE_SIZES:
+            raise ValueError(f"page_tokens {page_tokens} must be one of {PAGE_SIZES}")
+        self.pt = page_tokens
         self.B, self.H, self.d = B, H, d
         self.mbits, self.vbits = mbits, vbits
         self.krb = (mbits + 1) * d // 8
@@ -61,11 +68,11 @@ class PagedKVStore:
     def _grow_pool(self, pages: int) -> None:
         H, d, dev = self.H, self.d, self.device
         old = self.num_pages
-        kpool = torch.zeros(pages, H, PAGE_TOKENS, self.krb, dtype=torch.uint8, device=dev)
-        knorm = torch.zeros(pages, H, PAGE_TOKENS, dtype=torch.float32, device=dev)
-        vpool = torch.zeros(pages, H, PAGE_TOKENS // 32, self.vbits, d, dtype=torch.int32,
-                            device=dev)
-        vnorm = torch.zeros(pages, H, PAGE_TOKENS, dtype=torch.float32, device=dev)
+        n = self.pt
+        kpool = torch.zeros(pages, H, n, self.krb, dtype=torch.uint8, device=dev)
+        knorm = torch.zeros(pages, H, n, dtype=torch.float32, device=dev)
+        vpool = torch.zeros(pages, H, n // 32, self.vbits, d, dtype=torch.int32, device=dev)
+        vnorm = torch.zeros(pages, H, n, dtype=torch.float32, device=dev)
         if old:
             kpool[:old].copy_(self.kpool)
             knorm[:old].copy_(self.knorm)
@@ -87,7 +94,7 @@ class PagedKVStore:
 
     def ensure(self, tokens: int) -> None:
         """Pages for tokens [0, tokens) of every sequence."""
-        need = -(-tokens // PAGE_TOKENS)
+        need = -(-tokens // self.pt)
         have = len(self.pages[0])
         if need <= have:
             return
@@ -120,28 +127,29 @@ class PagedKVStore:
     # ------------------------------------------------ token <-> page rows
 
     def _rows(self, t0: int, S: int) -> torch.Tensor:
-        """(B, H, S) flat row ids (pool row p H 64 + h 64 + slot) of tokens [t0, t0 + S)."""
+        """(B, H, S) flat row ids (pool row (p H + h) n + slot) of tokens [t0, t0 + S)."""
+        n = self.pt
         t = torch.arange(t0, t0 + S, device=self.device)
-        page = self.table.long()[:, t // PAGE_TOKENS]                      # (B, S)
+        page = self.table.long()[:, t // n]                                 # (B, S)
         h = torch.arange(self.H, device=self.device)
-        return (page[:, None, :] * self.H + h[None, :, None]) * PAGE_TOKENS + \
-            (t % PAGE_TOKENS)[None, None, :]
+        return (page[:, None, :] * self.H + h[None, :, None]) * n + (t % n)[None, None, :]
 
     def _tiles(self, t0: int, S: int) -> tuple[torch.Tensor, int, int]:
         """Flat V tile ids (B, H, n) of the 32-token tiles covering [t0, t0 + S),
         with the first tile index j0 = t0 // 32 and n."""
         j0, j1 = t0 // 32, (t0 + S - 1) // 32 + 1
+        tp = self.pt // 32                                                  # tiles per page
         j = torch.arange(j0, j1, device=self.device)
-        page = self.table.long()[:, j // 2]
+        page = self.table.long()[:, j // tp]
         h = torch.arange(self.H, device=self.device)
-        return (page[:, None, :] * self.H + h[None, :, None]) * 2 + (j % 2)[None, None, :], \
+        return (page[:, None, :] * self.H + h[None, :, None]) * tp + (j % tp)[None, None, :], \
             j0, j1 - j0
 
     def write_from(self, tmp: KVStore, t0: int, S: int) -> None:
-        """Tokens [t0 % 64, t0 % 64 + S) of a contiguous store into the pages at
+        """Tokens [t0 % n, t0 % n + S) of a contiguous store into the pages at
         [t0, t0 + S): K rows and norms by row, V tile words merged under the
         mask of those tokens' bits."""
-        o = t0 % PAGE_TOKENS
+        o = t0 % self.pt
         rows = self._rows(t0, S).reshape(-1)
         self.kpool.view(-1, self.krb)[rows] = tmp.kst[:, :, o:o + S].reshape(-1, self.krb)
         self.knorm.view(-1)[rows] = tmp.knorm[:, :, o:o + S].reshape(-1)
@@ -179,20 +187,24 @@ class PagedQuashKVEngine(QuashKVEngine):
     """QuashKVEngine (quashkv/engine.py:54-360) over a paged store.
 
     Same quantizers, append / attention / clear / metrics semantics; tokens
-    live in 64-token pages of one pool (``num_pages`` to start with).  bf16 /
+    live in pages of ``page_tokens`` tokens from one pool (``num_pages`` to start with).  bf16 /
     fp16 K/V compress straight into the pages; other dtypes go through the
     generic compress kernel and are scattered into the pages.  Attention runs
     the integer-MFMA split-K kernel, which covers head_dim 64 / 128 with keys
     of 2 or 3 total bits (``covers``)."""
 
     def __init__(self, head_dim: int = 128, key_bits: int = 3, value_bits: int = 3,
-                 seed: int = 42, device=None, num_pages: int = 0):
+                 seed: int = 42, device=None, num_pages: int = 0,
+                 page_tokens: int = PAGE_TOKENS):
         super().__init__(head_dim=head_dim, key_bits=key_bits, value_bits=value_bits, seed=seed,
                          device=device)
         if not self.covers(head_dim, key_bits, value_bits):
             raise ValueError("the paged cache runs head_dim 64 or 128, key_bits 2 or 3 and "
                              "value_bits 1..4")
+        if page_tokens not in PAGE_SIZES:
+            raise ValueError(f"page_tokens {page_tokens} must be one of {PAGE_SIZES}")
         self.initial_pages = num_pages
+        self.page_tokens = page_tokens
         self._paged: Optional[PagedKVStore] = None
 
     @staticmethod
@@ -216,9 +228,9 @@ class PagedQuashKVEngine(QuashKVEngine):
             raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
                              f"(B={st.B}, H={st.H})")
         if st is None:
-            pages = self.initial_pages or B * max(1, -(-S // PAGE_TOKENS))
+            pages = self.initial_pages or B * max(1, -(-S // self.page_tokens))
             st = self._paged = PagedKVStore(B, H, d, self.key_bits - 1, self.value_bits, pages,
-                                            dev)
+                                            dev, self.page_tokens)
         t0 = self._total_tokens
         st.ensure(t0 + S)
         if S > 0 and not self._append_paged(keys, values, t0):
@@ -246,12 +258,12 @@ class PagedQuashKVEngine(QuashKVEngine):
         N.check(L.qkv_paged_store_append(
             dt, k.data_ptr(), None, B, H, S, d, kq.mse_bits, vq.bits, mq.Pi.data_ptr(),
             kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(), st.knorm.data_ptr(),
-            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, t0,
-            stream))
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, st.pt,
+            t0, stream))
         N.check(L.qkv_paged_store_append(
             dt, None, v.data_ptr(), B, H, S, d, kq.mse_bits, vq.bits, vq.Pi.data_ptr(), None,
             None, None, vb.ptr, None, None, st.vpool.data_ptr(), st.vnorm.data_ptr(),
-            st.table.data_ptr(), st.pages_per_seq, t0, stream))
+            st.table.data_ptr(), st.pages_per_seq, st.pt, t0, stream))
         return True
 
     def _append_scatter(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
@@ -271,8 +283,8 @@ class PagedQuashKVEngine(QuashKVEngine):
                       mq.codebook.centroids, kq.mse_bits, kq.S, kc, kb, kn, packed=False)
         compress_into(N.QKV_MODE_MSE, values.reshape(n, d), vq.Pi, vq.codebook.boundaries,
                       vq.codebook.centroids, vq.bits, None, vc, None, vn, packed=False)
-        o = t0 % PAGE_TOKENS
         st = self._paged
+        o = t0 % st.pt
         tmp = KVStore(B, H, d, st.mbits, st.vbits, o + S, dev)
         tmp.knorm[:, :, o:o + S].copy_(kn.view(B, H, S))
         tmp.vnorm[:, :, o:o + S].copy_(vn.view(B, H, S))
@@ -353,8 +365,8 @@ class PagedQuashKVEngine(QuashKVEngine):
         out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
         N.check(L.qkv_paged_decode_attention(
             q.data_ptr(), N.dtype_code(q.dtype), st.kpool.data_ptr(), st.knorm.data_ptr(),
-            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, T,
-            B, Hq, st.H, Q, d, st.mbits, st.vbits, mq.Pi.data_ptr(), kc.ptr, vc.ptr,
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, st.pt,
+            T, B, Hq, st.H, Q, d, st.mbits, st.vbits, mq.Pi.data_ptr(), kc.ptr, vc.ptr,
             kq.S.data_ptr(), float(kq.qjl_scale), float(scale), 1 if causal else 0,
             out.data_ptr(), N.dtype_code(out_dtype), self._workspace.data_ptr(),
             self._workspace.numel(), splits, N.stream(dev)))

@@ -5,11 +5,34 @@ against the table."""
 
 import torch
 
-from quashkv_amd.paged import PAGE_TOKENS, PagedKVStore
+from quashkv_amd.paged import PAGE_SIZES, PagedKVStore
+
+PAGE_TOKENS = PAGE_TOKENS_T = 64
+
+
+def test_page_sizes():
+    assert PAGE_SIZES == (64, 128, 256, 512, 1024, 2048)
+    import pytest
+    with pytest.raises(ValueError, match="page_tokens"):
+        PagedKVStore(1, 1, 64, 2, 3, 1, torch.device("cpu"), page_tokens=96)
+    st = PagedKVStore(2, 3, 64, 2, 3, 2, torch.device("cpu"), page_tokens=256)
+    st.ensure(300)                               # two 256-token pages each
+    assert all(len(p) == 2 for p in st.pages) and st.kpool.shape[2] == 256
+    rows = st._rows(250, 10)                     # crosses the page edge at 256
+    tiles, j0, n = st._tiles(250, 10)            # tiles 7 (page 0) and 8 (page 1)
+    assert (j0, n) == (7, 2)
+    for b in range(2):
+        for h in range(3):
+            for i, t in enumerate(range(250, 260)):
+                pg = st.pages[b][t // 256]
+                assert int(rows[b, h, i]) == (pg * 3 + h) * 256 + t % 256
+            assert int(tiles[b, h, 0]) == (st.pages[b][0] * 3 + h) * 8 + 7
+            assert int(tiles[b, h, 1]) == (st.pages[b][1] * 3 + h) * 8 + 0
 
 
 def test_pages_table_and_rows():
-    st = PagedKVStore(B=3, H=2, d=64, mbits=2, vbits=3, num_pages=4, device=torch.device("cpu"))
+    st = PagedKVStore(B=3, H=2, d=64, mbits=2, vbits=3, num_pages=4, device=torch.device("cpu"),
+                      page_tokens=PAGE_TOKENS_T)
     st.free = [3, 1, 0, 2]
     st.ensure(1)                                 # one page per sequence
     assert st.pages == [[3], [1], [0]] and st.free == [2]
