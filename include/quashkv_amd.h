@@ -463,6 +463,18 @@ int qkv_paged_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kp
                                int32_t causal, void* out, int32_t out_dtype, void* workspace,
                                int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* qkv_decode_attention_layers over paged stores: per-layer pools (host arrays
+ * of n_layers device pointers) and one page table shared by all layers (a
+ * serving engine's block table); workspace sized for B x n_layers sequences. */
+int qkv_paged_decode_attention_layers(
+    int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kpool,
+    const float* const* knorm, const uint32_t* const* vpool, const float* const* vnorm,
+    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int64_t T,
+    int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+    const float* const* pi, const float* kcent_host, const float* vcent_host,
+    const float* const* signs, float qjl_scale, float scale, int32_t causal, void* const* out,
+    int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1927,14 +1927,18 @@ extern "C" int qkv_paged_decode_attention(
 // workspace is sized for a batch of B * n_layers sequences.  Only the MFMA
 // path takes layers (symmetric codebooks, key MSE bits <= 2, d = 64 or 128,
 // store capacity a multiple of 64, splits of at most 2048 tokens).
-extern "C" int qkv_decode_attention_layers(
-    int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kstore,
-    const float* const* knorm, const uint32_t* const* vstore, const float* const* vnorm,
-    int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-    int32_t kbits, int32_t vbits, const float* const* pi, const float* kcent_host,
-    const float* vcent_host, const float* const* signs, float qjl_scale, float scale,
-    int32_t causal, void* const* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
-    int32_t n_splits, void* stream) {
+// The layer-batched decode over contiguous stores (page_table null) or over
+// per-layer page pools sharing one page table (pages of 1 << plg tokens).
+static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype,
+                         const uint8_t* const* kstore, const float* const* knorm,
+                         const uint32_t* const* vstore, const float* const* vnorm,
+                         int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv,
+                         int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+                         const float* const* pi, const float* kcent_host,
+                         const float* vcent_host, const float* const* signs, float qjl_scale,
+                         float scale, int32_t causal, void* const* out, int32_t out_dtype,
+                         void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream,
+                         const int32_t* page_table, int32_t pages_per_seq, int plg) {
   QKV_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, "n_layers %d not in 1..%d", n_layers,
               kMaxLayers);
   QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && signs && out && kcent_host &&
@@ -1969,6 +1973,9 @@ extern "C" int qkv_decode_attention_layers(
     ol.pi[l] = pi[l];
     ol.out[l] = out[l];
   }
+  kv.ptab = page_table;
+  kv.pmax = pages_per_seq;
+  kv.plg = plg;
   auto s = static_cast<hipStream_t>(stream);
   st = prepare_layers(ql, n_layers, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
                       vcent_host, qjl_scale, workspace, ws_bytes, n_splits, s);
@@ -1978,6 +1985,44 @@ extern "C" int qkv_decode_attention_layers(
   if (st != QKV_OK) return st;
   return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
                         n_splits, s);
+}
+
+extern "C" int qkv_decode_attention_layers(
+    int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kstore,
+    const float* const* knorm, const uint32_t* const* vstore, const float* const* vnorm,
+    int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
+    int32_t kbits, int32_t vbits, const float* const* pi, const float* kcent_host,
+    const float* vcent_host, const float* const* signs, float qjl_scale, float scale,
+    int32_t causal, void* const* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+    int32_t n_splits, void* stream) {
+  return decode_layers(n_layers, q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq,
+                       Hkv, Q, d, kbits, vbits, pi, kcent_host, vcent_host, signs, qjl_scale,
+                       scale, causal, out, out_dtype, workspace, ws_bytes, n_splits, stream,
+                       nullptr, 0, 0);
+}
+
+// One decode step over n_layers layers kept in paged stores: per-layer page
+// pools (host arrays of device pointers) and ONE page table shared by every
+// layer, as a serving engine's block table is.
+extern "C" int qkv_paged_decode_attention_layers(
+    int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kpool,
+    const float* const* knorm, const uint32_t* const* vpool, const float* const* vnorm,
+    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int64_t T,
+    int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+    const float* const* pi, const float* kcent_host, const float* vcent_host,
+    const float* const* signs, float qjl_scale, float scale, int32_t causal, void* const* out,
+    int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
+  QKV_REQUIRE(page_table && pages_per_seq > 0 && qkv_aligned(page_table, 4),
+              "page table missing or not 4-byte aligned");
+  const int plg = qkv_page_lg(page_tokens);
+  QKV_REQUIRE(plg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
+  QKV_REQUIRE(T <= (int64_t(pages_per_seq) << plg),
+              "%lld tokens exceed the page table's %d pages of %d", (long long)T, pages_per_seq,
+              page_tokens);
+  return decode_layers(n_layers, q, q_dtype, kpool, knorm, vpool, vnorm,
+                       int64_t(pages_per_seq) << plg, T, B, Hq, Hkv, Q, d, kbits, vbits, pi,
+                       kcent_host, vcent_host, signs, qjl_scale, scale, causal, out, out_dtype,
+                       workspace, ws_bytes, n_splits, stream, page_table, pages_per_seq, plg);
 }
 
 // Decode attention over mixed-precision K rows (3-bit outlier / 2-bit regular

@@ -209,3 +209,54 @@ def test_model_manager_generation():
     assert m.total_compressed_bytes() > 0
     m.clear()
     assert all(l.total_tokens == 0 for l in m.layers)
+
+
+@pytest.mark.parametrize("d,page_tokens", [(128, 64), (64, 256)])
+def test_paged_layers_match_single_layer_calls(d, page_tokens):
+    """qkv_paged_decode_attention_layers (per-layer pools, one shared page
+    table) against one qkv_paged_decode_attention call per layer with the same
+    split count: identical outputs."""
+    NL, B, H, Hq, Q = 3, 2, 2, 8, 1
+    L = N.lib()
+    engs = []
+    gen = torch.Generator(device=DEV).manual_seed(d + page_tokens)
+    for l in range(NL):
+        e = PagedQuashKVEngine(head_dim=d, seed=42 + l, device=DEV, page_tokens=page_tokens)
+        e._paged = PagedKVStore(B, H, d, 2, 3, 3, torch.device(DEV), page_tokens)
+        random.Random(7).shuffle(e._paged.free)          # the same page order in every layer
+        for S in (200, 1, 99):
+            e.append(torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=torch.bfloat16),
+                     torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=torch.bfloat16))
+        engs.append(e)
+    tab = engs[0].paged_store.table
+    assert all(torch.equal(e.paged_store.table, tab) for e in engs)
+    T = engs[0].total_tokens
+    qs = [torch.randn(B, Hq, Q, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+          for _ in range(NL)]
+    splits = L.qkv_attention_splits(B * NL, Hq, H, Q, d, T)
+    ws_bytes = L.qkv_attention_workspace_bytes(B * NL, Hq, H, Q, d, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    outs = [torch.empty(B, Hq, Q, d, device=DEV) for _ in range(NL)]
+    st0, kq0 = engs[0].paged_store, engs[0].key_quantizer
+    kc = N.HostFloats(kq0.mse_quantizer.codebook.centroids_host)
+    vc = N.HostFloats(engs[0].value_quantizer.codebook.centroids_host)
+    arr = lambda ts: N.ptr_array([t.data_ptr() for t in ts])
+    sts = [e.paged_store for e in engs]
+    N.check(L.qkv_paged_decode_attention_layers(
+        NL, arr(qs), N.QKV_BF16, arr([s.kpool for s in sts]), arr([s.knorm for s in sts]),
+        arr([s.vpool for s in sts]), arr([s.vnorm for s in sts]), tab.data_ptr(),
+        st0.pages_per_seq, page_tokens, T, B, Hq, H, Q, d, 2, 3,
+        arr([e.key_quantizer.mse_quantizer.Pi for e in engs]), kc.ptr, vc.ptr,
+        arr([e.key_quantizer.S for e in engs]), float(kq0.qjl_scale), 1.0 / math.sqrt(d), 0,
+        arr(outs), N.QKV_F32, ws.data_ptr(), ws_bytes, splits, N.stream(torch.device(DEV))))
+    for e, q, o in zip(engs, qs, outs):
+        st, kq = e.paged_store, e.key_quantizer
+        ref = torch.empty_like(o)
+        N.check(L.qkv_paged_decode_attention(
+            q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
+            st.vpool.data_ptr(), st.vnorm.data_ptr(), tab.data_ptr(), st.pages_per_seq,
+            page_tokens, T, B, Hq, H, Q, d, 2, 3, kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr,
+            kq.S.data_ptr(), float(kq.qjl_scale), 1.0 / math.sqrt(d), 0, ref.data_ptr(),
+            N.QKV_F32, ws.data_ptr(), ws_bytes, splits, N.stream(torch.device(DEV))))
+        assert torch.equal(o, ref)
+        _close(o, _oracle(q, e, causal=False))
