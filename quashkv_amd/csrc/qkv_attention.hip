@@ -425,14 +425,20 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
   const float* __restrict__ signs = ql.signs[layer];
   const int r0 = chunk * kRowsM;
   const int nr = min(kRowsM, R - r0);
-  // this thread's part of a Pi row: all float4 loads issued before use
-  const int j = tid % D, half = tid / D;
-  float4 prow[KP / 4];
+  // Pi staged in LDS by coalesced loads (rows padded by 4 floats: the
+  // threads of a wave then read 16 rows' float4s conflict-free), then this
+  // thread's part of row j from there
+  extern __shared__ __align__(16) float4 pis[];  // [D][(D + 4) / 4]
+  constexpr int PR4 = (D + 4) / 4;
   {
-    const float4* src = reinterpret_cast<const float4*>(pi + int64_t(j) * D + half * KP);
+    const float4* src = reinterpret_cast<const float4*>(pi);
 #pragma unroll
-    for (int k4 = 0; k4 < KP / 4; ++k4) prow[k4] = src[k4];
+    for (int x = 0; x < D * D / 4 / 256; ++x) {
+      const int i = tid + 256 * x, row = i / (D / 4), c4 = i - row * (D / 4);
+      pis[row * PR4 + c4] = src[i];
+    }
   }
+  const int j = tid % D, half = tid / D;
   float qv[kRowsM * D / 256];
 #pragma unroll
   for (int x = 0; x < kRowsM * D / 256; ++x) {
@@ -454,6 +460,9 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     qs[i / D][i % D] = qv[x];
   }
   __syncthreads();
+  float4 prow[KP / 4];
+#pragma unroll
+  for (int k4 = 0; k4 < KP / 4; ++k4) prow[k4] = pis[j * PR4 + half * (KP / 4) + k4];
   {  // ||q_r||^2: wave w sums row w
     const int wave = tid >> 6, lane = tid & 63;
     float ss = 0.f;
@@ -577,6 +586,20 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
     rowc[(int64_t(bhc) * kRowsM + r) * 2 + 1] = ldexpf(1.f, -fq);
   }
+}
+
+// Dynamic LDS of prepare_mfma<D, NPL> (the padded Pi), raising the kernel's
+// limit past 64 KiB once where needed.
+template <int D, int NPL>
+uint32_t prep_lds() {
+  constexpr uint32_t bytes = D * (D + 4) * 4;
+  if constexpr (bytes > 65536) {
+    static const bool raised = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&prepare_mfma<D, NPL>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) == hipSuccess;
+    (void)raised;
+  }
+  return bytes;
 }
 
 // Four waves per SIMD (at most 128 VGPRs): with 4 workgroups per CU the split
@@ -1573,7 +1596,9 @@ int prepare_layers(const QLayers& ql, int nl, int32_t q_dtype, int32_t B, int32_
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const dim3 grid(B * nl * Hkv * chunks);
 #define QKV_PREP(DD, NPLV)                                                                   \
-  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), 0, s, ql, B, q_dtype,       \
+  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), (prep_lds<DD, NPLV>()), s,  \
+                     ql, B,                                                                 \
+                     q_dtype,                                                               \
                      qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),    \
                      at<float>(workspace, L.rowc), at<float>(workspace, L.qw))
     if (d == 128) {
@@ -1659,7 +1684,8 @@ extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int3
   ql.q[0] = q;
   ql.pi[0] = pi_perm;
   ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
-  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256), 0, s, ql, B,
+  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256),
+                     (prep_lds<128, 3>()), s, ql, B,
                      q_dtype, 0.f, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
                      at<float>(workspace, L.rowc), nullptr);
   QKV_LAUNCHED();
@@ -2203,7 +2229,8 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
   ql.pi[0] = pisrc;
   ql.signs[0] = ssrc;
 #define QKV_PREP(NPLV)                                                                        \
-  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256), 0, s, ql, 1, qdt,    \
+  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256),                     \
+                     (prep_lds<128, NPLV>()), s, ql, 1, qdt,                                \
                      qjl_scale, M, 1, 1, M, chunks, tb, aq, rowc, nullptr)
   if (mbits == 1) QKV_PREP(2);
   else if (mbits == 2) QKV_PREP(3);
