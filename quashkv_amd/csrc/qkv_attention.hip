@@ -388,6 +388,25 @@ __device__ __forceinline__ void mfma_settle() {
 // Thread (j, part) rotates coordinate j of all rows over one of 256 / D parts
 // of k, then turns coordinate j of rows part, part + 256 / D, ... into digit
 // bytes, scattered into an LDS image of the operands that is copied out whole.
+// Sum over the wave through DPP lane moves (no LDS round trips): prefix sums
+// within each 16-lane row (row_shr 1, 2, 4, 8), then the row totals folded
+// into lane 63 (row_bcast 15 into rows 1 and 3, row_bcast 31 into rows 2
+// and 3), read back to every lane.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf,
+                                                        true));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0x111>(v);
+  v = dpp_add<0x112>(v);
+  v = dpp_add<0x114>(v);
+  v = dpp_add<0x118>(v);
+  v = dpp_add<0x142, 0xa>(v);
+  v = dpp_add<0x143, 0xc>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
 template <int D, int NPL>
 __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dtype,
                                                     float alpha, int Hq, int Hkv, int Q, int R,
@@ -471,7 +490,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
       const float a = qs[wave][lane + 64 * c];
       ss = fmaf(a, a, ss);
     }
-    ss = qkv_wave_sum(ss);
+    ss = wave_sum_dpp(ss);
     if (lane == 0) nqs[wave] = ss;
   }
   {  // q~_j = sum_k q_k Pi[j][k], this thread's part of k for all rows
@@ -559,8 +578,8 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
     for (int rr = 0; rr < RPT; ++rr) {
-      const float a = qkv_wave_sum(csq[rr]);
-      const float c = qkv_wave_sum(csw[rr]);
+      const float a = wave_sum_dpp(csq[rr]);
+      const float c = wave_sum_dpp(csw[rr]);
       if (lane == 0) {
         red[wave][rr][0] = a;
         red[wave][rr][1] = c;
