@@ -397,6 +397,26 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf,
                                                         true));
 }
+// max of v and the DPP-moved v (lanes without a source keep v)
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_max(float v) {
+  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(
+                      __float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf, false)));
+}
+// Max over each 16-lane row, left in the row's last lane (prefix maxima).
+__device__ __forceinline__ float row_max_last(float v) {
+  v = dpp_max<0x111>(v);
+  v = dpp_max<0x112>(v);
+  v = dpp_max<0x114>(v);
+  return dpp_max<0x118>(v);
+}
+// Max over the wave, read back to every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = row_max_last(v);
+  v = dpp_max<0x142, 0xa>(v);
+  v = dpp_max<0x143, 0xc>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v = dpp_add<0x111>(v);
   v = dpp_add<0x112>(v);
@@ -803,11 +823,10 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   }
 #pragma unroll
   for (int c = 0; c < RC; ++c) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mloc[c] = fmaxf(mloc[c], __shfl_xor(mloc[c], o, 64));
-    if (ln == 0) red_m[wave][kRowsM * c + lg] = mloc[c];
+    mloc[c] = row_max_last(mloc[c]);  // the 16 lanes of a row group: max in lane 15
+    if (ln == 15) red_m[wave][kRowsM * c + lg] = mloc[c];
   }
-  vmax = qkv_wave_max(vmax);
+  vmax = wave_max_dpp(vmax);
   if (lane == 0) red_v[wave] = vmax;
   __syncthreads();
 
@@ -902,7 +921,7 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
       dst[128] = static_cast<uint8_t>(dg >> 16);
       dst[192] = static_cast<uint8_t>(dg >> 24);
     }
-    lsum = qkv_wave_sum(lsum);
+    lsum = wave_sum_dpp(lsum);
     // sum_t Z_t s_t: what an all-ones plane would accumulate (this lane's
     // tokens all share i = lane % 8)
     const int64_t usum = wave_sum_i64(xsum << ii);
