@@ -281,6 +281,28 @@ int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
                          void* out, int32_t out_dtype, void* workspace,
                          int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* No counterpart in the reference: qkv_decode_attention for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * qkv_decode_attention without `workspace` / `ws_bytes`: the workspace is a
+ * static device array of QKV_NOALLOC_SCRATCH_BYTES held by the library on
+ * each GPU it runs on until the process ends.  A call whose workspace
+ * (qkv_attention_workspace_bytes) exceeds that size returns QKV_E_INVALID.
+ * The library allocates nothing on this path.  Calls that overlap on one GPU
+ * (different streams or threads) share the array and race; the last call's
+ * contents stay in it. */
+#define QKV_NOALLOC_SCRATCH_BYTES (16 << 20)
+int qkv_decode_attention_noalloc(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                                 const float* knorm, const uint32_t* vstore,
+                                 const float* vnorm, int64_t t_stride, int64_t T,
+                                 int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
+                                 int32_t d, int32_t kbits, int32_t vbits,
+                                 const float* pi, const float* kcent_host,
+                                 const float* vcent_host, const float* signs,
+                                 float qjl_scale, float scale, int32_t causal,
+                                 void* out, int32_t out_dtype, int32_t n_splits,
+                                 void* stream);
+
 /* The phases qkv_decode_attention runs, exposed so a caller can overlap or
  * time them separately (same arguments and workspace, one stream):
  *   prepare  q~ = q Pi^T, w = alpha |q~| S and the MFMA query operands

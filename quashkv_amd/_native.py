@@ -23,6 +23,7 @@ QKV_F32, QKV_F16, QKV_BF16 = 0, 1, 2
 QKV_MODE_MSE, QKV_MODE_IP = 0, 1
 QKV_FMT_UNPACKED, QKV_FMT_PACKED, QKV_FMT_KPLANES, QKV_FMT_VTILES = 0, 1, 2, 3
 QKV_FLAG_PACKED, QKV_FLAG_PRE_ROTATED = 1, 2
+NOALLOC_SCRATCH_BYTES = 16 << 20  # QKV_NOALLOC_SCRATCH_BYTES
 
 _DTYPE = {torch.float32: QKV_F32, torch.float16: QKV_F16, torch.bfloat16: QKV_BF16}
 
@@ -75,6 +76,9 @@ _SIGS = {
     "qkv_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                     _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32, _f32, _i32,
                                     _p, _i32, _p, _i64, _i32, _p]),
+    "qkv_decode_attention_noalloc": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
+                                            _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32,
+                                            _f32, _i32, _p, _i32, _i32, _p]),
     "qkv_attention_prepare": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p,
                                      _p, _p, _p, _f32, _p, _i64, _i32, _p]),
     "qkv_attention_partial": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32,

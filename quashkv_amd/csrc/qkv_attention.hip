@@ -37,6 +37,7 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <mutex>
 
 #include "qkv_common.h"
 
@@ -1933,6 +1934,73 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
                            vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
                            workspace, ws_bytes, n_splits, stream);
+}
+
+// ------------------------------------------------------------ no-allocation variant
+//
+// qkv_decode_attention with its workspace in a file-scope device array of
+// QKV_NOALLOC_SCRATCH_BYTES instead of a caller buffer, for callers that
+// cannot allocate.  Each GPU holds its own copy of the array (for the life of
+// the process); its address on the current device is looked up once per
+// device with hipGetSymbolAddress and only that address is handed to kernels.
+// Every kernel of the decode step writes each workspace entry it later reads
+// (query operands, row constants, split partials), so nothing has to start at
+// zero.  Calls that overlap on one GPU share the array and race.
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[QKV_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kScratchDevices = 64;
+std::mutex scratch_mu;
+void* scratch_dev[kScratchDevices] = {};
+
+// Address of `scratch` on the current device (nullptr + error set on failure).
+void* scratch_on_current_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    qkv_set_error("no usable current HIP device for the scratch array");
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      qkv_set_error("hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                    hipGetErrorString(e));
+      return nullptr;
+    }
+    scratch_dev[dev] = ptr;
+  }
+  return scratch_dev[dev];
+}
+
+}  // namespace
+
+extern "C" int qkv_decode_attention_noalloc(const void* q, int32_t q_dtype,
+                                            const uint8_t* kstore, const float* knorm,
+                                            const uint32_t* vstore, const float* vnorm,
+                                            int64_t t_stride, int64_t T, int32_t B, int32_t Hq,
+                                            int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+                                            int32_t vbits, const float* pi,
+                                            const float* kcent_host, const float* vcent_host,
+                                            const float* signs, float qjl_scale, float scale,
+                                            int32_t causal, void* out, int32_t out_dtype,
+                                            int32_t n_splits, void* stream) {
+  QKV_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Q > 0 && Hq % Hkv == 0, "invalid shape");
+  QKV_REQUIRE(n_splits >= 1 && n_splits <= 1024, "n_splits %d out of range", n_splits);
+  const int64_t need = qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits);
+  QKV_REQUIRE(need > 0, "invalid shape");
+  QKV_REQUIRE(need <= int64_t(QKV_NOALLOC_SCRATCH_BYTES),
+              "qkv_decode_attention_noalloc: this call needs %lld workspace bytes, more than "
+              "the %lld-byte scratch array (use qkv_decode_attention with a workspace)",
+              (long long)need, (long long)QKV_NOALLOC_SCRATCH_BYTES);
+  void* ws = scratch_on_current_device();
+  if (ws == nullptr) return QKV_E_HIP;
+  return qkv_decode_attention(q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv,
+                              Q, d, kbits, vbits, pi, kcent_host, vcent_host, signs, qjl_scale,
+                              scale, causal, out, out_dtype, ws, QKV_NOALLOC_SCRATCH_BYTES,
+                              n_splits, stream);
 }
 
 // Decode attention over a paged store (pages of 64 tokens holding all Hkv
