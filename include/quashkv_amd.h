@@ -497,6 +497,16 @@ int qkv_paged_decode_attention_layers(
     const float* const* signs, float qjl_scale, float scale, int32_t causal, void* const* out,
     int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement helper (no reference counterpart): streams `bytes` (a multiple
+ * of 16, 16-byte aligned) of `buf` with 16-byte loads, `unroll` (4, 8, 16)
+ * per lane in flight, nontemporal loads if `nontemporal`, over `grid`
+ * workgroups of 256, and writes one folded word per workgroup to sink[grid].
+ * The read-only HBM ceiling the decode kernels' roofline is compared with.
+ * ---------------------------------------------------------------------- */
+int qkv_hbm_read_probe(const void* buf, int64_t bytes, uint32_t* sink, int32_t grid,
+                       int32_t unroll, int32_t nontemporal, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -978,6 +978,587 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   }
 }
 
+// ------------------------------------------------------------ fused decode, d = 128
+//
+// The whole decode step at head_dim 128 (MSE key bits 1-2, value bits 1-4,
+// symmetric codebooks) in one kernel.  A workgroup of 8 waves takes one
+// (sequence, kv head, chunk of 4 query rows) over a range of tokens (a split)
+// and streams it in chunks of kChunkF tokens through a two-stage pipeline:
+//   key waves (0-7) score chunk c -- one 64-token tile each, integer MFMA on
+//     the K bit planes exactly as split_mfma does -- into LDS, and once the
+//     chunk's row maxima are known turn those scores into the int8 digit
+//     operands of the value product, in place;
+//   value waves (8-15) meanwhile accumulate chunk c - 1's value product for 16
+//     coordinates each (integer MFMA on the V bit planes, plus one product
+//     with an all-ones plane for the constant term) and merge it into a
+//     running fp32 (m, l, O~) per row: exact integers within a chunk, online
+//     softmax across chunks.
+// Each stage keeps its next chunk's K rows / V plane words in flight in
+// registers (nontemporal loads), so both HBM streams run while the other
+// stage computes; two workgroup barriers per chunk hand the LDS buffers over.
+// The query rotation and digit operands (prepare_mfma's work) run in the
+// prologue while the first chunk's loads are in flight.  With one split per
+// row group the epilogue divides by max(l, 1e-8) and un-rotates by Pi
+// (combine_kernel's work), so a decode step is a single launch; otherwise
+// the workgroup writes split partials for combine_kernel.
+constexpr int kChunkF = 512;              // tokens per pipeline chunk
+constexpr int kTilesF = kChunkF / 64;     // 64-token tiles per chunk (one per key wave)
+constexpr int kWavesKF = kTilesF;         // key waves
+constexpr int kThreadsF = 64 * 2 * kWavesKF;  // key waves + as many value waves
+constexpr int kVSplitF = 6;               // value tiles before the mid-chunk barrier
+
+struct ChunkStats {
+  float pmax[kWavesKF][4];   // [key wave][row] score maxima (log2 units)
+  float pvmax[kWavesKF];     // [key wave] value norm maxima
+  float plsum[kWavesKF][4];  // [key wave][row] sums of p
+};
+
+// Dynamic LDS of decode_fused (byte offsets).  The prologue's and the
+// epilogue's scratch rows overlay the chunk buffers.
+struct FusedLds {
+  static constexpr int PR4 = (128 + 4) / 4;             // padded Pi row, float4
+  static constexpr int PI = 0;                          // Pi [128][PR4]
+  static constexpr int STAGE = PI + 128 * PR4 * 16;     // query operand image, <= 6 KiB
+  static constexpr int BUF = STAGE + 6 * 1024;          // [2][kTilesF][1 KiB] scores / digits
+  static constexpr int STATS = BUF + 2 * kTilesF * 1024;
+  static constexpr int ROWC = STATS + 2 * int(sizeof(ChunkStats));  // [4][2] row constants
+  static constexpr int RED = ROWC + 32;                 // [8] norms, [8][2] row sums
+  static constexpr int TOTAL = RED + 128;
+  static_assert(BUF % 16 == 0 && STATS % 16 == 0, "alignment");
+};
+
+// Workgroup barrier ordering LDS accesses only: outstanding global loads (the
+// prefetched chunks) stay in flight across it.
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <typename T>
+__device__ __forceinline__ T ldnt(const T* p) {
+  return __builtin_nontemporal_load(p);
+}
+
+// aq_ws == nullptr: the prologue computes the query operands (Tables tb,
+// ql); else they come from prepare_mfma's workspace (aq_ws, rowc_ws).
+// final_out != 0 and one split: write the attention output through ol;
+// else split partials (part_o, part_ml) for combine_kernel.
+// PAGED: the store is a page pool addressed through kv.ptab.
+template <int MB, int VB, bool PAGED>
+__global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
+    QLayers ql, KVLayers kv, OutLayers ol, int Bl, int q_dtype, float alpha, int Hq, int Hkv,
+    int Q, int R, int chunks, Tables tb, int64_t t_stride, int64_t T, float scale, int causal,
+    int64_t split_len, int final_out, int out_dtype, const qkv_v4i* __restrict__ aq_ws,
+    const float* __restrict__ rowc_ws, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  constexpr int D = 128;
+  constexpr int NPL = MB + 1;            // planes per K row (MSE + QJL)
+  constexpr int KRB = NPL * D / 8;       // K row bytes
+  constexpr int DPL = KRB / 16;          // row dwords per lane group
+  constexpr int NU = KRB / 8;            // score MFMAs per 16 tokens
+  constexpr int NP = n_odd_subsets(VB);  // value planes
+  constexpr int PR4 = FusedLds::PR4;
+  constexpr int NT = kThreadsF;
+  static_assert(NU * 1024 <= 6 * 1024, "operand image");
+  static_assert(NT == 1024 && kWavesKF == 8, "layout below assumes 8 + 8 waves");
+
+  extern __shared__ __align__(16) uint8_t lds[];
+  float4* pis = reinterpret_cast<float4*>(lds + FusedLds::PI);
+  uint32_t* stage = reinterpret_cast<uint32_t*>(lds + FusedLds::STAGE);
+  uint8_t* bufs = lds + FusedLds::BUF;
+  ChunkStats* stats = reinterpret_cast<ChunkStats*>(lds + FusedLds::STATS);
+  float* rowcs = reinterpret_cast<float*>(lds + FusedLds::ROWC);
+  float* red = reinterpret_cast<float*>(lds + FusedLds::RED);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int G = Hq / Hkv;
+  const int split = blockIdx.x;
+  const int hkv = blockIdx.y / chunks, cki = blockIdx.y - hkv * chunks;
+  const int bz = blockIdx.z;  // over the batch of all layers
+  const int layer = bz / Bl, b = bz - layer * Bl;
+  const int r0 = cki * kRowsM;
+  const int nr = min(kRowsM, R - r0);
+  const int64_t bh = int64_t(b) * Hkv + hkv;  // in the layer's store
+  const int64_t ts = int64_t(split) * split_len;
+  const int64_t te = min<int64_t>(T, ts + split_len);
+  const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
+  const int ntiles = (ntok + 63) >> 6;
+  const int nch = (ntiles + kTilesF - 1) / kTilesF;
+  const uint8_t* __restrict__ kst = kv.kst[layer];
+  const float* __restrict__ knorm = kv.knorm[layer];
+  const uint32_t* __restrict__ vst = kv.vst[layer];
+  const float* __restrict__ vnorm = kv.vnorm[layer];
+  const bool keyw = wave < kWavesKF;
+  const int wi = wave & (kWavesKF - 1);  // index within the key or value waves
+
+  // First store row of the split's 64-token tile (contiguous stream, or the
+  // tile's page).  Whole tiles stay inside the capacity / page.  Every ring
+  // load is issued unconditionally -- a tile past the split's last re-reads
+  // the last one (an empty split reads its stream's first tile) and its data
+  // goes unused -- so each step issues a fixed number of loads and the
+  // in-order load counter waits only for the slot being consumed.  The page
+  // table is read through the constant address space (scalar loads, counted
+  // apart from the vector loads).
+  typedef const __attribute__((address_space(4))) int32_t* ctab_t;
+  const int64_t lts = ntiles > 0 ? ts : 0;
+  const int64_t srow0 = bh * t_stride + lts;  // contiguous: the split's first row
+  auto tile_row = [&](int tile) -> int64_t {
+    const int tc = ntiles > 0 ? min(tile, ntiles - 1) : 0;
+    if constexpr (PAGED) {
+      const ctab_t ptab = (ctab_t)kv.ptab;
+      const int tsh = kv.plg - 6;
+      const int gt = static_cast<int>(lts >> 6) + tc;
+      const int pg = ptab[int64_t(b) * kv.pmax + (gt >> tsh)];
+      return ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
+    } else {
+      return srow0 + int64_t(tc) * 64;
+    }
+  };
+
+  // ---- prologue loads (land in LDS before the first chunk's loads are issued)
+  const bool pro = aq_ws == nullptr;
+  const int pj = tid & (D - 1), ppart = tid >> 7;  // coordinate, part 0..7
+  float* qs = reinterpret_cast<float*>(bufs);              // [4][D] query rows
+  float* partb = reinterpret_cast<float*>(bufs + 2048);    // [2 k halves][4 rows][D]
+  float* sgns = reinterpret_cast<float*>(bufs + 6144);     // [D] QJL signs
+  if (pro) {
+    // Pi comes from L2 (every workgroup reads it)
+    const float4* src = reinterpret_cast<const float4*>(ql.pi[layer]);
+    float4 pst[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) pst[x] = src[tid + NT * x];
+    float qv = 0.f;
+    if (ppart < nr) {
+      const int row = r0 + ppart;
+      const int g = row / Q, qi = row - g * Q;
+      const int h = hkv * G + g;
+      qv = qkv_load(ql.q[layer], ((int64_t(b) * Hq + h) * Q + qi) * D + pj, q_dtype);
+    }
+    const float sgn = ql.signs[layer][pj];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int i = tid + NT * x, row = i >> 5, c4 = i & 31;
+      pis[row * PR4 + c4] = pst[x];
+    }
+    if (ppart < kRowsM) qs[ppart * D + pj] = qv;
+    if (ppart == 0) sgns[pj] = sgn;
+  } else {
+    // operands and row constants from prepare_mfma's workspace
+    const int64_t bhc = (int64_t(bz) * Hkv + hkv) * chunks + cki;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(aq_ws) + bhc * NU * 256;
+    uint32_t w[(NU * 256 + NT - 1) / NT];
+#pragma unroll
+    for (int x = 0; x < (NU * 256 + NT - 1) / NT; ++x)
+      if (tid + NT * x < NU * 256) w[x] = src[tid + NT * x];
+    const float rc = tid < 2 * kRowsM ? rowc_ws[bhc * kRowsM * 2 + tid] : 0.f;
+#pragma unroll
+    for (int x = 0; x < (NU * 256 + NT - 1) / NT; ++x)
+      if (tid + NT * x < NU * 256) stage[tid + NT * x] = w[x];
+    if (tid < 2 * kRowsM) rowcs[tid] = rc;
+  }
+
+  // ---- first chunk's loads (registers)
+  uint32_t kd[4][DPL];
+  float kn[4], vnr = 0.f;
+  uint32_t vw[kTilesF][VB];
+  const int blk = lg >> 1, hsh = 4 * (lg & 1);
+  const int vj = 16 * wi + ln;  // value wave: coordinate of this lane
+  // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
+  const uint32_t koff = ln * KRB + lg * DPL * 4;       // bytes into a tile's K rows
+  const uint32_t voff = blk * VB * D + vj;             // words into a tile's V planes
+  auto loadK = [&](int tile) {
+    const int64_t rb = tile_row(tile);
+    const uint8_t* kb = kst + rb * KRB;
+    const float* knb = knorm + rb;
+    const float* vnb = vnorm + rb;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+      const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + koff + sub * 16 * KRB);
+#pragma unroll
+      for (int x = 0; x < DPL; ++x) kd[sub][x] = ldnt(krow + x);
+      kn[sub] = ldnt(knb + sub * 16 + ln);
+    }
+    vnr = ldnt(vnb + lane);
+  };
+  auto loadV = [&](int slot, int tile) {
+    const uint32_t* vb = vst + (tile_row(tile) >> 5) * (VB * D);  // the tile's first V tile
+#pragma unroll
+    for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * D);
+  };
+  if (keyw) {
+    loadK(wi);
+  } else {
+#pragma unroll
+    for (int t = 0; t < kTilesF; ++t) loadV(t, t);
+  }
+
+  // ---- prologue math: q~ = q Pi^T, operand digits (prepare_mfma on 1024 threads)
+  if (pro) {
+    lds_sync();
+    if (ppart < kRowsM) {  // ||q_r||^2: row r = waves 2r, 2r + 1
+      const float qv = qs[ppart * D + pj];
+      const float ss = wave_sum_dpp(qv * qv);
+      if (lane == 0) red[wave] = ss;
+    }
+    {  // thread (j, r, k half): row r's partial dot product over k in [64 kh, 64 kh + 64)
+      const int r = ppart & 3, kh = ppart >> 2;
+      float acc = 0.f;
+#pragma unroll
+      for (int k4 = 0; k4 < 16; ++k4) {
+        const float4 p4 = pis[pj * PR4 + 16 * kh + k4];
+        const float4 q4 = reinterpret_cast<const float4*>(qs + r * D)[16 * kh + k4];
+        acc = fmaf(q4.x, p4.x, acc);
+        acc = fmaf(q4.y, p4.y, acc);
+        acc = fmaf(q4.z, p4.z, acc);
+        acc = fmaf(q4.w, p4.w, acc);
+      }
+      partb[(kh * kRowsM + r) * D + pj] = acc;
+    }
+    float kgmax = alpha;
+    if (tb.kmix) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
+      kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
+    } else {
+#pragma unroll
+      for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+    }
+    lds_sync();
+    if (ppart < kRowsM) {  // thread (j, r): coordinate j of row r into digit bytes
+      const int r = ppart;
+      const float v = partb[(0 * kRowsM + r) * D + pj] + partb[(1 * kRowsM + r) * D + pj];
+      const float w = alpha * fabsf(v) * sgns[pj];
+      const float wmax = 2.f * kgmax * sqrtf(red[2 * r] + red[2 * r + 1]);
+      int ex = 0;
+      if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
+      const int fqe = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
+      uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
+      auto put = [&](int p, float W) {
+        const int i = p & 7;
+        int Z = static_cast<int>(rintf(ldexpf(W, fqe - i)));
+        if (i == 7) Z = -Z;
+        const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+        const int w32 = p >> 5, e = i & 3, beta = (p >> 3) & 3;
+        const int g = w32 / DPL;
+        const int u = 2 * (w32 - g * DPL) + (i >> 2);
+        const int base = ((u * 64 + 16 * g + 4 * r) * 4 + e) * 4 + beta;
+#pragma unroll
+        for (int vv = 0; vv < 4; ++vv) sb[base + 16 * vv] = static_cast<uint8_t>(dg >> (8 * vv));
+      };
+      float csq;
+      if (tb.kmix) {
+        const bool outl = pj < tb.n_out;
+        csq = (outl ? tb.kco : tb.kcr) * v;
+        put(pj, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v);
+        put(D + pj, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v);
+        if (NPL == 3 && pj < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers
+          put(2 * D + pj, outl ? 2.f * tb.kgo[2] * v : 0.f);
+          put(2 * D + 64 + pj, outl ? 2.f * tb.kgo[3] * v : 0.f);
+        }
+      } else {
+        csq = v;
+#pragma unroll
+        for (int pl = 0; pl < MB; ++pl) put(pl * D + pj, 2.f * tb.kg[pl] * v);
+        put(MB * D + pj, 2.f * w);
+      }
+      // row constants: sums over j (row r = waves 2r, 2r + 1) into red[8 ..]
+      const float a = wave_sum_dpp(csq);
+      const float c = wave_sum_dpp(w);
+      if (lane == 0) {
+        red[8 + 2 * wave] = a;
+        red[8 + 2 * wave + 1] = c;
+      }
+    }
+    lds_sync();
+    if (tid < kRowsM) {  // row tid: score = kn 2^-fq (z + ...) in log2 units
+      const int rr = tid;
+      const float sq = red[8 + 4 * rr] + red[8 + 4 * rr + 2];
+      const float sw = red[8 + 4 * rr + 1] + red[8 + 4 * rr + 3];
+      const float wm = 2.f * kgmax * sqrtf(red[2 * rr] + red[2 * rr + 1]);
+      int er = 0;
+      if (wm > 0.f) frexpf(wm, &er);
+      const int fr = wm > 0.f ? 30 - er : 0;
+      rowcs[2 * rr + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
+      rowcs[2 * rr + 1] = ldexpf(1.f, -fr);
+    }
+  }
+  lds_sync();
+
+  const float scale2 = scale * 1.4426950408889634f;  // scores in log2 units
+  float orun = 0.f, lrun = 0.f, mrun = -INFINITY;     // value waves: row lg, coordinate vj
+
+  if (keyw) {
+    // ------------------------------------------------ key waves: tile wi of each chunk
+    qkv_v4i a[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) a[u] = *reinterpret_cast<const qkv_v4i*>(stage + (u * 64 + lane) * 4);
+    const float cr2 = rowcs[2 * lg] * scale2, fq2 = rowcs[2 * lg + 1] * scale2;
+    const bool row_ok = lg < nr;
+    // causal: split-relative token tl is visible to row lg iff tl <= clim
+    const int qi = (r0 + lg) % Q;
+    const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(INT_MAX);
+    const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, INT_MAX)));
+    int cmin = INT_MAX;  // the smallest limit over the valid rows (wave-uniform)
+    if (causal) {
+#pragma unroll
+      for (int r = 0; r < kRowsM; ++r) {
+        if (r < nr) {
+          const int q2 = (r0 + r) % Q;
+          cmin = static_cast<int>(min<int64_t>(cmin, max<int64_t>(-1, T - Q + q2 - ts)));
+        }
+      }
+    }
+    const int ii = lane & 7;
+    // token (lane) of a 64-token tile -> K position of the value MFMA:
+    // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
+    const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
+    // Z_t s_t = X 2^i with X = round(p' 2^(Fv - i)); the byte of bit 7 is -128,
+    // so those lanes store -X: sign and rounding offset fold into constants
+    const float sgn7 = ii == 7 ? -1.f : 1.f;
+    float vhold = 0.f;
+    for (int c = 0; c <= nch; ++c) {
+      uint8_t* cbuf = bufs + (c & 1) * kTilesF * 1024;
+      ChunkStats& cs = stats[c & 1];
+      const int tile = c * kTilesF + wi;
+      const bool have = c < nch && tile < ntiles;
+      // ---- stage 1: scores of tile wi of chunk c (the slot's refill is issued on
+      // every step, so the load count per step is fixed)
+      float mloc = -INFINITY, vloc = 0.f;
+      qkv_v4i acc[4];
+      float knt[4], vz = 0.f;
+      if (have) {
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) acc[sub] = qkv_v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          const int sh = 4 * (u & 1);
+#pragma unroll
+          for (int sub = 0; sub < 4; ++sub) {
+            const uint32_t x = kd[sub][u >> 1];
+            qkv_v4i bo;
+            bo[0] = static_cast<int>(x & (0x01010101u << sh));
+            bo[1] = static_cast<int>(x & (0x02020202u << sh));
+            bo[2] = static_cast<int>(x & (0x04040404u << sh));
+            bo[3] = static_cast<int>(x & (0x08080808u << sh));
+            acc[sub] = mfma_i8(a[u], bo, acc[sub]);
+          }
+        }
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) knt[sub] = kn[sub];
+        vz = vnr;
+      }
+      loadK(tile + kTilesF);  // the slot is free: refill it
+      if (have) {
+        mfma_settle();
+        const int tbase = tile * 64;
+        const bool full = tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
+        float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+          const int lo = __mul24(acc[sub][1], 256) + acc[sub][0];
+          const int hi = __mul24(acc[sub][3], 256) + acc[sub][2];
+          const float z = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
+          float sc = knt[sub] * fmaf(z, fq2, cr2);
+          if (!full) {
+            const int tl = tbase + sub * 16 + ln;
+            sc = (tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
+          }
+          srow[sub * 16 + ln] = sc;
+          mloc = fmaxf(mloc, sc);
+        }
+        if (tbase + 64 > ntok) vz = tbase + lane < ntok ? vz : 0.f;
+        vhold = vz;
+        vloc = vz;
+      }
+      mloc = row_max_last(mloc);  // the 16 lanes of row lg: max in lane 15
+      vloc = wave_max_dpp(vloc);
+      if (ln == 15) cs.pmax[wi][lg] = mloc;
+      if (lane == 0) cs.pvmax[wi] = vloc;
+      lds_sync();
+      // ---- stage 2: p = 2^(s - m), value digits in place
+      if (have) {
+        float mrow[kRowsM];
+#pragma unroll
+        for (int r = 0; r < kRowsM; ++r) {
+          float m = cs.pmax[0][r];
+#pragma unroll
+          for (int w = 1; w < kWavesKF; ++w) m = fmaxf(m, cs.pmax[w][r]);
+          mrow[r] = (r < nr && m > -INFINITY) ? m : INFINITY;  // absent row: every p = 0
+        }
+        float vmx = cs.pvmax[0];
+#pragma unroll
+        for (int w = 1; w < kWavesKF; ++w) vmx = fmaxf(vmx, cs.pvmax[w]);
+        int ev = 0;
+        if (vmx > 0.f) frexpf(vmx, &ev);
+        const int Fv = vmx > 0.f ? 29 - ev : 0;  // vmx 2^Fv < 2^29
+        const float vzs = vhold * ldexpf(sgn7, Fv - ii);
+        const float hz = 0.5f * sgn7;
+        uint8_t* tb8 = cbuf + wi * 1024;
+#pragma unroll
+        for (int r = 0; r < kRowsM; ++r) {
+          const float s = reinterpret_cast<const float*>(tb8 + r * 256)[lane];
+          const float p = __builtin_amdgcn_exp2f(s - mrow[r]);
+          const int Z = static_cast<int>(fmaf(p, vzs, hz));
+          // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
+          const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+          uint8_t* dst = tb8 + (4 * r) * 64 + kpos;
+          dst[0] = static_cast<uint8_t>(dg);
+          dst[64] = static_cast<uint8_t>(dg >> 8);
+          dst[128] = static_cast<uint8_t>(dg >> 16);
+          dst[192] = static_cast<uint8_t>(dg >> 24);
+          const float l = wave_sum_dpp(p);
+          if (lane == 0) cs.plsum[wi][r] = l;
+        }
+      } else if (c < nch && lane < kRowsM) {
+        cs.plsum[wi][lane] = 0.f;
+      }
+      lds_sync();
+    }
+  } else {
+    // ------------------------------------------------ value waves: coordinates 16 wi ..
+    qkv_v4i acc[NP], accU;
+#pragma unroll
+    for (int s = 0; s < NP; ++s) acc[s] = qkv_v4i{0, 0, 0, 0};
+    accU = qkv_v4i{0, 0, 0, 0};
+    qkv_v4i ones;  // an all-ones plane as the operand's bytes (b * 2^i, i = bit in byte)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ones[e] = static_cast<int>(0x01010101u << (e + hsh));
+    auto pv = [&](int slot, const uint8_t* tbase) {
+      const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(tbase + ln * 64 + lg * 16);
+#pragma unroll
+      for (int s = 0; s < NP; ++s) {
+        const uint32_t sub = odd_subset(VB, s);
+        uint32_t pw = 0;
+#pragma unroll
+        for (int k = 0; k < VB; ++k)
+          if (sub & (1u << k)) pw ^= vw[slot][k];
+        qkv_v4i av;
+        av[0] = static_cast<int>(pw & (0x01010101u << hsh));
+        av[1] = static_cast<int>(pw & (0x02020202u << hsh));
+        av[2] = static_cast<int>(pw & (0x04040404u << hsh));
+        av[3] = static_cast<int>(pw & (0x08080808u << hsh));
+        acc[s] = mfma_i8(bq, av, acc[s]);  // C[row x digit][coordinate]
+      }
+      accU = mfma_i8(bq, ones, accU);
+    };
+    for (int c = 0; c <= nch; ++c) {
+      const int cv = c - 1;  // the chunk this stage accumulates
+      const uint8_t* vbuf = bufs + (cv & 1) * kTilesF * 1024;
+      // slot t is refilled on every step (at step 0 with the tile it holds),
+      // so the load count per step is fixed
+#pragma unroll
+      for (int t = 0; t < kVSplitF; ++t) {
+        const int tile = cv * kTilesF + t;
+        if (cv >= 0 && tile < ntiles) pv(t, vbuf + t * 1024);
+        loadV(t, tile + kTilesF);
+      }
+      lds_sync();
+#pragma unroll
+      for (int t = kVSplitF; t < kTilesF; ++t) {
+        const int tile = cv * kTilesF + t;
+        if (cv >= 0 && tile < ntiles) pv(t, vbuf + t * 1024);
+        loadV(t, tile + kTilesF);
+      }
+      if (cv >= 0) {
+        // chunk cv: digits + planes -> fp32, merged into the running (m, l, O~).
+        // 2 Y_S - U per digit in exact int32 (|acc| < 2^21 for a 512-token
+        // chunk), then sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U).
+        mfma_settle();
+        const ChunkStats& cs = stats[cv & 1];
+        const int row = lg;
+        float M = cs.pmax[0][row], lc = cs.plsum[0][row], vmx = cs.pvmax[0];
+#pragma unroll
+        for (int w = 1; w < kWavesKF; ++w) {
+          M = fmaxf(M, cs.pmax[w][row]);
+          lc += cs.plsum[w][row];
+          vmx = fmaxf(vmx, cs.pvmax[w]);
+        }
+        int ev = 0;
+        if (vmx > 0.f) frexpf(vmx, &ev);
+        const int Fv = vmx > 0.f ? 29 - ev : 0;
+        float val = 0.f;
+#pragma unroll
+        for (int s = 0; s < NP; ++s) {
+          int tv[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) tv[v] = 2 * acc[s][v] - accU[v];
+          const int lo = __mul24(tv[1], 256) + tv[0];
+          const int hi = __mul24(tv[3], 256) + tv[2];
+          const float y = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
+          val = fmaf(tb.vg[s], y, val);
+          acc[s] = qkv_v4i{0, 0, 0, 0};
+        }
+        accU = qkv_v4i{0, 0, 0, 0};
+        const float oc = ldexpf(val, -Fv);
+        if (row < nr && M > -INFINITY) {
+          const float mn = fmaxf(mrun, M);
+          const float fa = mrun > -INFINITY ? __builtin_amdgcn_exp2f(mrun - mn) : 0.f;
+          const float fb = __builtin_amdgcn_exp2f(M - mn);
+          orun = fmaf(orun, fa, oc * fb);
+          lrun = fmaf(lrun, fa, lc * fb);
+          mrun = mn;
+        }
+      }
+      lds_sync();
+    }
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  if (final_out && gridDim.x == 1) {
+    // out = (O~ / max(l, 1e-8)) Pi_v, rows r0 .. r0 + nr - 1
+    float* obuf = reinterpret_cast<float*>(bufs);            // [4][D]
+    float* opart = reinterpret_cast<float*>(bufs + 2048);    // [4 k parts][4 rows][D]
+    if (!keyw) obuf[lg * D + vj] = lg < nr ? orun / fmaxf(lrun, 1e-8f) : 0.f;
+    const float* piv = ol.pi[layer];
+    if (!pro || piv != ql.pi[layer]) {  // values un-rotate by their own Pi
+      const float4* src = reinterpret_cast<const float4*>(piv);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int i = tid + NT * x, row = i >> 5, c4 = i & 31;
+        pis[row * PR4 + c4] = src[i];
+      }
+    }
+    lds_sync();
+    if (tid < 512) {  // thread (j4, r, kp): columns 4 j4 .. + 3 of row r, k in [32 kp, 32 kp + 32)
+      const int j4 = tid & 31, r = (tid >> 5) & 3, kp = tid >> 7;
+      float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+      for (int k = 32 * kp; k < 32 * kp + 32; ++k) {
+        const float o = obuf[r * D + k];
+        const float4 p4 = pis[k * PR4 + j4];
+        o4.x = fmaf(o, p4.x, o4.x);
+        o4.y = fmaf(o, p4.y, o4.y);
+        o4.z = fmaf(o, p4.z, o4.z);
+        o4.w = fmaf(o, p4.w, o4.w);
+      }
+      reinterpret_cast<float4*>(opart)[(kp * kRowsM + r) * (D / 4) + j4] = o4;
+    }
+    lds_sync();
+    if (tid < 512) {
+      const int r = tid >> 7, j = tid & (D - 1);
+      if (r < nr) {
+        const float o = (opart[(0 * kRowsM + r) * D + j] + opart[(1 * kRowsM + r) * D + j]) +
+                        (opart[(2 * kRowsM + r) * D + j] + opart[(3 * kRowsM + r) * D + j]);
+        const int row = r0 + r;
+        const int g = row / Q, qi = row - g * Q;
+        const int h = hkv * G + g;
+        qkv_store(ol.out[layer], ((int64_t(b) * Hq + h) * Q + qi) * D + j, o, out_dtype);
+      }
+    }
+  } else if (!keyw) {
+    const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
+    if (lg < nr) {
+      part_o[(base + lg) * D + vj] = orun;
+      if (wi == 0 && ln == 0) {
+        part_ml[(base + lg) * 2 + 0] = mrun * 0.6931471805599453f;  // log2 -> natural units
+        part_ml[(base + lg) * 2 + 1] = lrun;
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------ combine
 
 constexpr int kRowsC = 4;       // query rows merged per block (many rows)
@@ -1504,13 +2085,30 @@ Tables make_tables(const float* kc, int mbits, const float* vc, int vbits) {
   return t;
 }
 
+// Mixed-precision key coefficients (3-bit outlier / 2-bit regular slots) into tb.
+bool add_kmix(Tables& tb, const float* out_cent, const float* reg_cent, int n_out) {
+  float kc_tmp[4];
+  float kconst_o = 0.f, kconst_r = 0.f;
+  if (!walsh_odd(out_cent, 3, tb.kgo, &kconst_o) || !walsh_odd(reg_cent, 2, kc_tmp, &kconst_r))
+    return false;
+  tb.kgr[0] = kc_tmp[0];
+  tb.kgr[1] = kc_tmp[1];
+  tb.kco = kconst_o;
+  tb.kcr = kconst_r;
+  tb.kmix = 1;
+  tb.n_out = n_out;
+  return true;
+}
+
 int64_t mfma_split_len(int64_t T, int n_splits) {
   return ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
 }
 
+// d = 128 runs on decode_fused (any split length), d = 64 on split_mfma
+// (splits of at most kSplitMax tokens, scores held in LDS).
 bool use_mfma(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
-  return tb.mfma_ok && (d == 128 || d == 64) && t_stride % 64 == 0 &&
-         mfma_split_len(T, n_splits) <= kSplitMax;
+  return tb.mfma_ok && t_stride % 64 == 0 &&
+         (d == 128 || (d == 64 && mfma_split_len(T, n_splits) <= kSplitMax));
 }
 
 int validate_common(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t n_splits,
@@ -1556,12 +2154,80 @@ int mfma_blocks_per_cu(int64_t split_len, int rc) {
     const hipError_t e =
         rc == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 2>, 256,
                                                                smem)
-                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<128, 2, 3, 1>, 256,
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 1>, 256,
                                                                smem);
     if (e != hipSuccess || v <= 0) v = 1;
     slot = v;
   }
   return slot;
+}
+
+// Splits of the fused d = 128 decode: enough workgroups for one per CU when
+// the row groups are fewer than the CUs, with at least ~1024 tokens each.
+int fused_splits(int64_t groups, int64_t T) {
+  const int64_t ncu = qkv_num_cus();
+  int64_t s = (ncu + groups - 1) / groups;
+  s = std::min<int64_t>(s, std::max<int64_t>(1, (T + 1023) / 1024));
+  return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(s, 1024)));
+}
+
+bool use_fused(const Tables& tb, int d, int64_t t_stride) {
+  return tb.mfma_ok && d == 128 && t_stride % 64 == 0;
+}
+
+// Launch decode_fused over nl layers (B sequences each; workspace for B * nl).
+// pro: query operands computed in the kernel (else prepare_mfma's, from the
+// workspace).  final_out with one split: the kernel writes the output (ol);
+// otherwise it writes split partials and the caller runs combine_layers.
+int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int nl, int B,
+                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int kbits, int vbits,
+                 const Tables& tb, int64_t t_stride, int64_t T, float scale, int causal,
+                 int n_splits, int final_out, int out_dtype, void* workspace, bool pro,
+                 hipStream_t s) {
+  const int R = (Hq / Hkv) * Q;
+  const WsLayout L = ws_layout(B * nl, Hkv, R, 128, n_splits);
+  const int chunks = (R + kRowsM - 1) / kRowsM;
+  const int64_t split_len = ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
+  const dim3 grid(n_splits, Hkv * chunks, B * nl);
+  const qkv_v4i* aq = pro ? nullptr : at<qkv_v4i>(workspace, L.aq);
+  const float* rowc = at<float>(workspace, L.rowc);
+  float* po = at<float>(workspace, L.po);
+  float* pml = at<float>(workspace, L.pml);
+  constexpr uint32_t smem = FusedLds::TOTAL;
+#define QKV_FU2(MB, VB, PG)                                                                    \
+  do {                                                                                         \
+    static const hipError_t attr_ = hipFuncSetAttribute(                                       \
+        reinterpret_cast<const void*>(&decode_fused<MB, VB, PG>),                              \
+        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));                   \
+    QKV_HIP(attr_);                                                                            \
+    hipLaunchKernelGGL((decode_fused<MB, VB, PG>), grid, dim3(kThreadsF), smem, s, ql, kv, ol, \
+                       B, q_dtype, alpha, Hq, Hkv, Q, R, chunks, tb, t_stride, T, scale,       \
+                       causal, split_len, final_out, out_dtype, aq, rowc, po, pml);            \
+  } while (0)
+#define QKV_FU(MB, VB)              \
+  do {                              \
+    if (kv.ptab)                    \
+      QKV_FU2(MB, VB, true);        \
+    else                            \
+      QKV_FU2(MB, VB, false);       \
+  } while (0)
+  switch (kbits * 10 + vbits) {
+    case 11: QKV_FU(1, 1); break;
+    case 12: QKV_FU(1, 2); break;
+    case 13: QKV_FU(1, 3); break;
+    case 14: QKV_FU(1, 4); break;
+    case 21: QKV_FU(2, 1); break;
+    case 22: QKV_FU(2, 2); break;
+    case 23: QKV_FU(2, 3); break;
+    case 24: QKV_FU(2, 4); break;
+    default:
+      qkv_set_error("fused decode: key MSE bits %d / value bits %d unsupported", kbits, vbits);
+      return QKV_E_UNSUPPORTED;
+  }
+#undef QKV_FU
+#undef QKV_FU2
+  QKV_LAUNCHED();
+  return QKV_OK;
 }
 
 }  // namespace
@@ -1572,6 +2238,7 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
                                         int32_t d, int64_t T) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
   const int R = (Hq / Hkv) * Q;
+  if (d == 128) return fused_splits(int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM), T);
   const int rc = mfma_rc(d, R);
   const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM * rc - 1) / (kRowsM * rc));
   const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
@@ -1701,19 +2368,10 @@ extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int3
   QKV_REQUIRE(q && pi_perm && out_cent_host && reg_cent_host, "null pointer");
   QKV_REQUIRE(qkv_aligned(pi_perm, 16), "pi must be 16-byte aligned");
   Tables tb{};
-  float kc_tmp[4];
-  float kconst_o = 0.f, kconst_r = 0.f;
-  if (!walsh_odd(out_cent_host, 3, tb.kgo, &kconst_o) ||
-      !walsh_odd(reg_cent_host, 2, kc_tmp, &kconst_r)) {
+  if (!add_kmix(tb, out_cent_host, reg_cent_host, n_out)) {
     qkv_set_error("mixed-precision keys need symmetric codebooks");
     return QKV_E_UNSUPPORTED;
   }
-  tb.kgr[0] = kc_tmp[0];
-  tb.kgr[1] = kc_tmp[1];
-  tb.kco = kconst_o;
-  tb.kcr = kconst_r;
-  tb.kmix = 1;
-  tb.n_out = n_out;
   tb.mfma_ok = 1;
   const int R = (Hq / Hkv) * Q;
   const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
@@ -1755,6 +2413,12 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
   float* po = at<float>(workspace, L.po);
   float* pml = at<float>(workspace, L.pml);
+  if (use_mfma(tb, d, t_stride, T, n_splits) && d == 128) {
+    // the fused kernel in partial mode: operands from prepare_mfma, split partials out
+    return launch_fused(QLayers{}, kv, OutLayers{}, nl, B, QKV_F32, 0.f, Hq, Hkv, Q, kbits,
+                        vbits, tb, t_stride, T, scale, causal, n_splits, 0, QKV_F32, workspace,
+                        false, s);
+  }
   if (use_mfma(tb, d, t_stride, T, n_splits)) {
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const int rc = mfma_rc(d, R);
@@ -1784,9 +2448,7 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
     case 23: QKV_MF(DD, 2, 3, RCV); break;         \
     case 24: QKV_MF(DD, 2, 4, RCV); break;         \
   }
-    if (d == 128) {
-      QKV_MFD(128, 1)
-    } else if (rc == 2) {
+    if (rc == 2) {
       QKV_MFD(64, 2)
     } else {
       QKV_MFD(64, 1)
@@ -1928,6 +2590,28 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
   QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host &&
                   signs && out,
               "null pointer");
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  if (use_fused(tb, d, t_stride)) {
+    QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4),
+                "pi must be 16-byte and the store 4-byte aligned");
+    QLayers ql{};
+    ql.q[0] = q;
+    ql.pi[0] = pi;
+    ql.signs[0] = signs;
+    KVLayers kv{};
+    kv.kst[0] = kstore;
+    kv.knorm[0] = knorm;
+    kv.vst[0] = vstore;
+    kv.vnorm[0] = vnorm;
+    OutLayers ol{};
+    ol.pi[0] = pi;
+    ol.out[0] = out;
+    auto s = static_cast<hipStream_t>(stream);
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+                      t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
+    if (st != QKV_OK || n_splits == 1) return st;
+    return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
+  }
   st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
                              vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
   if (st != QKV_OK) return st;
@@ -2034,9 +2718,6 @@ extern "C" int qkv_paged_decode_attention(
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(qkv_dtype_ok(out_dtype) && qkv_aligned(pi, 16), "pi must be 16-byte aligned");
-  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
-                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
-  if (st != QKV_OK) return st;
   KVLayers kv{};
   kv.kst[0] = kpool;
   kv.knorm[0] = knorm;
@@ -2045,6 +2726,24 @@ extern "C" int qkv_paged_decode_attention(
   kv.ptab = page_table;
   kv.pmax = pages_per_seq;
   kv.plg = plg;
+  if (d == 128) {
+    QLayers ql{};
+    ql.q[0] = q;
+    ql.pi[0] = pi;
+    ql.signs[0] = signs;
+    OutLayers ol{};
+    ol.pi[0] = pi;
+    ol.out[0] = out;
+    auto s = static_cast<hipStream_t>(stream);
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits,
+                      make_tables(kcent_host, kbits, vcent_host, vbits), t_stride, T, scale,
+                      causal, n_splits, 1, out_dtype, workspace, true, s);
+    if (st != QKV_OK || n_splits == 1) return st;
+    return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
+  }
+  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
+                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
+  if (st != QKV_OK) return st;
   st = partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
                       scale, causal, workspace, ws_bytes, n_splits,
                       static_cast<hipStream_t>(stream));
@@ -2109,6 +2808,13 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.pmax = pages_per_seq;
   kv.plg = plg;
   auto s = static_cast<hipStream_t>(stream);
+  if (d == 128) {
+    st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+                      t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
+    if (st != QKV_OK || n_splits == 1) return st;
+    return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
+                          n_splits, s);
+  }
   st = prepare_layers(ql, n_layers, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
                       vcent_host, qjl_scale, workspace, ws_bytes, n_splits, s);
   if (st != QKV_OK) return st;
@@ -2175,19 +2881,31 @@ extern "C" int qkv_decode_attention_kmixed(
   QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi_perm && out_cent_host &&
                   reg_cent_host && pi_v && vcent_host && out,
               "null pointer");
-  const Tables tb = make_tables(reg_cent_host, 2, vcent_host, vbits);
-  if (!use_mfma(tb, d, t_stride, T, n_splits)) {
-    qkv_set_error("mixed-precision keys need head_dim 128, a store capacity that is a "
-                  "multiple of 64, symmetric codebooks and splits of at most %d tokens",
-                  kSplitMax);
+  Tables tb = make_tables(reg_cent_host, 2, vcent_host, vbits);
+  if (d != 128 || (n_out != 32 && n_out != 64) || !use_fused(tb, d, t_stride) ||
+      !add_kmix(tb, out_cent_host, reg_cent_host, n_out)) {
+    qkv_set_error("mixed-precision keys need head_dim 128, 32 or 64 outlier channels, a store "
+                  "capacity that is a multiple of 64 and symmetric codebooks");
     return QKV_E_UNSUPPORTED;
   }
-  st = qkv_attention_prepare_kmixed(q, q_dtype, B, Hq, Hkv, Q, d, pi_perm, n_out, out_cent_host,
-                                    reg_cent_host, workspace, ws_bytes, n_splits, stream);
-  if (st != QKV_OK) return st;
-  return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, 2, vbits,
-                           pi_v, reg_cent_host, vcent_host, scale, causal, out, out_dtype,
-                           workspace, ws_bytes, n_splits, stream);
+  QKV_REQUIRE(qkv_aligned(pi_perm, 16) && qkv_aligned(pi_v, 16), "pi must be 16-byte aligned");
+  QLayers ql{};
+  ql.q[0] = q;
+  ql.pi[0] = pi_perm;
+  ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
+  KVLayers kv{};
+  kv.kst[0] = kstore;
+  kv.knorm[0] = knorm;
+  kv.vst[0] = vstore;
+  kv.vnorm[0] = vnorm;
+  OutLayers ol{};
+  ol.pi[0] = pi_v;
+  ol.out[0] = out;
+  auto s = static_cast<hipStream_t>(stream);
+  st = launch_fused(ql, kv, ol, 1, B, q_dtype, 0.f, Hq, Hkv, Q, 2, vbits, tb, t_stride, T, scale,
+                    causal, n_splits, 1, out_dtype, workspace, true, s);
+  if (st != QKV_OK || n_splits == 1) return st;
+  return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
 }
 
 // ------------------------------------------------------------ MIPS search (ABI)

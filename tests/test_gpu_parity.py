@@ -410,9 +410,10 @@ def test_attention_random_vs_oracle(d, Hkv, G, Qn, T_, causal, qdt):
 
 
 def test_attention_split_invariance_full_size():
-    """cfg3 shape (B=32, Hq=32, Hkv=8, d=128, T=8192): the split-K result is
-    independent of the number of splits (size-independent property), and the
-    MFMA kernel (splits <= 2048 tokens) agrees with the VALU kernel (one split)."""
+    """cfg3 shape (B=32, Hq=32, Hkv=8, d=128, T=8192): the fused decode kernel's
+    result is independent of the number of splits (size-independent property):
+    one split (the kernel merges and un-rotates itself) against 4, 7 and 32
+    splits (partials merged by the combine kernel)."""
     gen = torch.Generator(device="cpu").manual_seed(2)
     B, Hkv, G, d, T_ = 32, 8, 4, 128, 8192
     eng = Q.QuashKVEngine(head_dim=d, seed=42, device=DEV, pack_storage=True)
@@ -433,15 +434,13 @@ def test_attention_split_invariance_full_size():
         paths.append(L.qkv_attention_path(d, 2, 3, kc_h.ptr, vc_h.ptr, st.capacity, T_, ns))
         outs.append(K.attention_store(q, st, T_, kq.mse_quantizer.Pi, kh, vh, kq.S, kq.qjl_scale,
                                       n_splits=ns))
-    assert paths == [0, 1, 1, 1]
-    # MFMA split counts agree with each other over the whole batch
-    for o in outs[2:]:
-        assert_close(o, outs[1], rel=2e-5, cos=0.999999)
+    assert paths == [1, 1, 1, 1]
+    # split counts agree with each other over the whole batch
+    for o in outs[1:]:
+        assert_close(o, outs[0], rel=2e-5, cos=0.999999)
     for o in outs:
         assert torch.isfinite(o).all()
-    # every configuration against the oracle on a slice of the batch; the VALU
-    # kernel with ONE split sums 4096 tokens per coordinate serially in fp32,
-    # hence its looser bound
+    # every configuration against the oracle on a slice of the batch
     kc, kb, vc = (t[:4] for t in st.read_codes(0, T_))
     blocks = [dict(kcodes=kc.cpu(), kbits=kb.cpu(), knorm=st.knorm[:4, :, :T_].cpu(),
                    vcodes=vc.cpu(), vnorm=st.vnorm[:4, :, :T_].cpu())]
@@ -449,8 +448,7 @@ def test_attention_split_invariance_full_size():
                              kq.mse_quantizer.Pi.cpu(), kq.mse_quantizer.codebook.centroids.cpu(),
                              vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale)
     ref = ref.reshape(4, Hkv * G, 1, d)
-    assert_close(outs[0][:4], ref, rel=2e-4, cos=0.99999)
-    for o in outs[1:]:
+    for o in outs:
         assert_close(o[:4], ref, rel=2e-5, cos=0.999999)
 
 

@@ -160,9 +160,16 @@ def test_workspace_and_split_policy_are_consistent():
         ch = (R + 3) // 4
         assert ws == (4 * B * Hkv * R * 2 * d + B * Hkv * ch * 6 * 64 * 16 + B * Hkv * ch * 4 * 2 * 4
                       + 4 * (4 * B * Hkv * R * d + 4 * B * Hkv * R * 2))
-    # splits keep every split within the LDS-resident length and fill the chip
+    # d = 128 (fused kernel, any split length): one split per row group once
+    # the groups cover the CUs (256 here: no device), else splits of >= ~1024
+    # tokens up to one workgroup per CU
     for T_ in (1, 63, 64, 2048, 2049, 8192, 131072):
-        s = lib.qkv_attention_splits(32, 32, 8, 1, 128, T_)
+        assert lib.qkv_attention_splits(32, 32, 8, 1, 128, T_) == 1
+        s = lib.qkv_attention_splits(1, 32, 8, 1, 128, T_)
+        assert s == max(1, min(32, -(-T_ // 1024)))
+    # d = 64 (split_mfma): every split within the LDS-resident length
+    for T_ in (1, 63, 64, 2048, 2049, 8192, 131072):
+        s = lib.qkv_attention_splits(16, 14, 2, 1, 64, T_)
         assert 1 <= s <= max(1, (T_ + 63) // 64)
         assert -(-T_ // s) <= 2048 or s == 1024
 
@@ -173,7 +180,7 @@ def test_attention_path_selection():
     v3 = LloydMaxCodebook(128, 3).centroids_host
     kc, vc = N.HostFloats(k2), N.HostFloats(v3)
     assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 1
-    assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 1) == 0   # split > 2048
+    assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 1) == 1   # fused: any split
     assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8160, 8150, 8) == 0   # stride % 64
     assert lib.qkv_attention_path(96, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 0
     k64 = N.HostFloats(LloydMaxCodebook(64, 2).centroids_host)
