@@ -533,7 +533,8 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
         N.check(lib.qkv_paged_decode_attention(
             q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
             st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq,
-            st.pt, T, B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(), kc_h.ptr, vc_h.ptr,
+            st.pt, st.num_pages, T, B, HQ, HKV, 1, D, KEY_BITS - 1, VAL_BITS, mq.Pi.data_ptr(),
+            kc_h.ptr, vc_h.ptr,
             kq.S.data_ptr(), kq.qjl_scale, scale, 0, out.data_ptr(), N.QKV_F32, ws.data_ptr(),
             ws_bytes, splits, sptr))
 

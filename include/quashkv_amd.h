@@ -455,6 +455,10 @@ int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, int32_t d,
  *   vpool   32-token tiles (p H + h) P / 32 .. + P / 32 - 1, vbits x d uint32
  * page_table[b * pages_per_seq + t / P] is the page of sequence b's token t
  * (int32, device).  Every sequence of a call holds the same token count.
+ * num_pages is the pool's page count: an entry outside [0, num_pages) is
+ * never written through (appends drop those tokens) and its tiles are read
+ * from page 0 and masked out of attention, so a bad table cannot make the
+ * kernels touch memory outside the pool.
  * ---------------------------------------------------------------------- */
 
 /* qkv_store_append into a paged store: B sequences' new tokens
@@ -466,8 +470,8 @@ int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* value
                            const float* kcent_host, const float* kbound_host,
                            const float* vbound_host, uint8_t* kpool, float* knorm,
                            uint32_t* vpool, float* vnorm, const int32_t* page_table,
-                           int32_t pages_per_seq, int32_t page_tokens, int64_t t0,
-                           void* stream);
+                           int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
+                           int64_t t0, void* stream);
 
 /* qkv_decode_attention over a paged store of T tokens per sequence (the MFMA
  * path: symmetric codebooks, key MSE bits <= 2, d = 64 or 128; returns
@@ -477,7 +481,7 @@ int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* value
 int qkv_paged_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kpool,
                                const float* knorm, const uint32_t* vpool, const float* vnorm,
                                const int32_t* page_table, int32_t pages_per_seq,
-                               int32_t page_tokens, int64_t T,
+                               int32_t page_tokens, int32_t num_pages, int64_t T,
                                int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
                                int32_t kbits, int32_t vbits, const float* pi,
                                const float* kcent_host, const float* vcent_host,
@@ -491,7 +495,8 @@ int qkv_paged_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kp
 int qkv_paged_decode_attention_layers(
     int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kpool,
     const float* const* knorm, const uint32_t* const* vpool, const float* const* vnorm,
-    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int64_t T,
+    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
+    int64_t T,
     int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
     const float* const* pi, const float* kcent_host, const float* vcent_host,
     const float* const* signs, float qjl_scale, float scale, int32_t causal, void* const* out,

@@ -89,13 +89,15 @@ _SIGS = {
                                  _i32, _i32, _p, _p, _p, _f32, _i32, _p, _i32, _p, _i64, _i32,
                                  _p]),
     "qkv_paged_store_append": (_i32, [_i32, _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _p, _p,
-                                      _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i64, _p]),
-    "qkv_paged_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i64, _i32,
+                                      _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i64,
+                                      _p]),
+    "qkv_paged_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i64,
+                                          _i32,
                                           _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p,
                                           _f32, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
     "qkv_hbm_read_probe": (_i32, [_p, _i64, _p, _i32, _i32, _i32, _p]),
     "qkv_paged_decode_attention_layers": (_i32, [_i32, _p, _i32, _p, _p, _p, _p, _p, _i32, _i32,
-                                                 _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                 _i32, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                                  _p, _p, _p, _p, _f32, _f32, _i32, _p, _i32, _p,
                                                  _i64, _i32, _p]),
 }

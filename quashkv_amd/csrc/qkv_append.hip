@@ -314,7 +314,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       if (lane < 32) {
         if (32 * tt + li < nv) {
           const int64_t t = t0 + s0 + 32 * tt + li;
-          knorm[PAGED ? sp.row(t) : grp * t_stride + t] = nrm;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) knorm[r] = nrm;
         }
         invw[32 * tt + li] = iscale / nrm;
       }
@@ -370,8 +371,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 #pragma unroll
       for (int i = 0; i < NSK; ++i) {
         const int w = i * 64 + lane, r = w / RD;
-        if (w < nv * RD)
-          dst[sp.row(t0 + s0 + r) * RD + (w - r * RD)] = stg[i];
+        const int64_t row = sp.row(t0 + s0 + r);
+        if (w < nv * RD && row >= 0) dst[row * RD + (w - r * RD)] = stg[i];
       }
     } else {
       uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
@@ -563,7 +564,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       const float nrm = fmaxf(sqrtf(ss), 1e-8f);
       if (lane < 32 && ok[tt]) {
         const int64_t t = A0 + 32 * tt + li;
-        vnorm[PAGED ? sp.row(t) : grp * t_stride + t] = nrm;
+        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+        if (r >= 0) vnorm[r] = nrm;
       }
       inv[tt] = iscale / nrm;
     }
@@ -612,8 +614,9 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       if (hi <= lo) continue;
       const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
                                           : (((1u << (hi - lo)) - 1u) << lo);
-      const int64_t vt = PAGED ? (sp.row(tok0) >> 5)
-                               : grp * (t_stride >> 5) + (tok0 >> 5);
+      const int64_t vrow = PAGED ? sp.row(tok0) : 0;
+      if (vrow < 0) continue;  // a page outside the pool: nothing written
+      const int64_t vt = PAGED ? (vrow >> 5) : grp * (t_stride >> 5) + (tok0 >> 5);
       uint32_t* p = vst + (vt * VB + k) * D + j;
       uint32_t val = stg[i];
       if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
@@ -778,7 +781,7 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
                                 void* stream) {
   return store_append_impl(in_dtype, keys, values, groups, S, d, mbits, vbits, pi, signs,
                            kcent_host, kbound_host, vbound_host, kstore, knorm, vstore, vnorm,
-                           t_stride, t0, QkvPages{nullptr, 0, 1, 6}, stream);
+                           t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream);
 }
 
 extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
@@ -787,16 +790,17 @@ extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const 
                                       const float* kcent_host, const float* kbound_host,
                                       const float* vbound_host, uint8_t* kpool, float* knorm,
                                       uint32_t* vpool, float* vnorm, const int32_t* page_table,
-                                      int32_t pages_per_seq, int32_t page_tokens, int64_t t0,
-                                      void* stream) {
+                                      int32_t pages_per_seq, int32_t page_tokens,
+                                      int32_t num_pages, int64_t t0, void* stream) {
   QKV_REQUIRE(B >= 0 && H > 0 && int64_t(B) * H < (int64_t(1) << 31), "invalid shape");
   QKV_REQUIRE(page_table && pages_per_seq > 0, "null page table");
+  QKV_REQUIRE(num_pages > 0, "num_pages %d must be positive", num_pages);
   const int lg = qkv_page_lg(page_tokens);
   QKV_REQUIRE(lg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
   QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
   return store_append_impl(in_dtype, keys, values, int64_t(B) * H, S, d, mbits, vbits, pi,
                            signs, kcent_host, kbound_host, vbound_host, kpool, knorm, vpool,
-                           vnorm, page_tokens, t0, QkvPages{page_table, pages_per_seq, H, lg},
+                           vnorm, page_tokens, t0, QkvPages{page_table, pages_per_seq, H, lg, num_pages},
                            stream);
 }
 

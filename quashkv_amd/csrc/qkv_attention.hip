@@ -84,6 +84,8 @@ struct KVLayers {  // the store
   const int32_t* ptab;  // paged store: page of sequence b's token t at
   int32_t pmax;         // ptab[b * pmax + (t >> plg)] (nullptr: contiguous
   int32_t plg;          // streams of t_stride rows); pages of 1 << plg tokens
+  int32_t npages;       // pages in the pool: a tile on a page outside [0, npages)
+                        // is read from page 0 and masked (contributes nothing)
 };
 struct OutLayers {  // un-rotation and output
   const float* pi[kMaxLayers];
@@ -736,8 +738,13 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int32_t* __restrict__ ptab = kv.ptab;
   int tile_page = 0;
   const int tsh = kv.plg - 6;  // log2 of the 64-token tiles per page
-  if (ptab != nullptr && lane < ntile1)
+  if (ptab != nullptr && lane < ntile1) {
     tile_page = ptab[bseq * kv.pmax + ((static_cast<int>(ts >> 6) + lane) >> tsh)];
+    if (tile_page < 0 || tile_page >= kv.npages) tile_page = -1;  // outside the pool
+  }
+  // lanes' bit: the split's tile of that lane lies on a page of the pool
+  const uint64_t page_okm = ptab != nullptr ? __ballot(tile_page >= 0) : ~uint64_t(0);
+  if (tile_page < 0) tile_page = 0;
   auto tile_row = [&](int tile) -> int64_t {
     if (ptab)
       return ((int64_t(__builtin_amdgcn_readlane(tile_page, tile)) * Hkv + hkv) << kv.plg) +
@@ -792,7 +799,7 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const int tl = tile * 64 + sub * 16 + ln;
-      const bool in = tl < ntok;
+      const bool in = tl < ntok && ((page_okm >> tile) & 1u);
 #pragma unroll
       for (int c = 0; c < RC; ++c) {
         const float z = static_cast<float>(acc[c][sub][0]) +
@@ -1110,10 +1117,22 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       const ctab_t ptab = (ctab_t)kv.ptab;
       const int tsh = kv.plg - 6;
       const int gt = static_cast<int>(lts >> 6) + tc;
-      const int pg = ptab[int64_t(b) * kv.pmax + (gt >> tsh)];
+      int pg = ptab[int64_t(b) * kv.pmax + (gt >> tsh)];
+      if (pg < 0 || pg >= kv.npages) pg = 0;  // outside the pool: read page 0, masked
       return ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
     } else {
       return srow0 + int64_t(tc) * 64;
+    }
+  };
+  // whether tile lies on a page of the pool (always, on a contiguous store)
+  auto page_ok = [&](int tile) -> bool {
+    if constexpr (PAGED) {
+      const ctab_t ptab = (ctab_t)kv.ptab;
+      const int gt = static_cast<int>(lts >> 6) + tile;
+      const int pg = ptab[int64_t(b) * kv.pmax + (gt >> (kv.plg - 6))];
+      return pg >= 0 && pg < kv.npages;
+    } else {
+      return true;
     }
   };
 
@@ -1353,7 +1372,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       if (have) {
         mfma_settle();
         const int tbase = tile * 64;
-        const bool full = tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
+        const bool pok = page_ok(tile);
+        const bool full = pok && tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
         float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
@@ -1363,12 +1383,12 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
           float sc = knt[sub] * fmaf(z, fq2, cr2);
           if (!full) {
             const int tl = tbase + sub * 16 + ln;
-            sc = (tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
+            sc = (pok && tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
           }
           srow[sub * 16 + ln] = sc;
           mloc = fmaxf(mloc, sc);
         }
-        if (tbase + 64 > ntok) vz = tbase + lane < ntok ? vz : 0.f;
+        if (!full) vz = (pok && tbase + lane < ntok) ? vz : 0.f;
         vhold = vz;
         vloc = vz;
       }
@@ -2692,7 +2712,8 @@ extern "C" int qkv_decode_attention_noalloc(const void* q, int32_t q_dtype,
 extern "C" int qkv_paged_decode_attention(
     const void* q, int32_t q_dtype, const uint8_t* kpool, const float* knorm,
     const uint32_t* vpool, const float* vnorm, const int32_t* page_table, int32_t pages_per_seq,
-    int32_t page_tokens, int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+    int32_t page_tokens, int32_t num_pages, int64_t T, int32_t B, int32_t Hq, int32_t Hkv,
+    int32_t Q, int32_t d, int32_t kbits,
     int32_t vbits, const float* pi, const float* kcent_host, const float* vcent_host,
     const float* signs, float qjl_scale, float scale, int32_t causal, void* out,
     int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
@@ -2701,6 +2722,7 @@ extern "C" int qkv_paged_decode_attention(
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
   QKV_REQUIRE(page_table && pages_per_seq > 0 && qkv_aligned(page_table, 4),
               "page table missing or not 4-byte aligned");
+  QKV_REQUIRE(num_pages > 0, "num_pages %d must be positive", num_pages);
   const int plg = qkv_page_lg(page_tokens);
   QKV_REQUIRE(plg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
   QKV_REQUIRE(T <= (int64_t(pages_per_seq) << plg),
@@ -2726,6 +2748,7 @@ extern "C" int qkv_paged_decode_attention(
   kv.ptab = page_table;
   kv.pmax = pages_per_seq;
   kv.plg = plg;
+  kv.npages = num_pages;
   if (d == 128) {
     QLayers ql{};
     ql.q[0] = q;
@@ -2769,7 +2792,8 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
                          const float* vcent_host, const float* const* signs, float qjl_scale,
                          float scale, int32_t causal, void* const* out, int32_t out_dtype,
                          void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream,
-                         const int32_t* page_table, int32_t pages_per_seq, int plg) {
+                         const int32_t* page_table, int32_t pages_per_seq, int plg,
+                         int32_t num_pages) {
   QKV_REQUIRE(n_layers >= 1 && n_layers <= kMaxLayers, "n_layers %d not in 1..%d", n_layers,
               kMaxLayers);
   QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && signs && out && kcent_host &&
@@ -2807,6 +2831,7 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.ptab = page_table;
   kv.pmax = pages_per_seq;
   kv.plg = plg;
+  kv.npages = num_pages;
   auto s = static_cast<hipStream_t>(stream);
   if (d == 128) {
     st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
@@ -2836,7 +2861,7 @@ extern "C" int qkv_decode_attention_layers(
   return decode_layers(n_layers, q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq,
                        Hkv, Q, d, kbits, vbits, pi, kcent_host, vcent_host, signs, qjl_scale,
                        scale, causal, out, out_dtype, workspace, ws_bytes, n_splits, stream,
-                       nullptr, 0, 0);
+                       nullptr, 0, 0, 0);
 }
 
 // One decode step over n_layers layers kept in paged stores: per-layer page
@@ -2845,13 +2870,14 @@ extern "C" int qkv_decode_attention_layers(
 extern "C" int qkv_paged_decode_attention_layers(
     int32_t n_layers, const void* const* q, int32_t q_dtype, const uint8_t* const* kpool,
     const float* const* knorm, const uint32_t* const* vpool, const float* const* vnorm,
-    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int64_t T,
-    int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
-    const float* const* pi, const float* kcent_host, const float* vcent_host,
+    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
+    int64_t T, int32_t B, int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits,
+    int32_t vbits, const float* const* pi, const float* kcent_host, const float* vcent_host,
     const float* const* signs, float qjl_scale, float scale, int32_t causal, void* const* out,
     int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
   QKV_REQUIRE(page_table && pages_per_seq > 0 && qkv_aligned(page_table, 4),
               "page table missing or not 4-byte aligned");
+  QKV_REQUIRE(num_pages > 0, "num_pages %d must be positive", num_pages);
   const int plg = qkv_page_lg(page_tokens);
   QKV_REQUIRE(plg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
   QKV_REQUIRE(T <= (int64_t(pages_per_seq) << plg),
@@ -2860,7 +2886,8 @@ extern "C" int qkv_paged_decode_attention_layers(
   return decode_layers(n_layers, q, q_dtype, kpool, knorm, vpool, vnorm,
                        int64_t(pages_per_seq) << plg, T, B, Hq, Hkv, Q, d, kbits, vbits, pi,
                        kcent_host, vcent_host, signs, qjl_scale, scale, causal, out, out_dtype,
-                       workspace, ws_bytes, n_splits, stream, page_table, pages_per_seq, plg);
+                       workspace, ws_bytes, n_splits, stream, page_table, pages_per_seq, plg,
+                       num_pages);
 }
 
 // Decode attention over mixed-precision K rows (3-bit outlier / 2-bit regular

@@ -187,9 +187,10 @@ int qkv_decompress_mfma(const QkvDecompressArgs& a, hipStream_t s);
 // (pg * H + h) * 64 .. of the same row / tile arrays.
 struct QkvPages {
   const int32_t* tab;
-  int32_t pmax;  // pages per sequence in the table
-  int32_t H;     // kv heads
-  int32_t lg;    // log2 of the tokens per page
+  int32_t pmax;    // pages per sequence in the table
+  int32_t H;       // kv heads
+  int32_t lg;      // log2 of the tokens per page
+  int32_t npages;  // pages in the pool: entries outside [0, npages) are never written
 };
 
 // Pages hold 64 << k tokens, k = 0 .. 5 (whole 64-token tiles, at most one
@@ -208,10 +209,14 @@ inline int qkv_page_lg(int32_t page_tokens) {
 // token's 32-token V tile (store capacity a multiple of 32).
 struct QkvSpan {
   int64_t base0, base1;  // store row of the first token of page p0 and of p0 + 1
+                         // (-1: the table names a page outside the pool)
   int64_t p0;
   int lg;                // log2 of the page (64-token blocks on a contiguous store)
+  // store row of token t, or -1 when its page is outside the pool (callers
+  // then write nothing)
   __device__ __forceinline__ int64_t row(int64_t t) const {
-    return ((t >> lg) == p0 ? base0 : base1) + (t & ((int64_t(1) << lg) - 1));
+    const int64_t b = (t >> lg) == p0 ? base0 : base1;
+    return b < 0 ? -1 : b + (t & ((int64_t(1) << lg) - 1));
   }
 };
 
@@ -234,8 +239,8 @@ __device__ __forceinline__ QkvSpan qkv_span(const QkvPages& pg, int64_t grp, int
   const int p = static_cast<int>(s.p0);
   const int64_t pa = tb[p];
   const int64_t pb = p + 1 < pg.pmax ? tb[p + 1] : pa;
-  s.base0 = (pa * pg.H + h) << pg.lg;
-  s.base1 = (pb * pg.H + h) << pg.lg;
+  s.base0 = pa >= 0 && pa < pg.npages ? (pa * pg.H + h) << pg.lg : -1;
+  s.base1 = pb >= 0 && pb < pg.npages ? (pb * pg.H + h) << pg.lg : -1;
   return s;
 }
 

@@ -120,8 +120,10 @@ class QuashKVEngine:
         B, H, S, d = keys.shape
         st = self._store
         if st is not None and (st.B, st.H) != (B, H):
-            raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
-                             f"(B={st.B}, H={st.H})")
+            if self._total_tokens:
+                raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
+                                 f"(B={st.B}, H={st.H})")
+            st = self._store = None  # empty (cleared): any shape, as the reference allows
         if st is None:
             kmix = None
             if self._kmix:
@@ -263,6 +265,8 @@ class QuashKVEngine:
         return out
 
     def clear(self) -> None:
+        """Drop every cached token (quashkv/engine.py:174-177).  The store is kept
+        for reuse; the next append may have any (batch, heads) shape."""
         self._blocks = []
         self._total_tokens = 0
 

@@ -135,8 +135,18 @@ def quashkv_attention(module, query: torch.Tensor, key: torch.Tensor, value: tor
     return out.transpose(1, 2).contiguous(), None
 
 
-def _no_mask(*args, **kwargs):
-    """The fused kernel masks causally itself; no mask tensor is built."""
+def _no_mask(*args, attention_mask: Optional[torch.Tensor] = None, **kwargs):
+    """The fused kernel masks causally itself; no mask tensor is built.
+
+    The kernel attends every cached token of a sequence, so a batch with padded
+    positions (a 2-D padding mask holding any zero / False, as left-padded
+    batched generation passes) is refused rather than attended through."""
+    if attention_mask is not None and attention_mask.dim() == 2 and attention_mask.numel() > 0:
+        if not bool(attention_mask.bool().all()):
+            raise ValueError(
+                f"attn_implementation={ATTN_IMPLEMENTATION!r} runs unpadded batches only: the "
+                "attention mask pads some positions (batch sequences of one length, or one "
+                "sequence per call)")
     return None
 
 

@@ -317,9 +317,18 @@ def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[Compressed
 
     Blocks hold one uint8 per code, as in the reference.  They are packed once
     into a cache store and attended by the decode kernels.  Query heads may be
-    a multiple of the blocks' kv heads (GQA)."""
+    a multiple of the blocks' kv heads (GQA).  With ``causal``, query i sits at
+    position T - Q + i of the T cached tokens; ``total_kv_tokens`` may be 0 or
+    T (any other offset raises ValueError)."""
     if not blocks:
         raise ValueError("No compressed KV blocks in cache. Call append() first.")
+    # causal masking puts query i at position total_kv_tokens - Q + i
+    # (quashkv/triton_kernels/attention.py:118-121); the kernels place it at
+    # T - Q + i for the T cached tokens, so other offsets are refused
+    n_kv = sum(int(b.seq_len) for b in blocks)
+    if causal and total_kv_tokens not in (0, n_kv):
+        raise ValueError(f"causal attention places the queries at the end of the {n_kv} cached "
+                         f"tokens; total_kv_tokens={total_kv_tokens} is not supported")
     N.require_gpu(queries, Pi, what="fused_quantized_attention")
     kc = torch.cat([b.mse_indices for b in blocks], dim=2)
     kq = torch.cat([b.qjl_signs for b in blocks], dim=2)

@@ -42,6 +42,18 @@ PAGE_TOKENS = 256          # default page size
 PAGE_SIZES = tuple(64 << k for k in range(6))
 
 
+def check_page_table(table: torch.Tensor, num_pages: int) -> None:
+    """Host check of a page table (B, pages_per_seq) before it reaches the
+    device: every entry must name a page of the pool, [0, num_pages).  (The
+    kernels also never write through, and mask out, entries outside it.)"""
+    t = table.detach()
+    if t.dtype != torch.int32 or t.dim() != 2:
+        raise ValueError("page table must be a 2-D int32 tensor")
+    if t.numel() and (int(t.min()) < 0 or int(t.max()) >= num_pages):
+        raise ValueError(f"page table entries must lie in [0, {num_pages}); got "
+                         f"[{int(t.min())}, {int(t.max())}]")
+
+
 class PagedKVStore:
     """Page pool + page table of B sequences with H kv heads each."""
 
@@ -107,6 +119,7 @@ class PagedKVStore:
         tab = torch.zeros(self.B, width, dtype=torch.int32)
         for b in range(self.B):
             tab[b, :need] = torch.tensor(self.pages[b], dtype=torch.int32)
+        check_page_table(tab, self.num_pages)
         self.table = tab.to(self.device)
 
     def release(self) -> None:
@@ -225,8 +238,10 @@ class PagedQuashKVEngine(QuashKVEngine):
         B, H, S, d = keys.shape
         st = self._paged
         if st is not None and (st.B, st.H) != (B, H):
-            raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
-                             f"(B={st.B}, H={st.H})")
+            if self._total_tokens:
+                raise ValueError(f"append shape (B={B}, H={H}) does not match the cache "
+                                 f"(B={st.B}, H={st.H})")
+            st = self._paged = None  # empty (cleared): any shape, as the reference allows
         if st is None:
             pages = self.initial_pages or B * max(1, -(-S // self.page_tokens))
             st = self._paged = PagedKVStore(B, H, d, self.key_bits - 1, self.value_bits, pages,
@@ -259,11 +274,11 @@ class PagedQuashKVEngine(QuashKVEngine):
             dt, k.data_ptr(), None, B, H, S, d, kq.mse_bits, vq.bits, mq.Pi.data_ptr(),
             kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(), st.knorm.data_ptr(),
             st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, st.pt,
-            t0, stream))
+            st.num_pages, t0, stream))
         N.check(L.qkv_paged_store_append(
             dt, None, v.data_ptr(), B, H, S, d, kq.mse_bits, vq.bits, vq.Pi.data_ptr(), None,
             None, None, vb.ptr, None, None, st.vpool.data_ptr(), st.vnorm.data_ptr(),
-            st.table.data_ptr(), st.pages_per_seq, st.pt, t0, stream))
+            st.table.data_ptr(), st.pages_per_seq, st.pt, st.num_pages, t0, stream))
         return True
 
     def _append_scatter(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
@@ -366,7 +381,7 @@ class PagedQuashKVEngine(QuashKVEngine):
         N.check(L.qkv_paged_decode_attention(
             q.data_ptr(), N.dtype_code(q.dtype), st.kpool.data_ptr(), st.knorm.data_ptr(),
             st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, st.pt,
-            T, B, Hq, st.H, Q, d, st.mbits, st.vbits, mq.Pi.data_ptr(), kc.ptr, vc.ptr,
+            st.num_pages, T, B, Hq, st.H, Q, d, st.mbits, st.vbits, mq.Pi.data_ptr(), kc.ptr, vc.ptr,
             kq.S.data_ptr(), float(kq.qjl_scale), float(scale), 1 if causal else 0,
             out.data_ptr(), N.dtype_code(out_dtype), self._workspace.data_ptr(),
             self._workspace.numel(), splits, N.stream(dev)))

@@ -49,6 +49,10 @@ def main() -> None:
     import torch  # noqa: E402
 
     torch.set_num_threads(4)
+    import quashkv
+
+    # the reference, not this repository's quashkv layout over quashkv_amd
+    assert os.path.abspath(quashkv.__file__).startswith(os.path.abspath(args.ref)), quashkv.__file__
     from quashkv.codebook import LloydMaxCodebook, solve_lloyd_max
     from quashkv.quantizer import (
         MSEQuantizer,

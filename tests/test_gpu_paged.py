@@ -245,7 +245,7 @@ def test_paged_layers_match_single_layer_calls(d, page_tokens):
     N.check(L.qkv_paged_decode_attention_layers(
         NL, arr(qs), N.QKV_BF16, arr([s.kpool for s in sts]), arr([s.knorm for s in sts]),
         arr([s.vpool for s in sts]), arr([s.vnorm for s in sts]), tab.data_ptr(),
-        st0.pages_per_seq, page_tokens, T, B, Hq, H, Q, d, 2, 3,
+        st0.pages_per_seq, page_tokens, min(s.num_pages for s in sts), T, B, Hq, H, Q, d, 2, 3,
         arr([e.key_quantizer.mse_quantizer.Pi for e in engs]), kc.ptr, vc.ptr,
         arr([e.key_quantizer.S for e in engs]), float(kq0.qjl_scale), 1.0 / math.sqrt(d), 0,
         arr(outs), N.QKV_F32, ws.data_ptr(), ws_bytes, splits, N.stream(torch.device(DEV))))
@@ -255,7 +255,7 @@ def test_paged_layers_match_single_layer_calls(d, page_tokens):
         N.check(L.qkv_paged_decode_attention(
             q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
             st.vpool.data_ptr(), st.vnorm.data_ptr(), tab.data_ptr(), st.pages_per_seq,
-            page_tokens, T, B, Hq, H, Q, d, 2, 3, kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr,
+            page_tokens, st.num_pages, T, B, Hq, H, Q, d, 2, 3, kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr,
             kq.S.data_ptr(), float(kq.qjl_scale), 1.0 / math.sqrt(d), 0, ref.data_ptr(),
             N.QKV_F32, ws.data_ptr(), ws_bytes, splits, N.stream(torch.device(DEV))))
         assert torch.equal(o, ref)

@@ -608,3 +608,39 @@ def test_kernels_api_compress_vs_golden(golden):
     xh = K.fused_decompress_mse(T(g["mse_idx_d64_b3"]).to(DEV), T(g["mse_norm_d64_b3"]).to(DEV),
                                 q.Pi, q.codebook.centroids)
     assert_close(xh, T(g["fmse_xhat_d64_b3"]), rel=1e-5, cos=0.99999)
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_clear_then_new_batch_shape(paged):
+    """clear() empties the cache and the next append may have another (B, H)
+    (quashkv/engine.py:174-177): append B=2, clear, append B=3 with other kv
+    heads, attention against the oracle on the new cache."""
+    from quashkv_amd.paged import PagedQuashKVEngine
+    gen = torch.Generator().manual_seed(31)
+    d = 128
+    cls = PagedQuashKVEngine if paged else Q.QuashKVEngine
+    eng = cls(head_dim=d, seed=42, device=DEV)
+    k = torch.randn(2, 2, 70, d, generator=gen)
+    eng.append(k.to(DEV, torch.bfloat16), k.to(DEV, torch.bfloat16))
+    with pytest.raises(ValueError, match="does not match"):
+        eng.append(k[:1].to(DEV, torch.bfloat16), k[:1].to(DEV, torch.bfloat16))
+    eng.clear()
+    assert eng.total_tokens == 0
+    B, H, G, T_ = 3, 4, 2, 150
+    k2 = torch.randn(B, H, T_, d, generator=gen)
+    v2 = torch.randn(B, H, T_, d, generator=gen)
+    eng.append(k2.to(DEV, torch.bfloat16), v2.to(DEV, torch.bfloat16))
+    q = torch.randn(B, H * G, 1, d, generator=gen)
+    out = eng.attention(q.to(DEV)).cpu()
+    blocks = []
+    for blk in eng._cache:
+        mi, qj, vi = eng._unpack_block(blk)
+        blocks.append(dict(kcodes=mi.cpu(), kbits=qj.cpu(), knorm=blk.key_norms.cpu(),
+                           vcodes=vi.cpu(), vnorm=blk.val_norms.cpu()))
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    ref = R.attention_online(q.reshape(B, H, G, d), blocks, kq.mse_quantizer.Pi.cpu(),
+                             kq.mse_quantizer.codebook.centroids.cpu(),
+                             vq.codebook.centroids.cpu(), kq.S.cpu(),
+                             kq.qjl_scale).reshape(B, H * G, 1, d)
+    assert out.shape == (B, H * G, 1, d)
+    assert_close(out, ref, rel=2e-5, cos=0.999999)

@@ -61,3 +61,27 @@ def test_pages_table_and_rows():
     assert not any(st.pages) and len(st.free) == st.num_pages
     st.ensure(64)                                # released pages are handed out again
     assert len(set(sum(st.pages, []))) == 3 and len(st.free) == st.num_pages - 3
+
+
+def test_page_table_host_check():
+    import pytest
+    from quashkv_amd.paged import check_page_table
+    good = torch.tensor([[0, 3, 1], [2, 2, 0]], dtype=torch.int32)
+    check_page_table(good, 4)
+    for bad in (torch.tensor([[0, 4]], dtype=torch.int32), torch.tensor([[-1, 0]], dtype=torch.int32)):
+        with pytest.raises(ValueError, match="page table entries"):
+            check_page_table(bad, 4)
+    with pytest.raises(ValueError, match="int32"):
+        check_page_table(good.long(), 4)
+    # the store's own tables always pass (pages come from its pool)
+    st = PagedKVStore(3, 2, 64, 2, 3, 1, torch.device("cpu"), page_tokens=64)
+    st.ensure(200)
+    check_page_table(st.table, st.num_pages)
+
+
+def test_paged_abi_rejects_empty_pool():
+    from quashkv_amd import _native as N
+    L = N.lib()
+    st = L.qkv_paged_store_append(N.QKV_BF16, 16, None, 1, 1, 64, 128, 2, 3, 16, 16, 16, 16, 16,
+                                  16, 16, 16, 16, 16, 1, 64, 0, 0, None)
+    assert st == N.QKV_E_INVALID and "num_pages" in L.qkv_last_error().decode()
