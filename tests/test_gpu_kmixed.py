@@ -200,3 +200,61 @@ def test_kmixed_engine_errors():
     with pytest.raises(ValueError, match="32 or 64 outliers"):
         Q.QuashKVEngine(head_dim=128, device=DEV, key_quantizer=Q.MixedPrecisionMSEQuantizer(
             128, outlier_bits=3, regular_bits=2, n_outliers=16, device=DEV))
+
+
+def test_kmixed_cfg4_full_size():
+    """The long-context mixed-precision workload at its full size: B=1, 32
+    query heads over 8 kv heads, 131072 bf16 tokens appended in 64 chunks of
+    2048, keys MixedPrecisionMSE 3/2 bits with 32 outliers calibrated on 65536
+    keys whose raw channels 0, 4, .., 124 have sigma 8, values 4-bit MSE, one
+    bf16 query.  Per kv head: the kernel against the oracle's attention on the
+    store's own codes (fp32 arithmetic from the same bf16 query, rel <= 1e-3),
+    and end to end against the oracle's own codes of the same bf16 inputs
+    (rel <= 1e-2, cosine >= 0.9999)."""
+    B, Hq, Hkv, TT, CH = 1, 32, 8, 131072, 2048
+    G = Hq // Hkv
+    gen = torch.Generator().manual_seed(44)
+    out_ch = list(range(0, 128, 4))
+    cal = torch.randn(65536, 128, generator=gen)
+    cal[:, out_ch] *= 8.0
+    kq = Q.MixedPrecisionMSEQuantizer(128, outlier_bits=3, regular_bits=2, n_outliers=32,
+                                      seed=42, device=DEV)
+    kq.calibrate(cal.to(DEV))
+    eng = Q.QuashKVEngine(head_dim=128, value_bits=4, seed=42, device=DEV, key_quantizer=kq,
+                          capacity=TT)
+    vq = eng.value_quantizer
+    k = torch.randn(B, Hkv, TT, 128, generator=gen)
+    k[..., out_ch] *= 8.0
+    k = k.to(torch.bfloat16)
+    v = torch.randn(B, Hkv, TT, 128, generator=gen).to(torch.bfloat16)
+    q = torch.randn(B, Hq, 1, 128, generator=gen).to(torch.bfloat16)
+    kd, vd = k.to(DEV), v.to(DEV)
+    for a in range(0, TT, CH):
+        eng.append(kd[:, :, a:a + CH], vd[:, :, a:a + CH])
+    out = eng.attention(q.to(DEV)).cpu().double()
+    assert eng.total_tokens == TT
+    st = eng._store
+    kc, _, vc = st.read_codes(0, TT)
+    kc, vc = kc.cpu(), vc.cpu()
+    kn, vn = st.knorm[:, :, :TT].cpu(), st.vnorm[:, :, :TT].cpu()
+    del kd, vd
+    out_idx = kq._outlier_indices.cpu()
+    tabs = (kq.Pi.cpu(), out_idx, kq.outlier_codebook.centroids.cpu(),
+            kq.regular_codebook.centroids.cpu(), vq.Pi.cpu(), vq.codebook.centroids.cpu())
+    pi_k, t_out, t_reg = (kq.Pi.cpu(), kq.outlier_codebook.boundaries.cpu(),
+                          kq.regular_codebook.boundaries.cpu())
+    errs, e2e = [], []
+    for h in range(Hkv):
+        hs, qs = slice(h, h + 1), slice(G * h, G * h + G)
+        qh = q[:, qs].float()
+        ref = R.attention_mixed_keys(qh, kc[:, hs], kn[:, hs], vc[:, hs], vn[:, hs],
+                                     *tabs).double()
+        mine = out[:, qs]
+        errs.append(float((mine - ref).norm() / ref.norm()))
+        okc, okn = R.mixed_compress(k[:, hs].float(), pi_k, out_idx, t_out, t_reg)
+        ovc, ovn = R.compress_mse(v[:, hs].float(), vq.Pi.cpu(), vq.codebook.boundaries.cpu())
+        ref2 = R.attention_mixed_keys(qh, okc, okn, ovc, ovn, *tabs).double()
+        e2e.append((float((mine - ref2).norm() / ref2.norm()),
+                    float((mine.flatten() @ ref2.flatten()) / (mine.norm() * ref2.norm()))))
+    assert max(errs) <= 1e-3, errs
+    assert all(e <= 1e-2 and c >= 0.9999 for e, c in e2e), e2e
