@@ -232,6 +232,23 @@ int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
                      uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
                      void* stream);
 
+/* qkv_store_append from rotated unit vectors: the search, QJL and store code
+ * of qkv_store_append (the same device code, with the normalisation and the
+ * rotation skipped) on given fp32 rows y = (x / |x|) Pi^T, groups x S x d,
+ * with the norms to store (groups x S).  Replaces the code stage of
+ * InnerProductQuantizer.compress (quashkv/quantizer.py:225-242) for keys and
+ * of MSEQuantizer.compress (quashkv/quantizer.py:124-131) for values: codes
+ * equal quantize_boundary(y) = #{i : t_i < y} and the QJL bits
+ * [(y - c[code]) S >= 0] bit for bit, exact ties included.  yk or yv may be
+ * NULL to append only the other; rows 4-byte aligned.  Contiguous store only. */
+int qkv_store_append_rotated(const float* yk, const float* knorm_in, const float* yv,
+                             const float* vnorm_in, int64_t groups, int64_t S, int32_t d,
+                             int32_t mbits, int32_t vbits, const float* signs,
+                             const float* kcent_host, const float* kbound_host,
+                             const float* vbound_host, uint8_t* kstore, float* knorm,
+                             uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
+                             void* stream);
+
 /* Inverse of qkv_vtiles_pack: tokens [t0, t0 + S) -> groups x S x d uint8. */
 int qkv_vtiles_unpack(const uint32_t* src, int64_t groups, int64_t S, int32_t d,
                       int32_t vbits, int64_t tiles_per_group, int64_t t0, uint8_t* codes,
@@ -395,6 +412,17 @@ int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups, 
                             const float* out_bound_host, const float* reg_bound_host,
                             uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
                             void* stream);
+
+/* qkv_store_append_kmixed from rotated unit vectors in slot order (row j of
+ * y_slots' last axis = rotated channel perm[j]) with their norms: the kmixed
+ * search and row store of qkv_store_append_kmixed on given y, codes equal to
+ * MixedPrecisionMSEQuantizer's per-channel quantize_boundary
+ * (quashkv/mixed_precision.py:140-158) bit for bit. */
+int qkv_store_append_kmixed_rotated(const float* y_slots, const float* norm_in, int64_t groups,
+                                    int64_t S, int32_t d, int32_t n_out,
+                                    const float* out_bound_host, const float* reg_bound_host,
+                                    uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
+                                    void* stream);
 
 /* Decode attention over kmixed K rows and V tiles: scores
  * n_k <q Pi^T, c_channel[code]> (the reference's decompress-then-attend,

@@ -62,6 +62,10 @@ _SIGS = {
     "qkv_kmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p]),
     "qkv_store_append_kmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p, _p,
                                        _i64, _i64, _p]),
+    "qkv_store_append_rotated": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _p,
+                                        _p, _p, _p, _p, _p, _i64, _i64, _p]),
+    "qkv_store_append_kmixed_rotated": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _p, _p, _p, _p,
+                                               _i64, _i64, _p]),
     "qkv_attention_prepare_kmixed": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32,
                                             _p, _p, _p, _i64, _i32, _p]),
     "qkv_decode_attention_kmixed": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,

@@ -9,33 +9,36 @@
 // (quashkv/triton_kernels/compress.py:210-303).  The codes land in the K-row and
 // V-tile store formats that the decode kernel reads.
 //
-// Rotation.  z = x Pi^T runs on the 16x16x32 bf16 (fp16) MFMA with x as it is
+// Rotation.  z = x Pi^T runs on the 32x32x16 bf16 (fp16) MFMA with x as it is
 // stored (a bf16 / fp16 value is exact in the operand type) and Pi split into
 // a high and a low 16-bit part, Pi ~= Pi_hi + Pi_lo, accumulated in fp32: two
 // MFMA passes carry ~16 (bf16) / ~22 (fp16) significant bits of Pi, against
-// 24 for the reference's fp32 GEMM.  Codes computed from x may therefore
-// differ from the reference's where y lies within ~1e-5 relative of a
-// boundary (about 1e-6 of the coordinates); codes from an identical y go
-// through qkv_compress(QKV_FLAG_PRE_ROTATED), which is exact.
+// 24 for the reference's fp32 GEMM, and y = z / |x| (the reference divides
+// before the GEMM).  Codes computed from x may therefore differ from the
+// reference's where y lies within ~1e-5 relative of a boundary (about 1e-6 of
+// the coordinates).  The same kernels take a given fp32 y instead of x
+// (FROM_Y: the *_rotated entry points) and then run the search, QJL and store
+// code below on it; from an identical y the codes are the reference's, bit for
+// bit, ties included.
 //
-// Boundary search as lane masks.  For the value y of one coordinate,
-// code = #{i : t_i < y} (torch.bucketize, right=False).  A binary search over
-// the sorted thresholds decides one code bit per level with one compare,
-// [y > threshold], whose 64-lane result mask is directly that bit plane for
-// the wave's 64 values; the next level's threshold is picked per lane with
-// v_cndmask on the masks already found (levels of 1, 2, 4, ... candidates).
-// Lloyd-Max lists are symmetric about 0, so the top bit is [y > 0] and the
-// rest is a search of |y| in the positive half (the compare's abs modifier),
-// complemented for y <= 0: 4 VALU operations per 64 values for 3-bit codes.
-// Keys search the fine list c_0 < t_0 < c_1 < ... < c_{2^m-1} (centroids and
-// boundaries interleaved): its count f gives code = f >> 1 and the QJL bit
-// [(y - c[code]) S_j >= 0] = f & 1 (y lies in (c_code, t_code] exactly when f
-// is odd).  The sign S_j is folded in through the codebook's symmetry
-// (c_i = -c_{2^m-1-i}, t_i = -t_{2^m-2-i}): with y' = y S_j the search runs on
-// y', the QJL bit is unchanged and the code is complemented where S_j = -1.
-// Pi is staged with its rows scaled by S, so the MFMA yields y S directly.
-// Exact ties (y equal to a boundary or centroid) are a measure-zero event on
-// this path and resolve as [y' > f].
+// Boundary search as lane masks.  For the value y of one coordinate the
+// reference's code is #{i : t_i < y} (torch.bucketize, right=False) and the
+// QJL bit is [(y - c_code) S_j >= 0].  Keys search the fine list
+// c_0 < t_0 < c_1 < ... < c_{2^m-1} (centroids and boundaries interleaved):
+// its count f gives code = f >> 1 and, with the centroids counted as
+// [c <= y] where S_j > 0 and [c < y] where S_j < 0, the QJL bit = (f & 1)
+// xor [S_j < 0] -- exact, r = 0 included.  Lloyd-Max lists are symmetric about
+// 0 (t_mid = 0), so the top bit of f is [y > 0] and the rest is a search of
+// |y| in the positive half, complemented for y <= 0.  Strictness survives the
+// mirror through integer keys: a = rotl(bits(y), 1) = 2 |y|_bits + sign, and
+// thresholds 2 |p|_bits, so [a > 2 p] is [|y| > p] for y > 0 and [|y| >= p]
+// for y < 0 -- after the complement, a strict count of y on both sides.  The
+// centroid level compares a xor [S_j > 0], which flips that strictness for
+// S_j > 0.  Values search their boundaries the same way without the centroid
+// level.  A binary search decides one code bit per level with one compare,
+// whose 64-lane result mask is directly that bit plane for the wave's 64
+// values; the next level's threshold is picked per lane with v_cndmask on the
+// masks already found (levels of 1, 2, 4, ... candidates).
 //
 // Orientation.  32x32x16 MFMAs: a result VGPR holds one C row per 32-lane
 // half, 32 consecutive columns, so each half of a compare mask is one whole
@@ -48,6 +51,7 @@
 // coalesced vector stores.
 
 #include <cmath>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -69,8 +73,11 @@ constexpr int frag_n() { return (D / 32) * (D / 16) * 2 * 64; }
 constexpr int kFragN = frag_n<kD>();
 constexpr float kPScaleF16 = 256.f;     // keeps the fp16 low part of Pi out of subnormals
 
-struct Thresh {
-  float v[15];  // ascending comparison list
+// Positive half of a symmetric comparison list as integer keys 2 bits(p),
+// ascending (at most 7 entries: 4-bit value boundaries, the 3-bit key MSE
+// fine list).
+struct Half {
+  uint32_t t[7];
 };
 
 typedef float qkv_f32x16 __attribute__((ext_vector_type(16)));
@@ -100,8 +107,8 @@ __device__ __forceinline__ uint32_t put_lane(uint32_t old, uint32_t val) {
 
 // A wave-uniform value held in a VGPR (a v_cndmask may then take two of them
 // with its mask without exceeding the one-scalar-operand limit).
-__device__ __forceinline__ float in_vgpr(float x) {
-  float r;
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+  uint32_t r;
   asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
   return r;
 }
@@ -119,26 +126,51 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
-// Binary search of y in the ascending list t[0 .. 2^L - 2]: bit i of
-// #{j : t[j] < y} as the lane mask m[i].
-template <int L>
-__device__ __forceinline__ void search(float y, const float* t, uint64_t (&m)[L]) {
-  bool c[L];
-  static_for<L>([&](auto kc) {
-    constexpr int k = decltype(kc)::value;  // level k decides bit L - 1 - k
-    float cand[1 << k];
+// Binary search of the key a in the ascending key list t[0 .. 2^LM - 2]: bit i
+// of #{j : t[j] < a} as the lane mask g[i].  With CLAST the last level (whose
+// candidates are the list's even entries) compares ac instead of a.
+template <int LM, bool CLAST>
+__device__ __forceinline__ void search_keys(uint32_t a, uint32_t ac, const uint32_t* t,
+                                            uint64_t (&g)[LM]) {
+  bool c[LM];
+  static_for<LM>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;  // level k decides bit LM - 1 - k
+    uint32_t cand[1 << k];
 #pragma unroll
-    for (int p = 0; p < (1 << k); ++p) cand[p] = t[(2 * p + 1) * (1 << (L - 1 - k)) - 1];
-    // prefix bit j (LSB first) is c[L - k + j]
+    for (int p = 0; p < (1 << k); ++p) cand[p] = t[(2 * p + 1) * (1 << (LM - 1 - k)) - 1];
+    // prefix bit j (LSB first) is c[LM - k + j]
 #pragma unroll
     for (int j = 0; j < k; ++j)
 #pragma unroll
       for (int q = 0; q < (1 << (k - 1 - j)); ++q)
-        cand[q] = c[L - k + j] ? cand[2 * q + 1] : cand[2 * q];
-    c[L - 1 - k] = y > cand[0];
+        cand[q] = c[LM - k + j] ? cand[2 * q + 1] : cand[2 * q];
+    const uint32_t av = (CLAST && k == LM - 1) ? ac : a;
+    c[LM - 1 - k] = av > cand[0];
   });
 #pragma unroll
-  for (int i = 0; i < L; ++i) m[i] = lanes_where(c[i]);
+  for (int i = 0; i < LM; ++i) g[i] = lanes_where(c[i]);
+}
+
+// Strict count #{j : F[j] < y} over a list F of 2^L - 1 entries symmetric
+// about 0 (F[j] = -F[2^L - 2 - j], middle entry 0), given the integer keys of
+// its positive half: bit i as the lane mask m[i].  The top bit is [y > 0]; the
+// others search a = rotl(bits(y), 1) in the positive half and are
+// complemented for y <= 0.  With CLAST the last level counts an entry equal to
+// |y| as below y on the lanes where cx = 1 (see the file comment).
+template <int L, bool CLAST>
+__device__ __forceinline__ void search_sym(float y, const uint32_t* p, uint32_t cx,
+                                           uint64_t (&m)[L]) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, y);
+  // [y > 0] on the bits (denormals included, whatever the float mode)
+  const uint64_t pos = lanes_where(static_cast<int32_t>(u) > 0);
+  m[L - 1] = pos;
+  if constexpr (L > 1) {
+    const uint32_t a = __builtin_amdgcn_alignbit(u, u, 31);
+    uint64_t g[L - 1];
+    search_keys<L - 1, CLAST>(a, a ^ cx, p, g);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
+  }
 }
 
 typedef __bf16 qkv_bf16x2 __attribute__((ext_vector_type(2)));
@@ -161,23 +193,6 @@ __device__ __forceinline__ float sumsq(uint4 q, float s) {
   return s;
 }
 
-// Search of y in a list symmetric about 0 (t[i] = -t[2^L - 2 - i], t[2^(L-1) - 1]
-// = 0), given its positive half p[0 .. 2^(L-1) - 2]: bit i of #{j : t[j] < y}
-// as m[i].  The top bit is [y > 0]; the others search |y| in the positive
-// half and are complemented for y <= 0 (the count mirrors; exact ties with a
-// threshold on the negative side land one code lower than a strict count).
-template <int L>
-__device__ __forceinline__ void search_sym(float y, const float* p, uint64_t (&m)[L]) {
-  const uint64_t pos = lanes_where(y > 0.f);
-  m[L - 1] = pos;
-  if constexpr (L > 1) {
-    uint64_t g[L - 1];
-    search<L - 1>(fabsf(y), p, g);
-#pragma unroll
-    for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
-  }
-}
-
 template <bool F16>
 __device__ __forceinline__ uint16_t to16(float v) {
   if constexpr (F16)
@@ -197,10 +212,9 @@ __device__ __forceinline__ float from16(uint16_t h) {
 // Stage the rotation operand in LDS.  Entry ((b * 8 + s) * 2 + split) * 64 + l
 // holds, for lane l, Pi'[32 b + (l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
 // eight 16-bit values: the high part (split 0) or the low part (split 1) of
-// Pi' = diag(rowsign) Pi * pscale (rowsign = S for keys, none for values).
+// Pi' = Pi * pscale.
 template <bool F16, int D = kD>
-__device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
-                         const float* __restrict__ rowsign, float pscale) {
+__device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi, float pscale) {
   // kThreads threads (every launch uses that block size); each takes NPT
   // (block, k-step, lane) slots and writes both splits of each, with all of
   // its Pi loads in flight before the first conversion
@@ -208,7 +222,6 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
   constexpr int NPT = frag_n<D>() / 2 / kThreads;
   static_assert(NPT * 2 * kThreads == frag_n<D>(), "whole slots per thread");
   float4 p[NPT][2];
-  float sc[NPT];
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
@@ -216,15 +229,15 @@ __device__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
     const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
     p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
     p[x][1] = *reinterpret_cast<const float4*>(pi + j * D + k0 + 4);
-    sc[x] = (rowsign ? rowsign[j] : 1.f) * pscale;  // +-2^k: exact
   }
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
     const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
-    const float v[8] = {p[x][0].x * sc[x], p[x][0].y * sc[x], p[x][0].z * sc[x],
-                        p[x][0].w * sc[x], p[x][1].x * sc[x], p[x][1].y * sc[x],
-                        p[x][1].z * sc[x], p[x][1].w * sc[x]};
+    // pscale = 2^k: the scaling is exact
+    const float v[8] = {p[x][0].x * pscale, p[x][0].y * pscale, p[x][0].z * pscale,
+                        p[x][0].w * pscale, p[x][1].x * pscale, p[x][1].y * pscale,
+                        p[x][1].z * pscale, p[x][1].w * pscale};
     uint32_t hi[8], lo[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -258,32 +271,41 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
 
 // One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
 // grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
-// MB MSE planes, then the QJL plane).
-template <int MB, bool F16, int D, bool PAGED>
+// MB MSE planes, then the QJL plane).  FROM_Y: `xin` holds fp32 rotated unit
+// rows y (rows as above) and `nin` their norms; the normalisation and the
+// rotation are skipped, everything after them is the same code.
+template <int MB, bool F16, int D, bool PAGED, bool FROM_Y>
 __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
-    const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
-    const float* __restrict__ pi, const float* __restrict__ signs, Thresh fine,
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
     QkvPages pg) {
   constexpr int L = MB + 1;           // search levels over the fine list
-  constexpr int NF = (1 << L) - 1;    // c_0, t_0, c_1, ..., c_{2^MB - 1}
+  constexpr int NP = (1 << MB) - 1;   // positive half of the fine list c_0, t_0, ..., c_{2^MB-1}
   constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
   constexpr int NKS = D / 16;         // k-steps
   constexpr int RD = NBK * L;         // dwords per row
   constexpr int NSK = RD * kTok / 64; // staging dwords per lane
   static_assert(RD * kTok % 64 == 0, "whole staging dwords");
-  __shared__ uint4 frag[frag_n<D>()];
+  __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];
   __shared__ float4 inv_s[kWaves][kTok / 4];  // 1 / norm of the wave's tokens
-  stage_pi<F16, D>(frag, pi, signs, F16 ? kPScaleF16 : 1.f);
-  __syncthreads();
+  if constexpr (!FROM_Y) {
+    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
 
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
-  float fv[NF / 2];  // positive half of the fine list
+  uint32_t fv[NP];
 #pragma unroll
-  for (int i = 0; i < NF / 2; ++i) fv[i] = in_vgpr(fine.v[NF / 2 + 1 + i]);
+  for (int i = 0; i < NP; ++i) fv[i] = in_vgpr(fine.t[i]);
   uint64_t sneg[NBK];  // lanes whose coordinate 32 n + (l & 31) has S < 0
+  uint32_t cx[NBK];    // 1 where S >= 0: the centroid level counts c <= y there
 #pragma unroll
-  for (int n = 0; n < NBK; ++n) sneg[n] = lanes_where(signs[32 * n + li] < 0.f);
+  for (int n = 0; n < NBK; ++n) {
+    const bool neg = signs[32 * n + li] < 0.f;
+    sneg[n] = lanes_where(neg);
+    cx[n] = neg ? 0u : 1u;
+  }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
@@ -294,34 +316,43 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     QkvSpan sp{};
     if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, t0 + s0);
     uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
-    {
+    if constexpr (FROM_Y) {
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && 32 * tt + li < nv) {
+          const int64_t t = t0 + s0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) knorm[r] = nin[grp * S + s0 + 32 * tt + li];
+        }
+    } else {
       const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
       load_x<NKS>(xf, row, lane);
-    }
 
-    // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
-    // 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four consecutive tokens)
-    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+      // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
+      // 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four consecutive tokens)
+      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
-    for (int tt = 0; tt < kHalves; ++tt) {
-      float ss = 0.f;
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-      ss += __shfl_xor(ss, 32, 64);
-      const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (lane < 32) {
-        if (32 * tt + li < nv) {
-          const int64_t t = t0 + s0 + 32 * tt + li;
-          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0) knorm[r] = nrm;
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
+        if (lane < 32) {
+          if (32 * tt + li < nv) {
+            const int64_t t = t0 + s0 + 32 * tt + li;
+            const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+            if (r >= 0) knorm[r] = nrm;
+          }
+          invw[32 * tt + li] = iscale / nrm;
         }
-        invw[32 * tt + li] = iscale / nrm;
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-    __builtin_amdgcn_wave_barrier();
 
     uint32_t stg[NSK];
 #pragma unroll
@@ -332,31 +363,51 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
       // one coordinate block at a time: keeps the scheduler from overlapping
       // blocks (and their accumulators and fragments) beyond the register file
       __builtin_amdgcn_sched_barrier(0);
-      qkv_f32x16 acc[kHalves] = {};
+      // y of coordinate 32 n + (l & 31) for tokens 32 tt + 8 (v >> 2) + 4 (l >> 5) + (v & 3)
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
 #pragma unroll
-      for (int s = 0; s < NKS; ++s)
+        for (int tt = 0; tt < kHalves; ++tt)
 #pragma unroll
-        for (int sp = 0; sp < 2; ++sp) {
-          const uint4 bf = frag[((n * NKS + s) * 2 + sp) * 64 + lane];
+          for (int v = 0; v < 16; ++v) {
+            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * D + 32 * n + li];
+          }
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+        for (int s = 0; s < NKS; ++s)
+#pragma unroll
+          for (int sp2 = 0; sp2 < 2; ++sp2) {
+            const uint4 bf = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float4 iv4[4];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float4 q4 = iv4[v >> 2];
+            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            yv[tt][v] = acc[tt][v] * iv;
+          }
         }
+      }
       static_for<kHalves>([&](auto tc) {
         constexpr int tt = decltype(tc)::value;
-        float4 iv4[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
         static_for<16>([&](auto vc) {
           constexpr int v = decltype(vc)::value;
-          const float4 q4 = iv4[v >> 2];
-          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
           uint64_t f[L];
-          search_sym<L>(acc[tt][v] * iv, fv, f);  // on y_j S_j
+          search_sym<L, true>(yv[tt][v], fv, cx[n], f);
           // token ta (lanes 0..31) and ta + 4 (lanes 32..63)
           constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);
           static_for<L>([&](auto rc) {
             constexpr int r = decltype(rc)::value;  // plane r: MSE bit r, r = MB: QJL
-            const uint64_t w = r < MB ? (f[r + 1 < L ? r + 1 : 0] ^ sneg[n]) : f[0];
+            const uint64_t w = r < MB ? f[r < MB ? r + 1 : 0] : (f[0] ^ sneg[n]);
             constexpr int D0 = ta * RD + NBK * r + n, D1 = (ta + 4) * RD + NBK * r + n;
             stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w));
             stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w >> 32));
@@ -393,25 +444,28 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 // plane b0 and plane b1 of every coordinate, then a third plane holding b2 of
 // the NO outlier coordinates at bits 0.. and their parity b0^b1^b2 at bits
 // 64..  The outlier coordinates fill whole 32-coordinate blocks (NO = 32 or
-// 64), so each block's codebook is fixed at compile time.
-template <int NO, bool F16>
+// 64), so each block's codebook is fixed at compile time.  FROM_Y: `xin`
+// holds fp32 rotated unit rows in slot order and `nin` their norms.
+template <int NO, bool F16, bool FROM_Y>
 __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
-    const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
-    const float* __restrict__ pi_perm, Thresh po, Thresh pr, uint8_t* __restrict__ kst,
-    float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi_perm, Half po, Half pr,
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
   constexpr int RD = 12;              // dwords per row
   constexpr int NSK = RD * kTok / 64; // staging dwords per lane
   constexpr int NOB = NO / 32;        // outlier blocks
-  __shared__ uint4 frag[kFragN];
+  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];
   __shared__ float4 inv_s[kWaves][kTok / 4];
-  stage_pi<F16>(frag, pi_perm, nullptr, F16 ? kPScaleF16 : 1.f);
-  __syncthreads();
+  if constexpr (!FROM_Y) {
+    stage_pi<F16>(frag, pi_perm, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
 
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
-  float pov[3], prv[1];  // positive halves: outlier (3-bit) and regular (2-bit) boundaries
+  uint32_t pov[3], prv[1];  // positive halves: outlier (3-bit) and regular (2-bit) boundaries
 #pragma unroll
-  for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.v[i]);
-  prv[0] = in_vgpr(pr.v[0]);
+  for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.t[i]);
+  prv[0] = in_vgpr(pr.t[0]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
@@ -419,30 +473,35 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    float* nrow = knorm + grp * t_stride + t0 + s0;
     uint4 xf[kHalves][8];
-    {
+    if constexpr (FROM_Y) {
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && 32 * tt + li < nv) nrow[32 * tt + li] = nin[grp * S + s0 + 32 * tt + li];
+    } else {
       const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt)
         row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
       load_x(xf, row, lane);
-    }
-    float* nrow = knorm + grp * t_stride + t0 + s0;
-    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
-    for (int tt = 0; tt < kHalves; ++tt) {
-      float ss = 0.f;
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float ss = 0.f;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-      ss += __shfl_xor(ss, 32, 64);
-      const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (lane < 32) {
-        if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
-        invw[32 * tt + li] = iscale / nrm;
+        for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
+        if (lane < 32) {
+          if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
+          invw[32 * tt + li] = iscale / nrm;
+        }
       }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-    __builtin_amdgcn_wave_barrier();
 
     uint32_t stg[NSK];
 #pragma unroll
@@ -451,37 +510,56 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     static_for<4>([&](auto nc) {  // coordinate block n
       constexpr int n = decltype(nc)::value;
       __builtin_amdgcn_sched_barrier(0);
-      qkv_f32x16 acc[kHalves] = {};
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
 #pragma unroll
-      for (int s = 0; s < 8; ++s)
+        for (int tt = 0; tt < kHalves; ++tt)
 #pragma unroll
-        for (int sp = 0; sp < 2; ++sp) {
-          const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
+          for (int v = 0; v < 16; ++v) {
+            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * kD + 32 * n + li];
+          }
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) {
+            const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float4 iv4[4];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float4 q4 = iv4[v >> 2];
+            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            yv[tt][v] = acc[tt][v] * iv;
+          }
         }
+      }
       static_for<kHalves>([&](auto tc) {
         constexpr int tt = decltype(tc)::value;
-        float4 iv4[4];
-#pragma unroll
-        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
         static_for<16>([&](auto vc) {
           constexpr int v = decltype(vc)::value;
-          const float4 q4 = iv4[v >> 2];
-          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-          const float y = acc[tt][v] * iv;
+          const float y = yv[tt][v];
           constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);  // token of lanes 0..31
           uint64_t w[4];  // plane words: b0, b1 (+ outliers: b2, parity)
           if constexpr (n < NOB) {
             uint64_t m[3];
-            search_sym<3>(y, pov, m);
+            search_sym<3, false>(y, pov, 0u, m);
             w[0] = m[0];
             w[1] = m[1];
             w[2] = m[2];
             w[3] = m[0] ^ m[1] ^ m[2];
           } else {
             uint64_t m[2];
-            search_sym<2>(y, prv, m);
+            search_sym<2, false>(y, prv, 0u, m);
             w[0] = m[0];
             w[1] = m[1];
             w[2] = w[3] = 0;
@@ -511,25 +589,28 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
 
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
 // so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
-// already in the store.
-template <int VB, bool F16, int D, bool PAGED>
+// already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
+// their norms.
+template <int VB, bool F16, int D, bool PAGED, bool FROM_Y>
 __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
-    const uint16_t* __restrict__ x, int64_t S, int64_t tpg, int64_t ntiles,
-    const float* __restrict__ pi, Thresh bnd, uint32_t* __restrict__ vst,
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
-  constexpr int NB = (1 << VB) - 1;  // boundaries
+  constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
   constexpr int NPW = D / 64;        // staging dwords per (tile, plane)
   constexpr int NS = NPW * VB * kHalves;  // staging dwords per lane: tiles x VB planes x D / 64
-  __shared__ uint4 frag[frag_n<D>()];
-  stage_pi<F16, D>(frag, pi, nullptr, F16 ? kPScaleF16 : 1.f);
-  __syncthreads();
+  __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];
+  if constexpr (!FROM_Y) {
+    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
 
   const int lane = threadIdx.x & 63, li = lane & 31;
-  float bv[NB / 2 > 0 ? NB / 2 : 1];  // positive half of the boundaries
+  uint32_t bv[NP > 0 ? NP : 1];
 #pragma unroll
-  for (int i = 0; i < NB / 2; ++i) bv[i] = in_vgpr(bnd.v[NB / 2 + 1 + i]);
+  for (int i = 0; i < NP; ++i) bv[i] = in_vgpr(bnd.t[i]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t a_base = t0 & ~int64_t(31);
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
@@ -542,32 +623,43 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     QkvSpan sp{};
     if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, A0);
     bool ok[kHalves];
-    uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
-    {
-      const uint16_t* row[kHalves];
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) {
-        const int64_t si = d0 + 32 * tt + li;
-        ok[tt] = si >= 0 && si < S;
-        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1)) * D;
-      }
-      load_x<NKS>(xf, row, lane);
-    }
-
-    float inv[kHalves];  // token 32 tt + (l & 31): the C-column of this lane
+    int64_t src[kHalves];  // input row of this lane's token (clamped into [0, S))
 #pragma unroll
     for (int tt = 0; tt < kHalves; ++tt) {
-      float ss = 0.f;
+      const int64_t si = d0 + 32 * tt + li;
+      ok[tt] = si >= 0 && si < S;
+      src[tt] = grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1);
+    }
+    uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
+    float inv[kHalves];      // token 32 tt + (l & 31): the C-column of this lane
+    if constexpr (FROM_Y) {
 #pragma unroll
-      for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-      ss += __shfl_xor(ss, 32, 64);
-      const float nrm = fmaxf(sqrtf(ss), 1e-8f);
-      if (lane < 32 && ok[tt]) {
-        const int64_t t = A0 + 32 * tt + li;
-        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-        if (r >= 0) vnorm[r] = nrm;
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && ok[tt]) {
+          const int64_t t = A0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) vnorm[r] = nin[src[tt]];
+        }
+    } else {
+      const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+      load_x<NKS>(xf, row, lane);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
+        if (lane < 32 && ok[tt]) {
+          const int64_t t = A0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) vnorm[r] = nrm;
+        }
+        inv[tt] = iscale / nrm;
       }
-      inv[tt] = iscale / nrm;
     }
 
     uint32_t stg[NS];
@@ -577,21 +669,36 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     static_for<NBK>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
       constexpr int mb = decltype(mc)::value;
       __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
-      qkv_f32x16 acc[kHalves] = {};
+      // y of coordinate 32 mb + 8 (v >> 2) + 4 (l >> 5) + (v & 3), token 32 tt + (l & 31)
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
 #pragma unroll
-      for (int s = 0; s < NKS; ++s)
+        for (int tt = 0; tt < kHalves; ++tt)
 #pragma unroll
-        for (int sp = 0; sp < 2; ++sp) {
-          const uint4 af = frag[((mb * NKS + s) * 2 + sp) * 64 + lane];
+          for (int v = 0; v < 16; ++v)
+            yv[tt][v] = y[src[tt] * D + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
-        }
+        for (int s = 0; s < NKS; ++s)
+#pragma unroll
+          for (int sp2 = 0; sp2 < 2; ++sp2) {
+            const uint4 af = frag[((mb * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * inv[tt];
+      }
       static_for<kHalves>([&](auto tc) {  // V tile tt of the wave tile
         constexpr int tt = decltype(tc)::value;
         static_for<16>([&](auto vc) {
           constexpr int v = decltype(vc)::value;
           uint64_t m[VB];
-          search_sym<VB>(acc[tt][v] * inv[tt], bv, m);
+          search_sym<VB, false>(yv[tt][v], bv, 0u, m);
           // coordinate ca (lanes 0..31) and ca + 4 (lanes 32..63), tokens 32 tt + 0..31
           constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
           static_for<VB>([&](auto kc) {
@@ -633,32 +740,45 @@ bool symmetric(const float* v, int n) {
   return true;
 }
 
+// Integer keys 2 bits(p) of the positive half of an ascending list v[0 .. n-1]
+// symmetric about 0 (n odd); false unless those entries are positive and finite.
+bool positive_half(const float* v, int n, Half* h) {
+  for (int i = 0; i < n / 2; ++i) {
+    const float p = v[n / 2 + 1 + i];
+    if (!(p > 0.f) || !std::isfinite(p)) return false;
+    uint32_t b;
+    std::memcpy(&b, &p, 4);
+    h->t[i] = 2u * b;
+  }
+  return true;
+}
+
 int append_blocks(int64_t ntiles) {
   const int64_t cap = int64_t(qkv_num_cus()) * 2;  // two 64-KiB-LDS workgroups per CU
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((ntiles + kWaves - 1) / kWaves, cap)));
 }
 
-}  // namespace
-
-static int store_append_impl(int32_t in_dtype, const void* keys, const void* values,
-                             int64_t groups, int64_t S, int32_t d, int32_t mbits,
-                             int32_t vbits, const float* pi, const float* signs,
-                             const float* kcent_host, const float* kbound_host,
-                             const float* vbound_host, uint8_t* kstore, float* knorm,
-                             uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
-                             QkvPages pg, void* stream) {
+// qkv_store_append and its variants.  rotated: keys / values are fp32 rotated
+// unit rows y with their norms in knorm_in / vnorm_in (in_dtype unused).
+int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bool rotated,
+                      const float* knorm_in, const float* vnorm_in, int64_t groups, int64_t S,
+                      int32_t d, int32_t mbits, int32_t vbits, const float* pi,
+                      const float* signs, const float* kcent_host, const float* kbound_host,
+                      const float* vbound_host, uint8_t* kstore, float* knorm, uint32_t* vstore,
+                      float* vnorm, int64_t t_stride, int64_t t0, QkvPages pg, void* stream) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
   if (pg.tab == nullptr) {
     QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
                 "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
                 (long long)t_stride, (long long)t0, (long long)(t0 + S));
   } else {
+    QKV_REQUIRE(!rotated, "the rotated append writes the contiguous store only");
     QKV_REQUIRE(pg.H > 0 && groups % pg.H == 0, "groups must be batch x kv heads");
     QKV_REQUIRE(t0 + S <= (int64_t(pg.pmax) << pg.lg),
                 "page table of %d pages of %d tokens per sequence must hold tokens "
                 "[%lld, %lld)", pg.pmax, 1 << pg.lg, (long long)t0, (long long)(t0 + S));
   }
-  if (in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
+  if (!rotated && in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
     qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
     return QKV_E_UNSUPPORTED;
   }
@@ -666,41 +786,46 @@ static int store_append_impl(int32_t in_dtype, const void* keys, const void* val
     qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
     return QKV_E_UNSUPPORTED;
   }
+  const int in_align = rotated ? 4 : 16;
   if (keys) {
     if (mbits < 1 || mbits > 3) {
       qkv_set_error("store append: key MSE bits %d not in 1..3", mbits);
       return QKV_E_UNSUPPORTED;
     }
-    QKV_REQUIRE(pi && signs && kcent_host && kbound_host && kstore && knorm, "null pointer");
-    QKV_REQUIRE(qkv_aligned(keys, 16) && qkv_aligned(kstore, 4), "keys 16-B / store 4-B aligned");
+    QKV_REQUIRE((rotated || pi) && signs && kcent_host && kbound_host && kstore && knorm &&
+                    (!rotated || knorm_in),
+                "null pointer");
+    QKV_REQUIRE(qkv_aligned(keys, in_align) && qkv_aligned(kstore, 4),
+                "keys %d-B / store 4-B aligned", in_align);
   }
   if (values) {
     QKV_REQUIRE(qkv_bits_ok(vbits), "value bits %d not in 1..4", vbits);
-    QKV_REQUIRE(pi && vbound_host && vstore && vnorm, "null pointer");
-    QKV_REQUIRE(qkv_aligned(values, 16) && qkv_aligned(vstore, 4),
-                "values 16-B / store 4-B aligned");
+    QKV_REQUIRE((rotated || pi) && vbound_host && vstore && vnorm && (!rotated || vnorm_in),
+                "null pointer");
+    QKV_REQUIRE(qkv_aligned(values, in_align) && qkv_aligned(vstore, 4),
+                "values %d-B / store 4-B aligned", in_align);
   }
   QKV_REQUIRE(!pi || qkv_aligned(pi, 16), "pi must be 16-byte aligned");
-  Thresh fine{}, bnd{};
+  Half fine{}, bnd{};
   if (keys) {
     const int nc = 1 << mbits;
+    float fl[15];
     for (int i = 0; i < nc; ++i) {
-      fine.v[2 * i] = kcent_host[i];
-      if (i + 1 < nc) fine.v[2 * i + 1] = kbound_host[i];
+      fl[2 * i] = kcent_host[i];
+      if (i + 1 < nc) fl[2 * i + 1] = kbound_host[i];
     }
     bool asc = true;
-    for (int i = 0; i + 1 < 2 * nc - 1; ++i) asc = asc && fine.v[i] < fine.v[i + 1];
-    if (!asc || !symmetric(fine.v, 2 * nc - 1)) {
+    for (int i = 0; i + 1 < 2 * nc - 1; ++i) asc = asc && fl[i] < fl[i + 1];
+    if (!asc || !symmetric(fl, 2 * nc - 1) || !positive_half(fl, 2 * nc - 1, &fine)) {
       qkv_set_error("store append needs a symmetric key codebook with c_i < t_i < c_{i+1}");
       return QKV_E_UNSUPPORTED;
     }
   }
   if (values) {
     const int nb = (1 << vbits) - 1;
-    for (int i = 0; i < nb; ++i) bnd.v[i] = vbound_host[i];
     bool asc = true;
-    for (int i = 0; i + 1 < nb; ++i) asc = asc && bnd.v[i] < bnd.v[i + 1];
-    if (!asc || !symmetric(bnd.v, nb)) {
+    for (int i = 0; i + 1 < nb; ++i) asc = asc && vbound_host[i] < vbound_host[i + 1];
+    if (!asc || !symmetric(vbound_host, nb) || !positive_half(vbound_host, nb, &bnd)) {
       qkv_set_error("store append needs ascending value boundaries symmetric about 0");
       return QKV_E_UNSUPPORTED;
     }
@@ -711,14 +836,19 @@ static int store_append_impl(int32_t in_dtype, const void* keys, const void* val
   if (keys) {
     const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
-    const auto* xk = static_cast<const uint16_t*>(keys);
-#define QKV_K(MB, F, DD)                                                                   \
-  if (pg.tab)                                                                              \
-    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, true>), grid, dim3(kThreads), 0, s, xk, S,  \
-                       tpg, ntiles, pi, signs, fine, kstore, knorm, t_stride, t0, pg);     \
-  else                                                                                     \
-    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, false>), grid, dim3(kThreads), 0, s, xk, S, \
-                       tpg, ntiles, pi, signs, fine, kstore, knorm, t_stride, t0, pg)
+#define QKV_K(MB, F, DD)                                                                       \
+  if (rotated)                                                                                 \
+    hipLaunchKernelGGL((append_k_mfma<MB, false, DD, false, true>), grid, dim3(kThreads), 0, s, \
+                       keys, knorm_in, S, tpg, ntiles, pi, signs, fine, kstore, knorm,          \
+                       t_stride, t0, pg);                                                      \
+  else if (pg.tab)                                                                             \
+    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, true, false>), grid, dim3(kThreads), 0, s,     \
+                       keys, nullptr, S, tpg, ntiles, pi, signs, fine, kstore, knorm,           \
+                       t_stride, t0, pg);                                                      \
+  else                                                                                         \
+    hipLaunchKernelGGL((append_k_mfma<MB, F, DD, false, false>), grid, dim3(kThreads), 0, s,    \
+                       keys, nullptr, S, tpg, ntiles, pi, signs, fine, kstore, knorm,           \
+                       t_stride, t0, pg)
 #define QKV_KD(DD)                                  \
   switch (mbits * 2 + (f16 ? 1 : 0)) {              \
     case 2: QKV_K(1, false, DD); break;             \
@@ -741,14 +871,19 @@ static int store_append_impl(int32_t in_dtype, const void* keys, const void* val
     const int64_t a_base = t0 & ~int64_t(31);
     const int64_t tpg = (t0 + S - a_base + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
-    const auto* xv = static_cast<const uint16_t*>(values);
-#define QKV_V(VB, F, DD)                                                                   \
-  if (pg.tab)                                                                              \
-    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, true>), grid, dim3(kThreads), 0, s, xv, S,  \
-                       tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0, pg);             \
-  else                                                                                     \
-    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, false>), grid, dim3(kThreads), 0, s, xv, S, \
-                       tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0, pg)
+#define QKV_V(VB, F, DD)                                                                       \
+  if (rotated)                                                                                 \
+    hipLaunchKernelGGL((append_v_mfma<VB, false, DD, false, true>), grid, dim3(kThreads), 0, s, \
+                       values, vnorm_in, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,  \
+                       pg);                                                                    \
+  else if (pg.tab)                                                                             \
+    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, true, false>), grid, dim3(kThreads), 0, s,     \
+                       values, nullptr, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,   \
+                       pg);                                                                    \
+  else                                                                                         \
+    hipLaunchKernelGGL((append_v_mfma<VB, F, DD, false, false>), grid, dim3(kThreads), 0, s,    \
+                       values, nullptr, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,   \
+                       pg)
 #define QKV_VD(DD)                                  \
   switch (vbits * 2 + (f16 ? 1 : 0)) {              \
     case 2: QKV_V(1, false, DD); break;             \
@@ -772,6 +907,62 @@ static int store_append_impl(int32_t in_dtype, const void* keys, const void* val
   return QKV_OK;
 }
 
+// The kmixed key append (x or, rotated, y in slot order with its norms).
+int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const float* norm_in,
+                       int64_t groups, int64_t S, int32_t d, const float* pi_perm,
+                       int32_t n_out, const float* out_bound_host,
+                       const float* reg_bound_host, uint8_t* kstore, float* knorm,
+                       int64_t t_stride, int64_t t0, void* stream) {
+  QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
+              (long long)t_stride, (long long)t0, (long long)(t0 + S));
+  if (!rotated && in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
+    qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
+    return QKV_E_UNSUPPORTED;
+  }
+  if (d != kD || (n_out != 32 && n_out != 64)) {
+    qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(keys && (rotated || pi_perm) && out_bound_host && reg_bound_host && kstore &&
+                  knorm && (!rotated || norm_in),
+              "null pointer");
+  QKV_REQUIRE(qkv_aligned(keys, rotated ? 4 : 16) && qkv_aligned(kstore, 4) &&
+                  (rotated || qkv_aligned(pi_perm, 16)),
+              "keys / pi aligned (16-B bf16 / fp16 rows, 4-B fp32 rows) and store 4-B aligned");
+  Half po{}, pr{};
+  bool asc = true;
+  for (int i = 0; i + 1 < 7; ++i) asc = asc && out_bound_host[i] < out_bound_host[i + 1];
+  for (int i = 0; i + 1 < 3; ++i) asc = asc && reg_bound_host[i] < reg_bound_host[i + 1];
+  if (!asc || !symmetric(out_bound_host, 7) || !symmetric(reg_bound_host, 3) ||
+      !positive_half(out_bound_host, 7, &po) || !positive_half(reg_bound_host, 3, &pr)) {
+    qkv_set_error("mixed-precision keys need ascending boundaries symmetric about 0");
+    return QKV_E_UNSUPPORTED;
+  }
+  if (groups == 0 || S == 0) return QKV_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
+  const dim3 grid(append_blocks(ntiles));
+  const bool f16 = in_dtype == QKV_F16;
+#define QKV_KM(NOV, F, FY)                                                                    \
+  hipLaunchKernelGGL((append_kmix_mfma<NOV, F, FY>), grid, dim3(kThreads), 0, s, keys,       \
+                     norm_in, S, tpg, ntiles, pi_perm, po, pr, kstore, knorm, t_stride, t0)
+  if (n_out == 32) {
+    if (rotated) QKV_KM(32, false, true);
+    else if (f16) QKV_KM(32, true, false);
+    else QKV_KM(32, false, false);
+  } else {
+    if (rotated) QKV_KM(64, false, true);
+    else if (f16) QKV_KM(64, true, false);
+    else QKV_KM(64, false, false);
+  }
+#undef QKV_KM
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+}  // namespace
+
 extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
                                 int64_t groups, int64_t S, int32_t d, int32_t mbits,
                                 int32_t vbits, const float* pi, const float* signs,
@@ -779,9 +970,23 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
                                 const float* vbound_host, uint8_t* kstore, float* knorm,
                                 uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
                                 void* stream) {
-  return store_append_impl(in_dtype, keys, values, groups, S, d, mbits, vbits, pi, signs,
-                           kcent_host, kbound_host, vbound_host, kstore, knorm, vstore, vnorm,
-                           t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream);
+  return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, groups, S, d, mbits,
+                           vbits, pi, signs, kcent_host, kbound_host, vbound_host, kstore, knorm,
+                           vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream);
+}
+
+extern "C" int qkv_store_append_rotated(const float* yk, const float* knorm_in, const float* yv,
+                                        const float* vnorm_in, int64_t groups, int64_t S,
+                                        int32_t d, int32_t mbits, int32_t vbits,
+                                        const float* signs, const float* kcent_host,
+                                        const float* kbound_host, const float* vbound_host,
+                                        uint8_t* kstore, float* knorm, uint32_t* vstore,
+                                        float* vnorm, int64_t t_stride, int64_t t0,
+                                        void* stream) {
+  return store_append_impl(QKV_F32, yk, yv, true, knorm_in, vnorm_in, groups, S, d, mbits,
+                           vbits, nullptr, signs, kcent_host, kbound_host, vbound_host, kstore,
+                           knorm, vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0},
+                           stream);
 }
 
 extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
@@ -798,10 +1003,10 @@ extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const 
   const int lg = qkv_page_lg(page_tokens);
   QKV_REQUIRE(lg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
   QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
-  return store_append_impl(in_dtype, keys, values, int64_t(B) * H, S, d, mbits, vbits, pi,
-                           signs, kcent_host, kbound_host, vbound_host, kpool, knorm, vpool,
-                           vnorm, page_tokens, t0, QkvPages{page_table, pages_per_seq, H, lg, num_pages},
-                           stream);
+  return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, int64_t(B) * H, S, d,
+                           mbits, vbits, pi, signs, kcent_host, kbound_host, vbound_host, kpool,
+                           knorm, vpool, vnorm, page_tokens, t0,
+                           QkvPages{page_table, pages_per_seq, H, lg, num_pages}, stream);
 }
 
 extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups,
@@ -810,43 +1015,16 @@ extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64
                                        const float* reg_bound_host, uint8_t* kstore,
                                        float* knorm, int64_t t_stride, int64_t t0,
                                        void* stream) {
-  QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
-  QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
-              (long long)t_stride, (long long)t0, (long long)(t0 + S));
-  if (in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
-    qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
-    return QKV_E_UNSUPPORTED;
-  }
-  if (d != kD || (n_out != 32 && n_out != 64)) {
-    qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
-    return QKV_E_UNSUPPORTED;
-  }
-  QKV_REQUIRE(keys && pi_perm && out_bound_host && reg_bound_host && kstore && knorm,
-              "null pointer");
-  QKV_REQUIRE(qkv_aligned(keys, 16) && qkv_aligned(kstore, 4) && qkv_aligned(pi_perm, 16),
-              "keys / pi 16-B and store 4-B aligned");
-  Thresh po{}, pr{};
-  if (!symmetric(out_bound_host, 7) || !symmetric(reg_bound_host, 3)) {
-    qkv_set_error("mixed-precision keys need boundaries symmetric about 0");
-    return QKV_E_UNSUPPORTED;
-  }
-  for (int i = 0; i < 3; ++i) po.v[i] = out_bound_host[4 + i];
-  pr.v[0] = reg_bound_host[2];
-  if (groups == 0 || S == 0) return QKV_OK;
-  auto s = static_cast<hipStream_t>(stream);
-  const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
-  const dim3 grid(append_blocks(ntiles));
-  const auto* xk = static_cast<const uint16_t*>(keys);
-  const bool f16 = in_dtype == QKV_F16;
-#define QKV_KM(NOV, F)                                                                         \
-  hipLaunchKernelGGL((append_kmix_mfma<NOV, F>), grid, dim3(kThreads), 0, s, xk, S, tpg,     \
-                     ntiles, pi_perm, po, pr, kstore, knorm, t_stride, t0)
-  if (n_out == 32) {
-    if (f16) QKV_KM(32, true); else QKV_KM(32, false);
-  } else {
-    if (f16) QKV_KM(64, true); else QKV_KM(64, false);
-  }
-#undef QKV_KM
-  QKV_LAUNCHED();
-  return QKV_OK;
+  return kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm, n_out,
+                            out_bound_host, reg_bound_host, kstore, knorm, t_stride, t0, stream);
+}
+
+extern "C" int qkv_store_append_kmixed_rotated(const float* y_slots, const float* norm_in,
+                                               int64_t groups, int64_t S, int32_t d,
+                                               int32_t n_out, const float* out_bound_host,
+                                               const float* reg_bound_host, uint8_t* kstore,
+                                               float* knorm, int64_t t_stride, int64_t t0,
+                                               void* stream) {
+  return kmixed_append_impl(QKV_F32, y_slots, true, norm_in, groups, S, d, nullptr, n_out,
+                            out_bound_host, reg_bound_host, kstore, knorm, t_stride, t0, stream);
 }

@@ -169,3 +169,140 @@ def test_fused_append_engine_attention_vs_oracle():
     err = float((out - ref).norm() / ref.norm())
     cos = float((out.flatten() @ ref.flatten()) / (out.norm() * ref.norm()))
     assert err <= 1e-2 and cos >= 0.9999, (err, cos)
+
+
+# ---------------------------------------------------------------- from y
+#
+# qkv_store_append_rotated / qkv_store_append_kmixed_rotated run the search,
+# QJL and store code of the fused append on a given rotated y: codes equal the
+# reference's quantize_boundary / [(y - c[code]) S >= 0] bit for bit, on
+# values chosen to hit every tie: each boundary and centroid, its neighbours
+# one ulp away on both sides, both signs, +-0, denormals and huge values.
+
+def _specials(values):
+    sp = [0.0, -0.0, 1e-45, -1e-45, 1e-30, -1e-30, 1e30, -1e30, 1.0, -1.0]
+    for v in values:
+        v = np.float32(v)
+        for w in (v, -v):
+            sp += [w, np.nextafter(w, np.float32(np.inf)), np.nextafter(w, np.float32(-np.inf))]
+    return np.asarray(sp, dtype=np.float32)
+
+
+def _special_rows(seed, shape, values, n_random=0):
+    """Rows of special values at random coordinates (each value lands on
+    coordinates of both QJL signs), plus n_random rows of random unit y."""
+    sp = _specials(values)
+    rng = np.random.default_rng(seed)
+    y = sp[rng.integers(0, len(sp), size=shape)]
+    if n_random:
+        r = rng.standard_normal((*shape[:-2], n_random, shape[-1])).astype(np.float32)
+        r /= np.linalg.norm(r, axis=-1, keepdims=True)
+        y[..., :n_random, :] = r
+    return torch.from_numpy(y)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("mbits,vbits", [(1, 1), (2, 3), (3, 4), (2, 2), (1, 4), (3, 1)])
+def test_store_append_rotated_bit_exact(d, mbits, vbits):
+    from quashkv_amd.store import KVStore
+    groups_b, H, S = 2, 3, 300
+    kq = Q.InnerProductQuantizer(d=d, total_bits=mbits + 1, seed=17, device=DEV)
+    vq = Q.MSEQuantizer(d=d, bits=vbits, seed=17, device=DEV)
+    mq = kq.mse_quantizer
+    kcb, vcb = mq.codebook, vq.codebook
+    yk = _special_rows(mbits * 7 + d, (groups_b, H, S, d),
+                       list(kcb.centroids_host) + list(kcb.boundaries_host), n_random=40)
+    yv = _special_rows(vbits * 5 + d, (groups_b, H, S, d), list(vcb.boundaries_host),
+                       n_random=40)
+    g = torch.Generator().manual_seed(d)
+    kn = torch.rand(groups_b, H, S, generator=g) + 0.5
+    vn = torch.rand(groups_b, H, S, generator=g) + 0.5
+    st = KVStore(groups_b, H, d, mbits, vbits, S, DEV)
+    t0 = 0
+    yk_d, yv_d, kn_d, vn_d = (t.contiguous().to(DEV) for t in (yk, yv, kn, vn))
+    kc_h, kb_h, vb_h = (N.HostFloats(kcb.centroids_host), N.HostFloats(kcb.boundaries_host),
+                        N.HostFloats(vcb.boundaries_host))
+    N.check(N.lib().qkv_store_append_rotated(
+        yk_d.data_ptr(), kn_d.data_ptr(), yv_d.data_ptr(), vn_d.data_ptr(), groups_b * H, S, d,
+        mbits, vbits, kq.S.data_ptr(), kc_h.ptr, kb_h.ptr, vb_h.ptr, st.kst.data_ptr(),
+        st.knorm.data_ptr(), st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, t0,
+        N.stream(torch.device(DEV))))
+    kc, kb, vc = (t.cpu() for t in st.read_codes(0, S))
+    okc, okb = R.compress_ip_from_y(yk, kcb.boundaries.cpu(), kq.S.cpu(), kcb.centroids.cpu())
+    ovc = R.quantize_boundary(yv, vcb.boundaries.cpu())
+    assert torch.equal(kc, okc.to(torch.uint8))
+    assert torch.equal(kb, okb.to(torch.uint8))
+    assert torch.equal(vc, ovc.to(torch.uint8))
+    assert torch.equal(st.knorm[:, :, :S].cpu(), kn)
+    assert torch.equal(st.vnorm[:, :, :S].cpu(), vn)
+    # the r = 0 cases are present with both signs of S, and resolve to 1
+    r0 = yk == kcb.centroids.cpu()[okc.long()]
+    sgn = kq.S.cpu().expand_as(yk)
+    assert bool(r0[sgn > 0].any()) and bool(r0[sgn < 0].any())
+    assert bool((kb[r0] == 1).all())
+
+
+@pytest.mark.parametrize("n_out", [32, 64])
+def test_store_append_kmixed_rotated_bit_exact(n_out):
+    from quashkv_amd.store import KVStore
+    kq = Q.MixedPrecisionMSEQuantizer(128, outlier_bits=3, regular_bits=2, n_outliers=n_out,
+                                      seed=3, device=DEV)
+    g = torch.Generator().manual_seed(n_out)
+    out_idx = torch.randperm(128, generator=g)[:n_out].sort().values
+    kq.set_outlier_channels(out_idx.to(DEV))
+    oc, rc = kq.outlier_codebook, kq.regular_codebook
+    B, H, S = 2, 2, 260
+    y = _special_rows(n_out, (B, H, S, 128),
+                      list(oc.boundaries_host) + list(rc.boundaries_host), n_random=30)
+    nrm = torch.rand(B, H, S, generator=g) + 0.5
+    o = [int(i) for i in out_idx]
+    perm = o + [j for j in range(128) if j not in set(o)]
+    st = KVStore(B, H, 128, 2, 4, S, DEV, kmix=(perm, n_out))
+    ys = y[..., perm].contiguous().to(DEV)
+    nd = nrm.to(DEV)
+    ob_h, rb_h = N.HostFloats(oc.boundaries_host), N.HostFloats(rc.boundaries_host)
+    N.check(N.lib().qkv_store_append_kmixed_rotated(
+        ys.data_ptr(), nd.data_ptr(), B * H, S, 128, n_out, ob_h.ptr, rb_h.ptr,
+        st.kst.data_ptr(), st.knorm.data_ptr(), st.capacity, 0, N.stream(torch.device(DEV))))
+    kc = st.read_codes(0, S)[0].cpu()
+    mask = torch.zeros(128, dtype=torch.bool)
+    mask[out_idx] = True
+    ref = torch.empty(B, H, S, 128, dtype=torch.uint8)
+    ref[..., mask] = R.quantize_boundary(y[..., mask], oc.boundaries.cpu()).to(torch.uint8)
+    ref[..., ~mask] = R.quantize_boundary(y[..., ~mask], rc.boundaries.cpu()).to(torch.uint8)
+    assert torch.equal(kc, ref)
+    assert torch.equal(st.knorm[:, :, :S].cpu(), nrm)
+
+
+def test_store_append_cfg3_size_vs_oracle():
+    """The fused append from bf16 x at the full cfg3 shape (B=32, 8 kv heads,
+    8192 tokens, d=128, 3-bit keys with 4 outlier channels x10, 3-bit values):
+    codes against the oracle's compress_ip / compress_mse of the same inputs,
+    mismatch rate <= 1e-4 per stream, every mismatch one code step."""
+    B, H, T, d = 32, 8, 8192, 128
+    g = torch.Generator(device=DEV).manual_seed(2)
+    k = torch.randn(B, H, T, d, device=DEV, generator=g)
+    k[..., [11, 47, 83, 119]] *= 10.0
+    k = k.to(torch.bfloat16)
+    v = torch.randn(B, H, T, d, device=DEV, generator=g).to(torch.bfloat16)
+    eng = Q.QuashKVEngine(head_dim=d, key_bits=3, value_bits=3, seed=42, device=DEV, capacity=T)
+    eng.append(k, v)
+    st = eng._store
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    mq = kq.mse_quantizer
+    tabs = (mq.Pi.cpu(), mq.codebook.boundaries.cpu(), kq.S.cpu(), mq.codebook.centroids.cpu())
+    bad = [0, 0, 0]
+    total = 0
+    for b0 in range(0, B, 4):
+        kc, kb, vc = (t[b0:b0 + 4].cpu() for t in st.read_codes(0, T))
+        okc, okb, _ = R.compress_ip(k[b0:b0 + 4].cpu().float(), *tabs)
+        ovc, _ = R.compress_mse(v[b0:b0 + 4].cpu().float(), vq.Pi.cpu(),
+                                vq.codebook.boundaries.cpu())
+        for i, (a, r) in enumerate(((kc, okc), (kb, okb), (vc, ovc))):
+            diff = (a.to(torch.int16) - r.to(torch.int16)).abs()
+            assert int(diff.max()) <= 1
+            bad[i] += int((diff != 0).sum())
+        total += kc.numel()
+    rates = [x / total for x in bad]
+    print("cfg3 code mismatch rates (mse, qjl, value):", rates)
+    assert max(rates) <= 1e-4, rates
