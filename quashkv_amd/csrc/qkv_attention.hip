@@ -430,6 +430,14 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Max over each aligned group of 8 lanes, in every lane of the group
+// (quad_perm swaps of neighbours and pairs, then the half-row mirror).
+__device__ __forceinline__ float max8_dpp(float v) {
+  v = dpp_max<0xb1>(v);
+  v = dpp_max<0x4e>(v);
+  return dpp_max<0x141>(v);
+}
+
 template <int D, int NPL>
 __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dtype,
                                                     float alpha, int Hq, int Hkv, int Q, int R,
@@ -1017,8 +1025,11 @@ constexpr int kVSplitF = 6;               // value tiles before the mid-chunk ba
 struct ChunkStats {
   float pmax[kWavesKF][4];   // [key wave][row] score maxima (log2 units)
   float pvmax[kWavesKF];     // [key wave] value norm maxima
-  float plsum[kWavesKF][4];  // [key wave][row] sums of p
+  float scale[4];            // [row] 2^(m_prev - m_new): the running sums' rescale
+  int fv;                    // the value digits' fixed-point exponent
+  int pad[3];
 };
+constexpr float kMFloor = -1e30f;  // running maxima start here (finite: no inf - inf)
 
 // Dynamic LDS of decode_fused (byte offsets).  The prologue's and the
 // epilogue's scratch rows overlay the chunk buffers.
@@ -1030,7 +1041,8 @@ struct FusedLds {
   static constexpr int STATS = BUF + 2 * kTilesF * 1024;
   static constexpr int ROWC = STATS + 2 * int(sizeof(ChunkStats));  // [4][2] row constants
   static constexpr int RED = ROWC + 32;                 // [8] norms, [8][2] row sums
-  static constexpr int TOTAL = RED + 128;
+  static constexpr int LRED = RED + 128;                // [8 key waves][4 rows] sums of p
+  static constexpr int TOTAL = LRED + 128;
   static_assert(BUF % 16 == 0 && STATS % 16 == 0, "alignment");
 };
 
@@ -1187,11 +1199,29 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
   const uint32_t koff = ln * KRB + lg * DPL * 4;       // bytes into a tile's K rows
   const uint32_t voff = blk * VB * D + vj;             // words into a tile's V planes
+  // contiguous store: the split's bases, a tile as a 32-bit row offset from them
+  const uint8_t* kbase = kst + srow0 * KRB;
+  const float* knbase = knorm + srow0;
+  const float* vnbase = vnorm + srow0;
+  const uint32_t* vbase = vst + (srow0 >> 5) * (VB * D);  // srow0 is a multiple of 64
+  auto trow = [&](int tile) -> uint32_t {
+    return ntiles > 0 ? static_cast<uint32_t>(min(tile, ntiles - 1)) * 64u : 0u;
+  };
   auto loadK = [&](int tile) {
-    const int64_t rb = tile_row(tile);
-    const uint8_t* kb = kst + rb * KRB;
-    const float* knb = knorm + rb;
-    const float* vnb = vnorm + rb;
+    const uint8_t* kb;
+    const float* knb;
+    const float* vnb;
+    if constexpr (PAGED) {
+      const int64_t rb = tile_row(tile);
+      kb = kst + rb * KRB;
+      knb = knorm + rb;
+      vnb = vnorm + rb;
+    } else {
+      const uint32_t r = trow(tile);
+      kb = kbase + r * KRB;
+      knb = knbase + r;
+      vnb = vnbase + r;
+    }
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + koff + sub * 16 * KRB);
@@ -1202,7 +1232,11 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     vnr = ldnt(vnb + lane);
   };
   auto loadV = [&](int slot, int tile) {
-    const uint32_t* vb = vst + (tile_row(tile) >> 5) * (VB * D);  // the tile's first V tile
+    const uint32_t* vb;  // the tile's first V tile
+    if constexpr (PAGED)
+      vb = vst + (tile_row(tile) >> 5) * (VB * D);
+    else
+      vb = vbase + (trow(tile) >> 5) * (VB * D);
 #pragma unroll
     for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * D);
   };
@@ -1306,7 +1340,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   lds_sync();
 
   const float scale2 = scale * 1.4426950408889634f;  // scores in log2 units
-  float orun = 0.f, lrun = 0.f, mrun = -INFINITY;     // value waves: row lg, coordinate vj
+  float* lred = reinterpret_cast<float*>(lds + FusedLds::LRED);  // [key wave][row] sums of p
+  float orun = 0.f;  // value waves: row lg, coordinate vj, relative to the running maximum
 
   if (keyw) {
     // ------------------------------------------------ key waves: tile wi of each chunk
@@ -1336,117 +1371,140 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     // Z_t s_t = X 2^i with X = round(p' 2^(Fv - i)); the byte of bit 7 is -128,
     // so those lanes store -X: sign and rounding offset fold into constants
     const float sgn7 = ii == 7 ? -1.f : 1.f;
-    float vhold = 0.f;
-    for (int c = 0; c <= nch; ++c) {
+    // the chunk's maxima, one per lane: (key wave l & 7, row l >> 3) for lanes
+    // 0..31, the value-norm maximum of key wave l & 7 for lanes 32..
+    const int sidx = lane < 32 ? (lane & 7) * kRowsM + (lane >> 3) : kWavesKF * kRowsM + (lane & 7);
+    // running row maxima (log2 units, floored so that a row without a visible
+    // token yet gives p = 0 rather than NaN) and this lane's running sums of p
+    float mk[kRowsM], lacc[kRowsM];
+#pragma unroll
+    for (int r = 0; r < kRowsM; ++r) {
+      mk[r] = kMFloor;
+      lacc[r] = 0.f;
+    }
+    for (int c = 0; c < nch; ++c) {
       uint8_t* cbuf = bufs + (c & 1) * kTilesF * 1024;
       ChunkStats& cs = stats[c & 1];
       const int tile = c * kTilesF + wi;
-      const bool have = c < nch && tile < ntiles;
-      // ---- stage 1: scores of tile wi of chunk c (the slot's refill is issued on
-      // every step, so the load count per step is fixed)
-      float mloc = -INFINITY, vloc = 0.f;
+      // ---- stage 1: scores of tile wi of chunk c.  A tile past the split's
+      // last (only in the last chunk) runs on the re-read last tile and is
+      // masked out whole: its scores are -inf, so its p and value digits are 0.
       qkv_v4i acc[4];
-      float knt[4], vz = 0.f;
-      if (have) {
 #pragma unroll
-        for (int sub = 0; sub < 4; ++sub) acc[sub] = qkv_v4i{0, 0, 0, 0};
-#pragma unroll
-        for (int u = 0; u < NU; ++u) {
-          const int sh = 4 * (u & 1);
-#pragma unroll
-          for (int sub = 0; sub < 4; ++sub) {
-            const uint32_t x = kd[sub][u >> 1];
-            qkv_v4i bo;
-            bo[0] = static_cast<int>(x & (0x01010101u << sh));
-            bo[1] = static_cast<int>(x & (0x02020202u << sh));
-            bo[2] = static_cast<int>(x & (0x04040404u << sh));
-            bo[3] = static_cast<int>(x & (0x08080808u << sh));
-            acc[sub] = mfma_i8(a[u], bo, acc[sub]);
-          }
-        }
-#pragma unroll
-        for (int sub = 0; sub < 4; ++sub) knt[sub] = kn[sub];
-        vz = vnr;
-      }
-      loadK(tile + kTilesF);  // the slot is free: refill it
-      if (have) {
-        mfma_settle();
-        const int tbase = tile * 64;
-        const bool pok = page_ok(tile);
-        const bool full = pok && tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
-        float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
+      for (int u = 0; u < NU; ++u) {
+        const int sh = 4 * (u & 1);
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-          const int lo = __mul24(acc[sub][1], 256) + acc[sub][0];
-          const int hi = __mul24(acc[sub][3], 256) + acc[sub][2];
-          const float z = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
-          float sc = knt[sub] * fmaf(z, fq2, cr2);
-          if (!full) {
-            const int tl = tbase + sub * 16 + ln;
-            sc = (pok && tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
-          }
-          srow[sub * 16 + ln] = sc;
-          mloc = fmaxf(mloc, sc);
+          const uint32_t x = kd[sub][u >> 1];
+          qkv_v4i bo;
+          bo[0] = static_cast<int>(x & (0x01010101u << sh));
+          bo[1] = static_cast<int>(x & (0x02020202u << sh));
+          bo[2] = static_cast<int>(x & (0x04040404u << sh));
+          bo[3] = static_cast<int>(x & (0x08080808u << sh));
+          acc[sub] = mfma_i8(a[u], bo, u == 0 ? qkv_v4i{0, 0, 0, 0} : acc[sub]);
         }
-        if (!full) vz = (pok && tbase + lane < ntok) ? vz : 0.f;
-        vhold = vz;
-        vloc = vz;
       }
+      float knt[4];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) knt[sub] = kn[sub];
+      float vz = vnr;
+      loadK(tile + kTilesF);  // the slot is free: refill it
+      mfma_settle();
+      const int tbase = tile * 64;
+      const bool pok = page_ok(tile);
+      const bool full = pok && tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
+      float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int lo = __mul24(acc[sub][1], 256) + acc[sub][0];
+        const int hi = __mul24(acc[sub][3], 256) + acc[sub][2];
+        const float z = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
+        float sc = knt[sub] * fmaf(z, fq2, cr2);
+        if (!full) {
+          const int tl = tbase + sub * 16 + ln;
+          sc = (pok && tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
+        }
+        srow[sub * 16 + ln] = sc;
+        mloc = fmaxf(mloc, sc);
+      }
+      if (!full) vz = (pok && tbase + lane < ntok) ? vz : 0.f;
       mloc = row_max_last(mloc);  // the 16 lanes of row lg: max in lane 15
-      vloc = wave_max_dpp(vloc);
+      const float vloc = wave_max_dpp(vz);
       if (ln == 15) cs.pmax[wi][lg] = mloc;
       if (lane == 0) cs.pvmax[wi] = vloc;
       lds_sync();
-      // ---- stage 2: p = 2^(s - m), value digits in place
-      if (have) {
-        float mrow[kRowsM];
+      // ---- stage 2: new running maxima; p = 2^(s - m), value digits in place
+      const float t = max8_dpp(reinterpret_cast<const float*>(&cs)[sidx]);
+      float mrow[kRowsM];
 #pragma unroll
-        for (int r = 0; r < kRowsM; ++r) {
-          float m = cs.pmax[0][r];
+      for (int r = 0; r < kRowsM; ++r) {
+        const float Mc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 8 * r));
+        mrow[r] = fmaxf(mk[r], Mc);
+        const float rs = __builtin_amdgcn_exp2f(mk[r] - mrow[r]);  // 2^(m_prev - m_new)
+        lacc[r] *= rs;
+        mk[r] = mrow[r];
+        if (wi == 0 && lane == 0) cs.scale[r] = rs;
+      }
+      const float vmx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t), 32));
+      int ev = 0;
+      if (vmx > 0.f) frexpf(vmx, &ev);
+      const int Fv = vmx > 0.f ? 29 - ev : 0;  // vmx 2^Fv < 2^29
+      if (wi == 0 && lane == 0) cs.fv = Fv;
+      const float vzs = vz * ldexpf(sgn7, Fv - ii);
+      const float hz = 0.5f * sgn7;
+      uint8_t* tb8 = cbuf + wi * 1024;
 #pragma unroll
-          for (int w = 1; w < kWavesKF; ++w) m = fmaxf(m, cs.pmax[w][r]);
-          mrow[r] = (r < nr && m > -INFINITY) ? m : INFINITY;  // absent row: every p = 0
-        }
-        float vmx = cs.pvmax[0];
-#pragma unroll
-        for (int w = 1; w < kWavesKF; ++w) vmx = fmaxf(vmx, cs.pvmax[w]);
-        int ev = 0;
-        if (vmx > 0.f) frexpf(vmx, &ev);
-        const int Fv = vmx > 0.f ? 29 - ev : 0;  // vmx 2^Fv < 2^29
-        const float vzs = vhold * ldexpf(sgn7, Fv - ii);
-        const float hz = 0.5f * sgn7;
-        uint8_t* tb8 = cbuf + wi * 1024;
-#pragma unroll
-        for (int r = 0; r < kRowsM; ++r) {
-          const float s = reinterpret_cast<const float*>(tb8 + r * 256)[lane];
-          const float p = __builtin_amdgcn_exp2f(s - mrow[r]);
-          const int Z = static_cast<int>(fmaf(p, vzs, hz));
-          // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
-          const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
-          uint8_t* dst = tb8 + (4 * r) * 64 + kpos;
-          dst[0] = static_cast<uint8_t>(dg);
-          dst[64] = static_cast<uint8_t>(dg >> 8);
-          dst[128] = static_cast<uint8_t>(dg >> 16);
-          dst[192] = static_cast<uint8_t>(dg >> 24);
-          const float l = wave_sum_dpp(p);
-          if (lane == 0) cs.plsum[wi][r] = l;
-        }
-      } else if (c < nch && lane < kRowsM) {
-        cs.plsum[wi][lane] = 0.f;
+      for (int r = 0; r < kRowsM; ++r) {
+        const float s = reinterpret_cast<const float*>(tb8 + r * 256)[lane];
+        const float p = __builtin_amdgcn_exp2f(s - mrow[r]);
+        lacc[r] += p;
+        const int Z = static_cast<int>(fmaf(p, vzs, hz));
+        // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
+        const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+        const uint32_t dg8 = dg >> 8;
+        uint8_t* dst = tb8 + (4 * r) * 64 + kpos;
+        dst[0] = static_cast<uint8_t>(dg);
+        dst[64] = static_cast<uint8_t>(dg8);
+        dst[128] = static_cast<uint8_t>(dg >> 16);
+        dst[192] = static_cast<uint8_t>(dg8 >> 16);
       }
       lds_sync();
+    }
+    // the step in which the value waves take the last chunk
+    lds_sync();
+    lds_sync();
+    // the key waves' sums of p meet in LDS (read after the next barrier)
+#pragma unroll
+    for (int r = 0; r < kRowsM; ++r) {
+      const float l = wave_sum_dpp(lacc[r]);
+      if (lane == 0) lred[wi * kRowsM + r] = l;
+    }
+    if (!(final_out && gridDim.x == 1)) {
+      lds_sync();
+      if (wi == 0 && lane < nr) {  // split partials: (m, l) of row `lane`
+        float l = lred[lane];
+#pragma unroll
+        for (int w = 1; w < kWavesKF; ++w) l += lred[w * kRowsM + lane];
+        const float m = lane == 0 ? mk[0] : lane == 1 ? mk[1] : lane == 2 ? mk[2] : mk[3];
+        const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
+        part_ml[(base + lane) * 2 + 0] = m * 0.6931471805599453f;  // log2 -> natural units
+        part_ml[(base + lane) * 2 + 1] = l;
+      }
     }
   } else {
     // ------------------------------------------------ value waves: coordinates 16 wi ..
     qkv_v4i acc[NP], accU;
-#pragma unroll
-    for (int s = 0; s < NP; ++s) acc[s] = qkv_v4i{0, 0, 0, 0};
-    accU = qkv_v4i{0, 0, 0, 0};
     qkv_v4i ones;  // an all-ones plane as the operand's bytes (b * 2^i, i = bit in byte)
 #pragma unroll
     for (int e = 0; e < 4; ++e) ones[e] = static_cast<int>(0x01010101u << (e + hsh));
-    auto pv = [&](int slot, const uint8_t* tbase) {
-      const qkv_v4i bq = *reinterpret_cast<const qkv_v4i*>(tbase + ln * 64 + lg * 16);
+    // the digit operand of tile t of a chunk buffer
+    auto ldbq = [&](const uint8_t* vbuf, int t) {
+      return *reinterpret_cast<const qkv_v4i*>(vbuf + t * 1024 + ln * 64 + lg * 16);
+    };
+    // the first tile of a chunk starts the accumulators from zero
+    auto pv = [&](int slot, qkv_v4i bq, bool first) {
+      const qkv_v4i zero = qkv_v4i{0, 0, 0, 0};
 #pragma unroll
       for (int s = 0; s < NP; ++s) {
         const uint32_t sub = odd_subset(VB, s);
@@ -1459,69 +1517,66 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         av[1] = static_cast<int>(pw & (0x02020202u << hsh));
         av[2] = static_cast<int>(pw & (0x04040404u << hsh));
         av[3] = static_cast<int>(pw & (0x08080808u << hsh));
-        acc[s] = mfma_i8(bq, av, acc[s]);  // C[row x digit][coordinate]
+        acc[s] = mfma_i8(bq, av, first ? zero : acc[s]);  // C[row x digit][coordinate]
       }
-      accU = mfma_i8(bq, ones, accU);
+      accU = mfma_i8(bq, ones, first ? zero : accU);
     };
-    for (int c = 0; c <= nch; ++c) {
+    // step 0: the ring holds chunk 0; nothing to accumulate yet
+    lds_sync();
+    lds_sync();
+    for (int c = 1; c <= nch; ++c) {
       const int cv = c - 1;  // the chunk this stage accumulates
       const uint8_t* vbuf = bufs + (cv & 1) * kTilesF * 1024;
-      // slot t is refilled on every step (at step 0 with the tile it holds),
-      // so the load count per step is fixed
+      // slot t is refilled with tile t of the next chunk once consumed; tiles
+      // past the split's last are zero digits over re-read planes.  The digit
+      // operands are read one tile ahead (the buffer was completed in the
+      // previous step).
+      qkv_v4i bqn = ldbq(vbuf, 0);
 #pragma unroll
       for (int t = 0; t < kVSplitF; ++t) {
-        const int tile = cv * kTilesF + t;
-        if (cv >= 0 && tile < ntiles) pv(t, vbuf + t * 1024);
-        loadV(t, tile + kTilesF);
+        // one tile at a time: operations of later tiles hoisted above would wait
+        // on the in-order load counter for every load in flight
+        __builtin_amdgcn_sched_barrier(0);
+        const qkv_v4i bq = bqn;
+        bqn = ldbq(vbuf, t + 1);
+        pv(t, bq, t == 0);
+        loadV(t, (cv + 1) * kTilesF + t);
       }
       lds_sync();
 #pragma unroll
       for (int t = kVSplitF; t < kTilesF; ++t) {
-        const int tile = cv * kTilesF + t;
-        if (cv >= 0 && tile < ntiles) pv(t, vbuf + t * 1024);
-        loadV(t, tile + kTilesF);
+        __builtin_amdgcn_sched_barrier(0);
+        const qkv_v4i bq = bqn;
+        if (t + 1 < kTilesF) bqn = ldbq(vbuf, t + 1);
+        pv(t, bq, false);
+        loadV(t, (cv + 1) * kTilesF + t);
       }
-      if (cv >= 0) {
-        // chunk cv: digits + planes -> fp32, merged into the running (m, l, O~).
-        // 2 Y_S - U per digit in exact int32 (|acc| < 2^21 for a 512-token
-        // chunk), then sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U).
+      {
+        // chunk cv into the running O~: sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U)
+        // per digit half in exact int32 (|acc| < 2^21 for a 512-token chunk),
+        // then fp32; O~ = O~ 2^(m_prev - m_new) + sum_S g_S (...)
         mfma_settle();
         const ChunkStats& cs = stats[cv & 1];
-        const int row = lg;
-        float M = cs.pmax[0][row], lc = cs.plsum[0][row], vmx = cs.pvmax[0];
-#pragma unroll
-        for (int w = 1; w < kWavesKF; ++w) {
-          M = fmaxf(M, cs.pmax[w][row]);
-          lc += cs.plsum[w][row];
-          vmx = fmaxf(vmx, cs.pvmax[w]);
-        }
-        int ev = 0;
-        if (vmx > 0.f) frexpf(vmx, &ev);
-        const int Fv = vmx > 0.f ? 29 - ev : 0;
+        const float rs = cs.scale[lg];
+        const int Fv = cs.fv;
+        const int nulo = -(__mul24(accU[1], 256) + accU[0]);
+        const int nuhi = -(__mul24(accU[3], 256) + accU[2]);
         float val = 0.f;
 #pragma unroll
         for (int s = 0; s < NP; ++s) {
-          int tv[4];
-#pragma unroll
-          for (int v = 0; v < 4; ++v) tv[v] = 2 * acc[s][v] - accU[v];
-          const int lo = __mul24(tv[1], 256) + tv[0];
-          const int hi = __mul24(tv[3], 256) + tv[2];
+          const int lo = 2 * (__mul24(acc[s][1], 256) + acc[s][0]) + nulo;
+          const int hi = 2 * (__mul24(acc[s][3], 256) + acc[s][2]) + nuhi;
           const float y = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
           val = fmaf(tb.vg[s], y, val);
-          acc[s] = qkv_v4i{0, 0, 0, 0};
         }
-        accU = qkv_v4i{0, 0, 0, 0};
-        const float oc = ldexpf(val, -Fv);
-        if (row < nr && M > -INFINITY) {
-          const float mn = fmaxf(mrun, M);
-          const float fa = mrun > -INFINITY ? __builtin_amdgcn_exp2f(mrun - mn) : 0.f;
-          const float fb = __builtin_amdgcn_exp2f(M - mn);
-          orun = fmaf(orun, fa, oc * fb);
-          lrun = fmaf(lrun, fa, lc * fb);
-          mrun = mn;
-        }
+        orun = fmaf(orun, rs, ldexpf(val, -Fv));
       }
       lds_sync();
+    }
+    if (!(final_out && gridDim.x == 1)) {
+      lds_sync();
+      const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
+      if (lg < nr) part_o[(base + lg) * D + vj] = orun;
     }
   }
 
@@ -1530,7 +1585,13 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     // out = (O~ / max(l, 1e-8)) Pi_v, rows r0 .. r0 + nr - 1
     float* obuf = reinterpret_cast<float*>(bufs);            // [4][D]
     float* opart = reinterpret_cast<float*>(bufs + 2048);    // [4 k parts][4 rows][D]
-    if (!keyw) obuf[lg * D + vj] = lg < nr ? orun / fmaxf(lrun, 1e-8f) : 0.f;
+    lds_sync();  // the key waves' sums of p
+    if (!keyw) {
+      float l = lred[lg];
+#pragma unroll
+      for (int w = 1; w < kWavesKF; ++w) l += lred[w * kRowsM + lg];
+      obuf[lg * D + vj] = lg < nr ? orun / fmaxf(l, 1e-8f) : 0.f;
+    }
     const float* piv = ol.pi[layer];
     if (!pro || piv != ql.pi[layer]) {  // values un-rotate by their own Pi
       const float4* src = reinterpret_cast<const float4*>(piv);
@@ -1565,15 +1626,6 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         const int g = row / Q, qi = row - g * Q;
         const int h = hkv * G + g;
         qkv_store(ol.out[layer], ((int64_t(b) * Hq + h) * Q + qi) * D + j, o, out_dtype);
-      }
-    }
-  } else if (!keyw) {
-    const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
-    if (lg < nr) {
-      part_o[(base + lg) * D + vj] = orun;
-      if (wi == 0 && ln == 0) {
-        part_ml[(base + lg) * 2 + 0] = mrun * 0.6931471805599453f;  // log2 -> natural units
-        part_ml[(base + lg) * 2 + 1] = lrun;
       }
     }
   }
