@@ -42,6 +42,8 @@
 #include "qkv_common.h"
 
 typedef int qkv_v4i __attribute__((ext_vector_type(4)));
+typedef int qkv_v8i __attribute__((ext_vector_type(8)));
+typedef float qkv_v4f __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -438,7 +440,86 @@ __device__ __forceinline__ float max8_dpp(float v) {
   return dpp_max<0x141>(v);
 }
 
-template <int D, int NPL>
+// ---- fp4 key operands of the fused d = 128 decode
+//
+// The score MFMA there is v_mfma_scale_f32_16x16x128_f8f6f4 with A = the
+// query weights as fp8 (e4m3) digits and B = the K-row bits as fp4 (e2m1)
+// values, four bit-to-operand operations per 32 bits against eight for int8
+// bytes.  B: lane group g of a 16-token MFMA u takes K-row dword
+// w = g DPL + u and spreads its 32 bits over 32 fp4 elements by bit class
+// c = bit & 3: element 8 c + (bit >> 2) holds bit * {0.5, 1, 2}[c] for c < 3
+// (masks 0x11111111 << c) and 0.5 (1 - 2 bit) for c = 3
+// ((x & 0x88888888) | 0x11111111).  A row 4 r + d holds digit d of query row
+// r's weights W scaled by the class ({2, 1, 0.5, -1}; class 3 leaves W / 2 in
+// the row constant), as fp8 values q_d with
+//   W' 2^-sigma ~= q_0 + q_1 / 16 + q_2 / 256 + q_3 / 4096,
+// q_d the round-to-nearest fp8 of the remaining residual times 16^d, and the
+// MFMA's per-row E8M0 scale 2^(sigma - 4 d); |W'| 2^-sigma <= 224 keeps every
+// digit inside the fp8 range.  A's K order: lane group ga, byte ea <->
+// k = 16 ga + (ea & 15) + 64 (ea >> 4); B's: lane group gb, element eb <->
+// k = 32 gb + eb.
+//
+// The value side stays on the exact int8 MFMA: the f8f6f4 MFMA sums its
+// products with an error near 2^-10 of the largest one when the fp8 operands
+// span many binades, which the key weights (bounded by the rotation) absorb
+// within the score tolerance but the softmax-weighted value digits p |v| of a
+// peaked distribution do not.
+
+// A constant held in a VGPR: (x & c1) | c2 with c1, c2 in VGPRs is one
+// v_bitop3, where two literal operands would take two instructions.
+__device__ __forceinline__ uint32_t vgpr_u32(uint32_t x) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
+  return r;
+}
+
+// Four fp8 (e4m3) digits of x, |x| <= 224: digit d in byte d.
+__device__ __forceinline__ uint32_t fp8_digits(float x) {
+  uint32_t out = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int p = __builtin_amdgcn_cvt_pk_fp8_f32(x, 0.f, 0, false);
+    out |= static_cast<uint32_t>(p & 0xff) << (8 * d);
+    x = (x - __builtin_amdgcn_cvt_f32_fp8(p, 0)) * 16.f;
+  }
+  return out;
+}
+
+// Byte of the A-operand image (DPL MFMAs x 64 lanes x 32 bytes) holding row
+// bit p (dword p >> 5, bit p & 31) for A row m.
+template <int DPL>
+__device__ __forceinline__ int kf4_byte(int p, int m) {
+  const int w = p >> 5, bit = p & 31;
+  const int u = w % DPL, gb = w / DPL;
+  const int k = 32 * gb + 8 * (bit & 3) + (bit >> 2);
+  const int ga = (k & 63) >> 4, ea = (k & 15) + 16 * (k >> 6);
+  return (u * 64 + m + 16 * ga) * 32 + ea;
+}
+
+// Class factor of row bit p.
+__device__ __forceinline__ float kf4_factor(int p) {
+  const int c = p & 3;
+  return c == 0 ? 2.f : c == 1 ? 1.f : c == 2 ? 0.5f : -1.f;
+}
+
+// The row's exponent sigma from the bound wmax >= max |W|: 2 wmax 2^-sigma <= 224.
+__device__ __forceinline__ int kf4_sigma(float wmax) {
+  int e = 0;
+  if (wmax > 0.f) frexpf(wmax * (2.f / 224.f), &e);
+  return e;
+}
+
+// The digit bytes of weight W at row bit p of query row r into the image sb;
+// returns W's share of the row constant.
+template <int DPL>
+__device__ __forceinline__ float kf4_put(uint8_t* sb, int p, float W, int sigma, int r) {
+  const uint32_t dg = fp8_digits(ldexpf(W * kf4_factor(p), -sigma));
+#pragma unroll
+  for (int d = 0; d < 4; ++d) sb[kf4_byte<DPL>(p, 4 * r + d)] = static_cast<uint8_t>(dg >> (8 * d));
+  return (p & 3) == 3 ? 0.5f * W : 0.f;
+}
+
+template <int D, int NPL, bool FP4>
 __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dtype,
                                                     float alpha, int Hq, int Hkv, int Q, int R,
                                                     int chunks, Tables tb,
@@ -457,11 +538,12 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
   static_assert(D == 128 || D == 64, "64- or 128-dim rows");
   static_assert(D == 64 || KRB % 16 == 0, "128-dim rows split into 4 lane groups");
   static_assert(kRowsM == 4, "rows per chunk");
+  static_assert(!FP4 || (D == 128 && NPL <= 3), "fp4 operands: the fused d = 128 decode");
   __shared__ float qs[kRowsM][D];
   __shared__ float part[NPART][kRowsM][D];
   __shared__ float nqs[kRowsM];
   __shared__ uint32_t stage[NW];
-  __shared__ float red[4][RPT][2];  // [wave][row slot][sq, sw]
+  __shared__ float red[4][RPT][3];  // [wave][row slot][sq, sw, fp4 halves]
 
   const int tid = threadIdx.x;
   const int G = Hq / Hkv;
@@ -553,7 +635,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
 
   uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
   // digit bytes of weight W at row bit p of row r
-  auto put = [&](int p, float W, int fq, int r) {
+  auto put8 = [&](int p, float W, int fq, int r) {
     const int i = p & 7;
     int Z = static_cast<int>(rintf(ldexpf(W, fq - i)));
     if (i == 7) Z = -Z;
@@ -571,10 +653,11 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
 #pragma unroll
     for (int v = 0; v < 4; ++v) sb[base + 16 * v] = static_cast<uint8_t>(dg >> (8 * v));
   };
-  float csq[RPT], csw[RPT];
+  float csq[RPT], csw[RPT], chf[RPT];
 #pragma unroll
   for (int rr = 0; rr < RPT; ++rr) {
     const int r = half + NPART * rr;
+    float hf = 0.f;
     float v = 0.f;
 #pragma unroll
     for (int pp = 0; pp < NPART; ++pp) v += part[pp][r][j];
@@ -587,7 +670,14 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     const float wmax = 2.f * kgmax * sqrtf(nqs[r]);
     int ex = 0;
     if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
-    const int fq = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
+    // int8 digits: the fixed-point exponent (|Z| < 2^30); fp4: the row's sigma
+    const int fq = FP4 ? kf4_sigma(wmax) : wmax > 0.f ? 30 - ex : 0;
+    auto put = [&](int pb, float W, int fqv, int rv) {
+      if constexpr (FP4)
+        hf += kf4_put<DPL>(sb, pb, W, fqv, rv);
+      else
+        put8(pb, W, fqv, rv);
+    };
     if (D == 128 && tb.kmix) {
       const bool outl = j < tb.n_out;
       csq[rr] = (outl ? tb.kco : tb.kcr) * v;
@@ -604,6 +694,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
       put(MB * D + j, 2.f * w, fq, r);
     }
     csw[rr] = w;
+    chf[rr] = hf;
   }
   {  // row constants: sums over j (a wave holds 64 j of one part)
     const int wave = tid >> 6, lane = tid & 63;
@@ -611,9 +702,11 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     for (int rr = 0; rr < RPT; ++rr) {
       const float a = wave_sum_dpp(csq[rr]);
       const float c = wave_sum_dpp(csw[rr]);
+      const float h = FP4 ? wave_sum_dpp(chf[rr]) : 0.f;
       if (lane == 0) {
         red[wave][rr][0] = a;
         red[wave][rr][1] = c;
+        red[wave][rr][2] = h;
       }
     }
   }
@@ -623,29 +716,32 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
   for (int x = 0; x < NW / 256; ++x) aqw[tid + 256 * x] = stage[tid + 256 * x];
   if (tid < kRowsM) {  // row r = tid: part r % NPART (waves WPP h ..), slot r / NPART
     const int r = tid, h = r % NPART, rr = r / NPART;
-    float sq = 0.f, sw = 0.f;
+    float sq = 0.f, sw = 0.f, sh = 0.f;
 #pragma unroll
     for (int w = 0; w < WPP; ++w) {
       sq += red[WPP * h + w][rr][0];
       sw += red[WPP * h + w][rr][1];
+      sh += red[WPP * h + w][rr][2];
     }
     const float wmax = 2.f * kgmax * sqrtf(nqs[r]);
     int ex = 0;
     if (wmax > 0.f) frexpf(wmax, &ex);
     const int fq = wmax > 0.f ? 30 - ex : 0;
-    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
-    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 1] = ldexpf(1.f, -fq);
+    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = (tb.kmix ? sq - sw : tb.kconst * sq - sw) + sh;
+    // fp4: the row's sigma (an integer, as a float); int8: 2^-Fq
+    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 1] =
+        FP4 ? static_cast<float>(kf4_sigma(wmax)) : ldexpf(1.f, -fq);
   }
 }
 
 // Dynamic LDS of prepare_mfma<D, NPL> (the padded Pi), raising the kernel's
 // limit past 64 KiB once where needed.
-template <int D, int NPL>
+template <int D, int NPL, bool FP4>
 uint32_t prep_lds() {
   constexpr uint32_t bytes = D * (D + 4) * 4;
   if constexpr (bytes > 65536) {
     static const bool raised = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&prepare_mfma<D, NPL>),
+        reinterpret_cast<const void*>(&prepare_mfma<D, NPL, FP4>),
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)) == hipSuccess;
     (void)raised;
   }
@@ -1074,7 +1170,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   constexpr int NPL = MB + 1;            // planes per K row (MSE + QJL)
   constexpr int KRB = NPL * D / 8;       // K row bytes
   constexpr int DPL = KRB / 16;          // row dwords per lane group
-  constexpr int NU = KRB / 8;            // score MFMAs per 16 tokens
+  constexpr int NU = KRB / 8;            // operand image: NU x 256 dwords (DPL fp4 MFMAs)
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int PR4 = FusedLds::PR4;
   constexpr int NT = kThreadsF;
@@ -1284,22 +1380,10 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       const float v = partb[(0 * kRowsM + r) * D + pj] + partb[(1 * kRowsM + r) * D + pj];
       const float w = alpha * fabsf(v) * sgns[pj];
       const float wmax = 2.f * kgmax * sqrtf(red[2 * r] + red[2 * r + 1]);
-      int ex = 0;
-      if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
-      const int fqe = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
+      const int sig = kf4_sigma(wmax);
       uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
-      auto put = [&](int p, float W) {
-        const int i = p & 7;
-        int Z = static_cast<int>(rintf(ldexpf(W, fqe - i)));
-        if (i == 7) Z = -Z;
-        const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
-        const int w32 = p >> 5, e = i & 3, beta = (p >> 3) & 3;
-        const int g = w32 / DPL;
-        const int u = 2 * (w32 - g * DPL) + (i >> 2);
-        const int base = ((u * 64 + 16 * g + 4 * r) * 4 + e) * 4 + beta;
-#pragma unroll
-        for (int vv = 0; vv < 4; ++vv) sb[base + 16 * vv] = static_cast<uint8_t>(dg >> (8 * vv));
-      };
+      float hf = 0.f;  // this coordinate's share of the row constant (bit class 3)
+      auto put = [&](int p, float W) { hf += kf4_put<DPL>(sb, p, W, sig, r); };
       float csq;
       if (tb.kmix) {
         const bool outl = pj < tb.n_out;
@@ -1319,22 +1403,22 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       // row constants: sums over j (row r = waves 2r, 2r + 1) into red[8 ..]
       const float a = wave_sum_dpp(csq);
       const float c = wave_sum_dpp(w);
+      const float h = wave_sum_dpp(hf);
       if (lane == 0) {
         red[8 + 2 * wave] = a;
         red[8 + 2 * wave + 1] = c;
+        red[24 + wave] = h;
       }
     }
     lds_sync();
-    if (tid < kRowsM) {  // row tid: score = kn 2^-fq (z + ...) in log2 units
+    if (tid < kRowsM) {  // row tid: score = kn (z + const) in log2 units
       const int rr = tid;
       const float sq = red[8 + 4 * rr] + red[8 + 4 * rr + 2];
       const float sw = red[8 + 4 * rr + 1] + red[8 + 4 * rr + 3];
+      const float sh = red[24 + 2 * rr] + red[24 + 2 * rr + 1];
       const float wm = 2.f * kgmax * sqrtf(red[2 * rr] + red[2 * rr + 1]);
-      int er = 0;
-      if (wm > 0.f) frexpf(wm, &er);
-      const int fr = wm > 0.f ? 30 - er : 0;
-      rowcs[2 * rr + 0] = tb.kmix ? sq - sw : tb.kconst * sq - sw;
-      rowcs[2 * rr + 1] = ldexpf(1.f, -fr);
+      rowcs[2 * rr + 0] = (tb.kmix ? sq - sw : tb.kconst * sq - sw) + sh;
+      rowcs[2 * rr + 1] = static_cast<float>(kf4_sigma(wm));  // the row's sigma
     }
   }
   lds_sync();
@@ -1345,10 +1429,14 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
 
   if (keyw) {
     // ------------------------------------------------ key waves: tile wi of each chunk
-    qkv_v4i a[NU];
+    const uint32_t k88 = vgpr_u32(0x88888888u), k11 = vgpr_u32(0x11111111u);
+    // fp8 digit operands of the score MFMAs, one per K-row dword of a lane group
+    qkv_v8i a[DPL];
 #pragma unroll
-    for (int u = 0; u < NU; ++u) a[u] = *reinterpret_cast<const qkv_v4i*>(stage + (u * 64 + lane) * 4);
-    const float cr2 = rowcs[2 * lg] * scale2, fq2 = rowcs[2 * lg + 1] * scale2;
+    for (int u = 0; u < DPL; ++u) a[u] = *reinterpret_cast<const qkv_v8i*>(stage + (u * 64 + lane) * 8);
+    const float cr2 = rowcs[2 * lg] * scale2;
+    // E8M0 scale of this lane's operand row ln = 4 r + d: 2^(sigma_r - 4 d)
+    const int asc = 127 + static_cast<int>(rowcs[2 * (ln >> 2) + 1]) - 4 * (ln & 3);
     const bool row_ok = lg < nr;
     // causal: split-relative token tl is visible to row lg iff tl <= clim
     const int qi = (r0 + lg) % Q;
@@ -1389,19 +1477,20 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       // ---- stage 1: scores of tile wi of chunk c.  A tile past the split's
       // last (only in the last chunk) runs on the re-read last tile and is
       // masked out whole: its scores are -inf, so its p and value digits are 0.
-      qkv_v4i acc[4];
+      qkv_v4f acc[4];
 #pragma unroll
-      for (int u = 0; u < NU; ++u) {
-        const int sh = 4 * (u & 1);
+      for (int u = 0; u < DPL; ++u) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-          const uint32_t x = kd[sub][u >> 1];
-          qkv_v4i bo;
-          bo[0] = static_cast<int>(x & (0x01010101u << sh));
-          bo[1] = static_cast<int>(x & (0x02020202u << sh));
-          bo[2] = static_cast<int>(x & (0x04040404u << sh));
-          bo[3] = static_cast<int>(x & (0x08080808u << sh));
-          acc[sub] = mfma_i8(a[u], bo, u == 0 ? qkv_v4i{0, 0, 0, 0} : acc[sub]);
+          const uint32_t x = kd[sub][u];
+          qkv_v8i bo;  // 32 fp4 elements (4 dwords) by bit class
+          bo[0] = static_cast<int>(x & 0x11111111u);
+          bo[1] = static_cast<int>(x & 0x22222222u);
+          bo[2] = static_cast<int>(x & 0x44444444u);
+          bo[3] = static_cast<int>((x & k88) | k11);
+          bo[4] = bo[5] = bo[6] = bo[7] = 0;
+          acc[sub] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+              a[u], bo, u == 0 ? qkv_v4f{0.f, 0.f, 0.f, 0.f} : acc[sub], 0, 4, 0, asc, 0, 127);
         }
       }
       float knt[4];
@@ -1417,10 +1506,9 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       float mloc = -INFINITY;
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) {
-        const int lo = __mul24(acc[sub][1], 256) + acc[sub][0];
-        const int hi = __mul24(acc[sub][3], 256) + acc[sub][2];
-        const float z = fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo));
-        float sc = knt[sub] * fmaf(z, fq2, cr2);
+        // the four digit rows of row lg, already scaled: z = sum of them
+        const float z = (acc[sub][0] + acc[sub][1]) + (acc[sub][2] + acc[sub][3]);
+        float sc = knt[sub] * fmaf(z, scale2, cr2);
         if (!full) {
           const int tl = tbase + sub * 16 + ln;
           sc = (pok && tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
@@ -2374,7 +2462,8 @@ int prepare_layers(const QLayers& ql, int nl, int32_t q_dtype, int32_t B, int32_
     const int chunks = (R + kRowsM - 1) / kRowsM;
     const dim3 grid(B * nl * Hkv * chunks);
 #define QKV_PREP(DD, NPLV)                                                                   \
-  hipLaunchKernelGGL((prepare_mfma<DD, NPLV>), grid, dim3(256), (prep_lds<DD, NPLV>()), s,  \
+  hipLaunchKernelGGL((prepare_mfma<DD, NPLV, DD == 128>), grid, dim3(256),                  \
+                     (prep_lds<DD, NPLV, DD == 128>()), s,                                  \
                      ql, B,                                                                 \
                      q_dtype,                                                               \
                      qjl_scale, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),    \
@@ -2453,8 +2542,8 @@ extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int3
   ql.q[0] = q;
   ql.pi[0] = pi_perm;
   ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
-  hipLaunchKernelGGL((prepare_mfma<128, 3>), dim3(B * Hkv * chunks), dim3(256),
-                     (prep_lds<128, 3>()), s, ql, B,
+  hipLaunchKernelGGL((prepare_mfma<128, 3, true>), dim3(B * Hkv * chunks), dim3(256),
+                     (prep_lds<128, 3, true>()), s, ql, B,
                      q_dtype, 0.f, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
                      at<float>(workspace, L.rowc), nullptr);
   QKV_LAUNCHED();
@@ -3132,8 +3221,8 @@ extern "C" int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, 
   ql.pi[0] = pisrc;
   ql.signs[0] = ssrc;
 #define QKV_PREP(NPLV)                                                                        \
-  hipLaunchKernelGGL((prepare_mfma<128, NPLV>), dim3(chunks), dim3(256),                     \
-                     (prep_lds<128, NPLV>()), s, ql, 1, qdt,                                \
+  hipLaunchKernelGGL((prepare_mfma<128, NPLV, false>), dim3(chunks), dim3(256),                     \
+                     (prep_lds<128, NPLV, false>()), s, ql, 1, qdt,                                \
                      qjl_scale, M, 1, 1, M, chunks, tb, aq, rowc, nullptr)
   if (mbits == 1) QKV_PREP(2);
   else if (mbits == 2) QKV_PREP(3);
