@@ -631,7 +631,7 @@ def sub_cfg4(args, dev, stream) -> dict:
 
     n_th = B4 * HKV4 * TT
     alg_bytes = n_th * (36 + 4 + 64 + 4)       # 2.25-bit K packed tight + 4-bit V + norms
-    read_bytes = n_th * (48 + 4 + 64 + 4)      # what the kmixed rows hold
+    read_bytes = n_th * (st.krb + 4 + 64 + 4)  # what the store holds (40-byte kmixed rows)
     gbs = alg_bytes / (dec_ms * 1e-3) / 1e9
     res = {
         "what": "long-context mixed precision: B 1, 32/8 heads, d 128, 131072 bf16 tokens in "

@@ -378,17 +378,23 @@ int qkv_decode_attention_layers(int32_t n_layers, const void* const* q, int32_t 
                                 void* stream);
 
 /* ------------------------------------------------------------------------
- * Mixed-precision keys in the store (MixedPrecisionMSEQuantizer with 3-bit
- * outlier and 2-bit regular channels, quashkv/mixed_precision.py:25-197).
- * The reference has no packed format or attention for these keys; it keeps
- * one uint8 per code (:132-158) and reconstructs keys with decompress
- * (:160-187).  Here keys live in "kmixed" rows of 48 bytes (d = 128) over
- * coordinates permuted outliers first -- slot j holds rotated channel
- * perm[j] -- as [plane b0][plane b1][plane 2], where plane 2 holds b2 of the
- * n_out outlier slots at bits 0.. and their parity b0^b1^b2 at bits 64..
+ * Mixed-precision keys in the store (quashkv/mixed_precision.py).  The
+ * reference has no packed format or attention for these keys; it keeps one
+ * uint8 per code and reconstructs keys with decompress (:160-187; the IP
+ * quantizer's :283-297 adds one uint8 QJL bit per coordinate).  Here keys
+ * live in rows of whole dwords (d = 128) over coordinates permuted outliers
+ * first -- slot j holds rotated channel perm[j]:
+ *   kmixed   MixedPrecisionMSEQuantizer (:25-197), 3-bit outlier / 2-bit
+ *            regular channels: [plane b0][plane b1][b2 of the n_out outlier
+ *            slots][their parity b0^b1^b2], 32 + n_out / 4 bytes (40 or 48);
+ *   kipmixed MixedPrecisionIPQuantizer (:200-322) with outlier_bits 3 /
+ *            regular_bits 2, i.e. a 2-bit outlier / 1-bit regular MSE stage
+ *            plus a QJL bit on every coordinate: [plane b0][QJL plane][b1 of
+ *            the outlier slots], 32 + n_out / 8 bytes (36 or 40).
  *   perm_host  HOST int32[128], a permutation with the n_out outlier
  *              channels (ascending) first, then the regular ones (ascending)
  *   pi_perm    device d x d fp32: row j = Pi row perm[j]
+ *   signs_perm device fp32[128]: S[perm[j]] (kipmixed)
  *   n_out      32 or 64 (else QKV_E_UNSUPPORTED)
  * ---------------------------------------------------------------------- */
 
@@ -400,6 +406,15 @@ int qkv_kmixed_pack(const uint8_t* codes, int64_t n, const int32_t* perm_host,
 int qkv_kmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
                       int32_t n_out, int64_t seq, int64_t group_stride, uint8_t* codes,
                       void* stream);
+/* The same for kipmixed rows: MSE codes and QJL bits (one uint8 each, n x 128,
+ * channel order), as MixedPrecisionIPQuantizer.compress returns them
+ * (quashkv/mixed_precision.py:271-297). */
+int qkv_kipmixed_pack(const uint8_t* codes, const uint8_t* qjl, int64_t n,
+                      const int32_t* perm_host, int32_t n_out, uint8_t* dst, int64_t seq,
+                      int64_t group_stride, void* stream);
+int qkv_kipmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
+                        int32_t n_out, int64_t seq, int64_t group_stride, uint8_t* codes,
+                        uint8_t* qjl, void* stream);
 
 /* Fused compress of bf16 / fp16 keys (groups x S x 128) straight into
  * kmixed rows and norms at tokens [t0, t0 + S) of each group: the key half of
@@ -424,18 +439,33 @@ int qkv_store_append_kmixed_rotated(const float* y_slots, const float* norm_in, 
                                     uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
                                     void* stream);
 
+/* Fused compress of bf16 / fp16 keys into kipmixed rows and norms:
+ * MixedPrecisionIPQuantizer.compress (quashkv/mixed_precision.py:271-297) --
+ * per-channel boundary codes, QJL bit [(y - c[code]) S >= 0] -- straight into
+ * the store.  out_cent_host (4) / out_bound_host (3): HOST 2-bit outlier
+ * codebook; reg_cent_host (2) / reg_bound_host (1): 1-bit regular codebook
+ * (both symmetric). */
+int qkv_store_append_kipmixed(int32_t in_dtype, const void* keys, int64_t groups, int64_t S,
+                              int32_t d, const float* pi_perm, const float* signs_perm,
+                              int32_t n_out, const float* out_cent_host,
+                              const float* out_bound_host, const float* reg_cent_host,
+                              const float* reg_bound_host, uint8_t* kstore, float* knorm,
+                              int64_t t_stride, int64_t t0, void* stream);
+/* qkv_store_append_kipmixed from rotated unit vectors in slot order with
+ * their norms; codes and QJL bits equal the reference's
+ * (quashkv/mixed_precision.py:283-297) bit for bit, ties included. */
+int qkv_store_append_kipmixed_rotated(const float* y_slots, const float* norm_in,
+                                      int64_t groups, int64_t S, int32_t d,
+                                      const float* signs_perm, int32_t n_out,
+                                      const float* out_cent_host, const float* out_bound_host,
+                                      const float* reg_cent_host, const float* reg_bound_host,
+                                      uint8_t* kstore, float* knorm, int64_t t_stride,
+                                      int64_t t0, void* stream);
+
 /* Decode attention over kmixed K rows and V tiles: scores
  * n_k <q Pi^T, c_channel[code]> (the reference's decompress-then-attend,
  * quashkv/mixed_precision.py:160-187 with quashkv/engine.py:245-297), values
- * un-rotated by pi_v.  out_cent_host (8) / reg_cent_host (4): HOST centroids.
- * The prepare phase alone (query operands into the workspace) is exposed for
- * timing; qkv_attention_run with kbits = 2 and kcent_host = reg_cent_host
- * completes it. */
-int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int32_t B, int32_t Hq,
-                                 int32_t Hkv, int32_t Q, int32_t d, const float* pi_perm,
-                                 int32_t n_out, const float* out_cent_host,
-                                 const float* reg_cent_host, void* workspace,
-                                 int64_t ws_bytes, int32_t n_splits, void* stream);
+ * un-rotated by pi_v.  out_cent_host (8) / reg_cent_host (4): HOST centroids. */
 int qkv_decode_attention_kmixed(const void* q, int32_t q_dtype, const uint8_t* kstore,
                                 const float* knorm, const uint32_t* vstore,
                                 const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
@@ -446,6 +476,21 @@ int qkv_decode_attention_kmixed(const void* q, int32_t q_dtype, const uint8_t* k
                                 int32_t causal, void* out, int32_t out_dtype,
                                 void* workspace, int64_t ws_bytes, int32_t n_splits,
                                 void* stream);
+/* Decode attention over kipmixed K rows: scores as decompress_for_dot
+ * (quashkv/quantizer.py:244-279) with each channel's MSE codebook,
+ * n_k (<q~, c_channel[code]> + qjl_scale sum_j |q~_j| (2 b_j - 1) S_j),
+ * q~ = q Pi^T; the rest as qkv_decode_attention_kmixed.  out_cent_host (4) /
+ * reg_cent_host (2): HOST centroids of the 2-bit and 1-bit MSE codebooks. */
+int qkv_decode_attention_kipmixed(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                                  const float* knorm, const uint32_t* vstore,
+                                  const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+                                  int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits,
+                                  const float* pi_perm, const float* signs_perm,
+                                  float qjl_scale, int32_t n_out, const float* out_cent_host,
+                                  const float* reg_cent_host, const float* pi_v,
+                                  const float* vcent_host, float scale, int32_t causal,
+                                  void* out, int32_t out_dtype, void* workspace,
+                                  int64_t ws_bytes, int32_t n_splits, void* stream);
 
 /* ------------------------------------------------------------------------
  * Maximum inner-product search over K rows (the index form of the key store).

@@ -343,7 +343,7 @@ def compression_ratio(d: int, key_bits: int, value_bits: int,
 
 
 # ---------------------------------------------------------------------------
-# Mixed precision (quashkv/mixed_precision.py:92-187)
+# Mixed precision (quashkv/mixed_precision.py:92-322)
 # ---------------------------------------------------------------------------
 
 def mixed_calibrate(data: torch.Tensor, pi: torch.Tensor, n_outliers: int) -> torch.Tensor:
@@ -401,6 +401,69 @@ def attention_mixed_keys(q, kcodes, knorm, vcodes, vnorm, pi_k, outlier_idx, c_o
     v = (vcent[vcodes.long()] @ pi_v) * vnorm.unsqueeze(-1)
     qg = q.reshape(B, H, G * Q, d)
     w = torch.softmax((qg @ k.transpose(-1, -2)) * scale, dim=-1)
+    return (w @ v).reshape(B, Hq, Q, d)
+
+
+def _mixed_mask(d, outlier_idx):
+    mask = torch.zeros(d, dtype=torch.bool)
+    if outlier_idx is not None:
+        mask[outlier_idx] = True
+    return mask
+
+
+def mixed_ip_compress_from_y(y, outlier_idx, c_out, t_out, c_reg, t_reg, s):
+    """MixedPrecisionIPQuantizer's code stage on rotated unit vectors y
+    (mixed_precision.py:283-297): per-channel boundary codes, x_rot_hat from
+    each channel's centroids, QJL bit [(y - x_rot_hat) S >= 0]."""
+    mask = _mixed_mask(y.shape[-1], outlier_idx)
+    codes = torch.empty_like(y, dtype=torch.uint8)
+    codes[..., mask] = quantize_boundary(y[..., mask], t_out)
+    codes[..., ~mask] = quantize_boundary(y[..., ~mask], t_reg)
+    yhat = torch.empty_like(y)
+    yhat[..., mask] = c_out[codes[..., mask].long()]
+    yhat[..., ~mask] = c_reg[codes[..., ~mask].long()]
+    bits = (((y - yhat) * s) >= 0).to(torch.uint8)
+    return codes, bits
+
+
+def mixed_ip_compress(x, pi, outlier_idx, c_out, t_out, c_reg, t_reg, s):
+    """(mse codes, qjl bits, norms) of MixedPrecisionIPQuantizer.compress
+    (mixed_precision.py:271-297): norms clamped at 1e-8, y = (x / n) Pi^T."""
+    x = x.float()
+    n = x.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+    y = (x / n) @ pi.T
+    codes, bits = mixed_ip_compress_from_y(y, outlier_idx, c_out, t_out, c_reg, t_reg, s)
+    return codes, bits, n.squeeze(-1)
+
+
+def attention_mixed_ip_keys(q, kcodes, kbits, knorm, vcodes, vnorm, pi_k, outlier_idx, c_out,
+                            c_reg, s, qjl_scale, pi_v, vcent, scale: Optional[float] = None,
+                            causal: bool = False) -> torch.Tensor:
+    """Decode attention over mixed-precision IP keys: scores as
+    decompress_for_dot (quantizer.py:244-279) with each channel's MSE
+    centroid, n_k (<q~, c_ch[code]> + qjl_scale sum |q~| (2b - 1) S) scale,
+    softmax, V^ = c_v[code] Pi_v n (engine.py:245-297); causal masks key t
+    for query row i when t > T - Q + i.  q (B, Hq, Q, d), Hq a multiple of the
+    cache's heads (head h reads kv head h // G); codes (B, H, T, d)."""
+    q = q.float()
+    B, Hq, Q, d = q.shape
+    H, T = kcodes.shape[1], kcodes.shape[2]
+    G = Hq // H
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    mask = _mixed_mask(d, outlier_idx)
+    k_hat = torch.empty(*kcodes.shape, dtype=torch.float32)
+    k_hat[..., mask] = c_out[kcodes[..., mask].long()]
+    k_hat[..., ~mask] = c_reg[kcodes[..., ~mask].long()]
+    q_rot = (q @ pi_k.T).reshape(B, H, G * Q, d)
+    sv = kbits.float() * 2.0 - 1.0
+    sc = q_rot @ k_hat.transpose(-1, -2) + qjl_scale * ((q_rot.abs() * s) @ sv.transpose(-1, -2))
+    sc = knorm.unsqueeze(2) * sc * scale
+    if causal:
+        qi = torch.arange(G * Q) % Q
+        sc = sc.masked_fill(torch.arange(T)[None, :] > (T - Q + qi)[:, None], float("-inf"))
+    w = torch.softmax(sc, dim=-1)
+    v = (vcent[vcodes.long()] @ pi_v) * vnorm.unsqueeze(-1)
     return (w @ v).reshape(B, Hq, Q, d)
 
 

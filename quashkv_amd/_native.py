@@ -66,8 +66,15 @@ _SIGS = {
                                         _p, _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_store_append_kmixed_rotated": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _p, _p, _p, _p,
                                                _i64, _i64, _p]),
-    "qkv_attention_prepare_kmixed": (_i32, [_p, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i32,
-                                            _p, _p, _p, _i64, _i32, _p]),
+    "qkv_kipmixed_pack": (_i32, [_p, _p, _i64, _p, _i32, _p, _i64, _i64, _p]),
+    "qkv_kipmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p, _p]),
+    "qkv_store_append_kipmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _p, _i32, _p, _p, _p,
+                                         _p, _p, _p, _i64, _i64, _p]),
+    "qkv_store_append_kipmixed_rotated": (_i32, [_p, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p,
+                                                 _p, _p, _p, _i64, _i64, _p]),
+    "qkv_decode_attention_kipmixed": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
+                                             _i32, _i32, _i32, _i32, _p, _p, _f32, _i32, _p, _p,
+                                             _p, _p, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
     "qkv_decode_attention_kmixed": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
                                            _i32, _i32, _i32, _i32, _p, _i32, _p, _p, _p, _p,
                                            _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),

@@ -438,22 +438,30 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 
 // ------------------------------------------------- mixed-precision keys
 
-// MixedPrecisionMSEQuantizer keys (quashkv/mixed_precision.py:132-158) with
-// 3-bit outlier and 2-bit regular channels, into 48-byte rows over permuted
-// coordinates (outliers first; the caller passes Pi with its rows permuted):
-// plane b0 and plane b1 of every coordinate, then a third plane holding b2 of
-// the NO outlier coordinates at bits 0.. and their parity b0^b1^b2 at bits
-// 64..  The outlier coordinates fill whole 32-coordinate blocks (NO = 32 or
-// 64), so each block's codebook is fixed at compile time.  FROM_Y: `xin`
-// holds fp32 rotated unit rows in slot order and `nin` their norms.
-template <int NO, bool F16, bool FROM_Y>
+// Mixed-precision keys over permuted coordinates (outliers first; the caller
+// passes Pi with its rows permuted and, for IP keys, S in the same slot order)
+// into rows of whole dwords:
+//  * !IPM, MixedPrecisionMSEQuantizer (quashkv/mixed_precision.py:132-158)
+//    with 3-bit outlier and 2-bit regular channels: plane b0 and plane b1 of
+//    every slot, then b2 of the NO outlier slots, then their parity
+//    b0^b1^b2 -- 32 + NO / 4 bytes;
+//  * IPM, MixedPrecisionIPQuantizer (quashkv/mixed_precision.py:283-297) with
+//    a 2-bit outlier / 1-bit regular MSE stage: plane b0 of every slot, the
+//    QJL plane [(y - c) S >= 0] of every slot, then b1 of the NO outlier
+//    slots -- 32 + NO / 8 bytes.  The search runs over each codebook's fine
+//    list as append_k_mfma's does, so the QJL tie rule is the reference's.
+// The outlier slots fill whole 32-slot blocks (NO = 32 or 64), so each block's
+// codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
+// rows in slot order and `nin` their norms.
+template <int NO, bool F16, bool FROM_Y, bool IPM>
 __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
-    int64_t ntiles, const float* __restrict__ pi_perm, Half po, Half pr,
-    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0) {
-  constexpr int RD = 12;              // dwords per row
-  constexpr int NSK = RD * kTok / 64; // staging dwords per lane
-  constexpr int NOB = NO / 32;        // outlier blocks
+    int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
+    Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
+    int64_t t0) {
+  constexpr int NOB = NO / 32;                         // outlier blocks
+  constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
+  constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
   __shared__ uint4 frag[FROM_Y ? 1 : kFragN];
   __shared__ float4 inv_s[kWaves][kTok / 4];
   if constexpr (!FROM_Y) {
@@ -462,10 +470,22 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
   }
 
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
-  uint32_t pov[3], prv[1];  // positive halves: outlier (3-bit) and regular (2-bit) boundaries
+  // positive halves: outlier and regular boundaries (MSE keys) or fine lists
+  // (IP keys), three and one entries either way
+  uint32_t pov[3], prv[1];
 #pragma unroll
   for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.t[i]);
   prv[0] = in_vgpr(pr.t[0]);
+  uint64_t sneg[4] = {0, 0, 0, 0};  // IP: lanes whose slot 32 n + (l & 31) has S < 0
+  uint32_t cx[4] = {0u, 0u, 0u, 0u};  // IP: 1 where S >= 0 (centroid level counts c <= y)
+  if constexpr (IPM) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const bool neg = signs_perm[32 * n + li] < 0.f;
+      sneg[n] = lanes_where(neg);
+      cx[n] = neg ? 0u : 1u;
+    }
+  }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(gridDim.x) * kWaves;
 
@@ -549,8 +569,23 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
           constexpr int v = decltype(vc)::value;
           const float y = yv[tt][v];
           constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);  // token of lanes 0..31
-          uint64_t w[4];  // plane words: b0, b1 (+ outliers: b2, parity)
-          if constexpr (n < NOB) {
+          // plane words in row order: MSE keys b0, b1 (+ outliers: b2, parity);
+          // IP keys b0, QJL (+ outliers: b1)
+          uint64_t w[4] = {0, 0, 0, 0};
+          if constexpr (IPM) {
+            if constexpr (n < NOB) {
+              uint64_t f[3];
+              search_sym<3, true>(y, pov, cx[n], f);
+              w[0] = f[1];
+              w[1] = f[0] ^ sneg[n];
+              w[2] = f[2];
+            } else {
+              uint64_t f[2];
+              search_sym<2, true>(y, prv, cx[n], f);
+              w[0] = f[1];
+              w[1] = f[0] ^ sneg[n];
+            }
+          } else if constexpr (n < NOB) {
             uint64_t m[3];
             search_sym<3, false>(y, pov, 0u, m);
             w[0] = m[0];
@@ -562,12 +597,12 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
             search_sym<2, false>(y, prv, 0u, m);
             w[0] = m[0];
             w[1] = m[1];
-            w[2] = w[3] = 0;
           }
-          static_for<(n < NOB ? 4 : 2)>([&](auto rc) {
+          constexpr int NW = n < NOB ? (IPM ? 3 : 4) : 2;
+          static_for<NW>([&](auto rc) {
             constexpr int r = decltype(rc)::value;
-            // row dword: planes b0, b1 at word n; b2 / parity in the third plane
-            constexpr int dw = r < 2 ? 4 * r + n : 8 + n + (r == 3 ? 2 : 0);
+            // row dword: whole planes at word n, outlier words after them
+            constexpr int dw = r < 2 ? 4 * r + n : 8 + n + (r == 3 ? NOB : 0);
             constexpr int D0 = ta * RD + dw, D1 = (ta + 4) * RD + dw;
             stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w[r]));
             stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w[r] >> 32));
@@ -908,11 +943,28 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
 }
 
 // The kmixed key append (x or, rotated, y in slot order with its norms).
+// Fine list c_0 < t_0 < c_1 < ... < c_{2^bits - 1} of a codebook into fl.
+int fine_list(const float* cent, const float* bound, int bits, float* fl) {
+  const int nc = 1 << bits;
+  for (int i = 0; i < nc; ++i) {
+    fl[2 * i] = cent[i];
+    if (i + 1 < nc) fl[2 * i + 1] = bound[i];
+  }
+  return 2 * nc - 1;
+}
+
+// Mixed-precision key append.  ipm = false: MSE keys, 3-bit outlier / 2-bit
+// regular boundaries (out_bound 7, reg_bound 3 entries).  ipm = true: IP keys
+// with a 2-bit outlier / 1-bit regular MSE stage, searched over the fine
+// lists built from the centroids (4, 2) and boundaries (3, 1); signs_perm is S
+// in slot order.
 int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const float* norm_in,
                        int64_t groups, int64_t S, int32_t d, const float* pi_perm,
-                       int32_t n_out, const float* out_bound_host,
-                       const float* reg_bound_host, uint8_t* kstore, float* knorm,
-                       int64_t t_stride, int64_t t0, void* stream) {
+                       int32_t n_out, bool ipm, const float* signs_perm,
+                       const float* out_cent_host, const float* reg_cent_host,
+                       const float* out_bound_host, const float* reg_bound_host,
+                       uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
+                       void* stream) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
   QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
@@ -925,18 +977,28 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(keys && (rotated || pi_perm) && out_bound_host && reg_bound_host && kstore &&
-                  knorm && (!rotated || norm_in),
+                  knorm && (!rotated || norm_in) &&
+                  (!ipm || (signs_perm && out_cent_host && reg_cent_host)),
               "null pointer");
   QKV_REQUIRE(qkv_aligned(keys, rotated ? 4 : 16) && qkv_aligned(kstore, 4) &&
                   (rotated || qkv_aligned(pi_perm, 16)),
               "keys / pi aligned (16-B bf16 / fp16 rows, 4-B fp32 rows) and store 4-B aligned");
+  float lo[7], lr[3];
+  if (ipm) {
+    fine_list(out_cent_host, out_bound_host, 2, lo);
+    fine_list(reg_cent_host, reg_bound_host, 1, lr);
+  } else {
+    for (int i = 0; i < 7; ++i) lo[i] = out_bound_host[i];
+    for (int i = 0; i < 3; ++i) lr[i] = reg_bound_host[i];
+  }
   Half po{}, pr{};
   bool asc = true;
-  for (int i = 0; i + 1 < 7; ++i) asc = asc && out_bound_host[i] < out_bound_host[i + 1];
-  for (int i = 0; i + 1 < 3; ++i) asc = asc && reg_bound_host[i] < reg_bound_host[i + 1];
-  if (!asc || !symmetric(out_bound_host, 7) || !symmetric(reg_bound_host, 3) ||
-      !positive_half(out_bound_host, 7, &po) || !positive_half(reg_bound_host, 3, &pr)) {
-    qkv_set_error("mixed-precision keys need ascending boundaries symmetric about 0");
+  for (int i = 0; i + 1 < 7; ++i) asc = asc && lo[i] < lo[i + 1];
+  for (int i = 0; i + 1 < 3; ++i) asc = asc && lr[i] < lr[i + 1];
+  if (!asc || !symmetric(lo, 7) || !symmetric(lr, 3) || !positive_half(lo, 7, &po) ||
+      !positive_half(lr, 3, &pr)) {
+    qkv_set_error("mixed-precision keys need ascending %s symmetric about 0",
+                  ipm ? "fine lists c_i < t_i < c_{i+1}" : "boundaries");
     return QKV_E_UNSUPPORTED;
   }
   if (groups == 0 || S == 0) return QKV_OK;
@@ -944,18 +1006,27 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
   const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
   const dim3 grid(append_blocks(ntiles));
   const bool f16 = in_dtype == QKV_F16;
-#define QKV_KM(NOV, F, FY)                                                                    \
-  hipLaunchKernelGGL((append_kmix_mfma<NOV, F, FY>), grid, dim3(kThreads), 0, s, keys,       \
-                     norm_in, S, tpg, ntiles, pi_perm, po, pr, kstore, knorm, t_stride, t0)
+#define QKV_KM(NOV, F, FY, IP)                                                                 \
+  hipLaunchKernelGGL((append_kmix_mfma<NOV, F, FY, IP>), grid, dim3(kThreads), 0, s, keys,     \
+                     norm_in, S, tpg, ntiles, pi_perm, signs_perm, po, pr, kstore, knorm,      \
+                     t_stride, t0)
+#define QKV_KM_IN(NOV, IP)                \
+  do {                                    \
+    if (rotated)                          \
+      QKV_KM(NOV, false, true, IP);       \
+    else if (f16)                         \
+      QKV_KM(NOV, true, false, IP);       \
+    else                                  \
+      QKV_KM(NOV, false, false, IP);      \
+  } while (0)
   if (n_out == 32) {
-    if (rotated) QKV_KM(32, false, true);
-    else if (f16) QKV_KM(32, true, false);
-    else QKV_KM(32, false, false);
+    if (ipm) QKV_KM_IN(32, true);
+    else QKV_KM_IN(32, false);
   } else {
-    if (rotated) QKV_KM(64, false, true);
-    else if (f16) QKV_KM(64, true, false);
-    else QKV_KM(64, false, false);
+    if (ipm) QKV_KM_IN(64, true);
+    else QKV_KM_IN(64, false);
   }
+#undef QKV_KM_IN
 #undef QKV_KM
   QKV_LAUNCHED();
   return QKV_OK;
@@ -1015,8 +1086,9 @@ extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64
                                        const float* reg_bound_host, uint8_t* kstore,
                                        float* knorm, int64_t t_stride, int64_t t0,
                                        void* stream) {
-  return kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm, n_out,
-                            out_bound_host, reg_bound_host, kstore, knorm, t_stride, t0, stream);
+  return kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm, n_out, false,
+                            nullptr, nullptr, nullptr, out_bound_host, reg_bound_host, kstore,
+                            knorm, t_stride, t0, stream);
 }
 
 extern "C" int qkv_store_append_kmixed_rotated(const float* y_slots, const float* norm_in,
@@ -1025,6 +1097,33 @@ extern "C" int qkv_store_append_kmixed_rotated(const float* y_slots, const float
                                                const float* reg_bound_host, uint8_t* kstore,
                                                float* knorm, int64_t t_stride, int64_t t0,
                                                void* stream) {
-  return kmixed_append_impl(QKV_F32, y_slots, true, norm_in, groups, S, d, nullptr, n_out,
-                            out_bound_host, reg_bound_host, kstore, knorm, t_stride, t0, stream);
+  return kmixed_append_impl(QKV_F32, y_slots, true, norm_in, groups, S, d, nullptr, n_out, false,
+                            nullptr, nullptr, nullptr, out_bound_host, reg_bound_host, kstore,
+                            knorm, t_stride, t0, stream);
+}
+
+extern "C" int qkv_store_append_kipmixed(int32_t in_dtype, const void* keys, int64_t groups,
+                                         int64_t S, int32_t d, const float* pi_perm,
+                                         const float* signs_perm, int32_t n_out,
+                                         const float* out_cent_host, const float* out_bound_host,
+                                         const float* reg_cent_host, const float* reg_bound_host,
+                                         uint8_t* kstore, float* knorm, int64_t t_stride,
+                                         int64_t t0, void* stream) {
+  return kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm, n_out, true,
+                            signs_perm, out_cent_host, reg_cent_host, out_bound_host,
+                            reg_bound_host, kstore, knorm, t_stride, t0, stream);
+}
+
+extern "C" int qkv_store_append_kipmixed_rotated(const float* y_slots, const float* norm_in,
+                                                 int64_t groups, int64_t S, int32_t d,
+                                                 const float* signs_perm, int32_t n_out,
+                                                 const float* out_cent_host,
+                                                 const float* out_bound_host,
+                                                 const float* reg_cent_host,
+                                                 const float* reg_bound_host, uint8_t* kstore,
+                                                 float* knorm, int64_t t_stride, int64_t t0,
+                                                 void* stream) {
+  return kmixed_append_impl(QKV_F32, y_slots, true, norm_in, groups, S, d, nullptr, n_out, true,
+                            signs_perm, out_cent_host, reg_cent_host, out_bound_host,
+                            reg_bound_host, kstore, knorm, t_stride, t0, stream);
 }

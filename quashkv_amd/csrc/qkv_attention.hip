@@ -57,13 +57,17 @@ struct Tables {
   float vg[8];       // value Walsh coefficients, odd subsets (odd_subset order)
   float vconst;      // g_empty - sum vg (the plane form's constant)
   int mfma_ok;       // both codebooks admit the plane decomposition
-  // mixed-precision MSE keys (no QJL): rows hold planes b0, b1 of every
-  // coordinate, then b2 of the n_out first (outlier, 3-bit) coordinates at
-  // bits 0.. and their parity b0^b1^b2 at bits 64.. of the third plane
+  // mixed-precision keys over slots (outlier channels first), rows of whole
+  // dwords:
+  //   kmix 1, MSE keys 3-bit outlier / 2-bit regular (no QJL):
+  //     [b0 of every slot][b1 of every slot][b2 of the n_out outlier slots]
+  //     [their parity b0^b1^b2]
+  //   kmix 2, IP keys with a 2-bit outlier / 1-bit regular MSE stage:
+  //     [b0 of every slot][QJL of every slot][b1 of the outlier slots]
   int kmix;
   int n_out;
-  float kgo[4];      // outlier Walsh coefficients: b0, b1, b2, b0b1b2
-  float kgr[2];      // regular (2-bit) Walsh coefficients: b0, b1
+  float kgo[4];      // outlier Walsh coefficients: b0, b1 (, b2, b0b1b2)
+  float kgr[2];      // regular Walsh coefficients: b0 (, b1)
   float kco, kcr;    // -(sum of the coefficients) per kind
 };
 
@@ -485,12 +489,21 @@ __device__ __forceinline__ uint32_t fp8_digits(float x) {
   return out;
 }
 
+// First row dword that lane group g of a row of RDW dwords loads: groups own
+// dwords [g DPL, (g + 1) DPL) clipped to the row, and a group whose range
+// passes the row's end loads the row's last DPL dwords instead (its operand
+// bytes outside the dwords it owns are zero).
+template <int DPL, int RDW>
+__host__ __device__ constexpr int krow_base(int g) {
+  return g * DPL < RDW - DPL ? g * DPL : RDW - DPL;
+}
+
 // Byte of the A-operand image (DPL MFMAs x 64 lanes x 32 bytes) holding row
 // bit p (dword p >> 5, bit p & 31) for A row m.
-template <int DPL>
+template <int DPL, int RDW>
 __device__ __forceinline__ int kf4_byte(int p, int m) {
   const int w = p >> 5, bit = p & 31;
-  const int u = w % DPL, gb = w / DPL;
+  const int gb = w / DPL, u = w - krow_base<DPL, RDW>(gb);
   const int k = 32 * gb + 8 * (bit & 3) + (bit >> 2);
   const int ga = (k & 63) >> 4, ea = (k & 15) + 16 * (k >> 6);
   return (u * 64 + m + 16 * ga) * 32 + ea;
@@ -511,12 +524,41 @@ __device__ __forceinline__ int kf4_sigma(float wmax) {
 
 // The digit bytes of weight W at row bit p of query row r into the image sb;
 // returns W's share of the row constant.
-template <int DPL>
+template <int DPL, int RDW>
 __device__ __forceinline__ float kf4_put(uint8_t* sb, int p, float W, int sigma, int r) {
   const uint32_t dg = fp8_digits(ldexpf(W * kf4_factor(p), -sigma));
 #pragma unroll
-  for (int d = 0; d < 4; ++d) sb[kf4_byte<DPL>(p, 4 * r + d)] = static_cast<uint8_t>(dg >> (8 * d));
+  for (int d = 0; d < 4; ++d)
+    sb[kf4_byte<DPL, RDW>(p, 4 * r + d)] = static_cast<uint8_t>(dg >> (8 * d));
   return (p & 3) == 3 ? 0.5f * W : 0.f;
+}
+
+// Score weights of slot j of one query row (v = q~_j, w = alpha |v| S_j) at
+// their K-row bits through put(bit, W); returns the slot's share of the row's
+// MSE constant: v for IP keys (whose constant is kconst sum v), the slot's
+// codebook constant times v for mixed keys.
+template <int MB, typename P>
+__device__ __forceinline__ float key_weights(const Tables& tb, int j, float v, float w, P&& put) {
+  constexpr int D = 128;
+  if (tb.kmix) {
+    const bool outl = j < tb.n_out;
+    put(j, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v);
+    if (tb.kmix == 1) {
+      put(D + j, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v);
+      if (outl) {
+        put(2 * D + j, 2.f * tb.kgo[2] * v);
+        put(2 * D + tb.n_out + j, 2.f * tb.kgo[3] * v);
+      }
+    } else {
+      put(D + j, 2.f * w);
+      if (outl) put(2 * D + j, 2.f * tb.kgo[1] * v);
+    }
+    return (outl ? tb.kco : tb.kcr) * v;
+  }
+#pragma unroll
+  for (int pl = 0; pl < MB; ++pl) put(pl * D + j, 2.f * tb.kg[pl] * v);
+  put(MB * D + j, 2.f * w);
+  return v;
 }
 
 template <int D, int NPL, bool FP4>
@@ -623,14 +665,8 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     for (int r = 0; r < kRowsM; ++r) part[half][r][j] = acc[r];
   }
   float kgmax = alpha;
-  if (tb.kmix) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
-    kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
-  } else {
-#pragma unroll
-    for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
-  }
+  for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
   __syncthreads();
 
   uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
@@ -672,26 +708,16 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     if (wmax > 0.f) frexpf(wmax, &ex);  // wmax = f 2^ex, f in [0.5, 1)
     // int8 digits: the fixed-point exponent (|Z| < 2^30); fp4: the row's sigma
     const int fq = FP4 ? kf4_sigma(wmax) : wmax > 0.f ? 30 - ex : 0;
-    auto put = [&](int pb, float W, int fqv, int rv) {
-      if constexpr (FP4)
-        hf += kf4_put<DPL>(sb, pb, W, fqv, rv);
-      else
-        put8(pb, W, fqv, rv);
-    };
-    if (D == 128 && tb.kmix) {
-      const bool outl = j < tb.n_out;
-      csq[rr] = (outl ? tb.kco : tb.kcr) * v;
-      put(j, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v, fq, r);
-      put(D + j, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v, fq, r);
-      if (NPL == 3 && j < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers only
-        put(2 * D + j, outl ? 2.f * tb.kgo[2] * v : 0.f, fq, r);
-        put(2 * D + 64 + j, outl ? 2.f * tb.kgo[3] * v : 0.f, fq, r);
-      }
+    // IP keys (the mixed-key formats run on decode_fused's own prologue)
+    if constexpr (FP4) {
+      csq[rr] = key_weights<MB>(tb, j, v, w, [&](int pb, float W) {
+        hf += kf4_put<DPL, 4 * DPL>(sb, pb, W, fq, r);
+      });
     } else {
       csq[rr] = v;
 #pragma unroll
-      for (int pl = 0; pl < MB; ++pl) put(pl * D + j, 2.f * tb.kg[pl] * v, fq, r);
-      put(MB * D + j, 2.f * w, fq, r);
+      for (int pl = 0; pl < MB; ++pl) put8(pl * D + j, 2.f * tb.kg[pl] * v, fq, r);
+      put8(MB * D + j, 2.f * w, fq, r);
     }
     csw[rr] = w;
     chf[rr] = hf;
@@ -727,7 +753,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     int ex = 0;
     if (wmax > 0.f) frexpf(wmax, &ex);
     const int fq = wmax > 0.f ? 30 - ex : 0;
-    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = (tb.kmix ? sq - sw : tb.kconst * sq - sw) + sh;
+    rowc[(int64_t(bhc) * kRowsM + r) * 2 + 0] = tb.kconst * sq - sw + sh;
     // fp4: the row's sigma (an integer, as a float); int8: 2^-Fq
     rowc[(int64_t(bhc) * kRowsM + r) * 2 + 1] =
         FP4 ? static_cast<float>(kf4_sigma(wmax)) : ldexpf(1.f, -fq);
@@ -1160,17 +1186,19 @@ __device__ __forceinline__ T ldnt(const T* p) {
 // final_out != 0 and one split: write the attention output through ol;
 // else split partials (part_o, part_ml) for combine_kernel.
 // PAGED: the store is a page pool addressed through kv.ptab.
-template <int MB, int VB, bool PAGED>
+template <int RDW, int VB, bool PAGED>
 __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     QLayers ql, KVLayers kv, OutLayers ol, int Bl, int q_dtype, float alpha, int Hq, int Hkv,
     int Q, int R, int chunks, Tables tb, int64_t t_stride, int64_t T, float scale, int causal,
     int64_t split_len, int final_out, int out_dtype, const qkv_v4i* __restrict__ aq_ws,
     const float* __restrict__ rowc_ws, float* __restrict__ part_o, float* __restrict__ part_ml) {
   constexpr int D = 128;
-  constexpr int NPL = MB + 1;            // planes per K row (MSE + QJL)
-  constexpr int KRB = NPL * D / 8;       // K row bytes
-  constexpr int DPL = KRB / 16;          // row dwords per lane group
-  constexpr int NU = KRB / 8;            // operand image: NU x 256 dwords (DPL fp4 MFMAs)
+  // K rows of RDW dwords: IP keys 4 (MB + 1) (MSE planes + QJL plane), the
+  // mixed-key formats 9, 10 or 12 (the Tables comment)
+  constexpr int MB = RDW / 4 - 1;        // IP keys: MSE planes
+  constexpr int KRB = 4 * RDW;           // K row bytes
+  constexpr int DPL = (RDW + 3) / 4;     // row dwords per lane group = fp4 MFMAs per 16 tokens
+  constexpr int NU = 2 * DPL;            // operand image: NU x 256 dwords
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int PR4 = FusedLds::PR4;
   constexpr int NT = kThreadsF;
@@ -1271,6 +1299,11 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     }
     if (ppart < kRowsM) qs[ppart * D + pj] = qv;
     if (ppart == 0) sgns[pj] = sgn;
+    if constexpr (RDW % 4 != 0) {  // operand bytes no row dword feeds stay zero
+#pragma unroll
+      for (int x = 0; x < (NU * 256 + NT - 1) / NT; ++x)
+        if (tid + NT * x < NU * 256) stage[tid + NT * x] = 0u;
+    }
   } else {
     // operands and row constants from prepare_mfma's workspace
     const int64_t bhc = (int64_t(bz) * Hkv + hkv) * chunks + cki;
@@ -1293,7 +1326,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
   const int vj = 16 * wi + ln;  // value wave: coordinate of this lane
   // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
-  const uint32_t koff = ln * KRB + lg * DPL * 4;       // bytes into a tile's K rows
+  const uint32_t koff = ln * KRB + krow_base<DPL, RDW>(lg) * 4;  // bytes into a tile's K rows
   const uint32_t voff = blk * VB * D + vj;             // words into a tile's V planes
   // contiguous store: the split's bases, a tile as a 32-bit row offset from them
   const uint8_t* kbase = kst + srow0 * KRB;
@@ -1370,7 +1403,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
 #pragma unroll
       for (int r = 0; r < 4; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kgo[r]));
       kgmax = fmaxf(kgmax, fmaxf(fabsf(tb.kgr[0]), fabsf(tb.kgr[1])));
-    } else {
+    } else {  // IP keys
 #pragma unroll
       for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
     }
@@ -1383,23 +1416,9 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       const int sig = kf4_sigma(wmax);
       uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
       float hf = 0.f;  // this coordinate's share of the row constant (bit class 3)
-      auto put = [&](int p, float W) { hf += kf4_put<DPL>(sb, p, W, sig, r); };
-      float csq;
-      if (tb.kmix) {
-        const bool outl = pj < tb.n_out;
-        csq = (outl ? tb.kco : tb.kcr) * v;
-        put(pj, 2.f * (outl ? tb.kgo[0] : tb.kgr[0]) * v);
-        put(D + pj, 2.f * (outl ? tb.kgo[1] : tb.kgr[1]) * v);
-        if (NPL == 3 && pj < 64) {  // third plane: b2 at bits 0.., parity at bits 64.., outliers
-          put(2 * D + pj, outl ? 2.f * tb.kgo[2] * v : 0.f);
-          put(2 * D + 64 + pj, outl ? 2.f * tb.kgo[3] * v : 0.f);
-        }
-      } else {
-        csq = v;
-#pragma unroll
-        for (int pl = 0; pl < MB; ++pl) put(pl * D + pj, 2.f * tb.kg[pl] * v);
-        put(MB * D + pj, 2.f * w);
-      }
+      const float csq = key_weights<MB>(tb, pj, v, w, [&](int p, float W) {
+        hf += kf4_put<DPL, RDW>(sb, p, W, sig, r);
+      });
       // row constants: sums over j (row r = waves 2r, 2r + 1) into red[8 ..]
       const float a = wave_sum_dpp(csq);
       const float c = wave_sum_dpp(w);
@@ -2245,20 +2264,27 @@ Tables make_tables(const float* kc, int mbits, const float* vc, int vbits) {
   return t;
 }
 
-// Mixed-precision key coefficients (3-bit outlier / 2-bit regular slots) into tb.
-bool add_kmix(Tables& tb, const float* out_cent, const float* reg_cent, int n_out) {
-  float kc_tmp[4];
+// Mixed-precision key coefficients into tb: kind 1, MSE keys with 3-bit
+// outlier / 2-bit regular codebooks; kind 2, IP keys whose MSE stage has
+// 2-bit outlier / 1-bit regular codebooks.
+bool add_kmix(Tables& tb, int kind, const float* out_cent, const float* reg_cent, int n_out) {
+  const int ob = kind == 1 ? 3 : 2, rb = ob - 1;
+  float go[4] = {0.f, 0.f, 0.f, 0.f}, gr[4] = {0.f, 0.f, 0.f, 0.f};
   float kconst_o = 0.f, kconst_r = 0.f;
-  if (!walsh_odd(out_cent, 3, tb.kgo, &kconst_o) || !walsh_odd(reg_cent, 2, kc_tmp, &kconst_r))
+  if (!walsh_odd(out_cent, ob, go, &kconst_o) || !walsh_odd(reg_cent, rb, gr, &kconst_r))
     return false;
-  tb.kgr[0] = kc_tmp[0];
-  tb.kgr[1] = kc_tmp[1];
+  for (int i = 0; i < 4; ++i) tb.kgo[i] = go[i];
+  tb.kgr[0] = gr[0];
+  tb.kgr[1] = gr[1];
   tb.kco = kconst_o;
   tb.kcr = kconst_r;
-  tb.kmix = 1;
+  tb.kmix = kind;
   tb.n_out = n_out;
   return true;
 }
+
+// K row dwords of a mixed-key format (the Tables comment).
+int kmixed_rdw(int kind, int n_out) { return kind == 1 ? 8 + n_out / 16 : 8 + n_out / 32; }
 
 int64_t mfma_split_len(int64_t T, int n_splits) {
   return ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
@@ -2335,12 +2361,13 @@ bool use_fused(const Tables& tb, int d, int64_t t_stride) {
   return tb.mfma_ok && d == 128 && t_stride % 64 == 0;
 }
 
-// Launch decode_fused over nl layers (B sequences each; workspace for B * nl).
-// pro: query operands computed in the kernel (else prepare_mfma's, from the
-// workspace).  final_out with one split: the kernel writes the output (ol);
+// Launch decode_fused over nl layers (B sequences each; workspace for B * nl)
+// on K rows of rdw dwords: 4 (kbits + 1) for IP keys of kbits MSE bits,
+// kmixed_rdw() for the mixed-key formats.  pro: query operands computed in the
+// kernel (else prepare_mfma's, from the workspace).  final_out with one split: the kernel writes the output (ol);
 // otherwise it writes split partials and the caller runs combine_layers.
 int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int nl, int B,
-                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int kbits, int vbits,
+                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int rdw, int vbits,
                  const Tables& tb, int64_t t_stride, int64_t T, float scale, int causal,
                  int n_splits, int final_out, int out_dtype, void* workspace, bool pro,
                  hipStream_t s) {
@@ -2354,36 +2381,51 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
   float* po = at<float>(workspace, L.po);
   float* pml = at<float>(workspace, L.pml);
   constexpr uint32_t smem = FusedLds::TOTAL;
-#define QKV_FU2(MB, VB, PG)                                                                    \
+#define QKV_FU2(RW, VB, PG)                                                                    \
   do {                                                                                         \
     static const hipError_t attr_ = hipFuncSetAttribute(                                       \
-        reinterpret_cast<const void*>(&decode_fused<MB, VB, PG>),                              \
+        reinterpret_cast<const void*>(&decode_fused<RW, VB, PG>),                              \
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));                   \
     QKV_HIP(attr_);                                                                            \
-    hipLaunchKernelGGL((decode_fused<MB, VB, PG>), grid, dim3(kThreadsF), smem, s, ql, kv, ol, \
+    hipLaunchKernelGGL((decode_fused<RW, VB, PG>), grid, dim3(kThreadsF), smem, s, ql, kv, ol, \
                        B, q_dtype, alpha, Hq, Hkv, Q, R, chunks, tb, t_stride, T, scale,       \
                        causal, split_len, final_out, out_dtype, aq, rowc, po, pml);            \
   } while (0)
-#define QKV_FU(MB, VB)              \
+#define QKV_FU(RW, VB)              \
   do {                              \
     if (kv.ptab)                    \
-      QKV_FU2(MB, VB, true);        \
+      QKV_FU2(RW, VB, true);        \
     else                            \
-      QKV_FU2(MB, VB, false);       \
+      QKV_FU2(RW, VB, false);       \
   } while (0)
-  switch (kbits * 10 + vbits) {
-    case 11: QKV_FU(1, 1); break;
-    case 12: QKV_FU(1, 2); break;
-    case 13: QKV_FU(1, 3); break;
-    case 14: QKV_FU(1, 4); break;
-    case 21: QKV_FU(2, 1); break;
-    case 22: QKV_FU(2, 2); break;
-    case 23: QKV_FU(2, 3); break;
-    case 24: QKV_FU(2, 4); break;
+  // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) have no
+  // paged store
+  QKV_REQUIRE(rdw % 4 == 0 || kv.ptab == nullptr, "mixed keys are not paged");
+#define QKV_FUC(RW, VB)    \
+  QKV_FU2(RW, VB, false);  \
+  break
+  switch (rdw * 10 + vbits) {
+    case 81: QKV_FU(8, 1); break;
+    case 82: QKV_FU(8, 2); break;
+    case 83: QKV_FU(8, 3); break;
+    case 84: QKV_FU(8, 4); break;
+    case 121: QKV_FU(12, 1); break;
+    case 122: QKV_FU(12, 2); break;
+    case 123: QKV_FU(12, 3); break;
+    case 124: QKV_FU(12, 4); break;
+    case 91: QKV_FUC(9, 1);
+    case 92: QKV_FUC(9, 2);
+    case 93: QKV_FUC(9, 3);
+    case 94: QKV_FUC(9, 4);
+    case 101: QKV_FUC(10, 1);
+    case 102: QKV_FUC(10, 2);
+    case 103: QKV_FUC(10, 3);
+    case 104: QKV_FUC(10, 4);
     default:
-      qkv_set_error("fused decode: key MSE bits %d / value bits %d unsupported", kbits, vbits);
+      qkv_set_error("fused decode: K rows of %d dwords / value bits %d unsupported", rdw, vbits);
       return QKV_E_UNSUPPORTED;
   }
+#undef QKV_FUC
 #undef QKV_FU
 #undef QKV_FU2
   QKV_LAUNCHED();
@@ -2513,43 +2555,6 @@ extern "C" int qkv_attention_prepare(const void* q, int32_t q_dtype, int32_t B, 
                         static_cast<hipStream_t>(stream));
 }
 
-extern "C" int qkv_attention_prepare_kmixed(const void* q, int32_t q_dtype, int32_t B,
-                                            int32_t Hq, int32_t Hkv, int32_t Q, int32_t d,
-                                            const float* pi_perm, int32_t n_out,
-                                            const float* out_cent_host,
-                                            const float* reg_cent_host, void* workspace,
-                                            int64_t ws_bytes, int32_t n_splits, void* stream) {
-  QKV_REQUIRE(qkv_dtype_ok(q_dtype), "unsupported query dtype %d", q_dtype);
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
-  if (st != QKV_OK) return st;
-  if (d != 128 || (n_out != 32 && n_out != 64)) {
-    qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
-    return QKV_E_UNSUPPORTED;
-  }
-  QKV_REQUIRE(q && pi_perm && out_cent_host && reg_cent_host, "null pointer");
-  QKV_REQUIRE(qkv_aligned(pi_perm, 16), "pi must be 16-byte aligned");
-  Tables tb{};
-  if (!add_kmix(tb, out_cent_host, reg_cent_host, n_out)) {
-    qkv_set_error("mixed-precision keys need symmetric codebooks");
-    return QKV_E_UNSUPPORTED;
-  }
-  tb.mfma_ok = 1;
-  const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B, Hkv, R, d, n_splits);
-  const int chunks = (R + kRowsM - 1) / kRowsM;
-  auto s = static_cast<hipStream_t>(stream);
-  QLayers ql{};
-  ql.q[0] = q;
-  ql.pi[0] = pi_perm;
-  ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
-  hipLaunchKernelGGL((prepare_mfma<128, 3, true>), dim3(B * Hkv * chunks), dim3(256),
-                     (prep_lds<128, 3, true>()), s, ql, B,
-                     q_dtype, 0.f, Hq, Hkv, Q, R, chunks, tb, at<qkv_v4i>(workspace, L.aq),
-                     at<float>(workspace, L.rowc), nullptr);
-  QKV_LAUNCHED();
-  return QKV_OK;
-}
-
 // partial for nl layers (B sequences each)
 int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int32_t B,
                    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
@@ -2576,7 +2581,8 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
   float* pml = at<float>(workspace, L.pml);
   if (use_mfma(tb, d, t_stride, T, n_splits) && d == 128) {
     // the fused kernel in partial mode: operands from prepare_mfma, split partials out
-    return launch_fused(QLayers{}, kv, OutLayers{}, nl, B, QKV_F32, 0.f, Hq, Hkv, Q, kbits,
+    return launch_fused(QLayers{}, kv, OutLayers{}, nl, B, QKV_F32, 0.f, Hq, Hkv, Q,
+                        4 * (kbits + 1),
                         vbits, tb, t_stride, T, scale, causal, n_splits, 0, QKV_F32, workspace,
                         false, s);
   }
@@ -2768,7 +2774,8 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
     ol.pi[0] = pi;
     ol.out[0] = out;
     auto s = static_cast<hipStream_t>(stream);
-    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1), vbits,
+                      tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
     return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
@@ -2899,7 +2906,7 @@ extern "C" int qkv_paged_decode_attention(
     ol.pi[0] = pi;
     ol.out[0] = out;
     auto s = static_cast<hipStream_t>(stream);
-    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits,
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1), vbits,
                       make_tables(kcent_host, kbits, vcent_host, vbits), t_stride, T, scale,
                       causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
@@ -2975,7 +2982,8 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.npages = num_pages;
   auto s = static_cast<hipStream_t>(stream);
   if (d == 128) {
-    st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+    st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1),
+                      vbits, tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
     return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
@@ -3031,36 +3039,44 @@ extern "C" int qkv_paged_decode_attention_layers(
                        num_pages);
 }
 
-// Decode attention over mixed-precision K rows (3-bit outlier / 2-bit regular
-// MSE keys, no QJL) and b-bit MSE V tiles.  Only the MFMA path reads this row
-// format, so the store and split shape must admit it.
-extern "C" int qkv_decode_attention_kmixed(
-    const void* q, int32_t q_dtype, const uint8_t* kstore, const float* knorm,
-    const uint32_t* vstore, const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
-    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits, const float* pi_perm,
-    int32_t n_out, const float* out_cent_host, const float* reg_cent_host, const float* pi_v,
-    const float* vcent_host, float scale, int32_t causal, void* out, int32_t out_dtype,
-    void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
+namespace {
+
+// Decode attention over mixed-precision K rows (kind 1: MSE keys, kind 2: IP
+// keys; signs_perm and qjl_scale for kind 2) and b-bit MSE V tiles.  Only
+// decode_fused reads these row formats, so the store and split shape must
+// admit it.
+int kmixed_decode_impl(int kind, const void* q, int32_t q_dtype, const uint8_t* kstore,
+                       const float* knorm, const uint32_t* vstore, const float* vnorm,
+                       int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv,
+                       int32_t Q, int32_t d, int32_t vbits, const float* pi_perm,
+                       const float* signs_perm, float qjl_scale, int32_t n_out,
+                       const float* out_cent_host, const float* reg_cent_host,
+                       const float* pi_v, const float* vcent_host, float scale, int32_t causal,
+                       void* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+                       int32_t n_splits, void* stream) {
   QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
   QKV_REQUIRE(qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
   QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
   int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi_perm && out_cent_host &&
-                  reg_cent_host && pi_v && vcent_host && out,
+                  reg_cent_host && pi_v && vcent_host && out && (kind == 1 || signs_perm),
               "null pointer");
-  Tables tb = make_tables(reg_cent_host, 2, vcent_host, vbits);
+  // the value tables (the key entries of make_tables are unused here)
+  Tables tb = make_tables(reg_cent_host, kind == 1 ? 2 : 1, vcent_host, vbits);
   if (d != 128 || (n_out != 32 && n_out != 64) || !use_fused(tb, d, t_stride) ||
-      !add_kmix(tb, out_cent_host, reg_cent_host, n_out)) {
+      !add_kmix(tb, kind, out_cent_host, reg_cent_host, n_out)) {
     qkv_set_error("mixed-precision keys need head_dim 128, 32 or 64 outlier channels, a store "
                   "capacity that is a multiple of 64 and symmetric codebooks");
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(qkv_aligned(pi_perm, 16) && qkv_aligned(pi_v, 16), "pi must be 16-byte aligned");
+  QKV_REQUIRE(qkv_aligned(kstore, 4), "K rows must be 4-byte aligned");
   QLayers ql{};
   ql.q[0] = q;
   ql.pi[0] = pi_perm;
-  ql.signs[0] = pi_perm;  // read, weighted by alpha = 0: no QJL term
+  // MSE keys: read, weighted by alpha = 0 (no QJL term)
+  ql.signs[0] = kind == 1 ? pi_perm : signs_perm;
   KVLayers kv{};
   kv.kst[0] = kstore;
   kv.knorm[0] = knorm;
@@ -3070,10 +3086,40 @@ extern "C" int qkv_decode_attention_kmixed(
   ol.pi[0] = pi_v;
   ol.out[0] = out;
   auto s = static_cast<hipStream_t>(stream);
-  st = launch_fused(ql, kv, ol, 1, B, q_dtype, 0.f, Hq, Hkv, Q, 2, vbits, tb, t_stride, T, scale,
-                    causal, n_splits, 1, out_dtype, workspace, true, s);
+  st = launch_fused(ql, kv, ol, 1, B, q_dtype, kind == 1 ? 0.f : qjl_scale, Hq, Hkv, Q,
+                    kmixed_rdw(kind, n_out), vbits, tb, t_stride, T, scale, causal, n_splits, 1,
+                    out_dtype, workspace, true, s);
   if (st != QKV_OK || n_splits == 1) return st;
   return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
+}
+
+}  // namespace
+
+extern "C" int qkv_decode_attention_kmixed(
+    const void* q, int32_t q_dtype, const uint8_t* kstore, const float* knorm,
+    const uint32_t* vstore, const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits, const float* pi_perm,
+    int32_t n_out, const float* out_cent_host, const float* reg_cent_host, const float* pi_v,
+    const float* vcent_host, float scale, int32_t causal, void* out, int32_t out_dtype,
+    void* workspace, int64_t ws_bytes, int32_t n_splits, void* stream) {
+  return kmixed_decode_impl(1, q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv,
+                            Q, d, vbits, pi_perm, nullptr, 0.f, n_out, out_cent_host,
+                            reg_cent_host, pi_v, vcent_host, scale, causal, out, out_dtype,
+                            workspace, ws_bytes, n_splits, stream);
+}
+
+extern "C" int qkv_decode_attention_kipmixed(
+    const void* q, int32_t q_dtype, const uint8_t* kstore, const float* knorm,
+    const uint32_t* vstore, const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
+    int32_t Hq, int32_t Hkv, int32_t Q, int32_t d, int32_t vbits, const float* pi_perm,
+    const float* signs_perm, float qjl_scale, int32_t n_out, const float* out_cent_host,
+    const float* reg_cent_host, const float* pi_v, const float* vcent_host, float scale,
+    int32_t causal, void* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+    int32_t n_splits, void* stream) {
+  return kmixed_decode_impl(2, q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv,
+                            Q, d, vbits, pi_perm, signs_perm, qjl_scale, n_out, out_cent_host,
+                            reg_cent_host, pi_v, vcent_host, scale, causal, out, out_dtype,
+                            workspace, ws_bytes, n_splits, stream);
 }
 
 // ------------------------------------------------------------ MIPS search (ABI)

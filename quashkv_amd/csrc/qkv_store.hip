@@ -143,48 +143,69 @@ struct Perm128 {
   uint8_t p[128];  // slot -> channel
 };
 
-// one thread per (row, row dword)
-__global__ void kmixed_pack_kernel(const uint8_t* __restrict__ codes, int64_t n, Perm128 perm,
-                                   int n_out, uint8_t* __restrict__ dst, int64_t seq,
+// Mixed-precision K rows over slots (slot j = channel perm[j], the NO = n_out
+// outlier channels first), RD = kmixed_row_dwords(ipm, n_out) dwords:
+//   MSE keys (ipm = 0): [b0 x 4][b1 x 4][b2 of outliers][parity of outliers]
+//   IP keys  (ipm = 1): [b0 x 4][QJL x 4][b1 of outliers]
+__host__ __device__ inline int kmixed_row_dwords(int ipm, int n_out) {
+  return ipm ? 8 + n_out / 32 : 8 + n_out / 16;
+}
+
+// one thread per (row, row dword); qjl (IP keys) holds one bit per uint8
+__global__ void kmixed_pack_kernel(const uint8_t* __restrict__ codes,
+                                   const uint8_t* __restrict__ qjl, int64_t n, Perm128 perm,
+                                   int n_out, int ipm, uint8_t* __restrict__ dst, int64_t seq,
                                    int64_t gstride) {
-  const int64_t total = n * 12;
+  const int rd = kmixed_row_dwords(ipm, n_out), nob = n_out / 32;
+  const int64_t total = n * rd;
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * blockDim.x) {
-    const int64_t r = i / 12;
-    const int w = static_cast<int>(i - r * 12);
+    const int64_t r = i / rd;
+    const int w = static_cast<int>(i - r * rd);
     const uint8_t* c = codes + r * 128;
     uint32_t word = 0;
     for (int b = 0; b < 32; ++b) {
       uint32_t bit;
-      if (w < 8) {  // planes b0, b1
-        bit = (uint32_t(c[perm.p[32 * (w & 3) + b]]) >> (w >> 2)) & 1u;
+      if (w < 4) {
+        bit = c[perm.p[32 * w + b]] & 1u;
+      } else if (w < 8) {
+        const int ch = perm.p[32 * (w - 4) + b];
+        bit = ipm ? qjl[r * 128 + ch] & 1u : (c[ch] >> 1) & 1u;
       } else {
-        const int j = 32 * (w & 1) + b;  // outlier slot
-        if (j >= n_out) break;
-        const uint32_t code = c[perm.p[j]];
-        bit = w < 10 ? (code >> 2) & 1u : (code ^ (code >> 1) ^ (code >> 2)) & 1u;
+        const int k = (w - 8) / nob;  // 0: b2 (MSE) / b1 (IP); 1: parity (MSE)
+        const uint32_t code = c[perm.p[32 * (w - 8 - k * nob) + b]];
+        bit = ipm ? (code >> 1) & 1u
+                  : (k == 0 ? (code >> 2) & 1u : (code ^ (code >> 1) ^ (code >> 2)) & 1u);
       }
       word |= bit << b;
     }
     const int64_t row = qkv_grouped_row(r, seq, gstride);
-    reinterpret_cast<uint32_t*>(dst + row * 48)[w] = word;
+    reinterpret_cast<uint32_t*>(dst + row * (4 * rd))[w] = word;
   }
 }
 
 // one thread per (row, slot)
 __global__ void kmixed_unpack_kernel(const uint8_t* __restrict__ src, int64_t n, Perm128 perm,
-                                     int n_out, int64_t seq, int64_t gstride,
-                                     uint8_t* __restrict__ codes) {
+                                     int n_out, int ipm, int64_t seq, int64_t gstride,
+                                     uint8_t* __restrict__ codes, uint8_t* __restrict__ qjl) {
+  const int rd = kmixed_row_dwords(ipm, n_out);
   const int64_t total = n * 128;
   for (int64_t i = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; i < total;
        i += int64_t(gridDim.x) * blockDim.x) {
     const int64_t r = i >> 7;
     const int j = static_cast<int>(i & 127);
-    const uint8_t* row = src + qkv_grouped_row(r, seq, gstride) * 48;
-    uint32_t code = (row[j >> 3] >> (j & 7)) & 1u;
-    code |= ((row[16 + (j >> 3)] >> (j & 7)) & 1u) << 1;
-    if (j < n_out) code |= ((row[32 + (j >> 3)] >> (j & 7)) & 1u) << 2;
-    codes[r * 128 + perm.p[j]] = static_cast<uint8_t>(code);
+    const uint8_t* row = src + qkv_grouped_row(r, seq, gstride) * (4 * rd);
+    auto bit = [&](int byte0) { return (uint32_t(row[byte0 + (j >> 3)]) >> (j & 7)) & 1u; };
+    uint32_t code = bit(0);
+    const int ch = perm.p[j];
+    if (ipm) {
+      qjl[r * 128 + ch] = static_cast<uint8_t>(bit(16));
+      if (j < n_out) code |= bit(32) << 1;
+    } else {
+      code |= bit(16) << 1;
+      if (j < n_out) code |= bit(32) << 2;
+    }
+    codes[r * 128 + ch] = static_cast<uint8_t>(code);
   }
 }
 
@@ -290,39 +311,70 @@ extern "C" int qkv_vtiles_unpack(const uint32_t* src, int64_t groups, int64_t S,
 }
 
 
-extern "C" int qkv_kmixed_pack(const uint8_t* codes, int64_t n, const int32_t* perm_host,
-                               int32_t n_out, uint8_t* dst, int64_t seq, int64_t group_stride,
-                               void* stream) {
+namespace {
+
+int kmixed_pack_impl(const uint8_t* codes, const uint8_t* qjl, int ipm, int64_t n,
+                     const int32_t* perm_host, int32_t n_out, uint8_t* dst, int64_t seq,
+                     int64_t group_stride, void* stream) {
   QKV_REQUIRE(n >= 0, "negative row count");
   QKV_REQUIRE(perm_host, "null pointer");
   Perm128 perm;
   QKV_REQUIRE(make_perm(perm_host, n_out, &perm),
               "perm must be a permutation of 0..127 and n_out 32 or 64");
   if (n == 0) return QKV_OK;
-  QKV_REQUIRE(codes && dst, "null pointer");
+  QKV_REQUIRE(codes && dst && (!ipm || qjl), "null pointer");
   QKV_REQUIRE(qkv_aligned(dst, 4), "K rows must be 4-byte aligned");
   QKV_REQUIRE(seq > 0 && group_stride >= seq, "bad grouped-row layout");
-  hipLaunchKernelGGL(kmixed_pack_kernel, dim3(grid_for(n * 12)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), codes, n, perm, n_out, dst, seq,
-                     group_stride);
+  hipLaunchKernelGGL(kmixed_pack_kernel, dim3(grid_for(n * kmixed_row_dwords(ipm, n_out))),
+                     dim3(256), 0, static_cast<hipStream_t>(stream), codes, qjl, n, perm, n_out,
+                     ipm, dst, seq, group_stride);
   QKV_LAUNCHED();
   return QKV_OK;
+}
+
+int kmixed_unpack_impl(const uint8_t* src, int ipm, int64_t n, const int32_t* perm_host,
+                       int32_t n_out, int64_t seq, int64_t group_stride, uint8_t* codes,
+                       uint8_t* qjl, void* stream) {
+  QKV_REQUIRE(n >= 0, "negative row count");
+  QKV_REQUIRE(perm_host, "null pointer");
+  Perm128 perm;
+  QKV_REQUIRE(make_perm(perm_host, n_out, &perm),
+              "perm must be a permutation of 0..127 and n_out 32 or 64");
+  if (n == 0) return QKV_OK;
+  QKV_REQUIRE(src && codes && (!ipm || qjl), "null pointer");
+  QKV_REQUIRE(seq > 0 && group_stride >= seq, "bad grouped-row layout");
+  hipLaunchKernelGGL(kmixed_unpack_kernel, dim3(grid_for(n * 128)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), src, n, perm, n_out, ipm, seq,
+                     group_stride, codes, qjl);
+  QKV_LAUNCHED();
+  return QKV_OK;
+}
+
+}  // namespace
+
+extern "C" int qkv_kmixed_pack(const uint8_t* codes, int64_t n, const int32_t* perm_host,
+                               int32_t n_out, uint8_t* dst, int64_t seq, int64_t group_stride,
+                               void* stream) {
+  return kmixed_pack_impl(codes, nullptr, 0, n, perm_host, n_out, dst, seq, group_stride,
+                          stream);
 }
 
 extern "C" int qkv_kmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
                                  int32_t n_out, int64_t seq, int64_t group_stride,
                                  uint8_t* codes, void* stream) {
-  QKV_REQUIRE(n >= 0, "negative row count");
-  QKV_REQUIRE(perm_host, "null pointer");
-  Perm128 perm;
-  QKV_REQUIRE(make_perm(perm_host, n_out, &perm),
-              "perm must be a permutation of 0..127 and n_out 32 or 64");
-  if (n == 0) return QKV_OK;
-  QKV_REQUIRE(src && codes, "null pointer");
-  QKV_REQUIRE(seq > 0 && group_stride >= seq, "bad grouped-row layout");
-  hipLaunchKernelGGL(kmixed_unpack_kernel, dim3(grid_for(n * 128)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), src, n, perm, n_out, seq, group_stride,
-                     codes);
-  QKV_LAUNCHED();
-  return QKV_OK;
+  return kmixed_unpack_impl(src, 0, n, perm_host, n_out, seq, group_stride, codes, nullptr,
+                            stream);
+}
+
+extern "C" int qkv_kipmixed_pack(const uint8_t* codes, const uint8_t* qjl, int64_t n,
+                                 const int32_t* perm_host, int32_t n_out, uint8_t* dst,
+                                 int64_t seq, int64_t group_stride, void* stream) {
+  return kmixed_pack_impl(codes, qjl, 1, n, perm_host, n_out, dst, seq, group_stride, stream);
+}
+
+extern "C" int qkv_kipmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
+                                   int32_t n_out, int64_t seq, int64_t group_stride,
+                                   uint8_t* codes, uint8_t* qjl, void* stream) {
+  return kmixed_unpack_impl(src, 1, n, perm_host, n_out, seq, group_stride, codes, qjl,
+                            stream);
 }

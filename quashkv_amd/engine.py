@@ -14,12 +14,19 @@ API of quashkv/engine.py:54-360.  What changes underneath:
   on access, so code that walks blocks keeps working.
 * attention() runs the split-K decode kernels; query heads may be a multiple
   of the cached kv heads (GQA, head h reads kv head h // G).
-* ``key_quantizer=MixedPrecisionMSEQuantizer(128, 3, 2, 32 or 64)`` (an
-  extension: the reference engine takes IP keys only) keeps 2.5 / 3-bit
-  mixed-precision MSE keys in the store's "kmixed" rows; attention scores
-  them as the reference's decompress-then-attend would
-  (quashkv/mixed_precision.py:160-187).  The outlier channels are fixed at the
-  first append.
+* ``key_quantizer=`` (an extension: the reference engine builds its own IP
+  key quantizer) takes a mixed-precision key quantizer with 32 or 64 outlier
+  channels at head_dim 128:
+
+  - ``MixedPrecisionMSEQuantizer(128, 3, 2, n)`` keeps 2.25 / 2.5-bit MSE keys
+    in the store's "kmixed" rows; attention scores them as the reference's
+    decompress-then-attend would (quashkv/mixed_precision.py:160-187);
+  - ``MixedPrecisionIPQuantizer(128, 3, 2, n)`` keeps its 2/1-bit MSE codes
+    and QJL bits in "kipmixed" rows; attention scores them as
+    decompress_for_dot does for IP keys (quashkv/quantizer.py:244-279) with
+    each channel's MSE codebook.
+
+  The outlier channels are fixed at the first append.
 """
 
 from __future__ import annotations
@@ -33,7 +40,7 @@ import torch
 from . import _native as N
 from .constants import DEFAULT_SEED, DEFAULT_TOTAL_BITS
 from .kernels import attention_store, attention_store_kmixed
-from .mixed_precision import MixedPrecisionMSEQuantizer
+from .mixed_precision import MixedPrecisionIPQuantizer, MixedPrecisionMSEQuantizer
 from .packing import pack_bits, unpack_bits
 from .quantizer import InnerProductQuantizer, MSEQuantizer, _default_device, compress_into
 from .store import KVStore
@@ -63,7 +70,7 @@ class QuashKVEngine:
         device=None,
         pack_storage: bool = False,
         capacity: int = 0,
-        key_quantizer: Optional[MixedPrecisionMSEQuantizer] = None,
+        key_quantizer=None,
     ):
         self.head_dim = head_dim
         self.key_bits = key_bits
@@ -74,14 +81,16 @@ class QuashKVEngine:
         self.initial_capacity = capacity
 
         self._kmix = key_quantizer is not None
+        self._kmix_ip = isinstance(key_quantizer, MixedPrecisionIPQuantizer)
         if self._kmix:
             kq = key_quantizer
-            if not isinstance(kq, MixedPrecisionMSEQuantizer):
-                raise ValueError("key_quantizer must be a MixedPrecisionMSEQuantizer")
+            if not isinstance(kq, (MixedPrecisionMSEQuantizer, MixedPrecisionIPQuantizer)):
+                raise ValueError("key_quantizer must be a MixedPrecisionMSEQuantizer or a "
+                                 "MixedPrecisionIPQuantizer")
             if (kq.d != head_dim or head_dim != 128 or kq.outlier_bits != 3
                     or kq.regular_bits != 2 or kq.n_outliers not in (32, 64)):
-                raise ValueError("mixed-precision keys run on head_dim 128 with 3-bit outlier "
-                                 "and 2-bit regular channels, 32 or 64 outliers")
+                raise ValueError("mixed-precision keys run on head_dim 128 with outlier_bits 3 "
+                                 "and regular_bits 2, 32 or 64 outliers")
             self.key_quantizer = kq.to(self.device)
             self.key_bits = kq.effective_bits
         else:
@@ -94,7 +103,8 @@ class QuashKVEngine:
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
         self._host_tables = None   # codebook tables passed by value to qkv_store_append
-        self._kmix_tables = None   # (perm, pi_perm, n_out, host tables) of mixed keys
+        # mixed keys: (perm, pi_perm, n_out, host tables, S in slot order or None)
+        self._kmix_tables = None
 
     # ---------------------------------------------------------- compression
 
@@ -128,7 +138,7 @@ class QuashKVEngine:
             kmix = None
             if self._kmix:
                 perm, _, n_out, _ = self._kmix_setup()
-                kmix = (perm, n_out)
+                kmix = (perm, n_out, self._kmix_ip)
             st = self._store = KVStore(B, H, d, 2 if self._kmix else self.key_bits - 1,
                                        self.value_bits, max(self.initial_capacity, S), dev,
                                        kmix=kmix)
@@ -191,36 +201,50 @@ class QuashKVEngine:
 
     def _kmix_setup(self):
         """Slot order (outlier channels ascending, then the rest), Pi with its
-        rows in that order, n_out and the host codebook tables; fixed at the
-        first append."""
+        rows in that order, n_out and the host codebook tables (outlier and
+        regular centroids and boundaries, value boundaries, and for IP keys S
+        in slot order); fixed at the first append."""
         if self._kmix_tables is None:
             kq = self.key_quantizer
+            mq = kq.mse_quantizer if self._kmix_ip else kq
             if not kq.calibrated:
                 raise ValueError("mixed-precision keys need calibrate() or "
                                  "set_outlier_channels() before the first append")
-            mask = kq._outlier_mask.cpu()
+            mask = mq._outlier_mask.cpu()
             out = [j for j in range(self.head_dim) if bool(mask[j])]
             reg = [j for j in range(self.head_dim) if not bool(mask[j])]
             perm = out + reg
-            pi_perm = kq.Pi[torch.tensor(perm, device=kq.Pi.device)].contiguous()
-            oc, rc = kq.outlier_codebook, kq.regular_codebook
+            idx = torch.tensor(perm, device=mq.Pi.device)
+            pi_perm = mq.Pi[idx].contiguous()
+            oc, rc = mq.outlier_codebook, mq.regular_codebook
             host = (N.HostFloats(oc.centroids_host), N.HostFloats(rc.centroids_host),
                     N.HostFloats(oc.boundaries_host), N.HostFloats(rc.boundaries_host),
                     N.HostFloats(self.value_quantizer.codebook.boundaries_host))
-            self._kmix_tables = (perm, pi_perm, len(out), host)
-        return self._kmix_tables
+            signs_perm = kq.S.to(mq.Pi.device)[idx].float().contiguous() if self._kmix_ip else None
+            self._kmix_tables = (perm, pi_perm, len(out), host, signs_perm)
+        return self._kmix_tables[:4]
+
+    def _kmix_signs(self, device) -> Optional[torch.Tensor]:
+        """S in slot order (IP mixed keys), on ``device``."""
+        sp = self._kmix_tables[4]
+        if sp is not None and sp.device != device:
+            sp = sp.to(device)
+            self._kmix_tables = self._kmix_tables[:4] + (sp,)
+        return sp
 
     def _append_kmix(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
-        """Mixed-precision keys: bf16 / fp16 rows straight into kmixed rows
-        (qkv_store_append_kmixed); other dtypes through qkv_compress_mixed and
-        the kmixed packer.  Values as in the IP-key engine."""
+        """Mixed-precision keys: bf16 / fp16 rows straight into kmixed /
+        kipmixed rows (qkv_store_append_kmixed / _kipmixed); other dtypes
+        through qkv_compress_mixed and the row packers.  Values as in the
+        IP-key engine."""
         B, H, S, d = keys.shape
         st = self._store
         kq, vq = self.key_quantizer, self.value_quantizer
-        perm, pi_perm, n_out, (_, _, ob, rb, vb) = self._kmix_setup()
+        perm, pi_perm, n_out, (oc, rc, ob, rb, vb) = self._kmix_setup()
         if pi_perm.device != keys.device:
             pi_perm = pi_perm.to(keys.device)
-            self._kmix_tables = (perm, pi_perm, n_out, self._kmix_tables[3])
+            self._kmix_tables = (perm, pi_perm, n_out) + self._kmix_tables[3:]
+        sp = self._kmix_signs(keys.device)
         L = N.lib()
         stream = N.stream(keys.device)
         n = B * H * S
@@ -228,22 +252,32 @@ class QuashKVEngine:
         if fused:
             k, v = keys.contiguous(), values.contiguous()
             dt = N.dtype_code(k.dtype)
-            N.check(L.qkv_store_append_kmixed(dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(),
-                                              n_out, ob.ptr, rb.ptr, st.kst.data_ptr(),
-                                              st.knorm.data_ptr(), st.capacity, t0, stream))
+            if self._kmix_ip:
+                N.check(L.qkv_store_append_kipmixed(
+                    dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(), sp.data_ptr(), n_out,
+                    oc.ptr, ob.ptr, rc.ptr, rb.ptr, st.kst.data_ptr(), st.knorm.data_ptr(),
+                    st.capacity, t0, stream))
+            else:
+                N.check(L.qkv_store_append_kmixed(
+                    dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(), n_out, ob.ptr, rb.ptr,
+                    st.kst.data_ptr(), st.knorm.data_ptr(), st.capacity, t0, stream))
             N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, d, 2, vq.bits,
                                        vq.Pi.data_ptr(), None, None, None, vb.ptr, None, None,
                                        st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, t0,
                                        stream))
             return
-        kc, _, kn = kq._compress_into(N.QKV_MODE_MSE, keys.reshape(n, d), None)
+        if self._kmix_ip:
+            kc, kb, kn = kq.compress(keys.reshape(n, d))
+        else:
+            kc, kn = kq.compress(keys.reshape(n, d))
+            kb = None
         vc = torch.empty(n, d, dtype=torch.uint8, device=keys.device)
         vn = torch.empty(n, dtype=torch.float32, device=keys.device)
         compress_into(N.QKV_MODE_MSE, values.reshape(n, d), vq.Pi, vq.codebook.boundaries,
                       vq.codebook.centroids, vq.bits, None, vc, None, vn, packed=False)
         st.knorm[:, :, t0:t0 + S].copy_(kn.view(B, H, S))
         st.vnorm[:, :, t0:t0 + S].copy_(vn.view(B, H, S))
-        st.write_codes(t0, S, kc, None, vc)
+        st.write_codes(t0, S, kc, kb, vc)
 
     @property
     def _cache(self) -> list[CompressedKVBlock]:
@@ -255,7 +289,7 @@ class QuashKVEngine:
                 kc = pack_bits(kc, self.key_bits - 1)
                 kb = pack_bits(kb, 1)
                 vc = pack_bits(vc, self.value_bits)
-            elif self.pack_storage:
+            elif self.pack_storage:   # mixed key codes stay one uint8 each
                 vc = pack_bits(vc, self.value_bits)
             sl = slice(t0, t0 + s)
             out.append(CompressedKVBlock(
@@ -284,7 +318,7 @@ class QuashKVEngine:
             return block.mse_indices, block.qjl_signs, block.val_indices
         d = self.head_dim
         if self._kmix:
-            return (block.mse_indices, None,
+            return (block.mse_indices, block.qjl_signs,
                     unpack_bits(block.val_indices.contiguous(), self.value_bits, d))
         return (unpack_bits(block.mse_indices.contiguous(), self.key_bits - 1, d),
                 unpack_bits(block.qjl_signs.contiguous(), 1, d),
@@ -319,7 +353,9 @@ class QuashKVEngine:
             return attention_store_kmixed(
                 queries, st, self._total_tokens, pi_perm, n_out, oc, rc, vq.Pi,
                 vq.codebook.centroids_host, scale=scale, causal=causal, out_dtype=out_dtype,
-                workspace=self._workspace, n_splits=splits)
+                workspace=self._workspace, n_splits=splits,
+                signs_perm=self._kmix_signs(queries.device),
+                qjl_scale=kq.qjl_scale if self._kmix_ip else 0.0)
         return attention_store(
             queries, st, self._total_tokens, kq.mse_quantizer.Pi,
             kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host, kq.S,
@@ -345,8 +381,9 @@ class QuashKVEngine:
             return 0
         B, H = self._heads()
         d = self.head_dim
-        if self._kmix:   # one uint8 per key code (as MixedPrecisionMSEQuantizer keeps them)
-            row = d + (N.packed_row_bytes(d, self.value_bits) if self.pack_storage else d)
+        if self._kmix:   # one uint8 per key code (+ QJL bit), as the mixed quantizers keep them
+            krow = 2 * d if self._kmix_ip else d
+            row = krow + (N.packed_row_bytes(d, self.value_bits) if self.pack_storage else d)
             return B * H * self._total_tokens * (row + 8)
         if self.pack_storage:
             row = (N.packed_row_bytes(d, self.key_bits - 1) + N.packed_row_bytes(d, 1)
@@ -366,8 +403,9 @@ class QuashKVEngine:
         if self._store is not None:
             self._store.to(device)
         if self._kmix_tables is not None:
-            perm, pi_perm, n_out, host = self._kmix_tables
-            self._kmix_tables = (perm, pi_perm.to(self.device), n_out, host)
+            perm, pi_perm, n_out, host, sp = self._kmix_tables
+            self._kmix_tables = (perm, pi_perm.to(self.device), n_out, host,
+                                 None if sp is None else sp.to(self.device))
         self._workspace = None
         return self
 

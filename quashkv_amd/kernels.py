@@ -155,10 +155,15 @@ def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
                            val_centroids: Sequence[float], scale: Optional[float] = None,
                            causal: bool = False, out_dtype: torch.dtype = torch.float32,
                            workspace: Optional[torch.Tensor] = None,
-                           n_splits: Optional[int] = None) -> torch.Tensor:
-    """Decode attention over a store with mixed-precision ("kmixed") K rows:
-    scores n_k <q Pi^T, c_channel[code]> in the slot order of ``pi_perm``
-    (Pi's rows permuted outliers first), values un-rotated by ``Pi_v``."""
+                           n_splits: Optional[int] = None,
+                           signs_perm: Optional[torch.Tensor] = None,
+                           qjl_scale: float = 0.0) -> torch.Tensor:
+    """Decode attention over a store with mixed-precision K rows: scores
+    n_k <q Pi^T, c_channel[code]> in the slot order of ``pi_perm`` (Pi's rows
+    permuted outliers first), values un-rotated by ``Pi_v``.  With IP keys
+    (the store's "kipmixed" rows) ``signs_perm`` (S in slot order) and
+    ``qjl_scale`` add decompress_for_dot's QJL term
+    (quashkv/quantizer.py:244-279)."""
     dev = N.require_gpu(queries, store.kst, pi_perm, Pi_v, what="attention")
     B, Hq, Q, d = queries.shape
     Hkv = store.H
@@ -183,13 +188,23 @@ def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
     pi_perm, Pi_v = N.dense(pi_perm, Pi_v)
     vc = N.HostFloats(val_centroids)
     out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
-    N.check(L.qkv_decode_attention_kmixed(
-        q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
-        store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
-        store.vbits, pi_perm.data_ptr(), int(n_out), out_centroids.ptr, reg_centroids.ptr,
-        Pi_v.data_ptr(), vc.ptr, float(scale), 1 if causal else 0, out.data_ptr(),
-        N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
-        N.stream(dev)))
+    ip = store.kmix is not None and store.kmix[2]
+    common = (q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
+              store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
+              store.vbits, pi_perm.data_ptr())
+    tail = (Pi_v.data_ptr(), vc.ptr, float(scale), 1 if causal else 0, out.data_ptr(),
+            N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
+            N.stream(dev))
+    if ip:
+        if signs_perm is None:
+            raise ValueError("IP mixed-precision keys need signs_perm")
+        sp = N.dense(signs_perm)[0]
+        N.check(L.qkv_decode_attention_kipmixed(*common, sp.data_ptr(), float(qjl_scale),
+                                                int(n_out), out_centroids.ptr,
+                                                reg_centroids.ptr, *tail))
+    else:
+        N.check(L.qkv_decode_attention_kmixed(*common, int(n_out), out_centroids.ptr,
+                                              reg_centroids.ptr, *tail))
     return out
 
 

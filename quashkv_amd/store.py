@@ -12,10 +12,13 @@ stream (C ABI "Cache store formats"):
 * ``vst``   (B, H, C / 32, vbits, d) int32 -- V bit-plane tiles of 32 tokens;
 * ``vnorm`` (B, H, C) fp32.
 
-With mixed-precision keys (``kmix = (perm, n_out)``) ``kst`` holds 48-byte
-"kmixed" rows instead: planes b0 and b1 of every coordinate, then b2 and the
-parity b0^b1^b2 of the n_out outlier coordinates, over coordinates permuted
-outliers first (slot j = rotated channel perm[j]).
+With mixed-precision keys (``kmix = (perm, n_out, ip)``) ``kst`` holds rows
+over coordinates permuted outliers first (slot j = rotated channel perm[j]):
+
+* MSE keys ("kmixed", 3/2-bit): planes b0 and b1 of every slot, then b2 and
+  the parity b0^b1^b2 of the n_out outlier slots -- 32 + n_out / 4 bytes;
+* IP keys ("kipmixed", 2/1-bit MSE stage + QJL): plane b0 and the QJL plane
+  of every slot, then b1 of the outlier slots -- 32 + n_out / 8 bytes.
 
 The capacity C is a multiple of 64 and doubles when an append needs room.
 Writes and reads go through the store converters of libquashkv_hip.so.
@@ -45,12 +48,14 @@ class KVStore:
         self.mbits, self.vbits = mbits, vbits
         self.kmix = None
         if kmix is not None:
-            perm, n_out = kmix
+            perm, n_out, ip = kmix
             if d != 128 or n_out not in (32, 64):
                 raise ValueError("mixed-precision keys need head_dim 128 and 32 or 64 outliers")
-            self.kmix = (N.HostInts(perm), int(n_out))
-            mbits = self.mbits = 2   # rows of three 16-byte planes
-        self.krb = (mbits + 1) * d // 8
+            self.kmix = (N.HostInts(perm), int(n_out), bool(ip))
+            self.mbits = 2
+            self.krb = 32 + (n_out // 8 if ip else n_out // 4)
+        else:
+            self.krb = (mbits + 1) * d // 8
         self.device = torch.device(device)
         self.capacity = 0
         self.kst = self.knorm = self.vst = self.vnorm = None
@@ -93,14 +98,18 @@ class KVStore:
     def write_codes(self, t0: int, S: int, kcodes: torch.Tensor, kqjl: Optional[torch.Tensor],
                     vcodes: torch.Tensor) -> None:
         """Unpacked uint8 codes (B*H*S, d) of tokens [t0, t0 + S) into the store
-        (``kqjl`` None with mixed-precision keys)."""
+        (``kqjl`` None with mixed-precision MSE keys)."""
         L = N.lib()
         n = self.B * self.H * S
         stream = N.stream(self.device)
         if self.kmix is not None:
-            perm, n_out = self.kmix
-            N.check(L.qkv_kmixed_pack(kcodes.data_ptr(), n, perm.ptr, n_out, self.k_row_ptr(t0),
-                                      S, self.capacity, stream))
+            perm, n_out, ip = self.kmix
+            if ip:
+                N.check(L.qkv_kipmixed_pack(kcodes.data_ptr(), kqjl.data_ptr(), n, perm.ptr,
+                                            n_out, self.k_row_ptr(t0), S, self.capacity, stream))
+            else:
+                N.check(L.qkv_kmixed_pack(kcodes.data_ptr(), n, perm.ptr, n_out,
+                                          self.k_row_ptr(t0), S, self.capacity, stream))
         else:
             N.check(L.qkv_kplanes_pack(kcodes.data_ptr(), kqjl.data_ptr(), n, self.d, self.mbits,
                                        self.k_row_ptr(t0), self.krb, S, self.capacity, stream))
@@ -109,19 +118,24 @@ class KVStore:
 
     def read_codes(self, t0: int, S: int):
         """(kcodes, kqjl, vcodes) of tokens [t0, t0 + S) as (B, H, S, d) uint8
-        (kqjl None with mixed-precision keys)."""
+        (kqjl None with mixed-precision MSE keys)."""
         L = N.lib()
         B, H, d = self.B, self.H, self.d
         kc = torch.empty(B, H, S, d, dtype=torch.uint8, device=self.device)
-        kq = torch.empty_like(kc) if self.kmix is None else None
+        kq = torch.empty_like(kc) if self.kmix is None or self.kmix[2] else None
         vc = torch.empty_like(kc)
         if S == 0:
             return kc, kq, vc
         stream = N.stream(self.device)
         if self.kmix is not None:
-            perm, n_out = self.kmix
-            N.check(L.qkv_kmixed_unpack(self.k_row_ptr(t0), B * H * S, perm.ptr, n_out, S,
-                                        self.capacity, kc.data_ptr(), stream))
+            perm, n_out, ip = self.kmix
+            if ip:
+                N.check(L.qkv_kipmixed_unpack(self.k_row_ptr(t0), B * H * S, perm.ptr, n_out, S,
+                                              self.capacity, kc.data_ptr(), kq.data_ptr(),
+                                              stream))
+            else:
+                N.check(L.qkv_kmixed_unpack(self.k_row_ptr(t0), B * H * S, perm.ptr, n_out, S,
+                                            self.capacity, kc.data_ptr(), stream))
         else:
             N.check(L.qkv_kplanes_unpack(self.k_row_ptr(t0), self.krb, B * H * S, d, self.mbits,
                                          S, self.capacity, kc.data_ptr(), kq.data_ptr(), stream))

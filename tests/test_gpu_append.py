@@ -257,7 +257,7 @@ def test_store_append_kmixed_rotated_bit_exact(n_out):
     nrm = torch.rand(B, H, S, generator=g) + 0.5
     o = [int(i) for i in out_idx]
     perm = o + [j for j in range(128) if j not in set(o)]
-    st = KVStore(B, H, 128, 2, 4, S, DEV, kmix=(perm, n_out))
+    st = KVStore(B, H, 128, 2, 4, S, DEV, kmix=(perm, n_out, False))
     ys = y[..., perm].contiguous().to(DEV)
     nd = nrm.to(DEV)
     ob_h, rb_h = N.HostFloats(oc.boundaries_host), N.HostFloats(rc.boundaries_host)

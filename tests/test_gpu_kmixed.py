@@ -63,7 +63,8 @@ def test_kmixed_rows_round_trip_and_bit_model(n_out):
     perm = _perm(out_idx)
     ph = N.HostInts(perm)
     L = N.lib()
-    dst = torch.zeros(2 * gstride, 48, dtype=torch.uint8, device=DEV)
+    rb = 32 + n_out // 4                 # row bytes: b0, b1, outlier b2, outlier parity
+    dst = torch.zeros(2 * gstride, rb, dtype=torch.uint8, device=DEV)
     N.check(L.qkv_kmixed_pack(codes.to(DEV).data_ptr(), n, ph.ptr, n_out, dst.data_ptr(), seq,
                               gstride, N.stream(dst.device)))
     back = torch.empty(n, 128, dtype=torch.uint8, device=DEV)
@@ -78,10 +79,10 @@ def test_kmixed_rows_round_trip_and_bit_model(n_out):
         bits = np.unpackbits(row, bitorder="little")
         assert np.array_equal(bits[0:128], c[r] & 1)
         assert np.array_equal(bits[128:256], (c[r] >> 1) & 1)
-        p2 = np.zeros(128, np.uint32)
-        p2[:n_out] = (c[r, :n_out] >> 2) & 1
-        p2[64:64 + n_out] = (c[r, :n_out] ^ (c[r, :n_out] >> 1) ^ (c[r, :n_out] >> 2)) & 1
-        assert np.array_equal(bits[256:384], p2)
+        co = c[r, :n_out]
+        assert np.array_equal(bits[256:256 + n_out], (co >> 2) & 1)
+        assert np.array_equal(bits[256 + n_out:256 + 2 * n_out], (co ^ (co >> 1) ^ (co >> 2)) & 1)
+        assert len(bits) == 256 + 2 * n_out
     # rows outside the groups' first 35 stay zero
     assert not dst.cpu()[seq:gstride].any() and not dst.cpu()[gstride + seq:].any()
 

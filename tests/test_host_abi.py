@@ -115,6 +115,42 @@ def test_kmixed_host_validation():
     assert st == N.QKV_E_UNSUPPORTED and "multiple of 64" in lib.qkv_last_error().decode()
 
 
+def test_kipmixed_host_validation():
+    lib = N.lib()
+    perm = N.HostInts(list(range(128)))
+    bad = N.HostInts([0] * 128)
+    assert lib.qkv_kipmixed_pack(16, 16, 4, bad.ptr, 32, 16, 4, 4, None) == N.QKV_E_INVALID
+    assert "permutation" in lib.qkv_last_error().decode()
+    assert lib.qkv_kipmixed_pack(16, None, 4, perm.ptr, 32, 16, 4, 4, None) == N.QKV_E_INVALID
+    assert lib.qkv_kipmixed_unpack(16, 4, perm.ptr, 32, 4, 4, 16, None, None) == N.QKV_E_INVALID
+    oc, ob = N.HostFloats([-1.5, -0.5, 0.5, 1.5]), N.HostFloats([-1, 0, 1])
+    rc, rb = N.HostFloats([-0.8, 0.8]), N.HostFloats([0.0])
+    # fp32 keys and other outlier counts are not covered by the fused append
+    assert lib.qkv_store_append_kipmixed(N.QKV_F32, 16, 1, 1, 128, 16, 16, 32, oc.ptr, ob.ptr,
+                                         rc.ptr, rb.ptr, 16, 16, 64, 0, None) == \
+        N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append_kipmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 16, 48, oc.ptr, ob.ptr,
+                                         rc.ptr, rb.ptr, 16, 16, 64, 0, None) == \
+        N.QKV_E_UNSUPPORTED
+    # the fine list c_0 < t_0 < c_1 ... must interleave
+    oc_bad = N.HostFloats([-1.5, -1.2, 1.2, 1.5])
+    assert lib.qkv_store_append_kipmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 16, 32, oc_bad.ptr,
+                                         ob.ptr, rc.ptr, rb.ptr, 16, 16, 64, 0, None) == \
+        N.QKV_E_UNSUPPORTED
+    assert "fine lists" in lib.qkv_last_error().decode()
+    assert lib.qkv_store_append_kipmixed(N.QKV_BF16, 16, 1, 1, 128, 16, None, 32, oc.ptr, ob.ptr,
+                                         rc.ptr, rb.ptr, 16, 16, 64, 0, None) == N.QKV_E_INVALID
+    vc = N.HostFloats([-2, -1, 1, 2])
+    st = lib.qkv_decode_attention_kipmixed(256, 0, 256, 256, 256, 256, 96, 90, 1, 8, 8, 1, 128,
+                                           2, 256, 256, 0.01, 32, oc.ptr, rc.ptr, 256, vc.ptr,
+                                           0.1, 0, 256, 0, 256, 1 << 30, 1, None)
+    assert st == N.QKV_E_UNSUPPORTED and "multiple of 64" in lib.qkv_last_error().decode()
+    st = lib.qkv_decode_attention_kipmixed(256, 0, 256, 256, 256, 256, 128, 90, 1, 8, 8, 1, 128,
+                                           2, 256, None, 0.01, 32, oc.ptr, rc.ptr, 256, vc.ptr,
+                                           0.1, 0, 256, 0, 256, 1 << 30, 1, None)
+    assert st == N.QKV_E_INVALID
+
+
 def test_layers_host_validation():
     lib = N.lib()
     a = N.ptr_array([256] * 33)

@@ -289,6 +289,78 @@ def test_attention_mixed_keys_pinned(golden):
     assert torch.allclose(got.double(), ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("tag", ["a", "b", "c", "d"])
+def test_mixed_ip_golden(golden, tag):
+    """mixed_ip_compress against MixedPrecisionIPQuantizer.compress's own
+    outputs (codes, QJL bits and norms bit for bit): d 128 with 32 and 64
+    outliers, d 64 with 4/3-bit channels, and an uncalibrated quantizer
+    (regular codebook everywhere)."""
+    g, cb = golden("mixed_ip"), golden("codebooks")
+    d, ob, rb, n_out, seed, calibrated = (int(v) for v in g[f"{tag}_cfg"])
+    pi, s = R.random_orthogonal(d, seed), R.random_signs(d, seed)
+    assert torch.equal(s, T(g[f"{tag}_S"]))
+    out_idx = T(g[f"{tag}_outliers"]) if calibrated else None
+    if calibrated:
+        assert out_idx.numel() == n_out
+    tabs = (T(cb[f"c_d{d}_b{ob - 1}"]), T(cb[f"t_d{d}_b{ob - 1}"]),
+            T(cb[f"c_d{d}_b{rb - 1}"]), T(cb[f"t_d{d}_b{rb - 1}"]))
+    codes, bits, norms = R.mixed_ip_compress(T(g[f"{tag}_x"]), pi, out_idx, *tabs, s)
+    assert torch.equal(codes, T(g[f"{tag}_codes"]))
+    assert torch.equal(bits, T(g[f"{tag}_qjl"]))
+    assert torch.equal(norms, T(g[f"{tag}_norm"]))
+
+
+def test_attention_mixed_ip_keys_pinned(golden):
+    """attention_mixed_ip_keys against the golden-pinned routines: with every
+    channel in one codebook (no outliers, or all outliers) it is
+    attention_naive over IP blocks, causal and not; mixed, its scores are the
+    sum of decompress_for_dot over the outlier channels with the outlier
+    codebook and over the rest with the regular one (the other channels'
+    query zeroed), through an fp64 softmax with GQA head h -> kv head h // G."""
+    cb = golden("codebooks")
+    g = torch.Generator().manual_seed(9)
+    B, H, G, Q, Tn, d = 2, 2, 3, 2, 11, 128
+    pi_k, pi_v = R.random_orthogonal(d, 42), R.random_orthogonal(d, 7)
+    s = R.random_signs(d, 42)
+    alpha = R.QJL_COEFF / d
+    c_out, c_reg, c_v = T(cb["c_d128_b2"]), T(cb["c_d128_b1"]), T(cb["c_d128_b3"])
+    kb = torch.randint(0, 2, (B, H, Tn, d), generator=g, dtype=torch.uint8)
+    vc = torch.randint(0, 8, (B, H, Tn, d), generator=g, dtype=torch.uint8)
+    kn = torch.rand(B, H, Tn, generator=g) + 0.5
+    vn = torch.rand(B, H, Tn, generator=g) + 0.5
+    # one codebook everywhere (G = 1, values un-rotated by the key Pi as the
+    # IP engine does): attention_naive, pinned by attention.npz
+    q1 = torch.randn(B, H, Q, d, generator=g)
+    for outl, c_all in ((None, c_reg), (torch.arange(d), c_out)):
+        codes = torch.randint(0, c_all.numel(), (B, H, Tn, d), generator=g, dtype=torch.uint8)
+        blk = dict(kcodes=codes, kbits=kb, knorm=kn, vcodes=vc, vnorm=vn)
+        for causal in (False, True):
+            got = R.attention_mixed_ip_keys(q1, codes, kb, kn, vc, vn, pi_k, outl, c_out, c_reg,
+                                            s, alpha, pi_k, c_v, causal=causal)
+            ref = R.attention_naive(q1, [blk], pi_k, c_all, c_v, s, alpha, causal=causal)
+            assert torch.allclose(got, ref, rtol=1e-5, atol=1e-6)
+    # mixed: per-codebook decompress_for_dot, fp64 softmax
+    out_idx = torch.arange(1, 128, 4)
+    mask = torch.zeros(d, dtype=torch.bool)
+    mask[out_idx] = True
+    kc = torch.randint(0, 2, (B, H, Tn, d), generator=g, dtype=torch.uint8)
+    kc[..., out_idx] = torch.randint(0, 4, (B, H, Tn, 32), generator=g, dtype=torch.uint8)
+    q = torch.randn(B, H * G, Q, d, generator=g)
+    got = R.attention_mixed_ip_keys(q, kc, kb, kn, vc, vn, pi_k, out_idx, c_out, c_reg, s,
+                                    alpha, pi_v, c_v)
+    q_rot = (q @ pi_k.T).reshape(B, H, G * Q, 1, d)
+    one = torch.ones(B, H, 1, Tn)
+    kc5, kb5 = kc.unsqueeze(2), kb.unsqueeze(2)
+    sc = (R.decompress_for_dot(kc5, kb5, one, q_rot * mask, c_out, s * mask, alpha)
+          + R.decompress_for_dot(kc5.clamp(max=1), kb5, one, q_rot * ~mask, c_reg, s * ~mask,
+                                 alpha))
+    sc = (kn.unsqueeze(2) * sc).double() / math.sqrt(d)
+    w = torch.softmax(sc, dim=-1)
+    v = ((c_v[vc.long()] @ pi_v) * vn.unsqueeze(-1)).double()
+    ref = (w @ v).reshape(B, H * G, Q, d)
+    assert torch.allclose(got.double(), ref, rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("d,bits", [(64, 3), (128, 3), (128, 4)])
 def test_index_golden(golden, d, bits):
     g, cb = golden("index"), golden("codebooks")
