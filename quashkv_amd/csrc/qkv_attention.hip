@@ -56,7 +56,8 @@ struct Tables {
   float kconst;      // g_empty - sum_r kg[r]
   float vg[8];       // value Walsh coefficients, odd subsets (odd_subset order)
   float vconst;      // g_empty - sum vg (the plane form's constant)
-  int mfma_ok;       // both codebooks admit the plane decomposition
+  int mfma_ok;       // both codebooks admit the plane decomposition, key MSE bits <= 2
+  int fused_ok;      // the same with key MSE bits <= 3 (decode_fused, d = 128)
   // mixed-precision keys over slots (outlier channels first), rows of whole
   // dwords:
   //   kmix 1, MSE keys 3-bit outlier / 2-bit regular (no QJL):
@@ -500,10 +501,14 @@ __host__ __device__ constexpr int krow_base(int g) {
 
 // Byte of the A-operand image (DPL MFMAs x 64 lanes x 32 bytes) holding row
 // bit p (dword p >> 5, bit p & 31) for A row m.
+// RDW = 16 (IP keys of 3 MSE bits) runs on a virtual row of five 128-bit
+// planes b0, b1, b2, b0^b1^b2 and QJL, and lane group g takes dword g of each
+// plane (it computes the parity dword from the three it loads).
 template <int DPL, int RDW>
 __device__ __forceinline__ int kf4_byte(int p, int m) {
   const int w = p >> 5, bit = p & 31;
-  const int gb = w / DPL, u = w - krow_base<DPL, RDW>(gb);
+  const int gb = RDW == 16 ? (w & 3) : w / DPL;
+  const int u = RDW == 16 ? (w >> 2) : w - krow_base<DPL, RDW>(gb);
   const int k = 32 * gb + 8 * (bit & 3) + (bit >> 2);
   const int ga = (k & 63) >> 4, ea = (k & 15) + 16 * (k >> 6);
   return (u * 64 + m + 16 * ga) * 32 + ea;
@@ -1158,8 +1163,9 @@ constexpr float kMFloor = -1e30f;  // running maxima start here (finite: no inf 
 struct FusedLds {
   static constexpr int PR4 = (128 + 4) / 4;             // padded Pi row, float4
   static constexpr int PI = 0;                          // Pi [128][PR4]
-  static constexpr int STAGE = PI + 128 * PR4 * 16;     // query operand image, <= 6 KiB
-  static constexpr int BUF = STAGE + 6 * 1024;          // [2][kTilesF][1 KiB] scores / digits
+  static constexpr int STAGE = PI + 128 * PR4 * 16;     // query operand image
+  static constexpr int STAGE_BYTES = 10 * 1024;         // up to five fp4 MFMAs per 16 tokens
+  static constexpr int BUF = STAGE + STAGE_BYTES;       // [2][kTilesF][1 KiB] scores / digits
   static constexpr int STATS = BUF + 2 * kTilesF * 1024;
   static constexpr int ROWC = STATS + 2 * int(sizeof(ChunkStats));  // [4][2] row constants
   static constexpr int RED = ROWC + 32;                 // [8] norms, [8][2] row sums
@@ -1193,16 +1199,20 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     int64_t split_len, int final_out, int out_dtype, const qkv_v4i* __restrict__ aq_ws,
     const float* __restrict__ rowc_ws, float* __restrict__ part_o, float* __restrict__ part_ml) {
   constexpr int D = 128;
-  // K rows of RDW dwords: IP keys 4 (MB + 1) (MSE planes + QJL plane), the
-  // mixed-key formats 9, 10 or 12 (the Tables comment)
-  constexpr int MB = RDW / 4 - 1;        // IP keys: MSE planes
-  constexpr int KRB = 4 * RDW;           // K row bytes
-  constexpr int DPL = (RDW + 3) / 4;     // row dwords per lane group = fp4 MFMAs per 16 tokens
-  constexpr int NU = 2 * DPL;            // operand image: NU x 256 dwords
+  // K rows of RDW dwords: IP keys 4 (mbits + 1) (MSE planes + QJL plane), the
+  // mixed-key formats 9, 10 or 12 (the Tables comment).  IP keys of 3 MSE
+  // bits (RDW = 16) weigh four virtual MSE planes b0, b1, b2, b0^b1^b2.
+  constexpr bool VROW = RDW == 16;
+  constexpr int MB = VROW ? 4 : RDW / 4 - 1;  // IP keys: weighted MSE planes
+  constexpr int KRB = 4 * RDW;                 // K row bytes
+  // fp4 MFMAs per 16 tokens = (virtual) row dwords per lane group
+  constexpr int DPL = VROW ? 5 : (RDW + 3) / 4;
+  constexpr int NLD = VROW ? 4 : DPL;          // row dwords a lane loads per token
+  constexpr int NU = 2 * DPL;                  // operand image: NU x 256 dwords
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int PR4 = FusedLds::PR4;
   constexpr int NT = kThreadsF;
-  static_assert(NU * 1024 <= 6 * 1024, "operand image");
+  static_assert(NU * 1024 <= FusedLds::STAGE_BYTES, "operand image");
   static_assert(NT == 1024 && kWavesKF == 8, "layout below assumes 8 + 8 waves");
 
   extern __shared__ __align__(16) uint8_t lds[];
@@ -1320,13 +1330,14 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   }
 
   // ---- first chunk's loads (registers)
-  uint32_t kd[4][DPL];
+  uint32_t kd[4][NLD];
   float kn[4], vnr = 0.f;
   uint32_t vw[kTilesF][VB];
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
   const int vj = 16 * wi + ln;  // value wave: coordinate of this lane
   // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
-  const uint32_t koff = ln * KRB + krow_base<DPL, RDW>(lg) * 4;  // bytes into a tile's K rows
+  // bytes into a tile's K rows (VROW: dword lg of each plane)
+  const uint32_t koff = ln * KRB + (VROW ? lg : krow_base<DPL, RDW>(lg)) * 4;
   const uint32_t voff = blk * VB * D + vj;             // words into a tile's V planes
   // contiguous store: the split's bases, a tile as a 32-bit row offset from them
   const uint8_t* kbase = kst + srow0 * KRB;
@@ -1355,7 +1366,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     for (int sub = 0; sub < 4; ++sub) {
       const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + koff + sub * 16 * KRB);
 #pragma unroll
-      for (int x = 0; x < DPL; ++x) kd[sub][x] = ldnt(krow + x);
+      for (int x = 0; x < NLD; ++x) kd[sub][x] = ldnt(krow + (VROW ? 4 * x : x));
       kn[sub] = ldnt(knb + sub * 16 + ln);
     }
     vnr = ldnt(vnb + lane);
@@ -1501,7 +1512,11 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       for (int u = 0; u < DPL; ++u) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-          const uint32_t x = kd[sub][u];
+          // VROW: planes b0, b1, b2, their parity, QJL
+          const uint32_t x = !VROW ? kd[sub][u < NLD ? u : 0]
+                             : u < 3   ? kd[sub][u]
+                             : u == 3  ? kd[sub][0] ^ kd[sub][1] ^ kd[sub][2]
+                                       : kd[sub][3];
           qkv_v8i bo;  // 32 fp4 elements (4 dwords) by bit class
           bo[0] = static_cast<int>(x & 0x11111111u);
           bo[1] = static_cast<int>(x & 0x22222222u);
@@ -2257,10 +2272,11 @@ Tables make_tables(const float* kc, int mbits, const float* vc, int vbits) {
     t.kc[i] = i < (1 << mbits) ? kc[i] : 0.f;
     t.vc[i] = i < (1 << vbits) ? vc[i] : 0.f;
   }
-  bool ok = mbits >= 1 && mbits <= 2 && vbits >= 1 && vbits <= 4;
+  bool ok = mbits >= 1 && mbits <= 3 && vbits >= 1 && vbits <= 4;
   if (ok) ok = walsh_odd(kc, mbits, t.kg, &t.kconst);
   if (ok) ok = walsh_odd(vc, vbits, t.vg, &t.vconst);
-  t.mfma_ok = ok ? 1 : 0;
+  t.fused_ok = ok ? 1 : 0;
+  t.mfma_ok = ok && mbits <= 2 ? 1 : 0;
   return t;
 }
 
@@ -2358,7 +2374,12 @@ int fused_splits(int64_t groups, int64_t T) {
 }
 
 bool use_fused(const Tables& tb, int d, int64_t t_stride) {
-  return tb.mfma_ok && d == 128 && t_stride % 64 == 0;
+  return tb.fused_ok && d == 128 && t_stride % 64 == 0;
+}
+
+// The single-call decode paths: decode_fused at d = 128, split_mfma at d = 64.
+bool use_mfma_path(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
+  return d == 128 ? use_fused(tb, d, t_stride) : use_mfma(tb, d, t_stride, T, n_splits);
 }
 
 // Launch decode_fused over nl layers (B sequences each; workspace for B * nl)
@@ -2413,6 +2434,10 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
     case 122: QKV_FU(12, 2); break;
     case 123: QKV_FU(12, 3); break;
     case 124: QKV_FU(12, 4); break;
+    case 161: QKV_FU(16, 1); break;
+    case 162: QKV_FU(16, 2); break;
+    case 163: QKV_FU(16, 3); break;
+    case 164: QKV_FU(16, 4); break;
     case 91: QKV_FUC(9, 1);
     case 92: QKV_FUC(9, 2);
     case 93: QKV_FUC(9, 3);
@@ -2479,7 +2504,7 @@ extern "C" int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
   if (!kcent_host || !vcent_host || !qkv_bits_ok(kbits) || !qkv_bits_ok(vbits) || n_splits < 1)
     return -1;
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  return use_mfma(tb, d, t_stride, T, n_splits) ? 1 : 0;
+  return use_mfma_path(tb, d, t_stride, T, n_splits) ? 1 : 0;
 }
 
 // prepare for nl layers (B sequences each; the workspace holds B * nl)
@@ -2882,9 +2907,11 @@ extern "C" int qkv_paged_decode_attention(
                   out,
               "null pointer");
   const int64_t t_stride = int64_t(pages_per_seq) << plg;
-  if (!use_mfma(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride, T, n_splits)) {
+  if (!use_mfma_path(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride, T,
+                     n_splits)) {
     qkv_set_error("paged stores decode on the MFMA path only (symmetric codebooks, key MSE "
-                  "bits <= 2, d = 64 or 128, splits of at most %d tokens)", kSplitMax);
+                  "bits <= 3 at d = 128 and <= 2 at d = 64 with splits of at most %d tokens)",
+                  kSplitMax);
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(qkv_dtype_ok(out_dtype) && qkv_aligned(pi, 16), "pi must be 16-byte aligned");
@@ -2956,10 +2983,10 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   int st = validate_common(B * n_layers, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  if (!use_mfma(tb, d, t_stride, T, n_splits)) {
+  if (!use_mfma_path(tb, d, t_stride, T, n_splits)) {
     qkv_set_error("layer-batched decode runs on the MFMA path (symmetric codebooks, key MSE "
-                  "bits <= 2, head_dim 64 or 128, capacity a multiple of 64, splits of at "
-                  "most %d tokens)", kSplitMax);
+                  "bits <= 3 at head_dim 128 and <= 2 at 64, capacity a multiple of 64, "
+                  "splits of at most %d tokens)", kSplitMax);
     return QKV_E_UNSUPPORTED;
   }
   QLayers ql{};

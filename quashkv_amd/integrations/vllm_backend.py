@@ -8,8 +8,9 @@ layers) and register_quashkv_backend (raises ImportError without vLLM).
 The reference's page manager wraps an engine of per-append tensors and never
 uses ``block_size``.  Here a layer keeps its tokens in the paged store
 (quashkv_amd.paged: pages of PAGE_TOKENS tokens from one pool, a device page
-table per sequence) whenever the paged kernels cover the configuration (head_size 64 or
-128, key_bits 2 or 3), and a contiguous-store QuashKVEngine otherwise; both
+table per sequence) whenever the paged kernels cover the configuration (head_size 128
+with key_bits 2..4, or 64 with key_bits 2 or 3), and a contiguous-store QuashKVEngine
+otherwise; both
 give the same codes and attention.  ``block_size`` must divide the page
 (vLLM blocks then map onto page slots).
 """

@@ -82,9 +82,9 @@ def _close(got, ref):
 
 
 @pytest.mark.parametrize("page_tokens", [64, 256])
-@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (2, 4)])
+@pytest.mark.parametrize("d,key_bits,value_bits", [
+    (d, kb, vb) for d in (64, 128) for kb, vb in ((3, 3), (2, 4))] + [(128, 4, 3)])
 def test_paged_matches_contiguous(d, dtype, key_bits, value_bits, page_tokens):
     B, H, G = 3, 2, 4
     seed = d + key_bits * 10 + value_bits

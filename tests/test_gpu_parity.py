@@ -372,21 +372,24 @@ def test_gqa_vs_golden(golden):
     assert_close(out, T(g["gqa_out"]), rel=1e-3, cos=0.9999)
 
 
-@pytest.mark.parametrize("d,Hkv,G,Qn,T_,causal,qdt", [
-    (128, 8, 4, 1, 3000, False, torch.bfloat16),
-    (64, 2, 7, 1, 2049, False, torch.float16),
-    (128, 2, 4, 3, 700, True, torch.float32),
-    (96, 3, 2, 2, 513, True, torch.float32),
-    (128, 1, 40, 1, 300, False, torch.float32),     # 40 rows -> two row chunks
+@pytest.mark.parametrize("d,Hkv,G,Qn,T_,causal,qdt,kb", [
+    (128, 8, 4, 1, 3000, False, torch.bfloat16, 3),
+    (64, 2, 7, 1, 2049, False, torch.float16, 3),
+    (128, 2, 4, 3, 700, True, torch.float32, 3),
+    (96, 3, 2, 2, 513, True, torch.float32, 3),
+    (128, 1, 40, 1, 300, False, torch.float32, 3),     # 40 rows -> two row chunks
+    (128, 8, 4, 1, 3000, False, torch.bfloat16, 4),    # 3-bit key MSE: parity plane
+    (128, 2, 4, 3, 700, True, torch.float32, 4),
+    (128, 1, 40, 1, 2100, False, torch.float16, 4),
 ])
-def test_attention_random_vs_oracle(d, Hkv, G, Qn, T_, causal, qdt):
+def test_attention_random_vs_oracle(d, Hkv, G, Qn, T_, causal, qdt, kb):
     gen = torch.Generator().manual_seed(T_)
     B = 2
     k = torch.randn(B, Hkv, T_, d, generator=gen)
     k[..., 3] *= 10.0
     v = torch.randn(B, Hkv, T_, d, generator=gen)
     q = torch.randn(B, Hkv * G, Qn, d, generator=gen).to(qdt)
-    eng = Q.QuashKVEngine(head_dim=d, seed=3, device=DEV, pack_storage=True)
+    eng = Q.QuashKVEngine(head_dim=d, key_bits=kb, seed=3, device=DEV, pack_storage=True)
     half = T_ // 3
     eng.append(k[:, :, :half].to(DEV), v[:, :, :half].to(DEV))
     eng.append(k[:, :, half:].to(DEV), v[:, :, half:].to(DEV))
@@ -497,8 +500,9 @@ def test_attention_d64_cfg2_shape_splits_and_paths():
     assert_close(outs[0][:3], ref.reshape(3, Hkv * G, 1, d), rel=2e-5, cos=0.999999)
 
 
-@pytest.mark.parametrize("d", [128, 64])
-@pytest.mark.parametrize("key_bits,value_bits", [(2, 1), (2, 2), (2, 4), (3, 1), (3, 2), (3, 4)])
+@pytest.mark.parametrize("d,key_bits,value_bits", [
+    (d, kb, vb) for d in (128, 64) for kb, vb in ((2, 1), (2, 2), (2, 4), (3, 1), (3, 2), (3, 4))
+] + [(128, 4, vb) for vb in (1, 2, 3, 4)])
 def test_mfma_bit_widths_vs_oracle(key_bits, value_bits, d):
     gen = torch.Generator().manual_seed(10 * key_bits + value_bits + d)
     B, Hkv, G, T_ = 2, 2, 3, 1000

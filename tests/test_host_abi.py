@@ -230,7 +230,9 @@ def test_attention_path_selection():
     k1 = N.HostFloats(LloydMaxCodebook(128, 1).centroids_host)
     assert lib.qkv_attention_path(128, 1, 3, k1.ptr, vc.ptr, 256, 256, 1) == 1
     k3 = N.HostFloats(LloydMaxCodebook(128, 3).centroids_host)
-    assert lib.qkv_attention_path(128, 3, 3, k3.ptr, vc.ptr, 256, 256, 1) == 0
+    assert lib.qkv_attention_path(128, 3, 3, k3.ptr, vc.ptr, 256, 256, 1) == 1   # parity plane
+    k3_64 = N.HostFloats(LloydMaxCodebook(64, 3).centroids_host)
+    assert lib.qkv_attention_path(64, 3, 3, k3_64.ptr, v64.ptr, 256, 256, 1) == 0
     asym = N.HostFloats([-1.0, -0.25, 0.5, 1.0])
     assert lib.qkv_attention_path(128, 2, 3, asym.ptr, vc.ptr, 256, 256, 1) == 0
 
