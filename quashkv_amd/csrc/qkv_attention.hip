@@ -501,14 +501,15 @@ __host__ __device__ constexpr int krow_base(int g) {
 
 // Byte of the A-operand image (DPL MFMAs x 64 lanes x 32 bytes) holding row
 // bit p (dword p >> 5, bit p & 31) for A row m.
-// RDW = 16 (IP keys of 3 MSE bits) runs on a virtual row of five 128-bit
-// planes b0, b1, b2, b0^b1^b2 and QJL, and lane group g takes dword g of each
-// plane (it computes the parity dword from the three it loads).
-template <int DPL, int RDW>
+// PMAJ (plane-major rows): lane group g takes dword g of each 128-bit plane
+// of a virtual row, MFMA u plane u -- IP keys of 3 MSE bits (virtual planes
+// b0, b1, b2, b0^b1^b2, QJL; the parity dword computed from the loaded ones)
+// and 96-dim rows (planes of 3 dwords; lane group 3 has no data).
+template <int DPL, int RDW, bool PMAJ>
 __device__ __forceinline__ int kf4_byte(int p, int m) {
   const int w = p >> 5, bit = p & 31;
-  const int gb = RDW == 16 ? (w & 3) : w / DPL;
-  const int u = RDW == 16 ? (w >> 2) : w - krow_base<DPL, RDW>(gb);
+  const int gb = PMAJ ? (w & 3) : w / DPL;
+  const int u = PMAJ ? (w >> 2) : w - krow_base<DPL, RDW>(gb);
   const int k = 32 * gb + 8 * (bit & 3) + (bit >> 2);
   const int ga = (k & 63) >> 4, ea = (k & 15) + 16 * (k >> 6);
   return (u * 64 + m + 16 * ga) * 32 + ea;
@@ -529,12 +530,12 @@ __device__ __forceinline__ int kf4_sigma(float wmax) {
 
 // The digit bytes of weight W at row bit p of query row r into the image sb;
 // returns W's share of the row constant.
-template <int DPL, int RDW>
+template <int DPL, int RDW, bool PMAJ>
 __device__ __forceinline__ float kf4_put(uint8_t* sb, int p, float W, int sigma, int r) {
   const uint32_t dg = fp8_digits(ldexpf(W * kf4_factor(p), -sigma));
 #pragma unroll
   for (int d = 0; d < 4; ++d)
-    sb[kf4_byte<DPL, RDW>(p, 4 * r + d)] = static_cast<uint8_t>(dg >> (8 * d));
+    sb[kf4_byte<DPL, RDW, PMAJ>(p, 4 * r + d)] = static_cast<uint8_t>(dg >> (8 * d));
   return (p & 3) == 3 ? 0.5f * W : 0.f;
 }
 
@@ -716,7 +717,7 @@ __global__ __launch_bounds__(256) void prepare_mfma(QLayers ql, int Bl, int q_dt
     // IP keys (the mixed-key formats run on decode_fused's own prologue)
     if constexpr (FP4) {
       csq[rr] = key_weights<MB>(tb, j, v, w, [&](int pb, float W) {
-        hf += kf4_put<DPL, 4 * DPL>(sb, pb, W, fq, r);
+        hf += kf4_put<DPL, 4 * DPL, false>(sb, pb, W, fq, r);
       });
     } else {
       csq[rr] = v;
@@ -1160,6 +1161,18 @@ constexpr float kMFloor = -1e30f;  // running maxima start here (finite: no inf 
 
 // Dynamic LDS of decode_fused (byte offsets).  The prologue's and the
 // epilogue's scratch rows overlay the chunk buffers.
+// Float4 i of a 128 x 128 row-major matrix holding the DS x DS matrix at src
+// in its top-left corner, zero elsewhere.
+template <int DS>
+__device__ __forceinline__ float4 pi_f4(const float4* __restrict__ src, int i) {
+  if constexpr (DS == 128) {
+    return src[i];
+  } else {
+    const int row = i >> 5, c4 = i & 31;
+    return row < DS && c4 < DS / 4 ? src[row * (DS / 4) + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
 struct FusedLds {
   static constexpr int PR4 = (128 + 4) / 4;             // padded Pi row, float4
   static constexpr int PI = 0;                          // Pi [128][PR4]
@@ -1192,22 +1205,30 @@ __device__ __forceinline__ T ldnt(const T* p) {
 // final_out != 0 and one split: write the attention output through ol;
 // else split partials (part_o, part_ml) for combine_kernel.
 // PAGED: the store is a page pool addressed through kv.ptab.
-template <int RDW, int VB, bool PAGED>
+template <int RDW, int VB, bool PAGED, int DS>
 __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     QLayers ql, KVLayers kv, OutLayers ol, int Bl, int q_dtype, float alpha, int Hq, int Hkv,
     int Q, int R, int chunks, Tables tb, int64_t t_stride, int64_t T, float scale, int causal,
     int64_t split_len, int final_out, int out_dtype, const qkv_v4i* __restrict__ aq_ws,
     const float* __restrict__ rowc_ws, float* __restrict__ part_o, float* __restrict__ part_ml) {
+  // DS: the stored head dim, 128 or 96; the operands are 128 wide, the
+  // coordinates past DS zero (query, Pi and S padded in the prologue)
   constexpr int D = 128;
-  // K rows of RDW dwords: IP keys 4 (mbits + 1) (MSE planes + QJL plane), the
-  // mixed-key formats 9, 10 or 12 (the Tables comment).  IP keys of 3 MSE
-  // bits (RDW = 16) weigh four virtual MSE planes b0, b1, b2, b0^b1^b2.
-  constexpr bool VROW = RDW == 16;
-  constexpr int MB = VROW ? 4 : RDW / 4 - 1;  // IP keys: weighted MSE planes
+  static_assert(DS == 128 || DS == 96, "stored head dim");
+  constexpr int PD = DS / 32;  // dwords per stored plane
+  // K rows of RDW dwords: IP keys PD (mbits + 1) (MSE planes + QJL plane), at
+  // d = 128 also the mixed-key formats of 9, 10 or 12 dwords (the Tables
+  // comment).  Plane-major (PMAJ) rows: 3 MSE bits (weighing four virtual MSE
+  // planes b0, b1, b2, b0^b1^b2) or d = 96.
+  constexpr bool PMAJ = DS != 128 || RDW == 16;
+  constexpr int NPS = PMAJ ? RDW / PD : 0;    // stored planes of a plane-major row
+  constexpr bool PAR = PMAJ && NPS == 4;      // 3 MSE bits: the parity plane is computed
+  constexpr int MB = PMAJ ? (PAR ? 4 : NPS - 1) : RDW / 4 - 1;  // IP keys: weighted MSE planes
   constexpr int KRB = 4 * RDW;                 // K row bytes
   // fp4 MFMAs per 16 tokens = (virtual) row dwords per lane group
-  constexpr int DPL = VROW ? 5 : (RDW + 3) / 4;
-  constexpr int NLD = VROW ? 4 : DPL;          // row dwords a lane loads per token
+  constexpr int DPL = PMAJ ? MB + 1 : (RDW + 3) / 4;
+  constexpr int NLD = PMAJ ? NPS : DPL;        // row dwords a lane loads per token
+  static_assert(!PMAJ || NPS * PD == RDW, "whole planes");
   constexpr int NU = 2 * DPL;                  // operand image: NU x 256 dwords
   constexpr int NP = n_odd_subsets(VB);  // value planes
   constexpr int PR4 = FusedLds::PR4;
@@ -1293,15 +1314,15 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     const float4* src = reinterpret_cast<const float4*>(ql.pi[layer]);
     float4 pst[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) pst[x] = src[tid + NT * x];
+    for (int x = 0; x < 4; ++x) pst[x] = pi_f4<DS>(src, tid + NT * x);
     float qv = 0.f;
-    if (ppart < nr) {
+    if (ppart < nr && pj < DS) {
       const int row = r0 + ppart;
       const int g = row / Q, qi = row - g * Q;
       const int h = hkv * G + g;
-      qv = qkv_load(ql.q[layer], ((int64_t(b) * Hq + h) * Q + qi) * D + pj, q_dtype);
+      qv = qkv_load(ql.q[layer], ((int64_t(b) * Hq + h) * Q + qi) * DS + pj, q_dtype);
     }
-    const float sgn = ql.signs[layer][pj];
+    const float sgn = pj < DS ? ql.signs[layer][pj] : 0.f;
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const int i = tid + NT * x, row = i >> 5, c4 = i & 31;
@@ -1309,7 +1330,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     }
     if (ppart < kRowsM) qs[ppart * D + pj] = qv;
     if (ppart == 0) sgns[pj] = sgn;
-    if constexpr (RDW % 4 != 0) {  // operand bytes no row dword feeds stay zero
+    if constexpr (!PMAJ && RDW % 4 != 0) {  // operand bytes no row dword feeds stay zero
 #pragma unroll
       for (int x = 0; x < (NU * 256 + NT - 1) / NT; ++x)
         if (tid + NT * x < NU * 256) stage[tid + NT * x] = 0u;
@@ -1336,14 +1357,17 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   const int blk = lg >> 1, hsh = 4 * (lg & 1);
   const int vj = 16 * wi + ln;  // value wave: coordinate of this lane
   // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
-  // bytes into a tile's K rows (VROW: dword lg of each plane)
-  const uint32_t koff = ln * KRB + (VROW ? lg : krow_base<DPL, RDW>(lg)) * 4;
-  const uint32_t voff = blk * VB * D + vj;             // words into a tile's V planes
+  // bytes into a tile's K rows (PMAJ: dword lg of each plane; lane group 3 of
+  // a 96-dim row re-reads group 2's, under zero operand bytes)
+  const uint32_t koff = ln * KRB + (PMAJ ? min(lg, PD - 1) : krow_base<DPL, RDW>(lg)) * 4;
+  // words into a tile's V planes (coordinates past DS read coordinate DS - 1
+  // and give zero)
+  const uint32_t voff = blk * VB * DS + min(vj, DS - 1);
   // contiguous store: the split's bases, a tile as a 32-bit row offset from them
   const uint8_t* kbase = kst + srow0 * KRB;
   const float* knbase = knorm + srow0;
   const float* vnbase = vnorm + srow0;
-  const uint32_t* vbase = vst + (srow0 >> 5) * (VB * D);  // srow0 is a multiple of 64
+  const uint32_t* vbase = vst + (srow0 >> 5) * (VB * DS);  // srow0 is a multiple of 64
   auto trow = [&](int tile) -> uint32_t {
     return ntiles > 0 ? static_cast<uint32_t>(min(tile, ntiles - 1)) * 64u : 0u;
   };
@@ -1366,7 +1390,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     for (int sub = 0; sub < 4; ++sub) {
       const uint32_t* krow = reinterpret_cast<const uint32_t*>(kb + koff + sub * 16 * KRB);
 #pragma unroll
-      for (int x = 0; x < NLD; ++x) kd[sub][x] = ldnt(krow + (VROW ? 4 * x : x));
+      for (int x = 0; x < NLD; ++x) kd[sub][x] = ldnt(krow + (PMAJ ? PD * x : x));
       kn[sub] = ldnt(knb + sub * 16 + ln);
     }
     vnr = ldnt(vnb + lane);
@@ -1374,11 +1398,11 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   auto loadV = [&](int slot, int tile) {
     const uint32_t* vb;  // the tile's first V tile
     if constexpr (PAGED)
-      vb = vst + (tile_row(tile) >> 5) * (VB * D);
+      vb = vst + (tile_row(tile) >> 5) * (VB * DS);
     else
-      vb = vbase + (trow(tile) >> 5) * (VB * D);
+      vb = vbase + (trow(tile) >> 5) * (VB * DS);
 #pragma unroll
-    for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * D);
+    for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * DS);
   };
   if (keyw) {
     loadK(wi);
@@ -1428,7 +1452,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
       float hf = 0.f;  // this coordinate's share of the row constant (bit class 3)
       const float csq = key_weights<MB>(tb, pj, v, w, [&](int p, float W) {
-        hf += kf4_put<DPL, RDW>(sb, p, W, sig, r);
+        hf += kf4_put<DPL, RDW, PMAJ>(sb, p, W, sig, r);
       });
       // row constants: sums over j (row r = waves 2r, 2r + 1) into red[8 ..]
       const float a = wave_sum_dpp(csq);
@@ -1512,8 +1536,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       for (int u = 0; u < DPL; ++u) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-          // VROW: planes b0, b1, b2, their parity, QJL
-          const uint32_t x = !VROW ? kd[sub][u < NLD ? u : 0]
+          // PAR: planes b0, b1, b2, their parity, QJL
+          const uint32_t x = !PAR ? kd[sub][u < NLD ? u : 0]
                              : u < 3   ? kd[sub][u]
                              : u == 3  ? kd[sub][0] ^ kd[sub][1] ^ kd[sub][2]
                                        : kd[sub][3];
@@ -1698,7 +1722,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     if (!(final_out && gridDim.x == 1)) {
       lds_sync();
       const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
-      if (lg < nr) part_o[(base + lg) * D + vj] = orun;
+      if (lg < nr && vj < DS) part_o[(base + lg) * DS + vj] = orun;
     }
   }
 
@@ -1712,7 +1736,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       float l = lred[lg];
 #pragma unroll
       for (int w = 1; w < kWavesKF; ++w) l += lred[w * kRowsM + lg];
-      obuf[lg * D + vj] = lg < nr ? orun / fmaxf(l, 1e-8f) : 0.f;
+      obuf[lg * D + vj] = lg < nr && vj < DS ? orun / fmaxf(l, 1e-8f) : 0.f;
     }
     const float* piv = ol.pi[layer];
     if (!pro || piv != ql.pi[layer]) {  // values un-rotate by their own Pi
@@ -1720,7 +1744,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
 #pragma unroll
       for (int x = 0; x < 4; ++x) {
         const int i = tid + NT * x, row = i >> 5, c4 = i & 31;
-        pis[row * PR4 + c4] = src[i];
+        pis[row * PR4 + c4] = pi_f4<DS>(src, i);
       }
     }
     lds_sync();
@@ -1741,13 +1765,13 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     lds_sync();
     if (tid < 512) {
       const int r = tid >> 7, j = tid & (D - 1);
-      if (r < nr) {
+      if (r < nr && j < DS) {
         const float o = (opart[(0 * kRowsM + r) * D + j] + opart[(1 * kRowsM + r) * D + j]) +
                         (opart[(2 * kRowsM + r) * D + j] + opart[(3 * kRowsM + r) * D + j]);
         const int row = r0 + r;
         const int g = row / Q, qi = row - g * Q;
         const int h = hkv * G + g;
-        qkv_store(ol.out[layer], ((int64_t(b) * Hq + h) * Q + qi) * D + j, o, out_dtype);
+        qkv_store(ol.out[layer], ((int64_t(b) * Hq + h) * Q + qi) * DS + j, o, out_dtype);
       }
     }
   }
@@ -2374,26 +2398,27 @@ int fused_splits(int64_t groups, int64_t T) {
 }
 
 bool use_fused(const Tables& tb, int d, int64_t t_stride) {
-  return tb.fused_ok && d == 128 && t_stride % 64 == 0;
+  return tb.fused_ok && (d == 128 || d == 96) && t_stride % 64 == 0;
 }
 
-// The single-call decode paths: decode_fused at d = 128, split_mfma at d = 64.
+// The single-call decode paths: decode_fused at d = 128 and 96, split_mfma at
+// d = 64.
 bool use_mfma_path(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
-  return d == 128 ? use_fused(tb, d, t_stride) : use_mfma(tb, d, t_stride, T, n_splits);
+  return d == 64 ? use_mfma(tb, d, t_stride, T, n_splits) : use_fused(tb, d, t_stride);
 }
 
 // Launch decode_fused over nl layers (B sequences each; workspace for B * nl)
-// on K rows of rdw dwords: 4 (kbits + 1) for IP keys of kbits MSE bits,
-// kmixed_rdw() for the mixed-key formats.  pro: query operands computed in the
+// at head dim d (128 or 96) on K rows of rdw dwords: (d / 32) (kbits + 1) for
+// IP keys of kbits MSE bits, kmixed_rdw() for the mixed-key formats.  pro: query operands computed in the
 // kernel (else prepare_mfma's, from the workspace).  final_out with one split: the kernel writes the output (ol);
 // otherwise it writes split partials and the caller runs combine_layers.
 int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int nl, int B,
-                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int rdw, int vbits,
-                 const Tables& tb, int64_t t_stride, int64_t T, float scale, int causal,
-                 int n_splits, int final_out, int out_dtype, void* workspace, bool pro,
-                 hipStream_t s) {
+                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int d, int rdw,
+                 int vbits, const Tables& tb, int64_t t_stride, int64_t T, float scale,
+                 int causal, int n_splits, int final_out, int out_dtype, void* workspace,
+                 bool pro, hipStream_t s) {
   const int R = (Hq / Hkv) * Q;
-  const WsLayout L = ws_layout(B * nl, Hkv, R, 128, n_splits);
+  const WsLayout L = ws_layout(B * nl, Hkv, R, d, n_splits);
   const int chunks = (R + kRowsM - 1) / kRowsM;
   const int64_t split_len = ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
   const dim3 grid(n_splits, Hkv * chunks, B * nl);
@@ -2402,16 +2427,17 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
   float* po = at<float>(workspace, L.po);
   float* pml = at<float>(workspace, L.pml);
   constexpr uint32_t smem = FusedLds::TOTAL;
-#define QKV_FU2(RW, VB, PG)                                                                    \
+#define QKV_FU3(RW, VB, PG, DSV)                                                               \
   do {                                                                                         \
     static const hipError_t attr_ = hipFuncSetAttribute(                                       \
-        reinterpret_cast<const void*>(&decode_fused<RW, VB, PG>),                              \
+        reinterpret_cast<const void*>(&decode_fused<RW, VB, PG, DSV>),                         \
         hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem));                   \
     QKV_HIP(attr_);                                                                            \
-    hipLaunchKernelGGL((decode_fused<RW, VB, PG>), grid, dim3(kThreadsF), smem, s, ql, kv, ol, \
-                       B, q_dtype, alpha, Hq, Hkv, Q, R, chunks, tb, t_stride, T, scale,       \
-                       causal, split_len, final_out, out_dtype, aq, rowc, po, pml);            \
+    hipLaunchKernelGGL((decode_fused<RW, VB, PG, DSV>), grid, dim3(kThreadsF), smem, s, ql,   \
+                       kv, ol, B, q_dtype, alpha, Hq, Hkv, Q, R, chunks, tb, t_stride, T,      \
+                       scale, causal, split_len, final_out, out_dtype, aq, rowc, po, pml);     \
   } while (0)
+#define QKV_FU2(RW, VB, PG) QKV_FU3(RW, VB, PG, 128)
 #define QKV_FU(RW, VB)              \
   do {                              \
     if (kv.ptab)                    \
@@ -2419,12 +2445,38 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
     else                            \
       QKV_FU2(RW, VB, false);       \
   } while (0)
-  // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) have no
-  // paged store
-  QKV_REQUIRE(rdw % 4 == 0 || kv.ptab == nullptr, "mixed keys are not paged");
+  // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) and
+  // 96-dim rows have no paged store
+  QKV_REQUIRE((rdw % 4 == 0 && d == 128) || kv.ptab == nullptr,
+              "mixed keys and head_dim 96 are not paged");
 #define QKV_FUC(RW, VB)    \
   QKV_FU2(RW, VB, false);  \
   break
+#define QKV_FU96(RW, VB)              \
+  QKV_FU3(RW, VB, false, 96);         \
+  break
+  if (d == 96) {
+    switch (rdw * 10 + vbits) {
+      case 61: QKV_FU96(6, 1);
+      case 62: QKV_FU96(6, 2);
+      case 63: QKV_FU96(6, 3);
+      case 64: QKV_FU96(6, 4);
+      case 91: QKV_FU96(9, 1);
+      case 92: QKV_FU96(9, 2);
+      case 93: QKV_FU96(9, 3);
+      case 94: QKV_FU96(9, 4);
+      case 121: QKV_FU96(12, 1);
+      case 122: QKV_FU96(12, 2);
+      case 123: QKV_FU96(12, 3);
+      case 124: QKV_FU96(12, 4);
+      default:
+        qkv_set_error("fused decode (d = 96): K rows of %d dwords / value bits %d unsupported",
+                      rdw, vbits);
+        return QKV_E_UNSUPPORTED;
+    }
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
   switch (rdw * 10 + vbits) {
     case 81: QKV_FU(8, 1); break;
     case 82: QKV_FU(8, 2); break;
@@ -2450,9 +2502,11 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
       qkv_set_error("fused decode: K rows of %d dwords / value bits %d unsupported", rdw, vbits);
       return QKV_E_UNSUPPORTED;
   }
+#undef QKV_FU96
 #undef QKV_FUC
 #undef QKV_FU
 #undef QKV_FU2
+#undef QKV_FU3
   QKV_LAUNCHED();
   return QKV_OK;
 }
@@ -2465,7 +2519,8 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
                                         int32_t d, int64_t T) {
   if (B <= 0 || Hkv <= 0 || Hq <= 0 || Q <= 0 || T <= 0) return 1;
   const int R = (Hq / Hkv) * Q;
-  if (d == 128) return fused_splits(int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM), T);
+  if (d == 128 || d == 96)
+    return fused_splits(int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM), T);
   const int rc = mfma_rc(d, R);
   const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM * rc - 1) / (kRowsM * rc));
   const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
@@ -2606,7 +2661,7 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
   float* pml = at<float>(workspace, L.pml);
   if (use_mfma(tb, d, t_stride, T, n_splits) && d == 128) {
     // the fused kernel in partial mode: operands from prepare_mfma, split partials out
-    return launch_fused(QLayers{}, kv, OutLayers{}, nl, B, QKV_F32, 0.f, Hq, Hkv, Q,
+    return launch_fused(QLayers{}, kv, OutLayers{}, nl, B, QKV_F32, 0.f, Hq, Hkv, Q, d,
                         4 * (kbits + 1),
                         vbits, tb, t_stride, T, scale, causal, n_splits, 0, QKV_F32, workspace,
                         false, s);
@@ -2799,8 +2854,8 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
     ol.pi[0] = pi;
     ol.out[0] = out;
     auto s = static_cast<hipStream_t>(stream);
-    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1), vbits,
-                      tb,
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
+                      (d / 32) * (kbits + 1), vbits, tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
     return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
@@ -2907,10 +2962,11 @@ extern "C" int qkv_paged_decode_attention(
                   out,
               "null pointer");
   const int64_t t_stride = int64_t(pages_per_seq) << plg;
-  if (!use_mfma_path(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride, T,
-                     n_splits)) {
-    qkv_set_error("paged stores decode on the MFMA path only (symmetric codebooks, key MSE "
-                  "bits <= 3 at d = 128 and <= 2 at d = 64 with splits of at most %d tokens)",
+  if (d == 96 || !use_mfma_path(make_tables(kcent_host, kbits, vcent_host, vbits), d,
+                                t_stride, T, n_splits)) {
+    qkv_set_error("paged stores decode on the MFMA path only (d = 128 or 64, symmetric "
+                  "codebooks, key MSE bits <= 3 at d = 128 and <= 2 at d = 64 with splits of "
+                  "at most %d tokens)",
                   kSplitMax);
     return QKV_E_UNSUPPORTED;
   }
@@ -2933,7 +2989,8 @@ extern "C" int qkv_paged_decode_attention(
     ol.pi[0] = pi;
     ol.out[0] = out;
     auto s = static_cast<hipStream_t>(stream);
-    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1), vbits,
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
+                      (d / 32) * (kbits + 1), vbits,
                       make_tables(kcent_host, kbits, vcent_host, vbits), t_stride, T, scale,
                       causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
@@ -3009,8 +3066,8 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.npages = num_pages;
   auto s = static_cast<hipStream_t>(stream);
   if (d == 128) {
-    st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, 4 * (kbits + 1),
-                      vbits, tb,
+    st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
+                      (d / 32) * (kbits + 1), vbits, tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
     if (st != QKV_OK || n_splits == 1) return st;
     return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
@@ -3113,7 +3170,7 @@ int kmixed_decode_impl(int kind, const void* q, int32_t q_dtype, const uint8_t* 
   ol.pi[0] = pi_v;
   ol.out[0] = out;
   auto s = static_cast<hipStream_t>(stream);
-  st = launch_fused(ql, kv, ol, 1, B, q_dtype, kind == 1 ? 0.f : qjl_scale, Hq, Hkv, Q,
+  st = launch_fused(ql, kv, ol, 1, B, q_dtype, kind == 1 ? 0.f : qjl_scale, Hq, Hkv, Q, d,
                     kmixed_rdw(kind, n_out), vbits, tb, t_stride, T, scale, causal, n_splits, 1,
                     out_dtype, workspace, true, s);
   if (st != QKV_OK || n_splits == 1) return st;

@@ -381,6 +381,9 @@ def test_gqa_vs_golden(golden):
     (128, 8, 4, 1, 3000, False, torch.bfloat16, 4),    # 3-bit key MSE: parity plane
     (128, 2, 4, 3, 700, True, torch.float32, 4),
     (128, 1, 40, 1, 2100, False, torch.float16, 4),
+    (96, 4, 4, 1, 2500, False, torch.bfloat16, 3),     # d = 96: zero-padded operands
+    (96, 2, 1, 3, 900, True, torch.float32, 4),
+    (96, 2, 7, 1, 1100, False, torch.float16, 2),
 ])
 def test_attention_random_vs_oracle(d, Hkv, G, Qn, T_, causal, qdt, kb):
     gen = torch.Generator().manual_seed(T_)
@@ -502,7 +505,7 @@ def test_attention_d64_cfg2_shape_splits_and_paths():
 
 @pytest.mark.parametrize("d,key_bits,value_bits", [
     (d, kb, vb) for d in (128, 64) for kb, vb in ((2, 1), (2, 2), (2, 4), (3, 1), (3, 2), (3, 4))
-] + [(128, 4, vb) for vb in (1, 2, 3, 4)])
+] + [(128, 4, vb) for vb in (1, 2, 3, 4)] + [(96, kb, vb) for kb in (2, 3, 4) for vb in (1, 4)])
 def test_mfma_bit_widths_vs_oracle(key_bits, value_bits, d):
     gen = torch.Generator().manual_seed(10 * key_bits + value_bits + d)
     B, Hkv, G, T_ = 2, 2, 3, 1000

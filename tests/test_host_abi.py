@@ -218,7 +218,8 @@ def test_attention_path_selection():
     assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 1
     assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 1) == 1   # fused: any split
     assert lib.qkv_attention_path(128, 2, 3, kc.ptr, vc.ptr, 8160, 8150, 8) == 0   # stride % 64
-    assert lib.qkv_attention_path(96, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 0
+    assert lib.qkv_attention_path(96, 2, 3, kc.ptr, vc.ptr, 8192, 8192, 4) == 1   # fused, padded
+    assert lib.qkv_attention_path(96, 2, 3, kc.ptr, vc.ptr, 8160, 8150, 4) == 0
     k64 = N.HostFloats(LloydMaxCodebook(64, 2).centroids_host)
     v64 = N.HostFloats(LloydMaxCodebook(64, 3).centroids_host)
     assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 2048, 2048, 2) == 1
