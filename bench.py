@@ -186,6 +186,51 @@ def make_inputs(seed: int, dev, gen_dtype):
     return k.to(gen_dtype), v.to(gen_dtype)
 
 
+def compress_fp32(args, dev, stream) -> dict:
+    """The compress paths on fp32 rows at the cfg3 shape (2^21 K and 2^21 V
+    token-heads): the engine append (fused, fp32 rows split hi + lo for the
+    fp16 MFMA) into the packed store, and the reference's quantizer operators
+    InnerProductQuantizer.compress (keys) + MSEQuantizer.compress (values),
+    which return one uint8 code (and QJL bit) per coordinate
+    (qkv_compress_mfma).  Rooflines: the bytes each moves at 8 TB/s."""
+    import torch
+    import quashkv_amd as Q
+
+    k, v = make_inputs(11, dev, torch.float32)
+    eng = Q.QuashKVEngine(head_dim=D, key_bits=KEY_BITS, value_bits=VAL_BITS, seed=42,
+                          device=dev, capacity=T)
+
+    def append():
+        eng.clear()
+        eng.append(k, v)
+
+    for _ in range(5):
+        append()
+    app_ms = statistics.median(event_ms(append, args.compress_reps, stream))
+    kq, vq = eng.key_quantizer, eng.value_quantizer
+    api = lambda: (kq.compress(k), vq.compress(v))
+    for _ in range(3):
+        api()
+    api_ms = statistics.median(event_ms(api, args.compress_reps, stream))
+    n_th = B * HKV * T
+    n_vec = 2 * n_th
+    app_bytes = n_vec * D * 4 + n_th * kv_bytes_per_token_head(D)
+    api_bytes = n_vec * (D * 4 + 4) + n_th * (2 * D + D)   # codes (+ QJL bits) one byte each
+    del k, v, eng
+    return {
+        "what": "cfg3-shaped fp32 K/V (2^21 token-heads each): the engine append into the "
+                "packed store, and InnerProductQuantizer.compress + MSEQuantizer.compress "
+                "(unpacked uint8 codes) on the MFMA compress",
+        "append_gvec_s": round(n_vec / (app_ms * 1e-3) / 1e9, 4),
+        "append_pct_of_hbm_roofline": round(100 * app_bytes / (app_ms * 1e-3) / 1e9
+                                            / PEAK_HBM_GBS, 2),
+        "append_roofline_gvec_s": round(n_vec * PEAK_HBM_GBS * 1e9 / app_bytes / 1e9, 2),
+        "quantizer_api_gvec_s": round(n_vec / (api_ms * 1e-3) / 1e9, 4),
+        "quantizer_api_pct_of_hbm_roofline": round(100 * api_bytes / (api_ms * 1e-3) / 1e9
+                                                   / PEAK_HBM_GBS, 2),
+    }
+
+
 def cpu_baseline(eng, q, n_batch: int, reps: int):
     """Oracle online-softmax decode on the first n_batch sequences of the cache;
     also returns the GPU output's relative error against it."""
@@ -959,6 +1004,7 @@ def main() -> None:
             "us": round(dec_ms * 1e3, 1), "GB_s": round(dec_gbs, 1),
             "pct_of_hbm_peak": round(100 * dec_gbs / PEAK_HBM_GBS, 2), "bytes": dec_bytes,
         }
+        line["compress_fp32"] = compress_fp32(args, dev, stream)
         line["paged"] = paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h,
                                      kv_bytes)
         line["hf_attention_cfg2"] = hf_decode_step(args, dev, stream)

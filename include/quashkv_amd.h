@@ -114,13 +114,28 @@ int qkv_ip_dot(const uint8_t* codes, const uint8_t* qjl, const float* norms,
  *   codes      grouped rows of qkv_packed_row_bytes(d, bits) (or d if unpacked)
  *   qjl        grouped rows of the 1-bit QJL signs (IP only)
  *   norms      grouped fp32 norms max(||x||, 1e-8) (ignored if PRE_ROTATED)
- *   out_seq, out_group_stride  grouped-row addressing of codes/qjl/norms */
+ *   out_seq, out_group_stride  grouped-row addressing of codes/qjl/norms
+ * This is the VALU kernel for any d, tables and flags; d = 128 / 64 with
+ * symmetric codebooks run faster on qkv_compress_mfma below. */
 int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
                  const void* x, int64_t n, int32_t d,
                  const float* pi, const float* boundaries,
                  const float* centroids, int32_t bits, const float* signs,
                  uint8_t* codes, uint8_t* qjl, float* norms,
                  int64_t out_seq, int64_t out_group_stride, void* stream);
+
+/* qkv_compress's unpacked output (one uint8 code, and for IP one QJL bit, per
+ * coordinate at grouped rows; norms max(||x||, 1e-8)) on the MFMA, for the
+ * same reference operators (quashkv/quantizer.py:113-131, 211-242,
+ * quashkv/triton_kernels/compress.py:210-303): the rotation, search and tie
+ * rules of qkv_store_append.  d = 128 or 64; cent_host / bound_host are HOST
+ * copies of the codebook (2^bits centroids, 2^bits - 1 boundaries), which
+ * must be symmetric about 0 (else QKV_E_UNSUPPORTED, as for other d or bits
+ * beyond 1..3 (IP) / 1..4 (MSE)); x and pi 16-byte aligned. */
+int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, int64_t n, int32_t d,
+                      const float* pi, const float* cent_host, const float* bound_host,
+                      int32_t bits, const float* signs, uint8_t* codes, uint8_t* qjl,
+                      float* norms, int64_t out_seq, int64_t out_group_stride, void* stream);
 
 /* Fused decompress: unpack -> centroid gather [+ alpha S (2b-1)] -> Pi -> *norm.
  * Replaces fused_decompress_mse / fused_decompress_ip
@@ -212,9 +227,10 @@ int qkv_vtiles_pack(const uint8_t* codes, int64_t groups, int64_t S, int32_t d,
  * Replaces the compress half of QuashKVEngine.append (quashkv/engine.py:
  * 145-172: InnerProductQuantizer.compress for keys, quashkv/quantizer.py:
  * 211-242, MSEQuantizer.compress for values, quashkv/quantizer.py:113-131).
- *   in_dtype   QKV_BF16 or QKV_F16 (others: QKV_E_UNSUPPORTED)
- *   keys, values  groups x S x 128 rows, 16-byte aligned; either may be NULL
- *              to append only the other
+ *   in_dtype   QKV_BF16, QKV_F16 or QKV_F32 (fp32 rows are divided by their
+ *              norm first and split into fp16 hi + lo for the fp16 MFMA)
+ *   keys, values  groups x S x d rows (d = 128 or 64), 16-byte aligned;
+ *              either may be NULL to append only the other
  *   mbits      key MSE bits (1..3; key total bits - 1), vbits value bits (1..4)
  *   kcent_host, kbound_host  HOST arrays of the key MSE codebook (2^mbits
  *              centroids, 2^mbits - 1 boundaries; must be symmetric);
@@ -223,7 +239,7 @@ int qkv_vtiles_pack(const uint8_t* codes, int64_t groups, int64_t S, int32_t d,
  *              [t0, t0 + S) of every group are written, all others kept
  * Codes equal the reference's except where the rotated value lies within
  * ~1e-5 relative of a boundary (the rotation carries ~16 significant bits of
- * Pi for bf16 inputs, ~22 for fp16). */
+ * Pi for bf16 inputs, ~22 for fp16 and fp32). */
 int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
                      int64_t groups, int64_t S, int32_t d, int32_t mbits,
                      int32_t vbits, const float* pi, const float* signs,
@@ -416,7 +432,7 @@ int qkv_kipmixed_unpack(const uint8_t* src, int64_t n, const int32_t* perm_host,
                         int32_t n_out, int64_t seq, int64_t group_stride, uint8_t* codes,
                         uint8_t* qjl, void* stream);
 
-/* Fused compress of bf16 / fp16 keys (groups x S x 128) straight into
+/* Fused compress of bf16, fp16 or fp32 keys (groups x S x 128) straight into
  * kmixed rows and norms at tokens [t0, t0 + S) of each group: the key half of
  * qkv_store_append with MixedPrecisionMSEQuantizer.compress
  * (quashkv/mixed_precision.py:132-158) in place of InnerProductQuantizer.
@@ -439,7 +455,7 @@ int qkv_store_append_kmixed_rotated(const float* y_slots, const float* norm_in, 
                                     uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
                                     void* stream);
 
-/* Fused compress of bf16 / fp16 keys into kipmixed rows and norms:
+/* Fused compress of bf16, fp16 or fp32 keys into kipmixed rows and norms:
  * MixedPrecisionIPQuantizer.compress (quashkv/mixed_precision.py:271-297) --
  * per-channel boundary codes, QJL bit [(y - c[code]) S >= 0] -- straight into
  * the store.  out_cent_host (4) / out_bound_host (3): HOST 2-bit outlier

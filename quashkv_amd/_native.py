@@ -43,6 +43,8 @@ _SIGS = {
                             _p, _p, _p, _i64, _i64, _p]),
     "qkv_decompress": (_i32, [_i32, _i32, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p, _f32,
                               _i64, _i64, _p, _i32, _p]),
+    "qkv_compress_mfma": (_i32, [_i32, _i32, _p, _i64, _i32, _p, _p, _p, _i32, _p, _p, _p, _p,
+                                 _i64, _i64, _p]),
     "qkv_kplanes_row_bytes": (_i64, [_i32, _i32, _i32]),
     "qkv_vtiles_bytes": (_i64, [_i32, _i32, _i64]),
     "qkv_kplanes_pack": (_i32, [_p, _p, _i64, _i32, _i32, _p, _i64, _i64, _i64, _p]),
@@ -230,6 +232,22 @@ class HostFloats:
     @property
     def ptr(self) -> int:
         return ctypes.addressof(self.arr)
+
+
+_HOST_TABLES: dict = {}
+
+
+def host_table(t: torch.Tensor) -> HostFloats:
+    """A host copy of a small device table (codebook centroids / boundaries),
+    cached per tensor storage and version: the first use of a table costs one
+    device-to-host copy, later calls none."""
+    key = (t.data_ptr(), t._version, t.numel(), str(t.device), t.dtype)
+    h = _HOST_TABLES.get(key)
+    if h is None:
+        if len(_HOST_TABLES) > 256:
+            _HOST_TABLES.clear()
+        h = _HOST_TABLES[key] = HostFloats(t.detach().float().cpu().reshape(-1).tolist())
+    return h
 
 
 class HostInts:

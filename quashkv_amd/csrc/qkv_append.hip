@@ -1,6 +1,6 @@
-// Fused compress straight into the cache store, for bf16 / fp16 K and V rows
-// with d = 128 or 64: normalise -> rotate (MFMA) -> Lloyd-Max boundary search ->
-// QJL sign -> bit planes, one pass over the inputs.
+// Fused compress straight into the cache store, for bf16, fp16 or fp32 K and V
+// rows with d = 128 or 64: normalise -> rotate (MFMA) -> Lloyd-Max boundary
+// search -> QJL sign -> bit planes, one pass over the inputs.
 //
 // Reference: QuashKVEngine.append (quashkv/engine.py:145-172) compresses keys
 // with InnerProductQuantizer.compress (quashkv/quantizer.py:211-242) and values
@@ -14,9 +14,11 @@
 // a high and a low 16-bit part, Pi ~= Pi_hi + Pi_lo, accumulated in fp32: two
 // MFMA passes carry ~16 (bf16) / ~22 (fp16) significant bits of Pi, against
 // 24 for the reference's fp32 GEMM, and y = z / |x| (the reference divides
-// before the GEMM).  Codes computed from x may therefore differ from the
-// reference's where y lies within ~1e-5 relative of a boundary (about 1e-6 of
-// the coordinates).  The same kernels take a given fp32 y instead of x
+// before the GEMM).  fp32 rows are divided first, as the reference does:
+// x 2^8 / |x| is split into fp16 hi + lo and the fp16 MFMA sums hi Pi_hi +
+// hi Pi_lo + lo Pi_hi (~22 significant bits).  Codes computed from x may
+// therefore differ from the reference's where y lies within ~1e-5 (bf16 /
+// fp16 rows) or ~1e-6 (fp32 rows) relative of a boundary.  The same kernels take a given fp32 y instead of x
 // (FROM_Y: the *_rotated entry points) and then run the search, QJL and store
 // code below on it; from an identical y the codes are the reference's, bit for
 // bit, ties included.
@@ -130,9 +132,8 @@ __device__ __forceinline__ void static_for(F&& f) {
 // of #{j : t[j] < a} as the lane mask g[i].  With CLAST the last level (whose
 // candidates are the list's even entries) compares ac instead of a.
 template <int LM, bool CLAST>
-__device__ __forceinline__ void search_keys(uint32_t a, uint32_t ac, const uint32_t* t,
-                                            uint64_t (&g)[LM]) {
-  bool c[LM];
+__device__ __forceinline__ void search_levels(uint32_t a, uint32_t ac, const uint32_t* t,
+                                              bool (&c)[LM]) {
   static_for<LM>([&](auto kc) {
     constexpr int k = decltype(kc)::value;  // level k decides bit LM - 1 - k
     uint32_t cand[1 << k];
@@ -147,6 +148,13 @@ __device__ __forceinline__ void search_keys(uint32_t a, uint32_t ac, const uint3
     const uint32_t av = (CLAST && k == LM - 1) ? ac : a;
     c[LM - 1 - k] = av > cand[0];
   });
+}
+
+template <int LM, bool CLAST>
+__device__ __forceinline__ void search_keys(uint32_t a, uint32_t ac, const uint32_t* t,
+                                            uint64_t (&g)[LM]) {
+  bool c[LM];
+  search_levels<LM, CLAST>(a, ac, t, c);
 #pragma unroll
   for (int i = 0; i < LM; ++i) g[i] = lanes_where(c[i]);
 }
@@ -171,6 +179,22 @@ __device__ __forceinline__ void search_sym(float y, const uint32_t* p, uint32_t 
 #pragma unroll
     for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
   }
+}
+
+// search_sym's count for this lane alone (no lane masks).
+template <int L, bool CLAST>
+__device__ __forceinline__ uint32_t search_sym_count(float y, const uint32_t* p, uint32_t cx) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, y);
+  const bool pos = static_cast<int32_t>(u) > 0;
+  uint32_t f = pos ? 1u << (L - 1) : 0u;
+  if constexpr (L > 1) {
+    const uint32_t a = __builtin_amdgcn_alignbit(u, u, 31);
+    bool c[L - 1];
+    search_levels<L - 1, CLAST>(a, a ^ cx, p, c);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) f |= (c[i] == pos ? 1u : 0u) << i;
+  }
+  return f;
 }
 
 typedef __bf16 qkv_bf16x2 __attribute__((ext_vector_type(2)));
@@ -267,6 +291,60 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
       xf[tt][s] = *reinterpret_cast<const uint4*>(row[tt] + 16 * s + 8 * (lane >> 5));
 }
 
+// fp32 rows for the fp16 MFMA: x 2^8 / |x| = hi + lo, both fp16, in load_x's
+// fragment layout (xh, xl).  The rotation then sums hi Pi_hi + hi Pi_lo +
+// lo Pi_hi (Pi' = 2^8 Pi split likewise), ~22 significant bits, and the MFMA
+// result is 2^16 y.  |x| (clamped at 1e-8, as the reference clamps) of the
+// lane's token row per block in nrm.
+template <int NKS>
+__device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl)[kHalves][NKS],
+                                           float (&nrm)[kHalves],
+                                           const float* const (&row)[kHalves], int lane) {
+#pragma unroll
+  for (int tt = 0; tt < kHalves; ++tt) {
+    float4 v[NKS][2];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const float* p = row[tt] + 16 * s + 8 * (lane >> 5);
+      v[s][0] = *reinterpret_cast<const float4*>(p);
+      v[s][1] = *reinterpret_cast<const float4*>(p + 4);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ss = fmaf(v[s][h].x, v[s][h].x, ss);
+        ss = fmaf(v[s][h].y, v[s][h].y, ss);
+        ss = fmaf(v[s][h].z, v[s][h].z, ss);
+        ss = fmaf(v[s][h].w, v[s][h].w, ss);
+      }
+    ss += __shfl_xor(ss, 32, 64);
+    const float n = fmaxf(sqrtf(ss), 1e-8f);
+    nrm[tt] = n;
+    const float sc = 256.f / n;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const float a[8] = {v[s][0].x, v[s][0].y, v[s][0].z, v[s][0].w,
+                          v[s][1].x, v[s][1].y, v[s][1].z, v[s][1].w};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = a[2 * e] * sc, a1 = a[2 * e + 1] * sc;
+        const _Float16 h0 = static_cast<_Float16>(a0), h1 = static_cast<_Float16>(a1);
+        const _Float16 l0 = static_cast<_Float16>(a0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(a1 - static_cast<float>(h1));
+        hw[e] = __builtin_bit_cast(uint16_t, h0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lw[e] = __builtin_bit_cast(uint16_t, l0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+      }
+      xh[tt][s] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      xl[tt][s] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ keys
 
 // One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
@@ -274,12 +352,14 @@ __device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
 // MB MSE planes, then the QJL plane).  FROM_Y: `xin` holds fp32 rotated unit
 // rows y (rows as above) and `nin` their norms; the normalisation and the
 // rotation are skipped, everything after them is the same code.
-template <int MB, bool F16, int D, bool PAGED, bool FROM_Y>
+// XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
+template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
 __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
     QkvPages pg) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NP = (1 << MB) - 1;   // positive half of the fine list c_0, t_0, ..., c_{2^MB-1}
   constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
@@ -316,6 +396,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
     QkvSpan sp{};
     if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, t0 + s0);
     uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
     if constexpr (FROM_Y) {
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt)
@@ -325,29 +406,45 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
           if (r >= 0) knorm[r] = nin[grp * S + s0 + 32 * tt + li];
         }
     } else {
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
 #pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
-      load_x<NKS>(xf, row, lane);
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+        load_x_f32<NKS>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+        load_x<NKS>(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
 
-      // norms; 1 / n of token t goes to LDS, read back in C-row order (rows
-      // 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four consecutive tokens)
+      // norms; the scale of token t's MFMA result (1 / n, or 2^-16 for fp32
+      // rows scaled before the rotation) goes to LDS, read back in C-row order
+      // (rows 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four
+      // consecutive tokens)
       float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
-        float ss = 0.f;
-#pragma unroll
-        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-        ss += __shfl_xor(ss, 32, 64);
-        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
         if (lane < 32) {
           if (32 * tt + li < nv) {
             const int64_t t = t0 + s0 + 32 * tt + li;
             const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-            if (r >= 0) knorm[r] = nrm;
+            if (r >= 0) knorm[r] = nrm[tt];
           }
-          invw[32 * tt + li] = iscale / nrm;
+          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
         }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
@@ -382,7 +479,10 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
           for (int sp2 = 0; sp2 < 2; ++sp2) {
             const uint4 bf = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
 #pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+              if (F32 && sp2 == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+            }
           }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
@@ -453,12 +553,13 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
 // The outlier slots fill whole 32-slot blocks (NO = 32 or 64), so each block's
 // codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
 // rows in slot order and `nin` their norms.
-template <int NO, bool F16, bool FROM_Y, bool IPM>
+template <int NO, int XT, bool FROM_Y, bool IPM>
 __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
     int64_t t0) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;        // fp16 MFMA / fp32 rows split for it
   constexpr int NOB = NO / 32;                         // outlier blocks
   constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
   constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
@@ -495,28 +596,42 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
     float* nrow = knorm + grp * t_stride + t0 + s0;
     uint4 xf[kHalves][8];
+    uint4 xl[kHalves][F32 ? 8 : 1];  // fp32 rows: the low fp16 parts
     if constexpr (FROM_Y) {
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt)
         if (lane < 32 && 32 * tt + li < nv) nrow[32 * tt + li] = nin[grp * S + s0 + 32 * tt + li];
     } else {
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
 #pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-      load_x(xf, row, lane);
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+        load_x_f32<8>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+        load_x(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
       float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
-        float ss = 0.f;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-        ss += __shfl_xor(ss, 32, 64);
-        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
         if (lane < 32) {
-          if (32 * tt + li < nv) nrow[32 * tt + li] = nrm;
-          invw[32 * tt + li] = iscale / nrm;
+          if (32 * tt + li < nv) nrow[32 * tt + li] = nrm[tt];
+          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
         }
       }
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
@@ -548,7 +663,10 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
           for (int sp = 0; sp < 2; ++sp) {
             const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
 #pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+              if (F32 && sp == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+            }
           }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
@@ -620,17 +738,136 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
   }
 }
 
+// ------------------------------------------------ quantizer-API compress
+
+// MSEQuantizer.compress / InnerProductQuantizer.compress and fused_compress_*
+// (quashkv/quantizer.py:113-131,211-242, quashkv/triton_kernels/compress.py:
+// 210-303) on the MFMA: n rows of dimension D into one uint8 code (and, IP,
+// one QJL bit) per coordinate, row-major at grouped rows (seq, gstride), and
+// the fp32 norms.  The rotation, search and tie rules are append_k_mfma's
+// (tokens x coordinates); IP searches the fine list (L = MB + 1 levels), MSE
+// the boundaries (L = bits levels).  A lane's code byte lands beside its
+// 31 neighbours' (32 coordinates of one row per half-wave).
+template <int L, bool IP, int XT, int D>
+__global__ __launch_bounds__(kThreads, 2) void compress_mfma(
+    const void* __restrict__ xin, int64_t n, int64_t ntiles, const float* __restrict__ pi,
+    const float* __restrict__ signs, Half lst, uint8_t* __restrict__ codes,
+    uint8_t* __restrict__ qjl, float* __restrict__ norms, int64_t seq, int64_t gstride) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;
+  constexpr int NP = (1 << (L - 1)) - 1;  // positive half of the searched list
+  constexpr int NBK = D / 32, NKS = D / 16;
+  __shared__ uint4 frag[frag_n<D>()];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  uint32_t lv[NP > 0 ? NP : 1];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) lv[i] = in_vgpr(lst.t[i]);
+  uint32_t cx[NBK];  // IP: 1 where S >= 0 (the centroid level counts c <= y there)
+  uint32_t neg[NBK];  // IP: 1 where S < 0
+#pragma unroll
+  for (int b = 0; b < NBK; ++b) {
+    const bool ng = IP && signs[32 * b + li] < 0.f;
+    cx[b] = ng ? 0u : 1u;
+    neg[b] = ng ? 1u : 0u;
+  }
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
+
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
+    const int64_t s0 = tile * kTok;
+    const int nv = static_cast<int>(min<int64_t>(kTok, n - s0));
+    uint4 xf[kHalves][NKS];
+    uint4 xl[kHalves][F32 ? NKS : 1];
+    float nrm[kHalves];
+    if constexpr (F32) {
+      const float* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = static_cast<const float*>(xin) + (s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x_f32<NKS>(xf, xl, nrm, row, lane);
+    } else {
+      const uint16_t* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = static_cast<const uint16_t*>(xin) + (s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x<NKS>(xf, row, lane);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+      }
+    }
+    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+#pragma unroll
+    for (int tt = 0; tt < kHalves; ++tt) {
+      if (lane < 32) {
+        if (32 * tt + li < nv) norms[qkv_grouped_row(s0 + 32 * tt + li, seq, gstride)] = nrm[tt];
+        invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+
+    static_for<NBK>([&](auto nc) {  // coordinates 32 b .. 32 b + 31
+      constexpr int b = decltype(nc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+      for (int s = 0; s < NKS; ++s)
+#pragma unroll
+        for (int sp2 = 0; sp2 < 2; ++sp2) {
+          const uint4 bf = frag[((b * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt) {
+            acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+            if (F32 && sp2 == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+          }
+        }
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float4 iv4[4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float4 q4 = iv4[v >> 2];
+          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+          // token 32 tt + 8 (v >> 2) + 4 (l >> 5) + (v & 3), coordinate 32 b + (l & 31)
+          const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          const uint32_t f = search_sym_count<L, IP>(acc[tt][v] * iv, lv, cx[b]);
+          if (tk < nv) {
+            const int64_t o = qkv_grouped_row(s0 + tk, seq, gstride) * D + 32 * b + li;
+            if constexpr (IP) {
+              codes[o] = static_cast<uint8_t>(f >> 1);
+              qjl[o] = static_cast<uint8_t>((f & 1u) ^ neg[b]);
+            } else {
+              codes[o] = static_cast<uint8_t>(f);
+            }
+          }
+        }
+      }
+    });
+  }
+}
+
 // ---------------------------------------------------------------- values
 
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
 // so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
 // already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
 // their norms.
-template <int VB, bool F16, int D, bool PAGED, bool FROM_Y>
+template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
 __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
@@ -666,6 +903,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
       src[tt] = grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1);
     }
     uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
     float inv[kHalves];      // token 32 tt + (l & 31): the C-column of this lane
     if constexpr (FROM_Y) {
 #pragma unroll
@@ -676,24 +914,36 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
           if (r >= 0) vnorm[r] = nin[src[tt]];
         }
     } else {
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
 #pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
-      load_x<NKS>(xf, row, lane);
+        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+        load_x_f32<NKS>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+        load_x<NKS>(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
-        float ss = 0.f;
-#pragma unroll
-        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-        ss += __shfl_xor(ss, 32, 64);
-        const float nrm = fmaxf(sqrtf(ss), 1e-8f);
         if (lane < 32 && ok[tt]) {
           const int64_t t = A0 + 32 * tt + li;
           const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0) vnorm[r] = nrm;
+          if (r >= 0) vnorm[r] = nrm[tt];
         }
-        inv[tt] = iscale / nrm;
+        inv[tt] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
       }
     }
 
@@ -721,7 +971,10 @@ __global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
           for (int sp2 = 0; sp2 < 2; ++sp2) {
             const uint4 af = frag[((mb * NKS + s) * 2 + sp2) * 64 + lane];
 #pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
+              if (F32 && sp2 == 0) acc[tt] = mma<F16>(af, xl[tt][F32 ? s : 0], acc[tt]);
+            }
           }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt)
@@ -813,10 +1066,7 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
                 "page table of %d pages of %d tokens per sequence must hold tokens "
                 "[%lld, %lld)", pg.pmax, 1 << pg.lg, (long long)t0, (long long)(t0 + S));
   }
-  if (!rotated && in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
-    qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
-    return QKV_E_UNSUPPORTED;
-  }
+  QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
   if (d != 128 && d != 64) {
     qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
     return QKV_E_UNSUPPORTED;
@@ -867,13 +1117,13 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   }
   if (groups == 0 || S == 0) return QKV_OK;
   auto s = static_cast<hipStream_t>(stream);
-  const bool f16 = in_dtype == QKV_F16;
+  const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;  // the kernels' XT
   if (keys) {
     const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
     const dim3 grid(append_blocks(ntiles));
 #define QKV_K(MB, F, DD)                                                                       \
   if (rotated)                                                                                 \
-    hipLaunchKernelGGL((append_k_mfma<MB, false, DD, false, true>), grid, dim3(kThreads), 0, s, \
+    hipLaunchKernelGGL((append_k_mfma<MB, 0, DD, false, true>), grid, dim3(kThreads), 0, s,     \
                        keys, knorm_in, S, tpg, ntiles, pi, signs, fine, kstore, knorm,          \
                        t_stride, t0, pg);                                                      \
   else if (pg.tab)                                                                             \
@@ -885,13 +1135,16 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
                        keys, nullptr, S, tpg, ntiles, pi, signs, fine, kstore, knorm,           \
                        t_stride, t0, pg)
 #define QKV_KD(DD)                                  \
-  switch (mbits * 2 + (f16 ? 1 : 0)) {              \
-    case 2: QKV_K(1, false, DD); break;             \
-    case 3: QKV_K(1, true, DD); break;              \
-    case 4: QKV_K(2, false, DD); break;             \
-    case 5: QKV_K(2, true, DD); break;              \
-    case 6: QKV_K(3, false, DD); break;             \
-    case 7: QKV_K(3, true, DD); break;              \
+  switch (mbits * 3 + xt) {                         \
+    case 3: QKV_K(1, 0, DD); break;                 \
+    case 4: QKV_K(1, 1, DD); break;                 \
+    case 5: QKV_K(1, 2, DD); break;                 \
+    case 6: QKV_K(2, 0, DD); break;                 \
+    case 7: QKV_K(2, 1, DD); break;                 \
+    case 8: QKV_K(2, 2, DD); break;                 \
+    case 9: QKV_K(3, 0, DD); break;                 \
+    case 10: QKV_K(3, 1, DD); break;                \
+    case 11: QKV_K(3, 2, DD); break;                \
   }
     if (d == 128) {
       QKV_KD(128)
@@ -908,7 +1161,7 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
     const dim3 grid(append_blocks(ntiles));
 #define QKV_V(VB, F, DD)                                                                       \
   if (rotated)                                                                                 \
-    hipLaunchKernelGGL((append_v_mfma<VB, false, DD, false, true>), grid, dim3(kThreads), 0, s, \
+    hipLaunchKernelGGL((append_v_mfma<VB, 0, DD, false, true>), grid, dim3(kThreads), 0, s,     \
                        values, vnorm_in, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,  \
                        pg);                                                                    \
   else if (pg.tab)                                                                             \
@@ -920,15 +1173,19 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
                        values, nullptr, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,   \
                        pg)
 #define QKV_VD(DD)                                  \
-  switch (vbits * 2 + (f16 ? 1 : 0)) {              \
-    case 2: QKV_V(1, false, DD); break;             \
-    case 3: QKV_V(1, true, DD); break;              \
-    case 4: QKV_V(2, false, DD); break;             \
-    case 5: QKV_V(2, true, DD); break;              \
-    case 6: QKV_V(3, false, DD); break;             \
-    case 7: QKV_V(3, true, DD); break;              \
-    case 8: QKV_V(4, false, DD); break;             \
-    case 9: QKV_V(4, true, DD); break;              \
+  switch (vbits * 3 + xt) {                         \
+    case 3: QKV_V(1, 0, DD); break;                 \
+    case 4: QKV_V(1, 1, DD); break;                 \
+    case 5: QKV_V(1, 2, DD); break;                 \
+    case 6: QKV_V(2, 0, DD); break;                 \
+    case 7: QKV_V(2, 1, DD); break;                 \
+    case 8: QKV_V(2, 2, DD); break;                 \
+    case 9: QKV_V(3, 0, DD); break;                 \
+    case 10: QKV_V(3, 1, DD); break;                \
+    case 11: QKV_V(3, 2, DD); break;                \
+    case 12: QKV_V(4, 0, DD); break;                \
+    case 13: QKV_V(4, 1, DD); break;                \
+    case 14: QKV_V(4, 2, DD); break;                \
   }
     if (d == 128) {
       QKV_VD(128)
@@ -968,10 +1225,7 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
   QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
-  if (!rotated && in_dtype != QKV_BF16 && in_dtype != QKV_F16) {
-    qkv_set_error("store append runs on bf16 / fp16 inputs (got dtype %d)", in_dtype);
-    return QKV_E_UNSUPPORTED;
-  }
+  QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
   if (d != kD || (n_out != 32 && n_out != 64)) {
     qkv_set_error("mixed-precision keys run on head_dim 128 with 32 or 64 outlier channels");
     return QKV_E_UNSUPPORTED;
@@ -982,7 +1236,7 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
               "null pointer");
   QKV_REQUIRE(qkv_aligned(keys, rotated ? 4 : 16) && qkv_aligned(kstore, 4) &&
                   (rotated || qkv_aligned(pi_perm, 16)),
-              "keys / pi aligned (16-B bf16 / fp16 rows, 4-B fp32 rows) and store 4-B aligned");
+              "keys / pi aligned (16-B input rows, 4-B rotated rows) and store 4-B aligned");
   float lo[7], lr[3];
   if (ipm) {
     fine_list(out_cent_host, out_bound_host, 2, lo);
@@ -1005,7 +1259,7 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
   auto s = static_cast<hipStream_t>(stream);
   const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
   const dim3 grid(append_blocks(ntiles));
-  const bool f16 = in_dtype == QKV_F16;
+  const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;  // the kernel's XT
 #define QKV_KM(NOV, F, FY, IP)                                                                 \
   hipLaunchKernelGGL((append_kmix_mfma<NOV, F, FY, IP>), grid, dim3(kThreads), 0, s, keys,     \
                      norm_in, S, tpg, ntiles, pi_perm, signs_perm, po, pr, kstore, knorm,      \
@@ -1013,11 +1267,13 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
 #define QKV_KM_IN(NOV, IP)                \
   do {                                    \
     if (rotated)                          \
-      QKV_KM(NOV, false, true, IP);       \
-    else if (f16)                         \
-      QKV_KM(NOV, true, false, IP);       \
+      QKV_KM(NOV, 0, true, IP);           \
+    else if (xt == 2)                     \
+      QKV_KM(NOV, 2, false, IP);          \
+    else if (xt == 1)                     \
+      QKV_KM(NOV, 1, false, IP);          \
     else                                  \
-      QKV_KM(NOV, false, false, IP);      \
+      QKV_KM(NOV, 0, false, IP);          \
   } while (0)
   if (n_out == 32) {
     if (ipm) QKV_KM_IN(32, true);
@@ -1126,4 +1382,82 @@ extern "C" int qkv_store_append_kipmixed_rotated(const float* y_slots, const flo
   return kmixed_append_impl(QKV_F32, y_slots, true, norm_in, groups, S, d, nullptr, n_out, true,
                             signs_perm, out_cent_host, reg_cent_host, out_bound_host,
                             reg_bound_host, kstore, knorm, t_stride, t0, stream);
+}
+
+extern "C" int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, int64_t n,
+                                 int32_t d, const float* pi, const float* cent_host,
+                                 const float* bound_host, int32_t bits, const float* signs,
+                                 uint8_t* codes, uint8_t* qjl, float* norms, int64_t out_seq,
+                                 int64_t out_group_stride, void* stream) {
+  QKV_REQUIRE(mode == QKV_MODE_MSE || mode == QKV_MODE_IP, "mode must be MSE or IP");
+  QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
+  QKV_REQUIRE(n >= 0, "negative row count");
+  const bool ip = mode == QKV_MODE_IP;
+  if ((d != 128 && d != 64) || bits < 1 || bits > (ip ? 3 : 4)) {
+    qkv_set_error("MFMA compress runs on head_dim 128 or 64 with %s bits in 1..%d",
+                  ip ? "key MSE" : "value", ip ? 3 : 4);
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(pi && bound_host && (!ip || (cent_host && signs)), "null pointer");
+  // the searched list: IP the fine list c_0 < t_0 < ... < c_{2^bits-1}, MSE the boundaries
+  float lst[15];
+  int nl;
+  if (ip) {
+    nl = fine_list(cent_host, bound_host, bits, lst);
+  } else {
+    nl = (1 << bits) - 1;
+    for (int i = 0; i < nl; ++i) lst[i] = bound_host[i];
+  }
+  bool asc = true;
+  for (int i = 0; i + 1 < nl; ++i) asc = asc && lst[i] < lst[i + 1];
+  Half h{};
+  if (!asc || !symmetric(lst, nl) || !positive_half(lst, nl, &h)) {
+    qkv_set_error("MFMA compress needs a codebook symmetric about 0%s",
+                  ip ? " with c_i < t_i < c_{i+1}" : "");
+    return QKV_E_UNSUPPORTED;
+  }
+  if (n == 0) return QKV_OK;
+  const int64_t seq = out_seq > 0 ? out_seq : n;
+  const int64_t gst = out_group_stride > 0 ? out_group_stride : seq;
+  QKV_REQUIRE(x && codes && norms && (!ip || qjl), "null pointer");
+  QKV_REQUIRE(qkv_aligned(x, 16) && qkv_aligned(pi, 16), "x rows and pi must be 16-byte aligned");
+  QKV_REQUIRE(gst >= seq, "bad grouped-row layout");
+  auto s = static_cast<hipStream_t>(stream);
+  const int64_t ntiles = (n + kTok - 1) / kTok;
+  const dim3 grid(append_blocks(ntiles));
+  const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;
+#define QKV_C(LV, IPV, XTV, DD)                                                                 \
+  hipLaunchKernelGGL((compress_mfma<LV, IPV, XTV, DD>), grid, dim3(kThreads), 0, s, x, n,      \
+                     ntiles, pi, signs, h, codes, qjl, norms, seq, gst)
+#define QKV_CX(LV, IPV, DD)        \
+  do {                             \
+    if (xt == 2)                   \
+      QKV_C(LV, IPV, 2, DD);       \
+    else if (xt == 1)              \
+      QKV_C(LV, IPV, 1, DD);       \
+    else                           \
+      QKV_C(LV, IPV, 0, DD);       \
+  } while (0)
+#define QKV_CD(DD)                                         \
+  do {                                                     \
+    if (ip) {                                              \
+      if (bits == 1) QKV_CX(2, true, DD);                  \
+      else if (bits == 2) QKV_CX(3, true, DD);             \
+      else QKV_CX(4, true, DD);                            \
+    } else {                                               \
+      if (bits == 1) QKV_CX(1, false, DD);                 \
+      else if (bits == 2) QKV_CX(2, false, DD);            \
+      else if (bits == 3) QKV_CX(3, false, DD);            \
+      else QKV_CX(4, false, DD);                           \
+    }                                                      \
+  } while (0)
+  if (d == 128)
+    QKV_CD(128);
+  else
+    QKV_CD(64);
+#undef QKV_CD
+#undef QKV_CX
+#undef QKV_C
+  QKV_LAUNCHED();
+  return QKV_OK;
 }

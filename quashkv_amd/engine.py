@@ -168,9 +168,11 @@ class QuashKVEngine:
         self._total_tokens += S
 
     def _append_fused(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
-        """bf16 / fp16 rows at head_dim 128 or 64: compress straight into the
-        store (qkv_store_append).  False when that kernel does not cover the call."""
-        if (keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype
+        """bf16, fp16 or fp32 rows at head_dim 128 or 64: compress straight into
+        the store (qkv_store_append).  False when that kernel does not cover the
+        call."""
+        if (keys.dtype not in (torch.bfloat16, torch.float16, torch.float32)
+                or values.dtype != keys.dtype
                 or self.head_dim not in (64, 128) or not 2 <= self.key_bits <= 4):
             return False
         B, H, S, d = keys.shape
@@ -233,7 +235,7 @@ class QuashKVEngine:
         return sp
 
     def _append_kmix(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
-        """Mixed-precision keys: bf16 / fp16 rows straight into kmixed /
+        """Mixed-precision keys: bf16, fp16 or fp32 rows straight into kmixed /
         kipmixed rows (qkv_store_append_kmixed / _kipmixed); other dtypes
         through qkv_compress_mixed and the row packers.  Values as in the
         IP-key engine."""
@@ -248,7 +250,8 @@ class QuashKVEngine:
         L = N.lib()
         stream = N.stream(keys.device)
         n = B * H * S
-        fused = keys.dtype in (torch.bfloat16, torch.float16) and values.dtype == keys.dtype
+        fused = (keys.dtype in (torch.bfloat16, torch.float16, torch.float32)
+                 and values.dtype == keys.dtype)
         if fused:
             k, v = keys.contiguous(), values.contiguous()
             dt = N.dtype_code(k.dtype)

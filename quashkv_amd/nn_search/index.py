@@ -83,7 +83,8 @@ class QuashIndex:
         L = N.lib()
         stream = N.stream(dev)
         done = False
-        if x.dtype in (torch.bfloat16, torch.float16) and self.dim == 128 and 2 <= self.bits <= 4:
+        if (x.dtype in (torch.bfloat16, torch.float16, torch.float32) and self.dim in (64, 128)
+                and 2 <= self.bits <= 4):
             kc, kb, _ = self._host_tables()
             st = L.qkv_store_append(N.dtype_code(x.dtype), x.data_ptr(), None, 1, n, self.dim,
                                     q.mse_bits, 1, mq.Pi.data_ptr(), q.S.data_ptr(), kc.ptr,

@@ -16,7 +16,7 @@ ABI "Paged cache store"), with n = page_tokens:
 page ``table[b, t // n]``.  Larger pages keep more of a sequence's K/V
 contiguous in HBM (better DRAM locality when pages are scattered); smaller
 ones waste less of the last page.  The append kernels (qkv_paged_store_append)
-compress bf16 / fp16 K/V straight into the pages; the split-K decode kernel
+compress bf16, fp16 or fp32 K/V straight into the pages; the split-K decode kernel
 (qkv_paged_decode_attention) follows the table per 32-token tile.  Pages come
 from a free list and return to it on clear(); a reused page keeps its old
 bits until tokens overwrite them (appends write whole K rows and merge V
@@ -255,8 +255,9 @@ class PagedQuashKVEngine(QuashKVEngine):
         self._total_tokens += S
 
     def _append_paged(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
-        """bf16 / fp16 K/V straight into the pages (qkv_paged_store_append)."""
-        if keys.dtype not in (torch.bfloat16, torch.float16) or values.dtype != keys.dtype:
+        """bf16, fp16 or fp32 K/V straight into the pages (qkv_paged_store_append)."""
+        if (keys.dtype not in (torch.bfloat16, torch.float16, torch.float32)
+                or values.dtype != keys.dtype):
             return False
         B, H, S, d = keys.shape
         kq, vq = self.key_quantizer, self.value_quantizer

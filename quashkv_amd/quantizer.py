@@ -55,8 +55,15 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
                   centroids: torch.Tensor, bits: int, signs: Optional[torch.Tensor],
                   codes: torch.Tensor, qjl: Optional[torch.Tensor], norms: Optional[torch.Tensor],
                   packed: bool, out_seq: Optional[int] = None,
-                  out_group_stride: Optional[int] = None, pre_rotated: bool = False) -> None:
-    """Run the fused compress kernel, writing into caller-owned buffers."""
+                  out_group_stride: Optional[int] = None, pre_rotated: bool = False,
+                  host_tables: Optional[tuple] = None) -> None:
+    """Run the fused compress, writing into caller-owned buffers.
+
+    Rows of head_dim 128 or 64 with a symmetric codebook run on the MFMA
+    compress (qkv_compress_mfma; packed outputs through the bit packer after
+    it); other shapes, pre-rotated rows and asymmetric tables on the VALU
+    kernel (qkv_compress).  ``host_tables`` = (centroids, boundaries) host
+    copies (N.HostFloats) spare the one-time copy of the device tables."""
     d = pi.shape[0]
     dev = N.require_gpu(x, pi, codes, what="compress")
     xf = _flat_rows(x, d)
@@ -71,7 +78,34 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
     if not pre_rotated:
         N.require_extent(norms, rows * 4, "compress norms")
     pi, boundaries, centroids, signs = N.dense(pi, boundaries, centroids, signs)
-    N.check(N.lib().qkv_compress(
+    L = N.lib()
+    if (not pre_rotated and d in (64, 128) and n > 0 and xf.data_ptr() % 16 == 0
+            and (not packed or seq == n)):
+        ip = mode == N.QKV_MODE_IP
+        if host_tables is not None:
+            ch, bh = host_tables
+        else:   # the MSE search reads the boundaries only
+            bh = N.host_table(boundaries)
+            ch = N.host_table(centroids) if ip else bh
+        if packed:   # unpacked codes first, then the bit packer
+            c_out = torch.empty(n, d, dtype=torch.uint8, device=dev)
+            q_out = torch.empty(n, d, dtype=torch.uint8, device=dev) if ip else None
+        else:
+            c_out, q_out = codes, qjl
+        st = L.qkv_compress_mfma(mode, N.dtype_code(xf.dtype), xf.data_ptr(), n, d, pi.data_ptr(),
+                                 ch.ptr, bh.ptr, bits, N.ptr(signs), c_out.data_ptr(),
+                                 N.ptr(q_out), norms.data_ptr(), seq, gst, N.stream(dev))
+        if st == N.QKV_OK:
+            if packed:
+                N.check(L.qkv_pack_bits(c_out.data_ptr(), codes.data_ptr(), n, d, bits,
+                                        N.stream(dev)))
+                if ip:
+                    N.check(L.qkv_pack_bits(q_out.data_ptr(), qjl.data_ptr(), n, d, 1,
+                                            N.stream(dev)))
+            return
+        if st != N.QKV_E_UNSUPPORTED:
+            N.check(st)
+    N.check(L.qkv_compress(
         mode, N.dtype_code(xf.dtype), flags, xf.data_ptr(), n, d, N.ptr(pi),
         boundaries.data_ptr(), centroids.data_ptr(), bits, N.ptr(signs), codes.data_ptr(),
         N.ptr(qjl), N.ptr(norms), seq, gst, N.stream(dev)))

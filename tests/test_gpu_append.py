@@ -50,7 +50,7 @@ def _mismatch(a, b):
 
 
 @pytest.mark.parametrize("d", [128, 64])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (2, 1), (4, 4), (3, 2)])
 def test_store_append_matches_unfused_path(dtype, key_bits, value_bits, d):
     gen = torch.Generator().manual_seed(key_bits * 10 + value_bits + d)
@@ -73,7 +73,7 @@ def test_store_append_matches_unfused_path(dtype, key_bits, value_bits, d):
 
 
 @pytest.mark.parametrize("d", [128, 64])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_store_append_vs_oracle(dtype, d):
     """Codes and norms against the CPU restatement of compress_ip / compress_mse
     (quashkv/quantizer.py:113-131, 211-242) on the same (upcast) inputs."""
@@ -92,9 +92,11 @@ def test_store_append_vs_oracle(dtype, d):
                                   mq.codebook.centroids.cpu())
     ovc, ovn = R.compress_mse(v.float().reshape(-1, d), vq.Pi.cpu(),
                               vq.codebook.boundaries.cpu())
+    # fp32 rows are split hi + lo for the fp16 MFMA: ~22 bits, fewer near-ties
+    bar = 2e-5 if dtype == torch.float32 else 1e-4
     for got, ref in ((kc, okc), (kb, okb), (vc, ovc)):
         rate, step = _mismatch(got.reshape(-1, d), ref.reshape(-1, d))
-        assert rate <= 1e-4 and step <= 1, (rate, step)
+        assert rate <= bar and step <= 1, (rate, step)
     for got, ref in ((st.knorm[:, :, :S], okn), (st.vnorm[:, :, :S], ovn)):
         got, ref = got.cpu().double().reshape(-1), ref.double().reshape(-1)
         assert float(((got - ref).abs() / ref).max()) <= 2e-6

@@ -1,0 +1,161 @@
+"""GPU parity of the MFMA compress behind the reference's quantizer operators:
+MSEQuantizer.compress / InnerProductQuantizer.compress and fused_compress_mse
+/ fused_compress_ip (quashkv/quantizer.py:113-131, 211-242,
+quashkv/triton_kernels/compress.py:210-303) through qkv_compress_mfma, and
+QuashIndex.add on fp32 rows through the fused store append.
+
+Bars: codes against the oracle's compress_mse / compress_ip on the same
+(upcast) inputs with a mismatch rate <= 1e-4 (bf16 / fp16 rows; <= 2e-5 for
+fp32 rows, split hi + lo for the fp16 MFMA), every mismatch one code step;
+norms within 2e-6 relative; the unpacked codes equal, bit for bit, what the
+fused store append writes from the same rows (the same rotation and search);
+packed and grouped outputs equal the packer and the dense layout exactly."""
+
+import pytest
+import torch
+
+import quashkv_amd as Q
+from quashkv_amd import _native as N
+from quashkv_amd import kernels as K
+from quashkv_amd.packing import pack_bits
+from quashkv_amd.quantizer import compress_into
+from oracle import ref_math as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(autouse=True, scope="module")
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+    N.lib()
+
+
+def _x(n, d, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, d, generator=g) * torch.exp(torch.randn(n, 1, generator=g))
+    x[:, [c for c in (3, 29, 61) if c < d]] *= 10.0
+    x[7] = 0.0                                   # a zero row: norm clamped at 1e-8
+    return x.to(dtype)
+
+
+def _mismatch(a, b):
+    a, b = a.cpu().to(torch.int16), b.cpu().to(torch.int16)
+    diff = (a - b).abs()
+    return float((diff != 0).double().mean()), int(diff.max()) if diff.numel() else 0
+
+
+def _bar(dtype):
+    return 2e-5 if dtype == torch.float32 else 1e-4
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("bits", [1, 2, 3, 4])
+def test_mse_compress_vs_oracle(d, dtype, bits):
+    n = 6000 + d + bits                       # not a multiple of the 32-row tile
+    x = _x(n, d, dtype, 10 * bits + d)
+    q = Q.MSEQuantizer(d, bits=bits, seed=42, device=DEV)
+    codes, norms = q.compress(x.to(DEV))
+    oc, on = R.compress_mse(x.float(), q.Pi.cpu(), q.codebook.boundaries.cpu())
+    rate, step = _mismatch(codes, oc)
+    assert rate <= _bar(dtype) and step <= 1, (rate, step)
+    got, ref = norms.cpu().double(), on.double()
+    assert float(((got - ref).abs() / ref).max()) <= 2e-6
+    # fused_compress_mse (device tables, host copies cached) gives the same
+    c2, n2 = K.fused_compress_mse(x.to(DEV), q.Pi, q.codebook.boundaries)
+    assert torch.equal(c2, codes) and torch.equal(n2, norms)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("tb", [2, 3, 4])
+def test_ip_compress_vs_oracle(d, dtype, tb):
+    n = 5000 + 3 * d + tb
+    x = _x(n, d, dtype, 7 * tb + d)
+    q = Q.InnerProductQuantizer(d, total_bits=tb, seed=42, device=DEV)
+    mq = q.mse_quantizer
+    codes, bits, norms = q.compress(x.to(DEV))
+    oc, ob, on = R.compress_ip(x.float(), mq.Pi.cpu(), mq.codebook.boundaries.cpu(), q.S.cpu(),
+                               mq.codebook.centroids.cpu())
+    for got, ref in ((codes, oc), (bits, ob)):
+        rate, step = _mismatch(got, ref)
+        assert rate <= _bar(dtype) and step <= 1, (rate, step)
+    got, ref = norms.cpu().double(), on.double()
+    assert float(((got - ref).abs() / ref).max()) <= 2e-6
+    c2, b2, n2 = K.fused_compress_ip(x.to(DEV), mq.Pi, mq.codebook.boundaries, q.S,
+                                     mq.codebook.centroids)
+    assert torch.equal(c2, codes) and torch.equal(b2, bits) and torch.equal(n2, norms)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compress_equals_store_append(d, dtype):
+    """The quantizer-API kernel and the fused store append share the rotation
+    and the search: the same rows give the same codes, bit for bit."""
+    B, H, S = 2, 3, 333
+    x = _x(B * H * S, d, dtype, d + 1).reshape(B, H, S, d)
+    v = _x(B * H * S, d, dtype, d + 2).reshape(B, H, S, d)
+    eng = Q.QuashKVEngine(head_dim=d, key_bits=3, value_bits=4, seed=9, device=DEV)
+    eng.append(x.to(DEV), v.to(DEV))
+    kc, kb, vc = eng._store.read_codes(0, S)
+    c1, b1, n1 = eng.key_quantizer.compress(x.to(DEV))
+    c2, n2 = eng.value_quantizer.compress(v.to(DEV))
+    assert torch.equal(kc, c1) and torch.equal(kb, b1) and torch.equal(vc, c2)
+    assert torch.equal(eng._store.knorm[:, :, :S], n1)
+    assert torch.equal(eng._store.vnorm[:, :, :S], n2)
+
+
+def test_compress_grouped_and_packed_outputs():
+    d, bits, n, seq, gst = 128, 3, 700, 100, 128
+    x = _x(n, d, torch.float32, 5).to(DEV)
+    q = Q.InnerProductQuantizer(d, total_bits=bits + 1, seed=3, device=DEV)
+    mq = q.mse_quantizer
+    dense_c, dense_b, dense_n = q.compress(x)
+    groups = n // seq
+    gc = torch.zeros(groups * gst, d, dtype=torch.uint8, device=DEV)
+    gb = torch.zeros_like(gc)
+    gn = torch.zeros(groups * gst, dtype=torch.float32, device=DEV)
+    compress_into(N.QKV_MODE_IP, x, mq.Pi, mq.codebook.boundaries, mq.codebook.centroids, bits,
+                  q.S, gc, gb, gn, packed=False, out_seq=seq, out_group_stride=gst)
+    rows = torch.cat([torch.arange(g * gst, g * gst + seq) for g in range(groups)]).to(DEV)
+    assert torch.equal(gc[rows], dense_c) and torch.equal(gb[rows], dense_b)
+    assert torch.equal(gn[rows], dense_n)
+    keep = torch.ones(groups * gst, dtype=torch.bool, device=DEV)
+    keep[rows] = False
+    assert not gc[keep].any() and not gn[keep].any()
+    pc = torch.empty(n, N.packed_row_bytes(d, bits), dtype=torch.uint8, device=DEV)
+    pb = torch.empty(n, N.packed_row_bytes(d, 1), dtype=torch.uint8, device=DEV)
+    pn = torch.empty(n, dtype=torch.float32, device=DEV)
+    compress_into(N.QKV_MODE_IP, x, mq.Pi, mq.codebook.boundaries, mq.codebook.centroids, bits,
+                  q.S, pc, pb, pn, packed=True)
+    assert torch.equal(pc, pack_bits(dense_c, bits)) and torch.equal(pb, pack_bits(dense_b, 1))
+    assert torch.equal(pn, dense_n)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+def test_index_add_fp32_vs_oracle(d):
+    """QuashIndex.add of fp32 rows (the fused append into the index's K rows)
+    against the oracle's compress_ip of the same rows."""
+    n = 20011
+    x = _x(n, d, torch.float32, 77 + d)
+    x = x / x.norm(dim=-1, keepdim=True).clamp(min=1e-8)
+    idx = Q.QuashIndex(dim=d, bits=3, seed=42, device=DEV)
+    idx.add(x.to(DEV))
+    q = idx.quantizer
+    mq = q.mse_quantizer
+    oc, ob, on = R.compress_ip(x, mq.Pi.cpu(), mq.codebook.boundaries.cpu(), q.S.cpu(),
+                               mq.codebook.centroids.cpu())
+    rb = idx._row_bytes
+    rows = idx._rows[:n].contiguous()
+    kc = torch.empty(n, d, dtype=torch.uint8, device=DEV)
+    kb = torch.empty_like(kc)
+    N.check(N.lib().qkv_kplanes_unpack(rows.data_ptr(), rb, n, d, 2, n, n, kc.data_ptr(),
+                                       kb.data_ptr(), N.stream(torch.device(DEV))))
+    for got, ref in ((kc, oc), (kb, ob)):
+        rate, step = _mismatch(got, ref)
+        assert rate <= 2e-5 and step <= 1, (rate, step)
+    got, ref = idx._norms[:n].cpu().double(), on.double()
+    assert float(((got - ref).abs() / ref).max()) <= 2e-6

@@ -72,9 +72,9 @@ def test_abi_rejects_before_launch():
 
 def test_store_append_validation():
     lib = N.lib()
-    # fp32 rows and head_dims other than 128 / 64 are not covered by the fused kernel
-    assert lib.qkv_store_append(N.QKV_F32, 16, None, 1, 1, 128, 2, 3, 16, 16, 16, 16, 16, 16,
-                                16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
+    # unknown input dtypes are refused, head_dims other than 128 / 64 not covered
+    assert lib.qkv_store_append(7, 16, None, 1, 1, 128, 2, 3, 16, 16, 16, 16, 16, 16,
+                                16, 16, 16, 64, 0, None) == N.QKV_E_INVALID
     assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 96, 2, 3, 16, 16, 16, 16, 16, 16,
                                 16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
     # capacity must hold the appended tokens
@@ -97,10 +97,10 @@ def test_kmixed_host_validation():
     assert "permutation" in lib.qkv_last_error().decode()
     assert lib.qkv_kmixed_pack(16, 4, perm.ptr, 48, 16, 4, 4, None) == N.QKV_E_INVALID
     assert lib.qkv_kmixed_unpack(16, 4, perm.ptr, 32, 4, 2, 16, None) == N.QKV_E_INVALID
-    # fp32 keys and other outlier counts are not covered by the fused append
+    # unknown input dtypes are refused, other outlier counts not covered
     ob, rb = N.HostFloats([-3, -2, -1, 0, 1, 2, 3]), N.HostFloats([-1, 0, 1])
-    assert lib.qkv_store_append_kmixed(N.QKV_F32, 16, 1, 1, 128, 16, 32, ob.ptr, rb.ptr, 16, 16,
-                                       64, 0, None) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append_kmixed(7, 16, 1, 1, 128, 16, 32, ob.ptr, rb.ptr, 16, 16,
+                                       64, 0, None) == N.QKV_E_INVALID
     assert lib.qkv_store_append_kmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 16, ob.ptr, rb.ptr, 16,
                                        16, 64, 0, None) == N.QKV_E_UNSUPPORTED
     asym = N.HostFloats([-3, -2, -1, 0.1, 1, 2, 3])
@@ -115,6 +115,31 @@ def test_kmixed_host_validation():
     assert st == N.QKV_E_UNSUPPORTED and "multiple of 64" in lib.qkv_last_error().decode()
 
 
+def test_compress_mfma_host_validation():
+    lib = N.lib()
+    c2, t2 = N.HostFloats([-1.5, -0.5, 0.5, 1.5]), N.HostFloats([-1.0, 0.0, 1.0])
+    # other head dims and bit widths are not covered (the VALU qkv_compress is)
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 96, 16, c2.ptr, t2.ptr, 2, 16,
+                                 16, 16, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 128, 16, c2.ptr, t2.ptr, 4, 16,
+                                 16, 16, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
+    # asymmetric tables, and a fine list that does not interleave
+    ta = N.HostFloats([-1.0, 0.1, 1.0])
+    assert lib.qkv_compress_mfma(N.QKV_MODE_MSE, N.QKV_F32, 16, 4, 128, 16, None, ta.ptr, 2, None,
+                                 16, None, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
+    cb = N.HostFloats([-1.5, -1.2, 1.2, 1.5])
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 128, 16, cb.ptr, t2.ptr, 2, 16,
+                                 16, 16, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
+    assert "symmetric" in lib.qkv_last_error().decode()
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, 9, 16, 4, 128, 16, c2.ptr, t2.ptr, 2, 16,
+                                 16, 16, 16, 4, 4, None) == N.QKV_E_INVALID
+    # IP needs the QJL output and the signs
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 128, 16, c2.ptr, t2.ptr, 2, None,
+                                 16, 16, 16, 4, 4, None) == N.QKV_E_INVALID
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 128, 16, c2.ptr, t2.ptr, 2, 16,
+                                 16, None, 16, 4, 4, None) == N.QKV_E_INVALID
+
+
 def test_kipmixed_host_validation():
     lib = N.lib()
     perm = N.HostInts(list(range(128)))
@@ -125,10 +150,10 @@ def test_kipmixed_host_validation():
     assert lib.qkv_kipmixed_unpack(16, 4, perm.ptr, 32, 4, 4, 16, None, None) == N.QKV_E_INVALID
     oc, ob = N.HostFloats([-1.5, -0.5, 0.5, 1.5]), N.HostFloats([-1, 0, 1])
     rc, rb = N.HostFloats([-0.8, 0.8]), N.HostFloats([0.0])
-    # fp32 keys and other outlier counts are not covered by the fused append
-    assert lib.qkv_store_append_kipmixed(N.QKV_F32, 16, 1, 1, 128, 16, 16, 32, oc.ptr, ob.ptr,
+    # unknown input dtypes are refused, other outlier counts not covered
+    assert lib.qkv_store_append_kipmixed(7, 16, 1, 1, 128, 16, 16, 32, oc.ptr, ob.ptr,
                                          rc.ptr, rb.ptr, 16, 16, 64, 0, None) == \
-        N.QKV_E_UNSUPPORTED
+        N.QKV_E_INVALID
     assert lib.qkv_store_append_kipmixed(N.QKV_BF16, 16, 1, 1, 128, 16, 16, 48, oc.ptr, ob.ptr,
                                          rc.ptr, rb.ptr, 16, 16, 64, 0, None) == \
         N.QKV_E_UNSUPPORTED
