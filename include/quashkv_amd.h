@@ -125,7 +125,8 @@ int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
                  int64_t out_seq, int64_t out_group_stride, void* stream);
 
 /* qkv_compress's unpacked output (one uint8 code, and for IP one QJL bit, per
- * coordinate at grouped rows; norms max(||x||, 1e-8)) on the MFMA, for the
+ * coordinate; norms max(||x||, 1e-8)) on the MFMA for dense rows (out_seq =
+ * n or out_group_stride = out_seq; grouped layouts: QKV_E_UNSUPPORTED), for the
  * same reference operators (quashkv/quantizer.py:113-131, 211-242,
  * quashkv/triton_kernels/compress.py:210-303): the rotation, search and tie
  * rules of qkv_store_append.  d = 128 or 64; cent_host / bound_host are HOST

@@ -354,7 +354,7 @@ __device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl
 // rotation are skipped, everything after them is the same code.
 // XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
 template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
-__global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
@@ -486,6 +486,11 @@ __global__ __launch_bounds__(kThreads, 2) void append_k_mfma(
           }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
+          if constexpr (F32) {  // rows scaled before the rotation: one constant
+#pragma unroll
+            for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * (1.f / 65536.f);
+            continue;
+          }
           float4 iv4[4];
 #pragma unroll
           for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
@@ -743,16 +748,15 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
 // MSEQuantizer.compress / InnerProductQuantizer.compress and fused_compress_*
 // (quashkv/quantizer.py:113-131,211-242, quashkv/triton_kernels/compress.py:
 // 210-303) on the MFMA: n rows of dimension D into one uint8 code (and, IP,
-// one QJL bit) per coordinate, row-major at grouped rows (seq, gstride), and
-// the fp32 norms.  The rotation, search and tie rules are append_k_mfma's
+// one QJL bit) per coordinate, row-major, and the fp32 norms.  The rotation, search and tie rules are append_k_mfma's
 // (tokens x coordinates); IP searches the fine list (L = MB + 1 levels), MSE
 // the boundaries (L = bits levels).  A lane's code byte lands beside its
 // 31 neighbours' (32 coordinates of one row per half-wave).
 template <int L, bool IP, int XT, int D>
-__global__ __launch_bounds__(kThreads, 2) void compress_mfma(
+__global__ __launch_bounds__(kThreads, 4) void compress_mfma(
     const void* __restrict__ xin, int64_t n, int64_t ntiles, const float* __restrict__ pi,
     const float* __restrict__ signs, Half lst, uint8_t* __restrict__ codes,
-    uint8_t* __restrict__ qjl, float* __restrict__ norms, int64_t seq, int64_t gstride) {
+    uint8_t* __restrict__ qjl, float* __restrict__ norms) {
   constexpr bool F16 = XT != 0, F32 = XT == 2;
   constexpr int NP = (1 << (L - 1)) - 1;  // positive half of the searched list
   constexpr int NBK = D / 32, NKS = D / 16;
@@ -780,7 +784,7 @@ __global__ __launch_bounds__(kThreads, 2) void compress_mfma(
     const int64_t s0 = tile * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, n - s0));
     uint4 xf[kHalves][NKS];
-    uint4 xl[kHalves][F32 ? NKS : 1];
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
     float nrm[kHalves];
     if constexpr (F32) {
       const float* row[kHalves];
@@ -807,8 +811,8 @@ __global__ __launch_bounds__(kThreads, 2) void compress_mfma(
 #pragma unroll
     for (int tt = 0; tt < kHalves; ++tt) {
       if (lane < 32) {
-        if (32 * tt + li < nv) norms[qkv_grouped_row(s0 + 32 * tt + li, seq, gstride)] = nrm[tt];
-        invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+        if (32 * tt + li < nv) norms[s0 + 32 * tt + li] = nrm[tt];
+        if (!F32) invw[32 * tt + li] = iscale / nrm[tt];
       }
     }
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
@@ -832,22 +836,32 @@ __global__ __launch_bounds__(kThreads, 2) void compress_mfma(
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
         float4 iv4[4];
+        if constexpr (!F32) {
 #pragma unroll
-        for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+        }
+        // this lane's first token 32 tt + 4 (l >> 5) at coordinate 32 b + (l & 31); the
+        // others sit at fixed offsets from it
+        const int64_t o0 = (s0 + 32 * tt + 4 * (lane >> 5)) * D + 32 * b + li;
+        uint8_t* cb = codes + o0;
+        uint8_t* qb = IP ? qjl + o0 : nullptr;
+        const int tk0 = 32 * tt + 4 * (lane >> 5);
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const float4 q4 = iv4[v >> 2];
-          const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-          // token 32 tt + 8 (v >> 2) + 4 (l >> 5) + (v & 3), coordinate 32 b + (l & 31)
-          const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+          float iv = 1.f / 65536.f;  // fp32 rows: scaled before the rotation
+          if constexpr (!F32) {
+            const float4 q4 = iv4[v >> 2];
+            iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+          }
+          // token tk0 + 8 (v >> 2) + (v & 3)
+          const int dt = 8 * (v >> 2) + (v & 3);
           const uint32_t f = search_sym_count<L, IP>(acc[tt][v] * iv, lv, cx[b]);
-          if (tk < nv) {
-            const int64_t o = qkv_grouped_row(s0 + tk, seq, gstride) * D + 32 * b + li;
+          if (tk0 + dt < nv) {
             if constexpr (IP) {
-              codes[o] = static_cast<uint8_t>(f >> 1);
-              qjl[o] = static_cast<uint8_t>((f & 1u) ^ neg[b]);
+              cb[dt * D] = static_cast<uint8_t>(f >> 1);
+              qb[dt * D] = static_cast<uint8_t>((f & 1u) ^ neg[b]);
             } else {
-              codes[o] = static_cast<uint8_t>(f);
+              cb[dt * D] = static_cast<uint8_t>(f);
             }
           }
         }
@@ -863,7 +877,7 @@ __global__ __launch_bounds__(kThreads, 2) void compress_mfma(
 // already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
 // their norms.
 template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
-__global__ __launch_bounds__(kThreads, 2) void append_v_mfma(
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
@@ -1422,13 +1436,17 @@ extern "C" int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, 
   QKV_REQUIRE(x && codes && norms && (!ip || qjl), "null pointer");
   QKV_REQUIRE(qkv_aligned(x, 16) && qkv_aligned(pi, 16), "x rows and pi must be 16-byte aligned");
   QKV_REQUIRE(gst >= seq, "bad grouped-row layout");
+  if (gst != seq && seq < n) {
+    qkv_set_error("MFMA compress writes dense rows (grouped layouts: qkv_compress)");
+    return QKV_E_UNSUPPORTED;
+  }
   auto s = static_cast<hipStream_t>(stream);
   const int64_t ntiles = (n + kTok - 1) / kTok;
   const dim3 grid(append_blocks(ntiles));
   const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;
 #define QKV_C(LV, IPV, XTV, DD)                                                                 \
   hipLaunchKernelGGL((compress_mfma<LV, IPV, XTV, DD>), grid, dim3(kThreads), 0, s, x, n,      \
-                     ntiles, pi, signs, h, codes, qjl, norms, seq, gst)
+                     ntiles, pi, signs, h, codes, qjl, norms)
 #define QKV_CX(LV, IPV, DD)        \
   do {                             \
     if (xt == 2)                   \

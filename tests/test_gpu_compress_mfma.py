@@ -9,7 +9,8 @@ Bars: codes against the oracle's compress_mse / compress_ip on the same
 fp32 rows, split hi + lo for the fp16 MFMA), every mismatch one code step;
 norms within 2e-6 relative; the unpacked codes equal, bit for bit, what the
 fused store append writes from the same rows (the same rotation and search);
-packed and grouped outputs equal the packer and the dense layout exactly."""
+packed outputs equal the packer's bytes exactly; grouped layouts (the VALU
+kernel) agree with the dense ones up to near-ties."""
 
 import pytest
 import torch
@@ -120,9 +121,13 @@ def test_compress_grouped_and_packed_outputs():
     gn = torch.zeros(groups * gst, dtype=torch.float32, device=DEV)
     compress_into(N.QKV_MODE_IP, x, mq.Pi, mq.codebook.boundaries, mq.codebook.centroids, bits,
                   q.S, gc, gb, gn, packed=False, out_seq=seq, out_group_stride=gst)
+    # grouped layouts run on the VALU kernel (qkv_compress): same codes up to
+    # near-ties of the two rotations
     rows = torch.cat([torch.arange(g * gst, g * gst + seq) for g in range(groups)]).to(DEV)
-    assert torch.equal(gc[rows], dense_c) and torch.equal(gb[rows], dense_b)
-    assert torch.equal(gn[rows], dense_n)
+    for got, ref in ((gc[rows], dense_c), (gb[rows], dense_b)):
+        rate, step = _mismatch(got, ref)
+        assert rate <= 1e-4 and step <= 1, (rate, step)
+    assert torch.allclose(gn[rows], dense_n, rtol=2e-6, atol=0)
     keep = torch.ones(groups * gst, dtype=torch.bool, device=DEV)
     keep[rows] = False
     assert not gc[keep].any() and not gn[keep].any()
