@@ -407,24 +407,35 @@ __device__ __forceinline__ float dpp_add(float v) {
   return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xf,
                                                         true));
 }
-// max of v and the DPP-moved v (lanes without a source keep v)
-template <int CTRL, int ROWS = 0xf>
-__device__ __forceinline__ float dpp_max(float v) {
-  return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(
-                      __float_as_int(v), __float_as_int(v), CTRL, ROWS, 0xf, false)));
-}
+// max of v and the DPP-moved v in one v_max_f32_dpp (lanes without a source,
+// or outside the row mask, keep v: the destination is v itself).  fmaxf over
+// a moved copy costs four instructions here (copy, DPP move, the NaN-quieting
+// max of the moved value, max), since the compiler neither folds the move into
+// the max nor drops the quieting; the values reduced here are never NaN.
+// The s_nop gives the two wait states a DPP read of a VGPR written by the
+// previous VALU instruction needs.
+#define QKV_DPP_MAX(NAME, CTRL)                                                        \
+  __device__ __forceinline__ float NAME(float v) {                                     \
+    asm volatile("s_nop 1\n\tv_max_f32_dpp %0, %0, %0 " CTRL : "+v"(v));                \
+    return v;                                                                          \
+  }
+QKV_DPP_MAX(dmax_shr1, "row_shr:1 row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_shr2, "row_shr:2 row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_shr4, "row_shr:4 row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_shr8, "row_shr:8 row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_bc15, "row_bcast:15 row_mask:0xa bank_mask:0xf")
+QKV_DPP_MAX(dmax_bc31, "row_bcast:31 row_mask:0xc bank_mask:0xf")
+QKV_DPP_MAX(dmax_swap1, "quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_swap2, "quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf")
+QKV_DPP_MAX(dmax_hmirror, "row_half_mirror row_mask:0xf bank_mask:0xf")
+#undef QKV_DPP_MAX
 // Max over each 16-lane row, left in the row's last lane (prefix maxima).
 __device__ __forceinline__ float row_max_last(float v) {
-  v = dpp_max<0x111>(v);
-  v = dpp_max<0x112>(v);
-  v = dpp_max<0x114>(v);
-  return dpp_max<0x118>(v);
+  return dmax_shr8(dmax_shr4(dmax_shr2(dmax_shr1(v))));
 }
 // Max over the wave, read back to every lane.
 __device__ __forceinline__ float wave_max_dpp(float v) {
-  v = row_max_last(v);
-  v = dpp_max<0x142, 0xa>(v);
-  v = dpp_max<0x143, 0xc>(v);
+  v = dmax_bc31(dmax_bc15(row_max_last(v)));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_sum_dpp(float v) {
@@ -440,9 +451,7 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // Max over each aligned group of 8 lanes, in every lane of the group
 // (quad_perm swaps of neighbours and pairs, then the half-row mirror).
 __device__ __forceinline__ float max8_dpp(float v) {
-  v = dpp_max<0xb1>(v);
-  v = dpp_max<0x4e>(v);
-  return dpp_max<0x141>(v);
+  return dmax_hmirror(dmax_swap2(dmax_swap1(v)));
 }
 
 // ---- fp4 key operands of the fused d = 128 decode
