@@ -45,7 +45,7 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 PEAK_INT8_TOPS = 5000.0
 METRIC = "decode attn over 3-bit KV: µs/step, HBM GB/s % of peak; compress Gvec/s"
-DTYPE = "i8 (MFMA, 30-bit fixed point) / f32"
+DTYPE = "fp8 x fp4 (scores) and i8 (values) on MFMA, exact; f32 softmax"
 TRAFFIC_RECORD = os.path.join(ROOT, "profiles", "decode_fused_cfg3_decode.md")
 
 B, HQ, HKV, D, T = 32, 32, 8, 128, 8192
@@ -960,7 +960,7 @@ def main() -> None:
             "executed_frac": round(2 * n_vec * 2 * D * D / (comp_ms * 1e-3) / 2.5e15, 4),
         },
         "roofline": {
-            "kernel": ("decode_fused<2, 3, false> (qkv_decode_attention, one launch)"
+            "kernel": ("decode_fused<12, 3, false, 128> (qkv_decode_attention, one launch)"
                        if splits == 1 else "qkv_decode_attention (decode_fused + combine)"),
             "bound": "hbm",
             "achieved": round(launch_gbs, 2),

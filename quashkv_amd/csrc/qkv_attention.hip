@@ -1130,16 +1130,17 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   }
 }
 
-// ------------------------------------------------------------ fused decode, d = 128
+// ------------------------------------------------------------ fused decode, d = 128 / 96
 //
-// The whole decode step at head_dim 128 (MSE key bits 1-2, value bits 1-4,
-// symmetric codebooks) in one kernel.  A workgroup of 8 waves takes one
-// (sequence, kv head, chunk of 4 query rows) over a range of tokens (a split)
-// and streams it in chunks of kChunkF tokens through a two-stage pipeline:
-//   key waves (0-7) score chunk c -- one 64-token tile each, integer MFMA on
-//     the K bit planes exactly as split_mfma does -- into LDS, and once the
-//     chunk's row maxima are known turn those scores into the int8 digit
-//     operands of the value product, in place;
+// The whole decode step at head_dim 128 or 96 (IP keys of MSE bits 1-3, the
+// two mixed-precision key formats, value bits 1-4, symmetric codebooks) in
+// one kernel.  A workgroup of 16 waves takes one (sequence, kv head, chunk of
+// 4 query rows) over a range of tokens (a split) and streams it in chunks of
+// kChunkF tokens through a two-stage pipeline:
+//   key waves (0-7) score chunk c -- one 64-token tile each, the fp8 x fp4
+//     scaled MFMA on the K bit planes (operands described above) -- into
+//     LDS, and once the chunk's row maxima are known turn those scores into
+//     the int8 digit operands of the value product, in place;
 //   value waves (8-15) meanwhile accumulate chunk c - 1's value product for 16
 //     coordinates each (integer MFMA on the V bit planes, plus one product
 //     with an all-ones plane for the constant term) and merge it into a

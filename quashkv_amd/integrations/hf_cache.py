@@ -116,24 +116,18 @@ class QuashKVCache:
             engine.clear()
 
     def compression_stats(self) -> dict:
-        """quashkv/integrations/hf_cache.py:179-203."""
-        total_original = 0
-        total_compressed = 0
-        tokens_per_layer = []
-        for engine in self.engines:
-            tokens_per_layer.append(engine.total_tokens)
-            if engine.total_tokens > 0:
-                d = engine.head_dim
-                per_token = 2 * d * 16
-                compressed = engine.key_bits * d + 32 + engine.value_bits * d + 32
-                total_original += engine.total_tokens * per_token
-                total_compressed += engine.total_tokens * compressed
+        """Bit totals over the layers (quashkv/integrations/hf_cache.py:179-203).
+
+        A token costs 2 d 16 bits as fp16 K and V rows, and (key_bits +
+        value_bits) d code bits plus two 32-bit norms compressed."""
+        tokens = [e.total_tokens for e in self.engines]
+        fp16_bits = sum(n * 32 * e.head_dim for n, e in zip(tokens, self.engines))
+        code_bits = sum(n * ((e.key_bits + e.value_bits) * e.head_dim + 64)
+                        for n, e in zip(tokens, self.engines))
         return {
             "num_layers": self.num_layers,
-            "tokens_per_layer": tokens_per_layer,
-            "total_original_bits": total_original,
-            "total_compressed_bits": total_compressed,
-            "overall_compression_ratio": (
-                total_original / total_compressed if total_compressed > 0 else 0
-            ),
+            "tokens_per_layer": tokens,
+            "total_original_bits": fp16_bits,
+            "total_compressed_bits": code_bits,
+            "overall_compression_ratio": fp16_bits / code_bits if code_bits else 0,
         }
