@@ -249,6 +249,23 @@ int qkv_store_append(int32_t in_dtype, const void* keys, const void* values,
                      uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
                      void* stream);
 
+/* qkv_store_append over n_layers (1..32) contiguous stores that share shapes,
+ * bit widths, codebooks, capacity t_stride and length t0 -- one decode step's
+ * new token(s) for every layer of a model, in one K and one V launch instead
+ * of one pair per layer (QuashKVEngine.append per layer, quashkv/engine.py:
+ * 145-172).  keys, values, kpi, signs, vpi (the key quantizer's Pi and S, the
+ * value quantizer's Pi), kstore, knorm, vstore and vnorm are HOST arrays of
+ * n_layers device pointers, each as in qkv_store_append (keys and values both
+ * required); the codebook tables are shared. */
+int qkv_store_append_layers(int32_t n_layers, int32_t in_dtype, const void* const* keys,
+                            const void* const* values, int64_t groups, int64_t S, int32_t d,
+                            int32_t mbits, int32_t vbits, const float* const* kpi,
+                            const float* const* signs, const float* const* vpi,
+                            const float* kcent_host, const float* kbound_host,
+                            const float* vbound_host, uint8_t* const* kstore,
+                            float* const* knorm, uint32_t* const* vstore, float* const* vnorm,
+                            int64_t t_stride, int64_t t0, void* stream);
+
 /* qkv_store_append from rotated unit vectors: the search, QJL and store code
  * of qkv_store_append (the same device code, with the normalisation and the
  * rotation skipped) on given fp32 rows y = (x / |x|) Pi^T, groups x S x d,

@@ -64,6 +64,8 @@ _SIGS = {
     "qkv_kmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p]),
     "qkv_store_append_kmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p, _p,
                                        _i64, _i64, _p]),
+    "qkv_store_append_layers": (_i32, [_i32, _i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p,
+                                       _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_store_append_rotated": (_i32, [_p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p, _p, _p,
                                         _p, _p, _p, _p, _p, _i64, _i64, _p]),
     "qkv_store_append_kmixed_rotated": (_i32, [_p, _p, _i64, _i64, _i32, _i32, _p, _p, _p, _p,

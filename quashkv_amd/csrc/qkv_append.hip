@@ -354,7 +354,7 @@ __device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl
 // rotation are skipped, everything after them is the same code.
 // XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
 template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
-__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
+__device__ __forceinline__ void append_k_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
@@ -539,6 +539,39 @@ __global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
       }
     }
   }
+}
+
+template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
+    QkvPages pg) {
+  append_k_run<MB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, signs, fine, kst, knorm,
+                                         t_stride, t0, pg);
+}
+
+// Per-layer pointers of a layer-batched append (kernel arguments by value):
+// rows, Pi, S (keys), store array and norms of layer l = blockIdx.y.
+constexpr int kMaxAppendLayers = 32;
+struct AppendLayers {
+  const void* x[kMaxAppendLayers];
+  const float* pi[kMaxAppendLayers];
+  const float* signs[kMaxAppendLayers];
+  void* st[kMaxAppendLayers];
+  float* nrm[kMaxAppendLayers];
+};
+
+// append_k_mfma over the contiguous stores of blockIdx.y's layer
+template <int MB, int XT, int D>
+__global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, int64_t S,
+                                                               int64_t tpg, int64_t ntiles,
+                                                               Half fine, int64_t t_stride,
+                                                               int64_t t0) {
+  const int l = blockIdx.y;
+  append_k_run<MB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], al.signs[l],
+                                        fine, static_cast<uint8_t*>(al.st[l]), al.nrm[l],
+                                        t_stride, t0, QkvPages{});
 }
 
 // ------------------------------------------------- mixed-precision keys
@@ -877,7 +910,7 @@ __global__ __launch_bounds__(kThreads, 4) void compress_mfma(
 // already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
 // their norms.
 template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
-__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
+__device__ __forceinline__ void append_v_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
@@ -1034,6 +1067,27 @@ __global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
   }
 }
 
+template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
+    float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
+  append_v_run<VB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, bnd, vst, vnorm, t_stride,
+                                         t0, pg);
+}
+
+// append_v_mfma over the contiguous stores of blockIdx.y's layer
+template <int VB, int XT, int D>
+__global__ __launch_bounds__(kThreads, 4) void append_v_layers(AppendLayers al, int64_t S,
+                                                               int64_t tpg, int64_t ntiles,
+                                                               Half bnd, int64_t t_stride,
+                                                               int64_t t0) {
+  const int l = blockIdx.y;
+  append_v_run<VB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], bnd,
+                                        static_cast<uint32_t*>(al.st[l]), al.nrm[l], t_stride,
+                                        t0, QkvPages{});
+}
+
 // -------------------------------------------------------------- host side
 
 bool symmetric(const float* v, int n) {
@@ -1053,6 +1107,37 @@ bool positive_half(const float* v, int n, Half* h) {
     h->t[i] = 2u * b;
   }
   return true;
+}
+
+// The search lists of the store append: the key fine list (centroids and
+// boundaries interleaved) and the value boundaries, as positive halves of
+// integer keys; QKV_E_UNSUPPORTED unless they are ascending and symmetric.
+int append_lists(bool keys, bool values, int mbits, int vbits, const float* kcent_host,
+                 const float* kbound_host, const float* vbound_host, Half* fine, Half* bnd) {
+  if (keys) {
+    const int nc = 1 << mbits;
+    float fl[15];
+    for (int i = 0; i < nc; ++i) {
+      fl[2 * i] = kcent_host[i];
+      if (i + 1 < nc) fl[2 * i + 1] = kbound_host[i];
+    }
+    bool asc = true;
+    for (int i = 0; i + 1 < 2 * nc - 1; ++i) asc = asc && fl[i] < fl[i + 1];
+    if (!asc || !symmetric(fl, 2 * nc - 1) || !positive_half(fl, 2 * nc - 1, fine)) {
+      qkv_set_error("store append needs a symmetric key codebook with c_i < t_i < c_{i+1}");
+      return QKV_E_UNSUPPORTED;
+    }
+  }
+  if (values) {
+    const int nb = (1 << vbits) - 1;
+    bool asc = true;
+    for (int i = 0; i + 1 < nb; ++i) asc = asc && vbound_host[i] < vbound_host[i + 1];
+    if (!asc || !symmetric(vbound_host, nb) || !positive_half(vbound_host, nb, bnd)) {
+      qkv_set_error("store append needs ascending value boundaries symmetric about 0");
+      return QKV_E_UNSUPPORTED;
+    }
+  }
+  return QKV_OK;
 }
 
 int append_blocks(int64_t ntiles) {
@@ -1106,29 +1191,9 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   }
   QKV_REQUIRE(!pi || qkv_aligned(pi, 16), "pi must be 16-byte aligned");
   Half fine{}, bnd{};
-  if (keys) {
-    const int nc = 1 << mbits;
-    float fl[15];
-    for (int i = 0; i < nc; ++i) {
-      fl[2 * i] = kcent_host[i];
-      if (i + 1 < nc) fl[2 * i + 1] = kbound_host[i];
-    }
-    bool asc = true;
-    for (int i = 0; i + 1 < 2 * nc - 1; ++i) asc = asc && fl[i] < fl[i + 1];
-    if (!asc || !symmetric(fl, 2 * nc - 1) || !positive_half(fl, 2 * nc - 1, &fine)) {
-      qkv_set_error("store append needs a symmetric key codebook with c_i < t_i < c_{i+1}");
-      return QKV_E_UNSUPPORTED;
-    }
-  }
-  if (values) {
-    const int nb = (1 << vbits) - 1;
-    bool asc = true;
-    for (int i = 0; i + 1 < nb; ++i) asc = asc && vbound_host[i] < vbound_host[i + 1];
-    if (!asc || !symmetric(vbound_host, nb) || !positive_half(vbound_host, nb, &bnd)) {
-      qkv_set_error("store append needs ascending value boundaries symmetric about 0");
-      return QKV_E_UNSUPPORTED;
-    }
-  }
+  if (const int st = append_lists(keys != nullptr, values != nullptr, mbits, vbits, kcent_host,
+                                  kbound_host, vbound_host, &fine, &bnd))
+    return st;
   if (groups == 0 || S == 0) return QKV_OK;
   auto s = static_cast<hipStream_t>(stream);
   const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;  // the kernels' XT
@@ -1200,6 +1265,127 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
     case 12: QKV_V(4, 0, DD); break;                \
     case 13: QKV_V(4, 1, DD); break;                \
     case 14: QKV_V(4, 2, DD); break;                \
+  }
+    if (d == 128) {
+      QKV_VD(128)
+    } else {
+      QKV_VD(64)
+    }
+#undef QKV_VD
+#undef QKV_V
+    QKV_LAUNCHED();
+  }
+  return QKV_OK;
+}
+
+// qkv_store_append_layers: one K and one V launch over n_layers contiguous
+// stores that share shapes, codebooks, capacity and length (grid.y = layer).
+int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* const* keys,
+                             const void* const* values, int64_t groups, int64_t S, int32_t d,
+                             int32_t mbits, int32_t vbits, const float* const* kpi,
+                             const float* const* signs, const float* const* vpi,
+                             const float* kcent_host, const float* kbound_host,
+                             const float* vbound_host, uint8_t* const* kstore,
+                             float* const* knorm, uint32_t* const* vstore,
+                             float* const* vnorm, int64_t t_stride, int64_t t0, void* stream) {
+  QKV_REQUIRE(n_layers >= 1 && n_layers <= kMaxAppendLayers, "n_layers %d not in 1..%d",
+              n_layers, kMaxAppendLayers);
+  QKV_REQUIRE(keys && values && kpi && signs && vpi && kstore && knorm && vstore && vnorm &&
+                  kcent_host && kbound_host && vbound_host,
+              "null pointer");
+  QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
+              "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
+              (long long)t_stride, (long long)t0, (long long)(t0 + S));
+  QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
+  if (d != 128 && d != 64) {
+    qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
+    return QKV_E_UNSUPPORTED;
+  }
+  if (mbits < 1 || mbits > 3) {
+    qkv_set_error("store append: key MSE bits %d not in 1..3", mbits);
+    return QKV_E_UNSUPPORTED;
+  }
+  QKV_REQUIRE(qkv_bits_ok(vbits), "value bits %d not in 1..4", vbits);
+  AppendLayers ak{}, av{};
+  for (int l = 0; l < n_layers; ++l) {
+    QKV_REQUIRE(keys[l] && values[l] && kpi[l] && signs[l] && vpi[l] && kstore[l] && knorm[l] &&
+                    vstore[l] && vnorm[l],
+                "null pointer (layer %d)", l);
+    QKV_REQUIRE(qkv_aligned(keys[l], 16) && qkv_aligned(values[l], 16) &&
+                    qkv_aligned(kpi[l], 16) && qkv_aligned(vpi[l], 16) &&
+                    qkv_aligned(kstore[l], 4) && qkv_aligned(vstore[l], 4),
+                "layer %d: rows and pi 16-B, stores 4-B aligned", l);
+    ak.x[l] = keys[l];
+    ak.pi[l] = kpi[l];
+    ak.signs[l] = signs[l];
+    ak.st[l] = kstore[l];
+    ak.nrm[l] = knorm[l];
+    av.x[l] = values[l];
+    av.pi[l] = vpi[l];
+    av.st[l] = vstore[l];
+    av.nrm[l] = vnorm[l];
+  }
+  Half fine{}, bnd{};
+  if (const int st = append_lists(true, true, mbits, vbits, kcent_host, kbound_host, vbound_host,
+                                  &fine, &bnd))
+    return st;
+  if (groups == 0 || S == 0) return QKV_OK;
+  auto s = static_cast<hipStream_t>(stream);
+  const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;
+  // workgroups per layer: the tiles' waves, at most two workgroups per CU over all layers
+  auto blocks = [&](int64_t ntiles) {
+    const int64_t cap = std::max<int64_t>(1, int64_t(qkv_num_cus()) * 2 / n_layers);
+    return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>((ntiles + kWaves - 1) / kWaves, cap)));
+  };
+  {
+    const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
+    const dim3 grid(blocks(ntiles), n_layers);
+#define QKV_K(MB, F, DD)                                                                     \
+  hipLaunchKernelGGL((append_k_layers<MB, F, DD>), grid, dim3(kThreads), 0, s, ak, S, tpg,    \
+                     ntiles, fine, t_stride, t0)
+#define QKV_KD(DD)                  \
+  switch (mbits * 3 + xt) {         \
+    case 3: QKV_K(1, 0, DD); break; \
+    case 4: QKV_K(1, 1, DD); break; \
+    case 5: QKV_K(1, 2, DD); break; \
+    case 6: QKV_K(2, 0, DD); break; \
+    case 7: QKV_K(2, 1, DD); break; \
+    case 8: QKV_K(2, 2, DD); break; \
+    case 9: QKV_K(3, 0, DD); break; \
+    case 10: QKV_K(3, 1, DD); break; \
+    case 11: QKV_K(3, 2, DD); break; \
+  }
+    if (d == 128) {
+      QKV_KD(128)
+    } else {
+      QKV_KD(64)
+    }
+#undef QKV_KD
+#undef QKV_K
+    QKV_LAUNCHED();
+  }
+  {
+    const int64_t a_base = t0 & ~int64_t(31);
+    const int64_t tpg = (t0 + S - a_base + kTok - 1) / kTok, ntiles = groups * tpg;
+    const dim3 grid(blocks(ntiles), n_layers);
+#define QKV_V(VB, F, DD)                                                                     \
+  hipLaunchKernelGGL((append_v_layers<VB, F, DD>), grid, dim3(kThreads), 0, s, av, S, tpg,    \
+                     ntiles, bnd, t_stride, t0)
+#define QKV_VD(DD)                   \
+  switch (vbits * 3 + xt) {          \
+    case 3: QKV_V(1, 0, DD); break;  \
+    case 4: QKV_V(1, 1, DD); break;  \
+    case 5: QKV_V(1, 2, DD); break;  \
+    case 6: QKV_V(2, 0, DD); break;  \
+    case 7: QKV_V(2, 1, DD); break;  \
+    case 8: QKV_V(2, 2, DD); break;  \
+    case 9: QKV_V(3, 0, DD); break;  \
+    case 10: QKV_V(3, 1, DD); break; \
+    case 11: QKV_V(3, 2, DD); break; \
+    case 12: QKV_V(4, 0, DD); break; \
+    case 13: QKV_V(4, 1, DD); break; \
+    case 14: QKV_V(4, 2, DD); break; \
   }
     if (d == 128) {
       QKV_VD(128)
@@ -1314,6 +1500,21 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
   return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, groups, S, d, mbits,
                            vbits, pi, signs, kcent_host, kbound_host, vbound_host, kstore, knorm,
                            vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream);
+}
+
+extern "C" int qkv_store_append_layers(int32_t n_layers, int32_t in_dtype,
+                                       const void* const* keys, const void* const* values,
+                                       int64_t groups, int64_t S, int32_t d, int32_t mbits,
+                                       int32_t vbits, const float* const* kpi,
+                                       const float* const* signs, const float* const* vpi,
+                                       const float* kcent_host, const float* kbound_host,
+                                       const float* vbound_host, uint8_t* const* kstore,
+                                       float* const* knorm, uint32_t* const* vstore,
+                                       float* const* vnorm, int64_t t_stride, int64_t t0,
+                                       void* stream) {
+  return store_append_layers_impl(n_layers, in_dtype, keys, values, groups, S, d, mbits, vbits,
+                                  kpi, signs, vpi, kcent_host, kbound_host, vbound_host, kstore,
+                                  knorm, vstore, vnorm, t_stride, t0, stream);
 }
 
 extern "C" int qkv_store_append_rotated(const float* yk, const float* knorm_in, const float* yv,

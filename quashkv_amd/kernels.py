@@ -211,7 +211,8 @@ def attention_store_kmixed(queries: torch.Tensor, store: KVStore, T: int,
 class LayerBatch:
     """Layer-batched decode over a fixed list of engines (a model's layers:
     one head_dim, bit widths, batch and kv heads), through
-    qkv_decode_attention_layers.  Per-layer constants (Pi, S, codebook tables)
+    qkv_decode_attention_layers, and the step's appends through
+    qkv_store_append_layers (``batch.append``).  Per-layer constants (Pi, S, codebook tables)
     and the workspace are prepared once; each call reads the current stores,
     so appends between calls are seen.  ``batch(queries)`` returns one
     (B, Hq, Q, d) output per layer, as ``engines[l].attention(queries[l])``."""
@@ -237,6 +238,7 @@ class LayerBatch:
         self._qjl = float(kq[0].qjl_scale)
         self._ws: Optional[torch.Tensor] = None
         self._stores = None   # (key, four pointer arrays) of the stores last seen
+        self._app = None      # value Pi and the append's boundary tables, on first append
 
     def _store_arrays(self):
         sts = [e._store for e in self.engines]
@@ -245,6 +247,63 @@ class LayerBatch:
         if self._stores is None or self._stores[0] != ptrs:
             self._stores = (ptrs, tuple(N.ptr_array(p) for p in ptrs))
         return self._stores[1]
+
+    def append(self, keys: Sequence[torch.Tensor], values: Sequence[torch.Tensor]) -> None:
+        """``engines[l].append(keys[l], values[l])`` for every layer.  When every
+        engine already holds a store of one length and the rows take the fused
+        append (bf16/fp16/fp32 rows of one shape, head_dim 64 or 128), all layers
+        go through one K and one V launch (qkv_store_append_layers); otherwise
+        each engine appends on its own."""
+        engines = self.engines
+        n = len(engines)
+        if len(keys) != n or len(values) != n:
+            raise ValueError("one key and one value tensor per engine")
+        k0 = keys[0]
+        e0 = engines[0]
+        sts = [e._store for e in engines]
+        T = e0.total_tokens
+        fused = (k0.dim() == 4 and k0.is_cuda
+                 and k0.dtype in (torch.bfloat16, torch.float16, torch.float32)
+                 and e0.head_dim in (64, 128) and 2 <= e0.key_bits <= 4
+                 and all(k.shape == k0.shape and v.shape == k0.shape and k.dtype == k0.dtype
+                         and v.dtype == k0.dtype and k.device == k0.device
+                         and v.device == k0.device for k, v in zip(keys, values)))
+        if fused:
+            B, H, S, d = k0.shape
+            fused = S > 0 and d == e0.head_dim and all(
+                st is not None and (st.B, st.H) == (B, H) and e.total_tokens == T
+                and st.kst.device == k0.device for e, st in zip(engines, sts))
+        if fused:
+            for st in sts:
+                st.ensure(T + S, T)
+            fused = len({st.capacity for st in sts}) == 1
+        if fused:
+            if self._app is None:
+                vq = [e.value_quantizer for e in engines]
+                mq0 = e0.key_quantizer.mse_quantizer
+                vpi = [N.dense(q.Pi)[0] for q in vq]
+                self._app = (vpi, N.ptr_array([t.data_ptr() for t in vpi]),
+                             N.HostFloats(mq0.codebook.boundaries_host),
+                             N.HostFloats(vq[0].codebook.boundaries_host))
+            _, vpi_arr, kb, vb = self._app
+            ks = [k.contiguous() for k in keys]
+            vs = [v.contiguous() for v in values]
+            kst, knorm, vst, vnorm = self._store_arrays()
+            L = N.lib()
+            status = L.qkv_store_append_layers(
+                n, N.dtype_code(k0.dtype), N.ptr_array([k.data_ptr() for k in ks]),
+                N.ptr_array([v.data_ptr() for v in vs]), B * H, S, d,
+                e0.key_quantizer.mse_bits, e0.value_bits, self._pi_arr, self._s_arr, vpi_arr,
+                self._kc.ptr, kb.ptr, vb.ptr, kst, knorm, vst, vnorm, sts[0].capacity, T,
+                N.stream(k0.device))
+            if status != N.QKV_E_UNSUPPORTED:
+                N.check(status)
+                for e in engines:
+                    e._blocks.append((T, S))
+                    e._total_tokens += S
+                return
+        for e, k, v in zip(engines, keys, values):
+            e.append(k, v)
 
     def __call__(self, queries: Sequence[torch.Tensor], scale: Optional[float] = None,
                  causal: bool = False, out_dtype: torch.dtype = torch.float32,

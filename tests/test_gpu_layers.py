@@ -104,3 +104,68 @@ def test_layer_batch_follows_appends_and_store_growth():
             x = torch.randn(2, 2, 60, 64, generator=gen).to(DEV, torch.float16)
             e.append(x, x)
     assert engines[0]._store.capacity > caps[0]
+
+
+def _stores_equal(a, b, T):
+    sa, sb = a._store, b._store
+    assert a.total_tokens == b.total_tokens == T and a.num_blocks == b.num_blocks
+    assert torch.equal(sa.kst[:, :, :T], sb.kst[:, :, :T])
+    assert torch.equal(sa.knorm[:, :, :T], sb.knorm[:, :, :T])
+    nt = (T + 31) // 32
+    if T % 32:   # bits of the last tile past T are not part of the cache
+        ta, tb = sa.vst[:, :, :nt].clone(), sb.vst[:, :, :nt].clone()
+        m = (1 << (T % 32)) - 1
+        ta[:, :, -1] &= m
+        tb[:, :, -1] &= m
+        assert torch.equal(ta, tb)
+    else:
+        assert torch.equal(sa.vst[:, :, :nt], sb.vst[:, :, :nt])
+    assert torch.equal(sa.vnorm[:, :, :T], sb.vnorm[:, :, :T])
+
+
+@pytest.mark.parametrize("d,key_bits,value_bits,dtype", [
+    (64, 3, 3, torch.bfloat16), (128, 3, 3, torch.float16), (128, 4, 4, torch.float32),
+    (64, 2, 2, torch.float32)])
+def test_layer_batch_append_matches_per_engine(d, key_bits, value_bits, dtype):
+    """batch.append (one K and one V launch over all layers) writes the same
+    store bytes, norms and bookkeeping as each engine's own append: one-token
+    decode steps, a multi-token append crossing a V tile, and a store growth."""
+    gen = torch.Generator().manual_seed(d + key_bits)
+    n, B, H = 6, 3, 2
+    mk = lambda: [Q.QuashKVEngine(head_dim=d, key_bits=key_bits, value_bits=value_bits,
+                                  seed=5 + l, device=DEV) for l in range(n)]
+    ea, eb = mk(), mk()
+    T = 61
+    for a, b in zip(ea, eb):   # prefill per engine (creates the stores)
+        x = torch.randn(B, H, T, d, generator=gen).to(DEV, dtype)
+        y = torch.randn(B, H, T, d, generator=gen).to(DEV, dtype)
+        a.append(x, y)
+        b.append(x, y)
+    batch = K.LayerBatch(ea)
+    for S in (1, 1, 1, 5, 1, 64):
+        ks = [torch.randn(B, H, S, d, generator=gen).to(DEV, dtype) for _ in range(n)]
+        vs = [torch.randn(B, H, S, d, generator=gen).to(DEV, dtype) for _ in range(n)]
+        batch.append(ks, vs)
+        for e, k, v in zip(eb, ks, vs):
+            e.append(k, v)
+        T += S
+        for a, b in zip(ea, eb):
+            _stores_equal(a, b, T)
+    qs = [torch.randn(B, H * 4, 1, d, generator=gen).to(DEV, torch.float16) for _ in range(n)]
+    for o, e, q in zip(batch(qs), eb, qs):
+        _close(o, e.attention(q), 2e-5)
+
+
+def test_layer_batch_append_falls_back():
+    """Engines without a store yet, or of different lengths, append one by one."""
+    gen = torch.Generator().manual_seed(3)
+    engines = [Q.QuashKVEngine(head_dim=64, seed=20 + l, device=DEV) for l in range(3)]
+    batch = K.LayerBatch(engines)
+    x = torch.randn(2, 2, 40, 64, generator=gen).to(DEV, torch.bfloat16)
+    batch.append([x] * 3, [x] * 3)            # no stores yet: per engine
+    assert all(e.total_tokens == 40 for e in engines)
+    engines[0].append(x[:, :, :1], x[:, :, :1])
+    batch.append([x[:, :, :2]] * 3, [x[:, :, :2]] * 3)   # lengths differ: per engine
+    assert [e.total_tokens for e in engines] == [43, 42, 42]
+    with pytest.raises(ValueError, match="one key and one value"):
+        batch.append([x] * 2, [x] * 3)

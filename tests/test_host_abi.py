@@ -191,6 +191,31 @@ def test_layers_host_validation():
     assert "MFMA path" in lib.qkv_last_error().decode()
 
 
+def test_store_append_layers_host_validation():
+    """Argument checks of qkv_store_append_layers (all before any launch)."""
+    lib = N.lib()
+    a = N.ptr_array([256] * 33)
+    cb = LloydMaxCodebook(64, 2)
+    kc, kb = N.HostFloats(cb.centroids_host), N.HostFloats(cb.boundaries_host)
+    vb = N.HostFloats(LloydMaxCodebook(64, 3).boundaries_host)
+    args = lambda n, dt=2, d=64, cap=128, k=kc, arr=a: (
+        n, dt, arr, arr, 4, 1, d, 2, 3, arr, arr, arr, k.ptr, kb.ptr, vb.ptr, arr, arr, arr, arr,
+        cap, 100, None)
+    assert lib.qkv_store_append_layers(*args(0)) == N.QKV_E_INVALID
+    assert lib.qkv_store_append_layers(*args(33)) == N.QKV_E_INVALID
+    assert "n_layers" in lib.qkv_last_error().decode()
+    assert lib.qkv_store_append_layers(*args(2, dt=7)) == N.QKV_E_INVALID
+    assert lib.qkv_store_append_layers(*args(2, cap=100)) == N.QKV_E_INVALID   # capacity
+    assert lib.qkv_store_append_layers(*args(2, d=96)) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append_layers(*args(2, arr=None)) == N.QKV_E_INVALID
+    nul = N.ptr_array([256, 0])
+    assert lib.qkv_store_append_layers(*args(2, arr=nul)) == N.QKV_E_INVALID
+    assert "layer 1" in lib.qkv_last_error().decode()
+    asym = N.HostFloats([-1.0, -0.25, 0.5, 1.0])
+    assert lib.qkv_store_append_layers(*args(2, k=asym)) == N.QKV_E_UNSUPPORTED
+    assert "symmetric" in lib.qkv_last_error().decode()
+
+
 def test_mips_host_validation():
     lib = N.lib()
     assert lib.qkv_mips_workspace_bytes(10, 80, 2, 10, 100) == -1      # dim
