@@ -1221,10 +1221,10 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     int Q, int R, int chunks, Tables tb, int64_t t_stride, int64_t T, float scale, int causal,
     int64_t split_len, int final_out, int out_dtype, const qkv_v4i* __restrict__ aq_ws,
     const float* __restrict__ rowc_ws, float* __restrict__ part_o, float* __restrict__ part_ml) {
-  // DS: the stored head dim, 128 or 96; the operands are 128 wide, the
+  // DS: the stored head dim, 128, 96 or 64; the operands are 128 wide, the
   // coordinates past DS zero (query, Pi and S padded in the prologue)
   constexpr int D = 128;
-  static_assert(DS == 128 || DS == 96, "stored head dim");
+  static_assert(DS == 128 || DS == 96 || DS == 64, "stored head dim");
   constexpr int PD = DS / 32;  // dwords per stored plane
   // K rows of RDW dwords: IP keys PD (mbits + 1) (MSE planes + QJL plane), at
   // d = 128 also the mixed-key formats of 9, 10 or 12 dwords (the Tables
@@ -2408,11 +2408,13 @@ int fused_splits(int64_t groups, int64_t T) {
 }
 
 bool use_fused(const Tables& tb, int d, int64_t t_stride) {
-  return tb.fused_ok && (d == 128 || d == 96) && t_stride % 64 == 0;
+  return tb.fused_ok && (d == 128 || d == 96 || d == 64) && t_stride % 64 == 0;
 }
 
-// The single-call decode paths: decode_fused at d = 128 and 96, split_mfma at
-// d = 64.
+// The MFMA decode of the layer-batched and paged entries: decode_fused at
+// d = 128 and 96, split_mfma at d = 64 (its two row chunks per workgroup read
+// a 5-8-row GQA group's K/V once).  Single calls take decode_fused at d = 64
+// too (use_fused), with the split count of this model.
 bool use_mfma_path(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
   return d == 64 ? use_mfma(tb, d, t_stride, T, n_splits) : use_fused(tb, d, t_stride);
 }
@@ -2457,7 +2459,7 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
   } while (0)
   // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) and
   // 96-dim rows have no paged store
-  QKV_REQUIRE((rdw % 4 == 0 && d == 128) || kv.ptab == nullptr,
+  QKV_REQUIRE((rdw % 4 == 0 && d == 128) || d == 64 || kv.ptab == nullptr,
               "mixed keys and head_dim 96 are not paged");
 #define QKV_FUC(RW, VB)    \
   QKV_FU2(RW, VB, false);  \
@@ -2465,6 +2467,34 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
 #define QKV_FU96(RW, VB)              \
   QKV_FU3(RW, VB, false, 96);         \
   break
+#define QKV_FU64(RW, VB)                \
+  if (kv.ptab)                          \
+    QKV_FU3(RW, VB, true, 64);          \
+  else                                  \
+    QKV_FU3(RW, VB, false, 64);         \
+  break
+  if (d == 64) {
+    switch (rdw * 10 + vbits) {
+      case 41: QKV_FU64(4, 1);
+      case 42: QKV_FU64(4, 2);
+      case 43: QKV_FU64(4, 3);
+      case 44: QKV_FU64(4, 4);
+      case 61: QKV_FU64(6, 1);
+      case 62: QKV_FU64(6, 2);
+      case 63: QKV_FU64(6, 3);
+      case 64: QKV_FU64(6, 4);
+      case 81: QKV_FU64(8, 1);
+      case 82: QKV_FU64(8, 2);
+      case 83: QKV_FU64(8, 3);
+      case 84: QKV_FU64(8, 4);
+      default:
+        qkv_set_error("fused decode (d = 64): K rows of %d dwords / value bits %d unsupported",
+                      rdw, vbits);
+        return QKV_E_UNSUPPORTED;
+    }
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
   if (d == 96) {
     switch (rdw * 10 + vbits) {
       case 61: QKV_FU96(6, 1);
@@ -2513,6 +2543,7 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
       return QKV_E_UNSUPPORTED;
   }
 #undef QKV_FU96
+#undef QKV_FU64
 #undef QKV_FUC
 #undef QKV_FU
 #undef QKV_FU2
@@ -2990,7 +3021,7 @@ extern "C" int qkv_paged_decode_attention(
   kv.pmax = pages_per_seq;
   kv.plg = plg;
   kv.npages = num_pages;
-  if (d == 128) {
+  if (d == 128 || d == 64) {  // decode_fused, as the contiguous single call
     QLayers ql{};
     ql.q[0] = q;
     ql.pi[0] = pi;

@@ -49,7 +49,10 @@ def test_layers_match_per_layer_and_oracle(d, G, Qn, causal):
         ref = K.attention_store(q, st, T, kq.mse_quantizer.Pi, kq.mse_quantizer.codebook.centroids_host,
                                 vq.codebook.centroids_host, kq.S, kq.qjl_scale, causal=causal,
                                 n_splits=ns)
-        _close(o, ref, 1e-6)
+        # at d = 64 the batch runs split_mfma (exact integer scores) and the
+        # single call decode_fused (fp8 query digits): both sit within 2e-5
+        # of the oracle, not bit-identical to each other
+        _close(o, ref, 1e-6 if d != 64 else 2e-5)
     # one layer against the oracle on its stored codes
     e, q, o = engines[2], qs[2], outs[2]
     st, kq, vq = e._store, e.key_quantizer, e.value_quantizer

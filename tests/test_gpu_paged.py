@@ -258,5 +258,11 @@ def test_paged_layers_match_single_layer_calls(d, page_tokens):
             page_tokens, st.num_pages, T, B, Hq, H, Q, d, 2, 3, kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr,
             kq.S.data_ptr(), float(kq.qjl_scale), 1.0 / math.sqrt(d), 0, ref.data_ptr(),
             N.QKV_F32, ws.data_ptr(), ws_bytes, splits, N.stream(torch.device(DEV))))
-        assert torch.equal(o, ref)
+        if d == 64:
+            # the batch runs split_mfma (exact integer scores), the single call
+            # decode_fused (fp8 query digits): both within 2e-5 of the oracle
+            err = float((o - ref).double().norm() / ref.double().norm())
+            assert err <= 2e-5, err
+        else:
+            assert torch.equal(o, ref)
         _close(o, _oracle(q, e, causal=False))
