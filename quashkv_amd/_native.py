@@ -218,7 +218,15 @@ def dense(*tensors: Optional[torch.Tensor]):
     return out
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device: torch.device) -> int:
+    """The current HIP stream of ``device`` as an integer handle (the raw
+    query skips building a torch Stream object on every kernel call)."""
+    if _RAW_STREAM is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

@@ -103,6 +103,7 @@ class QuashKVEngine:
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
         self._host_tables = None   # codebook tables passed by value to qkv_store_append
+        self._attn_tables = None   # (key MSE, value) centroids for the decode entry points
         # mixed keys: (perm, pi_perm, n_out, host tables, S in slot order or None)
         self._kmix_tables = None
 
@@ -359,9 +360,12 @@ class QuashKVEngine:
                 workspace=self._workspace, n_splits=splits,
                 signs_perm=self._kmix_signs(queries.device),
                 qjl_scale=kq.qjl_scale if self._kmix_ip else 0.0)
+        if self._attn_tables is None:
+            self._attn_tables = (N.HostFloats(kq.mse_quantizer.codebook.centroids_host),
+                                 N.HostFloats(vq.codebook.centroids_host))
+        kc, vc = self._attn_tables
         return attention_store(
-            queries, st, self._total_tokens, kq.mse_quantizer.Pi,
-            kq.mse_quantizer.codebook.centroids_host, vq.codebook.centroids_host, kq.S,
+            queries, st, self._total_tokens, kq.mse_quantizer.Pi, kc, vc, kq.S,
             kq.qjl_scale, scale=scale, causal=causal, out_dtype=out_dtype,
             workspace=self._workspace, n_splits=splits)
 

@@ -115,7 +115,8 @@ def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Ten
                     n_splits: Optional[int] = None) -> torch.Tensor:
     """Decode attention of (B, Hq, Q, d) queries over the first T tokens of a
     cache store.  ``key_centroids`` / ``val_centroids`` are the codebook values
-    (host floats).  Returns (B, Hq, Q, d) in ``out_dtype``."""
+    (host floats, or ``_native.HostFloats`` tables a caller keeps).  Returns
+    (B, Hq, Q, d) in ``out_dtype``."""
     dev = N.require_gpu(queries, store.kst, Pi, what="attention")
     B, Hq, Q, d = queries.shape
     Hkv = store.H
@@ -131,14 +132,15 @@ def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Ten
     L = N.lib()
     if n_splits is None:
         n_splits = L.qkv_attention_splits(B, Hq, Hkv, Q, d, T)
-    need = L.qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits)
-    if workspace is None or workspace.numel() < need:
+    if workspace is None:   # (a caller's workspace is size-checked by the library)
+        need = L.qkv_attention_workspace_bytes(B, Hq, Hkv, Q, d, n_splits)
         workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
     q = queries.contiguous()
     if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
         q = q.float()
     Pi, S = N.dense(Pi, S)
-    kc, vc = N.HostFloats(key_centroids), N.HostFloats(val_centroids)
+    kc = key_centroids if isinstance(key_centroids, N.HostFloats) else N.HostFloats(key_centroids)
+    vc = val_centroids if isinstance(val_centroids, N.HostFloats) else N.HostFloats(val_centroids)
     out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
     N.check(L.qkv_decode_attention(
         q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
