@@ -1,0 +1,1122 @@
+// Fused compress straight into the cache store, for bf16, fp16 or fp32 K and V
+// rows with d = 128 or 64: normalise -> rotate (MFMA) -> Lloyd-Max boundary
+// search -> QJL sign -> bit planes, one pass over the inputs.
+//
+// Reference: QuashKVEngine.append (quashkv/engine.py:145-172) compresses keys
+// with InnerProductQuantizer.compress (quashkv/quantizer.py:211-242) and values
+// with MSEQuantizer.compress (quashkv/quantizer.py:113-131); the GPU operator
+// surface is fused_compress_ip / fused_compress_mse
+// (quashkv/triton_kernels/compress.py:210-303).  The codes land in the K-row and
+// V-tile store formats that the decode kernel reads.
+//
+// Rotation.  z = x Pi^T runs on the 32x32x16 bf16 (fp16) MFMA with x as it is
+// stored (a bf16 / fp16 value is exact in the operand type) and Pi split into
+// a high and a low 16-bit part, Pi ~= Pi_hi + Pi_lo, accumulated in fp32: two
+// MFMA passes carry ~16 (bf16) / ~22 (fp16) significant bits of Pi, against
+// 24 for the reference's fp32 GEMM, and y = z / |x| (the reference divides
+// before the GEMM).  fp32 rows are divided first, as the reference does:
+// x 2^8 / |x| is split into fp16 hi + lo and the fp16 MFMA sums hi Pi_hi +
+// hi Pi_lo + lo Pi_hi (~22 significant bits).  Codes computed from x may
+// therefore differ from the reference's where y lies within ~1e-5 (bf16 /
+// fp16 rows) or ~1e-6 (fp32 rows) relative of a boundary.  The same kernels take a given fp32 y instead of x
+// (FROM_Y: the *_rotated entry points) and then run the search, QJL and store
+// code below on it; from an identical y the codes are the reference's, bit for
+// bit, ties included.
+//
+// Boundary search as lane masks.  For the value y of one coordinate the
+// reference's code is #{i : t_i < y} (torch.bucketize, right=False) and the
+// QJL bit is [(y - c_code) S_j >= 0].  Keys search the fine list
+// c_0 < t_0 < c_1 < ... < c_{2^m-1} (centroids and boundaries interleaved):
+// its count f gives code = f >> 1 and, with the centroids counted as
+// [c <= y] where S_j > 0 and [c < y] where S_j < 0, the QJL bit = (f & 1)
+// xor [S_j < 0] -- exact, r = 0 included.  Lloyd-Max lists are symmetric about
+// 0 (t_mid = 0), so the top bit of f is [y > 0] and the rest is a search of
+// |y| in the positive half, complemented for y <= 0.  Strictness survives the
+// mirror through integer keys: a = rotl(bits(y), 1) = 2 |y|_bits + sign, and
+// thresholds 2 |p|_bits, so [a > 2 p] is [|y| > p] for y > 0 and [|y| >= p]
+// for y < 0 -- after the complement, a strict count of y on both sides.  The
+// centroid level compares a xor [S_j > 0], which flips that strictness for
+// S_j > 0.  Values search their boundaries the same way without the centroid
+// level.  A binary search decides one code bit per level with one compare,
+// whose 64-lane result mask is directly that bit plane for the wave's 64
+// values; the next level's threshold is picked per lane with v_cndmask on the
+// masks already found (levels of 1, 2, 4, ... candidates).
+//
+// Orientation.  32x32x16 MFMAs: a result VGPR holds one C row per 32-lane
+// half, 32 consecutive columns, so each half of a compare mask is one whole
+// 32-bit store word.  Keys: C = tokens x coordinates, a mask half is the
+// plane word of 32 coordinates of one token (one dword of a K row).  Values:
+// C = coordinates x tokens, a mask half is the plane word of one coordinate
+// over 32 tokens (one V-tile word).  The A and B operand layouts are
+// symmetric, so the same x and Pi register fragments serve both orders.
+// Mask words are placed into staging VGPRs with v_writelane and stored with
+// coalesced vector stores.
+//
+// This header holds the device side (the kernels and their helpers) of the
+// fused store append; qkv_append.hip holds its C ABI and qkv_append_kv.hip
+// the one-launch key + value kernels, each translation unit instantiating
+// the templates it launches.
+
+#pragma once
+
+#include <cmath>
+#include <cstring>
+#include <type_traits>
+#include <utility>
+
+#include "qkv_common.h"
+
+// Types shared by both translation units of the append (kernel arguments and
+// the one-launch key + value launcher's signature).
+namespace qkv_app {
+
+// Positive half of a symmetric comparison list as integer keys 2 bits(p),
+// ascending (at most 7 entries: 4-bit value boundaries, the 3-bit key MSE
+// fine list).
+struct Half {
+  uint32_t t[7];
+};
+
+// Per-layer pointers of a layer-batched append (kernel arguments by value):
+// rows, Pi, S (keys), store array and norms of layer l = blockIdx.y.
+constexpr int kMaxAppendLayers = 32;
+struct AppendLayers {
+  const void* x[kMaxAppendLayers];
+  const float* pi[kMaxAppendLayers];
+  const float* signs[kMaxAppendLayers];
+  void* st[kMaxAppendLayers];
+  float* nrm[kMaxAppendLayers];
+};
+
+// One launch of append_k_run and append_v_run over n_layers contiguous stores
+// (grid.y = layer, grid.x = key workgroups then value workgroups), for
+// vbits == mbits + 1 (defined in qkv_append_kv.hip).  Returns false, launching
+// nothing, for the combinations it does not instantiate.
+bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& ak,
+                      const AppendLayers& av, int n_layers, int kblocks, int vblocks, int64_t S,
+                      int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, Half fine,
+                      Half bnd, int64_t t_stride, int64_t t0, hipStream_t s);
+
+}  // namespace qkv_app
+
+namespace {
+
+using qkv_app::AppendLayers;
+using qkv_app::Half;
+using qkv_app::kMaxAppendLayers;
+
+typedef __bf16 qkv_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 qkv_f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kD = 128;                 // head dim of the mixed-key path
+constexpr int kHalves = 1;              // 32-token MFMA column blocks per wave tile
+constexpr int kTok = 32 * kHalves;      // tokens per wave tile
+constexpr int kWaves = 8;               // waves per workgroup (two workgroups per CU)
+constexpr int kThreads = 64 * kWaves;
+// Pi fragments [block of 32 rows][k-step of 16][split][lane]: 64 KiB at d = 128
+template <int D>
+constexpr int frag_n() { return (D / 32) * (D / 16) * 2 * 64; }
+constexpr int kFragN = frag_n<kD>();
+constexpr float kPScaleF16 = 256.f;     // keeps the fp16 low part of Pi out of subnormals
+
+typedef float qkv_f32x16 __attribute__((ext_vector_type(16)));
+
+template <bool F16>
+__device__ __forceinline__ qkv_f32x16 mma(uint4 a, uint4 b, qkv_f32x16 c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(qkv_f16x8, a),
+                                                  __builtin_bit_cast(qkv_f16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(qkv_bf16x8, a),
+                                                   __builtin_bit_cast(qkv_bf16x8, b), c, 0, 0, 0);
+}
+
+// v_writelane through the LLVM intrinsic (no clang builtin spells it), so the
+// compiler sees the SGPR read and pads the VALU-writes-SGPR hazard before it.
+extern "C" __device__ int qkv_llvm_writelane(int val, int lane, int old) __asm(
+    "llvm.amdgcn.writelane.i32");
+
+// Value `val` (wave-uniform) into lane L of `old`.
+template <int L>
+__device__ __forceinline__ uint32_t put_lane(uint32_t old, uint32_t val) {
+  static_assert(L >= 0 && L < 64, "lane");
+  return static_cast<uint32_t>(
+      qkv_llvm_writelane(static_cast<int>(val), L, static_cast<int>(old)));
+}
+
+// A wave-uniform value held in a VGPR (a v_cndmask may then take two of them
+// with its mask without exceeding the one-scalar-operand limit).
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "s"(x));
+  return r;
+}
+
+__device__ __forceinline__ uint64_t lanes_where(bool p) { return __builtin_amdgcn_ballot_w64(p); }
+
+// f(std::integral_constant<int, 0>), ..., f(<N - 1>): compile-time unrolled
+// loops whose index feeds template arguments (v_writelane lane numbers).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Binary search of the key a in the ascending key list t[0 .. 2^LM - 2]: bit i
+// of #{j : t[j] < a} as the lane mask g[i].  With CLAST the last level (whose
+// candidates are the list's even entries) compares ac instead of a.
+template <int LM, bool CLAST>
+__device__ __forceinline__ void search_levels(uint32_t a, uint32_t ac, const uint32_t* t,
+                                              bool (&c)[LM]) {
+  static_for<LM>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;  // level k decides bit LM - 1 - k
+    uint32_t cand[1 << k];
+#pragma unroll
+    for (int p = 0; p < (1 << k); ++p) cand[p] = t[(2 * p + 1) * (1 << (LM - 1 - k)) - 1];
+    // prefix bit j (LSB first) is c[LM - k + j]
+#pragma unroll
+    for (int j = 0; j < k; ++j)
+#pragma unroll
+      for (int q = 0; q < (1 << (k - 1 - j)); ++q)
+        cand[q] = c[LM - k + j] ? cand[2 * q + 1] : cand[2 * q];
+    const uint32_t av = (CLAST && k == LM - 1) ? ac : a;
+    c[LM - 1 - k] = av > cand[0];
+  });
+}
+
+template <int LM, bool CLAST>
+__device__ __forceinline__ void search_keys(uint32_t a, uint32_t ac, const uint32_t* t,
+                                            uint64_t (&g)[LM]) {
+  bool c[LM];
+  search_levels<LM, CLAST>(a, ac, t, c);
+#pragma unroll
+  for (int i = 0; i < LM; ++i) g[i] = lanes_where(c[i]);
+}
+
+// Strict count #{j : F[j] < y} over a list F of 2^L - 1 entries symmetric
+// about 0 (F[j] = -F[2^L - 2 - j], middle entry 0), given the integer keys of
+// its positive half: bit i as the lane mask m[i].  The top bit is [y > 0]; the
+// others search a = rotl(bits(y), 1) in the positive half and are
+// complemented for y <= 0.  With CLAST the last level counts an entry equal to
+// |y| as below y on the lanes where cx = 1 (see the file comment).
+template <int L, bool CLAST>
+__device__ __forceinline__ void search_sym(float y, const uint32_t* p, uint32_t cx,
+                                           uint64_t (&m)[L]) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, y);
+  // [y > 0] on the bits (denormals included, whatever the float mode)
+  const uint64_t pos = lanes_where(static_cast<int32_t>(u) > 0);
+  m[L - 1] = pos;
+  if constexpr (L > 1) {
+    const uint32_t a = __builtin_amdgcn_alignbit(u, u, 31);
+    uint64_t g[L - 1];
+    search_keys<L - 1, CLAST>(a, a ^ cx, p, g);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
+  }
+}
+
+// search_sym's count for this lane alone (no lane masks).
+template <int L, bool CLAST>
+__device__ __forceinline__ uint32_t search_sym_count(float y, const uint32_t* p, uint32_t cx) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, y);
+  const bool pos = static_cast<int32_t>(u) > 0;
+  uint32_t f = pos ? 1u << (L - 1) : 0u;
+  if constexpr (L > 1) {
+    const uint32_t a = __builtin_amdgcn_alignbit(u, u, 31);
+    bool c[L - 1];
+    search_levels<L - 1, CLAST>(a, a ^ cx, p, c);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) f |= (c[i] == pos ? 1u : 0u) << i;
+  }
+  return f;
+}
+
+typedef __bf16 qkv_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 qkv_f16x2 __attribute__((ext_vector_type(2)));
+
+// s + sum of squares of the eight 16-bit values in q (v_dot2: exact products,
+// fp32 accumulation)
+template <bool F16>
+__device__ __forceinline__ float sumsq(uint4 q, float s) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (F16)
+      s = __builtin_amdgcn_fdot2(__builtin_bit_cast(qkv_f16x2, w[i]),
+                                 __builtin_bit_cast(qkv_f16x2, w[i]), s, false);
+    else
+      s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(qkv_bf16x2, w[i]),
+                                          __builtin_bit_cast(qkv_bf16x2, w[i]), s, false);
+  }
+  return s;
+}
+
+template <bool F16>
+__device__ __forceinline__ uint16_t to16(float v) {
+  if constexpr (F16)
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+  else
+    return qkv_f32_to_bf16(v);
+}
+
+template <bool F16>
+__device__ __forceinline__ float from16(uint16_t h) {
+  if constexpr (F16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  else
+    return qkv_bf16_to_f32(h);
+}
+
+// Stage the rotation operand in LDS.  Entry ((b * 8 + s) * 2 + split) * 64 + l
+// holds, for lane l, Pi'[32 b + (l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
+// eight 16-bit values: the high part (split 0) or the low part (split 1) of
+// Pi' = Pi * pscale.
+template <bool F16, int D = kD>
+__device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi, float pscale) {
+  // kThreads threads (every launch uses that block size); each takes NPT
+  // (block, k-step, lane) slots and writes both splits of each, with all of
+  // its Pi loads in flight before the first conversion
+  constexpr int NKS = D / 16;  // k-steps
+  constexpr int NPT = frag_n<D>() / 2 / kThreads;
+  static_assert(NPT * 2 * kThreads == frag_n<D>(), "whole slots per thread");
+  float4 p[NPT][2];
+#pragma unroll
+  for (int x = 0; x < NPT; ++x) {
+    const int u = threadIdx.x + kThreads * x;
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
+    const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
+    p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
+    p[x][1] = *reinterpret_cast<const float4*>(pi + j * D + k0 + 4);
+  }
+#pragma unroll
+  for (int x = 0; x < NPT; ++x) {
+    const int u = threadIdx.x + kThreads * x;
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
+    // pscale = 2^k: the scaling is exact
+    const float v[8] = {p[x][0].x * pscale, p[x][0].y * pscale, p[x][0].z * pscale,
+                        p[x][0].w * pscale, p[x][1].x * pscale, p[x][1].y * pscale,
+                        p[x][1].z * pscale, p[x][1].w * pscale};
+    uint32_t hi[8], lo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint16_t h = to16<F16>(v[i]);
+      hi[i] = h;
+      lo[i] = to16<F16>(v[i] - from16<F16>(h));
+    }
+    const int e = ((b * NKS + s) * 2) * 64 + ln;
+    frag[e] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
+                         hi[6] | (hi[7] << 16));
+    frag[e + 64] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
+                              lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
+  }
+}
+
+// x fragments of a wave tile: xf[tt][s], lane l = (row l & 31, half l >> 5)
+// holds x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt]
+// (this lane's token row of block tt; callers point lanes without a token at a
+// valid row, whose results are never stored).
+template <int NKS>
+__device__ __forceinline__ void load_x(uint4 (&xf)[kHalves][NKS],
+                                       const uint16_t* const (&row)[kHalves], int lane) {
+#pragma unroll
+  for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+    for (int s = 0; s < NKS; ++s)
+      xf[tt][s] = *reinterpret_cast<const uint4*>(row[tt] + 16 * s + 8 * (lane >> 5));
+}
+
+// fp32 rows for the fp16 MFMA: x 2^8 / |x| = hi + lo, both fp16, in load_x's
+// fragment layout (xh, xl).  The rotation then sums hi Pi_hi + hi Pi_lo +
+// lo Pi_hi (Pi' = 2^8 Pi split likewise), ~22 significant bits, and the MFMA
+// result is 2^16 y.  |x| (clamped at 1e-8, as the reference clamps) of the
+// lane's token row per block in nrm.
+template <int NKS>
+__device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl)[kHalves][NKS],
+                                           float (&nrm)[kHalves],
+                                           const float* const (&row)[kHalves], int lane) {
+#pragma unroll
+  for (int tt = 0; tt < kHalves; ++tt) {
+    float4 v[NKS][2];
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const float* p = row[tt] + 16 * s + 8 * (lane >> 5);
+      v[s][0] = *reinterpret_cast<const float4*>(p);
+      v[s][1] = *reinterpret_cast<const float4*>(p + 4);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        ss = fmaf(v[s][h].x, v[s][h].x, ss);
+        ss = fmaf(v[s][h].y, v[s][h].y, ss);
+        ss = fmaf(v[s][h].z, v[s][h].z, ss);
+        ss = fmaf(v[s][h].w, v[s][h].w, ss);
+      }
+    ss += __shfl_xor(ss, 32, 64);
+    const float n = fmaxf(sqrtf(ss), 1e-8f);
+    nrm[tt] = n;
+    const float sc = 256.f / n;
+#pragma unroll
+    for (int s = 0; s < NKS; ++s) {
+      const float a[8] = {v[s][0].x, v[s][0].y, v[s][0].z, v[s][0].w,
+                          v[s][1].x, v[s][1].y, v[s][1].z, v[s][1].w};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a0 = a[2 * e] * sc, a1 = a[2 * e + 1] * sc;
+        const _Float16 h0 = static_cast<_Float16>(a0), h1 = static_cast<_Float16>(a1);
+        const _Float16 l0 = static_cast<_Float16>(a0 - static_cast<float>(h0));
+        const _Float16 l1 = static_cast<_Float16>(a1 - static_cast<float>(h1));
+        hw[e] = __builtin_bit_cast(uint16_t, h0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, h1)) << 16);
+        lw[e] = __builtin_bit_cast(uint16_t, l0) |
+                (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, l1)) << 16);
+      }
+      xh[tt][s] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      xl[tt][s] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ keys
+
+// One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
+// grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
+// MB MSE planes, then the QJL plane).  FROM_Y: `xin` holds fp32 rotated unit
+// rows y (rows as above) and `nin` their norms; the normalisation and the
+// rotation are skipped, everything after them is the same code.
+// XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
+template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
+__device__ __forceinline__ void append_k_run(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
+    QkvPages pg, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
+  constexpr int L = MB + 1;           // search levels over the fine list
+  constexpr int NP = (1 << MB) - 1;   // positive half of the fine list c_0, t_0, ..., c_{2^MB-1}
+  constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
+  constexpr int NKS = D / 16;         // k-steps
+  constexpr int RD = NBK * L;         // dwords per row
+  constexpr int NSK = RD * kTok / 64; // staging dwords per lane
+  static_assert(RD * kTok % 64 == 0, "whole staging dwords");
+  if constexpr (!FROM_Y) {
+    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
+
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  uint32_t fv[NP];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) fv[i] = in_vgpr(fine.t[i]);
+  uint64_t sneg[NBK];  // lanes whose coordinate 32 n + (l & 31) has S < 0
+  uint32_t cx[NBK];    // 1 where S >= 0: the centroid level counts c <= y there
+#pragma unroll
+  for (int n = 0; n < NBK; ++n) {
+    const bool neg = signs[32 * n + li] < 0.f;
+    sneg[n] = lanes_where(neg);
+    cx[n] = neg ? 0u : 1u;
+  }
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(nb) * kWaves;
+
+  for (int64_t tile = int64_t(bid) * kWaves + wv; tile < ntiles; tile += wstep) {
+    const int64_t grp = tile / tpg;
+    const int64_t s0 = (tile - grp * tpg) * kTok;
+    const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    QkvSpan sp{};
+    if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, t0 + s0);
+    uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    if constexpr (FROM_Y) {
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && 32 * tt + li < nv) {
+          const int64_t t = t0 + s0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) knorm[r] = nin[grp * S + s0 + 32 * tt + li];
+        }
+    } else {
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+        load_x_f32<NKS>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+        load_x<NKS>(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
+
+      // norms; the scale of token t's MFMA result (1 / n, or 2^-16 for fp32
+      // rows scaled before the rotation) goes to LDS, read back in C-row order
+      // (rows 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four
+      // consecutive tokens)
+      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        if (lane < 32) {
+          if (32 * tt + li < nv) {
+            const int64_t t = t0 + s0 + 32 * tt + li;
+            const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+            if (r >= 0) knorm[r] = nrm[tt];
+          }
+          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+      __builtin_amdgcn_wave_barrier();
+    }
+
+    uint32_t stg[NSK];
+#pragma unroll
+    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
+
+    static_for<NBK>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
+      constexpr int n = decltype(nc)::value;
+      // one coordinate block at a time: keeps the scheduler from overlapping
+      // blocks (and their accumulators and fragments) beyond the register file
+      __builtin_amdgcn_sched_barrier(0);
+      // y of coordinate 32 n + (l & 31) for tokens 32 tt + 8 (v >> 2) + 4 (l >> 5) + (v & 3)
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * D + 32 * n + li];
+          }
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+        for (int s = 0; s < NKS; ++s)
+#pragma unroll
+          for (int sp2 = 0; sp2 < 2; ++sp2) {
+            const uint4 bf = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+              if (F32 && sp2 == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+            }
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          if constexpr (F32) {  // rows scaled before the rotation: one constant
+#pragma unroll
+            for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * (1.f / 65536.f);
+            continue;
+          }
+          float4 iv4[4];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float4 q4 = iv4[v >> 2];
+            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            yv[tt][v] = acc[tt][v] * iv;
+          }
+        }
+      }
+      static_for<kHalves>([&](auto tc) {
+        constexpr int tt = decltype(tc)::value;
+        static_for<16>([&](auto vc) {
+          constexpr int v = decltype(vc)::value;
+          uint64_t f[L];
+          search_sym<L, true>(yv[tt][v], fv, cx[n], f);
+          // token ta (lanes 0..31) and ta + 4 (lanes 32..63)
+          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);
+          static_for<L>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;  // plane r: MSE bit r, r = MB: QJL
+            const uint64_t w = r < MB ? f[r < MB ? r + 1 : 0] : (f[0] ^ sneg[n]);
+            constexpr int D0 = ta * RD + NBK * r + n, D1 = (ta + 4) * RD + NBK * r + n;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w >> 32));
+          });
+        });
+      });
+    });
+
+    if constexpr (PAGED) {
+      // dword w of the tile: row w / RD (token t0 + s0 + w / RD), dword w % RD
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kst);
+#pragma unroll
+      for (int i = 0; i < NSK; ++i) {
+        const int w = i * 64 + lane, r = w / RD;
+        const int64_t row = sp.row(t0 + s0 + r);
+        if (w < nv * RD && row >= 0) dst[row * RD + (w - r * RD)] = stg[i];
+      }
+    } else {
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+#pragma unroll
+      for (int i = 0; i < NSK; ++i) {
+        const int w = i * 64 + lane;
+        if (w < nv * RD) dst[w] = stg[i];
+      }
+    }
+  }
+}
+
+template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
+    QkvPages pg) {
+  __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];  // Pi operand fragments
+  __shared__ float4 inv_s[kWaves][kTok / 4];         // 1 / norm of each wave's tokens
+  append_k_run<MB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, signs, fine, kst, knorm,
+                                         t_stride, t0, pg, frag, inv_s, blockIdx.x, gridDim.x);
+}
+
+// append_k_mfma over the contiguous stores of blockIdx.y's layer
+template <int MB, int XT, int D>
+__global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, int64_t S,
+                                                               int64_t tpg, int64_t ntiles,
+                                                               Half fine, int64_t t_stride,
+                                                               int64_t t0) {
+  __shared__ uint4 frag[frag_n<D>()];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  const int l = blockIdx.y;
+  append_k_run<MB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], al.signs[l],
+                                        fine, static_cast<uint8_t*>(al.st[l]), al.nrm[l],
+                                        t_stride, t0, QkvPages{}, frag, inv_s, blockIdx.x,
+                                        gridDim.x);
+}
+
+// ------------------------------------------------- mixed-precision keys
+
+// Mixed-precision keys over permuted coordinates (outliers first; the caller
+// passes Pi with its rows permuted and, for IP keys, S in the same slot order)
+// into rows of whole dwords:
+//  * !IPM, MixedPrecisionMSEQuantizer (quashkv/mixed_precision.py:132-158)
+//    with 3-bit outlier and 2-bit regular channels: plane b0 and plane b1 of
+//    every slot, then b2 of the NO outlier slots, then their parity
+//    b0^b1^b2 -- 32 + NO / 4 bytes;
+//  * IPM, MixedPrecisionIPQuantizer (quashkv/mixed_precision.py:283-297) with
+//    a 2-bit outlier / 1-bit regular MSE stage: plane b0 of every slot, the
+//    QJL plane [(y - c) S >= 0] of every slot, then b1 of the NO outlier
+//    slots -- 32 + NO / 8 bytes.  The search runs over each codebook's fine
+//    list as append_k_mfma's does, so the QJL tie rule is the reference's.
+// The outlier slots fill whole 32-slot blocks (NO = 32 or 64), so each block's
+// codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
+// rows in slot order and `nin` their norms.
+template <int NO, int XT, bool FROM_Y, bool IPM>
+__global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
+    Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
+    int64_t t0) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;        // fp16 MFMA / fp32 rows split for it
+  constexpr int NOB = NO / 32;                         // outlier blocks
+  constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
+  constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
+  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  if constexpr (!FROM_Y) {
+    stage_pi<F16>(frag, pi_perm, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
+
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  // positive halves: outlier and regular boundaries (MSE keys) or fine lists
+  // (IP keys), three and one entries either way
+  uint32_t pov[3], prv[1];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.t[i]);
+  prv[0] = in_vgpr(pr.t[0]);
+  uint64_t sneg[4] = {0, 0, 0, 0};  // IP: lanes whose slot 32 n + (l & 31) has S < 0
+  uint32_t cx[4] = {0u, 0u, 0u, 0u};  // IP: 1 where S >= 0 (centroid level counts c <= y)
+  if constexpr (IPM) {
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const bool neg = signs_perm[32 * n + li] < 0.f;
+      sneg[n] = lanes_where(neg);
+      cx[n] = neg ? 0u : 1u;
+    }
+  }
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
+
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
+    const int64_t grp = tile / tpg;
+    const int64_t s0 = (tile - grp * tpg) * kTok;
+    const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    float* nrow = knorm + grp * t_stride + t0 + s0;
+    uint4 xf[kHalves][8];
+    uint4 xl[kHalves][F32 ? 8 : 1];  // fp32 rows: the low fp16 parts
+    if constexpr (FROM_Y) {
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && 32 * tt + li < nv) nrow[32 * tt + li] = nin[grp * S + s0 + 32 * tt + li];
+    } else {
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+        load_x_f32<8>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+        load_x(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
+      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        if (lane < 32) {
+          if (32 * tt + li < nv) nrow[32 * tt + li] = nrm[tt];
+          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+      __builtin_amdgcn_wave_barrier();
+    }
+
+    uint32_t stg[NSK];
+#pragma unroll
+    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
+
+    static_for<4>([&](auto nc) {  // coordinate block n
+      constexpr int n = decltype(nc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * kD + 32 * n + li];
+          }
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) {
+            const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+              if (F32 && sp == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+            }
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float4 iv4[4];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float4 q4 = iv4[v >> 2];
+            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            yv[tt][v] = acc[tt][v] * iv;
+          }
+        }
+      }
+      static_for<kHalves>([&](auto tc) {
+        constexpr int tt = decltype(tc)::value;
+        static_for<16>([&](auto vc) {
+          constexpr int v = decltype(vc)::value;
+          const float y = yv[tt][v];
+          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);  // token of lanes 0..31
+          // plane words in row order: MSE keys b0, b1 (+ outliers: b2, parity);
+          // IP keys b0, QJL (+ outliers: b1)
+          uint64_t w[4] = {0, 0, 0, 0};
+          if constexpr (IPM) {
+            if constexpr (n < NOB) {
+              uint64_t f[3];
+              search_sym<3, true>(y, pov, cx[n], f);
+              w[0] = f[1];
+              w[1] = f[0] ^ sneg[n];
+              w[2] = f[2];
+            } else {
+              uint64_t f[2];
+              search_sym<2, true>(y, prv, cx[n], f);
+              w[0] = f[1];
+              w[1] = f[0] ^ sneg[n];
+            }
+          } else if constexpr (n < NOB) {
+            uint64_t m[3];
+            search_sym<3, false>(y, pov, 0u, m);
+            w[0] = m[0];
+            w[1] = m[1];
+            w[2] = m[2];
+            w[3] = m[0] ^ m[1] ^ m[2];
+          } else {
+            uint64_t m[2];
+            search_sym<2, false>(y, prv, 0u, m);
+            w[0] = m[0];
+            w[1] = m[1];
+          }
+          constexpr int NW = n < NOB ? (IPM ? 3 : 4) : 2;
+          static_for<NW>([&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            // row dword: whole planes at word n, outlier words after them
+            constexpr int dw = r < 2 ? 4 * r + n : 8 + n + (r == 3 ? NOB : 0);
+            constexpr int D0 = ta * RD + dw, D1 = (ta + 4) * RD + dw;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w[r]));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w[r] >> 32));
+          });
+        });
+      });
+    });
+
+    uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+#pragma unroll
+    for (int i = 0; i < NSK; ++i) {
+      const int D = i * 64 + lane;
+      if (D < nv * RD) dst[D] = stg[i];
+    }
+  }
+}
+
+// ------------------------------------------------ quantizer-API compress
+
+// MSEQuantizer.compress / InnerProductQuantizer.compress and fused_compress_*
+// (quashkv/quantizer.py:113-131,211-242, quashkv/triton_kernels/compress.py:
+// 210-303) on the MFMA: n rows of dimension D into one uint8 code (and, IP,
+// one QJL bit) per coordinate, row-major, and the fp32 norms.  The rotation, search and tie rules are append_k_mfma's
+// (tokens x coordinates); IP searches the fine list (L = MB + 1 levels), MSE
+// the boundaries (L = bits levels).  A lane's code byte lands beside its
+// 31 neighbours' (32 coordinates of one row per half-wave).
+template <int L, bool IP, int XT, int D>
+__global__ __launch_bounds__(kThreads, 4) void compress_mfma(
+    const void* __restrict__ xin, int64_t n, int64_t ntiles, const float* __restrict__ pi,
+    const float* __restrict__ signs, Half lst, uint8_t* __restrict__ codes,
+    uint8_t* __restrict__ qjl, float* __restrict__ norms) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;
+  constexpr int NP = (1 << (L - 1)) - 1;  // positive half of the searched list
+  constexpr int NBK = D / 32, NKS = D / 16;
+  __shared__ uint4 frag[frag_n<D>()];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  uint32_t lv[NP > 0 ? NP : 1];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) lv[i] = in_vgpr(lst.t[i]);
+  uint32_t cx[NBK];  // IP: 1 where S >= 0 (the centroid level counts c <= y there)
+  uint32_t neg[NBK];  // IP: 1 where S < 0
+#pragma unroll
+  for (int b = 0; b < NBK; ++b) {
+    const bool ng = IP && signs[32 * b + li] < 0.f;
+    cx[b] = ng ? 0u : 1u;
+    neg[b] = ng ? 1u : 0u;
+  }
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t wstep = int64_t(gridDim.x) * kWaves;
+
+  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
+    const int64_t s0 = tile * kTok;
+    const int nv = static_cast<int>(min<int64_t>(kTok, n - s0));
+    uint4 xf[kHalves][NKS];
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    float nrm[kHalves];
+    if constexpr (F32) {
+      const float* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = static_cast<const float*>(xin) + (s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x_f32<NKS>(xf, xl, nrm, row, lane);
+    } else {
+      const uint16_t* row[kHalves];
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = static_cast<const uint16_t*>(xin) + (s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x<NKS>(xf, row, lane);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float ss = 0.f;
+#pragma unroll
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+      }
+    }
+    float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+#pragma unroll
+    for (int tt = 0; tt < kHalves; ++tt) {
+      if (lane < 32) {
+        if (32 * tt + li < nv) norms[s0 + 32 * tt + li] = nrm[tt];
+        if (!F32) invw[32 * tt + li] = iscale / nrm[tt];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+    __builtin_amdgcn_wave_barrier();
+
+    static_for<NBK>([&](auto nc) {  // coordinates 32 b .. 32 b + 31
+      constexpr int b = decltype(nc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+      for (int s = 0; s < NKS; ++s)
+#pragma unroll
+        for (int sp2 = 0; sp2 < 2; ++sp2) {
+          const uint4 bf = frag[((b * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt) {
+            acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
+            if (F32 && sp2 == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
+          }
+        }
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        float4 iv4[4];
+        if constexpr (!F32) {
+#pragma unroll
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+        }
+        // this lane's first token 32 tt + 4 (l >> 5) at coordinate 32 b + (l & 31); the
+        // others sit at fixed offsets from it
+        const int64_t o0 = (s0 + 32 * tt + 4 * (lane >> 5)) * D + 32 * b + li;
+        uint8_t* cb = codes + o0;
+        uint8_t* qb = IP ? qjl + o0 : nullptr;
+        const int tk0 = 32 * tt + 4 * (lane >> 5);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          float iv = 1.f / 65536.f;  // fp32 rows: scaled before the rotation
+          if constexpr (!F32) {
+            const float4 q4 = iv4[v >> 2];
+            iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+          }
+          // token tk0 + 8 (v >> 2) + (v & 3)
+          const int dt = 8 * (v >> 2) + (v & 3);
+          const uint32_t f = search_sym_count<L, IP>(acc[tt][v] * iv, lv, cx[b]);
+          if (tk0 + dt < nv) {
+            if constexpr (IP) {
+              cb[dt * D] = static_cast<uint8_t>(f >> 1);
+              qb[dt * D] = static_cast<uint8_t>((f & 1u) ^ neg[b]);
+            } else {
+              cb[dt * D] = static_cast<uint8_t>(f);
+            }
+          }
+        }
+      }
+    });
+  }
+}
+
+// ---------------------------------------------------------------- values
+
+// One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
+// so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
+// already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
+// their norms.
+template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
+__device__ __forceinline__ void append_v_run(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
+    float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg,
+    uint4* __restrict__ frag, int bid, int nb) {
+  constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
+  constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
+  constexpr int NBK = D / 32;        // coordinate blocks
+  constexpr int NKS = D / 16;        // k-steps
+  constexpr int NPW = D / 64;        // staging dwords per (tile, plane)
+  constexpr int NS = NPW * VB * kHalves;  // staging dwords per lane: tiles x VB planes x D / 64
+  if constexpr (!FROM_Y) {
+    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    __syncthreads();
+  }
+
+  const int lane = threadIdx.x & 63, li = lane & 31;
+  uint32_t bv[NP > 0 ? NP : 1];
+#pragma unroll
+  for (int i = 0; i < NP; ++i) bv[i] = in_vgpr(bnd.t[i]);
+  const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
+  const int64_t a_base = t0 & ~int64_t(31);
+  const int64_t wstep = int64_t(nb) * kWaves;
+
+  for (int64_t tile = int64_t(bid) * kWaves + (threadIdx.x >> 6); tile < ntiles;
+       tile += wstep) {
+    const int64_t grp = tile / tpg;
+    const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
+    const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
+    QkvSpan sp{};
+    if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, A0);
+    bool ok[kHalves];
+    int64_t src[kHalves];  // input row of this lane's token (clamped into [0, S))
+#pragma unroll
+    for (int tt = 0; tt < kHalves; ++tt) {
+      const int64_t si = d0 + 32 * tt + li;
+      ok[tt] = si >= 0 && si < S;
+      src[tt] = grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1);
+    }
+    uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
+    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    float inv[kHalves];      // token 32 tt + (l & 31): the C-column of this lane
+    if constexpr (FROM_Y) {
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        if (lane < 32 && ok[tt]) {
+          const int64_t t = A0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) vnorm[r] = nin[src[tt]];
+        }
+    } else {
+      float nrm[kHalves];
+      if constexpr (F32) {
+        const float* row[kHalves];
+        const auto* x = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+        load_x_f32<NKS>(xf, xl, nrm, row, lane);
+      } else {
+        const uint16_t* row[kHalves];
+        const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+        load_x<NKS>(xf, row, lane);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt) {
+          float ss = 0.f;
+#pragma unroll
+          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
+          ss += __shfl_xor(ss, 32, 64);
+          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
+        }
+      }
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt) {
+        if (lane < 32 && ok[tt]) {
+          const int64_t t = A0 + 32 * tt + li;
+          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+          if (r >= 0) vnorm[r] = nrm[tt];
+        }
+        inv[tt] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+      }
+    }
+
+    uint32_t stg[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i) stg[i] = 0u;
+
+    static_for<NBK>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
+      constexpr int mb = decltype(mc)::value;
+      __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
+      // y of coordinate 32 mb + 8 (v >> 2) + 4 (l >> 5) + (v & 3), token 32 tt + (l & 31)
+      float yv[kHalves][16];
+      if constexpr (FROM_Y) {
+        const auto* y = static_cast<const float*>(xin);
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            yv[tt][v] = y[src[tt] * D + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
+      } else {
+        qkv_f32x16 acc[kHalves] = {};
+#pragma unroll
+        for (int s = 0; s < NKS; ++s)
+#pragma unroll
+          for (int sp2 = 0; sp2 < 2; ++sp2) {
+            const uint4 af = frag[((mb * NKS + s) * 2 + sp2) * 64 + lane];
+#pragma unroll
+            for (int tt = 0; tt < kHalves; ++tt) {
+              acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
+              if (F32 && sp2 == 0) acc[tt] = mma<F16>(af, xl[tt][F32 ? s : 0], acc[tt]);
+            }
+          }
+#pragma unroll
+        for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * inv[tt];
+      }
+      static_for<kHalves>([&](auto tc) {  // V tile tt of the wave tile
+        constexpr int tt = decltype(tc)::value;
+        static_for<16>([&](auto vc) {
+          constexpr int v = decltype(vc)::value;
+          uint64_t m[VB];
+          search_sym<VB, false>(yv[tt][v], bv, 0u, m);
+          // coordinate ca (lanes 0..31) and ca + 4 (lanes 32..63), tokens 32 tt + 0..31
+          constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
+          static_for<VB>([&](auto kc) {
+            constexpr int k = decltype(kc)::value;
+            constexpr int D0 = (tt * VB + k) * D + ca, D1 = D0 + 4;
+            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(m[k]));
+            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(m[k] >> 32));
+          });
+        });
+      });
+    });
+
+    // store: staging dword i covers tile i / (NPW VB), plane (i / NPW) % VB,
+    // coordinates 64 (i % NPW) + lane
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      const int tau = i / (NPW * VB), k = (i / NPW) % VB, j = 64 * (i % NPW) + lane;
+      const int64_t tok0 = A0 + 32 * tau;
+      const int64_t lo = max<int64_t>(t0 - tok0, 0), hi = min<int64_t>(t0 + S - tok0, 32);
+      if (hi <= lo) continue;
+      const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
+                                          : (((1u << (hi - lo)) - 1u) << lo);
+      const int64_t vrow = PAGED ? sp.row(tok0) : 0;
+      if (vrow < 0) continue;  // a page outside the pool: nothing written
+      const int64_t vt = PAGED ? (vrow >> 5) : grp * (t_stride >> 5) + (tok0 >> 5);
+      uint32_t* p = vst + (vt * VB + k) * D + j;
+      uint32_t val = stg[i];
+      if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
+      *p = val;
+    }
+  }
+}
+
+template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
+__global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
+    float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
+  __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];  // Pi operand fragments
+  append_v_run<VB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, bnd, vst, vnorm, t_stride,
+                                         t0, pg, frag, blockIdx.x, gridDim.x);
+}
+
+// append_v_mfma over the contiguous stores of blockIdx.y's layer
+template <int VB, int XT, int D>
+__global__ __launch_bounds__(kThreads, 4) void append_v_layers(AppendLayers al, int64_t S,
+                                                               int64_t tpg, int64_t ntiles,
+                                                               Half bnd, int64_t t_stride,
+                                                               int64_t t0) {
+  __shared__ uint4 frag[frag_n<D>()];
+  const int l = blockIdx.y;
+  append_v_run<VB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], bnd,
+                                        static_cast<uint32_t*>(al.st[l]), al.nrm[l], t_stride,
+                                        t0, QkvPages{}, frag, blockIdx.x, gridDim.x);
+}
+
+}  // namespace

@@ -102,7 +102,8 @@ class QuashKVEngine:
         self._blocks: list[tuple[int, int]] = []   # (start, seq_len) per append
         self._total_tokens = 0
         self._workspace: Optional[torch.Tensor] = None
-        self._host_tables = None   # codebook tables passed by value to qkv_store_append
+        self._host_tables = None   # codebook tables passed by value to the store append
+        self._app_ptrs = None      # (tensors, pointer arrays) of the one-layer store append
         self._attn_tables = None   # (key MSE, value) centroids for the decode entry points
         # mixed keys: (perm, pi_perm, n_out, host tables, S in slot order or None)
         self._kmix_tables = None
@@ -186,20 +187,21 @@ class QuashKVEngine:
         kc, kb, vb = self._host_tables
         st = self._store
         k, v = keys.contiguous(), values.contiguous()
-        dt = N.dtype_code(k.dtype)
-        stream = N.stream(k.device)
-        L = N.lib()
-        status = L.qkv_store_append(dt, k.data_ptr(), None, B * H, S, d, kq.mse_bits, vq.bits,
-                                    mq.Pi.data_ptr(), kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr,
-                                    st.kst.data_ptr(), st.knorm.data_ptr(), st.vst.data_ptr(),
-                                    st.vnorm.data_ptr(), st.capacity, t0, stream)
+        # one layer through qkv_store_append_layers: the key and the value
+        # kernel in one launch for small appends (each quantizer has its own Pi)
+        ts = (mq.Pi, kq.S, vq.Pi, st.kst, st.knorm, st.vst, st.vnorm)
+        a = self._app_ptrs
+        if a is None or any(x is not y for x, y in zip(ts, a[0])):
+            a = self._app_ptrs = (ts, N.ptr_array([0]), N.ptr_array([0]),
+                                  *(N.ptr_array([t.data_ptr()]) for t in ts))
+        _, ka, va, kpi, sg, vpi, kst, kn, vst, vn = a
+        ka[0], va[0] = k.data_ptr(), v.data_ptr()
+        status = N.lib().qkv_store_append_layers(
+            1, N.dtype_code(k.dtype), ka, va, B * H, S, d, kq.mse_bits, vq.bits, kpi, sg, vpi,
+            kc.ptr, kb.ptr, vb.ptr, kst, kn, vst, vn, st.capacity, t0, N.stream(k.device))
         if status == N.QKV_E_UNSUPPORTED:
             return False
         N.check(status)
-        N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, d, kq.mse_bits, vq.bits,
-                                   vq.Pi.data_ptr(), None, None, None, vb.ptr,
-                                   None, None, st.vst.data_ptr(), st.vnorm.data_ptr(),
-                                   st.capacity, t0, stream))
         return True
 
     def _kmix_setup(self):

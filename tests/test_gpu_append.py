@@ -308,3 +308,68 @@ def test_store_append_cfg3_size_vs_oracle():
     rates = [x / total for x in bad]
     print("cfg3 code mismatch rates (mse, qjl, value):", rates)
     assert max(rates) <= 1e-4, rates
+
+
+def _kv_stores_equal(a, b, T):
+    assert torch.equal(a.kst[:, :, :T], b.kst[:, :, :T])
+    assert torch.equal(a.knorm[:, :, :T], b.knorm[:, :, :T])
+    assert torch.equal(a.vnorm[:, :, :T], b.vnorm[:, :, :T])
+    nt = (T + 31) // 32
+    va, vb = a.vst[:, :, :nt].clone(), b.vst[:, :, :nt].clone()
+    if T % 32:   # bits past T in the last tile are not part of the cache
+        va[:, :, -1] &= (1 << (T % 32)) - 1
+        vb[:, :, -1] &= (1 << (T % 32)) - 1
+    assert torch.equal(va, vb)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("mbits", [1, 2, 3])
+def test_one_launch_append_equals_two_launches(d, dtype, mbits):
+    """Small appends with value bits = key MSE bits + 1 run the key and the
+    value kernel as one launch (qkv_store_append_layers at one layer, and
+    qkv_store_append given keys and values under one Pi); the stores must be
+    bit-identical to a key-only call followed by a value-only call (two
+    launches), over ragged sizes and unaligned starts."""
+    vbits = mbits + 1
+    gen = torch.Generator().manual_seed(100 * mbits + d)
+    B, H, cap = 2, 3, 512
+    kq = Q.InnerProductQuantizer(d, mbits + 1, seed=7, device=DEV)
+    vq = Q.MSEQuantizer(d, vbits, seed=8, device=DEV)
+    mq = kq.mse_quantizer
+    kc = N.HostFloats(mq.codebook.centroids_host)
+    kb = N.HostFloats(mq.codebook.boundaries_host)
+    vb = N.HostFloats(vq.codebook.boundaries_host)
+    L = N.lib()
+    dt = N.dtype_code(dtype)
+    st = {name: Q.store.KVStore(B, H, d, mbits, vbits, cap, torch.device(DEV))
+          for name in ("one", "two", "one_pi", "two_pi")}
+    stream = N.stream(torch.device(DEV))
+
+    def arr(t):
+        return N.ptr_array([t.data_ptr()])
+
+    t0 = 0
+    for S in (1, 5, 37, 64, 1, 100, 3):
+        k = _rows(gen, (B, H, S, d), dtype).to(DEV)
+        v = _rows(gen, (B, H, S, d), dtype, outliers=False).to(DEV)
+        s = st["one"]
+        N.check(L.qkv_store_append_layers(
+            1, dt, arr(k), arr(v), B * H, S, d, mbits, vbits, arr(mq.Pi), arr(kq.S), arr(vq.Pi),
+            kc.ptr, kb.ptr, vb.ptr, arr(s.kst), arr(s.knorm), arr(s.vst), arr(s.vnorm), cap, t0,
+            stream))
+        for name, kpi, vpi, both in (("two", mq.Pi, vq.Pi, False), ("one_pi", mq.Pi, mq.Pi, True),
+                                     ("two_pi", mq.Pi, mq.Pi, False)):
+            s = st[name]
+            calls = [(k, v, kpi)] if both else [(k, None, kpi), (None, v, vpi)]
+            for kk, vv, pi in calls:
+                N.check(L.qkv_store_append(
+                    dt, kk.data_ptr() if kk is not None else None,
+                    vv.data_ptr() if vv is not None else None, B * H, S, d, mbits, vbits,
+                    pi.data_ptr(), kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, s.kst.data_ptr(),
+                    s.knorm.data_ptr(), s.vst.data_ptr(), s.vnorm.data_ptr(), cap, t0, stream))
+        t0 += S
+    torch.cuda.synchronize()
+    _kv_stores_equal(st["one"], st["two"], t0)
+    _kv_stores_equal(st["one_pi"], st["two_pi"], t0)
+    assert st["one"].knorm[:, :, :t0].abs().min() > 0   # every token was written
