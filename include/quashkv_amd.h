@@ -496,6 +496,23 @@ int qkv_store_append_kipmixed_rotated(const float* y_slots, const float* norm_in
                                       uint8_t* kstore, float* knorm, int64_t t_stride,
                                       int64_t t0, void* stream);
 
+/* QuashKVEngine.append (quashkv/engine.py:145-172: compress_keys, then
+ * compress_values) with a mixed-precision key quantizer: the key half of
+ * qkv_store_append_kmixed (ip = 0; signs_perm, out_cent_host and
+ * reg_cent_host may be NULL) or qkv_store_append_kipmixed (ip = 1) and the
+ * value half of qkv_store_append (vbits, vpi, vbound_host, vstore, vnorm) in
+ * one call, results identical to those two calls.  Small appends (a chunk of
+ * a few thousand tokens per kv head) run both halves in one launch; every
+ * argument is checked before anything is launched. */
+int qkv_store_append_kmixed_kv(int32_t in_dtype, const void* keys, const void* values,
+                               int64_t groups, int64_t S, int32_t d, const float* pi_perm,
+                               const float* signs_perm, int32_t n_out, int32_t ip,
+                               const float* out_cent_host, const float* out_bound_host,
+                               const float* reg_cent_host, const float* reg_bound_host,
+                               uint8_t* kstore, float* knorm, int32_t vbits, const float* vpi,
+                               const float* vbound_host, uint32_t* vstore, float* vnorm,
+                               int64_t t_stride, int64_t t0, void* stream);
+
 /* Decode attention over kmixed K rows and V tiles: scores
  * n_k <q Pi^T, c_channel[code]> (the reference's decompress-then-attend,
  * quashkv/mixed_precision.py:160-187 with quashkv/engine.py:245-297), values

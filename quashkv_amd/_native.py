@@ -74,6 +74,9 @@ _SIGS = {
     "qkv_kipmixed_unpack": (_i32, [_p, _i64, _p, _i32, _i64, _i64, _p, _p, _p]),
     "qkv_store_append_kipmixed": (_i32, [_i32, _p, _i64, _i64, _i32, _p, _p, _i32, _p, _p, _p,
                                          _p, _p, _p, _i64, _i64, _p]),
+    "qkv_store_append_kmixed_kv": (_i32, [_i32, _p, _p, _i64, _i64, _i32, _p, _p, _i32, _i32, _p,
+                                          _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64, _i64,
+                                          _p]),
     "qkv_store_append_kipmixed_rotated": (_i32, [_p, _p, _i64, _i64, _i32, _p, _i32, _p, _p, _p,
                                                  _p, _p, _p, _i64, _i64, _p]),
     "qkv_decode_attention_kipmixed": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,

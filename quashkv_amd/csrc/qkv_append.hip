@@ -372,7 +372,7 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
                        const float* out_cent_host, const float* reg_cent_host,
                        const float* out_bound_host, const float* reg_bound_host,
                        uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
-                       void* stream) {
+                       void* stream, Half* po_out = nullptr, Half* pr_out = nullptr) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
   QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
@@ -406,6 +406,11 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
                   ipm ? "fine lists c_i < t_i < c_{i+1}" : "boundaries");
     return QKV_E_UNSUPPORTED;
   }
+  if (po_out) {  // checks and lists only (the caller launches)
+    *po_out = po;
+    *pr_out = pr;
+    return QKV_OK;
+  }
   if (groups == 0 || S == 0) return QKV_OK;
   auto s = static_cast<hipStream_t>(stream);
   const int64_t tpg = (S + kTok - 1) / kTok, ntiles = groups * tpg;
@@ -437,6 +442,56 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
 #undef QKV_KM
   QKV_LAUNCHED();
   return QKV_OK;
+}
+
+// qkv_store_append_kmixed_kv: the kmixed / kipmixed key append and the value
+// append of the same tokens; one launch when both halves' workgroups are
+// resident at once, else the two kernels.  Every argument is checked before
+// anything is launched.
+int kmixed_kv_impl(int32_t in_dtype, const void* keys, const void* values, int64_t groups,
+                   int64_t S, int32_t d, const float* pi_perm, const float* signs_perm,
+                   int32_t n_out, bool ipm, const float* out_cent_host,
+                   const float* out_bound_host, const float* reg_cent_host,
+                   const float* reg_bound_host, uint8_t* kstore, float* knorm, int32_t vbits,
+                   const float* vpi, const float* vbound_host, uint32_t* vstore, float* vnorm,
+                   int64_t t_stride, int64_t t0, void* stream) {
+  Half po{}, pr{};
+  if (const int st = kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm,
+                                        n_out, ipm, signs_perm, out_cent_host, reg_cent_host,
+                                        out_bound_host, reg_bound_host, kstore, knorm, t_stride,
+                                        t0, stream, &po, &pr))
+    return st;
+  QKV_REQUIRE(qkv_bits_ok(vbits), "value bits %d not in 1..4", vbits);
+  QKV_REQUIRE(values && vpi && vbound_host && vstore && vnorm, "null pointer");
+  QKV_REQUIRE(qkv_aligned(values, 16) && qkv_aligned(vpi, 16) && qkv_aligned(vstore, 4),
+              "values / pi 16-B, store 4-B aligned");
+  QKV_REQUIRE(t_stride % 32 == 0, "store capacity %lld must be a multiple of 32",
+              (long long)t_stride);
+  Half fine{}, bnd{};
+  if (const int st = append_lists(false, true, 2, vbits, nullptr, nullptr, vbound_host, &fine,
+                                  &bnd))
+    return st;
+  if (groups == 0 || S == 0) return QKV_OK;
+  const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
+  const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
+  const int kb = append_blocks(kn), vb = append_blocks(vn);
+  const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;
+  if (kb + vb <= 2 * qkv_num_cus() &&
+      qkv_app::launch_append_kmixv(n_out, ipm, vbits, xt, keys, values, kb, vb, S, ktpg, kn, vtpg,
+                                   vn, pi_perm, signs_perm, po, pr, kstore, knorm, vpi, bnd,
+                                   vstore, vnorm, t_stride, t0,
+                                   static_cast<hipStream_t>(stream))) {
+    QKV_LAUNCHED();
+    return QKV_OK;
+  }
+  if (const int st = kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm,
+                                        n_out, ipm, signs_perm, out_cent_host, reg_cent_host,
+                                        out_bound_host, reg_bound_host, kstore, knorm, t_stride,
+                                        t0, stream))
+    return st;
+  return store_append_impl(in_dtype, nullptr, values, false, nullptr, nullptr, groups, S, d, 2,
+                           vbits, vpi, nullptr, nullptr, nullptr, vbound_host, nullptr, nullptr,
+                           vstore, vnorm, t_stride, t0, QkvPages{}, stream);
 }
 
 }  // namespace
@@ -534,6 +589,18 @@ extern "C" int qkv_store_append_kipmixed(int32_t in_dtype, const void* keys, int
   return kmixed_append_impl(in_dtype, keys, false, nullptr, groups, S, d, pi_perm, n_out, true,
                             signs_perm, out_cent_host, reg_cent_host, out_bound_host,
                             reg_bound_host, kstore, knorm, t_stride, t0, stream);
+}
+
+extern "C" int qkv_store_append_kmixed_kv(
+    int32_t in_dtype, const void* keys, const void* values, int64_t groups, int64_t S, int32_t d,
+    const float* pi_perm, const float* signs_perm, int32_t n_out, int32_t ip,
+    const float* out_cent_host, const float* out_bound_host, const float* reg_cent_host,
+    const float* reg_bound_host, uint8_t* kstore, float* knorm, int32_t vbits, const float* vpi,
+    const float* vbound_host, uint32_t* vstore, float* vnorm, int64_t t_stride, int64_t t0,
+    void* stream) {
+  return kmixed_kv_impl(in_dtype, keys, values, groups, S, d, pi_perm, signs_perm, n_out, ip != 0,
+                        out_cent_host, out_bound_host, reg_cent_host, reg_bound_host, kstore,
+                        knorm, vbits, vpi, vbound_host, vstore, vnorm, t_stride, t0, stream);
 }
 
 extern "C" int qkv_store_append_kipmixed_rotated(const float* y_slots, const float* norm_in,

@@ -97,6 +97,17 @@ bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& a
                       int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, Half fine,
                       Half bnd, int64_t t_stride, int64_t t0, hipStream_t s);
 
+// One launch of append_kmix_run (mixed-precision keys, n_out outlier slots,
+// IP or MSE) and append_v_run (value bits 2..4) over one contiguous store
+// (defined in qkv_append_kv.hip); false, launching nothing, for combinations
+// it does not instantiate.
+bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* keys,
+                         const void* values, int kblocks, int vblocks, int64_t S, int64_t ktpg,
+                         int64_t kntiles, int64_t vtpg, int64_t vntiles, const float* pi_perm,
+                         const float* signs_perm, Half po, Half pr, uint8_t* kst, float* knorm,
+                         const float* vpi, Half bnd, uint32_t* vst, float* vnorm,
+                         int64_t t_stride, int64_t t0, hipStream_t s);
+
 }  // namespace qkv_app
 
 namespace {
@@ -621,17 +632,15 @@ __global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, 
 // codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
 // rows in slot order and `nin` their norms.
 template <int NO, int XT, bool FROM_Y, bool IPM>
-__global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
+__device__ __forceinline__ void append_kmix_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
-    int64_t t0) {
+    int64_t t0, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb) {
   constexpr bool F16 = XT != 0, F32 = XT == 2;        // fp16 MFMA / fp32 rows split for it
   constexpr int NOB = NO / 32;                         // outlier blocks
   constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
   constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
-  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];
-  __shared__ float4 inv_s[kWaves][kTok / 4];
   if constexpr (!FROM_Y) {
     stage_pi<F16>(frag, pi_perm, F16 ? kPScaleF16 : 1.f);
     __syncthreads();
@@ -655,9 +664,9 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     }
   }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
-  const int64_t wstep = int64_t(gridDim.x) * kWaves;
+  const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = int64_t(blockIdx.x) * kWaves + wv; tile < ntiles; tile += wstep) {
+  for (int64_t tile = int64_t(bid) * kWaves + wv; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
@@ -803,6 +812,18 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
       if (D < nv * RD) dst[D] = stg[i];
     }
   }
+}
+
+template <int NO, int XT, bool FROM_Y, bool IPM>
+__global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
+    const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
+    int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
+    Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
+    int64_t t0) {
+  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];  // Pi operand fragments (rows in slot order)
+  __shared__ float4 inv_s[kWaves][kTok / 4];   // 1 / norm of each wave's tokens
+  append_kmix_run<NO, XT, FROM_Y, IPM>(xin, nin, S, tpg, ntiles, pi_perm, signs_perm, po, pr, kst,
+                                       knorm, t_stride, t0, frag, inv_s, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------ quantizer-API compress

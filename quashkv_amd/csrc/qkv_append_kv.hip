@@ -1,10 +1,12 @@
 // One launch for the key and the value half of a store append: the workgroups
-// of append_k_run and of append_v_run (qkv_append_dev.h) in one grid, so that
-// a small append -- one decode token per layer, a short chunk -- runs both
-// halves side by side on different CUs and pays one launch instead of two.
-// Instantiated for value bits = key MSE bits + 1 (key_bits == value_bits in
-// the reference's QuashKVEngine(key_bits, value_bits), quashkv/engine.py:62-90,
-// whose default is 3 / 3); other combinations launch the two kernels.
+// of the key kernel body (append_k_run, or append_kmix_run for mixed-precision
+// keys) and of append_v_run (qkv_append_dev.h) in one grid, so that a small
+// append -- one decode token per layer, a short chunk -- runs both halves side
+// by side on different CUs and pays one launch instead of two.  Instantiated
+// for value bits = key MSE bits + 1 (key_bits == value_bits in the reference's
+// QuashKVEngine(key_bits, value_bits), quashkv/engine.py:77-101, whose default
+// is 3 / 3) and, with mixed-precision keys, value bits 2..4; other
+// combinations launch the two kernels.
 
 #include "qkv_append_dev.h"
 
@@ -31,9 +33,73 @@ __global__ __launch_bounds__(kThreads, 4) void append_kv_layers(
                                           static_cast<int>(gridDim.x) - kblocks);
 }
 
+// Mixed-precision keys and their values: x < kblocks runs append_kmix_run over
+// kblocks workgroups, the rest append_v_run.
+template <int NO, bool IPM, int VB, int XT>
+__global__ __launch_bounds__(kThreads, 2) void append_kmixv(
+    const void* __restrict__ keys, const void* __restrict__ values, int kblocks, int64_t S,
+    int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles,
+    const float* __restrict__ pi_perm, const float* __restrict__ signs_perm, Half po, Half pr,
+    uint8_t* __restrict__ kst, float* __restrict__ knorm, const float* __restrict__ vpi, Half bnd,
+    uint32_t* __restrict__ vst, float* __restrict__ vnorm, int64_t t_stride, int64_t t0) {
+  __shared__ uint4 frag[kFragN];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  const int b = blockIdx.x;
+  if (b < kblocks)
+    append_kmix_run<NO, XT, false, IPM>(keys, nullptr, S, ktpg, kntiles, pi_perm, signs_perm, po,
+                                        pr, kst, knorm, t_stride, t0, frag, inv_s, b, kblocks);
+  else
+    append_v_run<VB, XT, kD, false, false>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vst,
+                                           vnorm, t_stride, t0, QkvPages{}, frag, b - kblocks,
+                                           static_cast<int>(gridDim.x) - kblocks);
+}
+
 }  // namespace
 
 namespace qkv_app {
+
+bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* keys,
+                         const void* values, int kblocks, int vblocks, int64_t S, int64_t ktpg,
+                         int64_t kntiles, int64_t vtpg, int64_t vntiles, const float* pi_perm,
+                         const float* signs_perm, Half po, Half pr, uint8_t* kst, float* knorm,
+                         const float* vpi, Half bnd, uint32_t* vst, float* vnorm,
+                         int64_t t_stride, int64_t t0, hipStream_t s) {
+  if ((n_out != 32 && n_out != 64) || vbits < 2 || vbits > 4 || xt < 0 || xt > 2) return false;
+  const dim3 grid(kblocks + vblocks);
+#define QKV_KMV(NOV, IP, VB, F)                                                                 \
+  hipLaunchKernelGGL((append_kmixv<NOV, IP, VB, F>), grid, dim3(kThreads), 0, s, keys, values,  \
+                     kblocks, S, ktpg, kntiles, vtpg, vntiles, pi_perm, signs_perm, po, pr, kst, \
+                     knorm, vpi, bnd, vst, vnorm, t_stride, t0)
+#define QKV_KMV_F(NOV, IP, VB)        \
+  switch (xt) {                      \
+    case 0: QKV_KMV(NOV, IP, VB, 0); break; \
+    case 1: QKV_KMV(NOV, IP, VB, 1); break; \
+    default: QKV_KMV(NOV, IP, VB, 2); break; \
+  }
+#define QKV_KMV_V(NOV, IP)               \
+  switch (vbits) {                      \
+    case 2: QKV_KMV_F(NOV, IP, 2); break; \
+    case 3: QKV_KMV_F(NOV, IP, 3); break; \
+    default: QKV_KMV_F(NOV, IP, 4); break; \
+  }
+  if (n_out == 32) {
+    if (ipm) {
+      QKV_KMV_V(32, true)
+    } else {
+      QKV_KMV_V(32, false)
+    }
+  } else {
+    if (ipm) {
+      QKV_KMV_V(64, true)
+    } else {
+      QKV_KMV_V(64, false)
+    }
+  }
+#undef QKV_KMV_V
+#undef QKV_KMV_F
+#undef QKV_KMV
+  return true;
+}
 
 bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& ak,
                       const AppendLayers& av, int n_layers, int kblocks, int vblocks, int64_t S,

@@ -239,9 +239,8 @@ class QuashKVEngine:
 
     def _append_kmix(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:
         """Mixed-precision keys: bf16, fp16 or fp32 rows straight into kmixed /
-        kipmixed rows (qkv_store_append_kmixed / _kipmixed); other dtypes
-        through qkv_compress_mixed and the row packers.  Values as in the
-        IP-key engine."""
+        kipmixed rows, with the values, in one qkv_store_append_kmixed_kv
+        call; other dtypes through qkv_compress_mixed and the row packers."""
         B, H, S, d = keys.shape
         st = self._store
         kq, vq = self.key_quantizer, self.value_quantizer
@@ -257,20 +256,14 @@ class QuashKVEngine:
                  and values.dtype == keys.dtype)
         if fused:
             k, v = keys.contiguous(), values.contiguous()
-            dt = N.dtype_code(k.dtype)
-            if self._kmix_ip:
-                N.check(L.qkv_store_append_kipmixed(
-                    dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(), sp.data_ptr(), n_out,
-                    oc.ptr, ob.ptr, rc.ptr, rb.ptr, st.kst.data_ptr(), st.knorm.data_ptr(),
-                    st.capacity, t0, stream))
-            else:
-                N.check(L.qkv_store_append_kmixed(
-                    dt, k.data_ptr(), B * H, S, d, pi_perm.data_ptr(), n_out, ob.ptr, rb.ptr,
-                    st.kst.data_ptr(), st.knorm.data_ptr(), st.capacity, t0, stream))
-            N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, d, 2, vq.bits,
-                                       vq.Pi.data_ptr(), None, None, None, vb.ptr, None, None,
-                                       st.vst.data_ptr(), st.vnorm.data_ptr(), st.capacity, t0,
-                                       stream))
+            # keys (kmixed / kipmixed rows) and values in one call, one launch
+            # for chunk-sized appends
+            N.check(L.qkv_store_append_kmixed_kv(
+                N.dtype_code(k.dtype), k.data_ptr(), v.data_ptr(), B * H, S, d,
+                pi_perm.data_ptr(), sp.data_ptr() if self._kmix_ip else None, n_out,
+                int(self._kmix_ip), oc.ptr, ob.ptr, rc.ptr, rb.ptr, st.kst.data_ptr(),
+                st.knorm.data_ptr(), vq.bits, vq.Pi.data_ptr(), vb.ptr, st.vst.data_ptr(),
+                st.vnorm.data_ptr(), st.capacity, t0, stream))
             return
         if self._kmix_ip:
             kc, kb, kn = kq.compress(keys.reshape(n, d))

@@ -259,3 +259,70 @@ def test_kmixed_cfg4_full_size():
                     float((mine.flatten() @ ref2.flatten()) / (mine.norm() * ref2.norm()))))
     assert max(errs) <= 1e-3, errs
     assert all(e <= 1e-2 and c >= 0.9999 for e, c in e2e), e2e
+
+
+def _kv_stores_equal(a, b, T):
+    assert torch.equal(a.kst[:, :, :T], b.kst[:, :, :T])
+    assert torch.equal(a.knorm[:, :, :T], b.knorm[:, :, :T])
+    assert torch.equal(a.vnorm[:, :, :T], b.vnorm[:, :, :T])
+    nt = (T + 31) // 32
+    va, vb = a.vst[:, :, :nt].clone(), b.vst[:, :, :nt].clone()
+    if T % 32:   # bits past T in the last tile are not part of the cache
+        va[:, :, -1] &= (1 << (T % 32)) - 1
+        vb[:, :, -1] &= (1 << (T % 32)) - 1
+    assert torch.equal(va, vb)
+
+
+@pytest.mark.parametrize("ip", [False, True])
+@pytest.mark.parametrize("n_out", [32, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("vbits", [4, 2, 1])
+def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits):
+    """qkv_store_append_kmixed_kv (keys and values in one launch for chunk-sized
+    appends; value bits 1 take the two-kernel path inside) writes the same
+    store, bit for bit, as qkv_store_append_kmixed / _kipmixed followed by the
+    value-only qkv_store_append, over ragged sizes and unaligned starts."""
+    cls = Q.MixedPrecisionIPQuantizer if ip else Q.MixedPrecisionMSEQuantizer
+    kq = cls(128, outlier_bits=3, regular_bits=2, n_outliers=n_out, seed=42, device=DEV)
+    out_idx = _outliers(n_out, seed=3)
+    kq.set_outlier_channels(out_idx.to(DEV))
+    eng = Q.QuashKVEngine(head_dim=128, value_bits=vbits, seed=42, device=DEV, key_quantizer=kq)
+    perm, pi_perm, no, (oc, rc, ob, rb, vb) = eng._kmix_setup()
+    pi_perm = pi_perm.to(DEV)
+    sp = eng._kmix_signs(torch.device(DEV))
+    vq = eng.value_quantizer
+    B, H, cap = 2, 3, 512
+    dev = torch.device(DEV)
+    one = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
+    two = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
+    L = N.lib()
+    dt = N.dtype_code(dtype)
+    stream = N.stream(dev)
+    gen = torch.Generator().manual_seed(n_out + vbits + 10 * int(ip))
+    t0 = 0
+    for S in (1, 37, 64, 5, 100):
+        k = torch.randn(B, H, S, 128, generator=gen)
+        k[..., out_idx] *= 8.0
+        k = k.to(dtype).to(DEV)
+        v = torch.randn(B, H, S, 128, generator=gen).to(dtype).to(DEV)
+        N.check(L.qkv_store_append_kmixed_kv(
+            dt, k.data_ptr(), v.data_ptr(), B * H, S, 128, pi_perm.data_ptr(),
+            sp.data_ptr() if ip else None, no, int(ip), oc.ptr, ob.ptr, rc.ptr, rb.ptr,
+            one.kst.data_ptr(), one.knorm.data_ptr(), vbits, vq.Pi.data_ptr(), vb.ptr,
+            one.vst.data_ptr(), one.vnorm.data_ptr(), cap, t0, stream))
+        if ip:
+            N.check(L.qkv_store_append_kipmixed(
+                dt, k.data_ptr(), B * H, S, 128, pi_perm.data_ptr(), sp.data_ptr(), no, oc.ptr,
+                ob.ptr, rc.ptr, rb.ptr, two.kst.data_ptr(), two.knorm.data_ptr(), cap, t0,
+                stream))
+        else:
+            N.check(L.qkv_store_append_kmixed(
+                dt, k.data_ptr(), B * H, S, 128, pi_perm.data_ptr(), no, ob.ptr, rb.ptr,
+                two.kst.data_ptr(), two.knorm.data_ptr(), cap, t0, stream))
+        N.check(L.qkv_store_append(dt, None, v.data_ptr(), B * H, S, 128, 2, vbits,
+                                   vq.Pi.data_ptr(), None, None, None, vb.ptr, None, None,
+                                   two.vst.data_ptr(), two.vnorm.data_ptr(), cap, t0, stream))
+        t0 += S
+    torch.cuda.synchronize()
+    _kv_stores_equal(one, two, t0)
+    assert one.knorm[:, :, :t0].abs().min() > 0

@@ -369,3 +369,29 @@ def test_hf_cache_host_logic():
     cfg = QuashKVCacheConfig(key_bits=4, value_bits=4, seed=7)
     c2 = QuashKVCache(num_layers=2, head_dim=128, config=cfg, device="cpu")
     assert c2.engines[0].key_bits == 4 and c2.engines[1].seed == 8
+
+
+def test_store_append_kmixed_kv_host_validation():
+    """Argument checks of qkv_store_append_kmixed_kv: every one before any
+    launch (fake device pointers; a call that passes them launches nothing
+    only when there is nothing to append)."""
+    lib = N.lib()
+    ob = N.HostFloats(LloydMaxCodebook(128, 3).boundaries_host)
+    rb = N.HostFloats(LloydMaxCodebook(128, 2).boundaries_host)
+    vb = N.HostFloats(LloydMaxCodebook(128, 4).boundaries_host)
+    P = 256
+
+    def call(groups=2, S=1, d=128, n_out=32, vbits=4, values=P, vstore=P, cap=128, dt=2):
+        return lib.qkv_store_append_kmixed_kv(dt, P, values, groups, S, d, P, None, n_out, 0,
+                                              None, ob.ptr, None, rb.ptr, P, P, vbits, P, vb.ptr,
+                                              vstore, P, cap, 0, None)
+
+    assert call(groups=0) == N.QKV_OK            # nothing to append: checks only
+    assert call(d=96) == N.QKV_E_UNSUPPORTED
+    assert call(n_out=16) == N.QKV_E_UNSUPPORTED
+    assert call(vbits=5) == N.QKV_E_INVALID
+    assert call(values=None) == N.QKV_E_INVALID
+    assert call(vstore=None) == N.QKV_E_INVALID
+    assert call(cap=100, S=1) == N.QKV_E_INVALID  # capacity not a multiple of 32
+    assert call(cap=64, S=65) == N.QKV_E_INVALID
+    assert call(dt=7) == N.QKV_E_INVALID
