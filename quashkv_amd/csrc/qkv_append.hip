@@ -117,7 +117,14 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
     // both halves in one launch when their workgroups are resident at once
     const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
     const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
-    const int kb = append_blocks(kn), vb = append_blocks(vn);
+    // a wave per 32-coordinate block of a tile while that fits one workgroup per
+    // CU, else a wave per tile while two per CU hold every workgroup
+    int ns = d / 32, kb = append_blocks(kn * ns), vb = append_blocks(vn * ns);
+    if (kb + vb > qkv_num_cus()) {
+      ns = 1;
+      kb = append_blocks(kn);
+      vb = append_blocks(vn);
+    }
     if (kb + vb <= 2 * qkv_num_cus()) {
       AppendLayers ak{}, av{};
       ak.x[0] = keys;
@@ -130,7 +137,7 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
       av.st[0] = vstore;
       av.nrm[0] = vnorm;
       if (qkv_app::launch_append_kv(mbits, vbits, xt, d, ak, av, 1, kb, vb, S, ktpg, kn, vtpg, vn,
-                                    fine, bnd, t_stride, t0, s)) {
+                                    fine, bnd, t_stride, t0, ns, s)) {
         QKV_LAUNCHED();
         return QKV_OK;
       }
@@ -281,10 +288,17 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
     // both halves in one launch when all their workgroups are resident at once
     const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
     const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
-    const int kb = blocks(kn), vb = blocks(vn);
+    // a wave per 32-coordinate block of a tile while that fits one workgroup per
+    // CU, else a wave per tile while two per CU hold every workgroup
+    int ns = d / 32, kb = blocks(kn * ns), vb = blocks(vn * ns);
+    if (int64_t(kb + vb) * n_layers > qkv_num_cus()) {
+      ns = 1;
+      kb = blocks(kn);
+      vb = blocks(vn);
+    }
     if (int64_t(kb + vb) * n_layers <= 2 * qkv_num_cus() &&
         qkv_app::launch_append_kv(mbits, vbits, xt, d, ak, av, n_layers, kb, vb, S, ktpg, kn,
-                                  vtpg, vn, fine, bnd, t_stride, t0, s)) {
+                                  vtpg, vn, fine, bnd, t_stride, t0, ns, s)) {
       QKV_LAUNCHED();
       return QKV_OK;
     }
@@ -474,12 +488,19 @@ int kmixed_kv_impl(int32_t in_dtype, const void* keys, const void* values, int64
   if (groups == 0 || S == 0) return QKV_OK;
   const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
   const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
-  const int kb = append_blocks(kn), vb = append_blocks(vn);
+  // a wave per 32-slot block of a tile while that fits one workgroup per CU,
+  // else a wave per tile while two per CU hold every workgroup
+  int ns = 4, kb = append_blocks(kn * ns), vb = append_blocks(vn * ns);
+  if (kb + vb > qkv_num_cus()) {
+    ns = 1;
+    kb = append_blocks(kn);
+    vb = append_blocks(vn);
+  }
   const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;
   if (kb + vb <= 2 * qkv_num_cus() &&
       qkv_app::launch_append_kmixv(n_out, ipm, vbits, xt, keys, values, kb, vb, S, ktpg, kn, vtpg,
                                    vn, pi_perm, signs_perm, po, pr, kstore, knorm, vpi, bnd,
-                                   vstore, vnorm, t_stride, t0,
+                                   vstore, vnorm, t_stride, t0, ns,
                                    static_cast<hipStream_t>(stream))) {
     QKV_LAUNCHED();
     return QKV_OK;

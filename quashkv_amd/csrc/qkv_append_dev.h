@@ -90,12 +90,14 @@ struct AppendLayers {
 
 // One launch of append_k_run and append_v_run over n_layers contiguous stores
 // (grid.y = layer, grid.x = key workgroups then value workgroups), for
-// vbits == mbits + 1 (defined in qkv_append_kv.hip).  Returns false, launching
-// nothing, for the combinations it does not instantiate.
+// vbits == mbits + 1 (defined in qkv_append_kv.hip); every wave takes one tile
+// (nsplit = 1) or one 32-coordinate block of one tile (nsplit = d / 32), and
+// the block counts must cover that.  Returns false, launching nothing, for
+// the combinations it does not instantiate or grids that do not cover.
 bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& ak,
                       const AppendLayers& av, int n_layers, int kblocks, int vblocks, int64_t S,
                       int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, Half fine,
-                      Half bnd, int64_t t_stride, int64_t t0, hipStream_t s);
+                      Half bnd, int64_t t_stride, int64_t t0, int nsplit, hipStream_t s);
 
 // One launch of append_kmix_run (mixed-precision keys, n_out outlier slots,
 // IP or MSE) and append_v_run (value bits 2..4) over one contiguous store
@@ -106,7 +108,7 @@ bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* key
                          int64_t kntiles, int64_t vtpg, int64_t vntiles, const float* pi_perm,
                          const float* signs_perm, Half po, Half pr, uint8_t* kst, float* knorm,
                          const float* vpi, Half bnd, uint32_t* vst, float* vnorm,
-                         int64_t t_stride, int64_t t0, hipStream_t s);
+                         int64_t t_stride, int64_t t0, int nsplit, hipStream_t s);
 
 }  // namespace qkv_app
 
@@ -401,12 +403,20 @@ __device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl
 // rows y (rows as above) and `nin` their norms; the normalisation and the
 // rotation are skipped, everything after them is the same code.
 // XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
-template <int MB, int XT, int D, bool PAGED, bool FROM_Y>
+//
+// ONE: small appends, where one wave's chain is the kernel's time.  Each wave
+// takes at most one tile (nb * kWaves >= ntiles * nsplit, the host's
+// guarantee), or with nsplit = D / 32 one 32-coordinate block of one tile, so
+// that the chain is a quarter (d = 128) or a half (d = 64) of a tile's MFMAs
+// and searches; a bf16 / fp16 wave's rows are loaded before Pi is staged, so
+// that the two global-load latencies overlap.
+template <int MB, int XT, int D, bool PAGED, bool FROM_Y, bool ONE = false>
 __device__ __forceinline__ void append_k_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
-    QkvPages pg, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb) {
+    QkvPages pg, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb,
+    int nsplit = 1) {
   constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NP = (1 << MB) - 1;   // positive half of the fine list c_0, t_0, ..., c_{2^MB-1}
@@ -415,12 +425,33 @@ __device__ __forceinline__ void append_k_run(
   constexpr int RD = NBK * L;         // dwords per row
   constexpr int NSK = RD * kTok / 64; // staging dwords per lane
   static_assert(RD * kTok % 64 == 0, "whole staging dwords");
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  // ONE with nsplit = NBK: wave (tile, coordinate block) = (g / NBK, g % NBK)
+  // for the global wave index g, each wave computing and storing that block's
+  // words only; nsplit = 1: wave g takes tile g whole
+  const int64_t gw = int64_t(bid) * kWaves + wv;
+  const bool split = ONE && nsplit > 1;
+  const int myblk = split ? static_cast<int>(gw % NBK) : 0;
+  constexpr bool PRE = ONE && !FROM_Y && !F32;  // rows loaded before the Pi staging
+  uint4 xpre[kHalves][PRE ? NKS : 1];
+  if constexpr (PRE) {
+    const int64_t tile = split ? gw / NBK : gw;
+    if (tile < ntiles) {
+      const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
+      const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+      const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+      load_x<NKS>(xpre, row, lane);
+    }
+  }
   if constexpr (!FROM_Y) {
     stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
     __syncthreads();
   }
 
-  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
   uint32_t fv[NP];
 #pragma unroll
   for (int i = 0; i < NP; ++i) fv[i] = in_vgpr(fine.t[i]);
@@ -435,7 +466,7 @@ __device__ __forceinline__ void append_k_run(
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = int64_t(bid) * kWaves + wv; tile < ntiles; tile += wstep) {
+  for (int64_t tile = split ? gw / NBK : gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
@@ -461,12 +492,19 @@ __device__ __forceinline__ void append_k_run(
           row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
         load_x_f32<NKS>(xf, xl, nrm, row, lane);
       } else {
-        const uint16_t* row[kHalves];
-        const auto* x = static_cast<const uint16_t*>(xin);
+        if constexpr (PRE) {
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
-        load_x<NKS>(xf, row, lane);
+          for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+            for (int s = 0; s < NKS; ++s) xf[tt][s] = xpre[tt][s];
+        } else {
+          const uint16_t* row[kHalves];
+          const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt)
+            row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+          load_x<NKS>(xf, row, lane);
+        }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
           float ss = 0.f;
@@ -488,7 +526,7 @@ __device__ __forceinline__ void append_k_run(
           if (32 * tt + li < nv) {
             const int64_t t = t0 + s0 + 32 * tt + li;
             const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-            if (r >= 0) knorm[r] = nrm[tt];
+            if (r >= 0 && myblk == 0) knorm[r] = nrm[tt];
           }
           invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
         }
@@ -503,6 +541,7 @@ __device__ __forceinline__ void append_k_run(
 
     static_for<NBK>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
       constexpr int n = decltype(nc)::value;
+      if (split && n != myblk) return;
       // one coordinate block at a time: keeps the scheduler from overlapping
       // blocks (and their accumulators and fragments) beyond the register file
       __builtin_amdgcn_sched_barrier(0);
@@ -580,10 +619,11 @@ __device__ __forceinline__ void append_k_run(
       uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
 #pragma unroll
       for (int i = 0; i < NSK; ++i) {
-        const int w = i * 64 + lane;
-        if (w < nv * RD) dst[w] = stg[i];
+        const int w = i * 64 + lane;  // dword w % RD of a row is word (w % RD) % NBK of a plane
+        if (w < nv * RD && (!split || w % NBK == myblk)) dst[w] = stg[i];
       }
     }
+    if constexpr (ONE) break;
   }
 }
 
@@ -631,22 +671,43 @@ __global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, 
 // The outlier slots fill whole 32-slot blocks (NO = 32 or 64), so each block's
 // codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
 // rows in slot order and `nin` their norms.
-template <int NO, int XT, bool FROM_Y, bool IPM>
+template <int NO, int XT, bool FROM_Y, bool IPM, bool ONE = false>
 __device__ __forceinline__ void append_kmix_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
-    int64_t t0, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb) {
+    int64_t t0, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb,
+    int nsplit = 1) {
   constexpr bool F16 = XT != 0, F32 = XT == 2;        // fp16 MFMA / fp32 rows split for it
   constexpr int NOB = NO / 32;                         // outlier blocks
   constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
   constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
+  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
+  // ONE, nsplit: the waves' tiles and slot blocks as in append_k_run
+  const int64_t gw = int64_t(bid) * kWaves + wv;
+  const bool split = ONE && nsplit > 1;
+  const int myblk = split ? static_cast<int>(gw % 4) : 0;
+  constexpr bool PRE = ONE && !FROM_Y && !F32;
+  uint4 xpre[kHalves][PRE ? 8 : 1];
+  if constexpr (PRE) {
+    const int64_t tile = split ? gw / 4 : gw;
+    if (tile < ntiles) {
+      const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
+      const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+      const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+      load_x(xpre, row, lane);
+    }
+  }
   if constexpr (!FROM_Y) {
     stage_pi<F16>(frag, pi_perm, F16 ? kPScaleF16 : 1.f);
     __syncthreads();
   }
 
-  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
   // positive halves: outlier and regular boundaries (MSE keys) or fine lists
   // (IP keys), three and one entries either way
   uint32_t pov[3], prv[1];
@@ -666,7 +727,7 @@ __device__ __forceinline__ void append_kmix_run(
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = int64_t(bid) * kWaves + wv; tile < ntiles; tile += wstep) {
+  for (int64_t tile = split ? gw / 4 : gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
@@ -687,12 +748,19 @@ __device__ __forceinline__ void append_kmix_run(
           row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
         load_x_f32<8>(xf, xl, nrm, row, lane);
       } else {
-        const uint16_t* row[kHalves];
-        const auto* x = static_cast<const uint16_t*>(xin);
+        if constexpr (PRE) {
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-        load_x(xf, row, lane);
+          for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) xf[tt][s] = xpre[tt][s];
+        } else {
+          const uint16_t* row[kHalves];
+          const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt)
+            row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
+          load_x(xf, row, lane);
+        }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
           float ss = 0.f;
@@ -706,7 +774,7 @@ __device__ __forceinline__ void append_kmix_run(
 #pragma unroll
       for (int tt = 0; tt < kHalves; ++tt) {
         if (lane < 32) {
-          if (32 * tt + li < nv) nrow[32 * tt + li] = nrm[tt];
+          if (32 * tt + li < nv && myblk == 0) nrow[32 * tt + li] = nrm[tt];
           invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
         }
       }
@@ -720,6 +788,7 @@ __device__ __forceinline__ void append_kmix_run(
 
     static_for<4>([&](auto nc) {  // coordinate block n
       constexpr int n = decltype(nc)::value;
+      if (split && n != myblk) return;
       __builtin_amdgcn_sched_barrier(0);
       float yv[kHalves][16];
       if constexpr (FROM_Y) {
@@ -809,8 +878,11 @@ __device__ __forceinline__ void append_kmix_run(
 #pragma unroll
     for (int i = 0; i < NSK; ++i) {
       const int D = i * 64 + lane;
-      if (D < nv * RD) dst[D] = stg[i];
+      // row dword e: block e % 4 for the four-dword planes, e - 8 (- NO / 32) past them
+      const int e = D % RD, blk = e < 8 ? (e & 3) : (e - 8) % NOB;
+      if (D < nv * RD && (!split || blk == myblk)) dst[D] = stg[i];
     }
+    if constexpr (ONE) break;
   }
 }
 
@@ -959,33 +1031,52 @@ __global__ __launch_bounds__(kThreads, 4) void compress_mfma(
 // so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
 // already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
 // their norms.
-template <int VB, int XT, int D, bool PAGED, bool FROM_Y>
+template <int VB, int XT, int D, bool PAGED, bool FROM_Y, bool ONE = false>
 __device__ __forceinline__ void append_v_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg,
-    uint4* __restrict__ frag, int bid, int nb) {
+    uint4* __restrict__ frag, int bid, int nb, int nsplit = 1) {
   constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
   constexpr int NPW = D / 64;        // staging dwords per (tile, plane)
   constexpr int NS = NPW * VB * kHalves;  // staging dwords per lane: tiles x VB planes x D / 64
+  const int lane = threadIdx.x & 63, li = lane & 31;
+  const int64_t a_base = t0 & ~int64_t(31);
+  // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
+  // ONE, nsplit: the waves' tiles and coordinate blocks as in append_k_run
+  const int64_t gw = int64_t(bid) * kWaves + (threadIdx.x >> 6);
+  const bool split = ONE && nsplit > 1;
+  const int myblk = split ? static_cast<int>(gw % NBK) : 0;
+  constexpr bool PRE = ONE && !FROM_Y && !F32;
+  uint4 xpre[kHalves][PRE ? NKS : 1];
+  if constexpr (PRE) {
+    const int64_t tile = split ? gw / NBK : gw;
+    if (tile < ntiles) {
+      const int64_t grp = tile / tpg;
+      const int64_t d0 = a_base + (tile - grp * tpg) * kTok - t0;
+      const uint16_t* row[kHalves];
+      const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+      for (int tt = 0; tt < kHalves; ++tt)
+        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(d0 + 32 * tt + li, 0), S - 1)) * D;
+      load_x<NKS>(xpre, row, lane);
+    }
+  }
   if constexpr (!FROM_Y) {
     stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
     __syncthreads();
   }
 
-  const int lane = threadIdx.x & 63, li = lane & 31;
   uint32_t bv[NP > 0 ? NP : 1];
 #pragma unroll
   for (int i = 0; i < NP; ++i) bv[i] = in_vgpr(bnd.t[i]);
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
-  const int64_t a_base = t0 & ~int64_t(31);
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = int64_t(bid) * kWaves + (threadIdx.x >> 6); tile < ntiles;
-       tile += wstep) {
+  for (int64_t tile = split ? gw / NBK : gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
@@ -1019,11 +1110,18 @@ __device__ __forceinline__ void append_v_run(
         for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
         load_x_f32<NKS>(xf, xl, nrm, row, lane);
       } else {
-        const uint16_t* row[kHalves];
-        const auto* x = static_cast<const uint16_t*>(xin);
+        if constexpr (PRE) {
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
-        load_x<NKS>(xf, row, lane);
+          for (int tt = 0; tt < kHalves; ++tt)
+#pragma unroll
+            for (int s = 0; s < NKS; ++s) xf[tt][s] = xpre[tt][s];
+        } else {
+          const uint16_t* row[kHalves];
+          const auto* x = static_cast<const uint16_t*>(xin);
+#pragma unroll
+          for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+          load_x<NKS>(xf, row, lane);
+        }
 #pragma unroll
         for (int tt = 0; tt < kHalves; ++tt) {
           float ss = 0.f;
@@ -1038,7 +1136,7 @@ __device__ __forceinline__ void append_v_run(
         if (lane < 32 && ok[tt]) {
           const int64_t t = A0 + 32 * tt + li;
           const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0) vnorm[r] = nrm[tt];
+          if (r >= 0 && myblk == 0) vnorm[r] = nrm[tt];
         }
         inv[tt] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
       }
@@ -1050,6 +1148,7 @@ __device__ __forceinline__ void append_v_run(
 
     static_for<NBK>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
       constexpr int mb = decltype(mc)::value;
+      if (split && mb != myblk) return;
       __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
       // y of coordinate 32 mb + 8 (v >> 2) + 4 (l >> 5) + (v & 3), token 32 tt + (l & 31)
       float yv[kHalves][16];
@@ -1101,6 +1200,7 @@ __device__ __forceinline__ void append_v_run(
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int tau = i / (NPW * VB), k = (i / NPW) % VB, j = 64 * (i % NPW) + lane;
+      if (split && (j >> 5) != myblk) continue;  // another wave's coordinate block
       const int64_t tok0 = A0 + 32 * tau;
       const int64_t lo = max<int64_t>(t0 - tok0, 0), hi = min<int64_t>(t0 + S - tok0, 32);
       if (hi <= lo) continue;
@@ -1114,6 +1214,7 @@ __device__ __forceinline__ void append_v_run(
       if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
       *p = val;
     }
+    if constexpr (ONE) break;
   }
 }
 

@@ -13,24 +13,28 @@
 namespace {
 
 // grid = (key workgroups + value workgroups, layers): x < kblocks runs the key
-// append of layer blockIdx.y over kblocks workgroups, the rest its value append.
+// append of layer blockIdx.y over kblocks workgroups, the rest its value
+// append; each wave takes one tile or, nsplit = d / 32, one 32-coordinate
+// block of one tile (the launchers check that the grid covers that), and its
+// rows load while Pi is staged.
 template <int MB, int VB, int XT, int D>
 __global__ __launch_bounds__(kThreads, 4) void append_kv_layers(
     AppendLayers ak, AppendLayers av, int kblocks, int64_t S, int64_t ktpg, int64_t kntiles,
-    int64_t vtpg, int64_t vntiles, Half fine, Half bnd, int64_t t_stride, int64_t t0) {
+    int64_t vtpg, int64_t vntiles, Half fine, Half bnd, int64_t t_stride, int64_t t0,
+    int nsplit) {
   __shared__ uint4 frag[frag_n<D>()];         // the running half's Pi fragments
   __shared__ float4 inv_s[kWaves][kTok / 4];  // key half: 1 / norm of each wave's tokens
   const int l = blockIdx.y, b = blockIdx.x;
   if (b < kblocks)
-    append_k_run<MB, XT, D, false, false>(ak.x[l], nullptr, S, ktpg, kntiles, ak.pi[l],
+    append_k_run<MB, XT, D, false, false, true>(ak.x[l], nullptr, S, ktpg, kntiles, ak.pi[l],
                                           ak.signs[l], fine, static_cast<uint8_t*>(ak.st[l]),
                                           ak.nrm[l], t_stride, t0, QkvPages{}, frag, inv_s, b,
-                                          kblocks);
+                                          kblocks, nsplit);
   else
-    append_v_run<VB, XT, D, false, false>(av.x[l], nullptr, S, vtpg, vntiles, av.pi[l], bnd,
+    append_v_run<VB, XT, D, false, false, true>(av.x[l], nullptr, S, vtpg, vntiles, av.pi[l], bnd,
                                           static_cast<uint32_t*>(av.st[l]), av.nrm[l], t_stride,
                                           t0, QkvPages{}, frag, b - kblocks,
-                                          static_cast<int>(gridDim.x) - kblocks);
+                                          static_cast<int>(gridDim.x) - kblocks, nsplit);
 }
 
 // Mixed-precision keys and their values: x < kblocks runs append_kmix_run over
@@ -41,17 +45,19 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmixv(
     int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles,
     const float* __restrict__ pi_perm, const float* __restrict__ signs_perm, Half po, Half pr,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, const float* __restrict__ vpi, Half bnd,
-    uint32_t* __restrict__ vst, float* __restrict__ vnorm, int64_t t_stride, int64_t t0) {
+    uint32_t* __restrict__ vst, float* __restrict__ vnorm, int64_t t_stride, int64_t t0,
+    int nsplit) {
   __shared__ uint4 frag[kFragN];
   __shared__ float4 inv_s[kWaves][kTok / 4];
   const int b = blockIdx.x;
   if (b < kblocks)
-    append_kmix_run<NO, XT, false, IPM>(keys, nullptr, S, ktpg, kntiles, pi_perm, signs_perm, po,
-                                        pr, kst, knorm, t_stride, t0, frag, inv_s, b, kblocks);
+    append_kmix_run<NO, XT, false, IPM, true>(keys, nullptr, S, ktpg, kntiles, pi_perm, signs_perm, po,
+                                        pr, kst, knorm, t_stride, t0, frag, inv_s, b, kblocks,
+                                        nsplit);
   else
-    append_v_run<VB, XT, kD, false, false>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vst,
+    append_v_run<VB, XT, kD, false, false, true>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vst,
                                            vnorm, t_stride, t0, QkvPages{}, frag, b - kblocks,
-                                           static_cast<int>(gridDim.x) - kblocks);
+                                           static_cast<int>(gridDim.x) - kblocks, nsplit);
 }
 
 }  // namespace
@@ -63,13 +69,17 @@ bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* key
                          int64_t kntiles, int64_t vtpg, int64_t vntiles, const float* pi_perm,
                          const float* signs_perm, Half po, Half pr, uint8_t* kst, float* knorm,
                          const float* vpi, Half bnd, uint32_t* vst, float* vnorm,
-                         int64_t t_stride, int64_t t0, hipStream_t s) {
+                         int64_t t_stride, int64_t t0, int nsplit, hipStream_t s) {
   if ((n_out != 32 && n_out != 64) || vbits < 2 || vbits > 4 || xt < 0 || xt > 2) return false;
+  // the kernel bodies run one tile (nsplit = 4: one slot block of one tile) per wave
+  if ((nsplit != 1 && nsplit != 4) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
+      int64_t(vblocks) * kWaves < vntiles * nsplit)
+    return false;
   const dim3 grid(kblocks + vblocks);
 #define QKV_KMV(NOV, IP, VB, F)                                                                 \
   hipLaunchKernelGGL((append_kmixv<NOV, IP, VB, F>), grid, dim3(kThreads), 0, s, keys, values,  \
                      kblocks, S, ktpg, kntiles, vtpg, vntiles, pi_perm, signs_perm, po, pr, kst, \
-                     knorm, vpi, bnd, vst, vnorm, t_stride, t0)
+                     knorm, vpi, bnd, vst, vnorm, t_stride, t0, nsplit)
 #define QKV_KMV_F(NOV, IP, VB)        \
   switch (xt) {                      \
     case 0: QKV_KMV(NOV, IP, VB, 0); break; \
@@ -104,12 +114,17 @@ bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* key
 bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& ak,
                       const AppendLayers& av, int n_layers, int kblocks, int vblocks, int64_t S,
                       int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, Half fine,
-                      Half bnd, int64_t t_stride, int64_t t0, hipStream_t s) {
+                      Half bnd, int64_t t_stride, int64_t t0, int nsplit, hipStream_t s) {
   if (vbits != mbits + 1 || (d != 128 && d != 64) || xt < 0 || xt > 2) return false;
+  // the kernel bodies run one tile (nsplit = d / 32: one coordinate block of one
+  // tile) per wave
+  if ((nsplit != 1 && nsplit != d / 32) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
+      int64_t(vblocks) * kWaves < vntiles * nsplit)
+    return false;
   const dim3 grid(kblocks + vblocks, n_layers);
 #define QKV_KV(MB, F, DD)                                                                      \
   hipLaunchKernelGGL((append_kv_layers<MB, MB + 1, F, DD>), grid, dim3(kThreads), 0, s, ak, av, \
-                     kblocks, S, ktpg, kntiles, vtpg, vntiles, fine, bnd, t_stride, t0)
+                     kblocks, S, ktpg, kntiles, vtpg, vntiles, fine, bnd, t_stride, t0, nsplit)
 #define QKV_KVD(DD)                  \
   switch (mbits * 3 + xt) {          \
     case 3: QKV_KV(1, 0, DD); break;  \

@@ -277,9 +277,11 @@ def _kv_stores_equal(a, b, T):
 @pytest.mark.parametrize("n_out", [32, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("vbits", [4, 2, 1])
-def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits):
+@pytest.mark.parametrize("shape", ["few", "many"])
+def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits, shape):
     """qkv_store_append_kmixed_kv (keys and values in one launch for chunk-sized
-    appends; value bits 1 take the two-kernel path inside) writes the same
+    appends: a wave per 32-slot block of a tile for few tiles, a wave per tile
+    for more; value bits 1 take the two-kernel path inside) writes the same
     store, bit for bit, as qkv_store_append_kmixed / _kipmixed followed by the
     value-only qkv_store_append, over ragged sizes and unaligned starts."""
     cls = Q.MixedPrecisionIPQuantizer if ip else Q.MixedPrecisionMSEQuantizer
@@ -291,7 +293,8 @@ def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits):
     pi_perm = pi_perm.to(DEV)
     sp = eng._kmix_signs(torch.device(DEV))
     vq = eng.value_quantizer
-    B, H, cap = 2, 3, 512
+    (B, H), sizes = ((2, 3), (1, 37, 64, 5, 100)) if shape == "few" else ((8, 8), (160, 7, 300))
+    cap = 512
     dev = torch.device(DEV)
     one = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
     two = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
@@ -300,7 +303,7 @@ def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits):
     stream = N.stream(dev)
     gen = torch.Generator().manual_seed(n_out + vbits + 10 * int(ip))
     t0 = 0
-    for S in (1, 37, 64, 5, 100):
+    for S in sizes:
         k = torch.randn(B, H, S, 128, generator=gen)
         k[..., out_idx] *= 8.0
         k = k.to(dtype).to(DEV)
