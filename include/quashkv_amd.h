@@ -597,6 +597,21 @@ int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* value
                            int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
                            int64_t t0, void* stream);
 
+/* QuashKVEngine.append (quashkv/engine.py:145-172) into a paged store: keys
+ * and values of the same tokens in one call, each with its own rotation (kpi:
+ * the key quantizer's Pi, vpi: the value quantizer's), results identical to
+ * qkv_paged_store_append called for the keys and then for the values.  Small
+ * appends (a decode step's token per sequence) run both halves in one
+ * launch; every argument is checked before anything is launched. */
+int qkv_paged_store_append_kv(int32_t in_dtype, const void* keys, const void* values, int32_t B,
+                              int32_t H, int64_t S, int32_t d, int32_t mbits, int32_t vbits,
+                              const float* kpi, const float* signs, const float* vpi,
+                              const float* kcent_host, const float* kbound_host,
+                              const float* vbound_host, uint8_t* kpool, float* knorm,
+                              uint32_t* vpool, float* vnorm, const int32_t* page_table,
+                              int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
+                              int64_t t0, void* stream);
+
 /* qkv_decode_attention over a paged store of T tokens per sequence (the MFMA
  * path: symmetric codebooks, key MSE bits <= 2, d = 64 or 128; returns
  * QKV_E_UNSUPPORTED otherwise).  Same arguments as qkv_decode_attention with

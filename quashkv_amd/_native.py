@@ -109,6 +109,9 @@ _SIGS = {
     "qkv_paged_store_append": (_i32, [_i32, _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _p, _p,
                                       _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i64,
                                       _p]),
+    "qkv_paged_store_append_kv": (_i32, [_i32, _p, _p, _i32, _i32, _i64, _i32, _i32, _i32, _p, _p,
+                                         _p, _p, _p, _p, _p, _p, _p, _p, _p, _i32, _i32, _i32,
+                                         _i64, _p]),
     "qkv_paged_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32, _i64,
                                           _i32,
                                           _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p,

@@ -65,10 +65,11 @@ int append_blocks(int64_t ntiles) {
 // unit rows y with their norms in knorm_in / vnorm_in (in_dtype unused).
 int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bool rotated,
                       const float* knorm_in, const float* vnorm_in, int64_t groups, int64_t S,
-                      int32_t d, int32_t mbits, int32_t vbits, const float* pi,
+                      int32_t d, int32_t mbits, int32_t vbits, const float* kpi,
                       const float* signs, const float* kcent_host, const float* kbound_host,
                       const float* vbound_host, uint8_t* kstore, float* knorm, uint32_t* vstore,
-                      float* vnorm, int64_t t_stride, int64_t t0, QkvPages pg, void* stream) {
+                      float* vnorm, int64_t t_stride, int64_t t0, QkvPages pg, void* stream,
+                      const float* vpi) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
   if (pg.tab == nullptr) {
     QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
@@ -92,7 +93,7 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
       qkv_set_error("store append: key MSE bits %d not in 1..3", mbits);
       return QKV_E_UNSUPPORTED;
     }
-    QKV_REQUIRE((rotated || pi) && signs && kcent_host && kbound_host && kstore && knorm &&
+    QKV_REQUIRE((rotated || kpi) && signs && kcent_host && kbound_host && kstore && knorm &&
                     (!rotated || knorm_in),
                 "null pointer");
     QKV_REQUIRE(qkv_aligned(keys, in_align) && qkv_aligned(kstore, 4),
@@ -100,12 +101,13 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   }
   if (values) {
     QKV_REQUIRE(qkv_bits_ok(vbits), "value bits %d not in 1..4", vbits);
-    QKV_REQUIRE((rotated || pi) && vbound_host && vstore && vnorm && (!rotated || vnorm_in),
+    QKV_REQUIRE((rotated || vpi) && vbound_host && vstore && vnorm && (!rotated || vnorm_in),
                 "null pointer");
     QKV_REQUIRE(qkv_aligned(values, in_align) && qkv_aligned(vstore, 4),
                 "values %d-B / store 4-B aligned", in_align);
   }
-  QKV_REQUIRE(!pi || qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  QKV_REQUIRE((!kpi || qkv_aligned(kpi, 16)) && (!vpi || qkv_aligned(vpi, 16)),
+              "pi must be 16-byte aligned");
   Half fine{}, bnd{};
   if (const int st = append_lists(keys != nullptr, values != nullptr, mbits, vbits, kcent_host,
                                   kbound_host, vbound_host, &fine, &bnd))
@@ -113,7 +115,7 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   if (groups == 0 || S == 0) return QKV_OK;
   auto s = static_cast<hipStream_t>(stream);
   const int xt = in_dtype == QKV_F32 ? 2 : in_dtype == QKV_F16 ? 1 : 0;  // the kernels' XT
-  if (keys && values && !rotated && pg.tab == nullptr) {
+  if (keys && values && !rotated) {
     // both halves in one launch when their workgroups are resident at once
     const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
     const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
@@ -125,15 +127,22 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
       kb = append_blocks(kn);
       vb = append_blocks(vn);
     }
-    if (kb + vb <= 2 * qkv_num_cus()) {
+    if (kb + vb <= 2 * qkv_num_cus() && pg.tab != nullptr) {
+      if (qkv_app::launch_append_kv_paged(mbits, vbits, xt, d, keys, values, kb, vb, S, ktpg, kn,
+                                          vtpg, vn, kpi, signs, vpi, fine, bnd, kstore, knorm,
+                                          vstore, vnorm, t_stride, t0, pg, ns, s)) {
+        QKV_LAUNCHED();
+        return QKV_OK;
+      }
+    } else if (kb + vb <= 2 * qkv_num_cus()) {
       AppendLayers ak{}, av{};
       ak.x[0] = keys;
-      ak.pi[0] = pi;
+      ak.pi[0] = kpi;
       ak.signs[0] = signs;
       ak.st[0] = kstore;
       ak.nrm[0] = knorm;
       av.x[0] = values;
-      av.pi[0] = pi;
+      av.pi[0] = vpi;
       av.st[0] = vstore;
       av.nrm[0] = vnorm;
       if (qkv_app::launch_append_kv(mbits, vbits, xt, d, ak, av, 1, kb, vb, S, ktpg, kn, vtpg, vn,
@@ -149,15 +158,15 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
 #define QKV_K(MB, F, DD)                                                                       \
   if (rotated)                                                                                 \
     hipLaunchKernelGGL((append_k_mfma<MB, 0, DD, false, true>), grid, dim3(kThreads), 0, s,     \
-                       keys, knorm_in, S, tpg, ntiles, pi, signs, fine, kstore, knorm,          \
+                       keys, knorm_in, S, tpg, ntiles, kpi, signs, fine, kstore, knorm,          \
                        t_stride, t0, pg);                                                      \
   else if (pg.tab)                                                                             \
     hipLaunchKernelGGL((append_k_mfma<MB, F, DD, true, false>), grid, dim3(kThreads), 0, s,     \
-                       keys, nullptr, S, tpg, ntiles, pi, signs, fine, kstore, knorm,           \
+                       keys, nullptr, S, tpg, ntiles, kpi, signs, fine, kstore, knorm,           \
                        t_stride, t0, pg);                                                      \
   else                                                                                         \
     hipLaunchKernelGGL((append_k_mfma<MB, F, DD, false, false>), grid, dim3(kThreads), 0, s,    \
-                       keys, nullptr, S, tpg, ntiles, pi, signs, fine, kstore, knorm,           \
+                       keys, nullptr, S, tpg, ntiles, kpi, signs, fine, kstore, knorm,           \
                        t_stride, t0, pg)
 #define QKV_KD(DD)                                  \
   switch (mbits * 3 + xt) {                         \
@@ -187,15 +196,15 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
 #define QKV_V(VB, F, DD)                                                                       \
   if (rotated)                                                                                 \
     hipLaunchKernelGGL((append_v_mfma<VB, 0, DD, false, true>), grid, dim3(kThreads), 0, s,     \
-                       values, vnorm_in, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,  \
+                       values, vnorm_in, S, tpg, ntiles, vpi, bnd, vstore, vnorm, t_stride, t0,  \
                        pg);                                                                    \
   else if (pg.tab)                                                                             \
     hipLaunchKernelGGL((append_v_mfma<VB, F, DD, true, false>), grid, dim3(kThreads), 0, s,     \
-                       values, nullptr, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,   \
+                       values, nullptr, S, tpg, ntiles, vpi, bnd, vstore, vnorm, t_stride, t0,   \
                        pg);                                                                    \
   else                                                                                         \
     hipLaunchKernelGGL((append_v_mfma<VB, F, DD, false, false>), grid, dim3(kThreads), 0, s,    \
-                       values, nullptr, S, tpg, ntiles, pi, bnd, vstore, vnorm, t_stride, t0,   \
+                       values, nullptr, S, tpg, ntiles, vpi, bnd, vstore, vnorm, t_stride, t0,   \
                        pg)
 #define QKV_VD(DD)                                  \
   switch (vbits * 3 + xt) {                         \
@@ -511,8 +520,8 @@ int kmixed_kv_impl(int32_t in_dtype, const void* keys, const void* values, int64
                                         t0, stream))
     return st;
   return store_append_impl(in_dtype, nullptr, values, false, nullptr, nullptr, groups, S, d, 2,
-                           vbits, vpi, nullptr, nullptr, nullptr, vbound_host, nullptr, nullptr,
-                           vstore, vnorm, t_stride, t0, QkvPages{}, stream);
+                           vbits, nullptr, nullptr, nullptr, nullptr, vbound_host, nullptr, nullptr,
+                           vstore, vnorm, t_stride, t0, QkvPages{}, stream, vpi);
 }
 
 }  // namespace
@@ -526,7 +535,7 @@ extern "C" int qkv_store_append(int32_t in_dtype, const void* keys, const void* 
                                 void* stream) {
   return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, groups, S, d, mbits,
                            vbits, pi, signs, kcent_host, kbound_host, vbound_host, kstore, knorm,
-                           vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream);
+                           vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0}, stream, pi);
 }
 
 extern "C" int qkv_store_append_layers(int32_t n_layers, int32_t in_dtype,
@@ -555,7 +564,7 @@ extern "C" int qkv_store_append_rotated(const float* yk, const float* knorm_in, 
   return store_append_impl(QKV_F32, yk, yv, true, knorm_in, vnorm_in, groups, S, d, mbits,
                            vbits, nullptr, signs, kcent_host, kbound_host, vbound_host, kstore,
                            knorm, vstore, vnorm, t_stride, t0, QkvPages{nullptr, 0, 1, 6, 0},
-                           stream);
+                           stream, nullptr);
 }
 
 extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
@@ -575,7 +584,27 @@ extern "C" int qkv_paged_store_append(int32_t in_dtype, const void* keys, const 
   return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, int64_t(B) * H, S, d,
                            mbits, vbits, pi, signs, kcent_host, kbound_host, vbound_host, kpool,
                            knorm, vpool, vnorm, page_tokens, t0,
-                           QkvPages{page_table, pages_per_seq, H, lg, num_pages}, stream);
+                           QkvPages{page_table, pages_per_seq, H, lg, num_pages}, stream, pi);
+}
+
+extern "C" int qkv_paged_store_append_kv(
+    int32_t in_dtype, const void* keys, const void* values, int32_t B, int32_t H, int64_t S,
+    int32_t d, int32_t mbits, int32_t vbits, const float* kpi, const float* signs,
+    const float* vpi, const float* kcent_host, const float* kbound_host,
+    const float* vbound_host, uint8_t* kpool, float* knorm, uint32_t* vpool, float* vnorm,
+    const int32_t* page_table, int32_t pages_per_seq, int32_t page_tokens, int32_t num_pages,
+    int64_t t0, void* stream) {
+  QKV_REQUIRE(keys && values, "null pointer");
+  QKV_REQUIRE(B >= 0 && H > 0 && int64_t(B) * H < (int64_t(1) << 31), "invalid shape");
+  QKV_REQUIRE(page_table && pages_per_seq > 0, "null page table");
+  QKV_REQUIRE(num_pages > 0, "num_pages %d must be positive", num_pages);
+  const int lg = qkv_page_lg(page_tokens);
+  QKV_REQUIRE(lg > 0, "page_tokens %d must be 64, 128, ..., 2048", page_tokens);
+  QKV_REQUIRE(qkv_aligned(page_table, 4), "page table 4-B aligned");
+  return store_append_impl(in_dtype, keys, values, false, nullptr, nullptr, int64_t(B) * H, S, d,
+                           mbits, vbits, kpi, signs, kcent_host, kbound_host, vbound_host, kpool,
+                           knorm, vpool, vnorm, page_tokens, t0,
+                           QkvPages{page_table, pages_per_seq, H, lg, num_pages}, stream, vpi);
 }
 
 extern "C" int qkv_store_append_kmixed(int32_t in_dtype, const void* keys, int64_t groups,

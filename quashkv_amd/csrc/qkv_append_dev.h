@@ -99,6 +99,16 @@ bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& a
                       int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, Half fine,
                       Half bnd, int64_t t_stride, int64_t t0, int nsplit, hipStream_t s);
 
+// launch_append_kv over one paged store (append_k_run and append_v_run with
+// PAGED), keys and values each with their own Pi.
+bool launch_append_kv_paged(int mbits, int vbits, int xt, int d, const void* keys,
+                            const void* values, int kblocks, int vblocks, int64_t S,
+                            int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles,
+                            const float* kpi, const float* signs, const float* vpi, Half fine,
+                            Half bnd, uint8_t* kpool, float* knorm, uint32_t* vpool,
+                            float* vnorm, int64_t t_stride, int64_t t0, const QkvPages& pg,
+                            int nsplit, hipStream_t s);
+
 // One launch of append_kmix_run (mixed-precision keys, n_out outlier slots,
 // IP or MSE) and append_v_run (value bits 2..4) over one contiguous store
 // (defined in qkv_append_kv.hip); false, launching nothing, for combinations
@@ -613,7 +623,8 @@ __device__ __forceinline__ void append_k_run(
       for (int i = 0; i < NSK; ++i) {
         const int w = i * 64 + lane, r = w / RD;
         const int64_t row = sp.row(t0 + s0 + r);
-        if (w < nv * RD && row >= 0) dst[row * RD + (w - r * RD)] = stg[i];
+        if (w < nv * RD && row >= 0 && (!split || w % NBK == myblk))
+          dst[row * RD + (w - r * RD)] = stg[i];
       }
     } else {
       uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));

@@ -37,6 +37,27 @@ __global__ __launch_bounds__(kThreads, 4) void append_kv_layers(
                                           static_cast<int>(gridDim.x) - kblocks, nsplit);
 }
 
+// The same over a paged store (two workgroups per CU, as the paged kernels).
+template <int MB, int VB, int XT, int D>
+__global__ __launch_bounds__(kThreads, 2) void append_kv_paged(
+    const void* __restrict__ keys, const void* __restrict__ values, int kblocks, int64_t S,
+    int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles, const float* __restrict__ kpi,
+    const float* __restrict__ signs, const float* __restrict__ vpi, Half fine, Half bnd,
+    uint8_t* __restrict__ kpool, float* __restrict__ knorm, uint32_t* __restrict__ vpool,
+    float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg, int nsplit) {
+  __shared__ uint4 frag[frag_n<D>()];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
+  const int b = blockIdx.x;
+  if (b < kblocks)
+    append_k_run<MB, XT, D, true, false, true>(keys, nullptr, S, ktpg, kntiles, kpi, signs, fine,
+                                               kpool, knorm, t_stride, t0, pg, frag, inv_s, b,
+                                               kblocks, nsplit);
+  else
+    append_v_run<VB, XT, D, true, false, true>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vpool,
+                                               vnorm, t_stride, t0, pg, frag, b - kblocks,
+                                               static_cast<int>(gridDim.x) - kblocks, nsplit);
+}
+
 // Mixed-precision keys and their values: x < kblocks runs append_kmix_run over
 // kblocks workgroups, the rest append_v_run.
 template <int NO, bool IPM, int VB, int XT>
@@ -108,6 +129,45 @@ bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* key
 #undef QKV_KMV_V
 #undef QKV_KMV_F
 #undef QKV_KMV
+  return true;
+}
+
+bool launch_append_kv_paged(int mbits, int vbits, int xt, int d, const void* keys,
+                            const void* values, int kblocks, int vblocks, int64_t S,
+                            int64_t ktpg, int64_t kntiles, int64_t vtpg, int64_t vntiles,
+                            const float* kpi, const float* signs, const float* vpi, Half fine,
+                            Half bnd, uint8_t* kpool, float* knorm, uint32_t* vpool,
+                            float* vnorm, int64_t t_stride, int64_t t0, const QkvPages& pg,
+                            int nsplit, hipStream_t s) {
+  if (vbits != mbits + 1 || (d != 128 && d != 64) || xt < 0 || xt > 2) return false;
+  if ((nsplit != 1 && nsplit != d / 32) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
+      int64_t(vblocks) * kWaves < vntiles * nsplit)
+    return false;
+  const dim3 grid(kblocks + vblocks);
+#define QKV_KVP(MB, F, DD)                                                                     \
+  hipLaunchKernelGGL((append_kv_paged<MB, MB + 1, F, DD>), grid, dim3(kThreads), 0, s, keys,    \
+                     values, kblocks, S, ktpg, kntiles, vtpg, vntiles, kpi, signs, vpi, fine,   \
+                     bnd, kpool, knorm, vpool, vnorm, t_stride, t0, pg, nsplit)
+#define QKV_KVPD(DD)                   \
+  switch (mbits * 3 + xt) {            \
+    case 3: QKV_KVP(1, 0, DD); break;  \
+    case 4: QKV_KVP(1, 1, DD); break;  \
+    case 5: QKV_KVP(1, 2, DD); break;  \
+    case 6: QKV_KVP(2, 0, DD); break;  \
+    case 7: QKV_KVP(2, 1, DD); break;  \
+    case 8: QKV_KVP(2, 2, DD); break;  \
+    case 9: QKV_KVP(3, 0, DD); break;  \
+    case 10: QKV_KVP(3, 1, DD); break; \
+    case 11: QKV_KVP(3, 2, DD); break; \
+    default: return false;             \
+  }
+  if (d == 128) {
+    QKV_KVPD(128)
+  } else {
+    QKV_KVPD(64)
+  }
+#undef QKV_KVPD
+#undef QKV_KVP
   return true;
 }
 

@@ -255,7 +255,7 @@ class PagedQuashKVEngine(QuashKVEngine):
         self._total_tokens += S
 
     def _append_paged(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
-        """bf16, fp16 or fp32 K/V straight into the pages (qkv_paged_store_append)."""
+        """bf16, fp16 or fp32 K/V straight into the pages (qkv_paged_store_append_kv)."""
         if (keys.dtype not in (torch.bfloat16, torch.float16, torch.float32)
                 or values.dtype != keys.dtype):
             return False
@@ -272,15 +272,12 @@ class PagedQuashKVEngine(QuashKVEngine):
         dt = N.dtype_code(k.dtype)
         stream = N.stream(k.device)
         L = N.lib()
-        N.check(L.qkv_paged_store_append(
-            dt, k.data_ptr(), None, B, H, S, d, kq.mse_bits, vq.bits, mq.Pi.data_ptr(),
-            kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(), st.knorm.data_ptr(),
-            st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq, st.pt,
-            st.num_pages, t0, stream))
-        N.check(L.qkv_paged_store_append(
-            dt, None, v.data_ptr(), B, H, S, d, kq.mse_bits, vq.bits, vq.Pi.data_ptr(), None,
-            None, None, vb.ptr, None, None, st.vpool.data_ptr(), st.vnorm.data_ptr(),
-            st.table.data_ptr(), st.pages_per_seq, st.pt, st.num_pages, t0, stream))
+        # keys and values in one call (one launch for a decode step's tokens)
+        N.check(L.qkv_paged_store_append_kv(
+            dt, k.data_ptr(), v.data_ptr(), B, H, S, d, kq.mse_bits, vq.bits, mq.Pi.data_ptr(),
+            kq.S.data_ptr(), vq.Pi.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(),
+            st.knorm.data_ptr(), st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(),
+            st.pages_per_seq, st.pt, st.num_pages, t0, stream))
         return True
 
     def _append_scatter(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> None:

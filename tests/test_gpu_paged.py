@@ -19,6 +19,7 @@ import random
 import pytest
 import torch
 
+import quashkv_amd as Q
 from quashkv_amd import _native as N
 from quashkv_amd.engine import QuashKVEngine
 from quashkv_amd.paged import PagedKVStore, PagedQuashKVEngine
@@ -266,3 +267,73 @@ def test_paged_layers_match_single_layer_calls(d, page_tokens):
         else:
             assert torch.equal(o, ref)
         _close(o, _oracle(q, e, causal=False))
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (4, 4), (3, 2)])
+@pytest.mark.parametrize("shape", ["few", "many"])
+def test_paged_kv_append_equals_two_calls(d, dtype, key_bits, value_bits, shape):
+    """qkv_paged_store_append_kv (keys and values in one launch for small
+    appends when value bits = key bits: a wave per 32-coordinate block of a
+    tile for few tiles, a wave per tile for more; 3/2 bits take two launches
+    inside) writes the same pool, bit for bit, as qkv_paged_store_append for
+    the keys and then for the values, over ragged sizes and unaligned starts
+    on shuffled pages."""
+    (B, H), sizes = ((2, 3), (1, 5, 37, 64, 1, 100)) if shape == "few" else \
+        ((8, 8), (160, 7, 300))
+    dev = torch.device(DEV)
+    kq = Q.InnerProductQuantizer(d, key_bits, seed=7, device=DEV)
+    vq = Q.MSEQuantizer(d, value_bits, seed=8, device=DEV)
+    mq = kq.mse_quantizer
+    kc = N.HostFloats(mq.codebook.centroids_host)
+    kb = N.HostFloats(mq.codebook.boundaries_host)
+    vb = N.HostFloats(vq.codebook.boundaries_host)
+    total = sum(sizes)
+    stores = []
+    for _ in range(2):
+        st = PagedKVStore(B, H, d, key_bits - 1, value_bits, B * 32 + 3, dev, 64)
+        st.ensure(total)
+        stores.append(st)
+    g = torch.Generator().manual_seed(11)
+    assert stores[0].num_pages >= B * stores[0].table.shape[1]
+    perm = torch.randperm(stores[0].num_pages, generator=g)[:B * stores[0].table.shape[1]]
+    tab = perm.view(B, -1).to(torch.int32).to(dev)   # shuffled pages, same table for both
+    for st in stores:
+        st.table = tab.clone()
+    L = N.lib()
+    dt = N.dtype_code(dtype)
+    stream = N.stream(dev)
+    t0 = 0
+    for S in sizes:
+        k = torch.randn(B, H, S, d, generator=g).to(dtype).to(DEV)
+        v = torch.randn(B, H, S, d, generator=g).to(dtype).to(DEV)
+        a, b = stores
+        N.check(L.qkv_paged_store_append_kv(
+            dt, k.data_ptr(), v.data_ptr(), B, H, S, d, key_bits - 1, value_bits,
+            mq.Pi.data_ptr(), kq.S.data_ptr(), vq.Pi.data_ptr(), kc.ptr, kb.ptr, vb.ptr,
+            a.kpool.data_ptr(), a.knorm.data_ptr(), a.vpool.data_ptr(), a.vnorm.data_ptr(),
+            a.table.data_ptr(), a.table.shape[1], a.pt, a.num_pages, t0, stream))
+        N.check(L.qkv_paged_store_append(
+            dt, k.data_ptr(), None, B, H, S, d, key_bits - 1, value_bits, mq.Pi.data_ptr(),
+            kq.S.data_ptr(), kc.ptr, kb.ptr, vb.ptr, b.kpool.data_ptr(), b.knorm.data_ptr(),
+            b.vpool.data_ptr(), b.vnorm.data_ptr(), b.table.data_ptr(), b.table.shape[1], b.pt,
+            b.num_pages, t0, stream))
+        N.check(L.qkv_paged_store_append(
+            dt, None, v.data_ptr(), B, H, S, d, key_bits - 1, value_bits, vq.Pi.data_ptr(),
+            None, None, None, vb.ptr, None, None, b.vpool.data_ptr(), b.vnorm.data_ptr(),
+            b.table.data_ptr(), b.table.shape[1], b.pt, b.num_pages, t0, stream))
+        t0 += S
+    torch.cuda.synchronize()
+    a, b = stores
+    ga, gb = a.gather(t0), b.gather(t0)       # contiguous copies of tokens [0, t0)
+    assert torch.equal(ga.kst[:, :, :t0], gb.kst[:, :, :t0])
+    assert torch.equal(ga.knorm[:, :, :t0], gb.knorm[:, :, :t0])
+    assert torch.equal(ga.vnorm[:, :, :t0], gb.vnorm[:, :, :t0])
+    nt = (t0 + 31) // 32
+    va, vb2 = ga.vst[:, :, :nt].clone(), gb.vst[:, :, :nt].clone()
+    if t0 % 32:
+        va[:, :, -1] &= (1 << (t0 % 32)) - 1
+        vb2[:, :, -1] &= (1 << (t0 % 32)) - 1
+    assert torch.equal(va, vb2)
+    assert ga.knorm[:, :, :t0].abs().min() > 0

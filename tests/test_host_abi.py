@@ -395,3 +395,28 @@ def test_store_append_kmixed_kv_host_validation():
     assert call(cap=100, S=1) == N.QKV_E_INVALID  # capacity not a multiple of 32
     assert call(cap=64, S=65) == N.QKV_E_INVALID
     assert call(dt=7) == N.QKV_E_INVALID
+
+
+def test_paged_store_append_kv_host_validation():
+    """Argument checks of qkv_paged_store_append_kv, all before any launch."""
+    lib = N.lib()
+    cb = LloydMaxCodebook(128, 2)
+    kc, kb = N.HostFloats(cb.centroids_host), N.HostFloats(cb.boundaries_host)
+    vb = N.HostFloats(LloydMaxCodebook(128, 3).boundaries_host)
+    P = 256
+
+    def call(keys=P, values=P, B=2, S=1, d=128, vbits=3, table=P, pt=64, npages=8, dt=2):
+        return lib.qkv_paged_store_append_kv(dt, keys, values, B, 2, S, d, 2, vbits, P, P, P,
+                                             kc.ptr, kb.ptr, vb.ptr, P, P, P, P, table, 4, pt,
+                                             npages, 0, None)
+
+    assert call(B=0) == N.QKV_OK                   # nothing to append: checks only
+    assert call(values=None) == N.QKV_E_INVALID
+    assert call(keys=None) == N.QKV_E_INVALID
+    assert call(table=None) == N.QKV_E_INVALID
+    assert call(pt=48) == N.QKV_E_INVALID           # pages of 64 * 2^k tokens
+    assert call(npages=0) == N.QKV_E_INVALID
+    assert call(S=4 * 64 + 1) == N.QKV_E_INVALID    # beyond the table's pages
+    assert call(d=96) == N.QKV_E_UNSUPPORTED
+    assert call(vbits=5) == N.QKV_E_INVALID
+    assert call(dt=7) == N.QKV_E_INVALID
