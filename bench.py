@@ -45,7 +45,8 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBS = 8000.0
 PEAK_INT8_TOPS = 5000.0
 METRIC = "decode attn over 3-bit KV: µs/step, HBM GB/s % of peak; compress Gvec/s"
-DTYPE = "fp8 x fp4 (scores) and i8 (values) on MFMA, exact; f32 softmax"
+DTYPE = ("fp8 x fp4 MFMA scores (query weights as 4 fp8 digits, ~16 bits), i8 MFMA values "
+         "(softmax weights as 29-bit fixed point); f32 softmax")
 TRAFFIC_RECORD = os.path.join(ROOT, "profiles", "decode_fused_cfg3_decode.md")
 
 B, HQ, HKV, D, T = 32, 32, 8, 128, 8192
@@ -775,8 +776,9 @@ def sub_cfg5(args, dev, stream) -> dict:
 
 SUBS = {"cfg1": sub_cfg1, "cfg2": sub_cfg2, "cfg4": sub_cfg4, "cfg5": sub_cfg5}
 # arithmetic of each workload's dominant kernel (d = 64 decodes and MIPS score on int8 MFMA)
-SUB_DTYPE = {"cfg1": DTYPE, "cfg2": "i8 on MFMA (scores and values), exact; f32 softmax",
-             "cfg4": DTYPE, "cfg5": "i8 on MFMA (scores), exact"}
+SUB_DTYPE = {"cfg1": DTYPE, "cfg2": ("i8 MFMA scores and values (30-bit fixed-point query "
+                                    "weights, 29-bit softmax weights); f32 softmax"),
+             "cfg4": DTYPE, "cfg5": "i8 MFMA scores (30-bit fixed-point query weights)"}
 SUB_KEYS = {"cfg1": "cfg1", "cfg2": "cfg2_layers", "cfg4": "cfg4", "cfg5": "cfg5"}
 
 

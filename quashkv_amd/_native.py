@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from typing import Optional
 
 import torch  # loads torch's HIP runtime first; the library binds to the same one
@@ -255,14 +256,28 @@ _HOST_TABLES: dict = {}
 
 def host_table(t: torch.Tensor) -> HostFloats:
     """A host copy of a small device table (codebook centroids / boundaries),
-    cached per tensor storage and version: the first use of a table costs one
-    device-to-host copy, later calls none."""
-    key = (t.data_ptr(), t._version, t.numel(), str(t.device), t.dtype)
-    h = _HOST_TABLES.get(key)
-    if h is None:
-        if len(_HOST_TABLES) > 256:
-            _HOST_TABLES.clear()
-        h = _HOST_TABLES[key] = HostFloats(t.detach().float().cpu().reshape(-1).tolist())
+    cached per tensor object: the first use of a table costs one
+    device-to-host copy, later calls with the same tensor none.
+
+    An entry holds a weak reference to the tensor it was made from and the
+    tensor's version counter (shared by its views, bumped by every in-place
+    write); it is used only while that same tensor is alive and unmodified,
+    and dropped when the tensor is freed.  A table that is freed and replaced
+    by another at the same address is therefore copied afresh."""
+    key = id(t)
+    ent = _HOST_TABLES.get(key)
+    if ent is not None:
+        ref, version, h = ent
+        if ref() is t and version == t._version:
+            return h
+    h = HostFloats(t.detach().float().cpu().reshape(-1).tolist())
+
+    def _drop(r, key=key):
+        e = _HOST_TABLES.get(key)
+        if e is not None and e[0] is r:
+            del _HOST_TABLES[key]
+
+    _HOST_TABLES[key] = (weakref.ref(t, _drop), t._version, h)
     return h
 
 

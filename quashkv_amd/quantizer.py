@@ -51,6 +51,12 @@ def _flat_rows(x: torch.Tensor, d: int) -> torch.Tensor:
     return x.contiguous()
 
 
+def _host_tables(cb) -> tuple:
+    """(centroids, boundaries) of a LloydMaxCodebook as host arrays, from
+    the fp32 values it keeps on the host."""
+    return N.HostFloats(cb.centroids_host), N.HostFloats(cb.boundaries_host)
+
+
 def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torch.Tensor,
                   centroids: torch.Tensor, bits: int, signs: Optional[torch.Tensor],
                   codes: torch.Tensor, qjl: Optional[torch.Tensor], norms: Optional[torch.Tensor],
@@ -181,8 +187,9 @@ class MSEQuantizer:
         n = int(torch.Size(lead).numel())
         codes = torch.empty(n, self.d, dtype=torch.uint8, device=dev)
         norms = torch.empty(n, dtype=torch.float32, device=dev)
-        compress_into(N.QKV_MODE_MSE, x, self.Pi, self.codebook.boundaries,
-                      self.codebook.centroids, self.bits, None, codes, None, norms, packed=False)
+        cb = self.codebook
+        compress_into(N.QKV_MODE_MSE, x, self.Pi, cb.boundaries, cb.centroids, self.bits, None,
+                      codes, None, norms, packed=False, host_tables=_host_tables(cb))
         return codes.reshape(*lead, self.d), norms.reshape(lead)
 
     def decompress(self, indices: torch.Tensor, norms: torch.Tensor) -> torch.Tensor:
@@ -239,7 +246,8 @@ class InnerProductQuantizer:
         norms = torch.empty(n, dtype=torch.float32, device=dev)
         mq = self.mse_quantizer
         compress_into(N.QKV_MODE_IP, x, mq.Pi, mq.codebook.boundaries, mq.codebook.centroids,
-                      self.mse_bits, self.S, codes, bits, norms, packed=False)
+                      self.mse_bits, self.S, codes, bits, norms, packed=False,
+                      host_tables=_host_tables(mq.codebook))
         return (codes.reshape(*lead, self.d), bits.reshape(*lead, self.d), norms.reshape(lead))
 
     def decompress_for_dot(self, mse_indices: torch.Tensor, qjl_signs: torch.Tensor,

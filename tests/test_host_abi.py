@@ -420,3 +420,20 @@ def test_paged_store_append_kv_host_validation():
     assert call(d=96) == N.QKV_E_UNSUPPORTED
     assert call(vbits=5) == N.QKV_E_INVALID
     assert call(dt=7) == N.QKV_E_INVALID
+
+
+def test_host_table_cache_follows_the_tensor_not_its_address():
+    """N.host_table's cached host copy belongs to one live tensor: a table
+    freed and replaced by another of the same size (often at the same
+    address) is copied afresh, and an in-place write to a live table is seen."""
+    for i in range(200):
+        t = torch.full((7,), float(i))
+        assert list(N.host_table(t).arr) == [float(i)] * 7
+        del t
+    t = torch.arange(5, dtype=torch.float32)
+    assert list(N.host_table(t).arr) == [0.0, 1.0, 2.0, 3.0, 4.0]
+    t.view(5)[2] = 9.0            # a write through a view bumps the shared version
+    assert list(N.host_table(t).arr) == [0.0, 1.0, 9.0, 3.0, 4.0]
+    n_before = len(N._HOST_TABLES)
+    del t
+    assert len(N._HOST_TABLES) == n_before - 1   # the entry goes with its tensor
