@@ -332,6 +332,33 @@ int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
                          void* out, int32_t out_dtype, void* workspace,
                          int64_t ws_bytes, int32_t n_splits, void* stream);
 
+/* qkv_decode_attention with per-sequence key ranges and a causal query
+ * position.  Replaces the causal placement of fused_quantized_attention
+ * (queries at total_kv_tokens - Q + i, quashkv/triton_kernels/attention.py:
+ * 118-121) and the padding mask that HF attention applies to the reference's
+ * reconstructed keys (quashkv/integrations/hf_cache.py:123-152, a left-padded
+ * batch masks each sequence's leading pad positions).
+ *   kv_start, kv_end  B int32 (device memory) or NULL: sequence b attends to
+ *                     the keys [kv_start[b], kv_end[b]) of its T cached tokens
+ *                     (NULL: 0 and T; values are clamped to [0, T]); keys
+ *                     outside contribute nothing, and a sequence with none
+ *                     gives zeros
+ *   q_end             causal only: query i of every sequence sits at position
+ *                     q_end - Q + i and sees the keys t <= q_end - Q + i;
+ *                     q_end = 0 places it at kv_end[b] - Q + i (T - Q + i)
+ * Other arguments as qkv_decode_attention; same workspace. */
+int qkv_decode_attention_ranges(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                                const float* knorm, const uint32_t* vstore,
+                                const float* vnorm, int64_t t_stride, int64_t T,
+                                const int32_t* kv_start, const int32_t* kv_end,
+                                int64_t q_end, int32_t B, int32_t Hq, int32_t Hkv,
+                                int32_t Q, int32_t d, int32_t kbits, int32_t vbits,
+                                const float* pi, const float* kcent_host,
+                                const float* vcent_host, const float* signs,
+                                float qjl_scale, float scale, int32_t causal,
+                                void* out, int32_t out_dtype, void* workspace,
+                                int64_t ws_bytes, int32_t n_splits, void* stream);
+
 /* No counterpart in the reference: qkv_decode_attention for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  Same arguments and results as

@@ -95,6 +95,9 @@ _SIGS = {
     "qkv_decode_attention": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32, _i32,
                                     _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32, _f32, _i32,
                                     _p, _i32, _p, _i64, _i32, _p]),
+    "qkv_decode_attention_ranges": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _p, _p, _i64,
+                                           _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _p, _p,
+                                           _p, _f32, _f32, _i32, _p, _i32, _p, _i64, _i32, _p]),
     "qkv_decode_attention_noalloc": (_i32, [_p, _i32, _p, _p, _p, _p, _i64, _i64, _i32, _i32,
                                             _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _f32,
                                             _f32, _i32, _p, _i32, _i32, _p]),

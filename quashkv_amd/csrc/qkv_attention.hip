@@ -133,7 +133,8 @@ __global__ __launch_bounds__(kTileG) void split_generic(
     const float* __restrict__ knorm, const uint32_t* __restrict__ vst,
     const float* __restrict__ vnorm, int64_t t_stride, int64_t T, int Hkv, int R, int Q,
     int row_chunks, int mbits, int vbits, Tables tb, float scale, int causal,
-    int64_t split_len, float* __restrict__ part_o, float* __restrict__ part_ml) {
+    int64_t split_len, const int32_t* __restrict__ klo, const int32_t* __restrict__ khi,
+    int64_t cbase, float* __restrict__ part_o, float* __restrict__ part_ml) {
   __shared__ float qs[kRowsG][D];
   __shared__ float ws[kRowsG][D];
   __shared__ float ps[kRowsG][kTileG];  // scores, then probabilities; reused at the end
@@ -174,6 +175,10 @@ __global__ __launch_bounds__(kTileG) void split_generic(
 
   const int64_t t_begin = int64_t(split) * split_len;
   const int64_t t_end = min<int64_t>(T, t_begin + split_len);
+  // this sequence's attended keys [k_lo, k_hi) and causal position
+  const int64_t k_lo = klo ? max<int64_t>(0, klo[b]) : 0;
+  const int64_t k_hi = khi ? min<int64_t>(T, khi[b]) : T;
+  const int64_t cpos = cbase > 0 ? cbase : k_hi;
 
   const int pj = tid & 127, hf = tid >> 7;  // PV layout: coordinate, token half
   float acc[kRowsG];
@@ -206,16 +211,16 @@ __global__ __launch_bounds__(kTileG) void split_generic(
         const int r = rb + i;
         if (r < nr) {
           float v = kn * s[i];
-          if (!valid) v = -INFINITY;
+          if (!valid || t < k_lo || t >= k_hi) v = -INFINITY;
           if (causal) {
             const int qi = (r_begin + r) % Q;
-            if (t > T - Q + qi) v = -INFINITY;
+            if (t > cpos - Q + qi) v = -INFINITY;
           }
           ps[r][tid] = v;
         }
       }
     }
-    vn[tid] = valid ? vnb[tc] : 0.f;
+    vn[tid] = valid && t >= k_lo && t < k_hi ? vnb[tc] : 0.f;
     __syncthreads();
 
     for (int r = 0; r < nr; ++r) {
@@ -570,6 +575,10 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int64_t ts = int64_t(split) * split_len;
   const int64_t te = min<int64_t>(T, ts + split_len);
   const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
+  // the sequence's attended keys, split-relative: [slo, shi)
+  const SeqRange sr = seq_range(kv, bseq, T);
+  const int slo = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.lo - ts)));
+  const int shi = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.hi - ts)));
 
   // ---------------- phase 1: scores of every token of the split -> LDS
   qkv_v4i a[RC][NU];
@@ -589,9 +598,9 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
     fq[c] = cv ? rowc[(bhc * kRowsM + lg) * 2 + 1] : 0.f;
     row_ok[c] = kRowsM * c + lg < nr;
     // causal: token tl (split-relative) is visible to this lane's row iff
-    // ts + tl <= T - Q + qi
+    // ts + tl <= cpos - Q + qi
     const int qi = (r0 + kRowsM * c + lg) % Q;
-    const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(kSplitMax);
+    const int64_t climit = causal ? (sr.cpos - Q + qi - ts) : int64_t(kSplitMax);
     clim[c] = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, kSplitMax)));
   }
 
@@ -670,7 +679,7 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const int tl = tile * 64 + sub * 16 + ln;
-      const bool in = tl < ntok && ((page_okm >> tile) & 1u);
+      const bool in = tl >= slo && tl < shi && ((page_okm >> tile) & 1u);
 #pragma unroll
       for (int c = 0; c < RC; ++c) {
         const float z = static_cast<float>(acc[c][sub][0]) +
@@ -1202,9 +1211,13 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     // E8M0 scale of this lane's operand row ln = 4 r + d: 2^(sigma_r - 4 d)
     const int asc = 127 + static_cast<int>(rowcs[2 * (ln >> 2) + 1]) - 4 * (ln & 3);
     const bool row_ok = lg < nr;
+    // the sequence's attended keys, split-relative: [slo, shi)
+    const SeqRange sr = seq_range(kv, b, T);
+    const int slo = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.lo - ts)));
+    const int shi = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.hi - ts)));
     // causal: split-relative token tl is visible to row lg iff tl <= clim
     const int qi = (r0 + lg) % Q;
-    const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(INT_MAX);
+    const int64_t climit = causal ? (sr.cpos - Q + qi - ts) : int64_t(INT_MAX);
     const int clim = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, INT_MAX)));
     int cmin = INT_MAX;  // the smallest limit over the valid rows (wave-uniform)
     if (causal) {
@@ -1212,7 +1225,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       for (int r = 0; r < kRowsM; ++r) {
         if (r < nr) {
           const int q2 = (r0 + r) % Q;
-          cmin = static_cast<int>(min<int64_t>(cmin, max<int64_t>(-1, T - Q + q2 - ts)));
+          cmin = static_cast<int>(min<int64_t>(cmin, max<int64_t>(-1, sr.cpos - Q + q2 - ts)));
         }
       }
     }
@@ -1269,7 +1282,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       mfma_settle();
       const int tbase = tile * 64;
       const bool pok = page_ok(tile);
-      const bool full = pok && tbase + 64 <= ntok && nr == kRowsM && tbase + 63 <= cmin;
+      const bool full = pok && tbase >= slo && tbase + 64 <= shi && nr == kRowsM &&
+                        tbase + 63 <= cmin;
       float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
       float mloc = -INFINITY;
 #pragma unroll
@@ -1279,12 +1293,12 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         float sc = knt[sub] * fmaf(z, scale2, cr2);
         if (!full) {
           const int tl = tbase + sub * 16 + ln;
-          sc = (pok && tl < ntok && row_ok && tl <= clim) ? sc : -INFINITY;
+          sc = (pok && tl >= slo && tl < shi && row_ok && tl <= clim) ? sc : -INFINITY;
         }
         srow[sub * 16 + ln] = sc;
         mloc = fmaxf(mloc, sc);
       }
-      if (!full) vz = (pok && tbase + lane < ntok) ? vz : 0.f;
+      if (!full) vz = (pok && tbase + lane >= slo && tbase + lane < shi) ? vz : 0.f;
       mloc = row_max_last(mloc);  // the 16 lanes of row lg: max in lane 15
       const float vloc = wave_max_dpp(vz);
       if (ln == 15) cs.pmax[wi][lg] = mloc;
@@ -2459,7 +2473,8 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
   case DD:                                                                                     \
     hipLaunchKernelGGL(split_generic<DD>, dim3(n_splits, Hkv * chunks, B), dim3(kTileG), 0, s, \
                        qw, kv.kst[0], kv.knorm[0], kv.vst[0], kv.vnorm[0], t_stride, T, Hkv,   \
-                       R, Q, chunks, kbits, vbits, tb, scale, causal, split_len, po, pml);     \
+                       R, Q, chunks, kbits, vbits, tb, scale, causal, split_len, kv.klo,       \
+                       kv.khi, kv.cbase, po, pml);                                             \
     break;
     QKV_CASE(64)
     QKV_CASE(96)
@@ -2557,6 +2572,71 @@ extern "C" int qkv_attention_run(const uint8_t* kstore, const float* knorm,
                                n_splits, stream);
 }
 
+namespace {
+
+// qkv_decode_attention over the key ranges of kr (klo / khi / cbase; the
+// store pointers of kr are ignored).
+int decode_attention_impl(const void* q, int32_t q_dtype, const uint8_t* kstore,
+                          const float* knorm, const uint32_t* vstore, const float* vnorm,
+                          int64_t t_stride, int64_t T, int32_t B, int32_t Hq, int32_t Hkv,
+                          int32_t Q, int32_t d, int32_t kbits, int32_t vbits, const float* pi,
+                          const float* kcent_host, const float* vcent_host, const float* signs,
+                          float qjl_scale, float scale, int32_t causal, void* out,
+                          int32_t out_dtype, void* workspace, int64_t ws_bytes, int32_t n_splits,
+                          const KVLayers& kr, void* stream) {
+  // validate everything before the first launch
+  QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
+  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
+  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
+  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
+              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
+              (long long)T);
+  QKV_REQUIRE(kr.cbase >= 0, "causal position %lld must be >= 0", (long long)kr.cbase);
+  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
+  if (st != QKV_OK) return st;
+  QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host &&
+                  signs && out,
+              "null pointer");
+  KVLayers kv{};
+  kv.kst[0] = kstore;
+  kv.knorm[0] = knorm;
+  kv.vst[0] = vstore;
+  kv.vnorm[0] = vnorm;
+  kv.klo = kr.klo;
+  kv.khi = kr.khi;
+  kv.cbase = kr.cbase;
+  auto s = static_cast<hipStream_t>(stream);
+  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  if (use_fused(tb, d, t_stride)) {
+    QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4),
+                "pi must be 16-byte and the store 4-byte aligned");
+    QLayers ql{};
+    ql.q[0] = q;
+    ql.pi[0] = pi;
+    ql.signs[0] = signs;
+    OutLayers ol{};
+    ol.pi[0] = pi;
+    ol.out[0] = out;
+    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
+                      (d / 32) * (kbits + 1), vbits, tb,
+                      t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
+    if (st != QKV_OK || n_splits == 1) return st;
+    return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
+  }
+  QKV_REQUIRE(qkv_dtype_ok(out_dtype), "unsupported output dtype %d", out_dtype);
+  QKV_REQUIRE(qkv_aligned(pi, 16), "pi must be 16-byte aligned");
+  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
+                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
+  if (st != QKV_OK) return st;
+  st = partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
+                      scale, causal, workspace, ws_bytes, n_splits, s);
+  if (st != QKV_OK) return st;
+  return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
+                               n_splits, stream);
+}
+
+}  // namespace
+
 extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_t* kstore,
                                     const float* knorm, const uint32_t* vstore,
                                     const float* vnorm, int64_t t_stride, int64_t T, int32_t B,
@@ -2566,47 +2646,30 @@ extern "C" int qkv_decode_attention(const void* q, int32_t q_dtype, const uint8_
                                     float qjl_scale, float scale, int32_t causal, void* out,
                                     int32_t out_dtype, void* workspace, int64_t ws_bytes,
                                     int32_t n_splits, void* stream) {
-  // validate everything before the first launch
-  QKV_REQUIRE(qkv_dtype_ok(q_dtype) && qkv_dtype_ok(out_dtype), "unsupported dtype");
-  QKV_REQUIRE(qkv_bits_ok(kbits) && qkv_bits_ok(vbits), "bits must be in {1, 2, 3, 4}");
-  QKV_REQUIRE(T > 0, "No compressed KV blocks in cache. Call append() first.");
-  QKV_REQUIRE(t_stride >= T && t_stride % 32 == 0,
-              "t_stride %lld must be >= T %lld and a multiple of 32", (long long)t_stride,
-              (long long)T);
-  int st = validate_common(B, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
-  if (st != QKV_OK) return st;
-  QKV_REQUIRE(q && kstore && knorm && vstore && vnorm && pi && kcent_host && vcent_host &&
-                  signs && out,
-              "null pointer");
-  const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  if (use_fused(tb, d, t_stride)) {
-    QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4),
-                "pi must be 16-byte and the store 4-byte aligned");
-    QLayers ql{};
-    ql.q[0] = q;
-    ql.pi[0] = pi;
-    ql.signs[0] = signs;
-    KVLayers kv{};
-    kv.kst[0] = kstore;
-    kv.knorm[0] = knorm;
-    kv.vst[0] = vstore;
-    kv.vnorm[0] = vnorm;
-    OutLayers ol{};
-    ol.pi[0] = pi;
-    ol.out[0] = out;
-    auto s = static_cast<hipStream_t>(stream);
-    st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
-                      (d / 32) * (kbits + 1), vbits, tb,
-                      t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
-    if (st != QKV_OK || n_splits == 1) return st;
-    return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
-  }
-  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
-                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
-  if (st != QKV_OK) return st;
-  return qkv_attention_run(kstore, knorm, vstore, vnorm, t_stride, T, B, Hq, Hkv, Q, d, kbits,
-                           vbits, pi, kcent_host, vcent_host, scale, causal, out, out_dtype,
-                           workspace, ws_bytes, n_splits, stream);
+  return decode_attention_impl(q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq,
+                               Hkv, Q, d, kbits, vbits, pi, kcent_host, vcent_host, signs,
+                               qjl_scale, scale, causal, out, out_dtype, workspace, ws_bytes,
+                               n_splits, KVLayers{}, stream);
+}
+
+extern "C" int qkv_decode_attention_ranges(
+    const void* q, int32_t q_dtype, const uint8_t* kstore, const float* knorm,
+    const uint32_t* vstore, const float* vnorm, int64_t t_stride, int64_t T,
+    const int32_t* kv_start, const int32_t* kv_end, int64_t q_end, int32_t B, int32_t Hq,
+    int32_t Hkv, int32_t Q, int32_t d, int32_t kbits, int32_t vbits, const float* pi,
+    const float* kcent_host, const float* vcent_host, const float* signs, float qjl_scale,
+    float scale, int32_t causal, void* out, int32_t out_dtype, void* workspace, int64_t ws_bytes,
+    int32_t n_splits, void* stream) {
+  QKV_REQUIRE(kv_start == nullptr || qkv_aligned(kv_start, 4), "kv_start must be 4-byte aligned");
+  QKV_REQUIRE(kv_end == nullptr || qkv_aligned(kv_end, 4), "kv_end must be 4-byte aligned");
+  KVLayers kr{};
+  kr.klo = kv_start;
+  kr.khi = kv_end;
+  kr.cbase = q_end;
+  return decode_attention_impl(q, q_dtype, kstore, knorm, vstore, vnorm, t_stride, T, B, Hq,
+                               Hkv, Q, d, kbits, vbits, pi, kcent_host, vcent_host, signs,
+                               qjl_scale, scale, causal, out, out_dtype, workspace, ws_bytes,
+                               n_splits, kr, stream);
 }
 
 // ------------------------------------------------------------ no-allocation variant

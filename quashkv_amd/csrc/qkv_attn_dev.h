@@ -57,7 +57,25 @@ struct KVLayers {  // the store
   int32_t plg;          // streams of t_stride rows); pages of 1 << plg tokens
   int32_t npages;       // pages in the pool: a tile on a page outside [0, npages)
                         // is read from page 0 and masked (contributes nothing)
+  // Per-sequence key ranges (nullptr: all T): sequence b attends to the keys
+  // [klo[b], khi[b]) of its T cached tokens, the rest masked like padding.
+  const int32_t* klo;
+  const int32_t* khi;
+  int64_t cbase;        // causal: query i sits at cbase - Q + i (0: at khi[b] - Q + i)
 };
+
+// The key range and causal position of sequence b (every layer shares them).
+struct SeqRange {
+  int64_t lo, hi;  // attended keys [lo, hi)
+  int64_t cpos;    // causal: query i at cpos - Q + i sees keys t <= cpos - Q + i
+};
+__device__ __forceinline__ SeqRange seq_range(const KVLayers& kv, int64_t b, int64_t T) {
+  SeqRange r;
+  r.lo = kv.klo ? max<int64_t>(0, kv.klo[b]) : 0;
+  r.hi = kv.khi ? min<int64_t>(T, kv.khi[b]) : T;
+  r.cpos = kv.cbase > 0 ? kv.cbase : r.hi;
+  return r;
+}
 struct OutLayers {  // un-rotation and output
   const float* pi[kMaxLayers];
   void* out[kMaxLayers];

@@ -326,12 +326,19 @@ class QuashKVEngine:
     # ------------------------------------------------------------ attention
 
     def attention(self, queries: torch.Tensor, scale: Optional[float] = None,
-                  causal: bool = False, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+                  causal: bool = False, out_dtype: torch.dtype = torch.float32, *,
+                  kv_start: Optional[torch.Tensor] = None, kv_end: Optional[torch.Tensor] = None,
+                  q_end: int = 0) -> torch.Tensor:
         """Attention of (B, Hq, Q, d) queries over the whole compressed cache.
 
         Same result as quashkv/engine.py:204-299 (scores in the rotated domain,
         softmax over all cached tokens, values un-rotated), computed by the
-        split-K HIP kernels.  Hq may be a multiple of the cached heads (GQA)."""
+        split-K HIP kernels.  Hq may be a multiple of the cached heads (GQA).
+
+        Beyond the reference: ``kv_start`` / ``kv_end`` ((B,) int tensors)
+        restrict sequence b to the cached keys [kv_start[b], kv_end[b]) -- the
+        padding of a batch -- and with ``causal`` a ``q_end`` > 0 places query
+        i at position q_end - Q + i instead of at the end of the cache."""
         if not self._blocks or self._total_tokens == 0:
             raise ValueError("No compressed KV blocks in cache. Call append() first.")
         st = self._store
@@ -347,7 +354,10 @@ class QuashKVEngine:
         if self._workspace is None or self._workspace.numel() < need \
                 or self._workspace.device != queries.device:
             self._workspace = torch.empty(max(need, 256), dtype=torch.uint8, device=queries.device)
+        ranged = kv_start is not None or kv_end is not None or q_end != 0
         if self._kmix:
+            if ranged:
+                raise ValueError("key ranges are not supported with mixed-precision keys")
             _, pi_perm, n_out, (oc, rc, _, _, _) = self._kmix_setup()
             return attention_store_kmixed(
                 queries, st, self._total_tokens, pi_perm, n_out, oc, rc, vq.Pi,
@@ -362,7 +372,8 @@ class QuashKVEngine:
         return attention_store(
             queries, st, self._total_tokens, kq.mse_quantizer.Pi, kc, vc, kq.S,
             kq.qjl_scale, scale=scale, causal=causal, out_dtype=out_dtype,
-            workspace=self._workspace, n_splits=splits)
+            workspace=self._workspace, n_splits=splits, kv_start=kv_start, kv_end=kv_end,
+            q_end=q_end)
 
     # -------------------------------------------------------------- metrics
 

@@ -18,8 +18,11 @@ registered attention function calls ``engine.attention`` on the layer's
 whole cache: scores from the IP keys (MSE codes + QJL bits) as
 QuashKVEngine.attention computes them (quashkv/engine.py:204-299), causal
 over the cache positions when a call brings several queries, GQA by kv-head
-sharing.  Attention masks are not applied beyond that (unpadded batches);
-the engine's shape and dtype checks raise as usual.
+sharing.  A padded batch (HF's 2-D padding mask, left-padded as batched
+generate makes it) becomes per-sequence key ranges [first kept, last kept + 1)
+that the kernel masks, as the reference's HF attention masks its
+reconstructed keys; padding must be a prefix and/or suffix of each row (a
+mask with holes raises).  The engine's shape and dtype checks raise as usual.
 """
 
 from __future__ import annotations
@@ -119,6 +122,14 @@ class QuashKVHFCache(Cache):
         return cls(num_layers, head_dim, config=config, device=device)
 
 
+class KVRanges:
+    """Per-sequence key ranges of a padded batch: sequence b attends to the
+    cached keys [start[b], end[b]) ((B,) int32 device tensors)."""
+
+    def __init__(self, start: torch.Tensor, end: torch.Tensor):
+        self.start, self.end = start, end
+
+
 def quashkv_attention(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                       attention_mask: Optional[torch.Tensor], scaling: Optional[float] = None,
                       dropout: float = 0.0, **kwargs):
@@ -130,29 +141,44 @@ def quashkv_attention(module, query: torch.Tensor, key: torch.Tensor, value: tor
                          "as past_key_values")
     if dropout:
         raise ValueError("quashkv attention has no dropout (inference only)")
-    out = layer.engine.attention(query, scale=scaling, causal=query.shape[2] > 1,
-                                 out_dtype=query.dtype)
+    causal = query.shape[2] > 1
+    if isinstance(attention_mask, KVRanges):
+        eng = layer.engine
+        out = eng.attention(query, scale=scaling, causal=causal, out_dtype=query.dtype,
+                            kv_start=attention_mask.start, kv_end=attention_mask.end,
+                            q_end=eng.total_tokens if causal else 0)
+    else:
+        out = layer.engine.attention(query, scale=scaling, causal=causal, out_dtype=query.dtype)
     return out.transpose(1, 2).contiguous(), None
 
 
-def _no_mask(*args, attention_mask: Optional[torch.Tensor] = None, **kwargs):
-    """The fused kernel masks causally itself; no mask tensor is built.
+def _range_mask(*args, attention_mask: Optional[torch.Tensor] = None, **kwargs):
+    """The fused kernel masks causally itself, so no mask tensor is built.
 
-    The kernel attends every cached token of a sequence, so a batch with padded
-    positions (a 2-D padding mask holding any zero / False, as left-padded
-    batched generation passes) is refused rather than attended through."""
-    if attention_mask is not None and attention_mask.dim() == 2 and attention_mask.numel() > 0:
-        if not bool(attention_mask.bool().all()):
-            raise ValueError(
-                f"attn_implementation={ATTN_IMPLEMENTATION!r} runs unpadded batches only: the "
-                "attention mask pads some positions (batch sequences of one length, or one "
-                "sequence per call)")
-    return None
+    A 2-D padding mask with padded positions (any False, as left-padded
+    batched generation passes) becomes per-sequence key ranges: each row must
+    keep one contiguous run of positions [start, end) (padding before and/or
+    after it); a row with holes raises ValueError."""
+    if attention_mask is None or attention_mask.dim() != 2 or attention_mask.numel() == 0:
+        return None
+    m = attention_mask.bool()
+    if bool(m.all()):
+        return None
+    n = m.shape[1]
+    kept = m.sum(dim=1)
+    start = torch.where(kept > 0, m.int().argmax(dim=1), torch.zeros_like(kept))
+    pos = torch.arange(n, device=m.device)
+    runs = (pos[None, :] >= start[:, None]) & (pos[None, :] < (start + kept)[:, None])
+    if not bool((runs == m).all()):
+        raise ValueError(
+            f"attn_implementation={ATTN_IMPLEMENTATION!r} masks padding before and after each "
+            "sequence; this attention mask has holes inside a sequence")
+    return KVRanges(start.to(torch.int32), (start + kept).to(torch.int32))
 
 
 def register() -> None:
     AttentionInterface.register(ATTN_IMPLEMENTATION, quashkv_attention)
-    AttentionMaskInterface.register(ATTN_IMPLEMENTATION, _no_mask)
+    AttentionMaskInterface.register(ATTN_IMPLEMENTATION, _range_mask)
 
 
 register()

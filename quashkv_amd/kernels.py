@@ -112,11 +112,16 @@ def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Ten
                     S: torch.Tensor, qjl_scale: float, scale: Optional[float] = None,
                     causal: bool = False, out_dtype: torch.dtype = torch.float32,
                     workspace: Optional[torch.Tensor] = None,
-                    n_splits: Optional[int] = None) -> torch.Tensor:
+                    n_splits: Optional[int] = None, kv_start: Optional[torch.Tensor] = None,
+                    kv_end: Optional[torch.Tensor] = None, q_end: int = 0) -> torch.Tensor:
     """Decode attention of (B, Hq, Q, d) queries over the first T tokens of a
     cache store.  ``key_centroids`` / ``val_centroids`` are the codebook values
     (host floats, or ``_native.HostFloats`` tables a caller keeps).  Returns
-    (B, Hq, Q, d) in ``out_dtype``."""
+    (B, Hq, Q, d) in ``out_dtype``.
+
+    ``kv_start`` / ``kv_end`` (B,) int32 on the device restrict sequence b to
+    the keys [kv_start[b], kv_end[b]) (padding); with ``causal``, query i sits
+    at ``q_end - Q + i`` when ``q_end > 0``, else at kv_end[b] - Q + i."""
     dev = N.require_gpu(queries, store.kst, Pi, what="attention")
     B, Hq, Q, d = queries.shape
     Hkv = store.H
@@ -142,12 +147,29 @@ def attention_store(queries: torch.Tensor, store: KVStore, T: int, Pi: torch.Ten
     kc = key_centroids if isinstance(key_centroids, N.HostFloats) else N.HostFloats(key_centroids)
     vc = val_centroids if isinstance(val_centroids, N.HostFloats) else N.HostFloats(val_centroids)
     out = torch.empty(B, Hq, Q, d, dtype=out_dtype, device=dev)
-    N.check(L.qkv_decode_attention(
+    if kv_start is None and kv_end is None and q_end == 0:
+        N.check(L.qkv_decode_attention(
+            q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
+            store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
+            store.mbits, store.vbits, Pi.data_ptr(), kc.ptr, vc.ptr, S.data_ptr(),
+            float(qjl_scale), float(scale), 1 if causal else 0, out.data_ptr(),
+            N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(), n_splits,
+            N.stream(dev)))
+        return out
+    rng = []
+    for t in (kv_start, kv_end):
+        if t is not None:
+            t = t.to(device=dev, dtype=torch.int32).contiguous()
+            if t.numel() != B:
+                raise ValueError(f"key ranges need one entry per sequence ({B}), got {t.numel()}")
+        rng.append(t)
+    N.check(L.qkv_decode_attention_ranges(
         q.data_ptr(), N.dtype_code(q.dtype), store.kst.data_ptr(), store.knorm.data_ptr(),
-        store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, B, Hq, Hkv, Q, d,
-        store.mbits, store.vbits, Pi.data_ptr(), kc.ptr, vc.ptr, S.data_ptr(), float(qjl_scale),
-        float(scale), 1 if causal else 0, out.data_ptr(), N.dtype_code(out_dtype),
-        workspace.data_ptr(), workspace.numel(), n_splits, N.stream(dev)))
+        store.vst.data_ptr(), store.vnorm.data_ptr(), store.capacity, T, N.ptr(rng[0]),
+        N.ptr(rng[1]), int(q_end), B, Hq, Hkv, Q, d, store.mbits, store.vbits, Pi.data_ptr(),
+        kc.ptr, vc.ptr, S.data_ptr(), float(qjl_scale), float(scale), 1 if causal else 0,
+        out.data_ptr(), N.dtype_code(out_dtype), workspace.data_ptr(), workspace.numel(),
+        n_splits, N.stream(dev)))
     return out
 
 
@@ -394,17 +416,14 @@ def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[Compressed
     Blocks hold one uint8 per code, as in the reference.  They are packed once
     into a cache store and attended by the decode kernels.  Query heads may be
     a multiple of the blocks' kv heads (GQA).  With ``causal``, query i sits at
-    position T - Q + i of the T cached tokens; ``total_kv_tokens`` may be 0 or
-    T (any other offset raises ValueError)."""
+    position total_kv_tokens - Q + i and sees the keys at positions <= it
+    (quashkv/triton_kernels/attention.py:118-121); total_kv_tokens = 0, the
+    default, places it at T - Q + i for the T cached tokens (the reference
+    would mask every key then)."""
     if not blocks:
         raise ValueError("No compressed KV blocks in cache. Call append() first.")
-    # causal masking puts query i at position total_kv_tokens - Q + i
-    # (quashkv/triton_kernels/attention.py:118-121); the kernels place it at
-    # T - Q + i for the T cached tokens, so other offsets are refused
-    n_kv = sum(int(b.seq_len) for b in blocks)
-    if causal and total_kv_tokens not in (0, n_kv):
-        raise ValueError(f"causal attention places the queries at the end of the {n_kv} cached "
-                         f"tokens; total_kv_tokens={total_kv_tokens} is not supported")
+    if total_kv_tokens < 0:
+        raise ValueError(f"total_kv_tokens must be >= 0, got {total_kv_tokens}")
     N.require_gpu(queries, Pi, what="fused_quantized_attention")
     kc = torch.cat([b.mse_indices for b in blocks], dim=2)
     kq = torch.cat([b.qjl_signs for b in blocks], dim=2)
@@ -415,4 +434,5 @@ def fused_quantized_attention(queries: torch.Tensor, blocks: Sequence[Compressed
     st = store_from_codes(kc, kq, kn, vc, vn, _bits_of(key_centroids), _bits_of(val_centroids))
     kh = key_centroids.detach().float().cpu().tolist()
     vh = val_centroids.detach().float().cpu().tolist()
-    return attention_store(queries, st, T, Pi, kh, vh, S, qjl_scale, scale=scale, causal=causal)
+    return attention_store(queries, st, T, Pi, kh, vh, S, qjl_scale, scale=scale, causal=causal,
+                           q_end=int(total_kv_tokens) if causal else 0)
