@@ -315,8 +315,9 @@ int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
 int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv,
                                       int32_t Q, int32_t d, int32_t n_splits);
 
-/* 1 if a call with these parameters runs the MFMA kernel, 0 for the VALU
- * kernel, -1 for invalid arguments. */
+/* 1 if a call with these parameters runs an MFMA kernel (symmetric codebooks,
+ * key MSE bits <= 3, t_stride a multiple of 64), 0 for the VALU kernel, -1
+ * for invalid arguments. */
 int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
                            const float* kcent_host, const float* vcent_host,
                            int64_t t_stride, int64_t T, int32_t n_splits);
@@ -640,7 +641,7 @@ int qkv_paged_store_append_kv(int32_t in_dtype, const void* keys, const void* va
                               int64_t t0, void* stream);
 
 /* qkv_decode_attention over a paged store of T tokens per sequence (the MFMA
- * path: symmetric codebooks, key MSE bits <= 2, d = 64 or 128; returns
+ * path: symmetric codebooks, key MSE bits <= 3, d = 64 or 128; returns
  * QKV_E_UNSUPPORTED otherwise).  Same arguments as qkv_decode_attention with
  * (kpool, knorm, vpool, vnorm, page_table, pages_per_seq, page_tokens) for the
  * store. */

@@ -2314,7 +2314,7 @@ extern "C" int32_t qkv_attention_path(int32_t d, int32_t kbits, int32_t vbits,
   if (!kcent_host || !vcent_host || !qkv_bits_ok(kbits) || !qkv_bits_ok(vbits) || n_splits < 1)
     return -1;
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  return use_mfma_path(tb, d, t_stride, T, n_splits) ? 1 : 0;
+  return use_fused(tb, d, t_stride) || use_mfma_path(tb, d, t_stride, T, n_splits) ? 1 : 0;
 }
 
 // prepare for nl layers (B sequences each; the workspace holds B * nl)
@@ -2766,12 +2766,9 @@ extern "C" int qkv_paged_decode_attention(
                   out,
               "null pointer");
   const int64_t t_stride = int64_t(pages_per_seq) << plg;
-  if (d == 96 || !use_mfma_path(make_tables(kcent_host, kbits, vcent_host, vbits), d,
-                                t_stride, T, n_splits)) {
+  if (d == 96 || !use_fused(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride)) {
     qkv_set_error("paged stores decode on the MFMA path only (d = 128 or 64, symmetric "
-                  "codebooks, key MSE bits <= 3 at d = 128 and <= 2 at d = 64 with splits of "
-                  "at most %d tokens)",
-                  kSplitMax);
+                  "codebooks, key MSE bits <= 3)");
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(qkv_dtype_ok(out_dtype) && qkv_aligned(pi, 16), "pi must be 16-byte aligned");
@@ -2844,10 +2841,14 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   int st = validate_common(B * n_layers, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  if (!use_mfma_path(tb, d, t_stride, T, n_splits)) {
+  // d = 64 batches run the split path (its two row chunks per workgroup read a
+  // 5-8-row GQA group's K/V once) where it takes the shape (key MSE bits <= 2,
+  // splits of at most kSplitMax tokens), decode_fused otherwise, as every
+  // other head dim
+  const bool split64 = d == 64 && use_mfma(tb, d, t_stride, T, n_splits);
+  if (!split64 && !use_fused(tb, d, t_stride)) {
     qkv_set_error("layer-batched decode runs on the MFMA path (symmetric codebooks, key MSE "
-                  "bits <= 3 at head_dim 128 and <= 2 at 64, capacity a multiple of 64, "
-                  "splits of at most %d tokens)", kSplitMax);
+                  "bits <= 3, capacity a multiple of 64)");
     return QKV_E_UNSUPPORTED;
   }
   QLayers ql{};
@@ -2869,7 +2870,7 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.plg = plg;
   kv.npages = num_pages;
   auto s = static_cast<hipStream_t>(stream);
-  if (d == 128) {
+  if (!split64) {
     st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
                       (d / 32) * (kbits + 1), vbits, tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);

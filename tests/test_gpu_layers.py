@@ -28,12 +28,16 @@ def _close(a, b, rel):
     assert err <= rel, err
 
 
-@pytest.mark.parametrize("d,G,Qn,causal", [(64, 7, 1, False), (128, 4, 1, False),
-                                            (128, 2, 3, True)])
-def test_layers_match_per_layer_and_oracle(d, G, Qn, causal):
-    gen = torch.Generator().manual_seed(d + G)
+@pytest.mark.parametrize("d,G,Qn,causal,kb", [
+    (64, 7, 1, False, 3), (128, 4, 1, False, 3), (128, 2, 3, True, 3),
+    (64, 7, 1, False, 4),       # 3-bit key MSE at d = 64: decode_fused (parity plane)
+    (64, 2, 3, True, 4),
+    (96, 4, 1, False, 3), (96, 2, 3, True, 4)])
+def test_layers_match_per_layer_and_oracle(d, G, Qn, causal, kb):
+    gen = torch.Generator().manual_seed(d + G + kb)
     n, B, Hkv, T = 5, 3, 2, 700
-    engines = [Q.QuashKVEngine(head_dim=d, seed=42 + l, device=DEV) for l in range(n)]
+    engines = [Q.QuashKVEngine(head_dim=d, key_bits=kb, seed=42 + l, device=DEV)
+               for l in range(n)]
     for e in engines:
         k = torch.randn(B, Hkv, T, d, generator=gen) * torch.exp(0.5 * torch.randn(B, Hkv, T, 1, generator=gen))
         v = torch.randn(B, Hkv, T, d, generator=gen)
@@ -49,10 +53,10 @@ def test_layers_match_per_layer_and_oracle(d, G, Qn, causal):
         ref = K.attention_store(q, st, T, kq.mse_quantizer.Pi, kq.mse_quantizer.codebook.centroids_host,
                                 vq.codebook.centroids_host, kq.S, kq.qjl_scale, causal=causal,
                                 n_splits=ns)
-        # at d = 64 the batch runs split_mfma (exact integer scores) and the
-        # single call decode_fused (fp8 query digits): both sit within 2e-5
-        # of the oracle, not bit-identical to each other
-        _close(o, ref, 1e-6 if d != 64 else 2e-5)
+        # at d = 64 with 1-2 key MSE bits the batch runs split_mfma (exact
+        # integer scores) and the single call decode_fused (fp8 query
+        # digits): both sit within 2e-5 of the oracle, not bit-identical
+        _close(o, ref, 1e-6 if d != 64 or kb == 4 else 2e-5)
     # one layer against the oracle on its stored codes
     e, q, o = engines[2], qs[2], outs[2]
     st, kq, vq = e._store, e.key_quantizer, e.value_quantizer

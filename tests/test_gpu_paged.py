@@ -85,7 +85,7 @@ def _close(got, ref):
 @pytest.mark.parametrize("page_tokens", [64, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("d,key_bits,value_bits", [
-    (d, kb, vb) for d in (64, 128) for kb, vb in ((3, 3), (2, 4))] + [(128, 4, 3)])
+    (d, kb, vb) for d in (64, 128) for kb, vb in ((3, 3), (2, 4))] + [(128, 4, 3), (64, 4, 3)])
 def test_paged_matches_contiguous(d, dtype, key_bits, value_bits, page_tokens):
     B, H, G = 3, 2, 4
     seed = d + key_bits * 10 + value_bits
@@ -337,3 +337,57 @@ def test_paged_kv_append_equals_two_calls(d, dtype, key_bits, value_bits, shape)
         vb2[:, :, -1] &= (1 << (t0 % 32)) - 1
     assert torch.equal(va, vb2)
     assert ga.knorm[:, :, :t0].abs().min() > 0
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("shape", ["few", "many"])
+def test_paged_kv_append_skips_pages_off_the_pool(d, shape):
+    """qkv_paged_store_append_kv never writes through page-table entries
+    outside the pool (-1 or >= num_pages): with such entries in the table,
+    every pool page that no valid entry names keeps its bytes, keys and values
+    and both norms, in the wave-per-block (few tiles) and wave-per-tile (many
+    tiles) modes; the pages the valid entries name are written."""
+    (B, H), sizes = ((2, 3), (1, 5, 37, 64, 1)) if shape == "few" else ((8, 8), (160, 7))
+    dev = torch.device(DEV)
+    kq = Q.InnerProductQuantizer(d, 3, seed=7, device=DEV)
+    vq = Q.MSEQuantizer(d, 3, seed=8, device=DEV)
+    mq = kq.mse_quantizer
+    kc = N.HostFloats(mq.codebook.centroids_host)
+    kb = N.HostFloats(mq.codebook.boundaries_host)
+    vb = N.HostFloats(vq.codebook.boundaries_host)
+    total = sum(sizes)
+    st = PagedKVStore(B, H, d, 2, 3, B * 8 + 5, dev, 64)
+    st.ensure(total)
+    g = torch.Generator().manual_seed(12)
+    per = st.table.shape[1]
+    tab = torch.randperm(st.num_pages, generator=g)[:B * per].view(B, per).to(torch.int32)
+    tab[0, 1] = -1                      # off the pool, both ways
+    tab[1, 0] = st.num_pages
+    tab[B - 1, per - 1] = st.num_pages + 7
+    st.table = tab.to(dev)
+    for t in (st.kpool, st.vpool):      # sentinel contents
+        t.copy_(torch.randint(0, 255, t.shape, generator=g, dtype=torch.int32).to(t.dtype).to(dev))
+    for t in (st.knorm, st.vnorm):
+        t.copy_(torch.randn(t.shape, generator=g).to(dev))
+    before = [t.clone() for t in (st.kpool, st.knorm, st.vpool, st.vnorm)]
+    L = N.lib()
+    stream = N.stream(dev)
+    t0 = 0
+    for S in sizes:
+        k = torch.randn(B, H, S, d, generator=g).to(torch.bfloat16).to(DEV)
+        v = torch.randn(B, H, S, d, generator=g).to(torch.bfloat16).to(DEV)
+        N.check(L.qkv_paged_store_append_kv(
+            N.QKV_BF16, k.data_ptr(), v.data_ptr(), B, H, S, d, 2, 3, mq.Pi.data_ptr(),
+            kq.S.data_ptr(), vq.Pi.data_ptr(), kc.ptr, kb.ptr, vb.ptr, st.kpool.data_ptr(),
+            st.knorm.data_ptr(), st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(),
+            per, st.pt, st.num_pages, t0, stream))
+        t0 += S
+    torch.cuda.synchronize()
+    used = sorted({int(p) for p in tab.flatten() if 0 <= int(p) < st.num_pages})
+    untouched = [p for p in range(st.num_pages) if p not in used]
+    assert untouched and used
+    for a, b0 in zip((st.kpool, st.knorm, st.vpool, st.vnorm), before):
+        assert torch.equal(a[untouched], b0[untouched])
+    # the first token's page of sequence 0 (a valid entry) was written
+    p0 = int(tab[0, 0])
+    assert not torch.equal(st.knorm[p0], before[1][p0])

@@ -274,7 +274,8 @@ def test_attention_path_selection():
     v64 = N.HostFloats(LloydMaxCodebook(64, 3).centroids_host)
     assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 2048, 2048, 2) == 1
     assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 2048, 2048, 1) == 1
-    assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 4096, 4096, 1) == 0   # split > 2048
+    assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 4096, 4096, 1) == 1   # fused: any split
+    assert lib.qkv_attention_path(64, 2, 3, k64.ptr, v64.ptr, 4064, 4000, 1) == 0   # stride % 64
     for vb in (1, 2, 4):
         v = N.HostFloats(LloydMaxCodebook(128, vb).centroids_host)
         assert lib.qkv_attention_path(128, 2, vb, kc.ptr, v.ptr, 256, 256, 1) == 1
@@ -283,7 +284,7 @@ def test_attention_path_selection():
     k3 = N.HostFloats(LloydMaxCodebook(128, 3).centroids_host)
     assert lib.qkv_attention_path(128, 3, 3, k3.ptr, vc.ptr, 256, 256, 1) == 1   # parity plane
     k3_64 = N.HostFloats(LloydMaxCodebook(64, 3).centroids_host)
-    assert lib.qkv_attention_path(64, 3, 3, k3_64.ptr, v64.ptr, 256, 256, 1) == 0
+    assert lib.qkv_attention_path(64, 3, 3, k3_64.ptr, v64.ptr, 256, 256, 1) == 1   # parity plane
     asym = N.HostFloats([-1.0, -0.25, 0.5, 1.0])
     assert lib.qkv_attention_path(128, 2, 3, asym.ptr, vc.ptr, 256, 256, 1) == 0
 

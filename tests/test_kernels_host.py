@@ -13,16 +13,15 @@ def _blocks(n):
     return [CompressedBlock(z, z, f, z, f, n)]
 
 
-def test_causal_total_kv_tokens_must_be_the_cache_length():
+def test_causal_total_kv_tokens_is_any_position():
     q = torch.zeros(1, 1, 2, 8)
     blocks = _blocks(5) + _blocks(3)
     args = (q, blocks, torch.eye(8), torch.zeros(4), torch.zeros(8), torch.ones(8), 0.1)
-    with pytest.raises(ValueError, match="total_kv_tokens=6"):
-        fused_quantized_attention(*args, causal=True, total_kv_tokens=6)
-    # 0 and the cache length (8) pass the check and reach the device check
-    for tk in (0, 8):
+    with pytest.raises(ValueError, match="total_kv_tokens must be >= 0"):
+        fused_quantized_attention(*args, causal=True, total_kv_tokens=-1)
+    # any offset (0: the cache length) passes the check and reaches the device check
+    for tk in (0, 6, 8, 11):
         with pytest.raises(RuntimeError, match="GPU"):
             fused_quantized_attention(*args, causal=True, total_kv_tokens=tk)
-    # non-causal calls ignore the offset, as the reference does
     with pytest.raises(RuntimeError, match="GPU"):
         fused_quantized_attention(*args, causal=False, total_kv_tokens=6)

@@ -26,12 +26,14 @@ def test_page_manager_init_and_store_choice():
     pm = QuashKVPageManager(num_kv_heads=4, head_size=64, config=QuashKVPageConfig(), device=CPU)
     assert pm.total_tokens == 0 and pm.num_kv_heads == 4 and pm.head_size == 64
     assert pm.paged and isinstance(pm.engine, PagedQuashKVEngine)
-    # head_dim 96, and 3-bit MSE keys (key_bits 4) at head_dim 64, stay on the
-    # contiguous store
-    for hs, kb in ((64, 4), (96, 3)):
-        pm = QuashKVPageManager(num_kv_heads=2, head_size=hs,
-                                config=QuashKVPageConfig(key_bits=kb), device=CPU)
-        assert not pm.paged and type(pm.engine) is QuashKVEngine
+    # 3-bit MSE keys (key_bits 4) at head_dim 64 are paged; head_dim 96 stays
+    # on the contiguous store
+    pm = QuashKVPageManager(num_kv_heads=2, head_size=64, config=QuashKVPageConfig(key_bits=4),
+                            device=CPU)
+    assert pm.paged and isinstance(pm.engine, PagedQuashKVEngine)
+    pm = QuashKVPageManager(num_kv_heads=2, head_size=96, config=QuashKVPageConfig(key_bits=3),
+                            device=CPU)
+    assert not pm.paged and type(pm.engine) is QuashKVEngine
 
 
 def test_block_size_must_divide_page():
@@ -81,4 +83,4 @@ def test_no_vllm_raises():
 
 def test_paged_engine_rejects_uncovered_config():
     with pytest.raises(ValueError, match="paged cache"):
-        PagedQuashKVEngine(head_dim=64, key_bits=4, device=CPU)
+        PagedQuashKVEngine(head_dim=96, key_bits=3, device=CPU)
