@@ -129,7 +129,7 @@ int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
  * n or out_group_stride = out_seq; grouped layouts: QKV_E_UNSUPPORTED), for the
  * same reference operators (quashkv/quantizer.py:113-131, 211-242,
  * quashkv/triton_kernels/compress.py:210-303): the rotation, search and tie
- * rules of qkv_store_append.  d = 128 or 64; cent_host / bound_host are HOST
+ * rules of qkv_store_append.  d = 128, 96 or 64; cent_host / bound_host are HOST
  * copies of the codebook (2^bits centroids, 2^bits - 1 boundaries), which
  * must be symmetric about 0 (else QKV_E_UNSUPPORTED, as for other d or bits
  * beyond 1..3 (IP) / 1..4 (MSE)); x and pi 16-byte aligned. */
@@ -230,7 +230,7 @@ int qkv_vtiles_pack(const uint8_t* codes, int64_t groups, int64_t S, int32_t d,
  * 211-242, MSEQuantizer.compress for values, quashkv/quantizer.py:113-131).
  *   in_dtype   QKV_BF16, QKV_F16 or QKV_F32 (fp32 rows are divided by their
  *              norm first and split into fp16 hi + lo for the fp16 MFMA)
- *   keys, values  groups x S x d rows (d = 128 or 64), 16-byte aligned;
+ *   keys, values  groups x S x d rows (d = 128, 96 or 64), 16-byte aligned;
  *              either may be NULL to append only the other
  *   mbits      key MSE bits (1..3; key total bits - 1), vbits value bits (1..4)
  *   kcent_host, kbound_host  HOST arrays of the key MSE codebook (2^mbits

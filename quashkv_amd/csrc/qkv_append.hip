@@ -83,8 +83,8 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
                 "[%lld, %lld)", pg.pmax, 1 << pg.lg, (long long)t0, (long long)(t0 + S));
   }
   QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
-  if (d != 128 && d != 64) {
-    qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
+  if (d != 128 && d != 96 && d != 64) {
+    qkv_set_error("store append runs on head_dim 128, 96 or 64 (got %d)", d);
     return QKV_E_UNSUPPORTED;
   }
   const int in_align = rotated ? 4 : 16;
@@ -182,6 +182,8 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   }
     if (d == 128) {
       QKV_KD(128)
+    } else if (d == 96) {
+      QKV_KD(96)
     } else {
       QKV_KD(64)
     }
@@ -223,6 +225,8 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
   }
     if (d == 128) {
       QKV_VD(128)
+    } else if (d == 96) {
+      QKV_VD(96)
     } else {
       QKV_VD(64)
     }
@@ -253,8 +257,8 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
               "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
   QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
-  if (d != 128 && d != 64) {
-    qkv_set_error("store append runs on head_dim 128 or 64 (got %d)", d);
+  if (d != 128 && d != 96 && d != 64) {
+    qkv_set_error("store append runs on head_dim 128, 96 or 64 (got %d)", d);
     return QKV_E_UNSUPPORTED;
   }
   if (mbits < 1 || mbits > 3) {
@@ -332,6 +336,8 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
   }
     if (d == 128) {
       QKV_KD(128)
+    } else if (d == 96) {
+      QKV_KD(96)
     } else {
       QKV_KD(64)
     }
@@ -363,6 +369,8 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
   }
     if (d == 128) {
       QKV_VD(128)
+    } else if (d == 96) {
+      QKV_VD(96)
     } else {
       QKV_VD(64)
     }
@@ -676,8 +684,8 @@ extern "C" int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, 
   QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);
   QKV_REQUIRE(n >= 0, "negative row count");
   const bool ip = mode == QKV_MODE_IP;
-  if ((d != 128 && d != 64) || bits < 1 || bits > (ip ? 3 : 4)) {
-    qkv_set_error("MFMA compress runs on head_dim 128 or 64 with %s bits in 1..%d",
+  if ((d != 128 && d != 96 && d != 64) || bits < 1 || bits > (ip ? 3 : 4)) {
+    qkv_set_error("MFMA compress runs on head_dim 128, 96 or 64 with %s bits in 1..%d",
                   ip ? "key MSE" : "value", ip ? 3 : 4);
     return QKV_E_UNSUPPORTED;
   }
@@ -740,6 +748,8 @@ extern "C" int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, 
   } while (0)
   if (d == 128)
     QKV_CD(128);
+  else if (d == 96)
+    QKV_CD(96);
   else
     QKV_CD(64);
 #undef QKV_CD

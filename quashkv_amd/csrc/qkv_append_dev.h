@@ -303,12 +303,12 @@ __device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* 
   // (block, k-step, lane) slots and writes both splits of each, with all of
   // its Pi loads in flight before the first conversion
   constexpr int NKS = D / 16;  // k-steps
-  constexpr int NPT = frag_n<D>() / 2 / kThreads;
-  static_assert(NPT * 2 * kThreads == frag_n<D>(), "whole slots per thread");
+  constexpr int NSLOT = frag_n<D>() / 2;
+  constexpr int NPT = (NSLOT + kThreads - 1) / kThreads;  // the last may be partial (d = 96)
   float4 p[NPT][2];
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
-    const int u = threadIdx.x + kThreads * x;
+    const int u = min(threadIdx.x + kThreads * x, NSLOT - 1);
     const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
     const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
     p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
@@ -317,6 +317,7 @@ __device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* 
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
+    if (NSLOT % kThreads != 0 && u >= NSLOT) break;
     const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
     // pscale = 2^k: the scaling is exact
     const float v[8] = {p[x][0].x * pscale, p[x][0].y * pscale, p[x][0].z * pscale,
@@ -433,8 +434,7 @@ __device__ __forceinline__ void append_k_run(
   constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
   constexpr int NKS = D / 16;         // k-steps
   constexpr int RD = NBK * L;         // dwords per row
-  constexpr int NSK = RD * kTok / 64; // staging dwords per lane
-  static_assert(RD * kTok % 64 == 0, "whole staging dwords");
+  constexpr int NSK = (RD * kTok + 63) / 64;  // staging dwords per lane (the last may be partial)
   const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
   // ONE with nsplit = NBK: wave (tile, coordinate block) = (g / NBK, g % NBK)
   // for the global wave index g, each wave computing and storing that block's
@@ -1052,8 +1052,8 @@ __device__ __forceinline__ void append_v_run(
   constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
-  constexpr int NPW = D / 64;        // staging dwords per (tile, plane)
-  constexpr int NS = NPW * VB * kHalves;  // staging dwords per lane: tiles x VB planes x D / 64
+  constexpr int NW = kHalves * VB * D;   // store words of a wave tile: [tile][plane][coordinate]
+  constexpr int NS = (NW + 63) / 64;     // staging dwords per lane (the last may be partial)
   const int lane = threadIdx.x & 63, li = lane & 31;
   const int64_t a_base = t0 & ~int64_t(31);
   // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
@@ -1206,11 +1206,13 @@ __device__ __forceinline__ void append_v_run(
       });
     });
 
-    // store: staging dword i covers tile i / (NPW VB), plane (i / NPW) % VB,
-    // coordinates 64 (i % NPW) + lane
+    // store: staging dword i of lane l is word w = 64 i + l of the tile's
+    // [tile][plane][coordinate] words
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
-      const int tau = i / (NPW * VB), k = (i / NPW) % VB, j = 64 * (i % NPW) + lane;
+      const int w = 64 * i + lane;
+      if (NW % 64 != 0 && w >= NW) continue;
+      const int tau = w / (VB * D), k = (w / D) % VB, j = w % D;
       if (split && (j >> 5) != myblk) continue;  // another wave's coordinate block
       const int64_t tok0 = A0 + 32 * tau;
       const int64_t lo = max<int64_t>(t0 - tok0, 0), hi = min<int64_t>(t0 + S - tok0, 32);

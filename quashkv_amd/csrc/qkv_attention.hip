@@ -2171,15 +2171,18 @@ int launch_fused(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int
     else                            \
       QKV_FU2(RW, VB, false);       \
   } while (0)
-  // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) and
-  // 96-dim rows have no paged store
-  QKV_REQUIRE((rdw % 4 == 0 && d == 128) || d == 64 || kv.ptab == nullptr,
-              "mixed keys and head_dim 96 are not paged");
+  // the mixed-key formats (9 and 10 dwords; 12 shares the IP code) have no
+  // paged store
+  QKV_REQUIRE((rdw % 4 == 0 && d == 128) || d == 64 || d == 96 || kv.ptab == nullptr,
+              "mixed keys are not paged");
 #define QKV_FUC(RW, VB)    \
   QKV_FU2(RW, VB, false);  \
   break
-#define QKV_FU96(RW, VB)              \
-  QKV_FU3(RW, VB, false, 96);         \
+#define QKV_FU96(RW, VB)                \
+  if (kv.ptab)                          \
+    QKV_FU3(RW, VB, true, 96);          \
+  else                                  \
+    QKV_FU3(RW, VB, false, 96);         \
   break
 #define QKV_FU64(RW, VB)                \
   if (kv.ptab)                          \
@@ -2766,9 +2769,9 @@ extern "C" int qkv_paged_decode_attention(
                   out,
               "null pointer");
   const int64_t t_stride = int64_t(pages_per_seq) << plg;
-  if (d == 96 || !use_fused(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride)) {
-    qkv_set_error("paged stores decode on the MFMA path only (d = 128 or 64, symmetric "
-                  "codebooks, key MSE bits <= 3)");
+  if (!use_fused(make_tables(kcent_host, kbits, vcent_host, vbits), d, t_stride)) {
+    qkv_set_error("paged stores decode on the MFMA path only (symmetric codebooks, key MSE "
+                  "bits <= 3)");
     return QKV_E_UNSUPPORTED;
   }
   QKV_REQUIRE(qkv_dtype_ok(out_dtype) && qkv_aligned(pi, 16), "pi must be 16-byte aligned");
@@ -2781,7 +2784,7 @@ extern "C" int qkv_paged_decode_attention(
   kv.pmax = pages_per_seq;
   kv.plg = plg;
   kv.npages = num_pages;
-  if (d == 128 || d == 64) {  // decode_fused, as the contiguous single call
+  {  // decode_fused, as the contiguous single call
     QLayers ql{};
     ql.q[0] = q;
     ql.pi[0] = pi;
@@ -2797,15 +2800,6 @@ extern "C" int qkv_paged_decode_attention(
     if (st != QKV_OK || n_splits == 1) return st;
     return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
   }
-  st = qkv_attention_prepare(q, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, pi, kcent_host,
-                             vcent_host, signs, qjl_scale, workspace, ws_bytes, n_splits, stream);
-  if (st != QKV_OK) return st;
-  st = partial_layers(kv, 1, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host, vcent_host,
-                      scale, causal, workspace, ws_bytes, n_splits,
-                      static_cast<hipStream_t>(stream));
-  if (st != QKV_OK) return st;
-  return qkv_attention_combine(B, Hq, Hkv, Q, d, pi, out, out_dtype, workspace, ws_bytes,
-                               n_splits, stream);
 }
 
 // One decode step over n_layers layers that share shapes, bit widths and

@@ -170,12 +170,12 @@ class QuashKVEngine:
         self._total_tokens += S
 
     def _append_fused(self, keys: torch.Tensor, values: torch.Tensor, t0: int) -> bool:
-        """bf16, fp16 or fp32 rows at head_dim 128 or 64: compress straight into
+        """bf16, fp16 or fp32 rows at head_dim 128, 96 or 64: compress straight into
         the store (qkv_store_append).  False when that kernel does not cover the
         call."""
         if (keys.dtype not in (torch.bfloat16, torch.float16, torch.float32)
                 or values.dtype != keys.dtype
-                or self.head_dim not in (64, 128) or not 2 <= self.key_bits <= 4):
+                or self.head_dim not in (64, 96, 128) or not 2 <= self.key_bits <= 4):
             return False
         B, H, S, d = keys.shape
         kq, vq = self.key_quantizer, self.value_quantizer

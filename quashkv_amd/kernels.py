@@ -288,7 +288,7 @@ class LayerBatch:
         T = e0.total_tokens
         fused = (k0.dim() == 4 and k0.is_cuda
                  and k0.dtype in (torch.bfloat16, torch.float16, torch.float32)
-                 and e0.head_dim in (64, 128) and 2 <= e0.key_bits <= 4
+                 and e0.head_dim in (64, 96, 128) and 2 <= e0.key_bits <= 4
                  and all(k.shape == k0.shape and v.shape == k0.shape and k.dtype == k0.dtype
                          and v.dtype == k0.dtype and k.device == k0.device
                          and v.device == k0.device for k, v in zip(keys, values)))

@@ -83,7 +83,7 @@ class QuashIndex:
         L = N.lib()
         stream = N.stream(dev)
         done = False
-        if (x.dtype in (torch.bfloat16, torch.float16, torch.float32) and self.dim in (64, 128)
+        if (x.dtype in (torch.bfloat16, torch.float16, torch.float32) and self.dim in (64, 96, 128)
                 and 2 <= self.bits <= 4):
             kc, kb, _ = self._host_tables()
             st = L.qkv_store_append(N.dtype_code(x.dtype), x.data_ptr(), None, 1, n, self.dim,

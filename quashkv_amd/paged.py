@@ -212,7 +212,7 @@ class PagedQuashKVEngine(QuashKVEngine):
         super().__init__(head_dim=head_dim, key_bits=key_bits, value_bits=value_bits, seed=seed,
                          device=device)
         if not self.covers(head_dim, key_bits, value_bits):
-            raise ValueError("the paged cache runs head_dim 128 or 64 with key_bits 2..4 and "
+            raise ValueError("the paged cache runs head_dim 128, 96 or 64 with key_bits 2..4 and "
                              "value_bits 1..4")
         if page_tokens not in PAGE_SIZES:
             raise ValueError(f"page_tokens {page_tokens} must be one of {PAGE_SIZES}")
@@ -222,7 +222,7 @@ class PagedQuashKVEngine(QuashKVEngine):
 
     @staticmethod
     def covers(head_dim: int, key_bits: int, value_bits: int) -> bool:
-        return head_dim in (128, 64) and key_bits in (2, 3, 4) and 1 <= value_bits <= 4
+        return head_dim in (128, 96, 64) and key_bits in (2, 3, 4) and 1 <= value_bits <= 4
 
     # -------------------------------------------------------------- storage
 

@@ -65,7 +65,7 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
                   host_tables: Optional[tuple] = None) -> None:
     """Run the fused compress, writing into caller-owned buffers.
 
-    Rows of head_dim 128 or 64 with a symmetric codebook run on the MFMA
+    Rows of head_dim 128, 96 or 64 with a symmetric codebook run on the MFMA
     compress (qkv_compress_mfma; packed outputs through the bit packer after
     it); other shapes, pre-rotated rows and asymmetric tables on the VALU
     kernel (qkv_compress).  ``host_tables`` = (centroids, boundaries) host
@@ -85,7 +85,7 @@ def compress_into(mode: int, x: torch.Tensor, pi: torch.Tensor, boundaries: torc
         N.require_extent(norms, rows * 4, "compress norms")
     pi, boundaries, centroids, signs = N.dense(pi, boundaries, centroids, signs)
     L = N.lib()
-    if (not pre_rotated and d in (64, 128) and n > 0 and xf.data_ptr() % 16 == 0
+    if (not pre_rotated and d in (64, 96, 128) and n > 0 and xf.data_ptr() % 16 == 0
             and (not packed or seq == n)):
         ip = mode == N.QKV_MODE_IP
         if host_tables is not None:

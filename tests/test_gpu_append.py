@@ -49,7 +49,7 @@ def _mismatch(a, b):
     return float((diff != 0).double().mean()), int(diff.max()) if diff.numel() else 0
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (2, 1), (4, 4), (3, 2)])
 def test_store_append_matches_unfused_path(dtype, key_bits, value_bits, d):
@@ -72,7 +72,7 @@ def test_store_append_matches_unfused_path(dtype, key_bits, value_bits, d):
         assert float(((a - b).abs() / b).max()) <= 2e-6
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_store_append_vs_oracle(dtype, d):
     """Codes and norms against the CPU restatement of compress_ip / compress_mse
@@ -203,7 +203,7 @@ def _special_rows(seed, shape, values, n_random=0):
     return torch.from_numpy(y)
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("mbits,vbits", [(1, 1), (2, 3), (3, 4), (2, 2), (1, 4), (3, 1)])
 def test_store_append_rotated_bit_exact(d, mbits, vbits):
     from quashkv_amd.store import KVStore
@@ -322,7 +322,7 @@ def _kv_stores_equal(a, b, T):
     assert torch.equal(va, vb)
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("mbits", [1, 2, 3])
 @pytest.mark.parametrize("shape", ["few", "many"])

@@ -52,7 +52,7 @@ def _bar(dtype):
     return 2e-5 if dtype == torch.float32 else 1e-4
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bits", [1, 2, 3, 4])
 def test_mse_compress_vs_oracle(d, dtype, bits):
@@ -70,7 +70,7 @@ def test_mse_compress_vs_oracle(d, dtype, bits):
     assert torch.equal(c2, codes) and torch.equal(n2, norms)
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("tb", [2, 3, 4])
 def test_ip_compress_vs_oracle(d, dtype, tb):
@@ -91,7 +91,7 @@ def test_ip_compress_vs_oracle(d, dtype, tb):
     assert torch.equal(c2, codes) and torch.equal(b2, bits) and torch.equal(n2, norms)
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_compress_equals_store_append(d, dtype):
     """The quantizer-API kernel and the fused store append share the rotation
@@ -140,7 +140,7 @@ def test_compress_grouped_and_packed_outputs():
     assert torch.equal(pn, dense_n)
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 def test_index_add_fp32_vs_oracle(d):
     """QuashIndex.add of fp32 rows (the fused append into the index's K rows)
     against the oracle's compress_ip of the same rows."""

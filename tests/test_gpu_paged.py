@@ -85,7 +85,8 @@ def _close(got, ref):
 @pytest.mark.parametrize("page_tokens", [64, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("d,key_bits,value_bits", [
-    (d, kb, vb) for d in (64, 128) for kb, vb in ((3, 3), (2, 4))] + [(128, 4, 3), (64, 4, 3)])
+    (d, kb, vb) for d in (64, 128) for kb, vb in ((3, 3), (2, 4))] + [(128, 4, 3), (64, 4, 3),
+                                                         (96, 3, 3), (96, 4, 2)])
 def test_paged_matches_contiguous(d, dtype, key_bits, value_bits, page_tokens):
     B, H, G = 3, 2, 4
     seed = d + key_bits * 10 + value_bits
@@ -212,7 +213,7 @@ def test_model_manager_generation():
     assert all(l.total_tokens == 0 for l in m.layers)
 
 
-@pytest.mark.parametrize("d,page_tokens", [(128, 64), (64, 256)])
+@pytest.mark.parametrize("d,page_tokens", [(128, 64), (64, 256), (96, 64)])
 def test_paged_layers_match_single_layer_calls(d, page_tokens):
     """qkv_paged_decode_attention_layers (per-layer pools, one shared page
     table) against one qkv_paged_decode_attention call per layer with the same
@@ -269,7 +270,7 @@ def test_paged_layers_match_single_layer_calls(d, page_tokens):
         _close(o, _oracle(q, e, causal=False))
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("key_bits,value_bits", [(3, 3), (4, 4), (3, 2)])
 @pytest.mark.parametrize("shape", ["few", "many"])
@@ -339,7 +340,7 @@ def test_paged_kv_append_equals_two_calls(d, dtype, key_bits, value_bits, shape)
     assert ga.knorm[:, :, :t0].abs().min() > 0
 
 
-@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("shape", ["few", "many"])
 def test_paged_kv_append_skips_pages_off_the_pool(d, shape):
     """qkv_paged_store_append_kv never writes through page-table entries

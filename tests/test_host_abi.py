@@ -72,10 +72,10 @@ def test_abi_rejects_before_launch():
 
 def test_store_append_validation():
     lib = N.lib()
-    # unknown input dtypes are refused, head_dims other than 128 / 64 not covered
+    # unknown input dtypes are refused, head_dims other than 128 / 96 / 64 not covered
     assert lib.qkv_store_append(7, 16, None, 1, 1, 128, 2, 3, 16, 16, 16, 16, 16, 16,
                                 16, 16, 16, 64, 0, None) == N.QKV_E_INVALID
-    assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 96, 2, 3, 16, 16, 16, 16, 16, 16,
+    assert lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 1, 80, 2, 3, 16, 16, 16, 16, 16, 16,
                                 16, 16, 16, 64, 0, None) == N.QKV_E_UNSUPPORTED
     # capacity must hold the appended tokens
     st = lib.qkv_store_append(N.QKV_BF16, 16, None, 1, 10, 128, 2, 3, 16, 16, 16, 16, 16, 16,
@@ -119,7 +119,7 @@ def test_compress_mfma_host_validation():
     lib = N.lib()
     c2, t2 = N.HostFloats([-1.5, -0.5, 0.5, 1.5]), N.HostFloats([-1.0, 0.0, 1.0])
     # other head dims and bit widths are not covered (the VALU qkv_compress is)
-    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 96, 16, c2.ptr, t2.ptr, 2, 16,
+    assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 80, 16, c2.ptr, t2.ptr, 2, 16,
                                  16, 16, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
     assert lib.qkv_compress_mfma(N.QKV_MODE_IP, N.QKV_F32, 16, 4, 128, 16, c2.ptr, t2.ptr, 4, 16,
                                  16, 16, 16, 4, 4, None) == N.QKV_E_UNSUPPORTED
@@ -206,7 +206,7 @@ def test_store_append_layers_host_validation():
     assert "n_layers" in lib.qkv_last_error().decode()
     assert lib.qkv_store_append_layers(*args(2, dt=7)) == N.QKV_E_INVALID
     assert lib.qkv_store_append_layers(*args(2, cap=100)) == N.QKV_E_INVALID   # capacity
-    assert lib.qkv_store_append_layers(*args(2, d=96)) == N.QKV_E_UNSUPPORTED
+    assert lib.qkv_store_append_layers(*args(2, d=80)) == N.QKV_E_UNSUPPORTED
     assert lib.qkv_store_append_layers(*args(2, arr=None)) == N.QKV_E_INVALID
     nul = N.ptr_array([256, 0])
     assert lib.qkv_store_append_layers(*args(2, arr=nul)) == N.QKV_E_INVALID
@@ -418,7 +418,7 @@ def test_paged_store_append_kv_host_validation():
     assert call(pt=48) == N.QKV_E_INVALID           # pages of 64 * 2^k tokens
     assert call(npages=0) == N.QKV_E_INVALID
     assert call(S=4 * 64 + 1) == N.QKV_E_INVALID    # beyond the table's pages
-    assert call(d=96) == N.QKV_E_UNSUPPORTED
+    assert call(d=80) == N.QKV_E_UNSUPPORTED
     assert call(vbits=5) == N.QKV_E_INVALID
     assert call(dt=7) == N.QKV_E_INVALID
 

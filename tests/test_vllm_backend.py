@@ -10,7 +10,6 @@ from quashkv_amd.integrations.vllm_backend import (
     HAS_VLLM, QuashKVModelManager, QuashKVPageConfig, QuashKVPageManager,
     register_quashkv_backend)
 from quashkv_amd.paged import PagedQuashKVEngine
-from quashkv_amd.engine import QuashKVEngine
 
 CPU = torch.device("cpu")
 
@@ -26,14 +25,13 @@ def test_page_manager_init_and_store_choice():
     pm = QuashKVPageManager(num_kv_heads=4, head_size=64, config=QuashKVPageConfig(), device=CPU)
     assert pm.total_tokens == 0 and pm.num_kv_heads == 4 and pm.head_size == 64
     assert pm.paged and isinstance(pm.engine, PagedQuashKVEngine)
-    # 3-bit MSE keys (key_bits 4) at head_dim 64 are paged; head_dim 96 stays
-    # on the contiguous store
-    pm = QuashKVPageManager(num_kv_heads=2, head_size=64, config=QuashKVPageConfig(key_bits=4),
-                            device=CPU)
-    assert pm.paged and isinstance(pm.engine, PagedQuashKVEngine)
-    pm = QuashKVPageManager(num_kv_heads=2, head_size=96, config=QuashKVPageConfig(key_bits=3),
-                            device=CPU)
-    assert not pm.paged and type(pm.engine) is QuashKVEngine
+    # every head_dim (64, 96, 128) and key/value width the config takes is paged
+    for d in (64, 96, 128):
+        for kb, vb in ((2, 1), (3, 3), (4, 4), (4, 2)):
+            pm = QuashKVPageManager(num_kv_heads=2, head_size=d,
+                                    config=QuashKVPageConfig(key_bits=kb, value_bits=vb),
+                                    device=CPU)
+            assert pm.paged and isinstance(pm.engine, PagedQuashKVEngine), (d, kb, vb)
 
 
 def test_block_size_must_divide_page():
@@ -83,4 +81,4 @@ def test_no_vllm_raises():
 
 def test_paged_engine_rejects_uncovered_config():
     with pytest.raises(ValueError, match="paged cache"):
-        PagedQuashKVEngine(head_dim=96, key_bits=3, device=CPU)
+        PagedQuashKVEngine(head_dim=80, key_bits=3, device=CPU)
