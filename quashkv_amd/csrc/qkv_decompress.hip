@@ -1,4 +1,4 @@
-// Fused decompress on the matrix cores (d = 64 and 128):
+// Fused decompress on the matrix cores (d = 64, 96 and 128):
 //
 //   x^ = ((c[code] [+ qjl_scale S (2 bit - 1)]) Pi) * n
 //
@@ -25,7 +25,9 @@
 // consecutive coordinates g d/4 .. g d/4 + d/4 - 1 of its vector; k-step ks of
 // the MFMA takes its elements 8 ks .. 8 ks + 7.  Pi's fragments in LDS use the
 // same coordinate order, so every lane reads its codes as one contiguous run
-// of the row (32 bytes unpacked, 12 bytes of a 3-bit row at d = 128).
+// of the row (32 bytes unpacked, 12 bytes of a 3-bit row at d = 128).  At
+// d = 96 a lane's run (24 coordinates) starts mid-dword in the bit-packed
+// formats; it is read as the dwords that hold it and aligned in registers.
 //
 // Values come from a 32-entry LDS table (16 codes x the two codebooks of the
 // mixed-precision format), pre-split into fp16 (hi, lo) pairs for MSE codes;
@@ -137,11 +139,35 @@ struct QjlWords {
   }
 };
 
-// Lane's NE bits of a bit plane / 1-bit row starting at byte `p`.
+// Bytes off .. off + NB - 1 of a dword-aligned row of row_words dwords, as
+// (NB + 3) / 4 words (bytes past NB unspecified): the dwords that hold them,
+// clamped to the row, shifted into place.
+template <int NB>
+__device__ __forceinline__ void lane_span(const uint8_t* row, int row_words, int off,
+                                          uint32_t* out) {
+  constexpr int NO = (NB + 3) / 4;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(row);
+  const int wi = off >> 2, sh = off & 3;
+  uint32_t a[NO + 1];
+#pragma unroll
+  for (int k = 0; k <= NO; ++k) a[k] = w[min(wi + k, row_words - 1)];
+#pragma unroll
+  for (int k = 0; k < NO; ++k) out[k] = __builtin_amdgcn_alignbyte(a[k + 1], a[k], sh);
+}
+
+// Lane's NE bits of a bit plane / 1-bit row starting at byte `p` (at d = 96
+// bits 24..31 are unspecified).
 template <int D>
 __device__ __forceinline__ uint32_t lane_bits(const uint8_t* p, int g) {
-  if constexpr (D == 128) return reinterpret_cast<const uint32_t*>(p)[g];
-  else return reinterpret_cast<const uint16_t*>(p)[g];
+  if constexpr (D == 128) {
+    return reinterpret_cast<const uint32_t*>(p)[g];
+  } else if constexpr (D == 96) {
+    uint32_t w;
+    lane_span<3>(p, 3, 3 * g, &w);
+    return w;
+  } else {
+    return reinterpret_cast<const uint16_t*>(p)[g];
+  }
 }
 
 // ------------------------------------------------------------------ shared parts
@@ -440,7 +466,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void* out, const Bloc
       static_cast<int>(nrows * d * obytes), 0x00020000);
 }
 
-// ------------------------------------------------- d = 64: per-wave pipeline
+// -------------------------------------------- d = 64 and 96: per-wave pipeline
 
 // One wave per block of 32 vectors, each wave fetching its next block (loads
 // only) before the current block's MFMAs and stores, then expanding it.
@@ -481,7 +507,8 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_waves(
   uint4* stg = &stage[wave * 288];
 
   Raw<D, FMT, BITS, IP, R> x;
-  uint4 rt[VT ? D / 64 : 1];  // V tiles: this lane's share of the tile's words
+  constexpr int NRT = (D + 63) / 64;
+  uint4 rt[VT ? NRT : 1];  // V tiles: this lane's share of the tile's words
   auto fetch = [&](int blk) {
     const BlockPos b(blk, bpg, RB, n, in_seq);
 #pragma unroll
@@ -494,23 +521,32 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_waves(
 #pragma unroll
       for (int i = 0; i < Raw<D, FMT, BITS, IP, R>::QWN; ++i) x.q[r][i] = 0u;
       if constexpr (FMT == QKV_FMT_UNPACKED) {
-        const uint4* src = reinterpret_cast<const uint4*>(codes + row * D + g * NE);
+        // NE bytes: 16-byte reads, 8-byte reads at d = 96 (NE = 24)
+        auto bytes = [&](const uint8_t* p, uint32_t* dst) {
+          if constexpr (NE % 16 == 0) {
+            const uint4* src = reinterpret_cast<const uint4*>(p);
 #pragma unroll
-        for (int i = 0; i < NE / 16; ++i) {
-          const uint4 v = src[i];
-          x.c[r][4 * i] = v.x; x.c[r][4 * i + 1] = v.y; x.c[r][4 * i + 2] = v.z; x.c[r][4 * i + 3] = v.w;
-        }
-        if constexpr (IP) {
-          const uint4* qsrc = reinterpret_cast<const uint4*>(qjl + row * D + g * NE);
+            for (int i = 0; i < NE / 16; ++i) {
+              const uint4 v = src[i];
+              dst[4 * i] = v.x; dst[4 * i + 1] = v.y; dst[4 * i + 2] = v.z; dst[4 * i + 3] = v.w;
+            }
+          } else {
+            const uint2* src = reinterpret_cast<const uint2*>(p);
 #pragma unroll
-          for (int i = 0; i < NE / 16; ++i) {
-            const uint4 v = qsrc[i];
-            x.q[r][4 * i] = v.x; x.q[r][4 * i + 1] = v.y; x.q[r][4 * i + 2] = v.z; x.q[r][4 * i + 3] = v.w;
+            for (int i = 0; i < NE / 8; ++i) {
+              const uint2 v = src[i];
+              dst[2 * i] = v.x; dst[2 * i + 1] = v.y;
+            }
           }
-        }
+        };
+        bytes(codes + row * D + g * NE, x.c[r]);
+        if constexpr (IP) bytes(qjl + row * D + g * NE, x.q[r]);
       } else if constexpr (FMT == QKV_FMT_PACKED) {
         const uint8_t* rp = codes + row * pb;
-        if constexpr (D == 128) {
+        if constexpr (D == 96) {
+          // 3 BITS bytes from byte 3 BITS g of a 12 BITS-byte row
+          lane_span<3 * BITS>(rp, 3 * BITS, 3 * BITS * g, x.c[r]);
+        } else if constexpr (D == 128) {
           const uint32_t* src = reinterpret_cast<const uint32_t*>(rp) + BITS * g;
 #pragma unroll
           for (int i = 0; i < BITS; ++i) x.c[r][i] = src[i];
@@ -533,7 +569,7 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_waves(
       const uint4* src = reinterpret_cast<const uint4*>(codes) +
                          ((b.grp * in_gstride + (b.t0 >> 5)) * bits) * (D / 4);
 #pragma unroll
-      for (int u = 0; u < D / 64; ++u) {
+      for (int u = 0; u < NRT; ++u) {
         const int i = lane + 64 * u;
         rt[u] = src[i < nd4 ? i : nd4 - 1];
       }
@@ -546,7 +582,7 @@ __global__ __launch_bounds__(kThreads, 2) void decompress_waves(
     if constexpr (VT) {
       wave_lds_sync();
 #pragma unroll
-      for (int u = 0; u < D / 64; ++u) stg[lane + 64 * u] = rt[u];
+      for (int u = 0; u < NRT; ++u) stg[lane + 64 * u] = rt[u];
       wave_lds_sync();
     }
     expand<D, FMT, BITS, IP, SEL, R>(x, stg, bits, lane, tab, lc, ah, al);
@@ -839,21 +875,24 @@ int dispatch(const QkvDecompressArgs& a, hipStream_t s) {
 }  // namespace
 
 bool qkv_decompress_mfma_ok(const QkvDecompressArgs& a) {
-  if (a.d != 64 && a.d != 128) return false;
+  if (!qkv_d_ok(a.d)) return false;
   // block numbers (32 vectors per block, per group) are 32-bit
   const int64_t groups = (a.n + a.in_seq - 1) / a.in_seq;
   if (groups * ((a.in_seq + 31) / 32) > int64_t(0x7fffffff) - int64_t(qkv_num_cus()) * 64) return false;
   if (a.sel && a.fmt != QKV_FMT_UNPACKED) return false;
   if (a.fmt == QKV_FMT_PACKED && a.mode == QKV_MODE_IP && a.bits == 4) return false;
-  // 16-byte unpacked reads, 4-byte (2-byte at d = 64) packed and plane reads
-  const int ca = a.fmt == QKV_FMT_UNPACKED || a.fmt == QKV_FMT_VTILES ? 16 : (a.d == 128 ? 4 : 2);
+  // unpacked reads of 16 bytes (8 at d = 96), V tiles of 16; packed and
+  // plane reads of 4 bytes (2 at d = 64)
+  const int ua = a.d == 96 ? 8 : 16, ba = a.d == 64 ? 2 : 4;
+  const int ca = a.fmt == QKV_FMT_UNPACKED ? ua : a.fmt == QKV_FMT_VTILES ? 16 : ba;
   if (!qkv_aligned(a.codes, ca)) return false;
   if (a.mode == QKV_MODE_IP && a.fmt != QKV_FMT_KPLANES &&
-      !qkv_aligned(a.qjl, a.fmt == QKV_FMT_UNPACKED ? 16 : (a.d == 128 ? 4 : 2)))
+      !qkv_aligned(a.qjl, a.fmt == QKV_FMT_UNPACKED ? ua : ba))
     return false;
   return qkv_aligned(a.out, 16);  // 16-byte output stores
 }
 
 int qkv_decompress_mfma(const QkvDecompressArgs& a, hipStream_t s) {
-  return a.d == 128 ? dispatch<128>(a, s) : dispatch<64>(a, s);
+  if (a.d == 128) return dispatch<128>(a, s);
+  return a.d == 96 ? dispatch<96>(a, s) : dispatch<64>(a, s);
 }

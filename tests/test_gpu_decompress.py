@@ -1,4 +1,4 @@
-"""GPU parity of the MFMA decompress kernels (d = 64 and 128) against the CPU
+"""GPU parity of the MFMA decompress kernels (d = 64, 96 and 128) against the CPU
 oracle: every code format (unpacked bytes, pack_bits rows, the store's K rows
 and V tiles), MSE and IP modes, all bit widths, grouped-row layouts with a
 partial last group, fp32 / fp16 / bf16 outputs and the mixed-precision
@@ -95,7 +95,7 @@ FMTS = {"unpacked": N.QKV_FMT_UNPACKED, "packed": N.QKV_FMT_PACKED,
         "kplanes": N.QKV_FMT_KPLANES, "vtiles": N.QKV_FMT_VTILES}
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 96, 128])
 @pytest.mark.parametrize("fmt", list(FMTS))
 @pytest.mark.parametrize("mode,bits", [("mse", 1), ("mse", 2), ("mse", 3), ("mse", 4),
                                        ("ip", 1), ("ip", 2), ("ip", 3)])
@@ -137,7 +137,7 @@ def test_decompress_formats_vs_oracle(d, fmt, mode, bits):
             assert float((diff > 0).double().mean()) <= 0.01
 
 
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 96, 128])
 def test_decompress_mixed_selector(d):
     """Mixed-precision codes (two codebooks selected per coordinate, unpacked)
     against the oracle's mixed_decompress (quashkv/mixed_precision.py:172-187)."""
