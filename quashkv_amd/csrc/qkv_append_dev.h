@@ -177,6 +177,30 @@ __device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
 
 __device__ __forceinline__ uint64_t lanes_where(bool p) { return __builtin_amdgcn_ballot_w64(p); }
 
+// 2 acc + bit `lane` of mask: shifts this lane's bit of a 64-lane compare mask
+// into a lane-local word (v_addc_co_u32 with the mask as carry-in, one
+// instruction per mask; no clang builtin spells the carry-in operand).
+__device__ __forceinline__ uint32_t shift_in(uint32_t acc, uint64_t mask) {
+  uint32_t r;
+  uint64_t co;
+  asm("v_addc_co_u32 %0, %1, %2, %2, %3" : "=v"(r), "=s"(co) : "v"(acc), "s"(mask));
+  return r;
+}
+
+// Two 16-bit lane-half accumulators into 32-bit words: lanes 0..31 get
+// a(l) | a(l + 32) << 16, lanes 32..63 get b(l - 32) | b(l) << 16.
+__device__ __forceinline__ uint32_t merge_halves(uint32_t a, uint32_t b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  return r[0] | (r[1] << 16);
+}
+
+// Position of C row m (0..31) of a 32x32 MFMA tile within its 32-block when
+// the operand rows are ordered so that lane half h's result registers
+// v = 0..15 (rows 8 (v >> 2) + 4 h + (v & 3)) hold positions 16 h + v.
+__host__ __device__ constexpr int half_major(int m) {
+  return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
+}
+
 // f(std::integral_constant<int, 0>), ..., f(<N - 1>): compile-time unrolled
 // loops whose index feeds template arguments (v_writelane lane numbers).
 template <typename F, int... I>
@@ -190,13 +214,13 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 // Binary search of the key a in the ascending key list t[0 .. 2^LM - 2]: bit i
 // of #{j : t[j] < a} as the lane mask g[i].  With CLAST the last level (whose
-// candidates are the list's even entries) compares ac instead of a.
-template <int LM, bool CLAST>
-__device__ __forceinline__ void search_levels(uint32_t a, uint32_t ac, const uint32_t* t,
-                                              bool (&c)[LM]) {
+// candidates are the list's even entries) compares ac instead of a.  T: the
+// integer keys, or floats for search_sym_scaled.
+template <int LM, bool CLAST, typename T>
+__device__ __forceinline__ void search_levels(T a, T ac, const T* t, bool (&c)[LM]) {
   static_for<LM>([&](auto kc) {
     constexpr int k = decltype(kc)::value;  // level k decides bit LM - 1 - k
-    uint32_t cand[1 << k];
+    T cand[1 << k];
 #pragma unroll
     for (int p = 0; p < (1 << k); ++p) cand[p] = t[(2 * p + 1) * (1 << (LM - 1 - k)) - 1];
     // prefix bit j (LSB first) is c[LM - k + j]
@@ -205,7 +229,7 @@ __device__ __forceinline__ void search_levels(uint32_t a, uint32_t ac, const uin
 #pragma unroll
       for (int q = 0; q < (1 << (k - 1 - j)); ++q)
         cand[q] = c[LM - k + j] ? cand[2 * q + 1] : cand[2 * q];
-    const uint32_t av = (CLAST && k == LM - 1) ? ac : a;
+    const T av = (CLAST && k == LM - 1) ? ac : a;
     c[LM - 1 - k] = av > cand[0];
   });
 }
@@ -238,6 +262,23 @@ __device__ __forceinline__ void search_sym(float y, const uint32_t* p, uint32_t 
     search_keys<L - 1, CLAST>(a, a ^ cx, p, g);
 #pragma unroll
     for (int i = 0; i < L - 1; ++i) m[i] = ~(g[i] ^ pos);
+  }
+}
+
+// search_sym's lane masks for a value z on another scale (z = y s, s > 0):
+// [z > 0] for the top bit and a search of |z| in P, the positive half of the
+// list times s, for the others.  Where |z| equals an entry of P the count may
+// land on either side of it (search_sym decides those exactly, on y).
+template <int L>
+__device__ __forceinline__ void search_sym_scaled(float z, const float* P, uint64_t (&m)[L]) {
+  const uint64_t pos = lanes_where(z > 0.f);
+  m[L - 1] = pos;
+  if constexpr (L > 1) {
+    const float az = fabsf(z);
+    bool c[L - 1];
+    search_levels<L - 1, false>(az, az, P, c);
+#pragma unroll
+    for (int i = 0; i < L - 1; ++i) m[i] = ~(lanes_where(c[i]) ^ pos);
   }
 }
 
@@ -293,11 +334,12 @@ __device__ __forceinline__ float from16(uint16_t h) {
     return qkv_bf16_to_f32(h);
 }
 
-// Stage the rotation operand in LDS.  Entry ((b * 8 + s) * 2 + split) * 64 + l
-// holds, for lane l, Pi'[32 b + (l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
+// Stage the rotation operand in LDS.  Entry ((b * NKS + s) * 2 + split) * 64 + l
+// holds, for lane l, Pi'[32 b + r(l & 31)][16 s + 8 (l >> 5) + e], e = 0..7, as
 // eight 16-bit values: the high part (split 0) or the low part (split 1) of
-// Pi' = Pi * pscale.
-template <bool F16, int D = kD>
+// Pi' = Pi * pscale; r(m) = m, or half_major(m) with PERM (the A operand of
+// the key append, whose result rows are then coordinates in half-major order).
+template <bool F16, int D = kD, bool PERM = false>
 __device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi, float pscale) {
   // kThreads threads (every launch uses that block size); each takes NPT
   // (block, k-step, lane) slots and writes both splits of each, with all of
@@ -310,7 +352,7 @@ __device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* 
   for (int x = 0; x < NPT; ++x) {
     const int u = min(threadIdx.x + kThreads * x, NSLOT - 1);
     const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
-    const int j = 32 * b + (ln & 31), k0 = 16 * s + 8 * (ln >> 5);
+    const int j = 32 * b + (PERM ? half_major(ln & 31) : (ln & 31)), k0 = 16 * s + 8 * (ln >> 5);
     p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
     p[x][1] = *reinterpret_cast<const float4*>(pi + j * D + k0 + 4);
   }
@@ -409,11 +451,19 @@ __device__ __forceinline__ void load_x_f32(uint4 (&xh)[kHalves][NKS], uint4 (&xl
 // ------------------------------------------------------------------ keys
 
 // One wave per tile of kTok consecutive tokens of one (b, h) group.  Input rows
-// grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * 16 bytes:
+// grp * S + s; store rows grp * t_stride + t0 + s ((MB + 1) * D / 8 bytes:
 // MB MSE planes, then the QJL plane).  FROM_Y: `xin` holds fp32 rotated unit
 // rows y (rows as above) and `nin` their norms; the normalisation and the
-// rotation are skipped, everything after them is the same code.
+// rotation are skipped, and the search is search_sym's exact one on y.
 // XT: the input rows' type, 0 bf16, 1 fp16, 2 fp32 (on the fp16 MFMA, split)
+//
+// Orientation: C = coordinates x tokens (A = Pi's rows in half-major order,
+// B = x), so lane l holds token l & 31 and, in register v, coordinate
+// 32 n + 16 (l >> 5) + v of block n.  Each compare mask is shifted into the
+// lanes' own 16-bit plane accumulators (shift_in), the two lane halves are
+// merged into 32-coordinate words (merge_halves), and every lane stores a
+// contiguous run of its own token's K row.  From x the search compares the
+// raw MFMA result against the list scaled by the lane's token norm.
 //
 // ONE: small appends, where one wave's chain is the kernel's time.  Each wave
 // takes at most one tile (nb * kWaves >= ntiles * nsplit, the host's
@@ -426,16 +476,18 @@ __device__ __forceinline__ void append_k_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, const float* __restrict__ signs, Half fine,
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
-    QkvPages pg, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb,
-    int nsplit = 1) {
+    QkvPages pg, uint4* __restrict__ frag, int bid, int nb, int nsplit = 1) {
+  static_assert(kHalves == 1, "one 32-token MFMA column block per wave tile");
   constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int L = MB + 1;           // search levels over the fine list
   constexpr int NP = (1 << MB) - 1;   // positive half of the fine list c_0, t_0, ..., c_{2^MB-1}
   constexpr int NBK = D / 32;         // coordinate blocks = dwords per plane
   constexpr int NKS = D / 16;         // k-steps
   constexpr int RD = NBK * L;         // dwords per row
-  constexpr int NSK = (RD * kTok + 63) / 64;  // staging dwords per lane (the last may be partial)
-  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
+  constexpr int RDH = (RD + 1) / 2;   // dwords per row a lane half stores
+  constexpr int LH = (L + 1) / 2;     // split: planes per lane half
+  const int lane = threadIdx.x & 63, li = lane & 31, hh = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile math on the SALU
   // ONE with nsplit = NBK: wave (tile, coordinate block) = (g / NBK, g % NBK)
   // for the global wave index g, each wave computing and storing that block's
   // words only; nsplit = 1: wave g takes tile g whole
@@ -443,35 +495,39 @@ __device__ __forceinline__ void append_k_run(
   const bool split = ONE && nsplit > 1;
   const int myblk = split ? static_cast<int>(gw % NBK) : 0;
   constexpr bool PRE = ONE && !FROM_Y && !F32;  // rows loaded before the Pi staging
-  uint4 xpre[kHalves][PRE ? NKS : 1];
+  uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
     const int64_t tile = split ? gw / NBK : gw;
     if (tile < ntiles) {
       const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
       const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+      const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
+                                (grp * S + s0 + min(li, nv - 1)) * D};
       load_x<NKS>(xpre, row, lane);
     }
   }
   if constexpr (!FROM_Y) {
-    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    stage_pi<F16, D, true>(frag, pi, F16 ? kPScaleF16 : 1.f);
     __syncthreads();
   }
 
+  // the positive half of the fine list: integer keys (FROM_Y) or floats
   uint32_t fv[NP];
+  float fp[NP];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) fv[i] = in_vgpr(fine.t[i]);
-  uint64_t sneg[NBK];  // lanes whose coordinate 32 n + (l & 31) has S < 0
-  uint32_t cx[NBK];    // 1 where S >= 0: the centroid level counts c <= y there
+  for (int i = 0; i < NP; ++i) {
+    fv[i] = in_vgpr(fine.t[i]);
+    fp[i] = __uint_as_float(fine.t[i] >> 1);
+  }
+  // per block n, bits v of this lane half's coordinates 32 n + 16 h + v:
+  // [S < 0] (the QJL plane's flip) and [S >= 0] (the exact search's centroid
+  // level counts c <= y there)
+  uint32_t qflip[NBK], cxw[NBK];
 #pragma unroll
   for (int n = 0; n < NBK; ++n) {
-    const bool neg = signs[32 * n + li] < 0.f;
-    sneg[n] = lanes_where(neg);
-    cx[n] = neg ? 0u : 1u;
+    const uint32_t negw = static_cast<uint32_t>(lanes_where(signs[32 * n + li] < 0.f));
+    qflip[n] = (negw >> (16 * hh)) & 0xffffu;
+    cxw[n] = qflip[n] ^ 0xffffu;
   }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
@@ -480,158 +536,125 @@ __device__ __forceinline__ void append_k_run(
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    const int64_t srow = grp * S + s0 + min(li, nv - 1);  // this lane's token row (clamped)
     QkvSpan sp{};
     if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, t0 + s0);
-    uint4 xf[kHalves][NKS];  // tokens past S read the last row; their results are not stored
-    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    uint4 xf[1][NKS];  // tokens past S read the last row; their results are not stored
+    uint4 xl[1][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    float thr[NP];               // the list in MFMA-result units of this lane's token
     if constexpr (FROM_Y) {
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        if (lane < 32 && 32 * tt + li < nv) {
-          const int64_t t = t0 + s0 + 32 * tt + li;
-          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0) knorm[r] = nin[grp * S + s0 + 32 * tt + li];
-        }
+      if (lane < 32 && li < nv) {
+        const int64_t t = t0 + s0 + li;
+        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+        if (r >= 0) knorm[r] = nin[srow];
+      }
     } else {
-      float nrm[kHalves];
+      float nrm[1];
       if constexpr (F32) {
-        const float* row[kHalves];
-        const auto* x = static_cast<const float*>(xin);
-#pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+        const float* row[1] = {static_cast<const float*>(xin) + srow * D};
         load_x_f32<NKS>(xf, xl, nrm, row, lane);
       } else {
         if constexpr (PRE) {
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-            for (int s = 0; s < NKS; ++s) xf[tt][s] = xpre[tt][s];
+          for (int s = 0; s < NKS; ++s) xf[0][s] = xpre[0][s];
         } else {
-          const uint16_t* row[kHalves];
-          const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt)
-            row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * D;
+          const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) + srow * D};
           load_x<NKS>(xf, row, lane);
         }
+        float ss = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) {
-          float ss = 0.f;
-#pragma unroll
-          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-          ss += __shfl_xor(ss, 32, 64);
-          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
-        }
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[0][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        nrm[0] = fmaxf(sqrtf(ss), 1e-8f);
       }
-
-      // norms; the scale of token t's MFMA result (1 / n, or 2^-16 for fp32
-      // rows scaled before the rotation) goes to LDS, read back in C-row order
-      // (rows 8 a + 4 (l >> 5) + 0..3 of VGPRs 4 a .. 4 a + 3 are four
-      // consecutive tokens)
-      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) {
-        if (lane < 32) {
-          if (32 * tt + li < nv) {
-            const int64_t t = t0 + s0 + 32 * tt + li;
-            const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-            if (r >= 0 && myblk == 0) knorm[r] = nrm[tt];
-          }
-          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
-        }
+      if (lane < 32 && li < nv) {
+        const int64_t t = t0 + s0 + li;
+        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+        if (r >= 0 && myblk == 0) knorm[r] = nrm[0];
       }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-      __builtin_amdgcn_wave_barrier();
+      // the MFMA result is y |x| / iscale (fp32 rows: 2^16 y)
+      const float zs = F32 ? 65536.f : nrm[0] / iscale;
+#pragma unroll
+      for (int i = 0; i < NP; ++i) thr[i] = fp[i] * zs;
     }
 
-    uint32_t stg[NSK];
+    uint32_t kw[RD];  // [plane][block]: this lane half's 16 bits of each row dword
 #pragma unroll
-    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
+    for (int i = 0; i < RD; ++i) kw[i] = 0u;
 
-    static_for<NBK>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: store word n of each plane
+    static_for<NBK>([&](auto nc) {  // coordinates 32 n .. 32 n + 31: word n of each plane
       constexpr int n = decltype(nc)::value;
       if (split && n != myblk) return;
       // one coordinate block at a time: keeps the scheduler from overlapping
       // blocks (and their accumulators and fragments) beyond the register file
       __builtin_amdgcn_sched_barrier(0);
-      // y of coordinate 32 n + (l & 31) for tokens 32 tt + 8 (v >> 2) + 4 (l >> 5) + (v & 3)
-      float yv[kHalves][16];
+      float yv[16];  // coordinate 32 n + 16 h + v of this lane's token
       if constexpr (FROM_Y) {
-        const auto* y = static_cast<const float*>(xin);
+        const float4* y = reinterpret_cast<const float4*>(static_cast<const float*>(xin) +
+                                                          srow * D + 32 * n + 16 * hh);
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * D + 32 * n + li];
-          }
+        for (int a = 0; a < 4; ++a) {
+          const float4 q = y[a];
+          yv[4 * a] = q.x; yv[4 * a + 1] = q.y; yv[4 * a + 2] = q.z; yv[4 * a + 3] = q.w;
+        }
       } else {
-        qkv_f32x16 acc[kHalves] = {};
+        qkv_f32x16 acc = {};
 #pragma unroll
         for (int s = 0; s < NKS; ++s)
 #pragma unroll
           for (int sp2 = 0; sp2 < 2; ++sp2) {
-            const uint4 bf = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
-#pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) {
-              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
-              if (F32 && sp2 == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
-            }
+            const uint4 af = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
+            acc = mma<F16>(af, xf[0][s], acc);
+            if (F32 && sp2 == 0) acc = mma<F16>(af, xl[0][F32 ? s : 0], acc);
           }
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) {
-          if constexpr (F32) {  // rows scaled before the rotation: one constant
-#pragma unroll
-            for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * (1.f / 65536.f);
-            continue;
-          }
-          float4 iv4[4];
-#pragma unroll
-          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float4 q4 = iv4[v >> 2];
-            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-            yv[tt][v] = acc[tt][v] * iv;
-          }
-        }
+        for (int v = 0; v < 16; ++v) yv[v] = acc[v];
       }
-      static_for<kHalves>([&](auto tc) {
-        constexpr int tt = decltype(tc)::value;
-        static_for<16>([&](auto vc) {
-          constexpr int v = decltype(vc)::value;
-          uint64_t f[L];
-          search_sym<L, true>(yv[tt][v], fv, cx[n], f);
-          // token ta (lanes 0..31) and ta + 4 (lanes 32..63)
-          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);
-          static_for<L>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;  // plane r: MSE bit r, r = MB: QJL
-            const uint64_t w = r < MB ? f[r < MB ? r + 1 : 0] : (f[0] ^ sneg[n]);
-            constexpr int D0 = ta * RD + NBK * r + n, D1 = (ta + 4) * RD + NBK * r + n;
-            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w));
-            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w >> 32));
-          });
-        });
+      // registers high to low: bit v of each accumulator is register v
+      static_for<16>([&](auto vc) {
+        constexpr int v = 15 - decltype(vc)::value;
+        uint64_t f[L];
+        if constexpr (FROM_Y)
+          search_sym<L, true>(yv[v], fv, (cxw[n] >> v) & 1u, f);
+        else
+          search_sym_scaled<L>(yv[v], thr, f);
+        // plane r: MSE bit r (fine-count bit r + 1); plane MB: QJL (bit 0)
+#pragma unroll
+        for (int r = 0; r < L; ++r) kw[r * NBK + n] = shift_in(kw[r * NBK + n], f[r < MB ? r + 1 : 0]);
       });
+      kw[MB * NBK + n] ^= qflip[n];
     });
 
-    if constexpr (PAGED) {
-      // dword w of the tile: row w / RD (token t0 + s0 + w / RD), dword w % RD
-      uint32_t* dst = reinterpret_cast<uint32_t*>(kst);
+    // lane half h stores dwords h RDH .. of its token's row (split: planes
+    // h LH .. of block myblk)
+    const int64_t tk = t0 + s0 + li;
+    const int64_t row = li < nv ? (PAGED ? sp.row(tk) : grp * t_stride + tk) : -1;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(kst) + row * RD;
+    if (split) {
 #pragma unroll
-      for (int i = 0; i < NSK; ++i) {
-        const int w = i * 64 + lane, r = w / RD;
-        const int64_t row = sp.row(t0 + s0 + r);
-        if (w < nv * RD && row >= 0 && (!split || w % NBK == myblk))
-          dst[row * RD + (w - r * RD)] = stg[i];
+      for (int i = 0; i < LH; ++i) {
+        const int rb = i + LH < L ? i + LH : i;
+        const uint32_t w = merge_halves(kw[i * NBK + myblk], kw[rb * NBK + myblk]);
+        const int r = hh ? rb : i;
+        if (row >= 0 && (hh == 0 || i + LH < L)) dst[r * NBK + myblk] = w;
       }
     } else {
-      uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+      uint32_t ow[RDH];
 #pragma unroll
-      for (int i = 0; i < NSK; ++i) {
-        const int w = i * 64 + lane;  // dword w % RD of a row is word (w % RD) % NBK of a plane
-        if (w < nv * RD && (!split || w % NBK == myblk)) dst[w] = stg[i];
+      for (int i = 0; i < RDH; ++i) ow[i] = merge_halves(kw[i], kw[i + RDH < RD ? i + RDH : i]);
+      if (row >= 0) {
+        uint32_t* d = dst + hh * RDH;
+        constexpr int VW = (RDH % 4 == 0 && RD % 4 == 0) ? 4 : (RDH % 2 == 0 && RD % 2 == 0) ? 2 : 1;
+#pragma unroll
+        for (int i = 0; i < RDH; i += VW) {
+          if (RD % 2 != 0 && hh == 1 && RDH + i >= RD) continue;
+          if constexpr (VW == 4)
+            *reinterpret_cast<uint4*>(d + i) = make_uint4(ow[i], ow[i + 1], ow[i + 2], ow[i + 3]);
+          else if constexpr (VW == 2)
+            *reinterpret_cast<uint2*>(d + i) = make_uint2(ow[i], ow[i + 1]);
+          else
+            d[i] = ow[i];
+        }
       }
     }
     if constexpr (ONE) break;
@@ -645,9 +668,8 @@ __global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_k_mfma(
     uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride, int64_t t0,
     QkvPages pg) {
   __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];  // Pi operand fragments
-  __shared__ float4 inv_s[kWaves][kTok / 4];         // 1 / norm of each wave's tokens
   append_k_run<MB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, signs, fine, kst, knorm,
-                                         t_stride, t0, pg, frag, inv_s, blockIdx.x, gridDim.x);
+                                         t_stride, t0, pg, frag, blockIdx.x, gridDim.x);
 }
 
 // append_k_mfma over the contiguous stores of blockIdx.y's layer
@@ -657,12 +679,10 @@ __global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, 
                                                                Half fine, int64_t t_stride,
                                                                int64_t t0) {
   __shared__ uint4 frag[frag_n<D>()];
-  __shared__ float4 inv_s[kWaves][kTok / 4];
   const int l = blockIdx.y;
   append_k_run<MB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], al.signs[l],
                                         fine, static_cast<uint8_t*>(al.st[l]), al.nrm[l],
-                                        t_stride, t0, QkvPages{}, frag, inv_s, blockIdx.x,
-                                        gridDim.x);
+                                        t_stride, t0, QkvPages{}, frag, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------- mixed-precision keys
@@ -1039,40 +1059,47 @@ __global__ __launch_bounds__(kThreads, 4) void compress_mfma(
 // ---------------------------------------------------------------- values
 
 // One wave per kTok store tokens [A0, A0 + kTok) of one group, A0 32-aligned,
-// so the wave owns whole V tiles; tokens outside [t0, t0 + S) keep the bits
+// so the wave owns one whole V tile; tokens outside [t0, t0 + S) keep the bits
 // already in the store.  FROM_Y: `xin` holds fp32 rotated unit rows and `nin`
-// their norms.
+// their norms, and the search is search_sym's exact one on y.
+//
+// Orientation: C = tokens x coordinates (A = x with the tile's token rows in
+// half-major order, B = Pi), so lane l holds coordinate 32 mb + (l & 31) and,
+// in register v, token 16 (l >> 5) + v of the tile.  Each compare mask is
+// shifted into the lanes' own 16-token plane accumulators (shift_in), the two
+// lane halves are merged into the tile's 32-token words (merge_halves), and
+// each lane stores its coordinate's word of two planes.  The tokens' 1 / |x|
+// reach the lanes through inv_s.
 template <int VB, int XT, int D, bool PAGED, bool FROM_Y, bool ONE = false>
 __device__ __forceinline__ void append_v_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg,
-    uint4* __restrict__ frag, int bid, int nb, int nsplit = 1) {
+    uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb, int nsplit = 1) {
+  static_assert(kHalves == 1, "one 32-token MFMA row block (one V tile) per wave tile");
   constexpr bool F16 = XT != 0, F32 = XT == 2;  // fp16 MFMA / fp32 rows split for it
   constexpr int NP = (1 << (VB - 1)) - 1;  // positive half of the boundaries
   constexpr int NBK = D / 32;        // coordinate blocks
   constexpr int NKS = D / 16;        // k-steps
-  constexpr int NW = kHalves * VB * D;   // store words of a wave tile: [tile][plane][coordinate]
-  constexpr int NS = (NW + 63) / 64;     // staging dwords per lane (the last may be partial)
-  const int lane = threadIdx.x & 63, li = lane & 31;
+  constexpr int KH = (VB + 1) / 2;   // planes per lane half in a merge
+  const int lane = threadIdx.x & 63, li = lane & 31, hh = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile math on the SALU
   const int64_t a_base = t0 & ~int64_t(31);
   // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
   // ONE, nsplit: the waves' tiles and coordinate blocks as in append_k_run
-  const int64_t gw = int64_t(bid) * kWaves + (threadIdx.x >> 6);
+  const int64_t gw = int64_t(bid) * kWaves + wv;
   const bool split = ONE && nsplit > 1;
   const int myblk = split ? static_cast<int>(gw % NBK) : 0;
+  const int wt = half_major(li);  // tile token of this lane's A-operand row
   constexpr bool PRE = ONE && !FROM_Y && !F32;
-  uint4 xpre[kHalves][PRE ? NKS : 1];
+  uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
     const int64_t tile = split ? gw / NBK : gw;
     if (tile < ntiles) {
       const int64_t grp = tile / tpg;
       const int64_t d0 = a_base + (tile - grp * tpg) * kTok - t0;
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        row[tt] = x + (grp * S + min<int64_t>(max<int64_t>(d0 + 32 * tt + li, 0), S - 1)) * D;
+      const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
+                                (grp * S + min<int64_t>(max<int64_t>(d0 + wt, 0), S - 1)) * D};
       load_x<NKS>(xpre, row, lane);
     }
   }
@@ -1081,152 +1108,138 @@ __device__ __forceinline__ void append_v_run(
     __syncthreads();
   }
 
+  // the positive half of the boundaries: integer keys (FROM_Y), floats (on y;
+  // fp32 rows compare the MFMA result 2^16 y against them times 2^16)
   uint32_t bv[NP > 0 ? NP : 1];
+  float bp[NP > 0 ? NP : 1];
 #pragma unroll
-  for (int i = 0; i < NP; ++i) bv[i] = in_vgpr(bnd.t[i]);
+  for (int i = 0; i < NP; ++i) {
+    bv[i] = in_vgpr(bnd.t[i]);
+    bp[i] = __uint_as_float(in_vgpr(bnd.t[i] >> 1)) * (F32 ? 65536.f : 1.f);
+  }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
   for (int64_t tile = split ? gw / NBK : gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
-    const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of lane-token 0
+    const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of tile token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
     QkvSpan sp{};
     if constexpr (PAGED) sp = qkv_span(pg, grp, t_stride, A0);
-    bool ok[kHalves];
-    int64_t src[kHalves];  // input row of this lane's token (clamped into [0, S))
-#pragma unroll
-    for (int tt = 0; tt < kHalves; ++tt) {
-      const int64_t si = d0 + 32 * tt + li;
-      ok[tt] = si >= 0 && si < S;
-      src[tt] = grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1);
-    }
-    uint4 xf[kHalves][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
-    uint4 xl[kHalves][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
-    float inv[kHalves];      // token 32 tt + (l & 31): the C-column of this lane
+    uint4 xf[1][NKS];  // tokens outside [t0, t0 + S) read a valid row; bits not stored
+    uint4 xl[1][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
     if constexpr (FROM_Y) {
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        if (lane < 32 && ok[tt]) {
-          const int64_t t = A0 + 32 * tt + li;
-          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0) vnorm[r] = nin[src[tt]];
-        }
+      const int64_t si = d0 + li;
+      if (lane < 32 && si >= 0 && si < S) {
+        const int64_t t = A0 + li;
+        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+        if (r >= 0) vnorm[r] = nin[grp * S + si];
+      }
     } else {
-      float nrm[kHalves];
+      const int64_t si = d0 + wt;
+      const int64_t src = grp * S + min<int64_t>(max<int64_t>(si, 0), S - 1);
+      float nrm[1];
       if constexpr (F32) {
-        const float* row[kHalves];
-        const auto* x = static_cast<const float*>(xin);
-#pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+        const float* row[1] = {static_cast<const float*>(xin) + src * D};
         load_x_f32<NKS>(xf, xl, nrm, row, lane);
       } else {
         if constexpr (PRE) {
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-            for (int s = 0; s < NKS; ++s) xf[tt][s] = xpre[tt][s];
+          for (int s = 0; s < NKS; ++s) xf[0][s] = xpre[0][s];
         } else {
-          const uint16_t* row[kHalves];
-          const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt) row[tt] = x + src[tt] * D;
+          const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) + src * D};
           load_x<NKS>(xf, row, lane);
         }
+        float ss = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) {
-          float ss = 0.f;
-#pragma unroll
-          for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-          ss += __shfl_xor(ss, 32, 64);
-          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
-        }
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[0][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        nrm[0] = fmaxf(sqrtf(ss), 1e-8f);
       }
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) {
-        if (lane < 32 && ok[tt]) {
-          const int64_t t = A0 + 32 * tt + li;
-          const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
-          if (r >= 0 && myblk == 0) vnorm[r] = nrm[tt];
-        }
-        inv[tt] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
+      if (lane < 32 && si >= 0 && si < S) {
+        const int64_t t = A0 + wt;
+        const int64_t r = PAGED ? sp.row(t) : grp * t_stride + t;
+        if (r >= 0 && myblk == 0) vnorm[r] = nrm[0];
+      }
+      if constexpr (!F32) {
+        // 1 / |x| of tile token wt, read back by the lanes holding it
+        if (lane < 32) reinterpret_cast<float*>(&inv_s[wv][0])[wt] = iscale / nrm[0];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
+        __builtin_amdgcn_wave_barrier();
       }
     }
-
-    uint32_t stg[NS];
-#pragma unroll
-    for (int i = 0; i < NS; ++i) stg[i] = 0u;
+    // the appended tokens [lo, hi) of the tile; a page outside the pool takes
+    // nothing
+    const int64_t lo = max<int64_t>(t0 - A0, 0), hi = min<int64_t>(t0 + S - A0, 32);
+    const uint32_t vm = hi - lo >= 32 ? 0xffffffffu
+                        : hi > lo    ? ((1u << static_cast<int>(hi - lo)) - 1u) << lo
+                                     : 0u;
+    const int64_t vrow = PAGED ? sp.row(A0) : 0;
+    const bool wr = vm != 0u && vrow >= 0;
+    const int64_t vt = PAGED ? (vrow >> 5) : grp * (t_stride >> 5) + (A0 >> 5);
+    uint32_t* vtile = vst + vt * (VB * D);
 
     static_for<NBK>([&](auto mc) {  // coordinates 32 mb .. 32 mb + 31
       constexpr int mb = decltype(mc)::value;
       if (split && mb != myblk) return;
       __builtin_amdgcn_sched_barrier(0);  // one coordinate block at a time (registers)
-      // y of coordinate 32 mb + 8 (v >> 2) + 4 (l >> 5) + (v & 3), token 32 tt + (l & 31)
-      float yv[kHalves][16];
+      float yv[16];  // token 16 h + v of the tile at coordinate 32 mb + (l & 31)
       if constexpr (FROM_Y) {
         const auto* y = static_cast<const float*>(xin);
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v)
-            yv[tt][v] = y[src[tt] * D + 32 * mb + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3)];
+        for (int v = 0; v < 16; ++v) {
+          const int64_t si = min<int64_t>(max<int64_t>(d0 + 16 * hh + v, 0), S - 1);
+          yv[v] = y[(grp * S + si) * D + 32 * mb + li];
+        }
       } else {
-        qkv_f32x16 acc[kHalves] = {};
+        qkv_f32x16 acc = {};
 #pragma unroll
         for (int s = 0; s < NKS; ++s)
 #pragma unroll
           for (int sp2 = 0; sp2 < 2; ++sp2) {
-            const uint4 af = frag[((mb * NKS + s) * 2 + sp2) * 64 + lane];
-#pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) {
-              acc[tt] = mma<F16>(af, xf[tt][s], acc[tt]);
-              if (F32 && sp2 == 0) acc[tt] = mma<F16>(af, xl[tt][F32 ? s : 0], acc[tt]);
-            }
+            const uint4 bf = frag[((mb * NKS + s) * 2 + sp2) * 64 + lane];
+            acc = mma<F16>(xf[0][s], bf, acc);
+            if (F32 && sp2 == 0) acc = mma<F16>(xl[0][F32 ? s : 0], bf, acc);
           }
+        if constexpr (F32) {
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
+          for (int v = 0; v < 16; ++v) yv[v] = acc[v];
+        } else {
+          float4 iv4[4];
 #pragma unroll
-          for (int v = 0; v < 16; ++v) yv[tt][v] = acc[tt][v] * inv[tt];
+          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][4 * hh + a];
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float4 q4 = iv4[v >> 2];
+            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
+            yv[v] = acc[v] * iv;
+          }
+        }
       }
-      static_for<kHalves>([&](auto tc) {  // V tile tt of the wave tile
-        constexpr int tt = decltype(tc)::value;
-        static_for<16>([&](auto vc) {
-          constexpr int v = decltype(vc)::value;
-          uint64_t m[VB];
-          search_sym<VB, false>(yv[tt][v], bv, 0u, m);
-          // coordinate ca (lanes 0..31) and ca + 4 (lanes 32..63), tokens 32 tt + 0..31
-          constexpr int ca = 32 * mb + 8 * (v >> 2) + (v & 3);
-          static_for<VB>([&](auto kc) {
-            constexpr int k = decltype(kc)::value;
-            constexpr int D0 = (tt * VB + k) * D + ca, D1 = D0 + 4;
-            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(m[k]));
-            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(m[k] >> 32));
-          });
-        });
-      });
-    });
-
-    // store: staging dword i of lane l is word w = 64 i + l of the tile's
-    // [tile][plane][coordinate] words
+      uint32_t va[VB];  // plane k: this lane half's 16 tokens (bit v = register v)
 #pragma unroll
-    for (int i = 0; i < NS; ++i) {
-      const int w = 64 * i + lane;
-      if (NW % 64 != 0 && w >= NW) continue;
-      const int tau = w / (VB * D), k = (w / D) % VB, j = w % D;
-      if (split && (j >> 5) != myblk) continue;  // another wave's coordinate block
-      const int64_t tok0 = A0 + 32 * tau;
-      const int64_t lo = max<int64_t>(t0 - tok0, 0), hi = min<int64_t>(t0 + S - tok0, 32);
-      if (hi <= lo) continue;
-      const uint32_t vm = (hi - lo == 32) ? 0xffffffffu
-                                          : (((1u << (hi - lo)) - 1u) << lo);
-      const int64_t vrow = PAGED ? sp.row(tok0) : 0;
-      if (vrow < 0) continue;  // a page outside the pool: nothing written
-      const int64_t vt = PAGED ? (vrow >> 5) : grp * (t_stride >> 5) + (tok0 >> 5);
-      uint32_t* p = vst + (vt * VB + k) * D + j;
-      uint32_t val = stg[i];
-      if (vm != 0xffffffffu) val = (*p & ~vm) | (val & vm);
-      *p = val;
-    }
+      for (int k = 0; k < VB; ++k) va[k] = 0u;
+      static_for<16>([&](auto vc) {
+        constexpr int v = 15 - decltype(vc)::value;
+        uint64_t m[VB];
+        if constexpr (FROM_Y)
+          search_sym<VB, false>(yv[v], bv, 0u, m);
+        else
+          search_sym_scaled<VB>(yv[v], bp, m);
+#pragma unroll
+        for (int k = 0; k < VB; ++k) va[k] = shift_in(va[k], m[k]);
+      });
+      // lanes 0..31 store plane i, lanes 32..63 plane i + KH
+#pragma unroll
+      for (int i = 0; i < KH; ++i) {
+        const int kb = i + KH < VB ? i + KH : i;
+        const uint32_t w = merge_halves(va[i], va[kb]);
+        if (wr && (hh == 0 || i + KH < VB)) {
+          uint32_t* p = vtile + (hh ? kb : i) * D + 32 * mb + li;
+          *p = vm == 0xffffffffu ? w : (*p & ~vm) | (w & vm);
+        }
+      }
+    });
     if constexpr (ONE) break;
   }
 }
@@ -1237,8 +1250,9 @@ __global__ __launch_bounds__(kThreads, PAGED ? 2 : 4) void append_v_mfma(
     int64_t ntiles, const float* __restrict__ pi, Half bnd, uint32_t* __restrict__ vst,
     float* __restrict__ vnorm, int64_t t_stride, int64_t t0, QkvPages pg) {
   __shared__ uint4 frag[FROM_Y ? 1 : frag_n<D>()];  // Pi operand fragments
+  __shared__ float4 inv_s[kWaves][kTok / 4];         // 1 / norm of each wave's tokens
   append_v_run<VB, XT, D, PAGED, FROM_Y>(xin, nin, S, tpg, ntiles, pi, bnd, vst, vnorm, t_stride,
-                                         t0, pg, frag, blockIdx.x, gridDim.x);
+                                         t0, pg, frag, inv_s, blockIdx.x, gridDim.x);
 }
 
 // append_v_mfma over the contiguous stores of blockIdx.y's layer
@@ -1248,10 +1262,11 @@ __global__ __launch_bounds__(kThreads, 4) void append_v_layers(AppendLayers al, 
                                                                Half bnd, int64_t t_stride,
                                                                int64_t t0) {
   __shared__ uint4 frag[frag_n<D>()];
+  __shared__ float4 inv_s[kWaves][kTok / 4];
   const int l = blockIdx.y;
   append_v_run<VB, XT, D, false, false>(al.x[l], nullptr, S, tpg, ntiles, al.pi[l], bnd,
                                         static_cast<uint32_t*>(al.st[l]), al.nrm[l], t_stride,
-                                        t0, QkvPages{}, frag, blockIdx.x, gridDim.x);
+                                        t0, QkvPages{}, frag, inv_s, blockIdx.x, gridDim.x);
 }
 
 }  // namespace

@@ -23,17 +23,17 @@ __global__ __launch_bounds__(kThreads, 4) void append_kv_layers(
     int64_t vtpg, int64_t vntiles, Half fine, Half bnd, int64_t t_stride, int64_t t0,
     int nsplit) {
   __shared__ uint4 frag[frag_n<D>()];         // the running half's Pi fragments
-  __shared__ float4 inv_s[kWaves][kTok / 4];  // key half: 1 / norm of each wave's tokens
+  __shared__ float4 inv_s[kWaves][kTok / 4];  // value half: 1 / norm of each wave's tokens
   const int l = blockIdx.y, b = blockIdx.x;
   if (b < kblocks)
     append_k_run<MB, XT, D, false, false, true>(ak.x[l], nullptr, S, ktpg, kntiles, ak.pi[l],
                                           ak.signs[l], fine, static_cast<uint8_t*>(ak.st[l]),
-                                          ak.nrm[l], t_stride, t0, QkvPages{}, frag, inv_s, b,
+                                          ak.nrm[l], t_stride, t0, QkvPages{}, frag, b,
                                           kblocks, nsplit);
   else
     append_v_run<VB, XT, D, false, false, true>(av.x[l], nullptr, S, vtpg, vntiles, av.pi[l], bnd,
                                           static_cast<uint32_t*>(av.st[l]), av.nrm[l], t_stride,
-                                          t0, QkvPages{}, frag, b - kblocks,
+                                          t0, QkvPages{}, frag, inv_s, b - kblocks,
                                           static_cast<int>(gridDim.x) - kblocks, nsplit);
 }
 
@@ -50,11 +50,11 @@ __global__ __launch_bounds__(kThreads, 2) void append_kv_paged(
   const int b = blockIdx.x;
   if (b < kblocks)
     append_k_run<MB, XT, D, true, false, true>(keys, nullptr, S, ktpg, kntiles, kpi, signs, fine,
-                                               kpool, knorm, t_stride, t0, pg, frag, inv_s, b,
+                                               kpool, knorm, t_stride, t0, pg, frag, b,
                                                kblocks, nsplit);
   else
     append_v_run<VB, XT, D, true, false, true>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vpool,
-                                               vnorm, t_stride, t0, pg, frag, b - kblocks,
+                                               vnorm, t_stride, t0, pg, frag, inv_s, b - kblocks,
                                                static_cast<int>(gridDim.x) - kblocks, nsplit);
 }
 
@@ -77,8 +77,9 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmixv(
                                         nsplit);
   else
     append_v_run<VB, XT, kD, false, false, true>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vst,
-                                           vnorm, t_stride, t0, QkvPages{}, frag, b - kblocks,
-                                           static_cast<int>(gridDim.x) - kblocks, nsplit);
+                                           vnorm, t_stride, t0, QkvPages{}, frag, inv_s,
+                                           b - kblocks, static_cast<int>(gridDim.x) - kblocks,
+                                           nsplit);
 }
 
 }  // namespace
