@@ -525,7 +525,7 @@ uint32_t prep_lds() {
 // RC row chunks (of 4 query rows) per workgroup: with RC = 2 (GQA groups of
 // 5..8 rows at d = 64) each K/V operand expanded from the store feeds two
 // MFMAs, and the split's K/V bytes are read once for 8 rows.
-template <int D, int MB, int VB, int RC>
+template <int D, int MB, int VB, int RC, bool RANGES>
 __global__ __launch_bounds__(256, 4) void split_mfma(
     const qkv_v4i* __restrict__ aq, const float* __restrict__ rowc, KVLayers kv, int Bl,
     int64_t t_stride, int64_t T, int Hkv, int R, int Q, int chunks, float scale, int causal,
@@ -575,10 +575,11 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
   const int64_t ts = int64_t(split) * split_len;
   const int64_t te = min<int64_t>(T, ts + split_len);
   const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
-  // the sequence's attended keys, split-relative: [slo, shi)
+  // the sequence's attended keys, split-relative: [slo, shi) (RANGES: the
+  // store has per-sequence key ranges)
   const SeqRange sr = seq_range(kv, bseq, T);
-  const int slo = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.lo - ts)));
-  const int shi = static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.hi - ts)));
+  const int slo = RANGES ? static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.lo - ts))) : 0;
+  const int shi = RANGES ? static_cast<int>(min<int64_t>(ntok, max<int64_t>(0, sr.hi - ts))) : ntok;
 
   // ---------------- phase 1: scores of every token of the split -> LDS
   qkv_v4i a[RC][NU];
@@ -679,7 +680,9 @@ __global__ __launch_bounds__(256, 4) void split_mfma(
 #pragma unroll
     for (int sub = 0; sub < 4; ++sub) {
       const int tl = tile * 64 + sub * 16 + ln;
-      const bool in = tl >= slo && tl < shi && ((page_okm >> tile) & 1u);
+      // (without ranges the bound is the split's length alone: the register
+      // allocation of this loop has no room for the lower bound)
+      const bool in = (RANGES ? tl >= slo && tl < shi : tl < ntok) && ((page_okm >> tile) & 1u);
 #pragma unroll
       for (int c = 0; c < RC; ++c) {
         const float z = static_cast<float>(acc[c][sub][0]) +
@@ -1501,6 +1504,444 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   }
 }
 
+// ------------------------------------------------------------ small decode, d = 64
+//
+// The decode step at head_dim 64 (IP keys of 1-2 MSE bits, value bits 1-4,
+// symmetric codebooks) over many short sequences -- a model's layers in one
+// call -- as one launch.  A workgroup of 4 waves takes one (sequence, kv
+// head, RC chunks of 4 query rows) over a split of its tokens:
+//   prologue: q~ = q Pi^T and the int8 digit operands of the scores
+//     (prepare_mfma's work, the same operand layout) for its 4 RC rows;
+//   then chunks of 256 tokens, two workgroup barriers each:
+//     A  wave w scores tile w of the chunk on the integer MFMA (split_mfma's
+//        plane operands) into LDS, with the tile's row and value-norm maxima;
+//     B  the running row maxima; wave w turns rows w, w + 4 of the chunk's
+//        scores into p = 2^(s - m) and the value product's int8 digits (a
+//        per-chunk fixed point), in place;
+//     C  wave w accumulates the chunk's value product for coordinates
+//        16 w .. 16 w + 15 (exact integers) and merges it into its running
+//        fp32 O~: online softmax across chunks;
+//   the next chunk's K rows load during A..C and its V planes during C, the
+//   scores alternate between two LDS buffers;
+//   epilogue: with one split, O~ / max(l, 1e-8) un-rotated by Pi into the
+//   output; otherwise split partials for combine_kernel.
+// With one split per (sequence, kv head) a 24-layer cfg2 batch is one round
+// of workgroups (three per CU), each streaming its 2,048 tokens.
+constexpr int kChunkS = 256;  // tokens per chunk: one 64-token tile per wave
+
+template <int MB, int VB, int RC, bool PAGED>
+__global__ __launch_bounds__(256, 3) void decode_small(
+    QLayers ql, KVLayers kv, OutLayers ol, int Bl, int q_dtype, float alpha, int Hq, int Hkv,
+    int Q, int R, int cgroups, Tables tb, int64_t t_stride, int64_t T, float scale, int causal,
+    int64_t split_len, int final_out, int out_dtype, float* __restrict__ part_o,
+    float* __restrict__ part_ml) {
+  constexpr int D = 64;
+  constexpr int NPL = MB + 1;            // K-row planes: MSE bits, QJL
+  constexpr int KRB = NPL * D / 8;       // K row bytes
+  constexpr int NU = NPL;                // score MFMAs per 16 tokens
+  constexpr int NP = n_odd_subsets(VB);  // value planes
+  constexpr int RW = kRowsM * RC;        // query rows per workgroup
+  constexpr int PR = D + 4;              // padded Pi row (floats)
+  static_assert(MB == 1 || MB == 2, "key MSE bits");
+  static_assert(RC == 1 || RC == 2, "row chunks");
+
+  __shared__ __align__(16) float pis[D * PR];          // Pi rows (query side, then values')
+  __shared__ __align__(16) float qs[RW][D];            // query rows; O~ / l in the epilogue
+  __shared__ __align__(16) uint32_t stage[RC * NU * 256];  // score operand image
+  __shared__ __align__(16) float sbuf[2][4][RW][64];   // scores -> value digits, per chunk
+  __shared__ float vns[2][kChunkS];                     // value norms of the chunk's tokens
+  __shared__ float red_m[4][RW];
+  __shared__ float red_v[4];
+  __shared__ float rowcs[RW][2];                        // score row constants
+  __shared__ float rsc[RW], mls[RW][2];
+  __shared__ int fvs;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int G = Hq / Hkv;
+  const int split = blockIdx.x;
+  const int hkv = blockIdx.y / cgroups, cgi = blockIdx.y - hkv * cgroups;
+  const int bz = blockIdx.z;  // over the batch of all layers
+  const int layer = bz / Bl, b = bz - layer * Bl;
+  const int r0 = cgi * RW;
+  const int nr = min(RW, R - r0);
+  const int64_t bh = int64_t(b) * Hkv + hkv;  // in the layer's store
+  const int64_t ts = int64_t(split) * split_len;
+  const int64_t te = min<int64_t>(T, ts + split_len);
+  const int ntok = te > ts ? static_cast<int>(te - ts) : 0;
+  const int ntile = (ntok + 63) >> 6;
+  const int nch = (ntok + kChunkS - 1) / kChunkS;
+  const uint8_t* __restrict__ kst = kv.kst[layer];
+  const float* __restrict__ knorm = kv.knorm[layer];
+  const uint32_t* __restrict__ vst = kv.vst[layer];
+  const float* __restrict__ vnorm = kv.vnorm[layer];
+
+  // ---- prologue: Pi and the query rows into LDS
+  {
+    const float4* src = reinterpret_cast<const float4*>(ql.pi[layer]);
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int i = tid + 256 * x, row = i >> 4, c4 = i & 15;
+      reinterpret_cast<float4*>(pis + row * PR)[c4] = src[i];
+    }
+#pragma unroll
+    for (int x = 0; x < RC; ++x) {
+      const int i = tid + 256 * x, r = i >> 6, j = i & 63;
+      float v = 0.f;
+      if (r < nr) {
+        const int row = r0 + r;
+        const int g = row / Q, qi = row - g * Q;
+        v = qkv_load(ql.q[layer], ((int64_t(b) * Hq + hkv * G + g) * Q + qi) * D + j, q_dtype);
+      }
+      qs[r][j] = v;
+    }
+  }
+  // the first chunk's loads fly during the prologue's arithmetic
+  typedef const __attribute__((address_space(4))) int32_t* ctab_t;
+  auto tile_row = [&](int tile) -> int64_t {  // first store row of the split's tile
+    const int tc = ntile > 0 ? min(tile, ntile - 1) : 0;
+    if constexpr (PAGED) {
+      const ctab_t ptab = (ctab_t)kv.ptab;
+      const int tsh = kv.plg - 6;
+      const int gt = static_cast<int>(ts >> 6) + tc;
+      int pg = ptab[int64_t(b) * kv.pmax + (gt >> tsh)];
+      if (pg < 0 || pg >= kv.npages) pg = 0;  // outside the pool: read page 0, masked
+      return ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
+    } else {
+      return bh * t_stride + ts + int64_t(tc) * 64;
+    }
+  };
+  auto page_ok = [&](int tile) -> bool {
+    if constexpr (PAGED) {
+      const ctab_t ptab = (ctab_t)kv.ptab;
+      const int gt = static_cast<int>(ts >> 6) + tile;
+      const int pg = ptab[int64_t(b) * kv.pmax + (gt >> (kv.plg - 6))];
+      return pg >= 0 && pg < kv.npages;
+    } else {
+      return true;
+    }
+  };
+  // per-tile bases are wave-uniform; lanes add fixed 32-bit offsets
+  uint32_t kd[4][NU];
+  float kn[4], vv[4];
+  const uint32_t koff = ln * (KRB / 4) + (lg >> 1);  // dwords into a tile's K rows
+  auto loadK = [&](int tile) {
+    const int64_t rb = tile_row(tile);
+    const uint32_t* kb = reinterpret_cast<const uint32_t*>(kst + rb * KRB);
+    const float* knb = knorm + rb;
+    const float* vnb = vnorm + rb;
+#pragma unroll
+    for (int sub = 0; sub < 4; ++sub) {
+#pragma unroll
+      for (int u = 0; u < NU; ++u) kd[sub][u] = ldnt(kb + koff + sub * 16 * (KRB / 4) + 2 * u);
+      kn[sub] = ldnt(knb + sub * 16 + ln);
+      vv[sub] = ldnt(vnb + sub * 16 + ln);
+    }
+  };
+  const int blk = lg >> 1, hsh = 4 * (lg & 1);
+  const int vj = 16 * wave + ln;  // this lane's value coordinate
+  const uint32_t voff = blk * VB * D + vj;  // words into a tile's V planes
+  uint32_t vw[4][VB];
+  auto loadV = [&](int slot, int tile) {
+    const uint32_t* vb = vst + (tile_row(tile) >> 5) * (VB * D);  // the tile's first V tile
+#pragma unroll
+    for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * D);
+  };
+  if (nch > 0) {
+    loadK(wave);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) loadV(t, t);
+  }
+  __syncthreads();
+
+  // ---- prologue math: q~, the digit operands and row constants (wave w: rows w, w + 4)
+  float kgmax = alpha;
+#pragma unroll
+  for (int r = 0; r < MB; ++r) kgmax = fmaxf(kgmax, fabsf(tb.kg[r]));
+  const float sgn = ql.signs[layer][lane];
+  uint8_t* sb = reinterpret_cast<uint8_t*>(stage);
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const int r = kRowsM * c + wave;
+    const float qj = qs[r][lane];
+    const float nq = wave_sum_dpp(qj * qj);
+    float v = 0.f;  // q~_j = sum_k q_k Pi[j][k], j = lane
+    const float4* prow = reinterpret_cast<const float4*>(pis + lane * PR);
+#pragma unroll
+    for (int k4 = 0; k4 < D / 4; ++k4) {
+      const float4 p4 = prow[k4];
+      const float4 q4 = reinterpret_cast<const float4*>(qs[r])[k4];
+      v = fmaf(q4.x, p4.x, v);
+      v = fmaf(q4.y, p4.y, v);
+      v = fmaf(q4.z, p4.z, v);
+      v = fmaf(q4.w, p4.w, v);
+    }
+    const float w = alpha * fabsf(v) * sgn;
+    const float wmax = 2.f * kgmax * sqrtf(nq);
+    int ex = 0;
+    if (wmax > 0.f) frexpf(wmax, &ex);
+    const int fq = wmax > 0.f ? 30 - ex : 0;  // |Z| < 2^30
+    // digit bytes of weight W at row bit p (the operand layout of prepare_mfma, D = 64)
+    auto put8 = [&](int p, float W) {
+      const int i = p & 7;
+      int Z = static_cast<int>(rintf(ldexpf(W, fq - i)));
+      if (i == 7) Z = -Z;
+      const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+      const int w32 = p >> 5, e = i & 3, beta = (p >> 3) & 3;
+      const int g = 2 * (w32 & 1) + (i >> 2), u = w32 >> 1;
+      const int base = c * NU * 1024 + ((u * 64 + 16 * g + 4 * wave) * 4 + e) * 4 + beta;
+#pragma unroll
+      for (int dv = 0; dv < 4; ++dv) sb[base + 16 * dv] = static_cast<uint8_t>(dg >> (8 * dv));
+    };
+#pragma unroll
+    for (int pl = 0; pl < MB; ++pl) put8(pl * D + lane, 2.f * tb.kg[pl] * v);
+    put8(MB * D + lane, 2.f * w);
+    const float sq = wave_sum_dpp(v);
+    const float sw = wave_sum_dpp(w);
+    if (lane == 0) {
+      rowcs[r][0] = tb.kconst * sq - sw;
+      rowcs[r][1] = ldexpf(1.f, -fq);
+    }
+  }
+  __syncthreads();
+  // the score operands stay in LDS (read back each chunk: registers)
+  const qkv_v4i* aop = reinterpret_cast<const qkv_v4i*>(stage) + lane;
+  float cr[RC], fqs[RC], mrun[RC], lrun[RC], orun[RC];
+  bool row_ok[RC];
+  int clim[RC];
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    const int rl = kRowsM * c + lg;  // this lane's row in the score phase
+    cr[c] = rowcs[rl][0];
+    fqs[c] = rowcs[rl][1];
+    row_ok[c] = rl < nr;
+    const int qi = (r0 + rl) % Q;
+    const int64_t climit = causal ? (T - Q + qi - ts) : int64_t(INT_MAX);
+    clim[c] = static_cast<int>(max<int64_t>(-1, min<int64_t>(climit, INT_MAX)));
+    mrun[c] = kMFloor;  // phase B: rows wave + 4 c
+    lrun[c] = 0.f;
+    orun[c] = 0.f;      // phase C: rows lg + 4 c, coordinate vj
+  }
+  const float scale2 = scale * 1.4426950408889634f;  // scores in log2 units
+  const int ii = lane & 7;
+  // token (lane) of a 64-token tile -> K position of the value MFMA:
+  // lane = 32 blk + 8 beta + i, K = 16 (2 blk + i / 4) + 4 (i % 4) + beta
+  const int kpos = 16 * (2 * (lane >> 5) + (ii >> 2)) + 4 * (ii & 3) + ((lane & 31) >> 3);
+
+  for (int ch = 0; ch < nch; ++ch) {
+    const int buf = ch & 1;
+    // ---- A: scores of tile `wave` of the chunk
+    const int tile = ch * 4 + wave;
+    {
+      qkv_v4i acc[RC][4];
+#pragma unroll
+      for (int c = 0; c < RC; ++c)
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) acc[c][sub] = qkv_v4i{0, 0, 0, 0};
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        qkv_v4i au[RC];
+#pragma unroll
+        for (int c = 0; c < RC; ++c) au[c] = aop[(c * NU + u) * 64];
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+          const uint32_t x = kd[sub][u];
+          qkv_v4i bo;
+          bo[0] = static_cast<int>(x & (0x01010101u << hsh));
+          bo[1] = static_cast<int>(x & (0x02020202u << hsh));
+          bo[2] = static_cast<int>(x & (0x04040404u << hsh));
+          bo[3] = static_cast<int>(x & (0x08080808u << hsh));
+#pragma unroll
+          for (int c = 0; c < RC; ++c) acc[c][sub] = mfma_i8(au[c], bo, acc[c][sub]);
+        }
+      }
+      float knt[4], vvt[4];
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        knt[sub] = kn[sub];
+        vvt[sub] = vv[sub];
+      }
+      if (ch + 1 < nch) loadK(tile + 4);  // the slot is free: the next chunk's tile
+      mfma_settle();
+      const bool pin = tile < ntile && page_ok(ntile > 0 ? min(tile, ntile - 1) : 0);
+      float mloc[RC], vmax = 0.f;
+#pragma unroll
+      for (int c = 0; c < RC; ++c) mloc[c] = -INFINITY;
+#pragma unroll
+      for (int sub = 0; sub < 4; ++sub) {
+        const int tl = tile * 64 + sub * 16 + ln;
+        const bool in = pin && tl < ntok;
+#pragma unroll
+        for (int c = 0; c < RC; ++c) {
+          // digits in two exact int32 halves (|acc| < 2^21), one rounding each
+          const int zlo = __mul24(acc[c][sub][1], 256) + acc[c][sub][0];
+          const int zhi = __mul24(acc[c][sub][3], 256) + acc[c][sub][2];
+          const float z = fmaf(static_cast<float>(zhi), 65536.f, static_cast<float>(zlo));
+          const float sc0 = knt[sub] * scale2 * fmaf(z, fqs[c], cr[c]);
+          const float sc = (in & row_ok[c] & (tl <= clim[c])) ? sc0 : -INFINITY;
+          sbuf[buf][wave][kRowsM * c + lg][sub * 16 + ln] = sc;
+          mloc[c] = fmaxf(mloc[c], sc);
+        }
+        const float vz = in ? vvt[sub] : 0.f;
+        vns[buf][wave * 64 + sub * 16 + ln] = vz;  // the four lane groups store the same value
+        vmax = fmaxf(vmax, vz);
+      }
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        mloc[c] = row_max_last(mloc[c]);  // the 16 lanes of a row: max in lane 15
+        if (ln == 15) red_m[wave][kRowsM * c + lg] = mloc[c];
+      }
+      vmax = wave_max_dpp(vmax);
+      if (lane == 0) red_v[wave] = vmax;
+    }
+    __syncthreads();
+    // ---- B: running maxima, p = 2^(s - m) and value digits of rows wave + 4 c
+    {
+      const float vmx = fmaxf(fmaxf(red_v[0], red_v[1]), fmaxf(red_v[2], red_v[3]));
+      int ev = 0;
+      if (vmx > 0.f) frexpf(vmx, &ev);
+      const int Fv = vmx > 0.f ? 29 - ev : 0;  // vmx 2^Fv < 2^29
+      const float zscale = ldexpf(1.f, Fv - ii);  // Z_t s_t = X 2^i, X = round(p' 2^(Fv - i))
+      uint8_t* pbase = reinterpret_cast<uint8_t*>(&sbuf[buf][0][0][0]);
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        const int row = kRowsM * c + wave;
+        const float mc = fmaxf(fmaxf(red_m[0][row], red_m[1][row]),
+                               fmaxf(red_m[2][row], red_m[3][row]));
+        const float mnew = fmaxf(mrun[c], mc);
+        const float rs = __builtin_amdgcn_exp2f(mrun[c] - mnew);
+        mrun[c] = mnew;
+        float lsum = 0.f;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const float p = __builtin_amdgcn_exp2f(sbuf[buf][tt][row][lane] - mnew);
+          lsum += p;
+          const int X = static_cast<int>(fmaf(p * vns[buf][tt * 64 + lane], zscale, 0.5f));
+          const int Z = ii == 7 ? -X : X;
+          // signed base-256 digits: byte v of (Z + 0x808080) ^ 0x808080
+          const uint32_t dg = (static_cast<uint32_t>(Z) + 0x808080u) ^ 0x808080u;
+          uint8_t* dst = pbase + (tt * RC + c) * 1024 + (4 * wave) * 64 + kpos;
+          dst[0] = static_cast<uint8_t>(dg);
+          dst[64] = static_cast<uint8_t>(dg >> 8);
+          dst[128] = static_cast<uint8_t>(dg >> 16);
+          dst[192] = static_cast<uint8_t>(dg >> 24);
+        }
+        lsum = wave_sum_dpp(lsum);
+        lrun[c] = fmaf(lrun[c], rs, lsum);
+        if (lane == 0) rsc[row] = rs;
+      }
+      if (tid == 0) fvs = Fv;
+    }
+    __syncthreads();
+    // ---- C: the chunk's value product for coordinate vj, merged into O~
+    {
+      const uint8_t* pbase = reinterpret_cast<const uint8_t*>(&sbuf[buf][0][0][0]);
+      qkv_v4i ones;  // an all-ones plane as the operand's bytes (b * 2^i, i = bit in byte)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ones[e] = static_cast<int>(0x01010101u << (e + hsh));
+      qkv_v4i acc2[RC][NP], accU[RC];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        qkv_v4i bq[RC];
+#pragma unroll
+        for (int c = 0; c < RC; ++c)
+          bq[c] = *reinterpret_cast<const qkv_v4i*>(pbase + (tt * RC + c) * 1024 + ln * 64 + lg * 16);
+#pragma unroll
+        for (int s = 0; s < NP; ++s) {
+          const uint32_t subs = odd_subset(VB, s);
+          uint32_t pw = 0;
+#pragma unroll
+          for (int k = 0; k < VB; ++k)
+            if (subs & (1u << k)) pw ^= vw[tt][k];
+          qkv_v4i av;
+          av[0] = static_cast<int>(pw & (0x01010101u << hsh));
+          av[1] = static_cast<int>(pw & (0x02020202u << hsh));
+          av[2] = static_cast<int>(pw & (0x04040404u << hsh));
+          av[3] = static_cast<int>(pw & (0x08080808u << hsh));
+#pragma unroll
+          for (int c = 0; c < RC; ++c)  // C[row x digit][coordinate]
+            acc2[c][s] = mfma_i8(bq[c], av, tt == 0 ? qkv_v4i{0, 0, 0, 0} : acc2[c][s]);
+        }
+#pragma unroll
+        for (int c = 0; c < RC; ++c)
+          accU[c] = mfma_i8(bq[c], ones, tt == 0 ? qkv_v4i{0, 0, 0, 0} : accU[c]);
+        if (ch + 1 < nch) loadV(tt, (ch + 1) * 4 + tt);
+      }
+      // sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U) per digit half in exact
+      // int32 (|acc| < 2^20 for a 256-token chunk), then fp32
+      mfma_settle();
+      const float oscale = ldexpf(1.f, -fvs);
+#pragma unroll
+      for (int c = 0; c < RC; ++c) {
+        const int row = kRowsM * c + lg;
+        const int nulo = -(__mul24(accU[c][1], 256) + accU[c][0]);
+        const int nuhi = -(__mul24(accU[c][3], 256) + accU[c][2]);
+        float val = 0.f;
+#pragma unroll
+        for (int s = 0; s < NP; ++s) {
+          const int lo = 2 * (__mul24(acc2[c][s][1], 256) + acc2[c][s][0]) + nulo;
+          const int hi = 2 * (__mul24(acc2[c][s][3], 256) + acc2[c][s][2]) + nuhi;
+          val = fmaf(tb.vg[s], fmaf(static_cast<float>(hi), 65536.f, static_cast<float>(lo)), val);
+        }
+        orun[c] = fmaf(orun[c], rsc[row], val * oscale);
+      }
+    }
+  }
+
+  // ---- epilogue: (m, l) of rows wave + 4 c to LDS, then output or partials
+#pragma unroll
+  for (int c = 0; c < RC; ++c) {
+    if (lane == 0) {
+      mls[kRowsM * c + wave][0] = mrun[c];
+      mls[kRowsM * c + wave][1] = lrun[c];
+    }
+  }
+  __syncthreads();
+  if (final_out && gridDim.x == 1) {
+    // out = (O~ / max(l, 1e-8)) Pi_v
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const int row = kRowsM * c + lg;
+      qs[row][vj] = row < nr ? orun[c] / fmaxf(mls[row][1], 1e-8f) : 0.f;
+    }
+    const float* piv = ol.pi[layer];
+    if (piv != ql.pi[layer]) {
+      const float4* src = reinterpret_cast<const float4*>(piv);
+#pragma unroll
+      for (int x = 0; x < 4; ++x) {
+        const int i = tid + 256 * x, row = i >> 4, c4 = i & 15;
+        reinterpret_cast<float4*>(pis + row * PR)[c4] = src[i];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const int r = kRowsM * c + wave;
+      if (r < nr) {
+        float o = 0.f;
+#pragma unroll 16
+        for (int k = 0; k < D; ++k) o = fmaf(qs[r][k], pis[k * PR + lane], o);
+        const int row = r0 + r;
+        const int g = row / Q, qi = row - g * Q;
+        qkv_store(ol.out[layer], ((int64_t(b) * Hq + hkv * G + g) * Q + qi) * D + lane, o,
+                  out_dtype);
+      }
+    }
+  } else {
+    const int64_t base = ((int64_t(split) * gridDim.z + bz) * Hkv + hkv) * R + r0;
+#pragma unroll
+    for (int c = 0; c < RC; ++c) {
+      const int row = kRowsM * c + lg;
+      if (row < nr) part_o[(base + row) * D + vj] = orun[c];
+    }
+    if (tid < nr) {
+      part_ml[(base + tid) * 2 + 0] = mls[tid][0] * 0.6931471805599453f;  // log2 -> natural units
+      part_ml[(base + tid) * 2 + 1] = mls[tid][1];
+    }
+  }
+}
+
 // ------------------------------------------------------------ combine
 
 constexpr int kRowsC = 4;       // query rows merged per block (many rows)
@@ -2102,9 +2543,9 @@ int mfma_blocks_per_cu(int64_t split_len, int rc) {
     int v = 0;
     const size_t smem = static_cast<size_t>(mfma_smem_bytes(nt * 64, rc));
     const hipError_t e =
-        rc == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 2>, 256,
+        rc == 2 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 2, false>, 256,
                                                                smem)
-                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 1>, 256,
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, split_mfma<64, 2, 3, 1, false>, 256,
                                                                smem);
     if (e != hipSuccess || v <= 0) v = 1;
     slot = v;
@@ -2131,6 +2572,58 @@ bool use_fused(const Tables& tb, int d, int64_t t_stride) {
 // too (use_fused), with the split count of this model.
 bool use_mfma_path(const Tables& tb, int d, int64_t t_stride, int64_t T, int n_splits) {
   return d == 64 ? use_mfma(tb, d, t_stride, T, n_splits) : use_fused(tb, d, t_stride);
+}
+
+// Launch decode_small over nl layers (d = 64, key MSE bits 1-2; B sequences
+// each; workspace for B * nl): final_out with one split writes the output
+// (ol), otherwise split partials for combine_layers.
+int launch_small(const QLayers& ql, const KVLayers& kv, const OutLayers& ol, int nl, int B,
+                 int q_dtype, float alpha, int Hq, int Hkv, int Q, int mbits, int vbits,
+                 const Tables& tb, int64_t t_stride, int64_t T, float scale, int causal,
+                 int n_splits, int final_out, int out_dtype, void* workspace, hipStream_t s) {
+  const int R = (Hq / Hkv) * Q;
+  const int rc = R > kRowsM ? 2 : 1;
+  const int cgroups = (R + kRowsM * rc - 1) / (kRowsM * rc);
+  const WsLayout L = ws_layout(B * nl, Hkv, R, 64, n_splits);
+  const int64_t split_len = ((T + n_splits - 1) / n_splits + 63) / 64 * 64;
+  const dim3 grid(n_splits, Hkv * cgroups, B * nl);
+  float* po = at<float>(workspace, L.po);
+  float* pml = at<float>(workspace, L.pml);
+#define QKV_SM(MBV, VBV, RCV)                                                                   \
+  do {                                                                                          \
+    if (kv.ptab)                                                                                \
+      hipLaunchKernelGGL((decode_small<MBV, VBV, RCV, true>), grid, dim3(256), 0, s, ql, kv,   \
+                         ol, B, q_dtype, alpha, Hq, Hkv, Q, R, cgroups, tb, t_stride, T, scale, \
+                         causal, split_len, final_out, out_dtype, po, pml);                     \
+    else                                                                                        \
+      hipLaunchKernelGGL((decode_small<MBV, VBV, RCV, false>), grid, dim3(256), 0, s, ql, kv,  \
+                         ol, B, q_dtype, alpha, Hq, Hkv, Q, R, cgroups, tb, t_stride, T, scale, \
+                         causal, split_len, final_out, out_dtype, po, pml);                     \
+  } while (0)
+#define QKV_SMV(MBV, RCV)                  \
+  switch (vbits) {                         \
+    case 1: QKV_SM(MBV, 1, RCV); break;    \
+    case 2: QKV_SM(MBV, 2, RCV); break;    \
+    case 3: QKV_SM(MBV, 3, RCV); break;    \
+    default: QKV_SM(MBV, 4, RCV); break;   \
+  }
+  if (mbits == 1) {
+    if (rc == 2) {
+      QKV_SMV(1, 2)
+    } else {
+      QKV_SMV(1, 1)
+    }
+  } else {
+    if (rc == 2) {
+      QKV_SMV(2, 2)
+    } else {
+      QKV_SMV(2, 1)
+    }
+  }
+#undef QKV_SMV
+#undef QKV_SM
+  QKV_LAUNCHED();
+  return QKV_OK;
 }
 
 // Launch decode_fused over nl layers (B sequences each; workspace for B * nl)
@@ -2432,15 +2925,22 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
     const dim3 grid(n_splits, Hkv * ((chunks + rc - 1) / rc), B * nl);
     const qkv_v4i* aq = at<qkv_v4i>(workspace, L.aq);
     const float* rowc = at<float>(workspace, L.rowc);
-#define QKV_MF(DD, MB, VB, RCV)                                                                \
-  do {                                                                                         \
-    if (smem > 65536)                                                                          \
-      QKV_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(&split_mfma<DD, MB, VB, RCV>), \
-                                  hipFuncAttributeMaxDynamicSharedMemorySize,                  \
-                                  static_cast<int>(smem)));                                    \
-    hipLaunchKernelGGL((split_mfma<DD, MB, VB, RCV>), grid, dim3(256),                         \
-                       static_cast<uint32_t>(smem), s, aq, rowc, kv, B, t_stride, T, Hkv, R,   \
-                       Q, chunks, scale, causal, split_len, tb, po, pml);                      \
+#define QKV_MF2(DD, MB, VB, RCV, RG)                                                            \
+  do {                                                                                          \
+    if (smem > 65536)                                                                           \
+      QKV_HIP(hipFuncSetAttribute(                                                              \
+          reinterpret_cast<const void*>(&split_mfma<DD, MB, VB, RCV, RG>),                      \
+          hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)));                  \
+    hipLaunchKernelGGL((split_mfma<DD, MB, VB, RCV, RG>), grid, dim3(256),                      \
+                       static_cast<uint32_t>(smem), s, aq, rowc, kv, B, t_stride, T, Hkv, R,    \
+                       Q, chunks, scale, causal, split_len, tb, po, pml);                       \
+  } while (0)
+#define QKV_MF(DD, MB, VB, RCV)                  \
+  do {                                           \
+    if (kv.klo || kv.khi)                        \
+      QKV_MF2(DD, MB, VB, RCV, true);            \
+    else                                         \
+      QKV_MF2(DD, MB, VB, RCV, false);           \
   } while (0)
 #define QKV_MFD(DD, RCV)                           \
   switch (kbits * 10 + vbits) {                    \
@@ -2460,6 +2960,7 @@ int partial_layers(const KVLayers& kv, int nl, int64_t t_stride, int64_t T, int3
     }
 #undef QKV_MFD
 #undef QKV_MF
+#undef QKV_MF2
     QKV_LAUNCHED();
     return QKV_OK;
   }
@@ -2835,11 +3336,10 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   int st = validate_common(B * n_layers, Hq, Hkv, Q, d, n_splits, workspace, ws_bytes);
   if (st != QKV_OK) return st;
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
-  // d = 64 batches run the split path (its two row chunks per workgroup read a
-  // 5-8-row GQA group's K/V once) where it takes the shape (key MSE bits <= 2,
-  // splits of at most kSplitMax tokens), decode_fused otherwise, as every
-  // other head dim
-  const bool split64 = d == 64 && use_mfma(tb, d, t_stride, T, n_splits);
+  // d = 64 batches run decode_small (its two row chunks per workgroup read a
+  // 5-8-row GQA group's K/V once) where it takes the shape (key MSE bits <= 2),
+  // decode_fused otherwise, as every other head dim
+  const bool split64 = d == 64 && tb.mfma_ok && t_stride % 64 == 0;
   if (!split64 && !use_fused(tb, d, t_stride)) {
     qkv_set_error("layer-batched decode runs on the MFMA path (symmetric codebooks, key MSE "
                   "bits <= 3, capacity a multiple of 64)");
@@ -2864,7 +3364,20 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
   kv.plg = plg;
   kv.npages = num_pages;
   auto s = static_cast<hipStream_t>(stream);
-  if (!split64) {
+  if (split64) {
+    // decode_small: one launch; one split per (sequence, kv head) where that
+    // gives at least two workgroups per CU, else the caller's split count
+    const int R = (Hq / Hkv) * Q;
+    const int rows_wg = R > kRowsM ? 2 * kRowsM : kRowsM;
+    const int64_t wgs = int64_t(B) * n_layers * Hkv * ((R + rows_wg - 1) / rows_wg);
+    const int ns = wgs >= 2 * int64_t(qkv_num_cus()) ? 1 : n_splits;
+    st = launch_small(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+                      t_stride, T, scale, causal, ns, 1, out_dtype, workspace, s);
+    if (st != QKV_OK || ns == 1) return st;
+    return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, ns,
+                          s);
+  }
+  {
     st = launch_fused(ql, kv, ol, n_layers, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
                       (d / 32) * (kbits + 1), vbits, tb,
                       t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, true, s);
@@ -2872,14 +3385,6 @@ static int decode_layers(int32_t n_layers, const void* const* q, int32_t q_dtype
     return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
                           n_splits, s);
   }
-  st = prepare_layers(ql, n_layers, q_dtype, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
-                      vcent_host, qjl_scale, workspace, ws_bytes, n_splits, s);
-  if (st != QKV_OK) return st;
-  st = partial_layers(kv, n_layers, t_stride, T, B, Hq, Hkv, Q, d, kbits, vbits, kcent_host,
-                      vcent_host, scale, causal, workspace, ws_bytes, n_splits, s);
-  if (st != QKV_OK) return st;
-  return combine_layers(ol, n_layers, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes,
-                        n_splits, s);
 }
 
 extern "C" int qkv_decode_attention_layers(

@@ -64,15 +64,16 @@ struct KVLayers {  // the store
   int64_t cbase;        // causal: query i sits at cbase - Q + i (0: at khi[b] - Q + i)
 };
 
-// The key range and causal position of sequence b (every layer shares them).
+// The key range and causal position of sequence b (every layer shares them),
+// for a workgroup-uniform b: the values are read into scalar registers.
 struct SeqRange {
   int64_t lo, hi;  // attended keys [lo, hi)
   int64_t cpos;    // causal: query i at cpos - Q + i sees keys t <= cpos - Q + i
 };
 __device__ __forceinline__ SeqRange seq_range(const KVLayers& kv, int64_t b, int64_t T) {
   SeqRange r;
-  r.lo = kv.klo ? max<int64_t>(0, kv.klo[b]) : 0;
-  r.hi = kv.khi ? min<int64_t>(T, kv.khi[b]) : T;
+  r.lo = kv.klo ? max<int64_t>(0, __builtin_amdgcn_readfirstlane(kv.klo[b])) : 0;
+  r.hi = kv.khi ? min<int64_t>(T, __builtin_amdgcn_readfirstlane(kv.khi[b])) : T;
   r.cpos = kv.cbase > 0 ? kv.cbase : r.hi;
   return r;
 }
