@@ -2772,30 +2772,15 @@ extern "C" int32_t qkv_attention_splits(int32_t B, int32_t Hq, int32_t Hkv, int3
   const int R = (Hq / Hkv) * Q;
   if (d == 128 || d == 96)
     return fused_splits(int64_t(B) * Hkv * ((R + kRowsM - 1) / kRowsM), T);
-  const int rc = mfma_rc(d, R);
+  // d = 64: decode_small (three workgroups per CU, 256-token chunks): enough
+  // splits for two workgroups per CU, of at least one chunk each (and at most
+  // kSplitMax tokens, the split kernel's LDS bound)
+  const int rc = R > kRowsM ? 2 : 1;
   const int64_t groups = int64_t(B) * Hkv * ((R + kRowsM * rc - 1) / (kRowsM * rc));
-  const int64_t min_s = (T + kSplitMax - 1) / kSplitMax;  // LDS-resident split length
-  const int64_t max_s = std::min<int64_t>((T + 63) / 64, 1024);
-  // Model: time ~ rounds x split length, rounds = ceil(workgroups / resident
-  // slots), slots from the occupancy at that split length.  Shorter splits
-  // raise occupancy (less LDS) but add per-split work; prefer >= 512 tokens.
-  int64_t best = std::max<int64_t>(min_s, 1);
-  double best_cost = 1e300;
-  for (int64_t c = std::max<int64_t>(min_s, 1); c <= max_s; ++c) {
-    const int64_t len = mfma_split_len(T, static_cast<int>(c));
-    if (len < 512 && c > min_s && c * 512 >= T) break;
-    const int64_t slots = int64_t(qkv_num_cus()) * mfma_blocks_per_cu(len, rc);
-    const int64_t wg = groups * c;
-    const int64_t rounds = (wg + slots - 1) / slots;
-    const double cost = static_cast<double>(rounds) * static_cast<double>(len + 256) /
-                        std::sqrt(static_cast<double>(std::min<int64_t>(slots / qkv_num_cus(), 4)));
-    if (cost < best_cost * 0.999) {
-      best_cost = cost;
-      best = c;
-    }
-    if (c > 64 * std::max<int64_t>(min_s, 1)) break;
-  }
-  return static_cast<int32_t>(std::max<int64_t>(best, 1));
+  const int64_t ncu = qkv_num_cus();
+  int64_t sp = std::min<int64_t>((2 * ncu + groups - 1) / groups, (T + kChunkS - 1) / kChunkS);
+  sp = std::max<int64_t>(sp, (T + kSplitMax - 1) / kSplitMax);
+  return static_cast<int32_t>(std::max<int64_t>(1, std::min<int64_t>(sp, 1024)));
 }
 
 extern "C" int64_t qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t Q,
@@ -3111,6 +3096,22 @@ int decode_attention_impl(const void* q, int32_t q_dtype, const uint8_t* kstore,
   kv.cbase = kr.cbase;
   auto s = static_cast<hipStream_t>(stream);
   const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+  if (d == 64 && tb.mfma_ok && t_stride % 64 == 0 && !kr.klo && !kr.khi && kr.cbase == 0) {
+    // decode_small: one launch (plus combine_kernel with several splits)
+    QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4),
+                "pi must be 16-byte and the store 4-byte aligned");
+    QLayers ql{};
+    ql.q[0] = q;
+    ql.pi[0] = pi;
+    ql.signs[0] = signs;
+    OutLayers ol{};
+    ol.pi[0] = pi;
+    ol.out[0] = out;
+    st = launch_small(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb, t_stride,
+                      T, scale, causal, n_splits, 1, out_dtype, workspace, s);
+    if (st != QKV_OK || n_splits == 1) return st;
+    return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits, s);
+  }
   if (use_fused(tb, d, t_stride)) {
     QKV_REQUIRE(qkv_aligned(pi, 16) && qkv_aligned(kstore, 4) && qkv_aligned(vstore, 4),
                 "pi must be 16-byte and the store 4-byte aligned");
@@ -3285,7 +3286,8 @@ extern "C" int qkv_paged_decode_attention(
   kv.pmax = pages_per_seq;
   kv.plg = plg;
   kv.npages = num_pages;
-  {  // decode_fused, as the contiguous single call
+  {  // the kernels of the contiguous single call: decode_small at d = 64 with
+     // key MSE bits <= 2, decode_fused otherwise
     QLayers ql{};
     ql.q[0] = q;
     ql.pi[0] = pi;
@@ -3294,6 +3296,14 @@ extern "C" int qkv_paged_decode_attention(
     ol.pi[0] = pi;
     ol.out[0] = out;
     auto s = static_cast<hipStream_t>(stream);
+    const Tables tb = make_tables(kcent_host, kbits, vcent_host, vbits);
+    if (d == 64 && tb.mfma_ok) {
+      st = launch_small(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, kbits, vbits, tb,
+                        t_stride, T, scale, causal, n_splits, 1, out_dtype, workspace, s);
+      if (st != QKV_OK || n_splits == 1) return st;
+      return combine_layers(ol, 1, B, Hq, Hkv, Q, d, out_dtype, workspace, ws_bytes, n_splits,
+                            s);
+    }
     st = launch_fused(ql, kv, ol, 1, B, q_dtype, qjl_scale, Hq, Hkv, Q, d,
                       (d / 32) * (kbits + 1), vbits,
                       make_tables(kcent_host, kbits, vcent_host, vbits), t_stride, T, scale,
