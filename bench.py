@@ -69,9 +69,23 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def host_cores() -> int:
+    """CPUs this process may run on: its affinity set, capped by a cgroup CPU
+    quota where one is set."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return max(1, n)
+
+
 def cpu_threads() -> int:
+    """torch CPU threads for the baselines: every core the process has."""
     import torch
-    torch.set_num_threads(min(os.cpu_count() or 1, 16))
+    torch.set_num_threads(host_cores())
     return torch.get_num_threads()
 
 
@@ -385,74 +399,109 @@ def paged_decode(args, dev, lib, sptr, stream, engines, queries, kc_h, vc_h, kv_
 
 
 def hf_decode_step(args, dev, stream):
-    """One decode step of cfg2's 24 layers (batch 16, 14 query / 2 kv heads,
-    head_dim 64, 2048 cached tokens, fp16 K/V) through the HF integrations:
-    the fused path (quashkv_amd.integrations.hf_attention: append the new
-    token, fused attention over the compressed cache) against the reference's
-    QuashKVCache path (append, reconstruct the whole K^ / V^ of the layer,
-    quashkv/integrations/hf_cache.py:123-152, then softmax attention over them)
-    and against attention over an uncompressed fp32 cache."""
+    """cfg2's decode step (24 layers, batch 16, 14 query / 2 kv heads, head_dim
+    64, 2048 cached tokens) two ways:
+
+    * per-layer attention work: the fused path's calls as the registered HF
+      attention function makes them (engine.append of the new token, then
+      engine.attention over the compressed cache, per layer) against the
+      reference's QuashKVCache path (append, reconstruct the whole K^ / V^ of
+      the layer, quashkv/integrations/hf_cache.py:123-152, then torch SDPA);
+    * a whole-model decode step of a Qwen2.5-0.5B-shaped model (24 layers,
+      hidden 896, MLP 4864; seeded random bf16 weights, 1024-token vocabulary)
+      through transformers' forward: attn_implementation="quashkv" with a
+      QuashKVHFCache (quashkv_amd.integrations.hf_attention), against the same
+      model with its own SDPA attention over an uncompressed bf16 DynamicCache
+      of the same length."""
     import torch
     import torch.nn.functional as F
-    from quashkv_amd.integrations.hf_attention import QuashKVHFCache
+    from quashkv_amd.integrations import hf_attention as HA
     from quashkv_amd.integrations.hf_cache import QuashKVCache
 
     NL, B2, HQ2, HKV2, D2, T2 = 24, 16, 14, 2, 64, 2048
     steps = max(4, args.steps // 3)
-    cap = T2 + 2 * (args.warmup + steps) + 64
+    cap = T2 + 4 * (args.warmup + steps) + 64
     g = torch.Generator(device=dev).manual_seed(5)
-    fused = QuashKVHFCache(NL, D2, device=dev)
+    fused = HA.QuashKVHFCache(NL, D2, device=dev)
     recon = QuashKVCache(NL, D2, device=dev)
+    kvs = []
     for l in range(NL):
-        k = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.float16)
-        v = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.float16)
+        k = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(B2, HKV2, T2, D2, generator=g, device=dev).to(torch.bfloat16)
+        kvs.append((k, v))
         for e in (fused.engines[l], recon.engines[l]):
             e.initial_capacity = cap
             e.append(k, v)
-    raw = [torch.randn(2, B2, HKV2, cap, D2, generator=g, device=dev) for _ in range(NL)]
-    q = torch.randn(B2, HQ2, 1, D2, generator=g, device=dev).to(torch.float16)
-    kn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.float16)
-    vn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.float16)
-    t_raw = [T2]
+    q = torch.randn(B2, HQ2, 1, D2, generator=g, device=dev).to(torch.bfloat16)
+    kn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.bfloat16)
+    vn = torch.randn(B2, HKV2, 1, D2, generator=g, device=dev).to(torch.bfloat16)
 
     def step_fused():
         for l in range(NL):
             e = fused.engines[l]
             e.append(kn, vn)
-            e.attention(q, out_dtype=torch.float16)
+            e.attention(q, out_dtype=torch.bfloat16)
 
     def step_recon():
         for l in range(NL):
             kh, vh = recon.update(kn, vn, l)
             F.scaled_dot_product_attention(q.float(), kh, vh, enable_gqa=True)
 
-    def step_raw():
-        t = t_raw[0]
-        for l in range(NL):
-            raw[l][0, :, :, t].copy_(kn[:, :, 0])
-            raw[l][1, :, :, t].copy_(vn[:, :, 0])
-            F.scaled_dot_product_attention(q.float(), raw[l][0, :, :, :t + 1],
-                                           raw[l][1, :, :, :t + 1], enable_gqa=True)
-        t_raw[0] = t + 1
-
-    res = {}
-    for name, fn in (("fused", step_fused), ("reconstruct", step_recon), ("fp32_raw", step_raw)):
+    def timed(fn, n):
         for _ in range(args.warmup):
             fn()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record(stream)
-        for _ in range(steps):
+        for _ in range(n):
             fn()
         b.record(stream)
         torch.cuda.synchronize()
-        res[name] = a.elapsed_time(b) / steps * 1e3
-    return {"what": "cfg2 decode step, 24 layers (B 16, 14/2 heads, d 64, ~2048 cached tokens): "
-                    "append + attention per layer",
-            "fused_us_per_step": round(res["fused"], 1),
+        return a.elapsed_time(b) / n * 1e3
+
+    res = {"fused": timed(step_fused, steps), "reconstruct": timed(step_recon, steps)}
+    del recon
+
+    # whole-model decode steps through transformers
+    from transformers import AutoModelForCausalLM, DynamicCache, Qwen2Config
+    HA.register()
+    mcfg = Qwen2Config(vocab_size=1024, hidden_size=HQ2 * D2, intermediate_size=4864,
+                       num_hidden_layers=NL, num_attention_heads=HQ2, num_key_value_heads=HKV2,
+                       max_position_embeddings=T2 + 1024, tie_word_embeddings=True)
+    torch.manual_seed(0)
+    models = {}
+    for attn in (HA.ATTN_IMPLEMENTATION, "sdpa"):
+        models[attn] = AutoModelForCausalLM.from_config(
+            mcfg, attn_implementation=attn, dtype=torch.bfloat16).to(dev).eval()
+    models["sdpa"].load_state_dict(models[HA.ATTN_IMPLEMENTATION].state_dict())
+    dyn = DynamicCache()
+    for l, (k, v) in enumerate(kvs):
+        dyn.update(k, v, l)
+    caches = {HA.ATTN_IMPLEMENTATION: fused, "sdpa": dyn}
+    ids = torch.randint(0, 1024, (B2, 1), generator=g, device=dev)
+
+    def model_step(attn):
+        cache = caches[attn]
+        pos = torch.full((B2, 1), cache.get_seq_length(), device=dev, dtype=torch.long)
+        with torch.no_grad():
+            models[attn](input_ids=ids, past_key_values=cache, position_ids=pos, use_cache=True)
+
+    res["model_quashkv"] = timed(lambda: model_step(HA.ATTN_IMPLEMENTATION), steps)
+    res["model_sdpa"] = timed(lambda: model_step("sdpa"), steps)
+    del models, caches, dyn
+    return {"what": "cfg2 decode step, 24 layers (B 16, 14/2 heads, d 64, ~2048 cached tokens)",
+            "attention_calls_us_per_step": round(res["fused"], 1),
+            "attention_calls_what": "engine.append + engine.attention per layer (the registered "
+                                    "attention function's work), bf16",
             "reconstruct_us_per_step": round(res["reconstruct"], 1),
-            "fp32_uncompressed_us_per_step": round(res["fp32_raw"], 1),
-            "fused_speedup_vs_reconstruct": round(res["reconstruct"] / res["fused"], 2)}
+            "reconstruct_what": "reference path: QuashKVCache.update (append + reconstruct K^/V^) "
+                                "+ torch SDPA per layer",
+            "fused_speedup_vs_reconstruct": round(res["reconstruct"] / res["fused"], 2),
+            "model_step_quashkv_us": round(res["model_quashkv"], 1),
+            "model_step_sdpa_uncompressed_us": round(res["model_sdpa"], 1),
+            "model_what": "transformers forward of one decode token, Qwen2.5-0.5B-shaped random "
+                          "bf16 model: attn_implementation='quashkv' + QuashKVHFCache vs "
+                          "'sdpa' + uncompressed bf16 DynamicCache"}
 
 
 # ------------------------------------------------------------------ other configs
@@ -1059,7 +1108,8 @@ def main() -> None:
             "sample": (f"oracle online-softmax decode (oracle/ref_math.attention_online, "
                        f"fp32 torch CPU) on {args.cpu_batch} of {B} sequences, all 8 kv "
                        f"heads, T={T}; median of {args.cpu_reps} reps = {med:.3f} s; "
-                       f"host {cpu_model()}")}
+                       f"host {cpu_model()}; torch threads = the {host_cores()} CPUs this "
+                       f"process may use (os.cpu_count() = {os.cpu_count()})")}
     print(json.dumps(line), flush=True)
 
 

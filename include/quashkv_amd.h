@@ -115,7 +115,7 @@ int qkv_ip_dot(const uint8_t* codes, const uint8_t* qjl, const float* norms,
  *   qjl        grouped rows of the 1-bit QJL signs (IP only)
  *   norms      grouped fp32 norms max(||x||, 1e-8) (ignored if PRE_ROTATED)
  *   out_seq, out_group_stride  grouped-row addressing of codes/qjl/norms
- * This is the VALU kernel for any d, tables and flags; d = 128 / 64 with
+ * This is the VALU kernel for any d, tables and flags; d = 128 / 96 / 64 with
  * symmetric codebooks run faster on qkv_compress_mfma below. */
 int qkv_compress(int32_t mode, int32_t in_dtype, int32_t flags,
                  const void* x, int64_t n, int32_t d,
@@ -150,11 +150,12 @@ int qkv_compress_mfma(int32_t mode, int32_t in_dtype, const void* x, int64_t n, 
  *              token 0), in_group_stride tiles per group, norms at
  *              group * 32 * in_group_stride + token (MSE mode only)
  *   out        n x d, out_dtype, contiguous
- * d = 64 / 128 run on the matrix cores (fp16 high/low split of Pi and of the
- * values, fp32 accumulation: within ~3e-6 relative of an fp32 evaluation);
- * they need 16-byte aligned out and unpacked code / V-tile pointers (4-byte,
- * 2-byte at d = 64, for packed rows and K rows).  d = 96 and other pointers
- * use a VALU kernel with fp32 arithmetic. */
+ * d = 64 / 96 / 128 run on the matrix cores (fp16 high/low split of Pi and
+ * of the values, fp32 accumulation: within ~3e-6 relative of an fp32
+ * evaluation); they need 16-byte aligned out and V-tile pointers, unpacked
+ * code pointers 16-byte (8-byte at d = 96) and packed / K-row pointers
+ * 4-byte (2-byte at d = 64) aligned.  Other pointers use a VALU kernel with
+ * fp32 arithmetic. */
 int qkv_decompress(int32_t mode, int32_t fmt,
                    const uint8_t* codes, const uint8_t* qjl, const float* norms,
                    int64_t n, int32_t d, int32_t bits,
@@ -420,7 +421,8 @@ int qkv_attention_run(const uint8_t* kstore, const float* knorm,
 
 /* One decode step over n_layers (1..32) layers sharing shapes, bit widths and
  * codebooks -- a model's layers, each with its own store, Pi, S, query and
- * output -- in three launches instead of 3 n_layers (quashkv/engine.py:
+ * output -- in one launch (decode_fused / decode_small; plus the merge of the
+ * splits when there are several) instead of n_layers calls (quashkv/engine.py:
  * 204-299 per layer).  q, kstore, knorm, vstore, vnorm, pi, signs and out are
  * HOST arrays of n_layers device pointers, each as in qkv_decode_attention;
  * the other arguments are shared.  The workspace and split count are those of
@@ -614,7 +616,8 @@ int qkv_mips_search(const void* queries, int32_t q_dtype, int32_t M, int32_t d,
  * ---------------------------------------------------------------------- */
 
 /* qkv_store_append into a paged store: B sequences' new tokens
- * [t0, t0 + S) (keys / values (B, H, S, d), bf16 or fp16, d = 64 or 128);
+ * [t0, t0 + S) (keys / values (B, H, S, d), bf16, fp16 or fp32, d = 64, 96
+ * or 128);
  * the pages covering them must be in the table.  Same arguments otherwise. */
 int qkv_paged_store_append(int32_t in_dtype, const void* keys, const void* values,
                            int32_t B, int32_t H, int64_t S, int32_t d, int32_t mbits,
@@ -641,7 +644,7 @@ int qkv_paged_store_append_kv(int32_t in_dtype, const void* keys, const void* va
                               int64_t t0, void* stream);
 
 /* qkv_decode_attention over a paged store of T tokens per sequence (the MFMA
- * path: symmetric codebooks, key MSE bits <= 3, d = 64 or 128; returns
+ * path: symmetric codebooks, key MSE bits <= 3, d = 64, 96 or 128; returns
  * QKV_E_UNSUPPORTED otherwise).  Same arguments as qkv_decode_attention with
  * (kpool, knorm, vpool, vnorm, page_table, pages_per_seq, page_tokens) for the
  * store. */
