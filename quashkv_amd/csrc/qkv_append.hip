@@ -121,7 +121,9 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
     const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
     // a wave per 32-coordinate block of a tile while that fits one workgroup per
     // CU, else a wave per tile while two per CU hold every workgroup
-    int ns = d / 32, kb = append_blocks(kn * ns), vb = append_blocks(vn * ns);
+    int ns = d / 32;
+    int kb = static_cast<int>(std::min<int64_t>(one_blocks(kn, ns), 1 << 20));
+    int vb = static_cast<int>(std::min<int64_t>(one_blocks(vn, ns), 1 << 20));
     if (kb + vb > qkv_num_cus()) {
       ns = 1;
       kb = append_blocks(kn);
@@ -303,7 +305,9 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
     const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
     // a wave per 32-coordinate block of a tile while that fits one workgroup per
     // CU, else a wave per tile while two per CU hold every workgroup
-    int ns = d / 32, kb = blocks(kn * ns), vb = blocks(vn * ns);
+    int ns = d / 32;
+    int kb = static_cast<int>(std::min<int64_t>(one_blocks(kn, ns), 1 << 20));
+    int vb = static_cast<int>(std::min<int64_t>(one_blocks(vn, ns), 1 << 20));
     if (int64_t(kb + vb) * n_layers > qkv_num_cus()) {
       ns = 1;
       kb = blocks(kn);
@@ -505,10 +509,13 @@ int kmixed_kv_impl(int32_t in_dtype, const void* keys, const void* values, int64
   if (groups == 0 || S == 0) return QKV_OK;
   const int64_t ktpg = (S + kTok - 1) / kTok, kn = groups * ktpg;
   const int64_t vtpg = (t0 + S - (t0 & ~int64_t(31)) + kTok - 1) / kTok, vn = groups * vtpg;
-  // a wave per 32-slot block of a tile while that fits one workgroup per CU,
-  // else a wave per tile while two per CU hold every workgroup
-  int ns = 4, kb = append_blocks(kn * ns), vb = append_blocks(vn * ns);
-  if (kb + vb > qkv_num_cus()) {
+  // a wave per 32-slot block of a tile while two workgroups per CU hold every
+  // workgroup (cfg4's 2048-token chunks: 512 workgroups, 12 us per chunk
+  // against 14.5 us for a wave per tile), else a wave per tile
+  int ns = 4;
+  int kb = static_cast<int>(std::min<int64_t>(one_blocks(kn, ns), 1 << 20));
+  int vb = static_cast<int>(std::min<int64_t>(one_blocks(vn, ns), 1 << 20));
+  if (kb + vb > 2 * qkv_num_cus()) {
     ns = 1;
     kb = append_blocks(kn);
     vb = append_blocks(vn);

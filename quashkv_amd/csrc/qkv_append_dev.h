@@ -326,6 +326,16 @@ __device__ __forceinline__ uint16_t to16(float v) {
     return qkv_f32_to_bf16(v);
 }
 
+typedef __bf16 qkv_bf16x2v __attribute__((ext_vector_type(2)));
+typedef float qkv_f32x2v __attribute__((ext_vector_type(2)));
+
+// a (low half) and b as bf16, each rounded to nearest even (one
+// v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  const qkv_f32x2v v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, qkv_bf16x2v));
+}
+
 template <bool F16>
 __device__ __forceinline__ float from16(uint16_t h) {
   if constexpr (F16)
@@ -339,45 +349,98 @@ __device__ __forceinline__ float from16(uint16_t h) {
 // eight 16-bit values: the high part (split 0) or the low part (split 1) of
 // Pi' = Pi * pscale; r(m) = m, or half_major(m) with PERM (the A operand of
 // the key append, whose result rows are then coordinates in half-major order).
+//
+// blk >= 0 stages the slots of coordinate block blk only (a workgroup whose
+// waves all compute that block), at the same positions.
 template <bool F16, int D = kD, bool PERM = false>
-__device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi, float pscale) {
+__device__ __forceinline__ void stage_pi(uint4* __restrict__ frag, const float* __restrict__ pi,
+                                         float pscale, int blk = -1) {
   // kThreads threads (every launch uses that block size); each takes NPT
   // (block, k-step, lane) slots and writes both splits of each, with all of
   // its Pi loads in flight before the first conversion
   constexpr int NKS = D / 16;  // k-steps
   constexpr int NSLOT = frag_n<D>() / 2;
   constexpr int NPT = (NSLOT + kThreads - 1) / kThreads;  // the last may be partial (d = 96)
+  constexpr int NS1 = NKS * 64;                           // one block's slots
+  static_assert(NS1 <= kThreads, "one block's slots: at most one per thread");
+  auto addr = [&](int u) {
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
+    const int j = 32 * b + (PERM ? half_major(ln & 31) : (ln & 31)), k0 = 16 * s + 8 * (ln >> 5);
+    return pi + j * D + k0;
+  };
+  auto put = [&](int u, float4 p0, float4 p1) {
+    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
+    // pscale = 2^k: the scaling is exact
+    const float v[8] = {p0.x * pscale, p0.y * pscale, p0.z * pscale, p0.w * pscale,
+                        p1.x * pscale, p1.y * pscale, p1.z * pscale, p1.w * pscale};
+    uint32_t hw[4], lw[4];  // pairs of 16-bit values, element 2 i low
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (F16) {
+        const uint32_t h0 = to16<true>(v[2 * i]), h1 = to16<true>(v[2 * i + 1]);
+        hw[i] = h0 | (h1 << 16);
+        lw[i] = to16<true>(v[2 * i] - from16<true>(h0)) |
+                (static_cast<uint32_t>(to16<true>(v[2 * i + 1] - from16<true>(h1))) << 16);
+      } else {
+        // v_cvt_pk_bf16_f32: two round-to-nearest-even conversions (the
+        // entries are finite)
+        hw[i] = pk_bf16(v[2 * i], v[2 * i + 1]);
+        lw[i] = pk_bf16(v[2 * i] - __uint_as_float(hw[i] << 16),
+                        v[2 * i + 1] - __uint_as_float(hw[i] & 0xffff0000u));
+      }
+    }
+    const int e = ((b * NKS + s) * 2) * 64 + ln;
+    frag[e] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    frag[e + 64] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  };
+  if (blk >= 0) {
+    if (threadIdx.x < NS1) {
+      const int u = blk * NS1 + threadIdx.x;
+      const float* a = addr(u);
+      put(u, *reinterpret_cast<const float4*>(a), *reinterpret_cast<const float4*>(a + 4));
+    }
+    return;
+  }
   float4 p[NPT][2];
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
-    const int u = min(threadIdx.x + kThreads * x, NSLOT - 1);
-    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
-    const int j = 32 * b + (PERM ? half_major(ln & 31) : (ln & 31)), k0 = 16 * s + 8 * (ln >> 5);
-    p[x][0] = *reinterpret_cast<const float4*>(pi + j * D + k0);
-    p[x][1] = *reinterpret_cast<const float4*>(pi + j * D + k0 + 4);
+    const float* a = addr(min(threadIdx.x + kThreads * x, NSLOT - 1));
+    p[x][0] = *reinterpret_cast<const float4*>(a);
+    p[x][1] = *reinterpret_cast<const float4*>(a + 4);
   }
 #pragma unroll
   for (int x = 0; x < NPT; ++x) {
     const int u = threadIdx.x + kThreads * x;
     if (NSLOT % kThreads != 0 && u >= NSLOT) break;
-    const int ln = u & 63, s = (u >> 6) % NKS, b = (u >> 6) / NKS;
-    // pscale = 2^k: the scaling is exact
-    const float v[8] = {p[x][0].x * pscale, p[x][0].y * pscale, p[x][0].z * pscale,
-                        p[x][0].w * pscale, p[x][1].x * pscale, p[x][1].y * pscale,
-                        p[x][1].z * pscale, p[x][1].w * pscale};
-    uint32_t hi[8], lo[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const uint16_t h = to16<F16>(v[i]);
-      hi[i] = h;
-      lo[i] = to16<F16>(v[i] - from16<F16>(h));
-    }
-    const int e = ((b * NKS + s) * 2) * 64 + ln;
-    frag[e] = make_uint4(hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16), hi[4] | (hi[5] << 16),
-                         hi[6] | (hi[7] << 16));
-    frag[e + 64] = make_uint4(lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16),
-                              lo[4] | (lo[5] << 16), lo[6] | (lo[7] << 16));
+    put(u, p[x][0], p[x][1]);
   }
+}
+
+// Workgroups of a one-tile-per-wave launch (ONE below): nsplit = 1 gives wave
+// g = b kWaves + w tile g; nsplit > 1 gives workgroup b coordinate block
+// b % nsplit of tiles (b / nsplit) kWaves + w, so that it stages that block of
+// Pi only.
+__host__ __device__ constexpr int64_t one_blocks(int64_t ntiles, int nsplit) {
+  return nsplit * ((ntiles + kWaves - 1) / kWaves);
+}
+
+constexpr int kXcds = 8;  // MI355X deals consecutive workgroups to its 8 XCDs in turn
+
+// Coordinate block `blk` and first tile of wave wv of workgroup bid of nb
+// (nsplit > 1).  Block-major; when nb is a whole number of rounds of kXcds
+// tile groups, the nsplit workgroups of a tile group share bid % kXcds, so
+// that they run on one XCD and its L2 fetches their rows once.
+__device__ __forceinline__ int64_t one_first(int bid, int nb, int nsplit, int wv, int& blk) {
+  int g;
+  if (nb % (kXcds * nsplit) == 0) {
+    const int r = bid / kXcds;
+    blk = r % nsplit;
+    g = (r / nsplit) * kXcds + bid % kXcds;
+  } else {
+    blk = bid % nsplit;
+    g = bid / nsplit;
+  }
+  return int64_t(g) * kWaves + wv;
 }
 
 // x fragments of a wave tile: xf[tt][s], lane l = (row l & 31, half l >> 5)
@@ -488,16 +551,17 @@ __device__ __forceinline__ void append_k_run(
   constexpr int LH = (L + 1) / 2;     // split: planes per lane half
   const int lane = threadIdx.x & 63, li = lane & 31, hh = lane >> 5;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile math on the SALU
-  // ONE with nsplit = NBK: wave (tile, coordinate block) = (g / NBK, g % NBK)
-  // for the global wave index g, each wave computing and storing that block's
-  // words only; nsplit = 1: wave g takes tile g whole
-  const int64_t gw = int64_t(bid) * kWaves + wv;
+  // ONE with nsplit = NBK: the workgroup's coordinate block and tiles as in
+  // one_blocks, each wave computing and storing that block's words only;
+  // nsplit = 1: wave g takes tile g whole
   const bool split = ONE && nsplit > 1;
-  const int myblk = split ? static_cast<int>(gw % NBK) : 0;
+  int myblk = 0;
+  const int64_t gw = split ? one_first(bid, nb, NBK, wv, myblk)  // the wave's first tile
+                           : int64_t(bid) * kWaves + wv;
   constexpr bool PRE = ONE && !FROM_Y && !F32;  // rows loaded before the Pi staging
   uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
-    const int64_t tile = split ? gw / NBK : gw;
+    const int64_t tile = gw;
     if (tile < ntiles) {
       const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
       const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
@@ -507,7 +571,7 @@ __device__ __forceinline__ void append_k_run(
     }
   }
   if constexpr (!FROM_Y) {
-    stage_pi<F16, D, true>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    stage_pi<F16, D, true>(frag, pi, F16 ? kPScaleF16 : 1.f, split ? myblk : -1);
     __syncthreads();
   }
 
@@ -532,7 +596,7 @@ __device__ __forceinline__ void append_k_run(
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = split ? gw / NBK : gw; tile < ntiles; tile += wstep) {
+  for (int64_t tile = gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
@@ -697,221 +761,204 @@ __global__ __launch_bounds__(kThreads, 4) void append_k_layers(AppendLayers al, 
 //  * IPM, MixedPrecisionIPQuantizer (quashkv/mixed_precision.py:283-297) with
 //    a 2-bit outlier / 1-bit regular MSE stage: plane b0 of every slot, the
 //    QJL plane [(y - c) S >= 0] of every slot, then b1 of the NO outlier
-//    slots -- 32 + NO / 8 bytes.  The search runs over each codebook's fine
-//    list as append_k_mfma's does, so the QJL tie rule is the reference's.
+//    slots -- 32 + NO / 8 bytes.
 // The outlier slots fill whole 32-slot blocks (NO = 32 or 64), so each block's
 // codebook is fixed at compile time.  FROM_Y: `xin` holds fp32 rotated unit
-// rows in slot order and `nin` their norms.
+// rows in slot order and `nin` their norms, searched exactly (search_sym, the
+// reference's QJL tie rule); from x the search compares the raw MFMA result
+// against each codebook's list scaled by the lane's token norm, as
+// append_k_run's does.  Orientation, lane-local words, ONE and nsplit as in
+// append_k_run (Pi's rows in slot order, half-major within each block).
 template <int NO, int XT, bool FROM_Y, bool IPM, bool ONE = false>
 __device__ __forceinline__ void append_kmix_run(
     const void* __restrict__ xin, const float* __restrict__ nin, int64_t S, int64_t tpg,
     int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
-    int64_t t0, uint4* __restrict__ frag, float4 (*inv_s)[kTok / 4], int bid, int nb,
-    int nsplit = 1) {
+    int64_t t0, uint4* __restrict__ frag, int bid, int nb, int nsplit = 1) {
+  static_assert(kHalves == 1, "one 32-token MFMA column block per wave tile");
   constexpr bool F16 = XT != 0, F32 = XT == 2;        // fp16 MFMA / fp32 rows split for it
   constexpr int NOB = NO / 32;                         // outlier blocks
+  constexpr int NBK = kD / 32;                         // slot blocks
+  constexpr int NKS = kD / 16;                         // k-steps
   constexpr int RD = IPM ? 8 + NOB : 8 + 2 * NOB;      // dwords per row
-  constexpr int NSK = (RD * kTok + 63) / 64;           // staging dwords per lane
-  const int lane = threadIdx.x & 63, li = lane & 31, wv = threadIdx.x >> 6;
-  // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
-  // ONE, nsplit: the waves' tiles and slot blocks as in append_k_run
-  const int64_t gw = int64_t(bid) * kWaves + wv;
+  constexpr int RDH = (RD + 1) / 2;                    // dwords per row a lane half stores
+  const int lane = threadIdx.x & 63, li = lane & 31, hh = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const bool split = ONE && nsplit > 1;
-  const int myblk = split ? static_cast<int>(gw % 4) : 0;
+  int myblk = 0;
+  const int64_t gw = split ? one_first(bid, nb, NBK, wv, myblk)  // the wave's first tile
+                           : int64_t(bid) * kWaves + wv;
   constexpr bool PRE = ONE && !FROM_Y && !F32;
-  uint4 xpre[kHalves][PRE ? 8 : 1];
+  uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
-    const int64_t tile = split ? gw / 4 : gw;
-    if (tile < ntiles) {
-      const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
+    if (gw < ntiles) {
+      const int64_t grp = gw / tpg, s0 = (gw - grp * tpg) * kTok;
       const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
-      const uint16_t* row[kHalves];
-      const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-      load_x(xpre, row, lane);
+      const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
+                                (grp * S + s0 + min(li, nv - 1)) * kD};
+      load_x<NKS>(xpre, row, lane);
     }
   }
   if constexpr (!FROM_Y) {
-    stage_pi<F16>(frag, pi_perm, F16 ? kPScaleF16 : 1.f);
+    stage_pi<F16, kD, true>(frag, pi_perm, F16 ? kPScaleF16 : 1.f, split ? myblk : -1);
     __syncthreads();
   }
 
   // positive halves: outlier and regular boundaries (MSE keys) or fine lists
-  // (IP keys), three and one entries either way
+  // (IP keys), three and one entries either way; integer keys (FROM_Y) or floats
   uint32_t pov[3], prv[1];
+  float pof[3], prf[1];
 #pragma unroll
-  for (int i = 0; i < 3; ++i) pov[i] = in_vgpr(po.t[i]);
+  for (int i = 0; i < 3; ++i) {
+    pov[i] = in_vgpr(po.t[i]);
+    pof[i] = __uint_as_float(po.t[i] >> 1);
+  }
   prv[0] = in_vgpr(pr.t[0]);
-  uint64_t sneg[4] = {0, 0, 0, 0};  // IP: lanes whose slot 32 n + (l & 31) has S < 0
-  uint32_t cx[4] = {0u, 0u, 0u, 0u};  // IP: 1 where S >= 0 (centroid level counts c <= y)
-  if constexpr (IPM) {
+  prf[0] = __uint_as_float(pr.t[0] >> 1);
+  // IP keys, per block n, bits v of this lane half's slots 32 n + 16 h + v:
+  // [S < 0] (the QJL plane's flip) and [S >= 0] (the exact search's centroid
+  // level counts c <= y there)
+  uint32_t qflip[NBK], cxw[NBK];
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const bool neg = signs_perm[32 * n + li] < 0.f;
-      sneg[n] = lanes_where(neg);
-      cx[n] = neg ? 0u : 1u;
+  for (int n = 0; n < NBK; ++n) {
+    qflip[n] = 0u;
+    if constexpr (IPM) {
+      const uint32_t negw = static_cast<uint32_t>(lanes_where(signs_perm[32 * n + li] < 0.f));
+      qflip[n] = (negw >> (16 * hh)) & 0xffffu;
     }
+    cxw[n] = qflip[n] ^ 0xffffu;
   }
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = split ? gw / 4 : gw; tile < ntiles; tile += wstep) {
+  for (int64_t tile = gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
+    const int64_t srow = grp * S + s0 + min(li, nv - 1);  // this lane's token row (clamped)
     float* nrow = knorm + grp * t_stride + t0 + s0;
-    uint4 xf[kHalves][8];
-    uint4 xl[kHalves][F32 ? 8 : 1];  // fp32 rows: the low fp16 parts
+    uint4 xf[1][NKS];
+    uint4 xl[1][F32 ? NKS : 1];  // fp32 rows: the low fp16 parts
+    float tho[3], thr[1];        // the lists in MFMA-result units of this lane's token
     if constexpr (FROM_Y) {
-#pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt)
-        if (lane < 32 && 32 * tt + li < nv) nrow[32 * tt + li] = nin[grp * S + s0 + 32 * tt + li];
+      if (lane < 32 && li < nv) nrow[li] = nin[srow];
     } else {
-      float nrm[kHalves];
+      float nrm[1];
       if constexpr (F32) {
-        const float* row[kHalves];
-        const auto* x = static_cast<const float*>(xin);
-#pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-          row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-        load_x_f32<8>(xf, xl, nrm, row, lane);
+        const float* row[1] = {static_cast<const float*>(xin) + srow * kD};
+        load_x_f32<NKS>(xf, xl, nrm, row, lane);
       } else {
         if constexpr (PRE) {
 #pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-            for (int s = 0; s < 8; ++s) xf[tt][s] = xpre[tt][s];
+          for (int s = 0; s < NKS; ++s) xf[0][s] = xpre[0][s];
         } else {
-          const uint16_t* row[kHalves];
-          const auto* x = static_cast<const uint16_t*>(xin);
-#pragma unroll
-          for (int tt = 0; tt < kHalves; ++tt)
-            row[tt] = x + (grp * S + s0 + min(32 * tt + li, nv - 1)) * kD;
-          load_x(xf, row, lane);
+          const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) + srow * kD};
+          load_x<NKS>(xf, row, lane);
         }
+        float ss = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) {
-          float ss = 0.f;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) ss = sumsq<F16>(xf[tt][s], ss);
-          ss += __shfl_xor(ss, 32, 64);
-          nrm[tt] = fmaxf(sqrtf(ss), 1e-8f);
-        }
+        for (int s = 0; s < NKS; ++s) ss = sumsq<F16>(xf[0][s], ss);
+        ss += __shfl_xor(ss, 32, 64);
+        nrm[0] = fmaxf(sqrtf(ss), 1e-8f);
       }
-      float* invw = reinterpret_cast<float*>(&inv_s[wv][0]);
+      if (lane < 32 && li < nv && myblk == 0) nrow[li] = nrm[0];
+      // the MFMA result is y |x| / iscale (fp32 rows: 2^16 y)
+      const float zs = F32 ? 65536.f : nrm[0] / iscale;
 #pragma unroll
-      for (int tt = 0; tt < kHalves; ++tt) {
-        if (lane < 32) {
-          if (32 * tt + li < nv && myblk == 0) nrow[32 * tt + li] = nrm[tt];
-          invw[32 * tt + li] = F32 ? 1.f / 65536.f : iscale / nrm[tt];
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes landed
-      __builtin_amdgcn_wave_barrier();
+      for (int i = 0; i < 3; ++i) tho[i] = pof[i] * zs;
+      thr[0] = prf[0] * zs;
     }
 
-    uint32_t stg[NSK];
+    // row dword of plane word r of block n: whole planes at word n, outlier
+    // words after them (MSE keys: b0, b1, b2, parity; IP keys: b0, QJL, b1)
+    auto dw = [](int r, int n) { return r < 2 ? 4 * r + n : 8 + n + (r == 3 ? NOB : 0); };
+    const int64_t row = li < nv ? grp * t_stride + t0 + s0 + li : -1;
+    uint32_t* dst = reinterpret_cast<uint32_t*>(kst) + row * RD;
+    uint32_t kw[RD];  // this lane half's 16 bits of each row dword
 #pragma unroll
-    for (int i = 0; i < NSK; ++i) stg[i] = 0u;
+    for (int i = 0; i < RD; ++i) kw[i] = 0u;
 
-    static_for<4>([&](auto nc) {  // coordinate block n
+    static_for<NBK>([&](auto nc) {  // slots 32 n .. 32 n + 31
       constexpr int n = decltype(nc)::value;
       if (split && n != myblk) return;
-      __builtin_amdgcn_sched_barrier(0);
-      float yv[kHalves][16];
+      __builtin_amdgcn_sched_barrier(0);  // one slot block at a time (registers)
+      constexpr bool OUT = n < NOB;
+      constexpr int L = OUT ? 3 : 2;      // search levels
+      constexpr int NW = OUT ? (IPM ? 3 : 4) : 2;  // row dwords of this block
+      float yv[16];  // slot 32 n + 16 h + v of this lane's token
       if constexpr (FROM_Y) {
-        const auto* y = static_cast<const float*>(xin);
+        const float4* y = reinterpret_cast<const float4*>(static_cast<const float*>(xin) +
+                                                          srow * kD + 32 * n + 16 * hh);
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int tk = 32 * tt + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-            yv[tt][v] = y[(grp * S + s0 + min(tk, nv - 1)) * kD + 32 * n + li];
-          }
+        for (int a = 0; a < 4; ++a) {
+          const float4 q = y[a];
+          yv[4 * a] = q.x; yv[4 * a + 1] = q.y; yv[4 * a + 2] = q.z; yv[4 * a + 3] = q.w;
+        }
       } else {
-        qkv_f32x16 acc[kHalves] = {};
+        qkv_f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < NKS; ++s)
 #pragma unroll
-          for (int sp = 0; sp < 2; ++sp) {
-            const uint4 bf = frag[((n * 8 + s) * 2 + sp) * 64 + lane];
-#pragma unroll
-            for (int tt = 0; tt < kHalves; ++tt) {
-              acc[tt] = mma<F16>(xf[tt][s], bf, acc[tt]);
-              if (F32 && sp == 0) acc[tt] = mma<F16>(xl[tt][F32 ? s : 0], bf, acc[tt]);
-            }
+          for (int sp2 = 0; sp2 < 2; ++sp2) {
+            const uint4 af = frag[((n * NKS + s) * 2 + sp2) * 64 + lane];
+            acc = mma<F16>(af, xf[0][s], acc);
+            if (F32 && sp2 == 0) acc = mma<F16>(af, xl[0][F32 ? s : 0], acc);
           }
 #pragma unroll
-        for (int tt = 0; tt < kHalves; ++tt) {
-          float4 iv4[4];
+        for (int v = 0; v < 16; ++v) yv[v] = acc[v];
+      }
+      // registers high to low: bit v of each accumulator is register v
+      static_for<16>([&](auto vc) {
+        constexpr int v = 15 - decltype(vc)::value;
+        uint64_t m[L];
+        if constexpr (FROM_Y)
+          search_sym<L, IPM>(yv[v], OUT ? pov : prv, (cxw[n] >> v) & 1u, m);
+        else
+          search_sym_scaled<L>(yv[v], OUT ? tho : thr, m);
+        if constexpr (IPM) {
+          // b0 = MSE bit 0 (fine-count bit 1), QJL = fine-count bit 0,
+          // outliers: b1 = MSE bit 1 (fine-count bit 2)
+          kw[dw(0, n)] = shift_in(kw[dw(0, n)], m[1]);
+          kw[dw(1, n)] = shift_in(kw[dw(1, n)], m[0]);
+          if constexpr (OUT) kw[dw(2, n)] = shift_in(kw[dw(2, n)], m[2]);
+        } else {
 #pragma unroll
-          for (int a = 0; a < 4; ++a) iv4[a] = inv_s[wv][8 * tt + 2 * a + (lane >> 5)];
+          for (int r = 0; r < L; ++r) kw[dw(r, n)] = shift_in(kw[dw(r, n)], m[r]);
+        }
+      });
+      if constexpr (IPM)
+        kw[dw(1, n)] ^= qflip[n];
+      else if constexpr (OUT)
+        kw[dw(3, n)] = kw[dw(0, n)] ^ kw[dw(1, n)] ^ kw[dw(2, n)];
+      if (split) {
+        // lane half h stores block n's words h LH ..
+        constexpr int LH = (NW + 1) / 2;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const float4 q4 = iv4[v >> 2];
-            const float iv = (v & 3) == 0 ? q4.x : (v & 3) == 1 ? q4.y : (v & 3) == 2 ? q4.z : q4.w;
-            yv[tt][v] = acc[tt][v] * iv;
-          }
+        for (int i = 0; i < LH; ++i) {
+          const int rb = i + LH < NW ? i + LH : i;
+          const uint32_t w = merge_halves(kw[dw(i, n)], kw[dw(rb, n)]);
+          if (row >= 0 && (hh == 0 || i + LH < NW)) dst[hh ? dw(rb, n) : dw(i, n)] = w;
         }
       }
-      static_for<kHalves>([&](auto tc) {
-        constexpr int tt = decltype(tc)::value;
-        static_for<16>([&](auto vc) {
-          constexpr int v = decltype(vc)::value;
-          const float y = yv[tt][v];
-          constexpr int ta = 32 * tt + 8 * (v >> 2) + (v & 3);  // token of lanes 0..31
-          // plane words in row order: MSE keys b0, b1 (+ outliers: b2, parity);
-          // IP keys b0, QJL (+ outliers: b1)
-          uint64_t w[4] = {0, 0, 0, 0};
-          if constexpr (IPM) {
-            if constexpr (n < NOB) {
-              uint64_t f[3];
-              search_sym<3, true>(y, pov, cx[n], f);
-              w[0] = f[1];
-              w[1] = f[0] ^ sneg[n];
-              w[2] = f[2];
-            } else {
-              uint64_t f[2];
-              search_sym<2, true>(y, prv, cx[n], f);
-              w[0] = f[1];
-              w[1] = f[0] ^ sneg[n];
-            }
-          } else if constexpr (n < NOB) {
-            uint64_t m[3];
-            search_sym<3, false>(y, pov, 0u, m);
-            w[0] = m[0];
-            w[1] = m[1];
-            w[2] = m[2];
-            w[3] = m[0] ^ m[1] ^ m[2];
-          } else {
-            uint64_t m[2];
-            search_sym<2, false>(y, prv, 0u, m);
-            w[0] = m[0];
-            w[1] = m[1];
-          }
-          constexpr int NW = n < NOB ? (IPM ? 3 : 4) : 2;
-          static_for<NW>([&](auto rc) {
-            constexpr int r = decltype(rc)::value;
-            // row dword: whole planes at word n, outlier words after them
-            constexpr int dw = r < 2 ? 4 * r + n : 8 + n + (r == 3 ? NOB : 0);
-            constexpr int D0 = ta * RD + dw, D1 = (ta + 4) * RD + dw;
-            stg[D0 >> 6] = put_lane<(D0 & 63)>(stg[D0 >> 6], static_cast<uint32_t>(w[r]));
-            stg[D1 >> 6] = put_lane<(D1 & 63)>(stg[D1 >> 6], static_cast<uint32_t>(w[r] >> 32));
-          });
-        });
-      });
     });
 
-    uint32_t* dst = reinterpret_cast<uint32_t*>(kst + (grp * t_stride + t0 + s0) * (RD * 4));
+    if (!split) {
+      // lane half h stores dwords h RDH .. of its token's row
+      uint32_t ow[RDH];
 #pragma unroll
-    for (int i = 0; i < NSK; ++i) {
-      const int D = i * 64 + lane;
-      // row dword e: block e % 4 for the four-dword planes, e - 8 (- NO / 32) past them
-      const int e = D % RD, blk = e < 8 ? (e & 3) : (e - 8) % NOB;
-      if (D < nv * RD && (!split || blk == myblk)) dst[D] = stg[i];
+      for (int i = 0; i < RDH; ++i) ow[i] = merge_halves(kw[i], kw[i + RDH < RD ? i + RDH : i]);
+      if (row >= 0) {
+        uint32_t* d = dst + hh * RDH;
+        constexpr int VW = (RDH % 2 == 0 && RD % 2 == 0) ? 2 : 1;
+#pragma unroll
+        for (int i = 0; i < RDH; i += VW) {
+          if (RD % 2 != 0 && hh == 1 && RDH + i >= RD) continue;
+          if constexpr (VW == 2)
+            *reinterpret_cast<uint2*>(d + i) = make_uint2(ow[i], ow[i + 1]);
+          else
+            d[i] = ow[i];
+        }
+      }
     }
     if constexpr (ONE) break;
   }
@@ -924,9 +971,8 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
     int64_t t0) {
   __shared__ uint4 frag[FROM_Y ? 1 : kFragN];  // Pi operand fragments (rows in slot order)
-  __shared__ float4 inv_s[kWaves][kTok / 4];   // 1 / norm of each wave's tokens
   append_kmix_run<NO, XT, FROM_Y, IPM>(xin, nin, S, tpg, ntiles, pi_perm, signs_perm, po, pr, kst,
-                                       knorm, t_stride, t0, frag, inv_s, blockIdx.x, gridDim.x);
+                                       knorm, t_stride, t0, frag, blockIdx.x, gridDim.x);
 }
 
 // ------------------------------------------------ quantizer-API compress
@@ -1086,15 +1132,16 @@ __device__ __forceinline__ void append_v_run(
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile math on the SALU
   const int64_t a_base = t0 & ~int64_t(31);
   // ONE (as in append_k_run): the wave's rows loaded before the Pi staging
-  // ONE, nsplit: the waves' tiles and coordinate blocks as in append_k_run
-  const int64_t gw = int64_t(bid) * kWaves + wv;
+  // ONE, nsplit: the workgroups' tiles and coordinate blocks as in append_k_run
   const bool split = ONE && nsplit > 1;
-  const int myblk = split ? static_cast<int>(gw % NBK) : 0;
+  int myblk = 0;
+  const int64_t gw = split ? one_first(bid, nb, NBK, wv, myblk)  // the wave's first tile
+                           : int64_t(bid) * kWaves + wv;
   const int wt = half_major(li);  // tile token of this lane's A-operand row
   constexpr bool PRE = ONE && !FROM_Y && !F32;
   uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
-    const int64_t tile = split ? gw / NBK : gw;
+    const int64_t tile = gw;
     if (tile < ntiles) {
       const int64_t grp = tile / tpg;
       const int64_t d0 = a_base + (tile - grp * tpg) * kTok - t0;
@@ -1104,7 +1151,7 @@ __device__ __forceinline__ void append_v_run(
     }
   }
   if constexpr (!FROM_Y) {
-    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f);
+    stage_pi<F16, D>(frag, pi, F16 ? kPScaleF16 : 1.f, split ? myblk : -1);
     __syncthreads();
   }
 
@@ -1120,7 +1167,7 @@ __device__ __forceinline__ void append_v_run(
   const float iscale = F16 ? 1.f / kPScaleF16 : 1.f;
   const int64_t wstep = int64_t(nb) * kWaves;
 
-  for (int64_t tile = split ? gw / NBK : gw; tile < ntiles; tile += wstep) {
+  for (int64_t tile = gw; tile < ntiles; tile += wstep) {
     const int64_t grp = tile / tpg;
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of tile token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)

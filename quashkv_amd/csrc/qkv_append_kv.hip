@@ -73,8 +73,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmixv(
   const int b = blockIdx.x;
   if (b < kblocks)
     append_kmix_run<NO, XT, false, IPM, true>(keys, nullptr, S, ktpg, kntiles, pi_perm, signs_perm, po,
-                                        pr, kst, knorm, t_stride, t0, frag, inv_s, b, kblocks,
-                                        nsplit);
+                                        pr, kst, knorm, t_stride, t0, frag, b, kblocks, nsplit);
   else
     append_v_run<VB, XT, kD, false, false, true>(values, nullptr, S, vtpg, vntiles, vpi, bnd, vst,
                                            vnorm, t_stride, t0, QkvPages{}, frag, inv_s,
@@ -94,8 +93,8 @@ bool launch_append_kmixv(int n_out, bool ipm, int vbits, int xt, const void* key
                          int64_t t_stride, int64_t t0, int nsplit, hipStream_t s) {
   if ((n_out != 32 && n_out != 64) || vbits < 2 || vbits > 4 || xt < 0 || xt > 2) return false;
   // the kernel bodies run one tile (nsplit = 4: one slot block of one tile) per wave
-  if ((nsplit != 1 && nsplit != 4) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
-      int64_t(vblocks) * kWaves < vntiles * nsplit)
+  if ((nsplit != 1 && nsplit != 4) || kblocks < one_blocks(kntiles, nsplit) ||
+      vblocks < one_blocks(vntiles, nsplit))
     return false;
   const dim3 grid(kblocks + vblocks);
 #define QKV_KMV(NOV, IP, VB, F)                                                                 \
@@ -141,8 +140,8 @@ bool launch_append_kv_paged(int mbits, int vbits, int xt, int d, const void* key
                             float* vnorm, int64_t t_stride, int64_t t0, const QkvPages& pg,
                             int nsplit, hipStream_t s) {
   if (vbits != mbits + 1 || (d != 128 && d != 64) || xt < 0 || xt > 2) return false;
-  if ((nsplit != 1 && nsplit != d / 32) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
-      int64_t(vblocks) * kWaves < vntiles * nsplit)
+  if ((nsplit != 1 && nsplit != d / 32) || kblocks < one_blocks(kntiles, nsplit) ||
+      vblocks < one_blocks(vntiles, nsplit))
     return false;
   const dim3 grid(kblocks + vblocks);
 #define QKV_KVP(MB, F, DD)                                                                     \
@@ -179,8 +178,8 @@ bool launch_append_kv(int mbits, int vbits, int xt, int d, const AppendLayers& a
   if (vbits != mbits + 1 || (d != 128 && d != 64) || xt < 0 || xt > 2) return false;
   // the kernel bodies run one tile (nsplit = d / 32: one coordinate block of one
   // tile) per wave
-  if ((nsplit != 1 && nsplit != d / 32) || int64_t(kblocks) * kWaves < kntiles * nsplit ||
-      int64_t(vblocks) * kWaves < vntiles * nsplit)
+  if ((nsplit != 1 && nsplit != d / 32) || kblocks < one_blocks(kntiles, nsplit) ||
+      vblocks < one_blocks(vntiles, nsplit))
     return false;
   const dim3 grid(kblocks + vblocks, n_layers);
 #define QKV_KV(MB, F, DD)                                                                      \
