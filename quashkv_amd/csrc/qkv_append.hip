@@ -71,6 +71,9 @@ int store_append_impl(int32_t in_dtype, const void* keys, const void* values, bo
                       float* vnorm, int64_t t_stride, int64_t t0, QkvPages pg, void* stream,
                       const float* vpi) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(S / kTok + 2 <= ((int64_t(1) << 31) - 1) / std::max<int64_t>(groups, 1),
+              "append of %lld groups x %lld tokens: more than 2^31 tiles", (long long)groups,
+              (long long)S);
   if (pg.tab == nullptr) {
     QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
                 "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
@@ -255,6 +258,9 @@ int store_append_layers_impl(int32_t n_layers, int32_t in_dtype, const void* con
                   kcent_host && kbound_host && vbound_host,
               "null pointer");
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(S / kTok + 2 <= ((int64_t(1) << 31) - 1) / std::max<int64_t>(groups, 1),
+              "append of %lld groups x %lld tokens: more than 2^31 tiles", (long long)groups,
+              (long long)S);
   QKV_REQUIRE(t_stride % 32 == 0 && t0 + S <= t_stride,
               "store capacity %lld (multiple of 32) must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
@@ -409,6 +415,9 @@ int kmixed_append_impl(int32_t in_dtype, const void* keys, bool rotated, const f
                        uint8_t* kstore, float* knorm, int64_t t_stride, int64_t t0,
                        void* stream, Half* po_out = nullptr, Half* pr_out = nullptr) {
   QKV_REQUIRE(groups >= 0 && S >= 0 && t0 >= 0, "negative size");
+  QKV_REQUIRE(S / kTok + 2 <= ((int64_t(1) << 31) - 1) / std::max<int64_t>(groups, 1),
+              "append of %lld groups x %lld tokens: more than 2^31 tiles", (long long)groups,
+              (long long)S);
   QKV_REQUIRE(t0 + S <= t_stride, "store capacity %lld must hold tokens [%lld, %lld)",
               (long long)t_stride, (long long)t0, (long long)(t0 + S));
   QKV_REQUIRE(qkv_dtype_ok(in_dtype), "unsupported input dtype %d", in_dtype);

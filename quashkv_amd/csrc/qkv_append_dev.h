@@ -443,6 +443,13 @@ __device__ __forceinline__ int64_t one_first(int bid, int nb, int nsplit, int wv
   return int64_t(g) * kWaves + wv;
 }
 
+// Group of tile `tile` (tpg tiles per group) in 32-bit arithmetic: the hosts
+// keep tile counts below 2^31 (a 64-bit division is ~130 scalar instructions
+// ahead of a wave's first load).
+__device__ __forceinline__ int64_t tile_group(int64_t tile, int64_t tpg) {
+  return static_cast<uint32_t>(tile) / static_cast<uint32_t>(tpg);
+}
+
 // x fragments of a wave tile: xf[tt][s], lane l = (row l & 31, half l >> 5)
 // holds x[token 32 tt + (l & 31)][16 s + 8 (l >> 5) .. + 7], read from row[tt]
 // (this lane's token row of block tt; callers point lanes without a token at a
@@ -563,7 +570,7 @@ __device__ __forceinline__ void append_k_run(
   if constexpr (PRE) {
     const int64_t tile = gw;
     if (tile < ntiles) {
-      const int64_t grp = tile / tpg, s0 = (tile - grp * tpg) * kTok;
+      const int64_t grp = tile_group(tile, tpg), s0 = (tile - grp * tpg) * kTok;
       const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
       const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
                                 (grp * S + s0 + min(li, nv - 1)) * D};
@@ -597,7 +604,7 @@ __device__ __forceinline__ void append_k_run(
   const int64_t wstep = int64_t(nb) * kWaves;
 
   for (int64_t tile = gw; tile < ntiles; tile += wstep) {
-    const int64_t grp = tile / tpg;
+    const int64_t grp = tile_group(tile, tpg);
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
     const int64_t srow = grp * S + s0 + min(li, nv - 1);  // this lane's token row (clamped)
@@ -792,7 +799,7 @@ __device__ __forceinline__ void append_kmix_run(
   uint4 xpre[1][PRE ? NKS : 1];
   if constexpr (PRE) {
     if (gw < ntiles) {
-      const int64_t grp = gw / tpg, s0 = (gw - grp * tpg) * kTok;
+      const int64_t grp = tile_group(gw, tpg), s0 = (gw - grp * tpg) * kTok;
       const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
       const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
                                 (grp * S + s0 + min(li, nv - 1)) * kD};
@@ -832,7 +839,7 @@ __device__ __forceinline__ void append_kmix_run(
   const int64_t wstep = int64_t(nb) * kWaves;
 
   for (int64_t tile = gw; tile < ntiles; tile += wstep) {
-    const int64_t grp = tile / tpg;
+    const int64_t grp = tile_group(tile, tpg);
     const int64_t s0 = (tile - grp * tpg) * kTok;
     const int nv = static_cast<int>(min<int64_t>(kTok, S - s0));
     const int64_t srow = grp * S + s0 + min(li, nv - 1);  // this lane's token row (clamped)
@@ -1143,7 +1150,7 @@ __device__ __forceinline__ void append_v_run(
   if constexpr (PRE) {
     const int64_t tile = gw;
     if (tile < ntiles) {
-      const int64_t grp = tile / tpg;
+      const int64_t grp = tile_group(tile, tpg);
       const int64_t d0 = a_base + (tile - grp * tpg) * kTok - t0;
       const uint16_t* row[1] = {static_cast<const uint16_t*>(xin) +
                                 (grp * S + min<int64_t>(max<int64_t>(d0 + wt, 0), S - 1)) * D};
@@ -1168,7 +1175,7 @@ __device__ __forceinline__ void append_v_run(
   const int64_t wstep = int64_t(nb) * kWaves;
 
   for (int64_t tile = gw; tile < ntiles; tile += wstep) {
-    const int64_t grp = tile / tpg;
+    const int64_t grp = tile_group(tile, tpg);
     const int64_t A0 = a_base + (tile - grp * tpg) * kTok;  // store token of tile token 0
     const int64_t d0 = A0 - t0;                              // its input index (may be < 0)
     QkvSpan sp{};
