@@ -325,20 +325,24 @@ def _kv_stores_equal(a, b, T):
 @pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("mbits", [1, 2, 3])
-@pytest.mark.parametrize("shape", ["few", "many"])
+@pytest.mark.parametrize("shape", ["few", "many", "xcd"])
 def test_one_launch_append_equals_two_launches(d, dtype, mbits, shape):
     """Small appends with value bits = key MSE bits + 1 run the key and the
     value kernel as one launch (qkv_store_append_layers at one layer, and
     qkv_store_append given keys and values under one Pi): a wave per
     32-coordinate block of a tile for few tiles ("few": 6 groups), a wave per
-    tile for more ("many": 64 groups, up to 10 tiles each).  The stores must
-    be bit-identical to a key-only call followed by a value-only call (two
-    launches), over ragged sizes and unaligned starts."""
+    tile for more ("many": 64 groups, up to 10 tiles each); "xcd": 8 groups
+    of 8 tiles, where the block workgroups of a tile group are placed on one
+    XCD (a whole number of rounds of 8 tile groups), then 7 tiles per group
+    (not), then an unaligned start.  The stores must be bit-identical to a
+    key-only call followed by a value-only call (two launches), over ragged
+    sizes and unaligned starts."""
     vbits = mbits + 1
     gen = torch.Generator().manual_seed(100 * mbits + d)
-    (B, H), sizes = ((2, 3), (1, 5, 37, 64, 1, 100, 3)) if shape == "few" else \
-        ((8, 8), (160, 7, 300))
-    cap = 512
+    (B, H), sizes = {"few": ((2, 3), (1, 5, 37, 64, 1, 100, 3)),
+                     "many": ((8, 8), (160, 7, 300)),
+                     "xcd": ((1, 8), (256, 200, 256))}[shape]
+    cap = 1024 if shape == "xcd" else 512
     kq = Q.InnerProductQuantizer(d, mbits + 1, seed=7, device=DEV)
     vq = Q.MSEQuantizer(d, vbits, seed=8, device=DEV)
     mq = kq.mse_quantizer

@@ -277,13 +277,16 @@ def _kv_stores_equal(a, b, T):
 @pytest.mark.parametrize("n_out", [32, 64])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("vbits", [4, 2, 1])
-@pytest.mark.parametrize("shape", ["few", "many"])
+@pytest.mark.parametrize("shape", ["few", "many", "chunk"])
 def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits, shape):
     """qkv_store_append_kmixed_kv (keys and values in one launch for chunk-sized
-    appends: a wave per 32-slot block of a tile for few tiles, a wave per tile
-    for more; value bits 1 take the two-kernel path inside) writes the same
-    store, bit for bit, as qkv_store_append_kmixed / _kipmixed followed by the
-    value-only qkv_store_append, over ragged sizes and unaligned starts."""
+    appends: a wave per 32-slot block of a tile while two workgroups per CU
+    hold the grid, a wave per tile for more; value bits 1 take the two-kernel
+    path inside) writes the same store, bit for bit, as
+    qkv_store_append_kmixed / _kipmixed followed by the value-only
+    qkv_store_append, over ragged sizes and unaligned starts.  "chunk": cfg4's
+    2048-token chunks of 8 kv heads (the block workgroups of a tile group on
+    one XCD), then shorter appends that are not whole rounds."""
     cls = Q.MixedPrecisionIPQuantizer if ip else Q.MixedPrecisionMSEQuantizer
     kq = cls(128, outlier_bits=3, regular_bits=2, n_outliers=n_out, seed=42, device=DEV)
     out_idx = _outliers(n_out, seed=3)
@@ -293,8 +296,9 @@ def test_kmixed_kv_append_equals_two_calls(ip, n_out, dtype, vbits, shape):
     pi_perm = pi_perm.to(DEV)
     sp = eng._kmix_signs(torch.device(DEV))
     vq = eng.value_quantizer
-    (B, H), sizes = ((2, 3), (1, 37, 64, 5, 100)) if shape == "few" else ((8, 8), (160, 7, 300))
-    cap = 512
+    (B, H), sizes = {"few": ((2, 3), (1, 37, 64, 5, 100)), "many": ((8, 8), (160, 7, 300)),
+                     "chunk": ((1, 8), (2048, 256, 200))}[shape]
+    cap = 4096 if shape == "chunk" else 512
     dev = torch.device(DEV)
     one = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
     two = Q.store.KVStore(B, H, 128, 2, vbits, cap, dev, kmix=(perm, no, ip))
