@@ -1,6 +1,6 @@
 // Fused compress straight into the cache store, for bf16, fp16 or fp32 K and V
-// rows with d = 128 or 64: normalise -> rotate (MFMA) -> Lloyd-Max boundary
-// search -> QJL sign -> bit planes, one pass over the inputs.
+// rows with d = 128, 96 or 64: normalise -> rotate (MFMA) -> Lloyd-Max
+// boundary search -> QJL sign -> bit planes, one pass over the inputs.
 //
 // Reference: QuashKVEngine.append (quashkv/engine.py:145-172) compresses keys
 // with InnerProductQuantizer.compress (quashkv/quantizer.py:211-242) and values
@@ -42,15 +42,17 @@
 // values; the next level's threshold is picked per lane with v_cndmask on the
 // masks already found (levels of 1, 2, 4, ... candidates).
 //
-// Orientation.  32x32x16 MFMAs: a result VGPR holds one C row per 32-lane
-// half, 32 consecutive columns, so each half of a compare mask is one whole
-// 32-bit store word.  Keys: C = tokens x coordinates, a mask half is the
-// plane word of 32 coordinates of one token (one dword of a K row).  Values:
-// C = coordinates x tokens, a mask half is the plane word of one coordinate
-// over 32 tokens (one V-tile word).  The A and B operand layouts are
-// symmetric, so the same x and Pi register fragments serve both orders.
-// Mask words are placed into staging VGPRs with v_writelane and stored with
-// coalesced vector stores.
+// Lane-local words.  In a 32x32x16 MFMA result, lane l holds C column l & 31
+// and, in its 16 registers, rows 8 (v >> 2) + 4 (l >> 5) + (v & 3).  The
+// store words are built inside the lanes: the lanes hold the word's owner
+// (keys: C = coordinates x tokens, lane = token; values: C = tokens x
+// coordinates, lane = coordinate), the rows of the other operand are ordered
+// half-major so that register v of lane half h is position 16 h + v, and
+// each compare mask is shifted into per-lane 16-bit accumulators through the
+// carry-in of v_addc_co_u32 (shift_in); the two lane halves then merge into
+// 32-bit words (merge_halves, v_permlane32_swap) and each lane stores its own
+// K-row dwords or V-tile words.  The A and B operand layouts are symmetric,
+// so the same x and Pi register fragments serve both orders.
 //
 // This header holds the device side (the kernels and their helpers) of the
 // fused store append; qkv_append.hip holds its C ABI and qkv_append_kv.hip
@@ -154,19 +156,6 @@ __device__ __forceinline__ qkv_f32x16 mma(uint4 a, uint4 b, qkv_f32x16 c) {
                                                    __builtin_bit_cast(qkv_bf16x8, b), c, 0, 0, 0);
 }
 
-// v_writelane through the LLVM intrinsic (no clang builtin spells it), so the
-// compiler sees the SGPR read and pads the VALU-writes-SGPR hazard before it.
-extern "C" __device__ int qkv_llvm_writelane(int val, int lane, int old) __asm(
-    "llvm.amdgcn.writelane.i32");
-
-// Value `val` (wave-uniform) into lane L of `old`.
-template <int L>
-__device__ __forceinline__ uint32_t put_lane(uint32_t old, uint32_t val) {
-  static_assert(L >= 0 && L < 64, "lane");
-  return static_cast<uint32_t>(
-      qkv_llvm_writelane(static_cast<int>(val), L, static_cast<int>(old)));
-}
-
 // A wave-uniform value held in a VGPR (a v_cndmask may then take two of them
 // with its mask without exceeding the one-scalar-operand limit).
 __device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
@@ -202,7 +191,8 @@ __host__ __device__ constexpr int half_major(int m) {
 }
 
 // f(std::integral_constant<int, 0>), ..., f(<N - 1>): compile-time unrolled
-// loops whose index feeds template arguments (v_writelane lane numbers).
+// loops whose index must be a constant (register-array indices, the slot
+// blocks' codebooks).
 template <typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);
@@ -977,7 +967,7 @@ __global__ __launch_bounds__(kThreads, 2) void append_kmix_mfma(
     int64_t ntiles, const float* __restrict__ pi_perm, const float* __restrict__ signs_perm,
     Half po, Half pr, uint8_t* __restrict__ kst, float* __restrict__ knorm, int64_t t_stride,
     int64_t t0) {
-  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];  // Pi operand fragments (rows in slot order)
+  __shared__ uint4 frag[FROM_Y ? 1 : kFragN];  // Pi fragments (slot order, half-major per block)
   append_kmix_run<NO, XT, FROM_Y, IPM>(xin, nin, S, tpg, ntiles, pi_perm, signs_perm, po, pr, kst,
                                        knorm, t_stride, t0, frag, blockIdx.x, gridDim.x);
 }
