@@ -994,36 +994,54 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   // load is issued unconditionally -- a tile past the split's last re-reads
   // the last one (an empty split reads its stream's first tile) and its data
   // goes unused -- so each step issues a fixed number of loads and the
-  // in-order load counter waits only for the slot being consumed.  The page
-  // table is read through the constant address space (scalar loads, counted
-  // apart from the vector loads).
-  typedef const __attribute__((address_space(4))) int32_t* ctab_t;
+  // in-order load counter waits only for the slot being consumed.
   const int64_t lts = ntiles > 0 ? ts : 0;
   const int64_t srow0 = bh * t_stride + lts;  // contiguous: the split's first row
-  auto tile_row = [&](int tile) -> int64_t {
+  // PAGED: the page entries of a chunk's kTilesF tiles come from one vector
+  // load per wave (lane l: the entry of tile l % kTilesF of chunk ch), a
+  // chunk ahead of their use (chunks 0 and 1 before the prologue), and a tile
+  // takes its entry with a lane read: no scalar load, whose wait would also
+  // drain the wave's LDS reads in flight, sits in the kernel.  Tiles past the
+  // split's last take the last tile's page (they are masked).
+  auto chunk_pages = [&](int ch) -> int32_t {
+    if constexpr (PAGED) {
+      const int t = ntiles > 0 ? min(ch * kTilesF + (lane & (kTilesF - 1)), ntiles - 1) : 0;
+      const int gt = static_cast<int>(lts >> 6) + t;
+      return kv.ptab[int64_t(b) * kv.pmax + (gt >> (kv.plg - 6))];
+    } else {
+      return 0;
+    }
+  };
+  // the value waves' per-lane form: lane l's word offset of the V tiles of
+  // tile l % kTilesF of chunk ch (entries pe), taken per tile with two lane
+  // reads
+  auto chunk_voffs = [&](int32_t pe, int ch) -> int64_t {
+    const int t = ntiles > 0 ? min(ch * kTilesF + (lane & (kTilesF - 1)), ntiles - 1) : 0;
+    const int tsh = kv.plg - 6;
+    const int gt = static_cast<int>(lts >> 6) + t;
+    const int pg = pe >= 0 && pe < kv.npages ? pe : 0;  // outside the pool: page 0
+    const int64_t row = ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
+    return (row >> 5) * (VB * DS);
+  };
+  auto lane_i64 = [](int64_t v, int l) -> int64_t {
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v)), l);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v) >> 32), l);
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+  };
+  // first store row of tile `tile` of the chunk whose entries chunk_pages
+  // gave (pe); ok: the tile lies on a page of the pool
+  auto tile_row_pe = [&](int32_t pe, int tile, bool& ok) -> int64_t {
     const int tc = ntiles > 0 ? min(tile, ntiles - 1) : 0;
-    if constexpr (PAGED) {
-      const ctab_t ptab = (ctab_t)kv.ptab;
-      const int tsh = kv.plg - 6;
-      const int gt = static_cast<int>(lts >> 6) + tc;
-      int pg = ptab[int64_t(b) * kv.pmax + (gt >> tsh)];
-      if (pg < 0 || pg >= kv.npages) pg = 0;  // outside the pool: read page 0, masked
-      return ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
-    } else {
-      return srow0 + int64_t(tc) * 64;
-    }
+    const int tsh = kv.plg - 6;
+    const int gt = static_cast<int>(lts >> 6) + tc;
+    int pg = __builtin_amdgcn_readlane(pe, tile & (kTilesF - 1));
+    ok = pg >= 0 && pg < kv.npages;
+    if (!ok) pg = 0;  // outside the pool: read page 0, masked
+    return ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
   };
-  // whether tile lies on a page of the pool (always, on a contiguous store)
-  auto page_ok = [&](int tile) -> bool {
-    if constexpr (PAGED) {
-      const ctab_t ptab = (ctab_t)kv.ptab;
-      const int gt = static_cast<int>(lts >> 6) + tile;
-      const int pg = ptab[int64_t(b) * kv.pmax + (gt >> (kv.plg - 6))];
-      return pg >= 0 && pg < kv.npages;
-    } else {
-      return true;
-    }
-  };
+
+  const int32_t pe0 = chunk_pages(0);  // (PAGED) chunk 0's entries
+  int32_t pe1 = chunk_pages(1);        // (PAGED) chunk 1's
 
   // ---- prologue loads (land in LDS before the first chunk's loads are issued)
   const bool pro = aq_ws == nullptr;
@@ -1093,12 +1111,13 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   auto trow = [&](int tile) -> uint32_t {
     return ntiles > 0 ? static_cast<uint32_t>(min(tile, ntiles - 1)) * 64u : 0u;
   };
-  auto loadK = [&](int tile) {
+  // (PAGED: prb is the tile's first store row)
+  auto loadK = [&](int tile, int64_t prb) {
     const uint8_t* kb;
     const float* knb;
     const float* vnb;
     if constexpr (PAGED) {
-      const int64_t rb = tile_row(tile);
+      const int64_t rb = prb;
       kb = kst + rb * KRB;
       knb = knorm + rb;
       vnb = vnorm + rb;
@@ -1117,20 +1136,23 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     }
     vnr = ldnt(vnb + lane);
   };
-  auto loadV = [&](int slot, int tile) {
+  // (PAGED: pvo is the word offset of the tile's first V tile)
+  auto loadV = [&](int slot, int tile, int64_t pvo) {
     const uint32_t* vb;  // the tile's first V tile
     if constexpr (PAGED)
-      vb = vst + (tile_row(tile) >> 5) * (VB * DS);
+      vb = vst + pvo;
     else
       vb = vbase + (trow(tile) >> 5) * (VB * DS);
 #pragma unroll
     for (int k = 0; k < VB; ++k) vw[slot][k] = ldnt(vb + voff + k * DS);
   };
+  bool pok0 = true;  // (key waves) tile wi lies on a page of the pool
   if (keyw) {
-    loadK(wi);
+    loadK(wi, PAGED ? tile_row_pe(pe0, wi, pok0) : 0);
   } else {
+    const int64_t vof = PAGED ? chunk_voffs(pe0, 0) : 0;
 #pragma unroll
-    for (int t = 0; t < kTilesF; ++t) loadV(t, t);
+    for (int t = 0; t < kTilesF; ++t) loadV(t, t, PAGED ? lane_i64(vof, t) : 0);
   }
 
   // ---- prologue math: q~ = q Pi^T, operand digits (prepare_mfma on 1024 threads)
@@ -1250,10 +1272,12 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
       mk[r] = kMFloor;
       lacc[r] = 0.f;
     }
+    bool pok = pok0;  // tile wi of chunk c lies on a page of the pool
     for (int c = 0; c < nch; ++c) {
       uint8_t* cbuf = bufs + (c & 1) * kTilesF * 1024;
       ChunkStats& cs = stats[c & 1];
       const int tile = c * kTilesF + wi;
+      const int32_t pe2 = chunk_pages(c + 2);
       // ---- stage 1: scores of tile wi of chunk c.  A tile past the split's
       // last (only in the last chunk) runs on the re-read last tile and is
       // masked out whole: its scores are -inf, so its p and value digits are 0.
@@ -1281,10 +1305,11 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
 #pragma unroll
       for (int sub = 0; sub < 4; ++sub) knt[sub] = kn[sub];
       float vz = vnr;
-      loadK(tile + kTilesF);  // the slot is free: refill it
+      bool pokn = true;
+      const int64_t rbn = PAGED ? tile_row_pe(pe1, tile + kTilesF, pokn) : 0;
+      loadK(tile + kTilesF, rbn);  // the slot is free: refill it
       mfma_settle();
       const int tbase = tile * 64;
-      const bool pok = page_ok(tile);
       const bool full = pok && tbase >= slo && tbase + 64 <= shi && nr == kRowsM &&
                         tbase + 63 <= cmin;
       float* srow = reinterpret_cast<float*>(cbuf + wi * 1024 + lg * 256);
@@ -1342,6 +1367,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         dst[128] = static_cast<uint8_t>(dg >> 16);
         dst[192] = static_cast<uint8_t>(dg8 >> 16);
       }
+      pok = pokn;
+      pe1 = pe2;
       lds_sync();
     }
     // the step in which the value waves take the last chunk
@@ -1399,6 +1426,8 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     lds_sync();
     for (int c = 1; c <= nch; ++c) {
       const int cv = c - 1;  // the chunk this stage accumulates
+      const int32_t pe2 = chunk_pages(c + 1);
+      const int64_t vof = PAGED ? chunk_voffs(pe1, c) : 0;  // the tiles loaded below
       const uint8_t* vbuf = bufs + (cv & 1) * kTilesF * 1024;
       // slot t is refilled with tile t of the next chunk once consumed; tiles
       // past the split's last are zero digits over re-read planes.  The digit
@@ -1413,7 +1442,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         const qkv_v4i bq = bqn;
         bqn = ldbq(vbuf, t + 1);
         pv(t, bq, t == 0);
-        loadV(t, (cv + 1) * kTilesF + t);
+        loadV(t, c * kTilesF + t, PAGED ? lane_i64(vof, t) : 0);
       }
       lds_sync();
 #pragma unroll
@@ -1422,8 +1451,9 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         const qkv_v4i bq = bqn;
         if (t + 1 < kTilesF) bqn = ldbq(vbuf, t + 1);
         pv(t, bq, false);
-        loadV(t, (cv + 1) * kTilesF + t);
+        loadV(t, c * kTilesF + t, PAGED ? lane_i64(vof, t) : 0);
       }
+      pe1 = pe2;
       {
         // chunk cv into the running O~: sum_t p'_t (2 phi_S,t - 1) = 2^-Fv (2 Y_S - U)
         // per digit half in exact int32 (|acc| < 2^21 for a 512-token chunk),

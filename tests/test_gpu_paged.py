@@ -341,6 +341,63 @@ def test_paged_kv_append_equals_two_calls(d, dtype, key_bits, value_bits, shape)
 
 
 @pytest.mark.parametrize("d", [128, 96, 64])
+@pytest.mark.parametrize("n_splits", [1, 0])
+def test_paged_decode_masks_pages_off_the_pool(d, n_splits):
+    """qkv_paged_decode_attention gives no weight to the tokens of a page whose
+    table entry lies outside the pool (-1 or >= num_pages): each sequence
+    attends like the oracle over its other tokens.  1,500 tokens in 64-token
+    pages: one split streams three 512-token chunks (n_splits 1), or the
+    library's split count (0).  The masked pages sit inside a chunk, on a
+    chunk's first tile and on the last, partial page."""
+    B, H, G, S, pt = 3, 2, 2, 1500, 64
+    dev = torch.device(DEV)
+    e = PagedQuashKVEngine(head_dim=d, seed=31, device=DEV, page_tokens=pt)
+    e._paged = PagedKVStore(B, H, d, 2, 3, 8, dev, pt)
+    random.Random(3).shuffle(e._paged.free)
+    gen = torch.Generator(device=DEV).manual_seed(d + n_splits)
+    e.append(torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=torch.bfloat16),
+             torch.randn(B, H, S, d, generator=gen, device=DEV, dtype=torch.bfloat16))
+    st, kq = e.paged_store, e.key_quantizer
+    per = st.pages_per_seq
+    off = {0: [(3, -1)], 1: [(8, st.num_pages), (17, -5)], 2: [((S - 1) // pt, st.num_pages + 9)]}
+    tab = st.table.clone()
+    for b, ents in off.items():
+        for page, val in ents:
+            tab[b, page] = val
+    q = torch.randn(B, H * G, 1, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+    L = N.lib()
+    splits = n_splits or L.qkv_attention_splits(B, H * G, H, 1, d, S)
+    ws_bytes = L.qkv_attention_workspace_bytes(B, H * G, H, 1, d, splits)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    out = torch.empty(B, H * G, 1, d, device=DEV)
+    kc = N.HostFloats(kq.mse_quantizer.codebook.centroids_host)
+    vc = N.HostFloats(e.value_quantizer.codebook.centroids_host)
+    N.check(L.qkv_paged_decode_attention(
+        q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(), st.vpool.data_ptr(),
+        st.vnorm.data_ptr(), tab.data_ptr(), per, pt, st.num_pages, S, B, H * G, H, 1, d, 2, 3,
+        kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr, kq.S.data_ptr(), float(kq.qjl_scale),
+        1.0 / math.sqrt(d), 0, out.data_ptr(), N.QKV_F32, ws.data_ptr(), ws_bytes, splits,
+        N.stream(dev)))
+    torch.cuda.synchronize()
+    cs = e._store                       # the tokens gathered into a contiguous store
+    kcd, kbt, vcd = (x.cpu() for x in cs.read_codes(0, S))
+    kn, vn = (x[:, :, :S].cpu() for x in (cs.knorm, cs.vnorm))
+    vq = e.value_quantizer
+    for b in range(B):
+        keep = torch.ones(S, dtype=torch.bool)
+        for page, _ in off[b]:
+            keep[page * pt:(page + 1) * pt] = False
+        sel = lambda t: t[b:b + 1, :, keep].repeat_interleave(G, dim=1)
+        blk = dict(kcodes=sel(kcd), kbits=sel(kbt), knorm=sel(kn), vcodes=sel(vcd),
+                   vnorm=sel(vn))
+        ref = R.attention_naive(q[b:b + 1].float().cpu(), [blk], kq.mse_quantizer.Pi.cpu(),
+                                kq.mse_quantizer.codebook.centroids.cpu(),
+                                vq.codebook.centroids.cpu(), kq.S.cpu(), kq.qjl_scale,
+                                scale=1.0 / math.sqrt(d))
+        _close(out[b:b + 1], ref)
+
+
+@pytest.mark.parametrize("d", [128, 96, 64])
 @pytest.mark.parametrize("shape", ["few", "many"])
 def test_paged_kv_append_skips_pages_off_the_pool(d, shape):
     """qkv_paged_store_append_kv never writes through page-table entries
