@@ -1023,11 +1023,6 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
     const int64_t row = ((int64_t(pg) * Hkv + hkv) << kv.plg) + ((gt & ((1 << tsh) - 1)) << 6);
     return (row >> 5) * (VB * DS);
   };
-  auto lane_i64 = [](int64_t v, int l) -> int64_t {
-    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v)), l);
-    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v) >> 32), l);
-    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-  };
   // first store row of tile `tile` of the chunk whose entries chunk_pages
   // gave (pe); ok: the tile lies on a page of the pool
   auto tile_row_pe = [&](int32_t pe, int tile, bool& ok) -> int64_t {
@@ -1152,7 +1147,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
   } else {
     const int64_t vof = PAGED ? chunk_voffs(pe0, 0) : 0;
 #pragma unroll
-    for (int t = 0; t < kTilesF; ++t) loadV(t, t, PAGED ? lane_i64(vof, t) : 0);
+    for (int t = 0; t < kTilesF; ++t) loadV(t, t, PAGED ? readlane_i64(vof, t) : 0);
   }
 
   // ---- prologue math: q~ = q Pi^T, operand digits (prepare_mfma on 1024 threads)
@@ -1442,7 +1437,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         const qkv_v4i bq = bqn;
         bqn = ldbq(vbuf, t + 1);
         pv(t, bq, t == 0);
-        loadV(t, c * kTilesF + t, PAGED ? lane_i64(vof, t) : 0);
+        loadV(t, c * kTilesF + t, PAGED ? readlane_i64(vof, t) : 0);
       }
       lds_sync();
 #pragma unroll
@@ -1451,7 +1446,7 @@ __global__ __launch_bounds__(kThreadsF, 1) void decode_fused(
         const qkv_v4i bq = bqn;
         if (t + 1 < kTilesF) bqn = ldbq(vbuf, t + 1);
         pv(t, bq, false);
-        loadV(t, c * kTilesF + t, PAGED ? lane_i64(vof, t) : 0);
+        loadV(t, c * kTilesF + t, PAGED ? readlane_i64(vof, t) : 0);
       }
       pe1 = pe2;
       {

@@ -110,6 +110,12 @@ __device__ __forceinline__ int64_t shfl_xor_i64(int64_t v, int mask) {
                               static_cast<uint32_t>(lo));
 }
 
+// lane l's value of a per-lane int64 (wave-uniform result)
+__device__ __forceinline__ int64_t readlane_i64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v)), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(static_cast<uint64_t>(v) >> 32), l);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += shfl_xor_i64(v, o);
