@@ -780,6 +780,8 @@ def sub_cfg5(args, dev, stream) -> dict:
     db /= db.norm(dim=1, keepdim=True)
     qs = torch.randn(M, DD, device=dev, generator=g)
     qs /= qs.norm(dim=1, keepdim=True)
+    # a throwaway index takes the first call's one-time costs (kernel loads)
+    QuashIndex(DD, bits=3, seed=42, device=dev).add(db[:4096])
     idx = QuashIndex(DD, bits=3, seed=42, device=dev)
     add_ms = event_ms(lambda: idx.add(db), 1, stream)[0]
     res_box = {}

@@ -2171,9 +2171,12 @@ struct MipsCfg {
 };
 
 // Rows of d < 128 (PDW = d / 32 dwords per plane) run as 128-wide rows whose
-// missing plane words are zero, against queries padded with zeros.
+// missing plane words are zero, against queries padded with zeros.  Two
+// workgroups per CU: the query operands (QC x NU x 4 registers), two groups'
+// accumulators and the pipelined expansion need more than a third of the
+// register file without spills.
 template <int MB, int PDW>
-__global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ aq,
+__global__ __launch_bounds__(256, 2) void mips_scan(const qkv_v4i* __restrict__ aq,
                                                  const float* __restrict__ rowc, int M,
                                                  const uint8_t* __restrict__ kst,
                                                  const float* __restrict__ norms, int64_t N,
@@ -2241,8 +2244,9 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
 
     qkv_v4i a[QC][NU];
     // theta: this chunk list's k-th score (a candidate must beat it);
-    // tg: the query's device-wide bound (a candidate must reach it)
-    float fq[QC], cr[QC], theta[QC], tg[QC];
+    // tg: the query's device-wide bound (a candidate must reach it);
+    // thr = max(the float above theta, tg): a candidate is a score >= thr
+    float fq[QC], cr[QC], theta[QC], tg[QC], thr[QC];
 #pragma unroll
     for (int c = 0; c < QC; ++c) {
       const int ch = min(chunk0 + c, nchunks - 1);
@@ -2255,6 +2259,7 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
       tg[c] = qg < M ? fkey_inv(__hip_atomic_load(&gth[qg], __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT))
                      : INFINITY;
+      thr[c] = fmaxf(-__FLT_MAX__, tg[c]);
     }
     for (int i = lane; i < QW * k; i += 64) {
       wls[i] = -INFINITY;
@@ -2271,7 +2276,8 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
         const int64_t v = s0 + i / RAWD;
         pre[x] = (i < SD && v < v1) ? kw[v * RAWD + i % RAWD] : 0u;
       }
-      if (tid < kMipsStep) pn = s0 + tid < v1 ? norms[s0 + tid] : 0.f;
+      // rows past the range score NaN, which no threshold test admits
+      if (tid < kMipsStep) pn = s0 + tid < v1 ? norms[s0 + tid] : __builtin_nanf("");
     };
     auto stash = [&](int buf) {
 #pragma unroll
@@ -2289,13 +2295,15 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
       if (more) fetch(s0 + kMipsStep);  // in flight during this step
       const uint32_t* rb = rows + buf * kMipsStep * RAWD;
       const float* nb = nrm_s + buf * kMipsStep;
-#pragma unroll 1
-      for (int g = 0; g < kMipsStep / 16; ++g) {
-        const int vl = g * 16 + ln;
+      // 16-vector groups, software-pipelined: group g + 1's row words are
+      // expanded and its MFMAs issued before group g's scores and candidates,
+      // so that the score arithmetic overlaps the matrix cores' work
+      constexpr int NG = kMipsStep / 16;
+      auto expand_mfma = [&](int g, qkv_v4i* acc) {
         // virtual row dwords lg*DPL .. : plane p < NS is the parity of the
         // code bits in odd subset p, plane NS the QJL plane
         uint32_t vd[C::DPL];
-        const uint32_t* rv = rb + vl * RAWD;
+        const uint32_t* rv = rb + (g * 16 + ln) * RAWD;
 #pragma unroll
         for (int x = 0; x < C::DPL; ++x) {
           uint32_t val = rv[voff[x][0]] & vmask[x][0];
@@ -2303,30 +2311,42 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
           for (int j = 1; j < NT; ++j) val ^= rv[voff[x][j]] & vmask[x][j];
           vd[x] = val;
         }
-        qkv_v4i bo[NU];
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
           const uint32_t x = vd[u >> 1];
           const int sh = 4 * (u & 1);
-          bo[u][0] = static_cast<int>(x & (0x01010101u << sh));
-          bo[u][1] = static_cast<int>(x & (0x02020202u << sh));
-          bo[u][2] = static_cast<int>(x & (0x04040404u << sh));
-          bo[u][3] = static_cast<int>(x & (0x08080808u << sh));
+          qkv_v4i bo;
+          bo[0] = static_cast<int>(x & (0x01010101u << sh));
+          bo[1] = static_cast<int>(x & (0x02020202u << sh));
+          bo[2] = static_cast<int>(x & (0x04040404u << sh));
+          bo[3] = static_cast<int>(x & (0x08080808u << sh));
+#pragma unroll
+          for (int c = 0; c < QC; ++c)
+            acc[c] = mfma_i8(a[c][u], bo, u == 0 ? qkv_v4i{0, 0, 0, 0} : acc[c]);
         }
-        const float nv = nb[vl];
-        const bool valid = s0 + vl < v1;
+      };
+      qkv_v4i accs[2][QC];
+      expand_mfma(0, accs[0]);
+      // (a group's accumulators are read after the next group's MFMAs and a
+      // branch; the first and the last group take the explicit pad)
+      mfma_settle();
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (g + 1 < NG) expand_mfma(g + 1, accs[(g + 1) & 1]);
+        if (g + 1 == NG) mfma_settle();
+        const qkv_v4i* acc = accs[g & 1];
+        const float nv = nb[g * 16 + ln];  // NaN past the range
         float sc[QC];
-        {
-          qkv_v4i acc[QC];
 #pragma unroll
-          for (int c = 0; c < QC; ++c) acc[c] = qkv_v4i{0, 0, 0, 0};
-#pragma unroll
-          for (int u = 0; u < NU; ++u)
-#pragma unroll
-            for (int c = 0; c < QC; ++c) acc[c] = mfma_i8(a[c][u], bo[u], acc[c]);
-          mfma_settle();
-#pragma unroll
-          for (int c = 0; c < QC; ++c) {
+        for (int c = 0; c < QC; ++c) {
+          if constexpr (NU * (1 << 20) < (1 << 23)) {
+            // |digit sums| < NU 2^20 < 2^23: two exact int32 halves
+            // (base 256), one rounding each
+            const int zlo = acc[c][0] + acc[c][1] * 256;
+            const int zhi = acc[c][2] + acc[c][3] * 256;
+            sc[c] = nv * fmaf(static_cast<float>(zhi), 65536.f * fq[c],
+                              fmaf(static_cast<float>(zlo), fq[c], cr[c]));
+          } else {
             const float z = static_cast<float>(acc[c][0]) +
                             256.f * static_cast<float>(acc[c][1]) +
                             65536.f * static_cast<float>(acc[c][2]) +
@@ -2336,8 +2356,7 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
         }
 #pragma unroll
         for (int c = 0; c < QC; ++c) {
-          uint64_t cand =
-              __builtin_amdgcn_ballot_w64(valid && sc[c] > theta[c] && sc[c] >= tg[c]);
+          uint64_t cand = __builtin_amdgcn_ballot_w64(sc[c] >= thr[c]);
           while (cand) {  // rare: insert in ascending lane (= index) order
             const int L = __builtin_ctzll(cand);
             cand &= cand - 1;
@@ -2367,7 +2386,10 @@ __global__ __launch_bounds__(256, 3) void mips_scan(const qkv_v4i* __restrict__ 
                 qi[ge] = static_cast<int>(s0 + g * 16 + (L & 15));
               }
               const float th = qs[k - 1];
-              if (lg == (L >> 4)) theta[c] = th;
+              if (lg == (L >> 4)) {
+                theta[c] = th;
+                thr[c] = fmaxf(nextafterf(th, INFINITY), tg[c]);
+              }
             }
           }
         }
