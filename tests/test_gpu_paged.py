@@ -135,6 +135,51 @@ def test_paged_clear_reuses_pages(dtype):
     _close(paged.attention(q), _oracle(q, paged, causal=False))
 
 
+@pytest.mark.parametrize("page_tokens", [64, 2048])
+def test_paged_long_split_matches_contiguous(page_tokens):
+    """One split streaming 4,133 tokens (nine 512-token chunks, the last one
+    partial) over shuffled pages: qkv_paged_decode_attention equals
+    qkv_decode_attention on the contiguous store bit for bit at the same
+    split count (each wave reads a chunk's page entries a chunk ahead)."""
+    B, Hq, H, d, T = 2, 32, 8, 128, 4133
+    cont, paged = _pair(d, 3, 3, B, H, seed=5, pool_pages=B * -(-T // page_tokens) + 2,
+                        page_tokens=page_tokens)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    k = torch.randn(B, H, T, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn(B, H, T, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+    cont.append(k, v)
+    paged.append(k, v)
+    q = torch.randn(B, Hq, 1, d, generator=gen, device=DEV, dtype=torch.bfloat16)
+    L = N.lib()
+    stream = N.stream(torch.device(DEV))
+    kq = cont.key_quantizer
+    kc = N.HostFloats(kq.mse_quantizer.codebook.centroids_host)
+    vc = N.HostFloats(cont.value_quantizer.codebook.centroids_host)
+    ws_bytes = L.qkv_attention_workspace_bytes(B, Hq, H, 1, d, 1)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+    outs = []
+    for eng in (cont, paged):
+        out = torch.empty(B, Hq, 1, d, device=DEV)
+        common = (T, B, Hq, H, 1, d, 2, 3, kq.mse_quantizer.Pi.data_ptr(), kc.ptr, vc.ptr,
+                  kq.S.data_ptr(), float(kq.qjl_scale), 1.0 / math.sqrt(d), 0, out.data_ptr(),
+                  N.QKV_F32, ws.data_ptr(), ws_bytes, 1, stream)
+        if eng is cont:
+            st = cont._store
+            N.check(L.qkv_decode_attention(q.data_ptr(), N.QKV_BF16, st.kst.data_ptr(),
+                                           st.knorm.data_ptr(), st.vst.data_ptr(),
+                                           st.vnorm.data_ptr(), st.capacity, *common))
+        else:
+            st = paged.paged_store
+            N.check(L.qkv_paged_decode_attention(
+                q.data_ptr(), N.QKV_BF16, st.kpool.data_ptr(), st.knorm.data_ptr(),
+                st.vpool.data_ptr(), st.vnorm.data_ptr(), st.table.data_ptr(), st.pages_per_seq,
+                st.pt, st.num_pages, *common))
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]), float((outs[0] - outs[1]).abs().max())
+    _close(outs[1], _oracle(q, paged, causal=False))
+
+
 def test_paged_cfg3_shape_decode_matches_contiguous():
     """cfg3's head layout (32 query / 8 kv heads, d = 128) at 4 sequences of
     1000 tokens appended as a prefill and decode steps."""
