@@ -3604,11 +3604,14 @@ struct MipsLayout {
 };
 
 // Vector chunks per query tile: enough (query tile, chunk) items for several
-// per workgroup slot, chunks of at least 16 steps, at most 256 chunks.
+// per workgroup slot (12 per CU: six per workgroup at two per CU; fewer,
+// longer chunks fill fewer per-chunk top-k lists -- cfg5 14.0 ms against
+// 14.4 at 24 per CU and 15.4 at 48), chunks of at least 16 steps, at most
+// 256 chunks.
 int mips_splits(int32_t M, int64_t N, int mbits) {
   const int qc = mbits <= 2 ? 4 : 2;
   const int64_t qtiles = (M + 16 * qc - 1) / (16 * qc);
-  const int64_t want = (24 * int64_t(qkv_num_cus()) + qtiles - 1) / qtiles;
+  const int64_t want = (12 * int64_t(qkv_num_cus()) + qtiles - 1) / qtiles;
   const int64_t maxs = std::max<int64_t>(1, (N + 16 * kMipsStep - 1) / (16 * kMipsStep));
   return static_cast<int>(std::max<int64_t>(1, std::min<int64_t>({want, maxs, 256})));
 }
