@@ -118,6 +118,30 @@ def test_index_edge_cases():
     assert len(packed) == 0
 
 
+def test_index_ties_lower_index_first():
+    """Equal scores (identical codes and norms) come out in ascending index
+    order, the order this build defines where torch.topk leaves it open:
+    duplicates of a query's own direction spread over the database (and so
+    over the scan's vector chunks) lead its list."""
+    gen = torch.Generator().manual_seed(3)
+    d, N_ = 128, 20000
+    db = torch.randn(N_, d, generator=gen)
+    q = torch.randn(4, d, generator=gen)
+    dups = [17, 4096, 9000, 19999]
+    for j in dups:
+        db[j] = q[0]
+    db = db / db.norm(dim=1, keepdim=True)
+    idx = QuashIndex(dim=d, bits=3, seed=11, device=DEV)
+    idx.add(db.to(DEV))
+    s, i = idx.search(q.to(DEV), 10)
+    s, i = s.cpu(), i.cpu()
+    assert i[0, :4].tolist() == dups
+    assert bool((s[0, :4] == s[0, 0]).all())
+    for r in range(4):   # within a run of equal scores the indices ascend
+        eq = s[r, 1:] == s[r, :-1]
+        assert bool((i[r, 1:][eq] > i[r, :-1][eq]).all())
+
+
 def test_index_recall_reasonable():
     gen = torch.Generator().manual_seed(0)
     db = torch.randn(5000, 128, generator=gen)
